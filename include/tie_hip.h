@@ -1,0 +1,136 @@
+/*
+ * tie_hip.h -- C ABI of the MI355X (gfx950) Qwen3-MoE FFN block for TIE.
+ *
+ * The reference (szemzoa/tie) runs the MoE FFN inline in
+ * transformer_layer_qwen3 (model_qwen3.c:404-471): per token a router GEMV
+ * (dispatch_mat_vec, model_qwen3.c:431-432), find_top_k (engine.c:891),
+ * softmax over the k selected logits (engine.c:864), k process_expert_task
+ * jobs on the thread pool (engine.c:916-964) and an fp32 weighted combine
+ * (model_qwen3.c:459-470).  This library replaces that whole branch with
+ * HIP kernels.  Every entry point is plain C: pointers, sizes and GGML type
+ * ids (gguf.h:8-36), no HIP or torch types.
+ *
+ * Return codes: 0 on success, a negative TIE_HIP_E* code otherwise; the
+ * library never exits the process.  tie_hip_last_error() describes the
+ * last failure of the calling thread.
+ */
+#ifndef TIE_HIP_H
+#define TIE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TIE_HIP_ABI_VERSION 1
+
+/* GGML type ids as in gguf.h:8-36 */
+#define TIE_GGML_F32 0
+#define TIE_GGML_Q4_K 12
+#define TIE_GGML_Q6_K 14
+#define TIE_GGML_BF16 30
+
+#define TIE_HIP_OK 0
+#define TIE_HIP_EINVAL (-1)  /* bad argument, shape or type (TIE: return -1, model_qwen3.c:407-410) */
+#define TIE_HIP_EHIP (-2)    /* a HIP runtime error */
+#define TIE_HIP_ENOMEM (-3)  /* device allocation failed */
+#define TIE_HIP_ENOINIT (-4) /* tie_hip_init() not called */
+
+#define TIE_SILU_TABLE_SIZE 8192 /* SILU_TABLE_SIZE, engine.h:10 */
+
+/* Forward flags */
+#define TIE_HIP_PATH_AUTO 0x0  /* exact fp32 GEMV path for small T, bf16 MFMA grouped GEMM above */
+#define TIE_HIP_PATH_EXACT 0x1 /* always the fp32 path that reproduces TIE's arithmetic bit for bit */
+#define TIE_HIP_PATH_MFMA 0x2  /* always the grouped-GEMM path */
+
+typedef struct tie_hip_layer tie_hip_layer;
+
+/* Library set-up on one HIP device; replaces the MoE-relevant part of
+ * engine_alloc (engine.c:14-40: thread pool, silu_table_init,
+ * math_dispatch_init).  Builds the SiLU table on the host CPU the way TIE
+ * does and uploads it. */
+int tie_hip_init(int device);
+
+/* Frees every device resource, including the weight cache. */
+void tie_hip_shutdown(void);
+
+/* Text of the last error on the calling thread ("" when none). */
+const char *tie_hip_last_error(void);
+
+/* Drop-in for the MoE branch of transformer_layer_qwen3
+ * (model_qwen3.c:404-471).  Host pointers, as TIE holds them:
+ *   x          ctx->mem.normed_ffn_input, [T][d] F32
+ *   router_w   ffn_gate_inp, F32 [E][d] (router_type must be TIE_GGML_F32)
+ *   gate/up    ffn_{gate,up}_exps, [E][F][d] in GGUF block layout
+ *   down       ffn_down_exps, [E][d][F] in GGUF block layout
+ *   out        ctx->mem.ffn_down_output, [T][d] F32
+ *   topk_idx_opt / topk_w_opt  optional [T][k] selected experts / weights
+ * Expert types: TIE_GGML_Q4_K, TIE_GGML_Q6_K or TIE_GGML_BF16.  d and F must
+ * be multiples of 256, k <= E <= 1024, k <= 32.  Weight tensors are uploaded
+ * once and cached, keyed by host pointer, type and size (they must stay
+ * valid and unchanged while cached, as TIE's mmap'd weights are).  Runs on
+ * the library's stream and returns after out is written. */
+int tie_hip_moe_ffn(const float *x, int T, int d, int F, int E, int k, const void *router_w, int router_type,
+		    const void *gate_exps, int gate_type, const void *up_exps, int up_type, const void *down_exps,
+		    int down_type, float *out, int32_t *topk_idx_opt, float *topk_w_opt);
+
+/* Replace the SiLU lookup table with the caller's (TIE's own silu_table,
+ * engine.c:12, as filled by silu_table_init, engine.c:297-303). */
+int tie_hip_set_silu_table(const float *table, int n);
+
+/* Build the SiLU table on the host CPU exactly as TIE's compiled
+ * silu_table_init does on this host (no GPU needed). */
+int tie_hip_silu_table_host(float *table, int n);
+
+/* ------------------------------------------------------------------ */
+/* Device-resident layers (inputs already in HBM)                       */
+/* ------------------------------------------------------------------ */
+
+typedef struct tie_hip_layer_desc {
+	int d, F, E;
+	const void *router_w; /* F32 [E][d] */
+	int router_type;      /* TIE_GGML_F32 */
+	const void *gate_exps;
+	int gate_type;
+	const void *up_exps;
+	int up_type;
+	const void *down_exps;
+	int down_type;
+	const float *router_bias; /* optional [E], added to the logits before top-k; NULL in TIE */
+	int src_on_device;        /* 1: the pointers above are device memory (GGUF layout) */
+	int literal_bf16_stride;  /* 1: BF16 experts start at e*rows*(in/256)*2 bytes, as
+				     process_expert_task computes it (engine.c:929-942) */
+} tie_hip_layer_desc;
+
+/* Upload (or copy on device) and repack one layer's weights into the
+ * device layout.  The source buffers may be freed afterwards. */
+int tie_hip_layer_create(const tie_hip_layer_desc *desc, tie_hip_layer **out);
+void tie_hip_layer_destroy(tie_hip_layer *layer);
+
+/* Device bytes held by a layer. */
+size_t tie_hip_layer_bytes(const tie_hip_layer *layer);
+
+/* MoE block on device pointers, enqueued on `stream` (a hipStream_t; NULL =
+ * the library stream).  x_dev/out_dev are [T][d] F32; topk outputs are
+ * optional [T][k].  Returns once enqueued; the caller synchronises. */
+int tie_hip_moe_forward(tie_hip_layer *layer, const float *x_dev, int T, int k, float *out_dev,
+			int32_t *topk_idx_dev, float *topk_w_dev, int flags, void *stream);
+
+/* The largest T that TIE_HIP_PATH_AUTO sends down the exact path. */
+int tie_hip_exact_max_tokens(void);
+void tie_hip_set_exact_max_tokens(int t);
+
+/* Make the n-th next device allocation fail with TIE_HIP_ENOMEM (n >= 1;
+ * 0 disarms).  Host-side fault injection for error-path tests. */
+void tie_hip_debug_fail_alloc(int n);
+
+/* Host build of the device expf (tie_expf.h) over n inputs, for checking
+ * it against the host libm (no GPU needed). */
+void tie_hip_host_expf(const float *in, float *out, size_t n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,148 @@
+"""GPU parity of the exact path: the HIP block, called through the C ABI,
+against the CPU oracle on the same inputs -- bit for bit.
+
+The oracle runs on this host's CPU and builds TIE's SiLU table with this
+host's reciprocal instruction, which is also what the library uploads at
+tie_hip_init(); the committed golden vectors pin the oracle itself (see
+test_oracle.py) and are compared directly where the host CPU matches the one
+they were made on.
+"""
+import numpy as np
+import pytest
+
+import tie_amd
+from conftest import bits, golden_layer, host_cpu_identity, load_golden, synth_layer
+from oracle import bind
+from tie_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device():
+    import torch
+    assert torch.cuda.is_available(), "GPU test without a GPU"
+    tie_amd.init(0)
+    yield
+    tie_amd.shutdown()
+
+
+def assert_same(got, want, what):
+    g, w = np.ascontiguousarray(got), np.ascontiguousarray(want)
+    if g.dtype == np.float32:
+        nz = bits(g) != bits(w)
+        if nz.any():
+            i = np.argwhere(nz)[0]
+            raise AssertionError("%s: %d of %d differ, first at %s: got %r want %r (max abs diff %g)" % (
+                what, int(nz.sum()), nz.size, tuple(i), g[tuple(i)], w[tuple(i)], float(np.max(np.abs(g - w)))))
+    else:
+        np.testing.assert_array_equal(g, w, err_msg=what)
+
+
+def run_both(layer, x, k):
+    print("case d=%d F=%d E=%d T=%d k=%d types=%d/%d" % (layer.d, layer.F, layer.E, x.shape[0], k,
+                                                         layer.gate_type, layer.down_type), flush=True)
+    out, idx, w = tie_amd.moe_ffn(x, layer, k)
+    ro, ri, rw = bind.moe_block(layer, x, k)
+    assert_same(idx, ri, "topk_idx")
+    assert_same(w, rw, "topk_w")
+    assert_same(out, ro, "out")
+    return out, idx, w
+
+
+def test_library_table_is_oracle_table():
+    assert_same(tie_amd.silu_table_host(), bind.silu_table(), "silu table")
+
+
+@pytest.mark.parametrize("name", ["gtiny_q4k_t8", "gtiny_q6k_q4k_t8", "gtiny_ties_t6", "g30b_q4k_t4",
+                                  "g235b_e16_t2"])
+def test_golden_cases(name):
+    g = load_golden(name)
+    layer = golden_layer(g)
+    out, idx, w = run_both(layer, g["x"], int(g["k"]))
+    assert_same(idx, g["topk_idx"], "golden topk_idx")
+    assert_same(w, g["topk_w"], "golden topk_w")
+    if str(g["cpu"]) == host_cpu_identity():
+        assert_same(out, g["out"], "golden out")
+
+
+@pytest.mark.parametrize("name,literal", [("g30b_bf16_zipf_t4", False), ("g30b_bf16_zipf_literal_t4", True)])
+def test_golden_bf16_zipf_device_api(name, literal):
+    import torch
+    g = load_golden(name)
+    s = golden_layer(g)
+    k = int(g["k"])
+    L = tie_amd.Layer.from_synth(s, literal_bf16_stride=literal)
+    x = torch.from_numpy(g["x"]).cuda()
+    T = x.shape[0]
+    out = torch.empty_like(x)
+    idx = torch.empty((T, k), dtype=torch.int32, device="cuda")
+    w = torch.empty((T, k), dtype=torch.float32, device="cuda")
+    L.forward(x, T, k, out, idx, w, flags=tie_amd.PATH_EXACT)
+    torch.cuda.synchronize()
+    ro, ri, rw = bind.moe_block(s, g["x"], k, literal_bf16_stride=literal)
+    assert_same(idx.cpu().numpy(), ri, "topk_idx")
+    assert_same(w.cpu().numpy(), rw, "topk_w")
+    assert_same(out.cpu().numpy(), ro, "out")
+    assert_same(idx.cpu().numpy(), g["topk_idx"], "golden topk_idx")
+    L.close()
+
+
+@pytest.mark.parametrize("cfg", ["30b_t1", "30b_t32", "235b_t1"])
+def test_full_size_configs(cfg):
+    c = synth.CONFIGS[cfg]
+    layer = synth_layer(c["seed"], c["d"], c["F"], c["E"], c["gu_type"], c["down_type"], c["zipf"])
+    x = synth.make_input(c["seed"], c["T"], c["d"])
+    run_both(layer, x, c["k"])
+
+
+def test_ragged_token_counts_and_k():
+    layer = synth_layer(21, 512, 512, 24, synth.Q4_K, synth.Q6_K, None)
+    for T, k in [(1, 1), (3, 2), (5, 7), (9, 24), (13, 8)]:
+        x = synth.make_input(21 + T, T, 512)
+        run_both(layer, x, k)
+
+
+def test_zero_tokens_and_nan_rows():
+    layer = synth_layer(22, 256, 256, 16, synth.Q4_K, synth.Q6_K, None)
+    out, idx, w = tie_amd.moe_ffn(np.zeros((0, 256), np.float32), layer, 4)
+    assert out.shape == (0, 256)
+    x = synth.make_input(22, 3, 256)
+    x[1, 7] = np.nan  # NaN logits: no expert enters the top-k
+    out, idx, w = tie_amd.moe_ffn(x, layer, 4)
+    ro, ri, rw = bind.moe_block(layer, x, 4)
+    assert_same(idx, ri, "topk_idx")
+    assert (idx[1] == -1).all()
+    assert_same(out[[0, 2]], ro[[0, 2]], "out")
+    assert (out[1] == 0).all() and (ro[1] == 0).all()
+
+
+def test_repeat_calls_are_identical():
+    layer = synth_layer(23, 2048, 768, 128, synth.Q4_K, synth.Q6_K, None)
+    x = synth.make_input(23, 2, 2048)
+    a = tie_amd.moe_ffn(x, layer, 8)
+    for _ in range(3):
+        b = tie_amd.moe_ffn(x, layer, 8)
+        for p, q in zip(a, b):
+            assert_same(p, q, "repeat")
+
+
+def test_argument_errors_and_injected_oom():
+    layer = synth_layer(24, 256, 256, 16, synth.Q4_K, synth.Q6_K, None)
+    x = synth.make_input(24, 2, 256)
+    with pytest.raises(tie_amd.TieError) as e:
+        tie_amd.moe_ffn(x, layer, 17)  # k > E
+    assert e.value.code == tie_amd.EINVAL
+    lib = tie_amd.lib()
+    rc = lib.tie_hip_moe_ffn(x.ctypes.data, 2, 250, 256, 16, 4, layer.router.ctypes.data, 0, layer.gate.ctypes.data,
+                             12, layer.up.ctypes.data, 12, layer.down.ctypes.data, 14, x.ctypes.data, None, None)
+    assert rc == tie_amd.EINVAL and "multiples of 256" in tie_amd.last_error()
+    rc = lib.tie_hip_moe_ffn(x.ctypes.data, 2, 256, 256, 16, 4, layer.router.ctypes.data, 0, layer.gate.ctypes.data,
+                             3, layer.up.ctypes.data, 3, layer.down.ctypes.data, 14, x.ctypes.data, None, None)
+    assert rc == tie_amd.EINVAL
+    other = synth_layer(25, 256, 256, 16, synth.Q4_K, synth.Q6_K, None)
+    lib.tie_hip_debug_fail_alloc(1)
+    with pytest.raises(tie_amd.TieError) as e:
+        tie_amd.moe_ffn(x, other, 4)  # first call uploads: that allocation fails
+    assert e.value.code == tie_amd.ENOMEM
+    run_both(other, x, 4)  # and the library recovers

@@ -1,0 +1,187 @@
+"""tie_amd -- MI355X (gfx950) Qwen3-MoE FFN block for TIE.
+
+The product is the C-ABI library ``libtie_hip.so`` (include/tie_hip.h),
+built from tie_amd/csrc by tie_amd/Makefile.  This module is a thin ctypes
+binding used by the tests and bench.py; it mirrors the C entry points one to
+one and adds no computation of its own.  Importing it never falls back to a
+CPU path: if the library is missing, every call raises.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libtie_hip.so")
+
+F32, Q4_K, Q6_K, BF16 = 0, 12, 14, 30
+OK, EINVAL, EHIP, ENOMEM, ENOINIT = 0, -1, -2, -3, -4
+PATH_AUTO, PATH_EXACT, PATH_MFMA = 0, 1, 2
+SILU_TABLE_SIZE = 8192
+
+# every symbol include/tie_hip.h declares
+EXPORTS = (
+    "tie_hip_init", "tie_hip_shutdown", "tie_hip_last_error", "tie_hip_moe_ffn", "tie_hip_set_silu_table",
+    "tie_hip_silu_table_host", "tie_hip_layer_create", "tie_hip_layer_destroy", "tie_hip_layer_bytes",
+    "tie_hip_moe_forward", "tie_hip_exact_max_tokens", "tie_hip_set_exact_max_tokens",
+    "tie_hip_debug_fail_alloc", "tie_hip_host_expf",
+)
+
+
+class TieError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__("tie_hip error %d: %s" % (code, msg))
+        self.code = code
+
+
+class LayerDesc(ctypes.Structure):
+    _fields_ = [
+        ("d", ctypes.c_int), ("F", ctypes.c_int), ("E", ctypes.c_int),
+        ("router_w", ctypes.c_void_p), ("router_type", ctypes.c_int),
+        ("gate_exps", ctypes.c_void_p), ("gate_type", ctypes.c_int),
+        ("up_exps", ctypes.c_void_p), ("up_type", ctypes.c_int),
+        ("down_exps", ctypes.c_void_p), ("down_type", ctypes.c_int),
+        ("router_bias", ctypes.c_void_p),
+        ("src_on_device", ctypes.c_int),
+        ("literal_bf16_stride", ctypes.c_int),
+    ]
+
+
+_lib = None
+
+
+def lib():
+    """The loaded C-ABI library (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError("libtie_hip.so is not built: run `make -C tie_amd` or __graft_entry__.build()")
+        L = ctypes.CDLL(LIB_PATH)
+        P, I = ctypes.c_void_p, ctypes.c_int
+        L.tie_hip_init.argtypes = [I]
+        L.tie_hip_init.restype = I
+        L.tie_hip_shutdown.restype = None
+        L.tie_hip_last_error.restype = ctypes.c_char_p
+        L.tie_hip_moe_ffn.argtypes = [P, I, I, I, I, I, P, I, P, I, P, I, P, I, P, P, P]
+        L.tie_hip_moe_ffn.restype = I
+        L.tie_hip_set_silu_table.argtypes = [P, I]
+        L.tie_hip_set_silu_table.restype = I
+        L.tie_hip_silu_table_host.argtypes = [P, I]
+        L.tie_hip_silu_table_host.restype = I
+        L.tie_hip_layer_create.argtypes = [ctypes.POINTER(LayerDesc), ctypes.POINTER(ctypes.c_void_p)]
+        L.tie_hip_layer_create.restype = I
+        L.tie_hip_layer_destroy.argtypes = [P]
+        L.tie_hip_layer_destroy.restype = None
+        L.tie_hip_layer_bytes.argtypes = [P]
+        L.tie_hip_layer_bytes.restype = ctypes.c_size_t
+        L.tie_hip_moe_forward.argtypes = [P, P, I, I, P, P, P, I, P]
+        L.tie_hip_moe_forward.restype = I
+        L.tie_hip_exact_max_tokens.restype = I
+        L.tie_hip_set_exact_max_tokens.argtypes = [I]
+        L.tie_hip_set_exact_max_tokens.restype = None
+        L.tie_hip_debug_fail_alloc.argtypes = [I]
+        L.tie_hip_debug_fail_alloc.restype = None
+        L.tie_hip_host_expf.argtypes = [P, P, ctypes.c_size_t]
+        L.tie_hip_host_expf.restype = None
+        _lib = L
+    return _lib
+
+
+def last_error():
+    return lib().tie_hip_last_error().decode()
+
+
+def check(rc):
+    if rc != OK:
+        raise TieError(rc, last_error())
+    return rc
+
+
+def _p(a):
+    if a is None:
+        return None
+    if isinstance(a, int):
+        return a
+    if hasattr(a, "data_ptr"):
+        return a.data_ptr()
+    return a.ctypes.data
+
+
+def init(device=0):
+    check(lib().tie_hip_init(device))
+
+
+def shutdown():
+    lib().tie_hip_shutdown()
+
+
+def silu_table_host():
+    t = np.empty(SILU_TABLE_SIZE, np.float32)
+    check(lib().tie_hip_silu_table_host(_p(t), SILU_TABLE_SIZE))
+    return t
+
+
+def set_silu_table(table):
+    table = np.ascontiguousarray(table, np.float32)
+    check(lib().tie_hip_set_silu_table(_p(table), table.size))
+
+
+def host_expf(x):
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty_like(x)
+    lib().tie_hip_host_expf(_p(x), _p(out), x.size)
+    return out
+
+
+def moe_ffn(x, layer, k, with_topk=True):
+    """tie_hip_moe_ffn on host arrays (the drop-in for model_qwen3.c:404-471).
+    `layer` is a tie_amd.synth.MoELayer (GGUF-layout host arrays)."""
+    x = np.ascontiguousarray(x, np.float32)
+    T, d = x.shape
+    out = np.empty((T, d), np.float32)
+    idx = np.empty((T, k), np.int32) if with_topk else None
+    w = np.empty((T, k), np.float32) if with_topk else None
+    if layer.bias is not None:
+        raise ValueError("tie_hip_moe_ffn has no router bias (TIE has none); use Layer for biased routing")
+    check(lib().tie_hip_moe_ffn(_p(x), T, d, layer.F, layer.E, k, _p(layer.router), F32, _p(layer.gate),
+                                layer.gate_type, _p(layer.up), layer.up_type, _p(layer.down), layer.down_type,
+                                _p(out), _p(idx), _p(w)))
+    return out, idx, w
+
+
+class Layer:
+    """A device-resident layer (tie_hip_layer_create).  Weight sources are
+    host numpy arrays or device tensors (anything with data_ptr())."""
+
+    def __init__(self, d, F, E, router, gate, up, down, gate_type, up_type, down_type, bias=None,
+                 on_device=False, literal_bf16_stride=False):
+        self.d, self.F, self.E = d, F, E
+        desc = LayerDesc(d, F, E, _p(router), F32, _p(gate), gate_type, _p(up), up_type, _p(down), down_type,
+                         _p(bias), int(on_device), int(literal_bf16_stride))
+        h = ctypes.c_void_p()
+        check(lib().tie_hip_layer_create(ctypes.byref(desc), ctypes.byref(h)))
+        self.handle = h
+
+    @classmethod
+    def from_synth(cls, s, literal_bf16_stride=False):
+        return cls(s.d, s.F, s.E, s.router, s.gate, s.up, s.down, s.gate_type, s.up_type, s.down_type,
+                   bias=s.bias, literal_bf16_stride=literal_bf16_stride)
+
+    def nbytes(self):
+        return lib().tie_hip_layer_bytes(self.handle)
+
+    def forward(self, x_dev, T, k, out_dev, topk_idx_dev=None, topk_w_dev=None, flags=PATH_AUTO, stream=None):
+        """Enqueue the block on device pointers (torch tensors or ints)."""
+        check(lib().tie_hip_moe_forward(self.handle, _p(x_dev), T, k, _p(out_dev), _p(topk_idx_dev),
+                                        _p(topk_w_dev), flags, stream))
+
+    def close(self):
+        if self.handle:
+            lib().tie_hip_layer_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

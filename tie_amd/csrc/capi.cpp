@@ -1,0 +1,503 @@
+// capi.cpp -- the C ABI (include/tie_hip.h): device state, weight upload
+// and cache, workspace, and the forward orchestration.
+#include <hip/hip_runtime.h>
+
+#include <map>
+#include <mutex>
+#include <string.h>
+#include <tuple>
+#include <vector>
+
+#include "common.h"
+
+namespace tie {
+int set_error(int code, const char *fmt, ...);
+void clear_error();
+int silu_table_host(float *tab, int n);
+} // namespace tie
+
+struct tie_hip_layer {
+	tie::Layer L;
+};
+
+namespace tie {
+
+struct Ctx {
+	int device = -1;
+	hipStream_t stream = nullptr;
+	float *silu = nullptr;
+	Workspace ws;
+	// host-pointer API: cached layers and staging buffers
+	std::map<std::tuple<const void *, const void *, const void *, const void *, int, int, int, int, int, int>,
+		 tie_hip_layer *>
+		cache;
+	float *x_dev = nullptr, *out_dev = nullptr, *w_dev = nullptr;
+	int32_t *idx_dev = nullptr;
+	size_t io_tokens = 0, io_d = 0, io_k = 0;
+	int exact_max_t = 64;
+	std::recursive_mutex mu;
+};
+
+static Ctx g;
+static int g_fail_alloc = 0;
+
+#define HIP_TRY(expr)                                                                                        \
+	do {                                                                                                 \
+		hipError_t e_ = (expr);                                                                      \
+		if (e_ != hipSuccess)                                                                        \
+			return set_error(TIE_HIP_EHIP, "%s failed: %s", #expr, hipGetErrorString(e_));      \
+	} while (0)
+
+static int dev_malloc(void **p, size_t bytes, const char *what)
+{
+	*p = nullptr;
+	if (g_fail_alloc > 0 && --g_fail_alloc == 0)
+		return set_error(TIE_HIP_ENOMEM, "injected allocation failure (%s, %zu bytes)", what, bytes);
+	if (bytes == 0)
+		bytes = 256;
+	hipError_t e = hipMalloc(p, bytes);
+	if (e != hipSuccess) {
+		*p = nullptr;
+		(void)hipGetLastError();
+		return set_error(TIE_HIP_ENOMEM, "hipMalloc(%zu) for %s failed: %s", bytes, what, hipGetErrorString(e));
+	}
+	return TIE_HIP_OK;
+}
+
+static size_t align256(size_t n)
+{
+	return (n + 255) & ~(size_t)255;
+}
+
+static bool expert_type_ok(int t)
+{
+	return t == TIE_GGML_Q4_K || t == TIE_GGML_Q6_K || t == TIE_GGML_BF16;
+}
+
+static size_t row_bytes(int type, int in)
+{
+	switch (type) {
+	case TIE_GGML_F32:
+		return (size_t)in * 4;
+	case TIE_GGML_BF16:
+		return (size_t)in * 2;
+	case TIE_GGML_Q4_K:
+		return (size_t)(in / QK) * Q4K_BYTES;
+	case TIE_GGML_Q6_K:
+		return (size_t)(in / QK) * Q6K_BYTES;
+	}
+	return 0;
+}
+
+static int check_shape(int d, int F, int E)
+{
+	if (d <= 0 || F <= 0 || E <= 0)
+		return set_error(TIE_HIP_EINVAL, "bad shape d=%d F=%d E=%d", d, F, E);
+	if (d % QK || F % QK)
+		return set_error(TIE_HIP_EINVAL, "d=%d and F=%d must be multiples of 256", d, F);
+	if (d > 64 * QK || F > 64 * QK)
+		return set_error(TIE_HIP_EINVAL, "d=%d, F=%d above the supported 16384", d, F);
+	if (E > MAX_E)
+		return set_error(TIE_HIP_EINVAL, "E=%d above %d", E, MAX_E);
+	return TIE_HIP_OK;
+}
+
+static int ensure_init()
+{
+	if (g.device < 0)
+		return set_error(TIE_HIP_ENOINIT, "tie_hip_init() has not been called");
+	HIP_TRY(hipSetDevice(g.device));
+	return TIE_HIP_OK;
+}
+
+// Grow the per-forward workspace to hold T tokens.
+static int ensure_workspace(int T, int k, int d, int F, int E)
+{
+	Workspace &w = g.ws;
+	const size_t pairs = (size_t)(T > 0 ? T : 1) * k;
+	if (w.alloc && pairs <= w.cap_pairs && (size_t)F <= w.cap_F && (size_t)d <= w.cap_d && (size_t)E <= w.cap_E)
+		return TIE_HIP_OK;
+	const size_t P = pairs > w.cap_pairs ? pairs : w.cap_pairs;
+	const size_t FF = (size_t)F > w.cap_F ? F : w.cap_F;
+	const size_t DD = (size_t)d > w.cap_d ? d : w.cap_d;
+	const size_t EE = (size_t)E > w.cap_E ? E : w.cap_E;
+	const size_t Tcap = P; // tokens <= pairs since k >= 1
+	size_t off = 0;
+	auto take = [&](size_t bytes) {
+		size_t o = off;
+		off += align256(bytes);
+		return o;
+	};
+	const size_t o_idx = take(P * 4), o_w = take(P * 4), o_cnt = take(EE * 4), o_off = take((EE + 1) * 4),
+		     o_pairs = take(P * 4), o_act = take((EE + 1) * 4), o_sync = take(64 * 4),
+		     o_logits = take(Tcap * EE * 4), o_h = take(3 * P * FF * 4), o_cnt2 = take(P * (FF / 64) * 4), o_hb = take(P * FF * 2),
+		     o_y = take(P * DD * 4);
+	void *mem = nullptr;
+	if (w.alloc) {
+		HIP_TRY(hipStreamSynchronize(g.stream));
+		HIP_TRY(hipFree(w.alloc));
+		w = Workspace();
+	}
+	int rc = dev_malloc(&mem, off, "workspace");
+	if (rc)
+		return rc;
+	uint8_t *b = (uint8_t *)mem;
+	w.alloc = mem;
+	w.topk_idx = (int32_t *)(b + o_idx);
+	w.topk_w = (float *)(b + o_w);
+	w.counts = (int32_t *)(b + o_cnt);
+	w.offsets = (int32_t *)(b + o_off);
+	w.pairs = (int32_t *)(b + o_pairs);
+	w.active = (int32_t *)(b + o_act);
+	w.sync = (uint32_t *)(b + o_sync);
+	w.logits = (float *)(b + o_logits);
+	w.h = (float *)(b + o_h);
+	w.tile_cnt = (uint32_t *)(b + o_cnt2);
+	w.hb = (uint16_t *)(b + o_hb);
+	w.y = (float *)(b + o_y);
+	w.cap_pairs = P;
+	w.cap_F = FF;
+	w.cap_d = DD;
+	w.cap_E = EE;
+	// completion counters start at zero and are reset by the kernels
+	HIP_TRY(hipMemsetAsync(w.sync, 0, 64 * 4, g.stream));
+	HIP_TRY(hipMemsetAsync(w.tile_cnt, 0, P * (FF / 64) * 4, g.stream));
+	HIP_TRY(hipStreamSynchronize(g.stream));
+	return TIE_HIP_OK;
+}
+
+static void free_layer(tie_hip_layer *l)
+{
+	if (!l)
+		return;
+	if (l->L.alloc)
+		(void)hipFree(l->L.alloc);
+	delete l;
+}
+
+static int create_layer(const tie_hip_layer_desc *ds, tie_hip_layer **out)
+{
+	*out = nullptr;
+	int rc = check_shape(ds->d, ds->F, ds->E);
+	if (rc)
+		return rc;
+	if (ds->router_type != TIE_GGML_F32)
+		return set_error(TIE_HIP_EINVAL, "router type %d unsupported (F32 only)", ds->router_type);
+	if (!expert_type_ok(ds->gate_type) || !expert_type_ok(ds->up_type) || !expert_type_ok(ds->down_type))
+		return set_error(TIE_HIP_EINVAL, "expert types %d/%d/%d unsupported (Q4_K, Q6_K, BF16)", ds->gate_type,
+				 ds->up_type, ds->down_type);
+	if (!ds->router_w || !ds->gate_exps || !ds->up_exps || !ds->down_exps)
+		return set_error(TIE_HIP_EINVAL, "null weight pointer");
+
+	const int d = ds->d, F = ds->F, E = ds->E;
+	tie_hip_layer *l = new tie_hip_layer();
+	Layer &L = l->L;
+	L.d = d;
+	L.F = F;
+	L.E = E;
+	auto setup = [&](ExpertTensor &t, int type, int rows, int in) {
+		t.type = type;
+		t.rows = rows;
+		t.in = in;
+		t.nb = in / QK;
+		t.rt = rows / PANEL_ROWS;
+		t.expert_bytes = (size_t)rows * row_bytes(type, in);
+	};
+	setup(L.gate, ds->gate_type, F, d);
+	setup(L.up, ds->up_type, F, d);
+	setup(L.down, ds->down_type, d, F);
+	const size_t b_router = align256((size_t)E * d * 4), b_bias = align256((size_t)E * 4);
+	const size_t b_gate = align256(E * L.gate.expert_bytes), b_up = align256(E * L.up.expert_bytes),
+		     b_down = align256(E * L.down.expert_bytes);
+	L.bytes = b_router + b_bias + b_gate + b_up + b_down;
+	rc = dev_malloc(&L.alloc, L.bytes, "layer weights");
+	if (rc) {
+		delete l;
+		return rc;
+	}
+	uint8_t *base = (uint8_t *)L.alloc;
+	L.router = (const float *)base;
+	L.bias = ds->router_bias ? (const float *)(base + b_router) : nullptr;
+	L.gate.data = base + b_router + b_bias;
+	L.up.data = L.gate.data + b_gate;
+	L.down.data = L.up.data + b_up;
+
+	const hipMemcpyKind kind = ds->src_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
+	hipError_t e = hipMemcpyAsync((void *)L.router, ds->router_w, (size_t)E * d * 4, kind, g.stream);
+	if (e == hipSuccess && ds->router_bias)
+		e = hipMemcpyAsync((void *)L.bias, ds->router_bias, (size_t)E * 4, kind, g.stream);
+	struct Src {
+		const ExpertTensor *t;
+		const void *p;
+	} srcs[3] = {{&L.gate, ds->gate_exps}, {&L.up, ds->up_exps}, {&L.down, ds->down_exps}};
+	void *tmp = nullptr;
+	for (int i = 0; i < 3 && e == hipSuccess; i++) {
+		const size_t n = (size_t)E * srcs[i].t->expert_bytes;
+		const uint8_t *src = (const uint8_t *)srcs[i].p;
+		if (!ds->src_on_device) {
+			rc = dev_malloc(&tmp, n, "upload staging");
+			if (rc)
+				break;
+			e = hipMemcpyAsync(tmp, srcs[i].p, n, hipMemcpyHostToDevice, g.stream);
+			src = (const uint8_t *)tmp;
+		}
+		if (e == hipSuccess)
+			e = launch_repack(*srcs[i].t, src, E, ds->literal_bf16_stride, g.stream);
+		if (e == hipSuccess)
+			e = hipStreamSynchronize(g.stream);
+		if (tmp) {
+			(void)hipFree(tmp);
+			tmp = nullptr;
+		}
+	}
+	if (e == hipSuccess && rc == 0)
+		e = hipStreamSynchronize(g.stream);
+	if (rc || e != hipSuccess) {
+		free_layer(l);
+		if (rc)
+			return rc;
+		return set_error(TIE_HIP_EHIP, "layer upload failed: %s", hipGetErrorString(e));
+	}
+	*out = l;
+	return TIE_HIP_OK;
+}
+
+static int forward(tie_hip_layer *layer, const float *x, int T, int k, float *out, int32_t *idx_out,
+		   float *w_out, int flags, hipStream_t s)
+{
+	if (!layer)
+		return set_error(TIE_HIP_EINVAL, "null layer");
+	const Layer &L = layer->L;
+	if (T < 0)
+		return set_error(TIE_HIP_EINVAL, "T=%d < 0", T);
+	if (k < 1 || k > L.E || k > MAX_K)
+		return set_error(TIE_HIP_EINVAL, "k=%d outside [1, min(E=%d, %d)]", k, L.E, MAX_K);
+	if (T == 0)
+		return TIE_HIP_OK;
+	if (!x || !out)
+		return set_error(TIE_HIP_EINVAL, "null x/out");
+	const bool mfma = (flags & TIE_HIP_PATH_MFMA) || (!(flags & TIE_HIP_PATH_EXACT) && T > g.exact_max_t);
+	if (mfma && (flags & TIE_HIP_PATH_MFMA))
+		return set_error(TIE_HIP_EINVAL, "the MFMA path is not built in this version");
+	if (L.d > 16 * QK || L.F > 16 * QK)
+		return set_error(TIE_HIP_EINVAL, "exact path supports d, F <= 4096");
+	int rc = ensure_workspace(T, k, L.d, L.F, L.E);
+	if (rc)
+		return rc;
+	Workspace &ws = g.ws;
+	HIP_TRY(launch_router(L, x, T, k, ws.logits, ws.topk_idx, ws.topk_w, ws.sync, s));
+	HIP_TRY(launch_dispatch(L, T, k, ws.topk_idx, ws, s));
+	HIP_TRY(launch_exact_experts(L, x, T, k, g.silu, ws, s));
+	HIP_TRY(launch_combine(T, L.d, k, ws.topk_w, ws.topk_idx, ws.y, out, s));
+	if (idx_out)
+		HIP_TRY(hipMemcpyAsync(idx_out, ws.topk_idx, (size_t)T * k * 4, hipMemcpyDeviceToDevice, s));
+	if (w_out)
+		HIP_TRY(hipMemcpyAsync(w_out, ws.topk_w, (size_t)T * k * 4, hipMemcpyDeviceToDevice, s));
+	return TIE_HIP_OK;
+}
+
+} // namespace tie
+
+using namespace tie;
+
+extern "C" int tie_hip_init(int device)
+{
+	std::lock_guard<std::recursive_mutex> lk(g.mu);
+	clear_error();
+	if (g.device >= 0) {
+		if (g.device == device)
+			return TIE_HIP_OK;
+		return set_error(TIE_HIP_EINVAL, "already initialised on device %d", g.device);
+	}
+	int n = 0;
+	HIP_TRY(hipGetDeviceCount(&n));
+	if (device < 0 || device >= n)
+		return set_error(TIE_HIP_EINVAL, "device %d not present (%d devices)", device, n);
+	HIP_TRY(hipSetDevice(device));
+	HIP_TRY(hipStreamCreateWithFlags(&g.stream, hipStreamNonBlocking));
+	std::vector<float> tab(SILU_N);
+	int rc = silu_table_host(tab.data(), SILU_N);
+	if (rc)
+		return rc;
+	rc = dev_malloc((void **)&g.silu, SILU_N * sizeof(float), "silu table");
+	if (rc)
+		return rc;
+	HIP_TRY(hipMemcpy(g.silu, tab.data(), SILU_N * sizeof(float), hipMemcpyHostToDevice));
+	g.device = device;
+	return TIE_HIP_OK;
+}
+
+extern "C" void tie_hip_shutdown(void)
+{
+	std::lock_guard<std::recursive_mutex> lk(g.mu);
+	if (g.device < 0)
+		return;
+	(void)hipSetDevice(g.device);
+	(void)hipStreamSynchronize(g.stream);
+	for (auto &kv : g.cache)
+		free_layer(kv.second);
+	g.cache.clear();
+	if (g.ws.alloc)
+		(void)hipFree(g.ws.alloc);
+	g.ws = Workspace();
+	for (void *p : {(void *)g.x_dev, (void *)g.out_dev, (void *)g.w_dev, (void *)g.idx_dev, (void *)g.silu})
+		if (p)
+			(void)hipFree(p);
+	g.x_dev = g.out_dev = g.w_dev = nullptr;
+	g.idx_dev = nullptr;
+	g.silu = nullptr;
+	g.io_tokens = g.io_d = g.io_k = 0;
+	(void)hipStreamDestroy(g.stream);
+	g.stream = nullptr;
+	g.device = -1;
+}
+
+extern "C" int tie_hip_set_silu_table(const float *table, int n)
+{
+	std::lock_guard<std::recursive_mutex> lk(g.mu);
+	clear_error();
+	int rc = ensure_init();
+	if (rc)
+		return rc;
+	if (!table || n != SILU_N)
+		return set_error(TIE_HIP_EINVAL, "silu table needs %d entries", SILU_N);
+	HIP_TRY(hipStreamSynchronize(g.stream));
+	HIP_TRY(hipMemcpy(g.silu, table, SILU_N * sizeof(float), hipMemcpyHostToDevice));
+	return TIE_HIP_OK;
+}
+
+extern "C" int tie_hip_layer_create(const tie_hip_layer_desc *desc, tie_hip_layer **out)
+{
+	std::lock_guard<std::recursive_mutex> lk(g.mu);
+	clear_error();
+	if (!out || !desc)
+		return set_error(TIE_HIP_EINVAL, "null argument");
+	*out = nullptr;
+	int rc = ensure_init();
+	if (rc)
+		return rc;
+	return create_layer(desc, out);
+}
+
+extern "C" void tie_hip_layer_destroy(tie_hip_layer *layer)
+{
+	std::lock_guard<std::recursive_mutex> lk(g.mu);
+	if (!layer)
+		return;
+	if (g.device >= 0)
+		(void)hipStreamSynchronize(g.stream);
+	free_layer(layer);
+}
+
+extern "C" size_t tie_hip_layer_bytes(const tie_hip_layer *layer)
+{
+	return layer ? layer->L.bytes : 0;
+}
+
+extern "C" int tie_hip_moe_forward(tie_hip_layer *layer, const float *x_dev, int T, int k, float *out_dev,
+				   int32_t *topk_idx_dev, float *topk_w_dev, int flags, void *stream)
+{
+	std::lock_guard<std::recursive_mutex> lk(g.mu);
+	clear_error();
+	int rc = ensure_init();
+	if (rc)
+		return rc;
+	hipStream_t s = stream ? (hipStream_t)stream : g.stream;
+	return forward(layer, x_dev, T, k, out_dev, topk_idx_dev, topk_w_dev, flags, s);
+}
+
+extern "C" int tie_hip_moe_ffn(const float *x, int T, int d, int F, int E, int k, const void *router_w,
+			       int router_type, const void *gate_exps, int gate_type, const void *up_exps, int up_type,
+			       const void *down_exps, int down_type, float *out, int32_t *topk_idx_opt,
+			       float *topk_w_opt)
+{
+	std::lock_guard<std::recursive_mutex> lk(g.mu);
+	clear_error();
+	int rc = ensure_init();
+	if (rc)
+		return rc;
+	rc = check_shape(d, F, E);
+	if (rc)
+		return rc;
+	if (T < 0 || (T > 0 && (!x || !out)))
+		return set_error(TIE_HIP_EINVAL, "bad T=%d or null x/out", T);
+	auto key = std::make_tuple(router_w, gate_exps, up_exps, down_exps, router_type, gate_type, up_type, down_type,
+				   d * 4096 + (F >> 8), E);
+	tie_hip_layer *layer = nullptr;
+	auto it = g.cache.find(key);
+	if (it != g.cache.end()) {
+		layer = it->second;
+		if (layer->L.d != d || layer->L.F != F || layer->L.E != E)
+			layer = nullptr;
+	}
+	if (!layer) {
+		tie_hip_layer_desc ds;
+		memset(&ds, 0, sizeof ds);
+		ds.d = d;
+		ds.F = F;
+		ds.E = E;
+		ds.router_w = router_w;
+		ds.router_type = router_type;
+		ds.gate_exps = gate_exps;
+		ds.gate_type = gate_type;
+		ds.up_exps = up_exps;
+		ds.up_type = up_type;
+		ds.down_exps = down_exps;
+		ds.down_type = down_type;
+		rc = create_layer(&ds, &layer);
+		if (rc)
+			return rc;
+		g.cache[key] = layer;
+	}
+	if (T == 0)
+		return TIE_HIP_OK;
+	if (k < 1 || k > E || k > MAX_K)
+		return set_error(TIE_HIP_EINVAL, "k=%d outside [1, min(E=%d, %d)]", k, E, MAX_K);
+	if ((size_t)T > g.io_tokens || (size_t)d > g.io_d || (size_t)k > g.io_k) {
+		HIP_TRY(hipStreamSynchronize(g.stream));
+		for (void *p : {(void *)g.x_dev, (void *)g.out_dev, (void *)g.w_dev, (void *)g.idx_dev})
+			if (p)
+				(void)hipFree(p);
+		g.x_dev = g.out_dev = g.w_dev = nullptr;
+		g.idx_dev = nullptr;
+		g.io_tokens = g.io_d = g.io_k = 0;
+		const size_t nt = T, nd = d, nk = k;
+		if ((rc = dev_malloc((void **)&g.x_dev, nt * nd * 4, "x staging")) ||
+		    (rc = dev_malloc((void **)&g.out_dev, nt * nd * 4, "out staging")) ||
+		    (rc = dev_malloc((void **)&g.w_dev, nt * nk * 4, "topk staging")) ||
+		    (rc = dev_malloc((void **)&g.idx_dev, nt * nk * 4, "topk staging")))
+			return rc;
+		g.io_tokens = nt;
+		g.io_d = nd;
+		g.io_k = nk;
+	}
+	HIP_TRY(hipMemcpyAsync(g.x_dev, x, (size_t)T * d * 4, hipMemcpyHostToDevice, g.stream));
+	rc = forward(layer, g.x_dev, T, k, g.out_dev, topk_idx_opt ? g.idx_dev : nullptr,
+		     topk_w_opt ? g.w_dev : nullptr, TIE_HIP_PATH_AUTO, g.stream);
+	if (rc)
+		return rc;
+	HIP_TRY(hipMemcpyAsync(out, g.out_dev, (size_t)T * d * 4, hipMemcpyDeviceToHost, g.stream));
+	if (topk_idx_opt)
+		HIP_TRY(hipMemcpyAsync(topk_idx_opt, g.idx_dev, (size_t)T * k * 4, hipMemcpyDeviceToHost, g.stream));
+	if (topk_w_opt)
+		HIP_TRY(hipMemcpyAsync(topk_w_opt, g.w_dev, (size_t)T * k * 4, hipMemcpyDeviceToHost, g.stream));
+	HIP_TRY(hipStreamSynchronize(g.stream));
+	return TIE_HIP_OK;
+}
+
+extern "C" int tie_hip_exact_max_tokens(void)
+{
+	return g.exact_max_t;
+}
+
+extern "C" void tie_hip_set_exact_max_tokens(int t)
+{
+	std::lock_guard<std::recursive_mutex> lk(g.mu);
+	g.exact_max_t = t < 0 ? 0 : t;
+}
+
+extern "C" void tie_hip_debug_fail_alloc(int n)
+{
+	std::lock_guard<std::recursive_mutex> lk(g.mu);
+	g_fail_alloc = n < 0 ? 0 : n;
+}

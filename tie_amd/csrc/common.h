@@ -1,0 +1,146 @@
+// common.h -- shared definitions of the gfx950 MoE block kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "../../include/tie_hip.h"
+
+namespace tie {
+
+constexpr int QK = 256;          // weights per K-quant super-block
+constexpr int Q4K_BYTES = 144;   // block_q4_k (gguf.h:108-113)
+constexpr int Q6K_BYTES = 210;   // block_q6_k (gguf.h:101-106)
+constexpr int PANEL_ROWS = 64;   // rows per weight panel = one wave64, one row per lane
+constexpr int Q4K_CHUNKS = 9;    // 144 B = 9 x 16 B
+constexpr int Q6K_CHUNKS = 13;   // ql 8 + qh 4 + scales 1 chunks of 16 B; d in a 128 B plane
+constexpr size_t Q4K_PANEL = (size_t)PANEL_ROWS * Q4K_BYTES; // 9216
+constexpr size_t Q6K_PANEL = (size_t)PANEL_ROWS * Q6K_BYTES; // 13440
+constexpr int MAX_K = 32;
+constexpr int MAX_E = 1024;
+constexpr int SILU_N = TIE_SILU_TABLE_SIZE;
+
+// Device layout of one stacked expert tensor [E][rows][in].
+//
+// Q4_K / Q6_K: "panels".  Rows are grouped 64 at a time (one per lane of a
+// wave64); panel (e, rt, b) holds block column b of rows rt*64 .. rt*64+63
+// of expert e.  Inside a panel, 16-byte chunk c of the block of lane i
+// sits at c*1024 + i*16, so a wave reads each chunk of its 64 blocks with
+// one fully coalesced 1 KiB global_load_dwordx4.  Q6_K's 210-byte blocks
+// are split into ql (8 chunks), qh (4), scales (1) and a trailing plane of
+// 64 fp16 d values, so the panel is exactly 64*210 bytes: no padding, no
+// extra HBM traffic.  The panel is also the (64 x 256) weight tile the
+// grouped GEMM dequantises into LDS.
+//
+// BF16: GGUF row-major [E][rows][in], unchanged.
+struct ExpertTensor {
+	const uint8_t *data = nullptr;
+	int type = 0;
+	int rows = 0, in = 0;   // per expert
+	int nb = 0;             // in / 256 (quantised types)
+	int rt = 0;             // rows / 64
+	size_t expert_bytes = 0;
+};
+
+__host__ __device__ inline size_t panel_bytes(int type)
+{
+	return type == TIE_GGML_Q4_K ? Q4K_PANEL : Q6K_PANEL;
+}
+
+struct Layer {
+	int d = 0, F = 0, E = 0;
+	const float *router = nullptr; // [E][d]
+	const float *bias = nullptr;   // [E] or null
+	ExpertTensor gate, up, down;
+	void *alloc = nullptr;         // one device allocation holding everything
+	size_t bytes = 0;
+};
+
+// Per-forward scratch (grown on demand, one per device).
+struct Workspace {
+	int32_t *topk_idx = nullptr;  // [T][k]
+	float *topk_w = nullptr;      // [T][k]
+	int32_t *counts = nullptr;    // [E]      tokens per expert
+	int32_t *offsets = nullptr;   // [E+1]    start of each expert's pair list
+	int32_t *pairs = nullptr;     // [T*k]    pair ids t*k+j grouped by expert
+	int32_t *active = nullptr;    // [E+1]    active experts; active[E] = count
+	uint32_t *sync = nullptr;     // [64]     grid-completion counters (self-resetting)
+	float *logits = nullptr;      // [T][E]   router logits
+	float *h = nullptr;           // [3][T*k][F] SwiGLU output, gate sums, up sums (exact path)
+	uint32_t *tile_cnt = nullptr; // [T*k][F/64] gate/up completion counters (self-resetting)
+	uint16_t *hb = nullptr;       // [T*k][F] SwiGLU activations (bf16 hi/lo, MFMA path)
+	float *y = nullptr;           // [T*k][d] expert outputs
+	size_t cap_pairs = 0, cap_F = 0, cap_d = 0, cap_E = 0;
+	void *alloc = nullptr;
+};
+
+// ---------------------------------------------------------------- launchers
+hipError_t launch_router(const Layer &L, const float *x, int T, int k, float *logits, int32_t *topk_idx,
+			 float *topk_w, uint32_t *counter, hipStream_t s);
+hipError_t launch_dispatch(const Layer &L, int T, int k, const int32_t *topk_idx, Workspace &ws, hipStream_t s);
+hipError_t launch_exact_experts(const Layer &L, const float *x, int T, int k, const float *silu, Workspace &ws,
+				hipStream_t s);
+hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, const float *silu, Workspace &ws,
+			       hipStream_t s);
+hipError_t launch_combine(int T, int d, int k, const float *topk_w, const int32_t *topk_idx, const float *y,
+			  float *out, hipStream_t s);
+hipError_t launch_repack(const ExpertTensor &dst, const uint8_t *src, int E, int literal_bf16_stride, hipStream_t s);
+
+// ---------------------------------------------------------------- device helpers
+#if defined(__HIPCC__)
+// The 8-lane horizontal sum of an AVX2 accumulator (lo+hi, hadd, hadd).
+__device__ __forceinline__ float hsum8(const float v[8])
+{
+	float s0 = v[0] + v[4], s1 = v[1] + v[5], s2 = v[2] + v[6], s3 = v[3] + v[7];
+	return (s0 + s1) + (s2 + s3);
+}
+
+// IEEE binary16 -> binary32, exact, in integer arithmetic (independent of
+// the denormal mode).
+__device__ __forceinline__ float half_bits_to_float(uint32_t h)
+{
+	uint32_t sign = (h & 0x8000u) << 16;
+	uint32_t e = (h >> 10) & 0x1f;
+	uint32_t m = h & 0x3ff;
+	uint32_t bits;
+	if (e == 0x1f) {
+		bits = sign | 0x7f800000u | (m << 13);
+	} else if (e != 0) {
+		bits = sign | ((e + 112u) << 23) | (m << 13);
+	} else if (m != 0) {
+		// value m * 2^-24 with the leading one at bit p
+		int p = 31 - __builtin_clz(m);
+		bits = sign | ((uint32_t)(p + 103) << 23) | ((m << (23 - p)) & 0x7fffffu);
+	} else {
+		bits = sign;
+	}
+	return __uint_as_float(bits);
+}
+
+__device__ __forceinline__ float bf16_bits_to_float(uint32_t b)
+{
+	return __uint_as_float(b << 16);
+}
+
+// TIE's table SiLU x gate (swiglu_activation_f32_f32_avx2,
+// math_avx2.c:908-950): pos = ((x + 10) * 8191) * 0.05f, round half to even
+// with CVTPS2DQ's INT_MIN for NaN / out-of-range, clamp to [0, 8190],
+// interpolate with one FMA; then multiply by up.
+__device__ __forceinline__ float tie_swiglu(float g, float u, const float *__restrict__ tab)
+{
+	float pos = ((g + 10.0f) * 8191.0f) * 0.05f;
+	int idx;
+	if (pos >= -2147483648.0f && pos < 2147483648.0f)
+		idx = (int)__builtin_rintf(pos);
+	else
+		idx = (int)0x80000000;
+	idx = idx < 0 ? 0 : idx;
+	idx = idx > SILU_N - 2 ? SILU_N - 2 : idx;
+	float frac = pos - (float)idx;
+	float y1 = tab[idx], y2 = tab[idx + 1];
+	float s = __builtin_fmaf(frac, y2 - y1, y1);
+	return s * u;
+}
+#endif
+
+} // namespace tie
