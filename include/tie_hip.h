@@ -126,6 +126,16 @@ void tie_hip_set_exact_max_tokens(int t);
  * 0 disarms).  Host-side fault injection for error-path tests. */
 void tie_hip_debug_fail_alloc(int n);
 
+/* Per-kernel timing: while enabled, every kernel the library launches is
+ * bracketed by HIP events recorded on its launch stream.  Enabling (or
+ * disabling) clears what was collected. */
+int tie_hip_profile_enable(int on);
+
+/* Sum of event-timed durations and launch count per kernel name since the
+ * last tie_hip_profile_enable(1); names come back comma-separated in
+ * `names`.  Synchronises the device.  Returns the number of names. */
+int tie_hip_profile_read(char *names, size_t names_cap, double *total_ms, int *launches, int max_kernels);
+
 /* Host build of the device expf (tie_expf.h) over n inputs, for checking
  * it against the host libm (no GPU needed). */
 void tie_hip_host_expf(const float *in, float *out, size_t n);

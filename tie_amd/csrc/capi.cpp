@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 
 #include <map>
+#include <string>
 #include <mutex>
 #include <string.h>
 #include <tuple>
@@ -40,6 +41,72 @@ struct Ctx {
 
 static Ctx g;
 static int g_fail_alloc = 0;
+
+// ---------------------------------------------------------------- profiling
+struct ProfRec {
+	int name;
+	hipEvent_t a, b;
+};
+static bool g_prof = false;
+static std::vector<std::string> g_prof_names;
+static std::vector<ProfRec> g_prof_recs;
+static std::vector<hipEvent_t> g_prof_pool;
+static int g_prof_open = -1;
+
+static hipEvent_t prof_event()
+{
+	if (!g_prof_pool.empty()) {
+		hipEvent_t e = g_prof_pool.back();
+		g_prof_pool.pop_back();
+		return e;
+	}
+	hipEvent_t e = nullptr;
+	if (hipEventCreate(&e) != hipSuccess)
+		return nullptr;
+	return e;
+}
+
+void prof_begin(const char *name, hipStream_t s)
+{
+	if (!g_prof)
+		return;
+	int id = -1;
+	for (size_t i = 0; i < g_prof_names.size(); i++)
+		if (g_prof_names[i] == name)
+			id = (int)i;
+	if (id < 0) {
+		id = (int)g_prof_names.size();
+		g_prof_names.push_back(name);
+	}
+	ProfRec r{id, prof_event(), prof_event()};
+	if (r.a)
+		(void)hipEventRecord(r.a, s);
+	g_prof_recs.push_back(r);
+	g_prof_open = (int)g_prof_recs.size() - 1;
+}
+
+void prof_end(hipStream_t s)
+{
+	if (!g_prof || g_prof_open < 0)
+		return;
+	ProfRec &r = g_prof_recs[g_prof_open];
+	if (r.b)
+		(void)hipEventRecord(r.b, s);
+	g_prof_open = -1;
+}
+
+static void prof_reset()
+{
+	for (auto &r : g_prof_recs) {
+		if (r.a)
+			g_prof_pool.push_back(r.a);
+		if (r.b)
+			g_prof_pool.push_back(r.b);
+	}
+	g_prof_recs.clear();
+	g_prof_names.clear();
+	g_prof_open = -1;
+}
 
 #define HIP_TRY(expr)                                                                                        \
 	do {                                                                                                 \
@@ -285,10 +352,16 @@ static int forward(tie_hip_layer *layer, const float *x, int T, int k, float *ou
 	if (rc)
 		return rc;
 	Workspace &ws = g.ws;
+	prof_begin("router", s);
 	HIP_TRY(launch_router(L, x, T, k, ws.logits, ws.topk_idx, ws.topk_w, ws.sync, s));
+	prof_end(s);
+	prof_begin("dispatch", s);
 	HIP_TRY(launch_dispatch(L, T, k, ws.topk_idx, ws, s));
+	prof_end(s);
 	HIP_TRY(launch_exact_experts(L, x, T, k, g.silu, ws, s));
+	prof_begin("combine", s);
 	HIP_TRY(launch_combine(T, L.d, k, ws.topk_w, ws.topk_idx, ws.y, out, s));
+	prof_end(s);
 	if (idx_out)
 		HIP_TRY(hipMemcpyAsync(idx_out, ws.topk_idx, (size_t)T * k * 4, hipMemcpyDeviceToDevice, s));
 	if (w_out)
@@ -500,4 +573,44 @@ extern "C" void tie_hip_debug_fail_alloc(int n)
 {
 	std::lock_guard<std::recursive_mutex> lk(g.mu);
 	g_fail_alloc = n < 0 ? 0 : n;
+}
+
+extern "C" int tie_hip_profile_enable(int on)
+{
+	std::lock_guard<std::recursive_mutex> lk(g.mu);
+	clear_error();
+	prof_reset();
+	g_prof = on != 0;
+	return TIE_HIP_OK;
+}
+
+extern "C" int tie_hip_profile_read(char *names, size_t names_cap, double *total_ms, int *launches, int max_kernels)
+{
+	std::lock_guard<std::recursive_mutex> lk(g.mu);
+	clear_error();
+	int rc = ensure_init();
+	if (rc)
+		return rc;
+	HIP_TRY(hipDeviceSynchronize());
+	const int n = (int)g_prof_names.size() < max_kernels ? (int)g_prof_names.size() : max_kernels;
+	std::string csv;
+	for (int i = 0; i < n; i++) {
+		total_ms[i] = 0.0;
+		launches[i] = 0;
+		csv += (i ? "," : "") + g_prof_names[i];
+	}
+	for (auto &r : g_prof_recs) {
+		if (r.name >= n || !r.a || !r.b)
+			continue;
+		float ms = 0.0f;
+		if (hipEventElapsedTime(&ms, r.a, r.b) == hipSuccess) {
+			total_ms[r.name] += ms;
+			launches[r.name] += 1;
+		}
+	}
+	if (names && names_cap) {
+		strncpy(names, csv.c_str(), names_cap - 1);
+		names[names_cap - 1] = 0;
+	}
+	return n;
 }

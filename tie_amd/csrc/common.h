@@ -86,6 +86,11 @@ hipError_t launch_combine(int T, int d, int k, const float *topk_w, const int32_
 			  float *out, hipStream_t s);
 hipError_t launch_repack(const ExpertTensor &dst, const uint8_t *src, int E, int literal_bf16_stride, hipStream_t s);
 
+// Per-kernel timing (tie_hip_profile_enable): HIP events recorded on the
+// launch stream around each kernel; no-ops while profiling is off.
+void prof_begin(const char *name, hipStream_t s);
+void prof_end(hipStream_t s);
+
 // ---------------------------------------------------------------- device helpers
 #if defined(__HIPCC__)
 // The 8-lane horizontal sum of an AVX2 accumulator (lo+hi, hadd, hadd).

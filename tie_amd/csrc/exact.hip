@@ -399,6 +399,7 @@ hipError_t launch_exact_experts(const Layer &L, const float *x, int T, int k, co
 	if (npairs == 0)
 		return hipSuccess;
 	hipError_t err;
+	prof_begin("exact_gate_up", s);
 	if (L.gate.type == L.up.type)
 		err = launch_rows<false>(L, 0, 2, L.gate, k, max_active, x, ws, silu, npairs, s);
 	else {
@@ -406,9 +407,13 @@ hipError_t launch_exact_experts(const Layer &L, const float *x, int T, int k, co
 		if (err == hipSuccess)
 			err = launch_rows<false>(L, 1, 1, L.up, k, max_active, x, ws, silu, npairs, s);
 	}
+	prof_end(s);
 	if (err != hipSuccess)
 		return err;
-	return launch_rows<true>(L, 0, 1, L.down, k, max_active, ws.h, ws, silu, npairs, s);
+	prof_begin("exact_down", s);
+	err = launch_rows<true>(L, 0, 1, L.down, k, max_active, ws.h, ws, silu, npairs, s);
+	prof_end(s);
+	return err;
 }
 
 } // namespace tie
