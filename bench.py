@@ -1,0 +1,318 @@
+"""Benchmark of the MI355X Qwen3-MoE FFN block (one GPU).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 30b_t32] [--extra 30b_t1,30b_t2048]
+
+A step is one MoE block forward (router, top-k, dispatch, experts, combine)
+over one batch of T tokens of synthetic input, with weights and inputs
+already resident in HBM.  Weights are cycled over L independently generated
+layers (and inputs over L token batches) so that no step finds its experts
+in the 256 MB MALL or the L2 left warm by the previous steps.
+
+Prints one JSON line: the headline workload (`value`, tokens/s), the
+roofline of its dominant kernel (event-timed on the library's stream), the
+CPU baseline (TIE's own compiled MoE path on the host cores, or the C
+restatement when the reference build cannot run here), and the extra
+workloads named by --extra.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import numpy as np  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+FP32_VALU_TFLOPS = 157.3    # MI355X fp32 (packed) vector peak
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------- workloads
+def gen_device_layer(torch, cfg, seed):
+    """GGUF-layout tensors for one layer, generated on the GPU (same
+    distributions as tie_amd.synth, different random stream)."""
+    from tie_amd import synth
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    d, F, E = cfg["d"], cfg["F"], cfg["E"]
+    dev = "cuda"
+
+    def half_abs(n):
+        return (torch.randn(n, generator=g, device=dev) * 0.01).abs().half().view(torch.uint8).reshape(n, 2)
+
+    def expert(wtype, rows, inn):
+        if wtype == synth.BF16:
+            w = torch.randn(E * rows * inn, generator=g, device=dev) * 0.02
+            return w.to(torch.bfloat16).view(torch.uint8)
+        nb = E * rows * (inn // 256)
+        if wtype == synth.Q4_K:
+            b = torch.randint(0, 256, (nb, 144), generator=g, device=dev, dtype=torch.uint8)
+            b[:, 0:2] = half_abs(nb)
+            b[:, 2:4] = half_abs(nb)
+        else:
+            b = torch.randint(0, 256, (nb, 210), generator=g, device=dev, dtype=torch.uint8)
+            b[:, 192:208] = torch.randint(-32, 32, (nb, 16), generator=g, device=dev,
+                                          dtype=torch.int8).view(torch.uint8)
+            b[:, 208:210] = half_abs(nb)
+        return b.reshape(-1)
+
+    router = torch.randn(E, d, generator=g, device=dev) * 0.02
+    gate = expert(cfg["gu_type"], F, d)
+    up = expert(cfg["gu_type"], F, d)
+    down = expert(cfg["down_type"], d, F)
+    bias = None
+    if cfg.get("zipf"):
+        bias = torch.from_numpy(synth.zipf_bias(E, s=cfg["zipf"], seed=seed + 7)).to(dev)
+    return router, gate, up, down, bias
+
+
+class Workload:
+    def __init__(self, torch, tie_amd, cfg, n_layers, seed0=4242):
+        self.cfg = cfg
+        self.layers = []
+        self.layer_bytes = 0
+        for i in range(n_layers):
+            r, g, u, dn, b = gen_device_layer(torch, cfg, seed0 + 17 * i)
+            L = tie_amd.Layer(cfg["d"], cfg["F"], cfg["E"], r, g, u, dn, cfg["gu_type"], cfg["gu_type"],
+                              cfg["down_type"], bias=b, on_device=True)
+            self.layer_bytes = L.nbytes()
+            self.layers.append(L)
+            del r, g, u, dn
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+
+
+def expert_bytes(cfg):
+    from tie_amd import synth
+    gu = cfg["F"] * synth.row_bytes(cfg["gu_type"], cfg["d"])
+    dn = cfg["d"] * synth.row_bytes(cfg["down_type"], cfg["F"])
+    return gu, dn
+
+
+def run_config(torch, tie_amd, wl, T, k, steps, warmup, flags):
+    """Times `steps` forwards of T tokens; returns the measurement dict."""
+    cfg = wl.cfg
+    d, F, E = cfg["d"], cfg["F"], cfg["E"]
+    nL = len(wl.layers)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(99)
+    X = torch.randn(nL, T, d, generator=gen, device="cuda")
+    out = torch.empty(T, d, device="cuda")
+    idx = torch.empty(nL, T, k, dtype=torch.int32, device="cuda")
+    w = torch.empty(nL, T, k, device="cuda")
+
+    def step(s, record_topk=False):
+        l = s % nL
+        wl.layers[l].forward(X[l], T, k, out, idx[l] if record_topk else None, w[l] if record_topk else None,
+                             flags=flags)
+
+    for s in range(nL):  # routing of every (layer, batch) pair, for the byte counts
+        step(s, record_topk=True)
+    for s in range(warmup):
+        step(s)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(steps):
+        step(s)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms = 1e3 * elapsed / steps
+
+    # per-kernel event timing over the same sequence of steps
+    tie_amd.profile_enable(True)
+    for s in range(steps):
+        step(s)
+    prof = tie_amd.profile_read()
+    tie_amd.profile_enable(False)
+
+    idx_h = idx.cpu().numpy()
+    U = np.array([len(np.unique(idx_h[l][idx_h[l] >= 0])) for l in range(nL)], np.float64)
+    U_avg = float(np.mean([U[s % nL] for s in range(steps)]))
+    gu_b, dn_b = expert_bytes(cfg)
+    pairs = T * k
+    kern_bytes = {
+        "router": E * d * 4 + T * d * 4,
+        "exact_gate_up": U_avg * gu_b + T * d * 4 + pairs * F * 4,
+        "exact_down": U_avg * dn_b + pairs * F * 4 + pairs * d * 4,
+        "combine": pairs * d * 4 + T * d * 4,
+        "dispatch": pairs * 4 * 2,
+        "mfma_gate_up": U_avg * gu_b + T * d * 4 + pairs * F * 2,
+        "mfma_down": U_avg * dn_b + pairs * F * 2 + pairs * d * 4,
+    }
+    kern_flops = {
+        "mfma_gate_up": 2.0 * pairs * 2 * F * d,
+        "mfma_down": 2.0 * pairs * F * d,
+        "exact_gate_up": 2.0 * pairs * 2 * F * d,
+        "exact_down": 2.0 * pairs * F * d,
+        "router": 2.0 * T * E * d,
+    }
+    block_bytes = E * d * 4 + U_avg * (gu_b + dn_b) + 2 * T * d * 4
+    block_flops = T * (2 * E * d + k * 6 * d * F)
+    kernels = {}
+    for name, (tot, n) in prof.items():
+        if n == 0:
+            continue
+        avg_ms = tot / n
+        kb = kern_bytes.get(name)
+        kf = kern_flops.get(name)
+        kernels[name] = {"avg_us": round(1e3 * avg_ms, 3), "launches": n,
+                         "alg_bytes": kb, "GBps": round(kb / (avg_ms * 1e-3) / 1e9, 1) if kb else None,
+                         "alg_flops": kf, "TFLOPs": round(kf / (avg_ms * 1e-3) / 1e12, 2) if kf else None}
+    return dict(T=T, k=k, ms=ms, tokens_per_s=T / (ms * 1e-3), U=U_avg, block_bytes=block_bytes,
+                block_flops=block_flops, block_GBps=block_bytes / (ms * 1e-3) / 1e9,
+                block_TFLOPs=block_flops / (ms * 1e-3) / 1e12, kernels=kernels, layers=nL)
+
+
+def roofline(m):
+    """Roofline object for the dominant (longest) kernel of a measurement."""
+    name, kd = max(m["kernels"].items(), key=lambda kv: kv[1]["avg_us"])
+    traffic = None
+    tfile = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(tfile):
+        with open(tfile) as f:
+            t = json.load(f)
+        traffic = t.get("%s@T%d" % (name, m["T"]))
+    # bound: MFMA when the kernel runs on the matrix cores and its algorithmic
+    # intensity is above the MI355X ridge point (2.5 PFLOP/s / 8 TB/s)
+    ridge = BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
+    mfma = name.startswith("mfma") and kd.get("alg_flops") and kd["alg_flops"] / kd["alg_bytes"] > ridge
+    if mfma:
+        return {"kernel": name, "bound": "mfma", "achieved": kd["TFLOPs"], "peak": BF16_PEAK_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(kd["TFLOPs"] / BF16_PEAK_TFLOPS, 4), "traffic": traffic,
+                "alg_flops_per_launch": kd["alg_flops"], "alg_bytes_per_launch": kd["alg_bytes"],
+                "avg_us": kd["avg_us"]}
+    achieved = kd["GBps"]
+    return {"kernel": name, "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+            "alg_bytes_per_launch": kd["alg_bytes"], "avg_us": kd["avg_us"]}
+
+
+# ---------------------------------------------------------------- CPU baseline
+def cpu_has(flag):
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("flags"):
+                    return flag in line.split()
+    except OSError:
+        pass
+    return False
+
+
+def cpu_baseline(cfg, k, budget_s=12.0):
+    """TIE's MoE path on the host cores: the reference's own sources compiled
+    (oracle/_ref, kind "reference") when its build can run on this CPU,
+    otherwise the C restatement (oracle/liboracle.so, kind "port")."""
+    from oracle import bind
+    from tie_amd import synth
+    layer = synth.make_layer(cfg["seed"], cfg["d"], cfg["F"], cfg["E"], cfg["gu_type"], cfg["down_type"],
+                             zipf=cfg.get("zipf"))
+    T = min(cfg["T"], 32)
+    x = synth.make_input(cfg["seed"], T, cfg["d"])
+    threads = 8  # TIE runs the k = 8 experts of a token as 8 pool tasks (model_qwen3.c:446-456)
+    use_ref = bind.ref_available() and cpu_has("avx512f") and cpu_has("avx2")
+    fn = (lambda: bind.ref_moe_block(layer, x, k, nthreads=threads)) if use_ref else \
+        (lambda: bind.moe_block(layer, x, k, nthreads=threads))
+    fn()  # warm-up (also builds the reference's thread pool)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    return {"value": round(n * T / el, 2), "unit": "tokens/s", "cores": threads,
+            "kind": "reference" if use_ref else "port",
+            "sample": "%d calls of T=%d tokens (%s weights, one layer) in %.1f s on %d host threads; nproc=%d" % (
+                n, T, synth.TYPE_NAMES[cfg["gu_type"]], el, threads, os.cpu_count() or 0)}
+
+
+# ---------------------------------------------------------------- main
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default="30b_t32")
+    ap.add_argument("--extra", default="30b_t1,30b_t2048")
+    ap.add_argument("--layers", type=int, default=0, help="weight layers cycled (0 = auto)")
+    ap.add_argument("--path", default="auto", choices=["auto", "exact", "mfma"])
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (collectives are out of scope); "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import tie_amd
+    from tie_amd import synth
+    tie_amd.init(0)
+    flags = {"auto": tie_amd.PATH_AUTO, "exact": tie_amd.PATH_EXACT, "mfma": tie_amd.PATH_MFMA}[args.path]
+
+    names = [args.config] + [c for c in args.extra.split(",") if c and c != args.config]
+    workloads = {}
+    results = {}
+    for name in names:
+        cfg = dict(synth.CONFIGS[name])
+        key = (cfg["d"], cfg["F"], cfg["E"], cfg["gu_type"], cfg["down_type"], cfg.get("zipf"))
+        if key not in workloads:
+            per_layer = cfg["E"] * sum(expert_bytes(cfg))
+            nL = args.layers or max(8, min(40, int(16e9 // per_layer)))
+            log("generating %d layers for %s (%.2f GB each)" % (nL, name, per_layer / 1e9))
+            workloads[key] = Workload(torch, tie_amd, cfg, nL)
+        steps = args.steps if name == args.config else max(10, args.steps // 4)
+        warm = args.warmup if name == args.config else max(2, args.warmup // 4)
+        log("timing %s: T=%d, %d warm-up + %d steps" % (name, cfg["T"], warm, steps))
+        results[name] = run_config(torch, tie_amd, workloads[key], cfg["T"], cfg["k"], steps, warm, flags)
+        log(json.dumps({name: results[name]}))
+
+    main_name = args.config
+    m = results[main_name]
+    cfg = synth.CONFIGS[main_name]
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline ...")
+        cpu = cpu_baseline(cfg, cfg["k"])
+    extra = {}
+    for name in names[1:]:
+        r = results[name]
+        extra[name] = {"tokens_per_s": round(r["tokens_per_s"], 1), "ms_per_step": round(r["ms"], 4),
+                       "block_GBps": round(r["block_GBps"], 1), "block_TFLOPs": round(r["block_TFLOPs"], 3),
+                       "roofline": roofline(r), "kernels": r["kernels"]}
+    line = {
+        "metric": "MoE block tokens/s (Qwen3-30B-A3B shape)",
+        "value": round(m["tokens_per_s"], 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(m["ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if any(k.startswith("mfma") for k in m["kernels"]) else "f32",
+        "data": "synthetic (seeded GGUF-layout Q4_K/Q6_K blocks, N(0,1) inputs; %d weight layers cycled)" % m[
+            "layers"],
+        "config": {"workload": "%s: d=%d F=%d E=%d k=%d T=%d, gate/up %s, down %s" % (
+            main_name, cfg["d"], cfg["F"], cfg["E"], cfg["k"], cfg["T"], synth.TYPE_NAMES[cfg["gu_type"]],
+            synth.TYPE_NAMES[cfg["down_type"]]), "T": cfg["T"], "path": args.path},
+        "roofline": roofline(m),
+        "cpu_baseline": cpu,
+        "block_GBps": round(m["block_GBps"], 1),
+        "distinct_experts_per_step": round(m["U"], 2),
+        "kernels": m["kernels"],
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

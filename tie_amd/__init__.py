@@ -83,6 +83,10 @@ def lib():
         L.tie_hip_debug_fail_alloc.restype = None
         L.tie_hip_host_expf.argtypes = [P, P, ctypes.c_size_t]
         L.tie_hip_host_expf.restype = None
+        L.tie_hip_profile_enable.argtypes = [I]
+        L.tie_hip_profile_enable.restype = I
+        L.tie_hip_profile_read.argtypes = [ctypes.c_char_p, ctypes.c_size_t, P, P, I]
+        L.tie_hip_profile_read.restype = I
         _lib = L
     return _lib
 
@@ -131,6 +135,22 @@ def host_expf(x):
     out = np.empty_like(x)
     lib().tie_hip_host_expf(_p(x), _p(out), x.size)
     return out
+
+
+def profile_enable(on=True):
+    check(lib().tie_hip_profile_enable(int(on)))
+
+
+def profile_read(max_kernels=32):
+    """{kernel name: (total ms, launches)} since profile_enable(True)."""
+    names = ctypes.create_string_buffer(4096)
+    tot = np.zeros(max_kernels, np.float64)
+    cnt = np.zeros(max_kernels, np.int32)
+    n = lib().tie_hip_profile_read(names, 4096, _p(tot), _p(cnt), max_kernels)
+    if n < 0:
+        check(n)
+    keys = names.value.decode().split(",") if n else []
+    return {k: (float(tot[i]), int(cnt[i])) for i, k in enumerate(keys)}
 
 
 def moe_ffn(x, layer, k, with_topk=True):

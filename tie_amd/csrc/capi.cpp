@@ -198,7 +198,9 @@ static int ensure_workspace(int T, int k, int d, int F, int E)
 	const size_t o_idx = take(P * 4), o_w = take(P * 4), o_cnt = take(EE * 4), o_off = take((EE + 1) * 4),
 		     o_pairs = take(P * 4), o_act = take((EE + 1) * 4), o_sync = take(64 * 4),
 		     o_logits = take(Tcap * EE * 4), o_h = take(3 * P * FF * 4), o_cnt2 = take(P * (FF / 64) * 4), o_hb = take(P * FF * 2),
-		     o_y = take(P * DD * 4);
+		     o_y = take(P * DD * 4), o_xb = take(Tcap * DD * 2);
+	const size_t max_tiles = (size_t)mfma_max_tiles((int)P, (int)EE);
+	const size_t o_te = take(max_tiles * 4), o_tm = take(max_tiles * 4), o_nt = take(4);
 	void *mem = nullptr;
 	if (w.alloc) {
 		HIP_TRY(hipStreamSynchronize(g.stream));
@@ -222,6 +224,10 @@ static int ensure_workspace(int T, int k, int d, int F, int E)
 	w.tile_cnt = (uint32_t *)(b + o_cnt2);
 	w.hb = (uint16_t *)(b + o_hb);
 	w.y = (float *)(b + o_y);
+	w.xb = (uint16_t *)(b + o_xb);
+	w.tile_e = (int32_t *)(b + o_te);
+	w.tile_m0 = (int32_t *)(b + o_tm);
+	w.ntiles = (int32_t *)(b + o_nt);
 	w.cap_pairs = P;
 	w.cap_F = FF;
 	w.cap_d = DD;
@@ -344,10 +350,11 @@ static int forward(tie_hip_layer *layer, const float *x, int T, int k, float *ou
 	if (!x || !out)
 		return set_error(TIE_HIP_EINVAL, "null x/out");
 	const bool mfma = (flags & TIE_HIP_PATH_MFMA) || (!(flags & TIE_HIP_PATH_EXACT) && T > g.exact_max_t);
-	if (mfma && (flags & TIE_HIP_PATH_MFMA))
-		return set_error(TIE_HIP_EINVAL, "the MFMA path is not built in this version");
-	if (L.d > 16 * QK || L.F > 16 * QK)
-		return set_error(TIE_HIP_EINVAL, "exact path supports d, F <= 4096");
+	if (mfma && L.gate.type != L.up.type)
+		return set_error(TIE_HIP_EINVAL, "the MFMA path needs gate and up of one type (got %d, %d)", L.gate.type,
+				 L.up.type);
+	if (mfma && L.gate.type != TIE_GGML_BF16 && L.down.type == TIE_GGML_BF16)
+		return set_error(TIE_HIP_EINVAL, "the MFMA path needs a quantised down when gate/up are quantised");
 	int rc = ensure_workspace(T, k, L.d, L.F, L.E);
 	if (rc)
 		return rc;
@@ -358,7 +365,10 @@ static int forward(tie_hip_layer *layer, const float *x, int T, int k, float *ou
 	prof_begin("dispatch", s);
 	HIP_TRY(launch_dispatch(L, T, k, ws.topk_idx, ws, s));
 	prof_end(s);
-	HIP_TRY(launch_exact_experts(L, x, T, k, g.silu, ws, s));
+	if (mfma)
+		HIP_TRY(launch_mfma_experts(L, x, T, k, g.silu, ws, s));
+	else
+		HIP_TRY(launch_exact_experts(L, x, T, k, g.silu, ws, s));
 	prof_begin("combine", s);
 	HIP_TRY(launch_combine(T, L.d, k, ws.topk_w, ws.topk_idx, ws.y, out, s));
 	prof_end(s);

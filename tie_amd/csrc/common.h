@@ -19,6 +19,7 @@ constexpr size_t Q6K_PANEL = (size_t)PANEL_ROWS * Q6K_BYTES; // 13440
 constexpr int MAX_K = 32;
 constexpr int MAX_E = 1024;
 constexpr int SILU_N = TIE_SILU_TABLE_SIZE;
+constexpr int MFMA_MT = 128; // pair rows per MFMA work tile
 
 // Device layout of one stacked expert tensor [E][rows][in].
 //
@@ -70,6 +71,10 @@ struct Workspace {
 	uint32_t *tile_cnt = nullptr; // [T*k][F/64] gate/up completion counters (self-resetting)
 	uint16_t *hb = nullptr;       // [T*k][F] SwiGLU activations (bf16 hi/lo, MFMA path)
 	float *y = nullptr;           // [T*k][d] expert outputs
+	uint16_t *xb = nullptr;       // [T][d]   x as bf16 (MFMA path)
+	int32_t *tile_e = nullptr;    // [max tiles] MFMA work list: expert of each 128-pair tile
+	int32_t *tile_m0 = nullptr;   // [max tiles] first pair of the tile within the expert
+	int32_t *ntiles = nullptr;    // [1]
 	size_t cap_pairs = 0, cap_F = 0, cap_d = 0, cap_E = 0;
 	void *alloc = nullptr;
 };
@@ -82,6 +87,7 @@ hipError_t launch_exact_experts(const Layer &L, const float *x, int T, int k, co
 				hipStream_t s);
 hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, const float *silu, Workspace &ws,
 			       hipStream_t s);
+int mfma_max_tiles(int npairs, int E);
 hipError_t launch_combine(int T, int d, int k, const float *topk_w, const int32_t *topk_idx, const float *y,
 			  float *out, hipStream_t s);
 hipError_t launch_repack(const ExpertTensor &dst, const uint8_t *src, int E, int literal_bf16_stride, hipStream_t s);

@@ -25,7 +25,10 @@ __global__ __launch_bounds__(DSP_THREADS) void dispatch_kernel(const int32_t *__
 							       int E, int32_t *__restrict__ counts,
 							       int32_t *__restrict__ offsets,
 							       int32_t *__restrict__ pairs,
-							       int32_t *__restrict__ active)
+							       int32_t *__restrict__ active,
+							       int32_t *__restrict__ tile_e,
+							       int32_t *__restrict__ tile_m0,
+							       int32_t *__restrict__ ntiles)
 {
 	extern __shared__ int32_t sm[];
 	int32_t *cnt = sm;          // [E]
@@ -53,6 +56,17 @@ __global__ __launch_bounds__(DSP_THREADS) void dispatch_kernel(const int32_t *__
 		}
 		offsets[E] = run;
 		active[E] = na;
+		// MFMA work list: 128-pair tiles of each active expert
+		int nt = 0;
+		for (int a = 0; a < na; a++) {
+			const int e = active[a];
+			for (int m0 = 0; m0 < cnt[e]; m0 += MFMA_MT) {
+				tile_e[nt] = e;
+				tile_m0[nt] = m0;
+				nt++;
+			}
+		}
+		ntiles[0] = nt;
 	}
 	__syncthreads();
 	for (int p = tid; p < npairs; p += DSP_THREADS) {
@@ -66,7 +80,7 @@ hipError_t launch_dispatch(const Layer &L, int T, int k, const int32_t *topk_idx
 {
 	const size_t lds = sizeof(int32_t) * 2 * (size_t)L.E;
 	hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(DSP_THREADS), lds, s, topk_idx, T * k, L.E, ws.counts,
-			   ws.offsets, ws.pairs, ws.active);
+			   ws.offsets, ws.pairs, ws.active, ws.tile_e, ws.tile_m0, ws.ntiles);
 	return hipGetLastError();
 }
 
