@@ -20,7 +20,43 @@ namespace tie {
 
 constexpr int DSP_THREADS = 1024;
 
-// One workgroup: LDS histogram, serial scan over E, LDS-atomic placement.
+// Exclusive prefix sum over the workgroup (DSP_THREADS threads, one value
+// each); also returns the total.
+__device__ __forceinline__ int block_exclusive_scan(int v, int *wsum, int &total)
+{
+	const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+	constexpr int NW = DSP_THREADS / 64;
+	int x = v;
+#pragma unroll
+	for (int off = 1; off < 64; off <<= 1) {
+		const int y = __shfl_up(x, off);
+		if (lane >= off)
+			x += y;
+	}
+	if (lane == 63)
+		wsum[wave] = x;
+	__syncthreads();
+	if (wave == 0) {
+		int s = lane < NW ? wsum[lane] : 0;
+#pragma unroll
+		for (int off = 1; off < NW; off <<= 1) {
+			const int y = __shfl_up(s, off);
+			if (lane >= off)
+				s += y;
+		}
+		if (lane < NW)
+			wsum[lane] = s;
+	}
+	__syncthreads();
+	const int prefix = wave > 0 ? wsum[wave - 1] : 0;
+	total = wsum[NW - 1];
+	__syncthreads();
+	return prefix + x - v;
+}
+
+// One workgroup: LDS histogram, parallel scans over the experts, LDS-atomic
+// placement of the pairs.  Also writes the MFMA work list (one entry per
+// MFMA_MT pairs of each active expert).
 __global__ __launch_bounds__(DSP_THREADS) void dispatch_kernel(const int32_t *__restrict__ topk_idx, int npairs,
 							       int E, int32_t *__restrict__ counts,
 							       int32_t *__restrict__ offsets,
@@ -33,6 +69,7 @@ __global__ __launch_bounds__(DSP_THREADS) void dispatch_kernel(const int32_t *__
 	extern __shared__ int32_t sm[];
 	int32_t *cnt = sm;          // [E]
 	int32_t *cur = sm + E;      // [E] running cursor
+	__shared__ int wsum[DSP_THREADS / 64];
 	const int tid = threadIdx.x;
 	for (int e = tid; e < E; e += DSP_THREADS)
 		cnt[e] = 0;
@@ -43,36 +80,35 @@ __global__ __launch_bounds__(DSP_THREADS) void dispatch_kernel(const int32_t *__
 			atomicAdd(&cnt[e], 1);
 	}
 	__syncthreads();
+	// E <= MAX_E == DSP_THREADS: one expert per thread
+	const int e = tid;
+	const int c = e < E ? cnt[e] : 0;
+	int total, nact, ntot;
+	const int off = block_exclusive_scan(c, wsum, total);
+	const int aidx = block_exclusive_scan(c > 0 ? 1 : 0, wsum, nact);
+	const int nt = (c + MFMA_MT - 1) / MFMA_MT;
+	const int toff = block_exclusive_scan(nt, wsum, ntot);
+	if (e < E) {
+		offsets[e] = off;
+		cur[e] = off;
+		counts[e] = c;
+		if (c > 0)
+			active[aidx] = e;
+		for (int t = 0; t < nt; t++) {
+			tile_e[toff + t] = e;
+			tile_m0[toff + t] = t * MFMA_MT;
+		}
+	}
 	if (tid == 0) {
-		int run = 0, na = 0;
-		for (int e = 0; e < E; e++) {
-			const int c = cnt[e];
-			offsets[e] = run;
-			cur[e] = run;
-			counts[e] = c;
-			if (c > 0)
-				active[na++] = e;
-			run += c;
-		}
-		offsets[E] = run;
-		active[E] = na;
-		// MFMA work list: 128-pair tiles of each active expert
-		int nt = 0;
-		for (int a = 0; a < na; a++) {
-			const int e = active[a];
-			for (int m0 = 0; m0 < cnt[e]; m0 += MFMA_MT) {
-				tile_e[nt] = e;
-				tile_m0[nt] = m0;
-				nt++;
-			}
-		}
-		ntiles[0] = nt;
+		offsets[E] = total;
+		active[E] = nact;
+		ntiles[0] = ntot;
 	}
 	__syncthreads();
 	for (int p = tid; p < npairs; p += DSP_THREADS) {
-		const int e = topk_idx[p];
-		if (e >= 0 && e < E)
-			pairs[atomicAdd(&cur[e], 1)] = p;
+		const int ex = topk_idx[p];
+		if (ex >= 0 && ex < E)
+			pairs[atomicAdd(&cur[ex], 1)] = p;
 	}
 }
 

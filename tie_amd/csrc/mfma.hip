@@ -30,6 +30,7 @@ namespace tie {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int MT = 128;       // pair rows per workgroup
 constexpr int NT = 128;       // weight rows per workgroup
@@ -62,150 +63,185 @@ struct MfmaArgs {
 	float *y;                // down out [pair][d]
 };
 
-// ------------------------------------------------------------------ B staging
-// Thread (m, i, half): panel m (0/1), panel row i, half of the 64-wide K slice.
-template <int TYPE>
-__device__ __forceinline__ void stage_b(const MfmaArgs &a, int e, int rt0, int kk, uint16_t *__restrict__ Bs)
+// ------------------------------------------------------------------ staging
+// Each K-step moves a 128 x 64 A tile and a 128 x 64 B tile into LDS.  The
+// global loads of step kk+1 are issued into registers before the MFMAs of
+// step kk (Pref), and written to the other LDS buffer (with the B dequant)
+// after them, so HBM latency overlaps the matrix work: one barrier per step.
+//
+// Thread roles: A -- row tid/2, half tid%2 (32 K values); B -- panel
+// m = tid/128, panel row i = (tid/2)%64, half h = tid%2.
+template <int TYPE, bool SPLIT> struct Pref {
+	u32x4 a[SPLIT ? 8 : 4];
+	u32x4 b[TYPE == TIE_GGML_Q4_K ? 2 : TYPE == TIE_GGML_Q6_K ? 5 : 4];
+	uint32_t d6;
+};
+
+// B row in LDS of (panel m, panel row i).  Gate/up interleave the two
+// matrices every 32 rows so that a wave's two 32-column MFMA tiles hold
+// the gate and the up values of the same F columns.
+__device__ __forceinline__ int b_row(bool down, int m, int i)
 {
-	const int tid = threadIdx.x;
-	const int m = tid >> 7, i = (tid >> 1) & 63, h = tid & 1;
-	const int nb = a.in / QK;
-	uint16_t *dst = Bs + (m * 64 + i) * LDK + 32 * h;
-	if (TYPE == TIE_GGML_BF16) {
-		// row-major [E][rows][in]; gate/up: matrix m, row rt0*64 + i; down: row (rt0 + m)*64 + i
-		const int mat = (a.w[0] == a.w[1]) ? 0 : m;
-		const int row = (a.w[0] == a.w[1]) ? (rt0 + m) * 64 + i : rt0 * 64 + i;
-		const uint4 *src = reinterpret_cast<const uint4 *>(a.w[mat] + (size_t)e * a.expert_bytes[mat] +
-								   ((size_t)row * a.in + kk * KS + 32 * h) * 2);
+	return down ? m * 64 + i : (i >> 5) * 64 + m * 32 + (i & 31);
+}
+
+template <int TYPE, bool DOWN, bool SPLIT>
+__device__ __forceinline__ void load_step(const MfmaArgs &a, const uint8_t *bsrc0, const uint8_t *bsrc1, const char *arow, bool alive,
+					  int kk, Pref<TYPE, SPLIT> &p)
+{
+	const int h = threadIdx.x & 1;
+	// A (rows past the tile's end read row 0 -- always valid -- and are
+	// zeroed when stored)
+	(void)alive;
+	if (!SPLIT) {
+		const u32x4 *src = reinterpret_cast<const u32x4 *>(arow + ((size_t)kk * KS + 32 * h) * 2);
 #pragma unroll
 		for (int c = 0; c < 4; c++)
-			reinterpret_cast<uint4 *>(dst)[c] = src[c];
-		return;
-	}
-	const int b = kk / 4;                  // super-block column
-	const int mat = (a.w[0] == a.w[1]) ? 0 : m;
-	const int rt = (a.w[0] == a.w[1]) ? rt0 + m : rt0;
-	const uint8_t *panel = a.w[mat] + (size_t)e * a.expert_bytes[mat] + ((size_t)rt * nb + b) * panel_bytes(TYPE);
-	const uint4 *pc = reinterpret_cast<const uint4 *>(panel) + i;
-	float w[32];
-	if (TYPE == TIE_GGML_Q4_K) {
-		// K slice = group g (sub-blocks 2g, 2g+1); half h = bytes 16h..16h+15 of the group
-		const int g = kk & 3;
-		const uint4 c0 = pc[0];
-		const uint4 q = pc[(1 + 2 * g + h) * 64];
-		const float d = half_bits_to_float(c0.x & 0xffffu), dmin = half_bits_to_float(c0.x >> 16);
-		const uint32_t s[3] = {c0.y, c0.z, c0.w};
-		auto sb = [&](int j) { return (s[j >> 2] >> (8 * (j & 3))) & 0xffu; };
-		uint32_t sc0, m0, sc1, m1;
-		const int j0 = 2 * g, j1 = 2 * g + 1;
-		if (j0 < 4) {
-			sc0 = sb(j0) & 63u;
-			m0 = sb(j0 + 4) & 63u;
-		} else {
-			sc0 = (sb(j0 + 4) & 15u) | ((sb(j0 - 4) >> 6) << 4);
-			m0 = (sb(j0 + 4) >> 4) | ((sb(j0) >> 6) << 4);
-		}
-		if (j1 < 4) {
-			sc1 = sb(j1) & 63u;
-			m1 = sb(j1 + 4) & 63u;
-		} else {
-			sc1 = (sb(j1 + 4) & 15u) | ((sb(j1 - 4) >> 6) << 4);
-			m1 = (sb(j1 + 4) >> 4) | ((sb(j1) >> 6) << 4);
-		}
-		const float D0 = d * (float)sc0, M0 = -(dmin * (float)m0);
-		const float D1 = d * (float)sc1, M1 = -(dmin * (float)m1);
-		const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-		for (int j = 0; j < 16; j++) {
-			const uint32_t byte = (qw[j >> 2] >> (8 * (j & 3))) & 0xffu;
-			w[j] = __builtin_fmaf((float)(byte & 15u), D0, M0);       // K = 16h + j
-			w[16 + j] = __builtin_fmaf((float)(byte >> 4), D1, M1);   // K = 32 + 16h + j
-		}
-		// lo nibbles land at K 16h..16h+15, hi nibbles at 32+16h..: two 16-wide runs
-		uint32_t p[16];
-#pragma unroll
-		for (int j = 0; j < 8; j++) {
-			p[j] = pack_bf16(w[2 * j], w[2 * j + 1]);
-			p[8 + j] = pack_bf16(w[16 + 2 * j], w[16 + 2 * j + 1]);
-		}
-		uint16_t *d0 = Bs + (m * 64 + i) * LDK + 16 * h;
-		uint16_t *d1 = d0 + 32;
-		reinterpret_cast<uint4 *>(d0)[0] = make_uint4(p[0], p[1], p[2], p[3]);
-		reinterpret_cast<uint4 *>(d0)[1] = make_uint4(p[4], p[5], p[6], p[7]);
-		reinterpret_cast<uint4 *>(d1)[0] = make_uint4(p[8], p[9], p[10], p[11]);
-		reinterpret_cast<uint4 *>(d1)[1] = make_uint4(p[12], p[13], p[14], p[15]);
-		return;
+			p.a[c] = src[c];
 	} else {
-		// Q6_K: K slice = half n of the block, quant rows r = 2*rp + h (elements 32r + l)
-		const int n = (kk >> 1) & 1, rp = kk & 1, r = 2 * rp + h;
-		const uint4 qa = pc[(4 * n + 2 * (r & 1)) * 64];
-		const uint4 qb = pc[(4 * n + 2 * (r & 1) + 1) * 64];
-		const uint4 ha = pc[(8 + 2 * n) * 64];
-		const uint4 hb = pc[(9 + 2 * n) * 64];
-		const uint4 sc = pc[12 * 64];
-		const float d = half_bits_to_float(reinterpret_cast<const uint16_t *>(panel + Q6K_CHUNKS * 1024)[i]);
-		const uint32_t qlw[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
-		const uint32_t qhw[8] = {ha.x, ha.y, ha.z, ha.w, hb.x, hb.y, hb.z, hb.w};
-		const uint32_t scw[4] = {sc.x, sc.y, sc.z, sc.w};
-		auto scale = [&](int j) { return (float)(int8_t)((scw[j >> 2] >> (8 * (j & 3))) & 0xffu); };
-		const float W0 = d * scale(8 * n + 0 + 2 * r), W1 = d * scale(8 * n + 1 + 2 * r);
-		const int nsh = 4 * (r >> 1), hsh = 2 * r;
+		const u32x4 *src = reinterpret_cast<const u32x4 *>(arow + ((size_t)kk * KS + 32 * h) * 4);
 #pragma unroll
-		for (int l = 0; l < 32; l++) {
-			const uint32_t L = (qlw[l >> 2] >> (8 * (l & 3))) & 0xffu;
-			const uint32_t H = (qhw[l >> 2] >> (8 * (l & 3))) & 0xffu;
-			const int qv = (int)(((L >> nsh) & 15u) | (((H >> hsh) & 3u) << 4)) - 32;
-			w[l] = (l < 16 ? W0 : W1) * (float)qv;
-		}
-		uint32_t p[16];
-#pragma unroll
-		for (int j = 0; j < 16; j++)
-			p[j] = pack_bf16(w[2 * j], w[2 * j + 1]);
+		for (int c = 0; c < 8; c++)
+			p.a[c] = src[c];
+	}
+	// B
+	const int m = threadIdx.x >> 7, i = (threadIdx.x >> 1) & 63;
+	if constexpr (TYPE == TIE_GGML_BF16) {
+		const u32x4 *src = reinterpret_cast<const u32x4 *>((m ? bsrc1 : bsrc0) + ((size_t)kk * KS + 32 * h) * 2);
 #pragma unroll
 		for (int c = 0; c < 4; c++)
-			reinterpret_cast<uint4 *>(dst)[c] = make_uint4(p[4 * c], p[4 * c + 1], p[4 * c + 2], p[4 * c + 3]);
+			p.b[c] = src[c];
+	} else {
+		const uint8_t *panel = (m ? bsrc1 : bsrc0) + (size_t)(kk / 4) * panel_bytes(TYPE);
+		const u32x4 *pc = reinterpret_cast<const u32x4 *>(panel) + i;
+		if constexpr (TYPE == TIE_GGML_Q4_K) {
+			const int g = kk & 3;
+			p.b[0] = pc[0];
+			p.b[1] = pc[(1 + 2 * g + h) * 64];
+		} else {
+			const int n = (kk >> 1) & 1, r = 2 * (kk & 1) + h;
+			p.b[0] = pc[(4 * n + 2 * (r & 1)) * 64];
+			p.b[1] = pc[(4 * n + 2 * (r & 1) + 1) * 64];
+			p.b[2] = pc[(8 + 2 * n) * 64];
+			p.b[3] = pc[(9 + 2 * n) * 64];
+			p.b[4] = pc[12 * 64];
+			p.d6 = reinterpret_cast<const uint16_t *>(panel + Q6K_CHUNKS * 1024)[i];
+		}
 	}
 }
 
-// ------------------------------------------------------------------ A staging
-// Thread (row, half): 32 bf16 of the row's 64-wide K slice.  DOWN rows are
-// positions in the expert-grouped pair list; gate/up rows are tokens.
-template <bool DOWN, bool SPLIT>
-__device__ __forceinline__ void stage_a(const MfmaArgs &a, int pbase, int nrows, int kk, uint16_t *__restrict__ As,
-					uint16_t *__restrict__ As_lo)
+template <int TYPE, bool DOWN, bool SPLIT>
+__device__ __forceinline__ void store_step(const Pref<TYPE, SPLIT> &p, bool alive, int kk, uint16_t *__restrict__ As,
+					   uint16_t *__restrict__ Alo, uint16_t *__restrict__ Bs)
 {
 	const int tid = threadIdx.x;
-	const int r = tid >> 1, h = tid & 1;
-	uint16_t *dst = As + r * LDK + 32 * h;
-	uint16_t *dlo = SPLIT ? As_lo + r * LDK + 32 * h : nullptr;
-	if (r >= nrows) {
+	const int h = tid & 1;
+	// A
+	{
+		uint16_t *dst = As + (tid >> 1) * LDK + 32 * h;
+		if (!alive) {
 #pragma unroll
-		for (int c = 0; c < 4; c++) {
-			reinterpret_cast<uint4 *>(dst)[c] = make_uint4(0, 0, 0, 0);
-			if (SPLIT)
-				reinterpret_cast<uint4 *>(dlo)[c] = make_uint4(0, 0, 0, 0);
+			for (int c = 0; c < 4; c++) {
+				reinterpret_cast<uint4 *>(dst)[c] = make_uint4(0, 0, 0, 0);
+				if (SPLIT)
+					reinterpret_cast<uint4 *>(Alo + (tid >> 1) * LDK + 32 * h)[c] = make_uint4(0, 0, 0, 0);
+			}
+		} else if (!SPLIT) {
+#pragma unroll
+			for (int c = 0; c < 4; c++)
+				reinterpret_cast<u32x4 *>(dst)[c] = p.a[c];
+		} else {
+			uint16_t *dlo = Alo + (tid >> 1) * LDK + 32 * h;
+#pragma unroll
+			for (int c = 0; c < 8; c++) {
+				const float4 v = make_float4(__uint_as_float(p.a[c].x), __uint_as_float(p.a[c].y),
+							     __uint_as_float(p.a[c].z), __uint_as_float(p.a[c].w));
+				const float hi0 = (float)(__bf16)v.x, hi1 = (float)(__bf16)v.y;
+				const float hi2 = (float)(__bf16)v.z, hi3 = (float)(__bf16)v.w;
+				reinterpret_cast<uint2 *>(dst)[c] = make_uint2(pack_bf16(hi0, hi1), pack_bf16(hi2, hi3));
+				reinterpret_cast<uint2 *>(dlo)[c] =
+					make_uint2(pack_bf16(v.x - hi0, v.y - hi1), pack_bf16(v.z - hi2, v.w - hi3));
+			}
 		}
-		return;
 	}
-	const int p = pbase + r;
-	const size_t row = DOWN ? (size_t)p : (size_t)(a.pairs[p] / a.k);
-	const size_t col = (size_t)kk * KS + 32 * h;
-	if (!SPLIT) {
-		const uint4 *src = reinterpret_cast<const uint4 *>(a.a16 + row * a.in + col);
+	// B
+	const int m = tid >> 7, i = (tid >> 1) & 63;
+	uint16_t *brow = Bs + b_row(DOWN, m, i) * LDK;
+	if constexpr (TYPE == TIE_GGML_BF16) {
 #pragma unroll
 		for (int c = 0; c < 4; c++)
-			reinterpret_cast<uint4 *>(dst)[c] = src[c];
-	} else {
-		const float4 *src = reinterpret_cast<const float4 *>(a.a32 + row * a.in + col);
+			reinterpret_cast<u32x4 *>(brow + 32 * h)[c] = p.b[c];
+	} else if constexpr (TYPE == TIE_GGML_Q4_K) {
+		// K slice = group g (sub-blocks 2g, 2g+1); half h = bytes 16h..16h+15 of the group
+		const int g = kk & 3;
+		const u32x4 c0 = p.b[0], q = p.b[1];
+		const float d = half_bits_to_float(c0.x & 0xffffu), dmin = half_bits_to_float(c0.x >> 16);
+		auto sb = [&](int j) {
+			const int wi = j >> 2;
+			const uint32_t wd = wi == 0 ? c0.y : (wi == 1 ? c0.z : c0.w);
+			return (wd >> (8 * (j & 3))) & 0xffu;
+		};
+		auto scale_min = [&](int j, uint32_t &sc, uint32_t &mn) {
+			if (j < 4) {
+				sc = sb(j) & 63u;
+				mn = sb(j + 4) & 63u;
+			} else {
+				sc = (sb(j + 4) & 15u) | ((sb(j - 4) >> 6) << 4);
+				mn = (sb(j + 4) >> 4) | ((sb(j) >> 6) << 4);
+			}
+		};
+		uint32_t sc0, m0, sc1, m1;
+		scale_min(2 * g, sc0, m0);
+		scale_min(2 * g + 1, sc1, m1);
+		const float D0 = d * (float)sc0, M0 = -(dmin * (float)m0);
+		const float D1 = d * (float)sc1, M1 = -(dmin * (float)m1);
+		const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+		uint32_t lo[8], hi[8];
 #pragma unroll
-		for (int c = 0; c < 8; c++) {
-			const float4 v = src[c];
-			const float hi0 = (float)(__bf16)v.x, hi1 = (float)(__bf16)v.y;
-			const float hi2 = (float)(__bf16)v.z, hi3 = (float)(__bf16)v.w;
-			reinterpret_cast<uint2 *>(dst)[c] = make_uint2(pack_bf16(hi0, hi1), pack_bf16(hi2, hi3));
-			reinterpret_cast<uint2 *>(dlo)[c] =
-				make_uint2(pack_bf16(v.x - hi0, v.y - hi1), pack_bf16(v.z - hi2, v.w - hi3));
+		for (int j = 0; j < 8; j++) {
+			const uint32_t b0 = (qw[j >> 1] >> (16 * (j & 1))) & 0xffu;
+			const uint32_t b1 = (qw[j >> 1] >> (16 * (j & 1) + 8)) & 0xffu;
+			lo[j] = pack_bf16(__builtin_fmaf((float)(b0 & 15u), D0, M0), __builtin_fmaf((float)(b1 & 15u), D0, M0));
+			hi[j] = pack_bf16(__builtin_fmaf((float)(b0 >> 4), D1, M1), __builtin_fmaf((float)(b1 >> 4), D1, M1));
 		}
+		uint16_t *d0 = brow + 16 * h; // lo nibbles: K 16h..16h+15; hi nibbles: 32+16h..
+		reinterpret_cast<uint4 *>(d0)[0] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+		reinterpret_cast<uint4 *>(d0)[1] = make_uint4(lo[4], lo[5], lo[6], lo[7]);
+		reinterpret_cast<uint4 *>(d0 + 32)[0] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+		reinterpret_cast<uint4 *>(d0 + 32)[1] = make_uint4(hi[4], hi[5], hi[6], hi[7]);
+	} else {
+		// Q6_K: K slice = half n of the block, quant row r = 2*(kk&1) + h
+		// (elements 32r + l); w = (d * sc) * (q - 32), exact in fp32
+		const int n = (kk >> 1) & 1, r = 2 * (kk & 1) + h;
+		const uint32_t qlw[8] = {p.b[0].x, p.b[0].y, p.b[0].z, p.b[0].w, p.b[1].x, p.b[1].y, p.b[1].z, p.b[1].w};
+		const uint32_t qhw[8] = {p.b[2].x, p.b[2].y, p.b[2].z, p.b[2].w, p.b[3].x, p.b[3].y, p.b[3].z, p.b[3].w};
+		const float d = half_bits_to_float(p.d6);
+		auto scale = [&](int j) {
+			const int wi = j >> 2;
+			const uint32_t wd = wi == 0 ? p.b[4].x : (wi == 1 ? p.b[4].y : (wi == 2 ? p.b[4].z : p.b[4].w));
+			return (float)(int8_t)((wd >> (8 * (j & 3))) & 0xffu);
+		};
+		const float W0 = d * scale(8 * n + 2 * r), W1 = d * scale(8 * n + 1 + 2 * r);
+		const float N0 = -32.0f * W0, N1 = -32.0f * W1;
+		const int nsh = 4 * (r >> 1), hsh = 2 * r;
+		uint32_t pk[16];
+#pragma unroll
+		for (int j = 0; j < 16; j++) {
+			float wv[2];
+#pragma unroll
+			for (int t = 0; t < 2; t++) {
+				const int l = 2 * j + t;
+				const uint32_t L = (qlw[l >> 2] >> (8 * (l & 3))) & 0xffu;
+				const uint32_t H = (qhw[l >> 2] >> (8 * (l & 3))) & 0xffu;
+				const uint32_t qv = ((L >> nsh) & 15u) | (((H >> hsh) & 3u) << 4);
+				wv[t] = l < 16 ? __builtin_fmaf((float)qv, W0, N0) : __builtin_fmaf((float)qv, W1, N1);
+			}
+			pk[j] = pack_bf16(wv[0], wv[1]);
+		}
+#pragma unroll
+		for (int c = 0; c < 4; c++)
+			reinterpret_cast<uint4 *>(brow + 32 * h)[c] = make_uint4(pk[4 * c], pk[4 * c + 1], pk[4 * c + 2],
+										 pk[4 * c + 3]);
 	}
 }
 
@@ -215,12 +251,14 @@ __device__ __forceinline__ bf16x8 lds_frag(const uint16_t *base, int row, int k)
 }
 
 // ------------------------------------------------------------------ kernel
+// Workgroup tile 128 pairs x 128 weight rows; 2 x 2 waves of 64 x 64, each
+// a 2 x 2 grid of 32 x 32 MFMA tiles.
 template <int TYPE, bool DOWN, bool SPLIT>
 __global__ __launch_bounds__(MF_THREADS) void mfma_experts_kernel(MfmaArgs a)
 {
-	__shared__ __attribute__((aligned(16))) uint16_t As[MT * LDK];
-	__shared__ __attribute__((aligned(16))) uint16_t Bs[NT * LDK];
-	__shared__ __attribute__((aligned(16))) uint16_t Alo[SPLIT ? MT * LDK : 8];
+	__shared__ __attribute__((aligned(16))) uint16_t As[2][MT * LDK];
+	__shared__ __attribute__((aligned(16))) uint16_t Bs[2][NT * LDK];
+	__shared__ __attribute__((aligned(16))) uint16_t Alo[SPLIT ? 2 : 1][SPLIT ? MT * LDK : 8];
 
 	const int tile = blockIdx.y;
 	if (tile >= *a.ntiles)
@@ -228,9 +266,30 @@ __global__ __launch_bounds__(MF_THREADS) void mfma_experts_kernel(MfmaArgs a)
 	const int e = a.tile_e[tile], m0 = a.tile_m0[tile];
 	const int pbase = a.offsets[e] + m0;
 	const int nrows = min(MT, a.offsets[e + 1] - pbase);
-	const int rt0 = DOWN ? 2 * blockIdx.x : blockIdx.x; // 64-row panel index of B row 0
 	const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+	const int wm = w >> 1, wn = w & 1;
 	const int lr = lane & 31, lk = 8 * (lane >> 5);
+
+	// this thread's A row and B source rows/panels
+	const int ar = threadIdx.x >> 1;
+	const bool alive = ar < nrows;
+	const size_t arow_idx = alive ? (DOWN ? (size_t)(pbase + ar) : (size_t)(a.pairs[pbase + ar] / a.k)) : 0;
+	const char *arow = SPLIT ? (const char *)(a.a32 + arow_idx * a.in) : (const char *)(a.a16 + arow_idx * a.in);
+	const uint8_t *bsrc[2];
+	{
+		const int bi = (threadIdx.x >> 1) & 63;
+		const int nb = a.in / QK;
+#pragma unroll
+		for (int mm = 0; mm < 2; mm++) {
+			const int mat = DOWN ? 0 : mm;
+			const int rt = DOWN ? 2 * blockIdx.x + mm : blockIdx.x;
+			const uint8_t *base = (mat ? a.w[1] : a.w[0]) + (size_t)e * (mat ? a.expert_bytes[1] : a.expert_bytes[0]);
+			if (TYPE == TIE_GGML_BF16)
+				bsrc[mm] = base + ((size_t)(rt * 64 + bi) * a.in) * 2;
+			else
+				bsrc[mm] = base + (size_t)rt * nb * panel_bytes(TYPE);
+		}
+	}
 
 	f32x16 acc[4];
 #pragma unroll
@@ -240,51 +299,64 @@ __global__ __launch_bounds__(MF_THREADS) void mfma_experts_kernel(MfmaArgs a)
 			acc[t][j] = 0.0f;
 
 	const int nk = a.in / KS;
+	Pref<TYPE, SPLIT> pf;
+	load_step<TYPE, DOWN, SPLIT>(a, bsrc[0], bsrc[1], arow, alive, 0, pf);
+	store_step<TYPE, DOWN, SPLIT>(pf, alive, 0, As[0], Alo[0], Bs[0]);
+	__syncthreads();
 	for (int kk = 0; kk < nk; kk++) {
-		__syncthreads();
-		stage_a<DOWN, SPLIT>(a, pbase, nrows, kk, As, Alo);
-		stage_b<TYPE>(a, e, rt0, kk, Bs);
-		__syncthreads();
+		const int cur = kk & 1;
+		if (kk + 1 < nk)
+			load_step<TYPE, DOWN, SPLIT>(a, bsrc[0], bsrc[1], arow, alive, kk + 1, pf);
+		const uint16_t *A = As[cur], *B = Bs[cur];
+		const uint16_t *AL = Alo[SPLIT ? cur : 0];
 #pragma unroll
 		for (int s = 0; s < KS / 16; s++) {
-			const bf16x8 av = lds_frag(As, 32 * w + lr, 16 * s + lk);
-			bf16x8 alo;
-			if (SPLIT)
-				alo = lds_frag(Alo, 32 * w + lr, 16 * s + lk);
-#pragma unroll
-			for (int t = 0; t < 4; t++) {
-				const bf16x8 bv = lds_frag(Bs, 32 * t + lr, 16 * s + lk);
-				acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv, acc[t], 0, 0, 0);
-				if (SPLIT)
-					acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(alo, bv, acc[t], 0, 0, 0);
+			const bf16x8 a0 = lds_frag(A, 64 * wm + lr, 16 * s + lk);
+			const bf16x8 a1 = lds_frag(A, 64 * wm + 32 + lr, 16 * s + lk);
+			const bf16x8 b0 = lds_frag(B, 64 * wn + lr, 16 * s + lk);
+			const bf16x8 b1 = lds_frag(B, 64 * wn + 32 + lr, 16 * s + lk);
+			acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b0, acc[0], 0, 0, 0);
+			acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b1, acc[1], 0, 0, 0);
+			acc[2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b0, acc[2], 0, 0, 0);
+			acc[3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b1, acc[3], 0, 0, 0);
+			if (SPLIT) {
+				const bf16x8 l0 = lds_frag(AL, 64 * wm + lr, 16 * s + lk);
+				const bf16x8 l1 = lds_frag(AL, 64 * wm + 32 + lr, 16 * s + lk);
+				acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(l0, b0, acc[0], 0, 0, 0);
+				acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(l0, b1, acc[1], 0, 0, 0);
+				acc[2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(l1, b0, acc[2], 0, 0, 0);
+				acc[3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(l1, b1, acc[3], 0, 0, 0);
 			}
 		}
+		if (kk + 1 < nk)
+			store_step<TYPE, DOWN, SPLIT>(pf, alive, kk + 1, As[cur ^ 1], Alo[SPLIT ? cur ^ 1 : 0], Bs[cur ^ 1]);
+		__syncthreads();
 	}
 
 	// D layout of v_mfma_f32_32x32x16: lane l, register j holds
 	// row 8*(j/4) + 4*(l/32) + j%4, column l%32.
 #pragma unroll
-	for (int j = 0; j < 16; j++) {
-		const int mrow = 32 * w + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
-		if (mrow >= nrows)
-			continue;
-		const int p = pbase + mrow;
-		if (!DOWN) {
-			// acc[0..1]: gate rows 0..63 of the tile, acc[2..3]: the same up rows
+	for (int i = 0; i < 2; i++) {
 #pragma unroll
-			for (int t = 0; t < 2; t++) {
-				const int col = blockIdx.x * 64 + 32 * t + lr;
-				const float hv = tie_swiglu(acc[t][j], acc[t + 2][j], a.silu);
+		for (int j = 0; j < 16; j++) {
+			const int mrow = 64 * wm + 32 * i + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
+			if (mrow >= nrows)
+				continue;
+			const int p = pbase + mrow;
+			if (!DOWN) {
+				// acc[2i]: gate, acc[2i+1]: up, of F column blockIdx.x*64 + 32*wn + lr
+				const int col = blockIdx.x * 64 + 32 * wn + lr;
+				const float hv = tie_swiglu(acc[2 * i][j], acc[2 * i + 1][j], a.silu);
 				if (SPLIT)
 					a.h32[(size_t)p * a.rows + col] = hv;
 				else
 					a.h16[(size_t)p * a.rows + col] = bf16_bits(hv);
+			} else {
+				const int pair = a.pairs[p];
+				float *yr = a.y + (size_t)pair * a.rows + blockIdx.x * 128 + 64 * wn + lr;
+				yr[0] = acc[2 * i][j];
+				yr[32] = acc[2 * i + 1][j];
 			}
-		} else {
-			const int pair = a.pairs[p];
-#pragma unroll
-			for (int t = 0; t < 4; t++)
-				a.y[(size_t)pair * a.rows + rt0 * 64 + 32 * t + lr] = acc[t][j];
 		}
 	}
 }

@@ -26,53 +26,72 @@
 namespace tie {
 
 // top-k (engine.c:891-914 semantics) + softmax (engine.c:864-888) for one
-// token, by one wave.  `lg` is the token's E logits in LDS.  Rank of a
-// candidate = number of valid logits ordered before it by (value desc,
-// index asc); NaN and -inf are never selected; unfilled slots are
-// {-1, -inf}.
-__device__ void topk_softmax_wave(const float *lg, int E, int k, float *slot_s, int *slot_i, int32_t *out_idx,
-				  float *out_w)
+// token, by one wave.  `lg` holds the token's E logits.  The k winners are
+// extracted one at a time by a wave-wide argmax under the order (value
+// descending, index ascending) -- the order find_top_k's strict-greater
+// insertion produces; NaN and -inf never qualify; unfilled slots are
+// {-1, -inf}.  Slot j's exponential is computed by lane j, the sum is
+// formed serially in slot order, and every weight is e_j * (1 / sum).
+__device__ void topk_softmax_wave(const float *lg, int E, int k, int32_t *out_idx, float *out_w)
 {
 	const int lane = threadIdx.x & 63;
-	for (int j = lane; j < k; j += 64) {
-		slot_s[j] = -__builtin_inff();
-		slot_i[j] = -1;
+	constexpr int PER = MAX_E / 64;
+	float v[PER];
+#pragma unroll
+	for (int q = 0; q < PER; q++) {
+		const int e = q * 64 + lane;
+		const float x = e < E ? lg[e] : -__builtin_inff();
+		v[q] = (x > -__builtin_inff()) ? x : -__builtin_inff(); // NaN -> never selected
 	}
-	__builtin_amdgcn_wave_barrier();
-	__builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-	for (int e = lane; e < E; e += 64) {
-		const float v = lg[e];
-		if (!(v > -__builtin_inff()))
-			continue;
-		int rank = 0;
-		for (int q = 0; q < E; q++) {
-			const float u = lg[q];
-			rank += (u > v) || (u == v && q < e);
+	float my_s = -__builtin_inff();
+	int my_i = -1;
+	for (int j = 0; j < k; j++) {
+		// lane-local best: first (lowest index) maximum
+		float bv = -__builtin_inff();
+		int be = 0x7fffffff;
+#pragma unroll
+		for (int q = 0; q < PER; q++)
+			if (v[q] > bv) {
+				bv = v[q];
+				be = q * 64 + lane;
+			}
+		// wave argmax by (value desc, index asc)
+#pragma unroll
+		for (int off = 32; off > 0; off >>= 1) {
+			const float ov = __shfl_xor(bv, off);
+			const int oe = __shfl_xor(be, off);
+			if (ov > bv || (ov == bv && oe < be)) {
+				bv = ov;
+				be = oe;
+			}
 		}
-		if (rank < k) {
-			slot_s[rank] = v;
-			slot_i[rank] = e;
+		const bool found = bv > -__builtin_inff();
+		if (lane == j) {
+			my_s = found ? bv : -__builtin_inff();
+			my_i = found ? be : -1;
+		}
+		if (found && (be & 63) == lane) {
+#pragma unroll
+			for (int q = 0; q < PER; q++)
+				if (q == (be >> 6))
+					v[q] = -__builtin_inff();
 		}
 	}
-	__builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-	__builtin_amdgcn_wave_barrier();
-	__builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-	if (lane == 0) {
-		float mx = slot_s[0];
-		for (int j = 1; j < k; j++)
-			if (slot_s[j] > mx)
-				mx = slot_s[j];
-		float ev[MAX_K];
-		float sum = 0.0f;
-		for (int j = 0; j < k; j++) {
-			ev[j] = tie_expf(slot_s[j] - mx);
-			sum = sum + ev[j];
-		}
-		const float inv = __fdiv_rn(1.0f, sum);
-		for (int j = 0; j < k; j++) {
-			out_w[j] = ev[j] * inv;
-			out_idx[j] = slot_i[j];
-		}
+	// softmax over the k selected logits: max is slot 0 (or -inf), exp per lane
+	float mx = __shfl(my_s, 0);
+	for (int j = 1; j < k; j++) {
+		const float sj = __shfl(my_s, j);
+		if (sj > mx)
+			mx = sj;
+	}
+	const float ev = lane < k ? tie_expf(my_s - mx) : 0.0f;
+	float sum = 0.0f;
+	for (int j = 0; j < k; j++)
+		sum = sum + __shfl(ev, j);
+	const float inv = __fdiv_rn(1.0f, sum);
+	if (lane < k) {
+		out_w[lane] = ev * inv;
+		out_idx[lane] = my_i;
 	}
 }
 
@@ -91,8 +110,6 @@ __global__ __launch_bounds__(RS_THREADS) void router_small_kernel(const float *_
 	float *ws = lds;
 	float *xs = lds + d;
 	__shared__ int s_last;
-	__shared__ float s_slot_s[RS_THREADS / 64][MAX_K];
-	__shared__ int s_slot_i[RS_THREADS / 64][MAX_K];
 
 	const int e = blockIdx.x;
 	const int t0 = blockIdx.y * RS_TOK;
@@ -152,7 +169,7 @@ __global__ __launch_bounds__(RS_THREADS) void router_small_kernel(const float *_
 		__builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
 		__builtin_amdgcn_wave_barrier();
 		__builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-		topk_softmax_wave(my, E, k, s_slot_s[wave], s_slot_i[wave], topk_idx + (size_t)t * k,
+		topk_softmax_wave(my, E, k, topk_idx + (size_t)t * k,
 				  topk_w + (size_t)t * k);
 		__builtin_amdgcn_wave_barrier();
 	}
@@ -175,8 +192,6 @@ __global__ __launch_bounds__(1024) void router_tiled_kernel(const float *__restr
 	float *wsm = lds;                      // [E][wst]
 	float *xsm = wsm + (size_t)E * wst;    // [RT_TOK][RT_KC]
 	float *lgm = xsm + RT_TOK * RT_KC;     // [RT_TOK][E]
-	int *slot_i = reinterpret_cast<int *>(lgm + RT_TOK * E); // [nwaves][MAX_K]
-	float *slot_s = reinterpret_cast<float *>(slot_i + 16 * MAX_K);
 
 	const int tid = threadIdx.x;
 	const int nthr = blockDim.x; // 4 * E
@@ -241,7 +256,7 @@ __global__ __launch_bounds__(1024) void router_tiled_kernel(const float *__restr
 	const int wave = tid >> 6;
 	const int nw = nthr >> 6;
 	for (int t = wave; t < nt; t += nw) {
-		topk_softmax_wave(lgm + t * E, E, k, slot_s + wave * MAX_K, slot_i + wave * MAX_K,
+		topk_softmax_wave(lgm + t * E, E, k,
 				  topk_idx + (size_t)(t0 + t) * k, topk_w + (size_t)(t0 + t) * k);
 		__builtin_amdgcn_wave_barrier();
 	}
