@@ -196,7 +196,7 @@ static int ensure_workspace(int T, int k, int d, int F, int E)
 		return o;
 	};
 	const size_t o_idx = take(P * 4), o_w = take(P * 4), o_cnt = take(EE * 4), o_off = take((EE + 1) * 4),
-		     o_pairs = take(P * 4), o_act = take((EE + 1) * 4), o_sync = take(64 * 4),
+		     o_pairs = take(P * 4), o_act = take((EE + 1) * 4), o_sync = take((Tcap / 4 + 64) * 4),
 		     o_logits = take(Tcap * EE * 4), o_h = take(3 * P * FF * 4), o_cnt2 = take(P * (FF / 64) * 4), o_hb = take(P * FF * 2),
 		     o_y = take(P * DD * 4), o_xb = take(Tcap * DD * 2);
 	const size_t max_tiles = (size_t)mfma_max_tiles((int)P, (int)EE);
@@ -233,7 +233,7 @@ static int ensure_workspace(int T, int k, int d, int F, int E)
 	w.cap_d = DD;
 	w.cap_E = EE;
 	// completion counters start at zero and are reset by the kernels
-	HIP_TRY(hipMemsetAsync(w.sync, 0, 64 * 4, g.stream));
+	HIP_TRY(hipMemsetAsync(w.sync, 0, (Tcap / 4 + 64) * 4, g.stream));
 	HIP_TRY(hipMemsetAsync(w.tile_cnt, 0, P * (FF / 64) * 4, g.stream));
 	HIP_TRY(hipStreamSynchronize(g.stream));
 	return TIE_HIP_OK;

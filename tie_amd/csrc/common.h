@@ -19,7 +19,7 @@ constexpr size_t Q6K_PANEL = (size_t)PANEL_ROWS * Q6K_BYTES; // 13440
 constexpr int MAX_K = 32;
 constexpr int MAX_E = 1024;
 constexpr int SILU_N = TIE_SILU_TABLE_SIZE;
-constexpr int MFMA_MT = 128; // pair rows per MFMA work tile
+constexpr int MFMA_MT = 256; // pair rows per MFMA work tile
 
 // Device layout of one stacked expert tensor [E][rows][in].
 //
@@ -65,7 +65,7 @@ struct Workspace {
 	int32_t *offsets = nullptr;   // [E+1]    start of each expert's pair list
 	int32_t *pairs = nullptr;     // [T*k]    pair ids t*k+j grouped by expert
 	int32_t *active = nullptr;    // [E+1]    active experts; active[E] = count
-	uint32_t *sync = nullptr;     // [64]     grid-completion counters (self-resetting)
+	uint32_t *sync = nullptr;     // [T/4+64] grid-completion counters (self-resetting)
 	float *logits = nullptr;      // [T][E]   router logits
 	float *h = nullptr;           // [3][T*k][F] SwiGLU output, gate sums, up sums (exact path)
 	uint32_t *tile_cnt = nullptr; // [T*k][F/64] gate/up completion counters (self-resetting)

@@ -3,19 +3,24 @@
 // Reference: TIE runs every (token, expert) pair as three GEMVs
 // (process_expert_task, engine.c:916-964) with no reuse of an expert's
 // weights across tokens.  For large T the pairs are grouped by expert
-// (dispatch.hip) and each expert's weights are dequantised once per tile and
+// (dispatch.hip) and each expert's weights are dequantised once and
 // multiplied against all of its tokens with v_mfma_f32_32x32x16_bf16:
 //
 //   gate/up:  G = X_e Wg_e^T, U = X_e Wu_e^T, h = silu_tab(G) * U  (fused)
 //   down:     Y = h_e Wd_e^T, scattered to the pairs' rows of y
 //
-// Tiles: a workgroup (4 waves) owns MT = 128 pair rows of one expert and
-// 128 weight rows (gate: 64 gate + the same 64 up rows, so the SwiGLU of
-// TIE's swiglu_activation_f32_f32_avx2 is applied to the accumulators in
-// registers; down: two 64-row panels).  K advances 64 at a time: the A tile
-// (bf16 activations, gathered by pair) is copied into LDS and the B tile is
-// dequantised from the panel layout straight into LDS as bf16.  Wave w
-// multiplies A rows 32w..32w+31 by the four 32-row B tiles.
+// Tiles: a workgroup (8 waves) owns up to MT = 256 pair rows of one expert
+// -- a whole expert at the usual prefill load of ~T*k/E rows, so each weight
+// is dequantised once per call -- and 128 weight rows (gate/up: 64 gate
+// rows and the same 64 up rows, so TIE's table SwiGLU
+// (swiglu_activation_f32_f32_avx2) is applied to the accumulators in
+// registers; down: two 64-row panels).  K advances 64 at a time through a
+// double-buffered LDS pipeline: the global loads of step k+1 are issued
+// into registers before the MFMAs of step k and written to the other buffer
+// after them (the B tile dequantised from the panel layout on the way), one
+// barrier per step.  Waves form a 4 (M) x 2 (N) grid of 64 x 64 tiles; the
+// M index runs fastest across SIMDs, so a half-full tile still keeps every
+// SIMD's matrix core busy.
 //
 // Numerics: fp32 accumulation of bf16 products.  Q4_K/Q6_K weights are
 // dequantised in fp32 exactly as TIE does (fma(q, d*sc, -dmin*m); d*sc*q)
@@ -29,23 +34,28 @@
 namespace tie {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int MT = 128;       // pair rows per workgroup
+constexpr int MT = MFMA_MT;   // pair rows per workgroup (256)
 constexpr int NT = 128;       // weight rows per workgroup
 constexpr int KS = 64;        // K per stage
 constexpr int LDK = KS + 8;   // LDS row stride (bf16) -- padding against bank conflicts
-constexpr int MF_THREADS = 256;
+constexpr int MF_THREADS = 512;
 
 __device__ __forceinline__ uint16_t bf16_bits(float f)
 {
 	return __builtin_bit_cast(uint16_t, (__bf16)f);
 }
 
+// two floats -> two round-to-nearest-even bf16 in one v_cvt_pk_bf16_f32
 __device__ __forceinline__ uint32_t pack_bf16(float a, float b)
 {
-	return (uint32_t)bf16_bits(a) | ((uint32_t)bf16_bits(b) << 16);
+	const f32x2 v = {a, b};
+	return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
 
 struct MfmaArgs {
@@ -64,17 +74,16 @@ struct MfmaArgs {
 };
 
 // ------------------------------------------------------------------ staging
-// Each K-step moves a 128 x 64 A tile and a 128 x 64 B tile into LDS.  The
-// global loads of step kk+1 are issued into registers before the MFMAs of
-// step kk (Pref), and written to the other LDS buffer (with the B dequant)
-// after them, so HBM latency overlaps the matrix work: one barrier per step.
-//
-// Thread roles: A -- row tid/2, half tid%2 (32 K values); B -- panel
-// m = tid/128, panel row i = (tid/2)%64, half h = tid%2.
+// Thread roles per K-step:
+//   A: row tid/2 (0..255), half tid%2 -- 32 K values
+//   B: panel m = tid/256, panel row i = (tid/4)%64, quarter q = tid%4 -- 16 K values
 template <int TYPE, bool SPLIT> struct Pref {
 	u32x4 a[SPLIT ? 8 : 4];
-	u32x4 b[TYPE == TIE_GGML_Q4_K ? 2 : TYPE == TIE_GGML_Q6_K ? 5 : 4];
-	uint32_t d6;
+	u32x4 b0;       // Q4_K: scales chunk; Q6_K: ql; BF16: K 16q..16q+7
+	u32x4 b1;       // Q6_K: qh; BF16: K 16q+8..16q+15
+	u32x2 q4;       // Q4_K: 8 quant bytes
+	uint32_t s6;    // Q6_K: the 4 scale bytes holding this thread's scale
+	uint32_t d6;    // Q6_K: fp16 d
 };
 
 // B row in LDS of (panel m, panel row i).  Gate/up interleave the two
@@ -85,14 +94,13 @@ __device__ __forceinline__ int b_row(bool down, int m, int i)
 	return down ? m * 64 + i : (i >> 5) * 64 + m * 32 + (i & 31);
 }
 
-template <int TYPE, bool DOWN, bool SPLIT>
-__device__ __forceinline__ void load_step(const MfmaArgs &a, const uint8_t *bsrc0, const uint8_t *bsrc1, const char *arow, bool alive,
-					  int kk, Pref<TYPE, SPLIT> &p)
+template <int TYPE, bool SPLIT>
+__device__ __forceinline__ void load_step(const uint8_t *bsrc0, const uint8_t *bsrc1, const char *arow, int kk,
+					  Pref<TYPE, SPLIT> &p)
 {
 	const int h = threadIdx.x & 1;
 	// A (rows past the tile's end read row 0 -- always valid -- and are
 	// zeroed when stored)
-	(void)alive;
 	if (!SPLIT) {
 		const u32x4 *src = reinterpret_cast<const u32x4 *>(arow + ((size_t)kk * KS + 32 * h) * 2);
 #pragma unroll
@@ -105,26 +113,28 @@ __device__ __forceinline__ void load_step(const MfmaArgs &a, const uint8_t *bsrc
 			p.a[c] = src[c];
 	}
 	// B
-	const int m = threadIdx.x >> 7, i = (threadIdx.x >> 1) & 63;
+	const int m = threadIdx.x >> 8, i = (threadIdx.x >> 2) & 63, q = threadIdx.x & 3;
+	const uint8_t *bsrc = m ? bsrc1 : bsrc0;
 	if constexpr (TYPE == TIE_GGML_BF16) {
-		const u32x4 *src = reinterpret_cast<const u32x4 *>((m ? bsrc1 : bsrc0) + ((size_t)kk * KS + 32 * h) * 2);
-#pragma unroll
-		for (int c = 0; c < 4; c++)
-			p.b[c] = src[c];
+		const u32x4 *src = reinterpret_cast<const u32x4 *>(bsrc + ((size_t)kk * KS + 16 * q) * 2);
+		p.b0 = src[0];
+		p.b1 = src[1];
 	} else {
-		const uint8_t *panel = (m ? bsrc1 : bsrc0) + (size_t)(kk / 4) * panel_bytes(TYPE);
-		const u32x4 *pc = reinterpret_cast<const u32x4 *>(panel) + i;
+		const uint8_t *panel = bsrc + (size_t)(kk / 4) * panel_bytes(TYPE);
+		const uint8_t *lane_blk = panel + i * 16;
 		if constexpr (TYPE == TIE_GGML_Q4_K) {
+			// group g = kk%4 is quant bytes 32g..32g+31 = chunks 1+2g, 2+2g;
+			// quarter q takes bytes 8q..8q+7 of the group
 			const int g = kk & 3;
-			p.b[0] = pc[0];
-			p.b[1] = pc[(1 + 2 * g + h) * 64];
+			p.b0 = *reinterpret_cast<const u32x4 *>(lane_blk);
+			p.q4 = *reinterpret_cast<const u32x2 *>(lane_blk + (1 + 2 * g + (q >> 1)) * 1024 + 8 * (q & 1));
 		} else {
-			const int n = (kk >> 1) & 1, r = 2 * (kk & 1) + h;
-			p.b[0] = pc[(4 * n + 2 * (r & 1)) * 64];
-			p.b[1] = pc[(4 * n + 2 * (r & 1) + 1) * 64];
-			p.b[2] = pc[(8 + 2 * n) * 64];
-			p.b[3] = pc[(9 + 2 * n) * 64];
-			p.b[4] = pc[12 * 64];
+			// half n = (kk/2)%2, quant row r = 2*(kk%2) + q/2, positions 16*(q%2)..+15
+			const int n = (kk >> 1) & 1, r = 2 * (kk & 1) + (q >> 1), hl = q & 1;
+			p.b0 = *reinterpret_cast<const u32x4 *>(lane_blk + (4 * n + 2 * (r & 1) + hl) * 1024);
+			p.b1 = *reinterpret_cast<const u32x4 *>(lane_blk + (8 + 2 * n + hl) * 1024);
+			const int sj = 8 * n + hl + 2 * r; // scale index
+			p.s6 = *reinterpret_cast<const uint32_t *>(lane_blk + 12 * 1024 + 4 * (sj >> 2));
 			p.d6 = reinterpret_cast<const uint16_t *>(panel + Q6K_CHUNKS * 1024)[i];
 		}
 	}
@@ -142,9 +152,9 @@ __device__ __forceinline__ void store_step(const Pref<TYPE, SPLIT> &p, bool aliv
 		if (!alive) {
 #pragma unroll
 			for (int c = 0; c < 4; c++) {
-				reinterpret_cast<uint4 *>(dst)[c] = make_uint4(0, 0, 0, 0);
+				reinterpret_cast<u32x4 *>(dst)[c] = u32x4{0, 0, 0, 0};
 				if (SPLIT)
-					reinterpret_cast<uint4 *>(Alo + (tid >> 1) * LDK + 32 * h)[c] = make_uint4(0, 0, 0, 0);
+					reinterpret_cast<u32x4 *>(Alo + (tid >> 1) * LDK + 32 * h)[c] = u32x4{0, 0, 0, 0};
 			}
 		} else if (!SPLIT) {
 #pragma unroll
@@ -154,27 +164,25 @@ __device__ __forceinline__ void store_step(const Pref<TYPE, SPLIT> &p, bool aliv
 			uint16_t *dlo = Alo + (tid >> 1) * LDK + 32 * h;
 #pragma unroll
 			for (int c = 0; c < 8; c++) {
-				const float4 v = make_float4(__uint_as_float(p.a[c].x), __uint_as_float(p.a[c].y),
-							     __uint_as_float(p.a[c].z), __uint_as_float(p.a[c].w));
-				const float hi0 = (float)(__bf16)v.x, hi1 = (float)(__bf16)v.y;
-				const float hi2 = (float)(__bf16)v.z, hi3 = (float)(__bf16)v.w;
-				reinterpret_cast<uint2 *>(dst)[c] = make_uint2(pack_bf16(hi0, hi1), pack_bf16(hi2, hi3));
-				reinterpret_cast<uint2 *>(dlo)[c] =
-					make_uint2(pack_bf16(v.x - hi0, v.y - hi1), pack_bf16(v.z - hi2, v.w - hi3));
+				const float v0 = __uint_as_float(p.a[c].x), v1 = __uint_as_float(p.a[c].y);
+				const float v2 = __uint_as_float(p.a[c].z), v3 = __uint_as_float(p.a[c].w);
+				const float hi0 = (float)(__bf16)v0, hi1 = (float)(__bf16)v1;
+				const float hi2 = (float)(__bf16)v2, hi3 = (float)(__bf16)v3;
+				reinterpret_cast<u32x2 *>(dst)[c] = u32x2{pack_bf16(hi0, hi1), pack_bf16(hi2, hi3)};
+				reinterpret_cast<u32x2 *>(dlo)[c] = u32x2{pack_bf16(v0 - hi0, v1 - hi1), pack_bf16(v2 - hi2, v3 - hi3)};
 			}
 		}
 	}
 	// B
-	const int m = tid >> 7, i = (tid >> 1) & 63;
+	const int m = tid >> 8, i = (tid >> 2) & 63, q = tid & 3;
 	uint16_t *brow = Bs + b_row(DOWN, m, i) * LDK;
 	if constexpr (TYPE == TIE_GGML_BF16) {
-#pragma unroll
-		for (int c = 0; c < 4; c++)
-			reinterpret_cast<u32x4 *>(brow + 32 * h)[c] = p.b[c];
+		reinterpret_cast<u32x4 *>(brow + 16 * q)[0] = p.b0;
+		reinterpret_cast<u32x4 *>(brow + 16 * q)[1] = p.b1;
 	} else if constexpr (TYPE == TIE_GGML_Q4_K) {
-		// K slice = group g (sub-blocks 2g, 2g+1); half h = bytes 16h..16h+15 of the group
+		// sub-blocks 2g (low nibbles, K 0..31) and 2g+1 (high nibbles, K 32..63)
 		const int g = kk & 3;
-		const u32x4 c0 = p.b[0], q = p.b[1];
+		const u32x4 c0 = p.b0;
 		const float d = half_bits_to_float(c0.x & 0xffffu), dmin = half_bits_to_float(c0.x >> 16);
 		auto sb = [&](int j) {
 			const int wi = j >> 2;
@@ -195,53 +203,50 @@ __device__ __forceinline__ void store_step(const Pref<TYPE, SPLIT> &p, bool aliv
 		scale_min(2 * g + 1, sc1, m1);
 		const float D0 = d * (float)sc0, M0 = -(dmin * (float)m0);
 		const float D1 = d * (float)sc1, M1 = -(dmin * (float)m1);
-		const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
-		uint32_t lo[8], hi[8];
+		uint32_t lo[2], hi[2];
+		lo[0] = p.q4.x & 0x0f0f0f0fu;
+		lo[1] = p.q4.y & 0x0f0f0f0fu;
+		hi[0] = (p.q4.x >> 4) & 0x0f0f0f0fu;
+		hi[1] = (p.q4.y >> 4) & 0x0f0f0f0fu;
+		// keep the masks byte-parallel so each weight is one v_cvt_f32_ubyteN
+		asm volatile("" : "+v"(lo[0]), "+v"(lo[1]), "+v"(hi[0]), "+v"(hi[1]));
+		uint32_t pl[4], ph[4];
+#pragma unroll
+		for (int j = 0; j < 4; j++) {
+			const uint32_t wl = lo[j >> 1], wh = hi[j >> 1];
+			const int s0 = 16 * (j & 1);
+			pl[j] = pack_bf16(__builtin_fmaf((float)((wl >> s0) & 0xffu), D0, M0),
+					  __builtin_fmaf((float)((wl >> (s0 + 8)) & 0xffu), D0, M0));
+			ph[j] = pack_bf16(__builtin_fmaf((float)((wh >> s0) & 0xffu), D1, M1),
+					  __builtin_fmaf((float)((wh >> (s0 + 8)) & 0xffu), D1, M1));
+		}
+		*reinterpret_cast<u32x4 *>(brow + 8 * q) = u32x4{pl[0], pl[1], pl[2], pl[3]};
+		*reinterpret_cast<u32x4 *>(brow + 32 + 8 * q) = u32x4{ph[0], ph[1], ph[2], ph[3]};
+	} else {
+		// Q6_K: q = (ql nibble | qh bits << 4); w = (d*sc) * (q - 32), exact in fp32
+		const int r = 2 * (kk & 1) + (q >> 1), hl = q & 1;
+		const int n = (kk >> 1) & 1;
+		const int sj = 8 * n + hl + 2 * r;
+		const float W = half_bits_to_float(p.d6) * (float)(int8_t)((p.s6 >> (8 * (sj & 3))) & 0xffu);
+		const float N = -32.0f * W;
+		const int nsh = 4 * (r >> 1), hsh = 2 * r;
+		uint32_t qv[4];
+		const uint32_t qlw[4] = {p.b0.x, p.b0.y, p.b0.z, p.b0.w};
+		const uint32_t qhw[4] = {p.b1.x, p.b1.y, p.b1.z, p.b1.w};
+#pragma unroll
+		for (int j = 0; j < 4; j++)
+			qv[j] = ((qlw[j] >> nsh) & 0x0f0f0f0fu) | (((qhw[j] >> hsh) & 0x03030303u) << 4);
+		asm volatile("" : "+v"(qv[0]), "+v"(qv[1]), "+v"(qv[2]), "+v"(qv[3]));
+		uint32_t pk[8];
 #pragma unroll
 		for (int j = 0; j < 8; j++) {
-			const uint32_t b0 = (qw[j >> 1] >> (16 * (j & 1))) & 0xffu;
-			const uint32_t b1 = (qw[j >> 1] >> (16 * (j & 1) + 8)) & 0xffu;
-			lo[j] = pack_bf16(__builtin_fmaf((float)(b0 & 15u), D0, M0), __builtin_fmaf((float)(b1 & 15u), D0, M0));
-			hi[j] = pack_bf16(__builtin_fmaf((float)(b0 >> 4), D1, M1), __builtin_fmaf((float)(b1 >> 4), D1, M1));
+			const uint32_t wd = qv[j >> 1];
+			const int s0 = 16 * (j & 1);
+			pk[j] = pack_bf16(__builtin_fmaf((float)((wd >> s0) & 0xffu), W, N),
+					  __builtin_fmaf((float)((wd >> (s0 + 8)) & 0xffu), W, N));
 		}
-		uint16_t *d0 = brow + 16 * h; // lo nibbles: K 16h..16h+15; hi nibbles: 32+16h..
-		reinterpret_cast<uint4 *>(d0)[0] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-		reinterpret_cast<uint4 *>(d0)[1] = make_uint4(lo[4], lo[5], lo[6], lo[7]);
-		reinterpret_cast<uint4 *>(d0 + 32)[0] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-		reinterpret_cast<uint4 *>(d0 + 32)[1] = make_uint4(hi[4], hi[5], hi[6], hi[7]);
-	} else {
-		// Q6_K: K slice = half n of the block, quant row r = 2*(kk&1) + h
-		// (elements 32r + l); w = (d * sc) * (q - 32), exact in fp32
-		const int n = (kk >> 1) & 1, r = 2 * (kk & 1) + h;
-		const uint32_t qlw[8] = {p.b[0].x, p.b[0].y, p.b[0].z, p.b[0].w, p.b[1].x, p.b[1].y, p.b[1].z, p.b[1].w};
-		const uint32_t qhw[8] = {p.b[2].x, p.b[2].y, p.b[2].z, p.b[2].w, p.b[3].x, p.b[3].y, p.b[3].z, p.b[3].w};
-		const float d = half_bits_to_float(p.d6);
-		auto scale = [&](int j) {
-			const int wi = j >> 2;
-			const uint32_t wd = wi == 0 ? p.b[4].x : (wi == 1 ? p.b[4].y : (wi == 2 ? p.b[4].z : p.b[4].w));
-			return (float)(int8_t)((wd >> (8 * (j & 3))) & 0xffu);
-		};
-		const float W0 = d * scale(8 * n + 2 * r), W1 = d * scale(8 * n + 1 + 2 * r);
-		const float N0 = -32.0f * W0, N1 = -32.0f * W1;
-		const int nsh = 4 * (r >> 1), hsh = 2 * r;
-		uint32_t pk[16];
-#pragma unroll
-		for (int j = 0; j < 16; j++) {
-			float wv[2];
-#pragma unroll
-			for (int t = 0; t < 2; t++) {
-				const int l = 2 * j + t;
-				const uint32_t L = (qlw[l >> 2] >> (8 * (l & 3))) & 0xffu;
-				const uint32_t H = (qhw[l >> 2] >> (8 * (l & 3))) & 0xffu;
-				const uint32_t qv = ((L >> nsh) & 15u) | (((H >> hsh) & 3u) << 4);
-				wv[t] = l < 16 ? __builtin_fmaf((float)qv, W0, N0) : __builtin_fmaf((float)qv, W1, N1);
-			}
-			pk[j] = pack_bf16(wv[0], wv[1]);
-		}
-#pragma unroll
-		for (int c = 0; c < 4; c++)
-			reinterpret_cast<uint4 *>(brow + 32 * h)[c] = make_uint4(pk[4 * c], pk[4 * c + 1], pk[4 * c + 2],
-										 pk[4 * c + 3]);
+		*reinterpret_cast<u32x4 *>(brow + 32 * (r & 1) + 16 * hl) = u32x4{pk[0], pk[1], pk[2], pk[3]};
+		*reinterpret_cast<u32x4 *>(brow + 32 * (r & 1) + 16 * hl + 8) = u32x4{pk[4], pk[5], pk[6], pk[7]};
 	}
 }
 
@@ -251,14 +256,15 @@ __device__ __forceinline__ bf16x8 lds_frag(const uint16_t *base, int row, int k)
 }
 
 // ------------------------------------------------------------------ kernel
-// Workgroup tile 128 pairs x 128 weight rows; 2 x 2 waves of 64 x 64, each
-// a 2 x 2 grid of 32 x 32 MFMA tiles.
 template <int TYPE, bool DOWN, bool SPLIT>
 __global__ __launch_bounds__(MF_THREADS) void mfma_experts_kernel(MfmaArgs a)
 {
-	__shared__ __attribute__((aligned(16))) uint16_t As[2][MT * LDK];
-	__shared__ __attribute__((aligned(16))) uint16_t Bs[2][NT * LDK];
-	__shared__ __attribute__((aligned(16))) uint16_t Alo[SPLIT ? 2 : 1][SPLIT ? MT * LDK : 8];
+	// split activations need a second A tile: single-buffered then (the BF16
+	// path is HBM-bound, the extra barrier costs little)
+	constexpr int NBUF = SPLIT ? 1 : 2;
+	__shared__ __attribute__((aligned(16))) uint16_t As[NBUF][MT * LDK];
+	__shared__ __attribute__((aligned(16))) uint16_t Bs[NBUF][NT * LDK];
+	__shared__ __attribute__((aligned(16))) uint16_t Alo[1][SPLIT ? MT * LDK : 8];
 
 	const int tile = blockIdx.y;
 	if (tile >= *a.ntiles)
@@ -267,17 +273,18 @@ __global__ __launch_bounds__(MF_THREADS) void mfma_experts_kernel(MfmaArgs a)
 	const int pbase = a.offsets[e] + m0;
 	const int nrows = min(MT, a.offsets[e + 1] - pbase);
 	const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-	const int wm = w >> 1, wn = w & 1;
+	const int wm = w >> 1, wn = w & 1; // M (64-row slab) and N (64-col slab) of this wave
 	const int lr = lane & 31, lk = 8 * (lane >> 5);
+	const bool wave_live = 64 * wm < nrows;
 
-	// this thread's A row and B source rows/panels
+	// this thread's A row and B source
 	const int ar = threadIdx.x >> 1;
 	const bool alive = ar < nrows;
 	const size_t arow_idx = alive ? (DOWN ? (size_t)(pbase + ar) : (size_t)(a.pairs[pbase + ar] / a.k)) : 0;
 	const char *arow = SPLIT ? (const char *)(a.a32 + arow_idx * a.in) : (const char *)(a.a16 + arow_idx * a.in);
 	const uint8_t *bsrc[2];
 	{
-		const int bi = (threadIdx.x >> 1) & 63;
+		const int bi = (threadIdx.x >> 2) & 63;
 		const int nb = a.in / QK;
 #pragma unroll
 		for (int mm = 0; mm < 2; mm++) {
@@ -298,17 +305,11 @@ __global__ __launch_bounds__(MF_THREADS) void mfma_experts_kernel(MfmaArgs a)
 		for (int j = 0; j < 16; j++)
 			acc[t][j] = 0.0f;
 
-	const int nk = a.in / KS;
-	Pref<TYPE, SPLIT> pf;
-	load_step<TYPE, DOWN, SPLIT>(a, bsrc[0], bsrc[1], arow, alive, 0, pf);
-	store_step<TYPE, DOWN, SPLIT>(pf, alive, 0, As[0], Alo[0], Bs[0]);
-	__syncthreads();
-	for (int kk = 0; kk < nk; kk++) {
-		const int cur = kk & 1;
-		if (kk + 1 < nk)
-			load_step<TYPE, DOWN, SPLIT>(a, bsrc[0], bsrc[1], arow, alive, kk + 1, pf);
+	auto compute = [&](int cur) {
+		if (!wave_live)
+			return;
 		const uint16_t *A = As[cur], *B = Bs[cur];
-		const uint16_t *AL = Alo[SPLIT ? cur : 0];
+		const uint16_t *AL = Alo[0];
 #pragma unroll
 		for (int s = 0; s < KS / 16; s++) {
 			const bf16x8 a0 = lds_frag(A, 64 * wm + lr, 16 * s + lk);
@@ -328,10 +329,27 @@ __global__ __launch_bounds__(MF_THREADS) void mfma_experts_kernel(MfmaArgs a)
 				acc[3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(l1, b1, acc[3], 0, 0, 0);
 			}
 		}
+	};
+
+	const int nk = a.in / KS;
+	Pref<TYPE, SPLIT> pf;
+	load_step<TYPE, SPLIT>(bsrc[0], bsrc[1], arow, 0, pf);
+	store_step<TYPE, DOWN, SPLIT>(pf, alive, 0, As[0], Alo[0], Bs[0]);
+	__syncthreads();
+	for (int kk = 0; kk < nk; kk++) {
+		const int cur = NBUF == 2 ? (kk & 1) : 0;
+		const int nxt = NBUF == 2 ? (cur ^ 1) : 0;
 		if (kk + 1 < nk)
-			store_step<TYPE, DOWN, SPLIT>(pf, alive, kk + 1, As[cur ^ 1], Alo[SPLIT ? cur ^ 1 : 0], Bs[cur ^ 1]);
+			load_step<TYPE, SPLIT>(bsrc[0], bsrc[1], arow, kk + 1, pf);
+		compute(cur);
+		if (NBUF == 1)
+			__syncthreads();
+		if (kk + 1 < nk)
+			store_step<TYPE, DOWN, SPLIT>(pf, alive, kk + 1, As[nxt], Alo[0], Bs[nxt]);
 		__syncthreads();
 	}
+	if (!wave_live)
+		return;
 
 	// D layout of v_mfma_f32_32x32x16: lane l, register j holds
 	// row 8*(j/4) + 4*(l/32) + j%4, column l%32.

@@ -147,34 +147,33 @@ __global__ __launch_bounds__(RS_THREADS) void router_small_kernel(const float *_
 		}
 	}
 
-	// grid completion: the last workgroup selects experts for every token
+	// completion per token group: the last of the E workgroups of this
+	// group (counter blockIdx.y, self-resetting) selects the experts of its
+	// tokens, one wave per token
 	__syncthreads();
+	uint32_t *cnt = counter + blockIdx.y;
 	if (tid == 0) {
 		__threadfence();
-		const uint32_t total = gridDim.x * gridDim.y;
-		const uint32_t prev = atomicAdd(counter, 1u);
-		s_last = (prev == total - 1);
+		const uint32_t prev = atomicAdd(cnt, 1u);
+		s_last = (prev == gridDim.x - 1);
 	}
 	__syncthreads();
 	if (!s_last)
 		return;
 	__threadfence();
-	float *lg = lds; // reuse: one token's logits at a time per wave
 	const int wave = tid >> 6;
-	const int nw = RS_THREADS / 64;
-	for (int t = wave; t < T; t += nw) {
-		float *my = lg + (size_t)wave * E;
+	if (wave < nt) {
+		const int t = t0 + wave;
+		float *my = lds + (size_t)wave * E;
 		for (int q = tid & 63; q < E; q += 64)
 			my[q] = __hip_atomic_load(logits + (size_t)t * E + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 		__builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
 		__builtin_amdgcn_wave_barrier();
 		__builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-		topk_softmax_wave(my, E, k, topk_idx + (size_t)t * k,
-				  topk_w + (size_t)t * k);
-		__builtin_amdgcn_wave_barrier();
+		topk_softmax_wave(my, E, k, topk_idx + (size_t)t * k, topk_w + (size_t)t * k);
 	}
 	if (tid == 0)
-		__hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+		__hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ------------------------------------------------------------ router_tiled
