@@ -12,7 +12,8 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libtie_hip.so")
+# TIE_AMD_LIB selects another build of the same library (e.g. a tuning variant)
+LIB_PATH = os.environ.get("TIE_AMD_LIB") or os.path.join(HERE, "libtie_hip.so")
 
 F32, Q4_K, Q6_K, BF16 = 0, 12, 14, 30
 OK, EINVAL, EHIP, ENOMEM, ENOINIT = 0, -1, -2, -3, -4
