@@ -198,7 +198,8 @@ static int ensure_workspace(int T, int k, int d, int F, int E)
 	const size_t o_idx = take(P * 4), o_w = take(P * 4), o_cnt = take(EE * 4), o_off = take((EE + 1) * 4),
 		     o_pairs = take(P * 4), o_act = take((EE + 1) * 4), o_sync = take((Tcap / 4 + 64) * 4),
 		     o_logits = take(Tcap * EE * 4), o_h = take(3 * P * FF * 4), o_cnt2 = take(P * (FF / 64) * 4), o_hb = take(P * FF * 2),
-		     o_y = take(P * DD * 4), o_xb = take(Tcap * DD * 2);
+		     o_y = take(P * DD * 4), o_xb = take(Tcap * DD * 2), o_hlo = take(P * FF * 2),
+		     o_xlo = take(Tcap * DD * 2);
 	const size_t max_tiles = (size_t)mfma_max_tiles((int)P, (int)EE);
 	const size_t o_te = take(max_tiles * 4), o_tm = take(max_tiles * 4), o_nt = take(4);
 	void *mem = nullptr;
@@ -225,6 +226,8 @@ static int ensure_workspace(int T, int k, int d, int F, int E)
 	w.hb = (uint16_t *)(b + o_hb);
 	w.y = (float *)(b + o_y);
 	w.xb = (uint16_t *)(b + o_xb);
+	w.hlo = (uint16_t *)(b + o_hlo);
+	w.xlo = (uint16_t *)(b + o_xlo);
 	w.tile_e = (int32_t *)(b + o_te);
 	w.tile_m0 = (int32_t *)(b + o_tm);
 	w.ntiles = (int32_t *)(b + o_nt);

@@ -71,8 +71,10 @@ struct Workspace {
 	uint32_t *tile_cnt = nullptr; // [T*k][F/64] gate/up completion counters (self-resetting)
 	uint16_t *hb = nullptr;       // [T*k][F] SwiGLU activations (bf16 hi/lo, MFMA path)
 	float *y = nullptr;           // [T*k][d] expert outputs
+	uint16_t *hlo = nullptr;      // [T*k][F] SwiGLU activations, bf16 remainder (MFMA path, BF16 weights)
 	uint16_t *xb = nullptr;       // [T][d]   x as bf16 (MFMA path)
-	int32_t *tile_e = nullptr;    // [max tiles] MFMA work list: expert of each 128-pair tile
+	uint16_t *xlo = nullptr;      // [T][d]   x - bf16(x) as bf16 (MFMA path, BF16 weights)
+	int32_t *tile_e = nullptr;    // [max tiles] MFMA work list: expert of each MFMA_MT-pair tile
 	int32_t *tile_m0 = nullptr;   // [max tiles] first pair of the tile within the expert
 	int32_t *ntiles = nullptr;    // [1]
 	size_t cap_pairs = 0, cap_F = 0, cap_d = 0, cap_E = 0;
