@@ -285,7 +285,7 @@ static int create_layer(const tie_hip_layer_desc *ds, tie_hip_layer **out)
 	const size_t b_router = align256((size_t)E * d * 4), b_bias = align256((size_t)E * 4);
 	const size_t b_gate = align256(E * L.gate.expert_bytes), b_up = align256(E * L.up.expert_bytes),
 		     b_down = align256(E * L.down.expert_bytes);
-	L.bytes = b_router + b_bias + b_gate + b_up + b_down;
+	L.bytes = 2 * b_router + b_bias + b_gate + b_up + b_down;
 	rc = dev_malloc(&L.alloc, L.bytes, "layer weights");
 	if (rc) {
 		delete l;
@@ -294,7 +294,8 @@ static int create_layer(const tie_hip_layer_desc *ds, tie_hip_layer **out)
 	uint8_t *base = (uint8_t *)L.alloc;
 	L.router = (const float *)base;
 	L.bias = ds->router_bias ? (const float *)(base + b_router) : nullptr;
-	L.gate.data = base + b_router + b_bias;
+	L.routerT = (const float *)(base + b_router + b_bias);
+	L.gate.data = base + 2 * b_router + b_bias;
 	L.up.data = L.gate.data + b_gate;
 	L.down.data = L.up.data + b_up;
 
@@ -302,6 +303,8 @@ static int create_layer(const tie_hip_layer_desc *ds, tie_hip_layer **out)
 	hipError_t e = hipMemcpyAsync((void *)L.router, ds->router_w, (size_t)E * d * 4, kind, g.stream);
 	if (e == hipSuccess && ds->router_bias)
 		e = hipMemcpyAsync((void *)L.bias, ds->router_bias, (size_t)E * 4, kind, g.stream);
+	if (e == hipSuccess)
+		e = launch_router_transpose(L, g.stream);
 	struct Src {
 		const ExpertTensor *t;
 		const void *p;

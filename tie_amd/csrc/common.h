@@ -51,6 +51,7 @@ __host__ __device__ inline size_t panel_bytes(int type)
 struct Layer {
 	int d = 0, F = 0, E = 0;
 	const float *router = nullptr; // [E][d]
+	const float *routerT = nullptr; // [d][E] (the tiled router kernel's layout)
 	const float *bias = nullptr;   // [E] or null
 	ExpertTensor gate, up, down;
 	void *alloc = nullptr;         // one device allocation holding everything
@@ -84,6 +85,7 @@ struct Workspace {
 // ---------------------------------------------------------------- launchers
 hipError_t launch_router(const Layer &L, const float *x, int T, int k, float *logits, int32_t *topk_idx,
 			 float *topk_w, uint32_t *counter, hipStream_t s);
+hipError_t launch_router_transpose(const Layer &L, hipStream_t s);
 hipError_t launch_dispatch(const Layer &L, int T, int k, const int32_t *topk_idx, Workspace &ws, hipStream_t s);
 hipError_t launch_exact_experts(const Layer &L, const float *x, int T, int k, const float *silu, Workspace &ws,
 				hipStream_t s);

@@ -45,9 +45,11 @@ TIE_HD uint64_t tie_as_u64(double d)
 	return __builtin_bit_cast(uint64_t, d);
 }
 
-TIE_HD float tie_expf(float x)
+// tab: the 32 entries of TIE_EXP2_TABLE (device code passes a copy in LDS:
+// a table lookup with a per-lane index is then an LDS read, not a load
+// from global memory)
+TIE_HD float tie_expf_tab(float x, const uint64_t *tab)
 {
-	const uint64_t tab[32] = TIE_EXP2_TABLE;
 	const double inv_ln2_n = 0x1.71547652b82fep+0 * 32.0;
 	const double shift = 0x1.8p+52;
 	const double c0 = 0x1.c6af84b912394p-5 / (32.0 * 32.0 * 32.0);
@@ -81,4 +83,10 @@ TIE_HD float tie_expf(float x)
 	y = __builtin_fma(zz, r2, y);
 	y = y * s;
 	return (float)y;
+}
+
+TIE_HD float tie_expf(float x)
+{
+	const uint64_t tab[32] = TIE_EXP2_TABLE;
+	return tie_expf_tab(x, tab);
 }
