@@ -19,7 +19,7 @@ constexpr size_t Q6K_PANEL = (size_t)PANEL_ROWS * Q6K_BYTES; // 13440
 constexpr int MAX_K = 32;
 constexpr int MAX_E = 1024;
 constexpr int SILU_N = TIE_SILU_TABLE_SIZE;
-constexpr int MFMA_MT = 256; // pair rows per MFMA work tile
+constexpr int MFMA_MT = 192; // pair rows per MFMA work tile at most
 
 // Device layout of one stacked expert tensor [E][rows][in].
 //

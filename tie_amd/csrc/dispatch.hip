@@ -94,9 +94,11 @@ __global__ __launch_bounds__(DSP_THREADS) void dispatch_kernel(const int32_t *__
 		counts[e] = c;
 		if (c > 0)
 			active[aidx] = e;
+		// the expert's pairs split evenly over its nt tiles
+		const int rpt = nt > 0 ? (c + nt - 1) / nt : 0;
 		for (int t = 0; t < nt; t++) {
 			tile_e[toff + t] = e;
-			tile_m0[toff + t] = t * MFMA_MT;
+			tile_m0[toff + t] = t * rpt;
 		}
 	}
 	if (tid == 0) {

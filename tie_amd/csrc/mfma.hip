@@ -5,28 +5,37 @@
 // weights across tokens.  For large T the pairs are grouped by expert
 // (dispatch.hip) and each expert's weights are dequantised once per work
 // tile and multiplied against all of the tile's tokens with
-// v_mfma_f32_16x16x32_bf16:
+// v_mfma_f32_32x32x16_bf16:
 //
 //   gate/up:  G = X_e Wg_e^T, U = X_e Wu_e^T, h = silu_tab(G) * U  (fused)
 //   down:     Y = h_e Wd_e^T, scattered to the pairs' rows of y
 //
-// Work tile: up to MT = 256 pair rows of one expert (the usual prefill load
-// is ~T*k/E rows, so an expert is one tile) x 128 F columns (gate/up: of
-// gate and of up) or 256 output columns (down).  A workgroup is 8 waves,
-// two per SIMD; wave w owns two 16-wide column tiles -- gate/up: the gate
-// and the up tile of F columns 16w..16w+15, so TIE's table SwiGLU
+// Work tile: up to MT = 192 pair rows of one expert (an expert with more
+// pairs is split evenly over several tiles; the usual prefill load is
+// ~T*k/E rows, one tile) x 128 F columns (gate/up: of gate and of up) or
+// 256 output columns (down).  A workgroup is 4 waves,
+// one per SIMD; wave w owns two 32-wide column tiles -- gate/up: the gate
+// and the up tile of F columns 32w..32w+31, so TIE's table SwiGLU
 // (swiglu_activation_f32_f32_avx2) is applied to the accumulators in
-// registers; down: columns 32w..32w+31 -- against all rows of the tile.
+// registers; down: columns 64w..64w+63 -- against all rows of the tile
+// (up to 6 x 2 accumulator tiles of 32x32, in the accumulation registers;
+// more rows would not leave the 256 architectural registers the
+// dequantisation pipeline needs).
 //
-// The weights never pass through LDS.  In the 16x16x32 B-operand layout a
-// lane holds 8 consecutive K values of one weight row; in the panel layout
-// (common.h) those are 8 consecutive quant bytes of one lane-row.  Each lane
-// loads its quant bytes straight from HBM into registers, one stage ahead,
-// and dequantises them into B fragments right before the MFMAs: every
-// weight of the tile is read and dequantised exactly once, and each B
-// fragment feeds up to 16 MFMAs (one per 16-row M tile).  Only the
-// activations (A, bf16) are staged, by direct global->LDS loads, through a
-// double-buffered LDS tile the 8 waves share; one barrier per K stage.
+// Both operands are staged per K stage of 128 by direct global->LDS loads
+// (global_load_lds_dwordx4) into double-buffered LDS tiles, one stage
+// ahead: the activations (A, bf16 rows gathered by pair) and, for Q4_K /
+// Q6_K, the raw panel chunks of the workgroup's 4 weight panels (1 KiB
+// each: the panel layout of common.h).  No register holds a prefetched
+// stage, so the pipeline costs no registers, and the compiler's wait-count
+// pass never sees (and never waits for) the prefetch: the stage barrier is
+// the wait.  In the 32x32x16 B-operand layout a lane holds 8 consecutive K
+// values of one weight row -- 8 consecutive quant bytes of its lane-row in
+// the panel -- which it reads from LDS and dequantises between the MFMAs:
+// every weight of the tile is dequantised exactly once, and each B fragment
+// feeds up to 6 MFMAs (one per 32-row M tile).  BF16 weights (already
+// MFMA operands) are prefetched into registers instead.  An A fragment
+// (1 KiB) feeds two MFMAs: 64 B of LDS reads per CU per clock.
 //
 // Numerics: fp32 accumulation of bf16 products.  Q4_K/Q6_K weights are
 // dequantised in fp32 (fma(q, d*sc, -dmin*m); d*sc*(q-32), both as TIE's
@@ -43,15 +52,15 @@ namespace tie {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int MT = MFMA_MT;   // pair rows per work tile (256)
-constexpr int NWAVES = 8;
+constexpr int MT = MFMA_MT;   // pair rows per work tile at most (192)
+constexpr int NWAVES = 4;
 constexpr int MF_THREADS = 64 * NWAVES;
-constexpr int GU_COLS = 16 * NWAVES; // gate/up: F columns per tile (128)
-constexpr int DN_COLS = 32 * NWAVES; // down: output columns per tile (256)
+constexpr int GU_COLS = 32 * NWAVES; // gate/up: F columns per tile (128)
+constexpr int DN_COLS = 64 * NWAVES; // down: output columns per tile (256)
 
 __device__ __forceinline__ uint16_t bf16_bits(float f)
 {
@@ -95,8 +104,16 @@ template <int TYPE> struct Cfg {
 	static constexpr int NDMA = MT / (NWAVES * RPI);     // DMA instructions per wave, plane and stage
 	static constexpr int A_TILE = MT * RB;               // bytes per plane
 	static constexpr int ABUF = NPL * A_TILE;            // bytes per buffer
-	static constexpr int NSTEP = KST / 32;               // MFMA K steps per stage
-	// The slot of 16-byte chunk c of row r is c ^ swz(r): the 16 rows of a
+	static constexpr int NSTEP = KST / 16;               // MFMA K steps per stage
+	// Quantised weights are staged through LDS too (panel chunks of the
+	// stage, by direct loads): no registers hold the next stage's weights.
+	// BF16 weights are prefetched into registers.
+	static constexpr bool B_LDS = !SPLIT;
+	static constexpr int NCH = TYPE == TIE_GGML_Q4_K ? 5 : 7; // 1 KiB chunks per panel and stage
+	static constexpr int PB = NCH * 1024;                     // bytes per panel and stage
+	static constexpr int BBUF = B_LDS ? 4 * PB + (TYPE == TIE_GGML_Q6_K ? 4 * 128 : 0) : 0; // + Q6_K d planes
+	static constexpr int LDS_A = 2 * ABUF, LDS_B = 2 * BBUF;
+	// The slot of 16-byte chunk c of row r is c ^ swz(r): the rows of a
 	// fragment read then spread over all LDS banks without row padding
 	// (which the direct global->LDS loads cannot make).
 	__device__ static int swz(int r) { return SPLIT ? (r >> 1) & 7 : r & 15; }
@@ -104,21 +121,22 @@ template <int TYPE> struct Cfg {
 
 // ------------------------------------------------------------------ B registers
 // One stage of one lane's two weight rows (j = 0, 1), straight from HBM.
-// Lane l: row n = l%16 of the column tile, K quarter kq = l/16 of each
-// 32-K MFMA step (K 8kq..8kq+7).
+//   lane l: row n = l%32 of the column tile, K half h = l/32 of each 16-K step
 template <int TYPE> struct BRegs;
+__device__ __forceinline__ uint32_t lds_addr(const void *p);
+__device__ __forceinline__ void dma16(const void *g, uint32_t lds);
 template <> struct BRegs<TIE_GGML_Q4_K> {
-	u32x2 q[2][2];  // [row][group]: quant bytes 8kq..8kq+7 of the group (low nibbles: step 0, high: step 1)
+	u32x2 q[2][4];  // quant bytes 8h..8h+7 of the stage's 4 quant chunks
 	u32x4 sc[2];    // chunk 0: d, dmin, 12 scale bytes
 };
 template <> struct BRegs<TIE_GGML_Q6_K> {
-	u32x2 ql[2][2]; // [row][p]: ql bytes 32p + 8kq .. +7 of the half
-	u32x2 qh[2];    // qh bytes 8kq .. +7 of the half
+	u32x2 ql[2][4]; // ql bytes 16p+8h..+7 of the half, p = 0..3
+	u32x2 qh[2][2]; // qh bytes 16p+8h..+7 of the half, p = 0..1
 	u32x2 sc[2];    // the half's 8 scales
 	uint32_t d[2];  // fp16 d
 };
 template <> struct BRegs<TIE_GGML_BF16> {
-	u32x4 w[2][2];  // [row][step]: K 32s + 8kq .. +7 of the stage
+	u32x4 w[2][4];  // K 16s+8h..+7 of the stage, s = 0..3
 };
 
 // The lane's two weight rows.  Quantised: the lane-row's 16-byte slot in
@@ -131,38 +149,99 @@ struct BSrc {
 };
 
 template <int TYPE>
-__device__ __forceinline__ void load_b(const BSrc &s, int st, int kq, BRegs<TYPE> &b)
+__device__ __forceinline__ void load_b(const BSrc &s, int st, int h, BRegs<TYPE> &b)
 {
 	constexpr int KST = Cfg<TYPE>::KST;
 	if constexpr (TYPE == TIE_GGML_BF16) {
 #pragma unroll
 		for (int j = 0; j < 2; j++)
 #pragma unroll
-			for (int q = 0; q < 2; q++)
-				b.w[j][q] = *reinterpret_cast<const u32x4 *>(s.p[j] + ((size_t)st * KST + 32 * q + 8 * kq) * 2);
+			for (int q = 0; q < 4; q++)
+				b.w[j][q] = *reinterpret_cast<const u32x4 *>(s.p[j] + ((size_t)st * KST + 16 * q + 8 * h) * 2);
 	} else {
 		const size_t kb = (size_t)(st >> 1) * panel_bytes(TYPE); // two stages per 256-weight block
 		const int half = st & 1;
-		// byte 8kq of a 32-byte run starting at chunk c: chunk c + kq/2, offset 8 (kq%2)
-		const int sub = (kq >> 1) * 1024 + 8 * (kq & 1);
 #pragma unroll
 		for (int j = 0; j < 2; j++) {
-			const uint8_t *blk = s.p[j] + kb + sub;
+			const uint8_t *blk = s.p[j] + kb;
 			if constexpr (TYPE == TIE_GGML_Q4_K) {
-				// groups 2*half + g: quant bytes at chunks 1 + 2(2*half + g)
+				// groups 2*half, 2*half+1: quant chunks 1+4*half .. 4+4*half
 #pragma unroll
-				for (int g = 0; g < 2; g++)
-					b.q[j][g] = *reinterpret_cast<const u32x2 *>(blk + (1 + 2 * (2 * half + g)) * 1024);
-				b.sc[j] = *reinterpret_cast<const u32x4 *>(s.p[j] + kb);
+				for (int q = 0; q < 4; q++)
+					b.q[j][q] = *reinterpret_cast<const u32x2 *>(blk + (1 + 4 * half + q) * 1024 + 8 * h);
+				b.sc[j] = *reinterpret_cast<const u32x4 *>(blk);
 			} else {
-				// ql of half n: chunks 4n..4n+3; qh: chunks 8+2n, 9+2n
 #pragma unroll
-				for (int p = 0; p < 2; p++)
-					b.ql[j][p] = *reinterpret_cast<const u32x2 *>(blk + (4 * half + 2 * p) * 1024);
-				b.qh[j] = *reinterpret_cast<const u32x2 *>(blk + (8 + 2 * half) * 1024);
-				b.sc[j] = *reinterpret_cast<const u32x2 *>(s.p[j] + kb + 12 * 1024 + 8 * half);
-				b.d[j] = *reinterpret_cast<const uint16_t *>(s.p[j] + kb + s.dofs[j]);
+				for (int q = 0; q < 4; q++)
+					b.ql[j][q] = *reinterpret_cast<const u32x2 *>(blk + (4 * half + q) * 1024 + 8 * h);
+#pragma unroll
+				for (int q = 0; q < 2; q++)
+					b.qh[j][q] = *reinterpret_cast<const u32x2 *>(blk + (8 + 2 * half + q) * 1024 + 8 * h);
+				b.sc[j] = *reinterpret_cast<const u32x2 *>(blk + 12 * 1024 + 8 * half);
+				b.d[j] = *reinterpret_cast<const uint16_t *>(blk + s.dofs[j]);
 			}
+		}
+	}
+}
+
+// The stage's weight chunks of the workgroup's 4 panels -> LDS buffer B:
+// panel p (gate/up: gate panels 0, 1 and up panels 2, 3 of the tile's 128
+// columns; down: 4 panels of its 256 columns), chunk slot c, 1 KiB each.
+// Q4_K slots: 0 scales, 1..4 the stage's quant chunks 1+4h..4+4h.  Q6_K
+// slots: 0..3 ql chunks 4h..4h+3, 4, 5 qh chunks 8+2h, 9+2h, 6 the scales;
+// then the 4 panels' d planes (128 B each).  h = st % 2 (the block half).
+template <int TYPE, bool DOWN>
+__device__ __forceinline__ void dma_b(const MfmaArgs &a, int e, int slab, int st, int w, uint8_t *B)
+{
+	using C = Cfg<TYPE>;
+	const int lane = threadIdx.x & 63, half = st & 1;
+	const size_t pbytes = panel_bytes(TYPE);
+	auto panel = [&](int p) {
+		const int mat = DOWN ? 0 : p >> 1;
+		const int rt = DOWN ? 4 * slab + p : 2 * slab + (p & 1);
+		return a.w[mat] + (size_t)e * a.expert_bytes[mat] + ((size_t)rt * (a.in / QK) + (st >> 1)) * pbytes;
+	};
+#pragma unroll
+	for (int c = 0; c < C::NCH; c++) {
+		const int it = NWAVES * c + w; // item: panel it / NCH, slot it % NCH; NWAVES == 4 panels
+		const int p = it / C::NCH, s = it % C::NCH;
+		int chunk;
+		if constexpr (TYPE == TIE_GGML_Q4_K)
+			chunk = s == 0 ? 0 : 4 * half + s;
+		else
+			chunk = s < 4 ? 4 * half + s : (s < 6 ? 8 + 2 * half + (s - 4) : 12);
+		dma16(panel(p) + chunk * 1024 + 16 * lane, __builtin_amdgcn_readfirstlane(lds_addr(B + p * C::PB + s * 1024)));
+	}
+	if constexpr (TYPE == TIE_GGML_Q6_K) {
+		if (lane < 8)
+			dma16(panel(w) + Q6K_CHUNKS * 1024 + 16 * lane,
+			      __builtin_amdgcn_readfirstlane(lds_addr(B + 4 * C::PB + w * 128)));
+	}
+}
+
+// The lane's weights of the stage from LDS buffer B: row j of the lane in
+// panel p[j], slot i[j].
+template <int TYPE>
+__device__ __forceinline__ void lds_b(const uint8_t *B, const int p[2], const int i[2], int st, int h, BRegs<TYPE> &b)
+{
+	using C = Cfg<TYPE>;
+#pragma unroll
+	for (int j = 0; j < 2; j++) {
+		const uint8_t *pb = B + p[j] * C::PB + i[j] * 16;
+		if constexpr (TYPE == TIE_GGML_Q4_K) {
+#pragma unroll
+			for (int q = 0; q < 4; q++)
+				b.q[j][q] = *reinterpret_cast<const u32x2 *>(pb + (1 + q) * 1024 + 8 * h);
+			b.sc[j] = *reinterpret_cast<const u32x4 *>(pb);
+		} else if constexpr (TYPE == TIE_GGML_Q6_K) {
+#pragma unroll
+			for (int q = 0; q < 4; q++)
+				b.ql[j][q] = *reinterpret_cast<const u32x2 *>(pb + q * 1024 + 8 * h);
+#pragma unroll
+			for (int q = 0; q < 2; q++)
+				b.qh[j][q] = *reinterpret_cast<const u32x2 *>(pb + (4 + q) * 1024 + 8 * h);
+			b.sc[j] = *reinterpret_cast<const u32x2 *>(pb + 6 * 1024 + 8 * (st & 1));
+			b.d[j] = *reinterpret_cast<const uint16_t *>(B + 4 * C::PB + p[j] * 128 + 2 * i[j]);
 		}
 	}
 }
@@ -226,30 +305,31 @@ __device__ __forceinline__ void group_factors(const BRegs<TYPE> &b, int st, int 
 	}
 }
 
-// Dequantise the B fragments of 32-K step s of stage st for both rows.
-// Q4_K: step s is group gi = s/2 of the stage, low (s even) or high nibbles.
-// Q6_K: the stage is half st%2 of the block and step s is its quarter r = s:
-// positions l = 8kq + i, code q = ql[l + 32(r%2)] nibble r/2 | qh[l] bits 2r
-// << 4, scale 8*half + l/16 + 2r (TIE's block_q6_k).
+// Dequantise the B fragments of 16-K step s of stage st for both rows.
+// Q4_K: step s is in group gi = s/4; steps 0, 1 of a group take the low
+// nibbles of its two chunks, steps 2, 3 the high nibbles.  Q6_K: the stage
+// is half st%2 of the block; step s is quarter r = s/2, positions
+// l = 16*(s%2) + 8h + i, code q = ql nibble | qh bits << 4 with scale
+// 8*half + l/16 + 2r (TIE's block_q6_k).
 template <int TYPE>
-__device__ __forceinline__ void deq_step(const BRegs<TYPE> &b, const Fac &f, int s, int kq, bf16x8 out[2])
+__device__ __forceinline__ void deq_step(const BRegs<TYPE> &b, const Fac &f, int s, bf16x8 out[2])
 {
 #pragma unroll
 	for (int j = 0; j < 2; j++) {
 		if constexpr (TYPE == TIE_GGML_BF16) {
 			out[j] = __builtin_bit_cast(bf16x8, b.w[j][s]);
 		} else if constexpr (TYPE == TIE_GGML_Q4_K) {
-			const int u = s & 1;
-			const u32x2 q = b.q[j][s >> 1];
+			const int gi = s >> 2, sub = s & 3, u = sub >> 1;
+			const u32x2 q = b.q[j][2 * gi + (sub & 1)];
 			out[j] = deq8((q.x >> (4 * u)) & 0x0f0f0f0fu, (q.y >> (4 * u)) & 0x0f0f0f0fu, f.D[j][u], f.M[j][u]);
 		} else {
-			const int r = s;
-			const u32x2 ql = b.ql[j][r & 1];
-			const u32x2 qh = b.qh[j];
+			const int r = s >> 1, lh = s & 1;
+			const u32x2 ql = b.ql[j][2 * (r & 1) + lh];
+			const u32x2 qh = b.qh[j][lh];
 			const int nsh = 4 * (r >> 1), hsh = 2 * r;
 			const uint32_t lo = ((ql.x >> nsh) & 0x0f0f0f0fu) | (((qh.x >> hsh) & 0x03030303u) << 4);
 			const uint32_t hi = ((ql.y >> nsh) & 0x0f0f0f0fu) | (((qh.y >> hsh) & 0x03030303u) << 4);
-			const int si = (kq >> 1) + 2 * r; // scale byte within the half's 8
+			const int si = lh + 2 * r;
 			const uint32_t sw = si < 4 ? b.sc[j].x : b.sc[j].y;
 			const float W = f.d6[j] * (float)(int8_t)((sw >> (8 * (si & 3))) & 0xffu);
 			out[j] = deq8(lo, hi, W, -32.0f * W);
@@ -265,9 +345,15 @@ __device__ __forceinline__ void deq_step(const BRegs<TYPE> &b, const Fac &f, int
 // covers rows RPI*(NWAVES c + w) ..; swz(row) does not depend on c.  Rows
 // past the tile's end are not loaded: an MFMA output row depends only on its
 // own A row, and the epilogue drops those rows.
+// The byte offsets of the tile's rows sit in an LDS table written once per
+// tile, not in registers, ordered so that the NDMA offsets one lane needs
+// per stage are contiguous (one wait per stage).  Rows past the tile's end
+// read the tile's first row instead (no branch; those LDS rows feed only
+// output rows the epilogue drops).
+constexpr int ROFF_STRIDE = 16; // offsets per lane slot (>= NDMA, multiple of 4)
 struct ASrc {
-	const char *base[2]; // planes + this lane's chunk offset
-	uint32_t off[8];     // byte offset of each row; ~0u: past the tile
+	const char *base[2];   // planes + this lane's chunk offset
+	const uint32_t *roff;  // LDS: this lane's ROFF_STRIDE row byte offsets
 };
 
 __device__ __forceinline__ uint32_t lds_addr(const void *p)
@@ -288,78 +374,89 @@ __device__ __forceinline__ void dma_a(const ASrc &s, int st, int w, const uint8_
 {
 	using C = Cfg<TYPE>;
 	const size_t ko = (size_t)st * C::RB;
+	uint32_t off[(C::NDMA + 3) / 4 * 4]; // whole 16-byte reads (the lane slot holds ROFF_STRIDE entries)
+	static_assert(C::NDMA <= ROFF_STRIDE, "row offset slot too small");
+#pragma unroll
+	for (int c = 0; c < C::NDMA; c += 4)
+		*reinterpret_cast<u32x4 *>(off + c) = *reinterpret_cast<const u32x4 *>(s.roff + c);
 #pragma unroll
 	for (int pl = 0; pl < C::NPL; pl++)
 #pragma unroll
 		for (int c = 0; c < C::NDMA; c++) {
-			const uint32_t dst = lds_addr(buf + pl * C::A_TILE + (C::RPI * (NWAVES * c + w)) * C::RB);
-			if (s.off[c] != ~0u)
-				dma16(s.base[pl] + s.off[c] + ko, __builtin_amdgcn_readfirstlane(dst));
+			const int r0 = C::RPI * (NWAVES * c + w);
+			const uint32_t dst = lds_addr(buf + pl * C::A_TILE + r0 * C::RB);
+			dma16(s.base[pl] + off[c] + ko, __builtin_amdgcn_readfirstlane(dst));
 		}
 }
 
 // Waits for this wave's global loads (the weights and the DMA of the next
-// stage) and LDS reads, then joins the workgroup.
+// stage) and LDS reads, then joins the workgroup.  Issued through the
+// builtins, not inline asm: the compiler's wait-count pass then knows that
+// every older load has landed, and inserts no wait inside the next stage
+// for the weights prefetched here (such a wait would also drain the
+// prefetch issued at that stage's start, which the pass cannot see).
 __device__ __forceinline__ void stage_barrier()
 {
-#ifdef TIE_EXP_NO_WAIT
-	asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-#else
-	asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-#endif
+	__builtin_amdgcn_s_waitcnt(0); // vmcnt(0) expcnt(0) lgkmcnt(0)
+	__builtin_amdgcn_s_barrier();
 }
 
-// One stage of MFMAs over NMT live 16-row M tiles.  Per 32-K step the two
-// B fragments are dequantised once and multiplied against every M tile;
-// the A fragments are read from LDS four tiles ahead of their MFMAs.  The
-// scheduling barrier per step keeps the compiler from hoisting a whole
-// stage of fragment reads (which would not fit two waves per SIMD).
+// One stage of MFMAs over NMT live 32-row M tiles.  The A fragments of 16-K
+// step s+1 are read from LDS and its B fragments dequantised while the
+// MFMAs of step s run (a single wave per SIMD: the MFMAs' 32-cycle issue
+// slots are where its VALU and LDS instructions go).
 template <int TYPE, int NMT>
 __device__ __forceinline__ void stage_mfma(const BRegs<TYPE> &b, int st, const uint8_t *__restrict__ A,
-					   f32x4 acc[16][2])
+					   f32x16 acc[6][2])
 {
 	using C = Cfg<TYPE>;
-	const int lane = threadIdx.x & 63, kq = lane >> 4;
-	// fragment row r = 16 mt + lane%16 (swz(r) = swz(lane%16)), chunk 4s + kq
-	const uint8_t *arow = A + (lane & 15) * C::RB;
-	const int key = C::swz(lane & 15);
+	constexpr int NA = NMT * C::NPL; // fragments per step (hi [+ lo] per tile)
+	const int lane = threadIdx.x & 63;
+	// fragment row r = 32 mt + lane%32 (swz(r) = swz(lane%32)), chunk 2s + lane/32
+	const uint8_t *arow = A + (lane & 31) * C::RB;
+	const int key = C::swz(lane & 31);
+	auto read = [&](int s, bf16x8 fr[NA]) {
+		const int slot = ((2 * s + (lane >> 5)) ^ key) * 16;
+#pragma unroll
+		for (int i = 0; i < NA; i++)
+			fr[i] = *reinterpret_cast<const bf16x8 *>(arow + (i / NMT) * C::A_TILE + (i % NMT) * 32 * C::RB +
+								  slot);
+	};
 	Fac f;
+	group_factors<TYPE>(b, st, 0, f);
+	bf16x8 fa[2][NA], fb[2][2];
+	read(0, fa[0]);
+	deq_step<TYPE>(b, f, 0, fb[0]);
 #pragma unroll
 	for (int s = 0; s < C::NSTEP; s++) {
-		if (TYPE == TIE_GGML_Q4_K ? s % 2 == 0 : s == 0)
-			group_factors<TYPE>(b, st, s / 2, f);
-		bf16x8 bf[2];
-		deq_step<TYPE>(b, f, s, kq, bf);
-		const int slot = ((4 * s + kq) ^ key) * 16;
+		const int cur = s & 1;
 #pragma unroll
-		for (int mt = 0; mt < NMT; mt++) {
-#pragma unroll
-			for (int pl = 0; pl < C::NPL; pl++) {
-				const bf16x8 av =
-					*reinterpret_cast<const bf16x8 *>(arow + pl * C::A_TILE + mt * 16 * C::RB + slot);
-#ifdef TIE_EXP_NO_MFMA
-				asm volatile("" ::"v"(av), "v"(bf[0]), "v"(bf[1]));
-#else
-				acc[mt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bf[0], acc[mt][0], 0, 0, 0);
-				acc[mt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bf[1], acc[mt][1], 0, 0, 0);
-#endif
-			}
+		for (int i = 0; i < NA; i++) {
+			const int mt = i % NMT;
+			acc[mt][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[cur][i], fb[cur][0], acc[mt][0], 0, 0, 0);
+			acc[mt][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[cur][i], fb[cur][1], acc[mt][1], 0, 0, 0);
+		}
+		if (s + 1 < C::NSTEP) {
+			read(s + 1, fa[cur ^ 1]);
+			if (TYPE == TIE_GGML_Q4_K && (s + 1) % 4 == 0)
+				group_factors<TYPE>(b, st, (s + 1) / 4, f);
+			deq_step<TYPE>(b, f, s + 1, fb[cur ^ 1]);
 		}
 		__builtin_amdgcn_sched_barrier(0);
 	}
 }
 
 // ------------------------------------------------------------------ kernel
-// One work tile with NMT = 4*NQ live 16-row M tiles (nrows <= 64*NQ).
-template <int TYPE, bool DOWN, int NQ>
-__device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, int e, int pbase, int nrows, int slab)
+// One work tile with NMT live 32-row M tiles (nrows <= 32 NMT).
+template <int TYPE, bool DOWN, int NMT>
+__device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_t *roff, int e, int pbase, int nrows,
+					 int slab)
 {
 	using C = Cfg<TYPE>;
-	constexpr int NMT = 4 * NQ;
 	const int nk = a.in / C::KST;
 	const int t = threadIdx.x;
 	const int w = __builtin_amdgcn_readfirstlane(t >> 6);
-	const int lane = t & 63, kq = lane >> 4;
+	const int lane = t & 63, h = lane >> 5;
 
 	ASrc as;
 	{
@@ -367,18 +464,21 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, int e, 
 		const int chunk = slot ^ C::swz(C::RPI * w + rsub);
 		as.base[0] = (const char *)a.a16 + 16 * chunk;
 		as.base[1] = (const char *)a.a16lo + 16 * chunk;
-#pragma unroll
-		for (int c = 0; c < 8; c++) {
-			const int r = C::RPI * (NWAVES * c + w) + rsub;
-			const int row = c < C::NDMA && r < nrows ? (DOWN ? pbase + r : a.pairs[pbase + r] / a.k) : -1;
-			as.off[c] = row < 0 ? ~0u : (uint32_t)((size_t)row * a.in * 2);
+		// row r = RPI (NWAVES c + w') + rsub' is entry c of lane slot RPI w' + rsub'
+		as.roff = roff + (C::RPI * w + rsub) * ROFF_STRIDE;
+		if (t < MT) {
+			const int r = t < nrows ? t : 0;
+			const int row = DOWN ? pbase + r : a.pairs[pbase + r] / a.k;
+			const int c = t / (C::RPI * NWAVES), ls = t % (C::RPI * NWAVES);
+			roff[ls * ROFF_STRIDE + c] = (uint32_t)((size_t)row * a.in * 2);
 		}
+		__syncthreads();
 	}
 	BSrc bs;
 #pragma unroll
 	for (int j = 0; j < 2; j++) {
 		const int mat = DOWN ? 0 : j;
-		const int row = DOWN ? slab * DN_COLS + 32 * w + 16 * j + (lane & 15) : slab * GU_COLS + 16 * w + (lane & 15);
+		const int row = DOWN ? slab * DN_COLS + 64 * w + 32 * j + (lane & 31) : slab * GU_COLS + 32 * w + (lane & 31);
 		const uint8_t *base = a.w[mat] + (size_t)e * a.expert_bytes[mat];
 		if constexpr (TYPE == TIE_GGML_BF16)
 			bs.p[j] = base + (size_t)row * a.in * 2;
@@ -388,68 +488,108 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, int e, 
 		bs.dofs[j] = Q6K_CHUNKS * 1024 + 2 * (row & 63) - 16 * (row & 63);
 	}
 
-	f32x4 acc[16][2];
+	f32x16 acc[6][2];
 #pragma unroll
 	for (int mt = 0; mt < NMT; mt++)
 #pragma unroll
 		for (int j = 0; j < 2; j++)
-			acc[mt][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+			for (int i = 0; i < 16; i++)
+				acc[mt][j][i] = 0.0f;
+
+	// the lane's two weight rows in the LDS panel buffer (quantised types)
+	int bp[2], bi[2];
+#pragma unroll
+	for (int j = 0; j < 2; j++) {
+		const int r = DOWN ? 64 * w + 32 * j + (lane & 31) : 32 * w + (lane & 31); // row within the matrix's tile
+		bp[j] = DOWN ? r >> 6 : 2 * j + (r >> 6);
+		bi[j] = r & 63;
+	}
+	uint8_t *Bs = As + C::LDS_A;
 
 	BRegs<TYPE> b0, b1;
-	load_b<TYPE>(bs, 0, kq, b0);
+	if constexpr (C::B_LDS)
+		dma_b<TYPE, DOWN>(a, e, slab, 0, w, Bs);
+	else
+		load_b<TYPE>(bs, 0, h, b0);
 	dma_a<TYPE>(as, 0, w, As);
 	stage_barrier();
 
-	// stage st: the weights and activations of st+1 are fetched (into
-	// registers and the other LDS buffer), then the MFMAs of st run
+	// stage st: the weights and activations of st+1 are fetched (into the
+	// other LDS buffers, or registers for BF16 weights), then the MFMAs of
+	// st run
 	auto body = [&](int st, BRegs<TYPE> &cur, BRegs<TYPE> &nxt) {
 		if (st + 1 < nk) {
-#ifndef TIE_EXP_NO_BLOAD
-			load_b<TYPE>(bs, st + 1, kq, nxt);
-#endif
-#ifndef TIE_EXP_NO_DMA
+			if constexpr (C::B_LDS)
+				dma_b<TYPE, DOWN>(a, e, slab, st + 1, w, Bs + ((st + 1) & 1) * C::BBUF);
+			else
+				load_b<TYPE>(bs, st + 1, h, nxt);
 			dma_a<TYPE>(as, st + 1, w, As + ((st + 1) & 1) * C::ABUF);
-#endif
 		}
+		if constexpr (C::B_LDS)
+			lds_b<TYPE>(Bs + (st & 1) * C::BBUF, bp, bi, st, h, cur);
 		stage_mfma<TYPE, NMT>(cur, st, As + (st & 1) * C::ABUF, acc);
 		stage_barrier();
 	};
-	for (int st = 0; st < nk; st += 2) {
-		body(st, b0, b1);
-		if (st + 1 < nk)
-			body(st + 1, b1, b0);
+	if constexpr (C::B_LDS) {
+		for (int st = 0; st < nk; st++)
+			body(st, b0, b0);
+	} else {
+		for (int st = 0; st < nk; st += 2) {
+			body(st, b0, b1);
+			if (st + 1 < nk)
+				body(st + 1, b1, b0);
+		}
 	}
 
-	// D layout of v_mfma_f32_16x16x32: lane l, register i holds
-	// row 4*(l/16) + i, column l%16.
+	// gate/up: TIE's SiLU table (32 KiB) into the now idle A buffers, so the
+	// epilogue's table lookups are LDS reads
+	const float *silu = a.silu;
+	if constexpr (!DOWN) {
+		static_assert(SILU_N * 4 <= 2 * C::ABUF, "SiLU table must fit the A buffers");
+#pragma unroll
+		for (int c = 0; c < SILU_N * 4 / 1024 / NWAVES; c++) {
+			const int off = 1024 * (NWAVES * c + w);
+			dma16(reinterpret_cast<const uint8_t *>(a.silu) + off + 16 * lane,
+			      __builtin_amdgcn_readfirstlane(lds_addr(As + off)));
+		}
+		stage_barrier();
+		silu = reinterpret_cast<const float *>(As);
+	}
+	// D layout of v_mfma_f32_32x32x16: lane l, register i holds
+	// row 8*(i/4) + 4*(l/32) + i%4, column l%32.
 #pragma unroll
 	for (int mt = 0; mt < NMT; mt++) {
 #pragma unroll
-		for (int i = 0; i < 4; i++) {
-			const int mrow = 16 * mt + 4 * kq + i;
+		for (int i = 0; i < 16; i++) {
+			const int mrow = 32 * mt + 8 * (i >> 2) + 4 * h + (i & 3);
 			if (mrow >= nrows)
 				continue;
 			const int p = pbase + mrow;
 			if (!DOWN) {
-				const int col = slab * GU_COLS + 16 * w + (lane & 15);
-				const float hv = tie_swiglu(acc[mt][0][i], acc[mt][1][i], a.silu);
+				const int col = slab * GU_COLS + 32 * w + (lane & 31);
+				const float hv = tie_swiglu(acc[mt][0][i], acc[mt][1][i], silu);
 				const uint16_t hi = bf16_bits(hv);
 				a.h16[(size_t)p * a.rows + col] = hi;
 				if (C::SPLIT)
 					a.h16lo[(size_t)p * a.rows + col] = bf16_bits(hv - bf16_bits_to_float(hi));
 			} else {
-				float *yr = a.y + (size_t)a.pairs[p] * a.rows + slab * DN_COLS + 32 * w + (lane & 15);
+				float *yr = a.y + (size_t)a.pairs[p] * a.rows + slab * DN_COLS + 64 * w + (lane & 31);
 				yr[0] = acc[mt][0][i];
-				yr[16] = acc[mt][1][i];
+				yr[32] = acc[mt][1][i];
 			}
 		}
+		// one M tile at a time: only its accumulators move to VGPRs
+		__builtin_amdgcn_sched_barrier(0);
 	}
 }
 
 template <int TYPE, bool DOWN>
-__global__ __launch_bounds__(MF_THREADS) void mfma_experts_kernel(MfmaArgs a)
+__global__ __launch_bounds__(MF_THREADS) __attribute__((amdgpu_waves_per_eu(1, 1))) void
+mfma_experts_kernel(MfmaArgs a)
 {
-	extern __shared__ __attribute__((aligned(16))) uint8_t As[]; // [2][ABUF]
+	extern __shared__ __attribute__((aligned(16))) uint8_t As[]; // A [2][ABUF] | B [2][BBUF] | row offsets
+	uint32_t *roff = reinterpret_cast<uint32_t *>(As + Cfg<TYPE>::LDS_A + Cfg<TYPE>::LDS_B);
 
 	// XCD-aware tile order.  Consecutive workgroup ids are spread round-robin
 	// over the 8 XCDs, each with its own L2.  The id is remapped so that each
@@ -465,21 +605,30 @@ __global__ __launch_bounds__(MF_THREADS) void mfma_experts_kernel(MfmaArgs a)
 		return;
 	const int tile = v / nslab;
 	const int slab = v % nslab;
+	// an expert's pairs are split evenly over ceil(count / MT) tiles
 	const int e = a.tile_e[tile], m0 = a.tile_m0[tile];
+	const int cnt = a.offsets[e + 1] - a.offsets[e];
+	const int ntl = (cnt + MT - 1) / MT;
 	const int pbase = a.offsets[e] + m0;
-	const int nrows = min(MT, a.offsets[e + 1] - pbase);
-	switch ((nrows + 63) >> 6) {
+	const int nrows = min((cnt + ntl - 1) / ntl, cnt - m0);
+	switch ((nrows + 31) >> 5) {
 	case 1:
-		run_tile<TYPE, DOWN, 1>(a, As, e, pbase, nrows, slab);
+		run_tile<TYPE, DOWN, 1>(a, As, roff, e, pbase, nrows, slab);
 		break;
 	case 2:
-		run_tile<TYPE, DOWN, 2>(a, As, e, pbase, nrows, slab);
+		run_tile<TYPE, DOWN, 2>(a, As, roff, e, pbase, nrows, slab);
 		break;
 	case 3:
-		run_tile<TYPE, DOWN, 3>(a, As, e, pbase, nrows, slab);
+		run_tile<TYPE, DOWN, 3>(a, As, roff, e, pbase, nrows, slab);
+		break;
+	case 4:
+		run_tile<TYPE, DOWN, 4>(a, As, roff, e, pbase, nrows, slab);
+		break;
+	case 5:
+		run_tile<TYPE, DOWN, 5>(a, As, roff, e, pbase, nrows, slab);
 		break;
 	default:
-		run_tile<TYPE, DOWN, 4>(a, As, e, pbase, nrows, slab);
+		run_tile<TYPE, DOWN, 6>(a, As, roff, e, pbase, nrows, slab);
 	}
 }
 
@@ -508,7 +657,8 @@ template <int TYPE, bool DOWN>
 static hipError_t launch_type(const MfmaArgs &a, dim3 grid, hipStream_t s)
 {
 	// the double-buffered A tile exceeds the default 64 KiB of dynamic LDS
-	constexpr size_t lds = 2 * (size_t)Cfg<TYPE>::ABUF;
+	constexpr size_t lds = (size_t)Cfg<TYPE>::LDS_A + Cfg<TYPE>::LDS_B + 4 * (size_t)(Cfg<TYPE>::RPI * NWAVES * ROFF_STRIDE);
+	static_assert(lds <= 160 * 1024, "LDS budget");
 	static bool attr = false;
 	if (!attr) {
 		const hipError_t err = hipFuncSetAttribute((const void *)mfma_experts_kernel<TYPE, DOWN>,
@@ -604,3 +754,4 @@ hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, con
 }
 
 } // namespace tie
+
