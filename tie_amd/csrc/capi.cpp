@@ -195,11 +195,10 @@ static int ensure_workspace(int T, int k, int d, int F, int E)
 		off += align256(bytes);
 		return o;
 	};
-	const size_t o_idx = take(P * 4), o_w = take(P * 4), o_cnt = take(EE * 4), o_off = take((EE + 1) * 4),
-		     o_pairs = take(P * 4), o_act = take((EE + 1) * 4), o_sync = take((Tcap / 4 + 64) * 4),
-		     o_logits = take(Tcap * EE * 4), o_h = take(3 * P * FF * 4), o_cnt2 = take(P * (FF / 64) * 4), o_hb = take(P * FF * 2),
-		     o_y = take(P * DD * 4), o_xb = take(Tcap * DD * 2), o_hlo = take(P * FF * 2),
-		     o_xlo = take(Tcap * DD * 2);
+	const size_t o_idx = take(P * 4), o_w = take(P * 4), o_off = take((EE + 1) * 4), o_pairs = take(P * 4),
+		     o_act = take((EE + 1) * 4), o_logits = take(Tcap * EE * 4), o_h = take(2 * P * FF * 4),
+		     o_hb = take(P * FF * 2), o_y = take(P * DD * 4), o_xb = take(Tcap * DD * 2),
+		     o_hlo = take(P * FF * 2), o_xlo = take(Tcap * DD * 2);
 	const size_t max_tiles = (size_t)mfma_max_tiles((int)P, (int)EE);
 	const size_t o_te = take(max_tiles * 4), o_tm = take(max_tiles * 4), o_nt = take(4);
 	void *mem = nullptr;
@@ -215,14 +214,11 @@ static int ensure_workspace(int T, int k, int d, int F, int E)
 	w.alloc = mem;
 	w.topk_idx = (int32_t *)(b + o_idx);
 	w.topk_w = (float *)(b + o_w);
-	w.counts = (int32_t *)(b + o_cnt);
 	w.offsets = (int32_t *)(b + o_off);
 	w.pairs = (int32_t *)(b + o_pairs);
 	w.active = (int32_t *)(b + o_act);
-	w.sync = (uint32_t *)(b + o_sync);
 	w.logits = (float *)(b + o_logits);
 	w.h = (float *)(b + o_h);
-	w.tile_cnt = (uint32_t *)(b + o_cnt2);
 	w.hb = (uint16_t *)(b + o_hb);
 	w.y = (float *)(b + o_y);
 	w.xb = (uint16_t *)(b + o_xb);
@@ -235,10 +231,6 @@ static int ensure_workspace(int T, int k, int d, int F, int E)
 	w.cap_F = FF;
 	w.cap_d = DD;
 	w.cap_E = EE;
-	// completion counters start at zero and are reset by the kernels
-	HIP_TRY(hipMemsetAsync(w.sync, 0, (Tcap / 4 + 64) * 4, g.stream));
-	HIP_TRY(hipMemsetAsync(w.tile_cnt, 0, P * (FF / 64) * 4, g.stream));
-	HIP_TRY(hipStreamSynchronize(g.stream));
 	return TIE_HIP_OK;
 }
 
@@ -365,16 +357,17 @@ static int forward(tie_hip_layer *layer, const float *x, int T, int k, float *ou
 	if (rc)
 		return rc;
 	Workspace &ws = g.ws;
-	prof_begin("router", s);
-	HIP_TRY(launch_router(L, x, T, k, ws.logits, ws.topk_idx, ws.topk_w, ws.sync, s));
-	prof_end(s);
-	prof_begin("dispatch", s);
-	HIP_TRY(launch_dispatch(L, T, k, ws.topk_idx, ws, s));
-	prof_end(s);
-	if (mfma)
+	if (mfma) {
+		prof_begin("router", s);
+		HIP_TRY(launch_router(L, x, T, k, ws.logits, ws.topk_idx, ws.topk_w, s));
+		prof_end(s);
+		prof_begin("dispatch", s);
+		HIP_TRY(launch_dispatch(L, T, k, ws.topk_idx, ws, s));
+		prof_end(s);
 		HIP_TRY(launch_mfma_experts(L, x, T, k, g.silu, ws, s));
-	else
-		HIP_TRY(launch_exact_experts(L, x, T, k, g.silu, ws, s));
+	} else {
+		HIP_TRY(launch_exact_block(L, x, T, k, g.silu, ws, s));
+	}
 	prof_begin("combine", s);
 	HIP_TRY(launch_combine(T, L.d, k, ws.topk_w, ws.topk_idx, ws.y, out, s));
 	prof_end(s);

@@ -62,14 +62,11 @@ struct Layer {
 struct Workspace {
 	int32_t *topk_idx = nullptr;  // [T][k]
 	float *topk_w = nullptr;      // [T][k]
-	int32_t *counts = nullptr;    // [E]      tokens per expert
 	int32_t *offsets = nullptr;   // [E+1]    start of each expert's pair list
 	int32_t *pairs = nullptr;     // [T*k]    pair ids t*k+j grouped by expert
 	int32_t *active = nullptr;    // [E+1]    active experts; active[E] = count
-	uint32_t *sync = nullptr;     // [T/4+64] grid-completion counters (self-resetting)
 	float *logits = nullptr;      // [T][E]   router logits
-	float *h = nullptr;           // [3][T*k][F] SwiGLU output, gate sums, up sums (exact path)
-	uint32_t *tile_cnt = nullptr; // [T*k][F/64] gate/up completion counters (self-resetting)
+	float *h = nullptr;           // [2][T*k][F] gate and up row sums (exact path)
 	uint16_t *hb = nullptr;       // [T*k][F] SwiGLU activations (bf16 hi/lo, MFMA path)
 	float *y = nullptr;           // [T*k][d] expert outputs
 	uint16_t *hlo = nullptr;      // [T*k][F] SwiGLU activations, bf16 remainder (MFMA path, BF16 weights)
@@ -83,12 +80,16 @@ struct Workspace {
 };
 
 // ---------------------------------------------------------------- launchers
+hipError_t launch_router_logits(const Layer &L, const float *x, int T, float *logits, hipStream_t s);
+hipError_t launch_router_select(const Layer &L, int T, int k, const float *logits, int32_t *topk_idx, float *topk_w,
+				hipStream_t s);
 hipError_t launch_router(const Layer &L, const float *x, int T, int k, float *logits, int32_t *topk_idx,
-			 float *topk_w, uint32_t *counter, hipStream_t s);
+			 float *topk_w, hipStream_t s);
 hipError_t launch_router_transpose(const Layer &L, hipStream_t s);
 hipError_t launch_dispatch(const Layer &L, int T, int k, const int32_t *topk_idx, Workspace &ws, hipStream_t s);
-hipError_t launch_exact_experts(const Layer &L, const float *x, int T, int k, const float *silu, Workspace &ws,
-				hipStream_t s);
+hipError_t launch_route_group(const Layer &L, int T, int k, const float *logits, Workspace &ws, hipStream_t s);
+hipError_t launch_exact_block(const Layer &L, const float *x, int T, int k, const float *silu, Workspace &ws,
+			      hipStream_t s);
 hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, const float *silu, Workspace &ws,
 			       hipStream_t s);
 int mfma_max_tiles(int npairs, int E);

@@ -15,110 +15,79 @@
 // in slot order j = 0..k-1 with one FMA per term, as model_qwen3.c:459-467
 // does (acc starts at +0.0f; slots with no expert contribute nothing).
 #include "common.h"
+#include "route.h"
 
 namespace tie {
 
 constexpr int DSP_THREADS = 1024;
 
-// Exclusive prefix sum over the workgroup (DSP_THREADS threads, one value
-// each); also returns the total.
-__device__ __forceinline__ int block_exclusive_scan(int v, int *wsum, int &total)
-{
-	const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-	constexpr int NW = DSP_THREADS / 64;
-	int x = v;
-#pragma unroll
-	for (int off = 1; off < 64; off <<= 1) {
-		const int y = __shfl_up(x, off);
-		if (lane >= off)
-			x += y;
-	}
-	if (lane == 63)
-		wsum[wave] = x;
-	__syncthreads();
-	if (wave == 0) {
-		int s = lane < NW ? wsum[lane] : 0;
-#pragma unroll
-		for (int off = 1; off < NW; off <<= 1) {
-			const int y = __shfl_up(s, off);
-			if (lane >= off)
-				s += y;
-		}
-		if (lane < NW)
-			wsum[lane] = s;
-	}
-	__syncthreads();
-	const int prefix = wave > 0 ? wsum[wave - 1] : 0;
-	total = wsum[NW - 1];
-	__syncthreads();
-	return prefix + x - v;
-}
-
-// One workgroup: LDS histogram, parallel scans over the experts, LDS-atomic
-// placement of the pairs.  Also writes the MFMA work list (one entry per
-// MFMA_MT pairs of each active expert).
+// One workgroup groups all pairs (group_pairs) and writes the MFMA work
+// list.
 __global__ __launch_bounds__(DSP_THREADS) void dispatch_kernel(const int32_t *__restrict__ topk_idx, int npairs,
-							       int E, int32_t *__restrict__ counts,
-							       int32_t *__restrict__ offsets,
+							       int E, int32_t *__restrict__ offsets,
 							       int32_t *__restrict__ pairs,
 							       int32_t *__restrict__ active,
 							       int32_t *__restrict__ tile_e,
 							       int32_t *__restrict__ tile_m0,
 							       int32_t *__restrict__ ntiles)
 {
-	extern __shared__ int32_t sm[];
-	int32_t *cnt = sm;          // [E]
-	int32_t *cur = sm + E;      // [E] running cursor
+	__shared__ int32_t cnt[MAX_E], cur[MAX_E];
 	__shared__ int wsum[DSP_THREADS / 64];
-	const int tid = threadIdx.x;
-	for (int e = tid; e < E; e += DSP_THREADS)
-		cnt[e] = 0;
-	__syncthreads();
-	for (int p = tid; p < npairs; p += DSP_THREADS) {
-		const int e = topk_idx[p];
-		if (e >= 0 && e < E)
-			atomicAdd(&cnt[e], 1);
-	}
-	__syncthreads();
-	// E <= MAX_E == DSP_THREADS: one expert per thread
-	const int e = tid;
-	const int c = e < E ? cnt[e] : 0;
-	int total, nact, ntot;
-	const int off = block_exclusive_scan(c, wsum, total);
-	const int aidx = block_exclusive_scan(c > 0 ? 1 : 0, wsum, nact);
-	const int nt = (c + MFMA_MT - 1) / MFMA_MT;
-	const int toff = block_exclusive_scan(nt, wsum, ntot);
-	if (e < E) {
-		offsets[e] = off;
-		cur[e] = off;
-		counts[e] = c;
-		if (c > 0)
-			active[aidx] = e;
-		// the expert's pairs split evenly over its nt tiles
-		const int rpt = nt > 0 ? (c + nt - 1) / nt : 0;
-		for (int t = 0; t < nt; t++) {
-			tile_e[toff + t] = e;
-			tile_m0[toff + t] = t * rpt;
-		}
-	}
-	if (tid == 0) {
-		offsets[E] = total;
-		active[E] = nact;
-		ntiles[0] = ntot;
-	}
-	__syncthreads();
-	for (int p = tid; p < npairs; p += DSP_THREADS) {
-		const int ex = topk_idx[p];
-		if (ex >= 0 && ex < E)
-			pairs[atomicAdd(&cur[ex], 1)] = p;
-	}
+	group_pairs<DSP_THREADS>(topk_idx, npairs, E, cnt, cur, wsum, offsets, pairs, active, tile_e, tile_m0, ntiles);
 }
 
 hipError_t launch_dispatch(const Layer &L, int T, int k, const int32_t *topk_idx, Workspace &ws, hipStream_t s)
 {
-	const size_t lds = sizeof(int32_t) * 2 * (size_t)L.E;
-	hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(DSP_THREADS), lds, s, topk_idx, T * k, L.E, ws.counts,
-			   ws.offsets, ws.pairs, ws.active, ws.tile_e, ws.tile_m0, ws.ntiles);
+	hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(DSP_THREADS), 0, s, topk_idx, T * k, L.E, ws.offsets,
+			   ws.pairs, ws.active, ws.tile_e, ws.tile_m0, ws.ntiles);
+	return hipGetLastError();
+}
+
+// Routing and grouping of a small batch (T*k <= RG_MAX_PAIRS) in one
+// workgroup: top-k + softmax of every token from its logits (8 lanes per
+// token when E <= 128, else a wave per token), then group_pairs.  Saves
+// the separate selection launch.
+constexpr int RG_MAX_PAIRS = 4096;
+__global__ __launch_bounds__(DSP_THREADS) void route_group_kernel(const float *__restrict__ logits, int T, int E,
+								  int k, int32_t *__restrict__ topk_idx,
+								  float *__restrict__ topk_w,
+								  int32_t *__restrict__ offsets,
+								  int32_t *__restrict__ pairs,
+								  int32_t *__restrict__ active)
+{
+	__shared__ int32_t cnt[MAX_E], cur[MAX_E];
+	__shared__ int wsum[DSP_THREADS / 64];
+	__shared__ float sel[(DSP_THREADS / 8) * MAX_K];
+	__shared__ uint64_t etab[32];
+	__shared__ int32_t sidx[RG_MAX_PAIRS];
+	const int tid = threadIdx.x;
+	if (tid < 32) {
+		const uint64_t tab[32] = TIE_EXP2_TABLE;
+		etab[tid] = tab[tid];
+	}
+	__syncthreads();
+	if (E <= 128) {
+		for (int t0 = 0; t0 < T; t0 += DSP_THREADS / 8) {
+			const int t = t0 + tid / 8;
+			if (t < T)
+				topk_softmax_group8(logits + (size_t)t * E, E, k, sel + (tid / 8) * MAX_K, etab,
+						    sidx + t * k, topk_w + (size_t)t * k);
+		}
+	} else {
+		for (int t = tid >> 6; t < T; t += DSP_THREADS / 64)
+			topk_softmax_wave(logits + (size_t)t * E, E, k, etab, sidx + t * k, topk_w + (size_t)t * k);
+	}
+	__syncthreads();
+	const int npairs = T * k;
+	for (int p = tid; p < npairs; p += DSP_THREADS)
+		topk_idx[p] = sidx[p];
+	group_pairs<DSP_THREADS>(sidx, npairs, E, cnt, cur, wsum, offsets, pairs, active, nullptr, nullptr, nullptr);
+}
+
+hipError_t launch_route_group(const Layer &L, int T, int k, const float *logits, Workspace &ws, hipStream_t s)
+{
+	hipLaunchKernelGGL(route_group_kernel, dim3(1), dim3(DSP_THREADS), 0, s, logits, T, L.E, k, ws.topk_idx,
+			   ws.topk_w, ws.offsets, ws.pairs, ws.active);
 	return hipGetLastError();
 }
 

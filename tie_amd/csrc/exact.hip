@@ -10,38 +10,83 @@
 // (:188-226).  The kernels here keep every rounding step and the order of
 // every sum, so their outputs equal TIE's exactly.
 //
-// Work decomposition (pairs = (token, slot) grouped by expert by
-// dispatch.hip):
-//   exact_q_rows    one workgroup per (64-row tile, active expert, matrix);
-//                   wave w owns block column w, lane i owns row i of the
-//                   tile.  The lane's super-block (144 or 210 bytes) is
-//                   read from the panel layout with coalesced 16-byte loads
-//                   and kept in VGPRs for every token routed to the expert;
-//                   the token's input vector is staged in LDS and read as
-//                   wave-uniform broadcasts; per-block dots meet in LDS and
-//                   lane i of wave 0 adds them in block order.
-//   exact_bf16_rows two threads per row, each owning four of the row's
-//                   eight lane accumulators.
-// Gate and up write their row sums; the down kernel applies TIE's table
-// SwiGLU while staging its input vector, so no separate activation pass.
+// Work decomposition ((token, slot) pairs grouped by expert):
+//   exact_gu_kernel    one workgroup per (64-row panel, active expert,
+//                      matrix); wave w owns super-block columns w, w+8, ..;
+//                      lane i owns row i.  The lane's super-block is read
+//                      once per group of up to 16 pairs with coalesced
+//                      16-byte panel loads and dequantised once per 8
+//                      weights for up to 4 pairs at a time; the input row
+//                      of each pair comes in through scalar loads (one
+//                      address per wave), so it reaches the FMAs as SGPR
+//                      operands.  Per-block dots meet in LDS and are added
+//                      in block order.  Writes the gate and up row sums.
+//                      For T <= 8 (E <= 128) every workgroup first selects
+//                      the experts of all tokens itself (top-k, softmax,
+//                      grouping): no separate routing launch.
+//   exact_down_kernel  one workgroup per (64-row panel of d, active
+//                      expert).  The prologue forms h = silu_tab(gate) * up
+//                      (swiglu_activation_f32_f32_avx2) for its pairs in
+//                      LDS; the blocks then read h as LDS broadcasts.
+//   BF16 weights       two threads per row, each owning four of the row's
+//                      eight lane accumulators.
+// No kernel waits on another workgroup: the only ordering is the launch
+// order on the stream.
 #include "common.h"
+#include "route.h"
 
 namespace tie {
 
-// Input vectors (x for gate/up, the SwiGLU output h for down) are read
-// through the constant address space: every lane of a wave reads the same
-// address, so the loads become scalar (s_load) and the values reach the
-// FMAs as SGPR operands -- no LDS staging, no broadcast traffic.
+// Input rows of the gate/up GEMVs are read through the constant address
+// space: every lane of a wave reads the same address, so the loads become
+// scalar (s_load) and the values reach the FMAs as SGPR operands.
 typedef const float __attribute__((address_space(4))) cfloat;
+// h rows of the down GEMV are LDS broadcasts.
+typedef const float __attribute__((address_space(3))) lfloat;
 
 // The launders below are empty asm statements that make a value opaque to
-// the compiler at one point of the instruction stream.  Without them the
-// scheduler hoists all 256 dequantised weights or all 256 input values of
-// a super-block to the top of the dot product and runs out of registers.
+// the compiler at one point of the instruction stream.  Volatile asm keeps
+// its order, so a step fence (every accumulator of every pair made opaque)
+// followed by the launders of a step's input pointers and quant words
+// pins the step between the FMAs of the step before and after it: without
+// that the scheduler hoists every input value and dequantised weight of a
+// super-block to the top and runs out of registers.
 __device__ __forceinline__ void launder(cfloat *&p)
 {
 	asm volatile("" : "+s"(p));
 }
+__device__ __forceinline__ void launder(lfloat *&p)
+{
+	asm volatile("" : "+v"(p));
+}
+template <int PC> __device__ __forceinline__ void step_fence(float (&a0)[PC][8], float (&a1)[PC][8])
+{
+#pragma unroll
+	for (int p = 0; p < PC; p++) {
+		asm volatile("" : "+v"(a0[p][0]), "+v"(a0[p][1]), "+v"(a0[p][2]), "+v"(a0[p][3]), "+v"(a0[p][4]),
+				  "+v"(a0[p][5]), "+v"(a0[p][6]), "+v"(a0[p][7]));
+		asm volatile("" : "+v"(a1[p][0]), "+v"(a1[p][1]), "+v"(a1[p][2]), "+v"(a1[p][3]), "+v"(a1[p][4]),
+				  "+v"(a1[p][5]), "+v"(a1[p][6]), "+v"(a1[p][7]));
+	}
+}
+
+// Tuning knobs (compile-time): the most pairs one dot product serves at a
+// time, and an optional occupancy target for the quantised kernels.
+#ifndef TIE_EXACT_PCMAX
+#define TIE_EXACT_PCMAX 4
+#endif
+#ifdef TIE_EXACT_WPE
+#define EXACT_OCC __attribute__((amdgpu_waves_per_eu(TIE_EXACT_WPE)))
+#else
+#define EXACT_OCC
+#endif
+
+constexpr int GU_WAVES = 8;       // waves of a gate/up workgroup
+constexpr int GU_THREADS = 64 * GU_WAVES;
+constexpr int PG_MAX = 16;        // pairs per LDS group
+constexpr int PART_FLOATS = 16384; // LDS budget of the per-block partial dots (64 KiB)
+constexpr int INLINE_T = 8;       // routing in the gate/up prologue up to this T (E <= 128)
+constexpr int INLINE_E = 128;
 
 // ------------------------------------------------------------------ blocks
 struct Q4KBlock {
@@ -79,9 +124,12 @@ __device__ __forceinline__ float ubyte(uint32_t w, int i)
 	return (float)((w >> (8 * i)) & 0xffu);
 }
 
-// dot_product_f32_q4k_avx2 (math_avx2.c:535-604) for the lane's block.
-template <typename XP>
-__device__ __forceinline__ float block_dot(const Q4KBlock &B, XP *x)
+// dot_product_f32_q4k_avx2 (math_avx2.c:535-604) of the lane's block with
+// PC input rows at once.  Each weight w = fma(q, d*sc, -(dmin*m)) is formed
+// once and used by the PC pairs; every pair keeps its own 16 accumulators
+// and sees exactly TIE's sequence of FMAs.
+template <int PC, typename XP>
+__device__ __forceinline__ void block_dots(const Q4KBlock &B, XP *const xs[PC], float out[PC])
 {
 	const uint32_t w0 = B.c[0].x;
 	const float d = half_bits_to_float(w0 & 0xffffu);
@@ -102,52 +150,69 @@ __device__ __forceinline__ float block_dot(const Q4KBlock &B, XP *x)
 		D[j] = d * (float)sc;
 		nM[j] = -(dmin * (float)m);
 	}
-	float a0[8], a1[8];
+	float a0[PC][8], a1[PC][8];
 #pragma unroll
-	for (int l = 0; l < 8; l++)
-		a0[l] = a1[l] = 0.0f;
+	for (int p = 0; p < PC; p++)
+#pragma unroll
+		for (int l = 0; l < 8; l++)
+			a0[p][l] = a1[p][l] = 0.0f;
 #pragma unroll
 	for (int g = 0; g < 4; g++) {
 		const float D1 = D[2 * g], M1 = nM[2 * g], D2 = D[2 * g + 1], M2 = nM[2 * g + 1];
 #pragma unroll
 		for (int o = 0; o < 2; o++) {
 			uint4 q = B.c[1 + 2 * g + o];
-			asm volatile("" : "+v"(q.x), "+v"(q.y), "+v"(q.z), "+v"(q.w)::"memory");
-			XP *xl = x + 64 * g + 16 * o;
-			launder(xl);
-			XP *xh = xl + 32;
 #pragma unroll
 			for (int h = 0; h < 4; h++) {
-				const uint32_t w = word(q, h);
+				step_fence<PC>(a0, a1);
+				uint32_t w = word(q, h);
+				asm volatile("" : "+v"(w));
 				uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
-				asm volatile("" : "+v"(lo), "+v"(hi)); // keeps one mask per 4 bytes + v_cvt_f32_ubyteN
+				float wl[4], wh[4];
 #pragma unroll
 				for (int i = 0; i < 4; i++) {
-					const int m = 4 * h + i;
-					float &A = (m < 8) ? a0[m & 7] : a1[m & 7];
-					A = __builtin_fmaf(xl[m], __builtin_fmaf(ubyte(lo, i), D1, M1), A);
-					A = __builtin_fmaf(xh[m], __builtin_fmaf(ubyte(hi, i), D2, M2), A);
+					wl[i] = __builtin_fmaf(ubyte(lo, i), D1, M1);
+					wh[i] = __builtin_fmaf(ubyte(hi, i), D2, M2);
+				}
+#pragma unroll
+				for (int p = 0; p < PC; p++) {
+					XP *xl = xs[p] + 64 * g + 16 * o + 4 * h;
+					launder(xl);
+#pragma unroll
+					for (int i = 0; i < 4; i++) {
+						const int m = 4 * h + i;
+						float &A = (m < 8) ? a0[p][m & 7] : a1[p][m & 7];
+						A = __builtin_fmaf(xl[i], wl[i], A);
+						A = __builtin_fmaf(xl[32 + i], wh[i], A);
+					}
 				}
 			}
 		}
 	}
-	float v[8];
 #pragma unroll
-	for (int l = 0; l < 8; l++)
-		v[l] = a0[l] + a1[l];
-	return hsum8(v);
+	for (int p = 0; p < PC; p++) {
+		float v[8];
+#pragma unroll
+		for (int l = 0; l < 8; l++)
+			v[l] = a0[p][l] + a1[p][l];
+		out[p] = hsum8(v);
+	}
 }
 
-// dot_product_f32_q6k_avx2 (math_avx2.c:411-495) for the lane's block.
-// Panel chunks: 0-7 ql[0..127], 8-11 qh[0..63], 12 the int8 scales.
-template <typename XP>
-__device__ __forceinline__ float block_dot(const Q6KBlock &B, XP *x)
+// dot_product_f32_q6k_avx2 (math_avx2.c:411-495) of the lane's block with
+// PC input rows.  Panel chunks: 0-7 ql[0..127], 8-11 qh[0..63], 12 the
+// int8 scales.  q - 32 is formed once per weight; per pair TIE's
+// fma(d*sc, (q - 32) * x, acc) follows, the product rounded on its own.
+template <int PC, typename XP>
+__device__ __forceinline__ void block_dots(const Q6KBlock &B, XP *const xs[PC], float out[PC])
 {
 	const float d = half_bits_to_float(B.d);
-	float a0[8], a1[8];
+	float a0[PC][8], a1[PC][8];
 #pragma unroll
-	for (int l = 0; l < 8; l++)
-		a0[l] = a1[l] = 0.0f;
+	for (int p = 0; p < PC; p++)
+#pragma unroll
+		for (int l = 0; l < 8; l++)
+			a0[p][l] = a1[p][l] = 0.0f;
 #pragma unroll
 	for (int n = 0; n < 2; n++) {
 #pragma unroll
@@ -165,32 +230,46 @@ __device__ __forceinline__ float block_dot(const Q6KBlock &B, XP *x)
 			const uint4 &chh = B.c[8 + 2 * n + (l >> 4)];
 #pragma unroll
 			for (int hw = 0; hw < 2; hw++) {
-					const int dw = ((l & 8) >> 2) + hw;
+				const int dw = ((l & 8) >> 2) + hw;
+				step_fence<PC>(a0, a1);
 				uint32_t L = word(cl, dw), L2 = word(cl2, dw), H = word(chh, dw);
-				asm volatile("" : "+v"(L), "+v"(L2), "+v"(H)::"memory");
-				XP *xq = x + 128 * n + l + 4 * hw;
-				launder(xq);
+				asm volatile("" : "+v"(L), "+v"(L2), "+v"(H));
 				const uint32_t q1 = (L & 0x0f0f0f0fu) | ((H & 0x03030303u) << 4);
 				const uint32_t q2 = (L2 & 0x0f0f0f0fu) | (((H >> 2) & 0x03030303u) << 4);
 				const uint32_t q3 = ((L >> 4) & 0x0f0f0f0fu) | (((H >> 4) & 0x03030303u) << 4);
 				const uint32_t q4 = ((L2 >> 4) & 0x0f0f0f0fu) | (((H >> 6) & 0x03030303u) << 4);
+				float f1[4], f2[4], f3[4], f4[4];
 #pragma unroll
 				for (int i = 0; i < 4; i++) {
-					const int m = 4 * hw + i;
-					XP *xb = xq + i;
-					a0[m] = __builtin_fmaf(W0, (ubyte(q1, i) - 32.0f) * xb[0], a0[m]);
-					a1[m] = __builtin_fmaf(W1, (ubyte(q2, i) - 32.0f) * xb[32], a1[m]);
-					a0[m] = __builtin_fmaf(W2, (ubyte(q3, i) - 32.0f) * xb[64], a0[m]);
-					a1[m] = __builtin_fmaf(W3, (ubyte(q4, i) - 32.0f) * xb[96], a1[m]);
+					f1[i] = ubyte(q1, i) - 32.0f;
+					f2[i] = ubyte(q2, i) - 32.0f;
+					f3[i] = ubyte(q3, i) - 32.0f;
+					f4[i] = ubyte(q4, i) - 32.0f;
+				}
+#pragma unroll
+				for (int p = 0; p < PC; p++) {
+					XP *xq = xs[p] + 128 * n + l + 4 * hw;
+					launder(xq);
+#pragma unroll
+					for (int i = 0; i < 4; i++) {
+						const int m = 4 * hw + i;
+						a0[p][m] = __builtin_fmaf(W0, f1[i] * xq[i], a0[p][m]);
+						a1[p][m] = __builtin_fmaf(W1, f2[i] * xq[32 + i], a1[p][m]);
+						a0[p][m] = __builtin_fmaf(W2, f3[i] * xq[64 + i], a0[p][m]);
+						a1[p][m] = __builtin_fmaf(W3, f4[i] * xq[96 + i], a1[p][m]);
+					}
 				}
 			}
 		}
 	}
-	float v[8];
 #pragma unroll
-	for (int l = 0; l < 8; l++)
-		v[l] = a0[l] + a1[l];
-	return hsum8(v);
+	for (int p = 0; p < PC; p++) {
+		float v[8];
+#pragma unroll
+		for (int l = 0; l < 8; l++)
+			v[l] = a0[p][l] + a1[p][l];
+		out[p] = hsum8(v);
+	}
 }
 
 template <int TYPE> struct BlockOf;
@@ -201,119 +280,184 @@ template <> struct BlockOf<TIE_GGML_Q6_K> {
 	using type = Q6KBlock;
 };
 
-struct RowsArgs {
-	const uint8_t *w[2];  // expert tensor data (panel layout / BF16 row-major)
-	float *sums[2];       // [pairs][rows] row results (gate, up) or y (down)
+// PC pairs of the group against the lane's block; part[(b*pg_cap + q) * 64 + lane]
+template <int PC, typename Block, typename XP, typename XF>
+__device__ __forceinline__ void pairs_chunk(const Block &blk, int q, XF xrow, float *part_b, int lane)
+{
+	XP *xs[PC];
+#pragma unroll
+	for (int p = 0; p < PC; p++)
+		xs[p] = xrow(q + p);
+	float out[PC];
+	block_dots<PC>(blk, xs, out);
+#pragma unroll
+	for (int p = 0; p < PC; p++)
+		part_b[(q + p) * 64 + lane] = out[p];
+}
+
+// All np pairs of a group against the lane's block, 4 / 2 / 1 at a time.
+template <typename Block, typename XP, typename XF>
+__device__ __forceinline__ void block_all_pairs(const Block &blk, int np, XF xrow, float *part_b, int lane)
+{
+	int q = 0;
+	if (TIE_EXACT_PCMAX >= 4)
+		for (; q + 4 <= np; q += 4)
+			pairs_chunk<4, Block, XP>(blk, q, xrow, part_b, lane);
+	for (; q + 2 <= np;) {
+		pairs_chunk<2, Block, XP>(blk, q, xrow, part_b, lane);
+		q += 2;
+	}
+	if (q < np)
+		pairs_chunk<1, Block, XP>(blk, q, xrow, part_b, lane);
+}
+
+// ------------------------------------------------------------ routing
+struct ExactArgs {
+	const uint8_t *w[2];  // gate/up (or down) tensor data, panel layout / BF16 row-major
 	size_t expert_bytes[2];
-	int rows, in, k, E;
-	const float *x;       // [T][in] (gate/up) or h [pairs][in] (down)
-	float *h;             // [pairs][rows] SwiGLU output (gate/up)
-	uint32_t *tile_cnt;   // [pairs][rows/64] gate/up completion counters
+	int rows, in, k, E, T;
+	const float *x;       // [T][d] (gate/up)
+	float *sums[2];       // [pairs][F] gate and up row sums (gate/up output, down input)
+	float *y;             // [pairs][d] down output
 	const float *silu;
-	const int32_t *offsets, *pairs, *active;
-	int mat_base;         // matrix index of blockIdx.z == 0 (0 gate, 1 up)
+	const float *logits;  // [T][E] (inline routing)
+	int32_t *topk_idx;    // [T][k]
+	float *topk_w;        // [T][k]
+	int32_t *offsets, *pairs, *active; // grouping (global)
+	int pg_cap;           // pairs per LDS group
+	int inline_route;
 };
 
-// Gate/up completion: each (pair, 64-row tile) is finished by two
-// workgroups, the gate one and the up one.  Both publish their row sums;
-// the second to arrive (counter 0 -> 1 -> reset) applies TIE's table SwiGLU
-// (swiglu_activation_f32_f32_avx2) to the tile and writes h.
-__device__ __forceinline__ void finish_gate_up(const RowsArgs &a, int m, int pair, int rt, int lane, float s)
+// Selection and grouping of all T <= INLINE_T tokens by one workgroup of NT
+// threads (E <= INLINE_E <= NT); workgroup (0,0,0) also publishes them for
+// the later kernels.  Results land in the LDS arrays of `R`.
+struct InlineRoute {
+	float lg[INLINE_T * INLINE_E];
+	float sel[INLINE_T * MAX_K];
+	float w[INLINE_T * MAX_K];
+	int32_t idx[INLINE_T * MAX_K];
+	int32_t cnt[INLINE_E], cur[INLINE_E];
+	int32_t offsets[INLINE_E + 1], active[INLINE_E + 1];
+	int32_t pairs[INLINE_T * MAX_K];
+	int wsum[16];
+	uint64_t etab[32];
+};
+
+template <int NT> __device__ __forceinline__ void inline_route(const ExactArgs &a, InlineRoute &R)
 {
-	const int nrt = a.rows / PANEL_ROWS;
-	const size_t o = (size_t)pair * a.rows + rt * PANEL_ROWS + lane;
-	a.sums[m][o] = s;
-	__threadfence();
-	uint32_t prev = 0;
-	uint32_t *cnt = a.tile_cnt + (size_t)pair * nrt + rt;
-	if (lane == 0)
-		prev = atomicAdd(cnt, 1u);
-	prev = __shfl(prev, 0);
-	if (prev == 1) {
-		__threadfence();
-		const float other = __hip_atomic_load(a.sums[1 - m] + o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-		const float g = m == 0 ? s : other;
-		const float u = m == 0 ? other : s;
-		a.h[o] = tie_swiglu(g, u, a.silu);
-		if (lane == 0)
-			__hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+	const int tid = threadIdx.x;
+	const int T = a.T, E = a.E, k = a.k;
+	if (tid < 32) {
+		const uint64_t tab[32] = TIE_EXP2_TABLE;
+		R.etab[tid] = tab[tid];
+	}
+	for (int i = tid; i < T * E; i += NT)
+		R.lg[i] = a.logits[i];
+	__syncthreads();
+	if (tid < 8 * T) {
+		const int t = tid >> 3;
+		topk_softmax_group8(R.lg + t * E, E, k, R.sel + t * MAX_K, R.etab, R.idx + t * k, R.w + t * k);
+	}
+	__syncthreads();
+	group_pairs<NT>(R.idx, T * k, E, R.cnt, R.cur, R.wsum, R.offsets, R.pairs, R.active, nullptr, nullptr,
+			nullptr);
+	if (blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0) {
+		for (int i = tid; i < T * k; i += NT) {
+			a.topk_idx[i] = R.idx[i];
+			a.topk_w[i] = R.w[i];
+			a.pairs[i] = R.pairs[i];
+		}
+		for (int i = tid; i <= E; i += NT) {
+			a.offsets[i] = R.offsets[i];
+			a.active[i] = R.active[i];
+		}
 	}
 }
 
-// ------------------------------------------------------------ exact_q_rows
-// One workgroup per (64-row tile, active expert, matrix).  Wave w owns
-// super-block columns w, w + 8, ...; lane i owns row i of the tile.  Per
-// pair the lane loads its block (coalesced panel chunks), forms the block
-// dot with the pair's input vector read by scalar loads, and the per-block
-// dots meet in LDS where wave 0 adds them in block order.
-constexpr int MAX_NB = 64; // super-blocks per row (in <= 16384)
-constexpr int Q_WAVES = 8;
-
-template <int TYPE, bool DOWN>
-__global__ __launch_bounds__(64 * Q_WAVES) void exact_q_rows_kernel(RowsArgs a)
+// ------------------------------------------------------------ gate / up
+// blockIdx = (64-row panel, active-expert slot, matrix).
+template <int TYPE>
+__global__ __launch_bounds__(GU_THREADS) EXACT_OCC void exact_gu_kernel(ExactArgs a)
 {
 	using Block = typename BlockOf<TYPE>::type;
-	__shared__ float part[MAX_NB][64];
-	const int m = a.mat_base + blockIdx.z;
+	extern __shared__ float part[]; // [nb][pg_cap][64]
+	__shared__ InlineRoute R;
+	const int32_t *offsets = a.offsets, *pairs = a.pairs, *active = a.active;
+	if (a.inline_route) {
+		inline_route<GU_THREADS>(a, R);
+		offsets = R.offsets;
+		pairs = R.pairs;
+		active = R.active;
+	}
 	const int slot = blockIdx.y;
-	if (slot >= a.active[a.E])
+	if (slot >= active[a.E])
 		return;
-	const int e = a.active[slot];
-	const int p0 = a.offsets[e], p1 = a.offsets[e + 1];
+	const int m = blockIdx.z;
+	const int e = active[slot];
+	const int p0 = offsets[e], p1 = offsets[e + 1];
 	const int rt = blockIdx.x;
 	const int lane = threadIdx.x & 63;
 	const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-	const int nw = blockDim.x >> 6;
 	const int nb = a.in / QK;
 	const size_t pb = panel_bytes(TYPE);
 	const uint8_t *panels = a.w[m] + (size_t)e * a.expert_bytes[m] + (size_t)rt * nb * pb;
+	const int pg_cap = a.pg_cap;
+	const int k = a.k, in = a.in;
+	const float *x = a.x;
 
-	for (int p = p0; p < p1; p++) {
-		const int pair = __builtin_amdgcn_readfirstlane(a.pairs[p]);
-		cfloat *xin = (cfloat *)(DOWN ? a.x + (size_t)pair * a.in : a.x + (size_t)(pair / a.k) * a.in);
-		for (int b = w; b < nb; b += nw) {
+	for (int g0 = p0; g0 < p1; g0 += pg_cap) {
+		const int np = min(pg_cap, p1 - g0);
+		const int32_t *gp = pairs + g0;
+		auto xrow = [&](int q) {
+			const int pair = __builtin_amdgcn_readfirstlane(gp[q]);
+			return (cfloat *)(x + (size_t)(pair / k) * in);
+		};
+		for (int b = w; b < nb; b += GU_WAVES) {
 			Block blk;
 			load_block(panels + (size_t)b * pb, lane, blk);
-			part[b][lane] = block_dot(blk, xin + QK * b);
+			auto xrow_b = [&](int q) { return xrow(q) + QK * b; };
+			block_all_pairs<Block, cfloat>(blk, np, xrow_b, part + (size_t)b * pg_cap * 64, lane);
 		}
 		__syncthreads();
-		if (w == 0) {
-			float s = 0.0f; // serial sum over super-blocks (math_avx2.c:762-766)
+		// serial sum over super-blocks (math_avx2.c:762-766)
+		for (int i = threadIdx.x; i < np * 64; i += GU_THREADS) {
+			const int q = i >> 6, r = i & 63;
+			float s = 0.0f;
 			for (int b = 0; b < nb; b++)
-				s = s + part[b][lane];
-			if (DOWN)
-				a.sums[m][(size_t)pair * a.rows + rt * PANEL_ROWS + lane] = s;
-			else
-				finish_gate_up(a, m, pair, rt, lane, s);
+				s = s + part[((size_t)b * pg_cap + q) * 64 + r];
+			a.sums[m][(size_t)gp[q] * a.rows + rt * PANEL_ROWS + r] = s;
 		}
 		__syncthreads();
 	}
 }
 
-// --------------------------------------------------------- exact_bf16_rows
-// mat_vec_row_f32_bf16_f32_avx2 + dot_product_f32_bf16_avx2
+// BF16 gate/up: mat_vec_row_f32_bf16_f32_avx2 + dot_product_f32_bf16_avx2
 // (math_avx2.c:148-158, 188-226): 8 lane accumulators over the whole row,
-// then hsum8.  Thread h of a row owns lanes 4h..4h+3; a workgroup covers
-// 64 rows (128 threads) so gate/up tiles match the SwiGLU completion tiles.
-template <bool DOWN>
-__global__ __launch_bounds__(128) void exact_bf16_rows_kernel(RowsArgs a)
+// then hsum8.  Thread h of a row owns lanes 4h..4h+3.
+constexpr int BF_THREADS = 128;
+__global__ __launch_bounds__(BF_THREADS) void exact_gu_bf16_kernel(ExactArgs a)
 {
-	const int m = a.mat_base + blockIdx.z;
+	__shared__ InlineRoute R;
+	const int32_t *offsets = a.offsets, *pairs = a.pairs, *active = a.active;
+	if (a.inline_route) {
+		inline_route<BF_THREADS>(a, R);
+		offsets = R.offsets;
+		pairs = R.pairs;
+		active = R.active;
+	}
 	const int slot = blockIdx.y;
-	if (slot >= a.active[a.E])
+	if (slot >= active[a.E])
 		return;
-	const int e = a.active[slot];
-	const int p0 = a.offsets[e], p1 = a.offsets[e + 1];
-	const int rt = blockIdx.x;
-	const int r = threadIdx.x >> 1; // row within the tile
-	const int h = threadIdx.x & 1;
-	const int row = rt * PANEL_ROWS + r;
+	const int m = blockIdx.z;
+	const int e = active[slot];
+	const int p0 = offsets[e], p1 = offsets[e + 1];
+	const int r = threadIdx.x >> 1, h = threadIdx.x & 1;
+	const int row = blockIdx.x * PANEL_ROWS + r;
 	const uint16_t *wr = reinterpret_cast<const uint16_t *>(a.w[m] + (size_t)e * a.expert_bytes[m]) +
 			     (size_t)row * a.in;
-
 	for (int p = p0; p < p1; p++) {
-		const int pair = a.pairs[p];
-		const float *xin = DOWN ? a.x + (size_t)pair * a.in : a.x + (size_t)(pair / a.k) * a.in;
+		const int pair = pairs[p];
+		const float *xin = a.x + (size_t)(pair / a.k) * a.in;
 		float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 		for (int i = 0; i < a.in; i += 8) {
 			const uint2 wv = *reinterpret_cast<const uint2 *>(wr + i + 4 * h);
@@ -329,89 +473,279 @@ __global__ __launch_bounds__(128) void exact_bf16_rows_kernel(RowsArgs a)
 		for (int i = 0; i < 4; i++)
 			o[i] = __shfl_xor(acc[i], 1);
 		const float s0 = acc[0] + o[0], s1 = acc[1] + o[1], s2 = acc[2] + o[2], s3 = acc[3] + o[3];
-		const float s = (s0 + s1) + (s2 + s3);
-		// rows of this tile gathered onto wave 0 lanes 0..63 through LDS
-		__shared__ float rs[PANEL_ROWS];
 		if (h == 0)
-			rs[r] = s;
+			a.sums[m][(size_t)pair * a.rows + row] = (s0 + s1) + (s2 + s3);
+	}
+}
+
+// ------------------------------------------------------------ down
+// h = silu_tab(gate) * up for the np pairs of a group, into LDS [np][F]
+__device__ __forceinline__ void stage_h(const ExactArgs &a, const int32_t *gp, int np, float *hs)
+{
+	const int F = a.in;
+	for (int i = threadIdx.x; i < np * F; i += blockDim.x) {
+		const int q = i / F, f = i - q * F;
+		const size_t o = (size_t)gp[q] * F + f;
+		hs[i] = tie_swiglu(a.sums[0][o], a.sums[1][o], a.silu);
+	}
+}
+
+// blockIdx = (64-row panel of d, active-expert slot); blockDim = 64 *
+// min(nb, 8).  Dynamic LDS: h [pg_cap][F] | part [nb][pg_cap][64].
+template <int TYPE>
+__global__ __launch_bounds__(512) EXACT_OCC void exact_down_kernel(ExactArgs a)
+{
+	using Block = typename BlockOf<TYPE>::type;
+	extern __shared__ float lds[];
+	const int slot = blockIdx.y;
+	if (slot >= a.active[a.E])
+		return;
+	const int e = a.active[slot];
+	const int p0 = a.offsets[e], p1 = a.offsets[e + 1];
+	const int rt = blockIdx.x;
+	const int lane = threadIdx.x & 63;
+	const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+	const int nw = blockDim.x >> 6;
+	const int F = a.in, nb = F / QK;
+	const size_t pb = panel_bytes(TYPE);
+	const uint8_t *panels = a.w[0] + (size_t)e * a.expert_bytes[0] + (size_t)rt * nb * pb;
+	const int pg_cap = a.pg_cap;
+	float *hs = lds;
+	float *part = lds + (size_t)pg_cap * F;
+
+	for (int g0 = p0; g0 < p1; g0 += pg_cap) {
+		const int np = min(pg_cap, p1 - g0);
+		const int32_t *gp = a.pairs + g0;
+		stage_h(a, gp, np, hs);
 		__syncthreads();
-		if (threadIdx.x < 64) {
-			const float v = rs[threadIdx.x];
-			if (DOWN)
-				a.sums[m][(size_t)pair * a.rows + rt * PANEL_ROWS + threadIdx.x] = v;
-			else
-				finish_gate_up(a, m, pair, rt, threadIdx.x, v);
+		for (int b = w; b < nb; b += nw) {
+			Block blk;
+			load_block(panels + (size_t)b * pb, lane, blk);
+			auto xrow_b = [&](int q) { return (lfloat *)(hs + (size_t)q * F + QK * b); };
+			block_all_pairs<Block, lfloat>(blk, np, xrow_b, part + (size_t)b * pg_cap * 64, lane);
+		}
+		__syncthreads();
+		for (int i = threadIdx.x; i < np * 64; i += blockDim.x) {
+			const int q = i >> 6, r = i & 63;
+			float s = 0.0f;
+			for (int b = 0; b < nb; b++)
+				s = s + part[((size_t)b * pg_cap + q) * 64 + r];
+			a.y[(size_t)gp[q] * a.rows + rt * PANEL_ROWS + r] = s;
+		}
+		__syncthreads();
+	}
+}
+
+// BF16 down: blockIdx = (64-row panel of d, slot), 128 threads.  Dynamic
+// LDS: h [pg_cap][F].
+__global__ __launch_bounds__(BF_THREADS) void exact_down_bf16_kernel(ExactArgs a)
+{
+	extern __shared__ float hs[];
+	const int slot = blockIdx.y;
+	if (slot >= a.active[a.E])
+		return;
+	const int e = a.active[slot];
+	const int p0 = a.offsets[e], p1 = a.offsets[e + 1];
+	const int r = threadIdx.x >> 1, h = threadIdx.x & 1;
+	const int row = blockIdx.x * PANEL_ROWS + r;
+	const int F = a.in;
+	const uint16_t *wr = reinterpret_cast<const uint16_t *>(a.w[0] + (size_t)e * a.expert_bytes[0]) +
+			     (size_t)row * F;
+	const int pg_cap = a.pg_cap;
+	for (int g0 = p0; g0 < p1; g0 += pg_cap) {
+		const int np = min(pg_cap, p1 - g0);
+		const int32_t *gp = a.pairs + g0;
+		stage_h(a, gp, np, hs);
+		__syncthreads();
+		for (int q = 0; q < np; q++) {
+			const float *xin = hs + (size_t)q * F;
+			float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+			for (int i = 0; i < F; i += 8) {
+				const uint2 wv = *reinterpret_cast<const uint2 *>(wr + i + 4 * h);
+				const float4 xv = *reinterpret_cast<const float4 *>(xin + i + 4 * h);
+				acc[0] = __builtin_fmaf(xv.x, bf16_bits_to_float(wv.x & 0xffffu), acc[0]);
+				acc[1] = __builtin_fmaf(xv.y, bf16_bits_to_float(wv.x >> 16), acc[1]);
+				acc[2] = __builtin_fmaf(xv.z, bf16_bits_to_float(wv.y & 0xffffu), acc[2]);
+				acc[3] = __builtin_fmaf(xv.w, bf16_bits_to_float(wv.y >> 16), acc[3]);
+			}
+			float o[4];
+#pragma unroll
+			for (int i = 0; i < 4; i++)
+				o[i] = __shfl_xor(acc[i], 1);
+			const float s0 = acc[0] + o[0], s1 = acc[1] + o[1], s2 = acc[2] + o[2], s3 = acc[3] + o[3];
+			if (h == 0)
+				a.y[(size_t)gp[q] * a.rows + row] = (s0 + s1) + (s2 + s3);
 		}
 		__syncthreads();
 	}
 }
 
 // ---------------------------------------------------------------- launcher
-template <bool DOWN>
-static hipError_t launch_rows(const Layer &L, int mat_base, int nmat, const ExpertTensor &t, int k, int max_active,
-			      const float *x, Workspace &ws, const float *silu, int npairs, hipStream_t s)
+static hipError_t set_lds_limit(const void *fn, size_t bytes)
 {
-	RowsArgs a;
-	if (DOWN) {
-		a.w[0] = a.w[1] = L.down.data;
-		a.expert_bytes[0] = a.expert_bytes[1] = L.down.expert_bytes;
-		a.sums[0] = a.sums[1] = ws.y;
-	} else {
-		a.w[0] = L.gate.data;
-		a.w[1] = L.up.data;
-		a.expert_bytes[0] = L.gate.expert_bytes;
-		a.expert_bytes[1] = L.up.expert_bytes;
-		a.sums[0] = ws.h + (size_t)npairs * L.F;     // gate sums
-		a.sums[1] = ws.h + 2 * (size_t)npairs * L.F; // up sums
-	}
-	a.rows = t.rows;
-	a.in = t.in;
-	a.k = k;
-	a.E = L.E;
-	a.x = x;
-	a.h = ws.h;
-	a.tile_cnt = ws.tile_cnt;
-	a.silu = silu;
-	a.offsets = ws.offsets;
-	a.pairs = ws.pairs;
-	a.active = ws.active;
-	a.mat_base = mat_base;
-	dim3 grid(t.rows / PANEL_ROWS, max_active, nmat);
-	if (t.type == TIE_GGML_BF16) {
-		hipLaunchKernelGGL(exact_bf16_rows_kernel<DOWN>, grid, dim3(128), 0, s, a);
-	} else {
-		const int nb = t.in / QK;
-		const int waves = nb < Q_WAVES ? nb : Q_WAVES;
-		if (t.type == TIE_GGML_Q4_K)
-			hipLaunchKernelGGL((exact_q_rows_kernel<TIE_GGML_Q4_K, DOWN>), grid, dim3(64 * waves), 0, s, a);
-		else
-			hipLaunchKernelGGL((exact_q_rows_kernel<TIE_GGML_Q6_K, DOWN>), grid, dim3(64 * waves), 0, s, a);
-	}
-	return hipGetLastError();
+	return hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
 }
 
-// ws.h holds three [pairs][F] planes: h (SwiGLU output), gate sums, up sums.
-hipError_t launch_exact_experts(const Layer &L, const float *x, int T, int k, const float *silu, Workspace &ws,
-				hipStream_t s)
+// Routing (logits, selection, grouping) and the expert GEMVs of the exact
+// path.  ws.h holds two [pairs][F] planes: the gate and the up row sums.
+hipError_t launch_exact_block(const Layer &L, const float *x, int T, int k, const float *silu, Workspace &ws,
+			      hipStream_t s)
 {
 	const int npairs = T * k;
-	const int max_active = npairs < L.E ? npairs : L.E;
 	if (npairs == 0)
 		return hipSuccess;
+	const int max_active = npairs < L.E ? npairs : L.E;
 	hipError_t err;
-	prof_begin("exact_gate_up", s);
-	if (L.gate.type == L.up.type)
-		err = launch_rows<false>(L, 0, 2, L.gate, k, max_active, x, ws, silu, npairs, s);
-	else {
-		err = launch_rows<false>(L, 0, 1, L.gate, k, max_active, x, ws, silu, npairs, s);
-		if (err == hipSuccess)
-			err = launch_rows<false>(L, 1, 1, L.up, k, max_active, x, ws, silu, npairs, s);
-	}
+	prof_begin("router", s);
+	err = launch_router_logits(L, x, T, ws.logits, s);
 	prof_end(s);
 	if (err != hipSuccess)
 		return err;
+	const bool inl = T <= INLINE_T && L.E <= INLINE_E && L.gate.type == L.up.type;
+	if (!inl) {
+		prof_begin("route_group", s);
+		if (npairs <= 4096)
+			err = launch_route_group(L, T, k, ws.logits, ws, s);
+		else {
+			err = launch_router_select(L, T, k, ws.logits, ws.topk_idx, ws.topk_w, s);
+			if (err == hipSuccess)
+				err = launch_dispatch(L, T, k, ws.topk_idx, ws, s);
+		}
+		prof_end(s);
+		if (err != hipSuccess)
+			return err;
+	}
+	ExactArgs a;
+	memset(&a, 0, sizeof a);
+	a.k = k;
+	a.E = L.E;
+	a.T = T;
+	a.x = x;
+	a.sums[0] = ws.h;
+	a.sums[1] = ws.h + (size_t)npairs * L.F;
+	a.y = ws.y;
+	a.silu = silu;
+	a.logits = ws.logits;
+	a.topk_idx = ws.topk_idx;
+	a.topk_w = ws.topk_w;
+	a.offsets = ws.offsets;
+	a.pairs = ws.pairs;
+	a.active = ws.active;
+	a.inline_route = inl ? 1 : 0;
+
+	prof_begin("exact_gate_up", s);
+	if (L.gate.type == L.up.type) {
+		ExactArgs g = a;
+		g.sums[0] = a.sums[0];
+		g.sums[1] = a.sums[1];
+		// blockIdx.z selects the matrix: gate (0) or up (1)
+		g.w[0] = L.gate.data;
+		g.w[1] = L.up.data;
+		g.expert_bytes[0] = L.gate.expert_bytes;
+		g.expert_bytes[1] = L.up.expert_bytes;
+		g.rows = L.F;
+		g.in = L.d;
+		dim3 grid(L.F / PANEL_ROWS, max_active, 2);
+		if (L.gate.type == TIE_GGML_BF16) {
+			hipLaunchKernelGGL(exact_gu_bf16_kernel, grid, dim3(BF_THREADS), 0, s, g);
+		} else {
+			const int nb = L.d / QK;
+			g.pg_cap = PG_MAX < PART_FLOATS / (nb * 64) ? PG_MAX : PART_FLOATS / (nb * 64);
+			if (g.pg_cap < 1)
+				g.pg_cap = 1;
+			const size_t lds = sizeof(float) * (size_t)nb * g.pg_cap * 64;
+			if (L.gate.type == TIE_GGML_Q4_K) {
+				err = set_lds_limit((const void *)exact_gu_kernel<TIE_GGML_Q4_K>, lds + sizeof(InlineRoute));
+				if (err == hipSuccess)
+					hipLaunchKernelGGL(exact_gu_kernel<TIE_GGML_Q4_K>, grid, dim3(GU_THREADS), lds, s, g);
+			} else {
+				err = set_lds_limit((const void *)exact_gu_kernel<TIE_GGML_Q6_K>, lds + sizeof(InlineRoute));
+				if (err == hipSuccess)
+					hipLaunchKernelGGL(exact_gu_kernel<TIE_GGML_Q6_K>, grid, dim3(GU_THREADS), lds, s, g);
+			}
+		}
+	} else {
+		// gate and up of different types: one launch per matrix, each with
+		// its matrix in slot 0 of the arguments
+		for (int mat = 0; mat < 2 && err == hipSuccess; mat++) {
+			ExactArgs g = a;
+			const ExpertTensor &t = mat == 0 ? L.gate : L.up;
+			g.w[0] = t.data;
+			g.expert_bytes[0] = t.expert_bytes;
+			g.sums[0] = a.sums[mat];
+			g.rows = t.rows;
+			g.in = t.in;
+			dim3 grid(t.rows / PANEL_ROWS, max_active, 1);
+			if (t.type == TIE_GGML_BF16) {
+				hipLaunchKernelGGL(exact_gu_bf16_kernel, grid, dim3(BF_THREADS), 0, s, g);
+			} else {
+				const int nb = t.in / QK;
+				g.pg_cap = PG_MAX < PART_FLOATS / (nb * 64) ? PG_MAX : PART_FLOATS / (nb * 64);
+				if (g.pg_cap < 1)
+					g.pg_cap = 1;
+				const size_t lds = sizeof(float) * (size_t)nb * g.pg_cap * 64;
+				if (t.type == TIE_GGML_Q4_K) {
+					err = set_lds_limit((const void *)exact_gu_kernel<TIE_GGML_Q4_K>,
+							    lds + sizeof(InlineRoute));
+					if (err == hipSuccess)
+						hipLaunchKernelGGL(exact_gu_kernel<TIE_GGML_Q4_K>, grid, dim3(GU_THREADS), lds,
+								   s, g);
+				} else {
+					err = set_lds_limit((const void *)exact_gu_kernel<TIE_GGML_Q6_K>,
+							    lds + sizeof(InlineRoute));
+					if (err == hipSuccess)
+						hipLaunchKernelGGL(exact_gu_kernel<TIE_GGML_Q6_K>, grid, dim3(GU_THREADS), lds,
+								   s, g);
+				}
+			}
+			if (err == hipSuccess)
+				err = hipGetLastError();
+		}
+	}
+	if (err == hipSuccess)
+		err = hipGetLastError();
+	prof_end(s);
+	if (err != hipSuccess)
+		return err;
+
 	prof_begin("exact_down", s);
-	err = launch_rows<true>(L, 0, 1, L.down, k, max_active, ws.h, ws, silu, npairs, s);
+	{
+		ExactArgs g = a;
+		g.w[0] = L.down.data;
+		g.expert_bytes[0] = L.down.expert_bytes;
+		g.rows = L.d;
+		g.in = L.F;
+		dim3 grid(L.d / PANEL_ROWS, max_active);
+		const int F = L.F, nb = F / QK;
+		if (L.down.type == TIE_GGML_BF16) {
+			g.pg_cap = PART_FLOATS / F < PG_MAX ? PART_FLOATS / F : PG_MAX;
+			if (g.pg_cap < 1)
+				g.pg_cap = 1;
+			const size_t lds = sizeof(float) * (size_t)g.pg_cap * F;
+			err = set_lds_limit((const void *)exact_down_bf16_kernel, lds);
+			if (err == hipSuccess)
+				hipLaunchKernelGGL(exact_down_bf16_kernel, grid, dim3(BF_THREADS), lds, s, g);
+		} else {
+			g.pg_cap = PART_FLOATS / (F + nb * 64);
+			if (g.pg_cap > PG_MAX)
+				g.pg_cap = PG_MAX;
+			if (g.pg_cap < 1)
+				g.pg_cap = 1;
+			const size_t lds = sizeof(float) * (size_t)g.pg_cap * (F + nb * 64);
+			const int nw = nb < 8 ? nb : 8;
+			const void *fn = L.down.type == TIE_GGML_Q4_K ? (const void *)exact_down_kernel<TIE_GGML_Q4_K>
+								      : (const void *)exact_down_kernel<TIE_GGML_Q6_K>;
+			err = set_lds_limit(fn, lds);
+			if (err == hipSuccess) {
+				if (L.down.type == TIE_GGML_Q4_K)
+					hipLaunchKernelGGL(exact_down_kernel<TIE_GGML_Q4_K>, grid, dim3(64 * nw), lds, s, g);
+				else
+					hipLaunchKernelGGL(exact_down_kernel<TIE_GGML_Q6_K>, grid, dim3(64 * nw), lds, s, g);
+			}
+		}
+		if (err == hipSuccess)
+			err = hipGetLastError();
+	}
 	prof_end(s);
 	return err;
 }

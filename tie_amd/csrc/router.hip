@@ -8,230 +8,41 @@
 // kernels below keep those exact operation sequences, so logits, selected
 // experts and gate weights are bit-identical to TIE's.
 //
-// Two shapes:
-//   router_small   one workgroup per (expert, group of 4 tokens); the expert
-//                  row and the tokens are staged in LDS with coalesced
-//                  16-byte loads, one thread per (token, lane) runs the
-//                  256-long FMA chain.  Used for small T, where spreading the
-//                  1 MiB router matrix over E workgroups matters most.  The
-//                  last workgroup of a token group (completion counter,
-//                  self-resetting) does top-k + softmax for its tokens.
-//   router_logits  one workgroup per 32 tokens x 32 experts over the
-//   + router_topk  transposed router matrix (stored at layer creation);
-//                  each thread runs 16 independent lane chains from LDS
-//                  tiles.  A second kernel selects the experts, 8 lanes per
-//                  token: no cross-workgroup handshake, whose agent-scope
-//                  fences cost more than the launch on this multi-XCD part.
+// Logit kernels (no cross-workgroup handshakes: an agent-scope fence costs
+// more than a launch on this multi-XCD part):
+//   router_small   T <= 4: one workgroup per expert row, row and tokens
+//                  staged in LDS, one thread per (token, lane) chain.
+//   router_mid     up to a few hundred tokens: one workgroup per (expert,
+//                  32 tokens), row in LDS, x streamed from L2.
+//   router_logits  large T: 32 tokens x 32 experts per workgroup over the
+//                  transposed router matrix staged by direct global->LDS
+//                  loads.
+// Selection kernels: router_topk (8 lanes per token, E <= 128) and
+// router_topk_wave (a wave per token, E <= 1024).  Small batches select
+// and group in one workgroup instead (route_group_kernel, dispatch.hip).
 #include "common.h"
-#include "tie_expf.h"
+#include "route.h"
 
 namespace tie {
 
-// top-k (engine.c:891-914 semantics) + softmax (engine.c:864-888) for one
-// token, by one wave.  `lg` holds the token's E logits.  The k winners are
-// extracted one at a time by a wave-wide argmax under the order (value
-// descending, index ascending) -- the order find_top_k's strict-greater
-// insertion produces; NaN and -inf never qualify; unfilled slots are
-// {-1, -inf}.  Slot j's exponential is computed by lane j, the sum is
-// formed serially in slot order, and every weight is e_j * (1 / sum).
-__device__ void topk_softmax_wave(const float *lg, int E, int k, const uint64_t *etab, int32_t *out_idx,
-				  float *out_w)
-{
-	const int lane = threadIdx.x & 63;
-	constexpr int PER = MAX_E / 64;
-	float v[PER];
-#pragma unroll
-	for (int q = 0; q < PER; q++) {
-		const int e = q * 64 + lane;
-		const float x = e < E ? lg[e] : -__builtin_inff();
-		v[q] = (x > -__builtin_inff()) ? x : -__builtin_inff(); // NaN -> never selected
-	}
-	float my_s = -__builtin_inff();
-	int my_i = -1;
-	for (int j = 0; j < k; j++) {
-		// lane-local best: first (lowest index) maximum
-		float bv = -__builtin_inff();
-		int be = 0x7fffffff;
-#pragma unroll
-		for (int q = 0; q < PER; q++)
-			if (v[q] > bv) {
-				bv = v[q];
-				be = q * 64 + lane;
-			}
-		// wave argmax by (value desc, index asc)
-#pragma unroll
-		for (int off = 32; off > 0; off >>= 1) {
-			const float ov = __shfl_xor(bv, off);
-			const int oe = __shfl_xor(be, off);
-			if (ov > bv || (ov == bv && oe < be)) {
-				bv = ov;
-				be = oe;
-			}
-		}
-		const bool found = bv > -__builtin_inff();
-		if (lane == j) {
-			my_s = found ? bv : -__builtin_inff();
-			my_i = found ? be : -1;
-		}
-		if (found && (be & 63) == lane) {
-#pragma unroll
-			for (int q = 0; q < PER; q++)
-				if (q == (be >> 6))
-					v[q] = -__builtin_inff();
-		}
-	}
-	// softmax over the k selected logits: max is slot 0 (or -inf), exp per lane
-	float mx = __shfl(my_s, 0);
-	for (int j = 1; j < k; j++) {
-		const float sj = __shfl(my_s, j);
-		if (sj > mx)
-			mx = sj;
-	}
-	const float ev = lane < k ? tie_expf_tab(my_s - mx, etab) : 0.0f;
-	float sum = 0.0f;
-	for (int j = 0; j < k; j++)
-		sum = sum + __shfl(ev, j);
-	const float inv = __fdiv_rn(1.0f, sum);
-	if (lane < k) {
-		out_w[lane] = ev * inv;
-		out_idx[lane] = my_i;
-	}
-}
-
-// DPP lane moves inside rows of 16 lanes (v_mov_b32 with a DPP control)
-template <int CTRL> __device__ __forceinline__ float dppf(float v)
-{
-	return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
-}
-template <int CTRL> __device__ __forceinline__ int dppi(int v)
-{
-	return __builtin_amdgcn_mov_dpp(v, CTRL, 0xf, 0xf, false);
-}
-constexpr int DPP_XOR1 = 0xb1;        // quad_perm [1,0,3,2]
-constexpr int DPP_XOR2 = 0x4e;        // quad_perm [2,3,0,1]
-constexpr int DPP_HALF_MIRROR = 0x141; // lane i <- lane 7-i within each 8
-constexpr int DPP_SHL1 = 0x101, DPP_SHL2 = 0x102, DPP_SHL4 = 0x104; // lane i <- lane i+n (row of 16)
-
-// hsum_f32_avx2's tree over the 8 lanes l = lane%8 of a group, on lane l = 0:
-// ((v0+v4)+(v1+v5)) + ((v2+v6)+(v3+v7))  (math_avx2.c:14-21)
-__device__ __forceinline__ float hsum8_lanes(float v)
-{
-	const float s = v + dppf<DPP_SHL4>(v); // lanes 0..3: s_m = v_m + v_m+4
-	const float a = s + dppf<DPP_SHL1>(s); // lane 0: s0 + s1, lane 2: s2 + s3
-	return a + dppf<DPP_SHL2>(a);          // lane 0: (s0 + s1) + (s2 + s3)
-}
-
-// The same selection and softmax for 8 tokens per wave: 8 lanes per token
-// (E <= 128, 16 logits per lane).  Identical order of selection (value
-// descending, index ascending; NaN and -inf never qualify) and identical
-// softmax arithmetic: the maximum over the slots, e_j = expf(s_j - max),
-// the sum formed serially in slot order, w_j = e_j * (1 / sum).  The
-// argmax runs over DPP lane moves.  `lg` is the group's token's E logits,
-// `sel` LDS scratch of MAX_K floats for that token.
-__device__ __forceinline__ void topk_softmax_group8(const float *lg, int E, int k, float *sel, const uint64_t *etab,
-						    int32_t *out_idx, float *out_w)
-{
-	constexpr int G = 8, V = 16;
-	const int lig = threadIdx.x & (G - 1);
-	float v[V];
-#pragma unroll
-	for (int q = 0; q < V; q++) {
-		const int e = q * G + lig;
-		const float x = e < E ? lg[e] : -__builtin_inff();
-		v[q] = (x > -__builtin_inff()) ? x : -__builtin_inff();
-	}
-	auto better = [](float ov, int oe, float bv, int be) { return ov > bv || (ov == bv && oe < be); };
-	for (int j = 0; j < k; j++) {
-		float bv = -__builtin_inff();
-		int be = 0x7fffffff;
-#pragma unroll
-		for (int q = 0; q < V; q++)
-			if (v[q] > bv) {
-				bv = v[q];
-				be = q * G + lig;
-			}
-		float ov = dppf<DPP_XOR1>(bv);
-		int oe = dppi<DPP_XOR1>(be);
-		if (better(ov, oe, bv, be)) {
-			bv = ov;
-			be = oe;
-		}
-		ov = dppf<DPP_XOR2>(bv);
-		oe = dppi<DPP_XOR2>(be);
-		if (better(ov, oe, bv, be)) {
-			bv = ov;
-			be = oe;
-		}
-		ov = dppf<DPP_HALF_MIRROR>(bv);
-		oe = dppi<DPP_HALF_MIRROR>(be);
-		if (better(ov, oe, bv, be)) {
-			bv = ov;
-			be = oe;
-		}
-		const bool found = bv > -__builtin_inff();
-		if (lig == 0) {
-			sel[j] = found ? bv : -__builtin_inff();
-			out_idx[j] = found ? be : -1;
-		}
-		if (found && (be & (G - 1)) == lig) {
-#pragma unroll
-			for (int q = 0; q < V; q++)
-				if (q == be / G)
-					v[q] = -__builtin_inff();
-		}
-	}
-	__builtin_amdgcn_wave_barrier();
-	float mx = sel[0];
-	for (int j = 1; j < k; j++)
-		if (sel[j] > mx)
-			mx = sel[j];
-	// e_j on lane j % 8, then the serial sum on lane 0
-	float ev[MAX_K / G];
-#pragma unroll
-	for (int q = 0; q < MAX_K / G; q++) {
-		const int j = q * G + lig;
-		ev[q] = j < k ? tie_expf_tab(sel[j] - mx, etab) : 0.0f;
-	}
-	__builtin_amdgcn_wave_barrier();
-#pragma unroll
-	for (int q = 0; q < MAX_K / G; q++) {
-		const int j = q * G + lig;
-		if (j < k)
-			sel[j] = ev[q];
-	}
-	__builtin_amdgcn_wave_barrier();
-	float sum = 0.0f;
-	for (int j = 0; j < k; j++)
-		sum = sum + sel[j];
-	const float inv = __fdiv_rn(1.0f, sum);
-#pragma unroll
-	for (int q = 0; q < MAX_K / G; q++) {
-		const int j = q * G + lig;
-		if (j < k)
-			out_w[j] = ev[q] * inv;
-	}
-}
-
 // ------------------------------------------------------------ router_small
-constexpr int RS_TOK = 4;     // tokens per workgroup
+// T <= RS_TOK: one workgroup per expert row; the row and the tokens are
+// staged in LDS with coalesced 16-byte loads and thread (t, l) runs the
+// lane-l chain of token t.  Spreads the 1 MiB router matrix over E
+// workgroups, which matters most at T = 1.
+constexpr int RS_TOK = 4;
 constexpr int RS_THREADS = 256;
 
 __global__ __launch_bounds__(RS_THREADS) void router_small_kernel(const float *__restrict__ x,
 								  const float *__restrict__ W,
 								  const float *__restrict__ bias, int T, int d, int E,
-								  int k, float *__restrict__ logits,
-								  int32_t *__restrict__ topk_idx,
-								  float *__restrict__ topk_w, uint32_t *counter)
+								  float *__restrict__ logits)
 {
 	extern __shared__ float lds[]; // W row [d] | x [RS_TOK][d]
 	float *ws = lds;
 	float *xs = lds + d;
-	__shared__ int s_last;
-	__shared__ uint64_t etab[32];
-
 	const int e = blockIdx.x;
-	const int t0 = blockIdx.y * RS_TOK;
-	const int nt = min(RS_TOK, T - t0);
+	const int nt = min(RS_TOK, T);
 	const int tid = threadIdx.x;
 	const int d4 = d >> 2;
 
@@ -239,64 +50,65 @@ __global__ __launch_bounds__(RS_THREADS) void router_small_kernel(const float *_
 	for (int i = tid; i < d4; i += RS_THREADS)
 		reinterpret_cast<float4 *>(ws)[i] = W4[i];
 	for (int t = 0; t < nt; t++) {
-		const float4 *x4 = reinterpret_cast<const float4 *>(x + (size_t)(t0 + t) * d);
+		const float4 *x4 = reinterpret_cast<const float4 *>(x + (size_t)t * d);
 		for (int i = tid; i < d4; i += RS_THREADS)
 			reinterpret_cast<float4 *>(xs + (size_t)t * d)[i] = x4[i];
 	}
 	__syncthreads();
-
-	if (tid < RS_TOK * 8) {
-		const int t = tid >> 3, l = tid & 7;
-		float acc = 0.0f;
-		if (t < nt) {
-			const float *xt = xs + (size_t)t * d;
-#pragma unroll 8
-			for (int i = 0; i < d; i += 8)
-				acc = __builtin_fmaf(xt[i + l], ws[i + l], acc);
-		}
-		// hsum8 across the 8 lanes of this chain group
-		float s = acc + __shfl_down(acc, 4, 8);
-		float a = s + __shfl_down(s, 1, 8);
-		float r = a + __shfl_down(a, 2, 8);
-		if (l == 0 && t < nt) {
-			if (bias)
-				r = r + bias[e];
-			logits[(size_t)(t0 + t) * E + e] = r;
-		}
-	}
-
-	// completion per token group: the last of the E workgroups of this
-	// group (counter blockIdx.y, self-resetting) selects the experts of its
-	// tokens, one wave per token
-	__syncthreads();
-	uint32_t *cnt = counter + blockIdx.y;
-	if (tid == 0) {
-		__threadfence();
-		const uint32_t prev = atomicAdd(cnt, 1u);
-		s_last = (prev == gridDim.x - 1);
-	}
-	__syncthreads();
-	if (!s_last)
+	if (tid >= RS_TOK * 8)
 		return;
-	if (tid < 32) {
-		const uint64_t tab[32] = TIE_EXP2_TABLE;
-		etab[tid] = tab[tid];
+	const int t = tid >> 3, l = tid & 7;
+	float acc = 0.0f;
+	if (t < nt) {
+		const float *xt = xs + (size_t)t * d;
+#pragma unroll 16
+		for (int i = 0; i < d; i += 8)
+			acc = __builtin_fmaf(xt[i + l], ws[i + l], acc);
 	}
-	__threadfence();
+	const float r = hsum8_lanes(acc);
+	if (l == 0 && t < nt)
+		logits[(size_t)t * E + e] = bias ? r + bias[e] : r;
+}
+
+// ------------------------------------------------------------ router_mid
+// RS_TOK < T (up to a few hundred tokens): one workgroup per (expert, 32
+// tokens).  The expert row is staged in LDS (read as a broadcast); thread
+// (t, l) streams x[t][8i + l] from global memory (L2-resident) with many
+// loads in flight and runs the lane-l chain of token t.
+constexpr int RM_TOK = 32;
+constexpr int RM_THREADS = RM_TOK * 8;
+
+__global__ __launch_bounds__(RM_THREADS) void router_mid_kernel(const float *__restrict__ x,
+								const float *__restrict__ W,
+								const float *__restrict__ bias, int T, int d, int E,
+								float *__restrict__ logits)
+{
+	extern __shared__ float ws[]; // W row [d]
+	const int e = blockIdx.x;
+	const int t0 = blockIdx.y * RM_TOK;
+	const int tid = threadIdx.x;
+	const float4 *W4 = reinterpret_cast<const float4 *>(W + (size_t)e * d);
+	for (int i = tid; i < (d >> 2); i += RM_THREADS)
+		reinterpret_cast<float4 *>(ws)[i] = W4[i];
 	__syncthreads();
-	const int wave = tid >> 6;
-	if (wave < nt) {
-		const int t = t0 + wave;
-		float *my = lds + (size_t)wave * E;
-		for (int q = tid & 63; q < E; q += 64)
-			my[q] = __hip_atomic_load(logits + (size_t)t * E + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-		__builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-		__builtin_amdgcn_wave_barrier();
-		__builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-		topk_softmax_wave(my, E, k, etab, topk_idx + (size_t)t * k, topk_w + (size_t)t * k);
+	const int t = t0 + (tid >> 3), l = tid & 7;
+	const bool live = t < T;
+	const float *xt = x + (size_t)(live ? t : 0) * d + l;
+	const float *wl = ws + l;
+	float acc = 0.0f;
+	constexpr int U = 32;
+	for (int i = 0; i < d; i += 8 * U) {
+		float xv[U];
+#pragma unroll
+		for (int u = 0; u < U; u++)
+			xv[u] = xt[i + 8 * u];
+#pragma unroll
+		for (int u = 0; u < U; u++)
+			acc = __builtin_fmaf(xv[u], wl[i + 8 * u], acc);
 	}
-	if (tid == 0)
-		__hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+	const float r = hsum8_lanes(acc);
+	if (l == 0 && live)
+		logits[(size_t)t * E + e] = bias ? r + bias[e] : r;
 }
 
 // ------------------------------------------------------------ router_logits
@@ -466,13 +278,34 @@ hipError_t launch_router_transpose(const Layer &L, hipStream_t s)
 	return hipGetLastError();
 }
 
-hipError_t launch_router(const Layer &L, const float *x, int T, int k, float *logits, int32_t *topk_idx,
-			 float *topk_w, uint32_t *counter, hipStream_t s)
+// ------------------------------------------------------------ router_topk_wave
+// E > 128: one wave per token (topk_softmax_wave, E <= MAX_E).
+constexpr int RW_THREADS = 256;
+__global__ __launch_bounds__(RW_THREADS) void router_topk_wave_kernel(const float *__restrict__ logits, int T, int E,
+								      int k, int32_t *__restrict__ topk_idx,
+								      float *__restrict__ topk_w)
+{
+	__shared__ uint64_t etab[32];
+	if (threadIdx.x < 32) {
+		const uint64_t tab[32] = TIE_EXP2_TABLE;
+		etab[threadIdx.x] = tab[threadIdx.x];
+	}
+	__syncthreads();
+	const int t = blockIdx.x * (RW_THREADS / 64) + (threadIdx.x >> 6);
+	if (t < T)
+		topk_softmax_wave(logits + (size_t)t * E, E, k, etab, topk_idx + (size_t)t * k, topk_w + (size_t)t * k);
+}
+
+hipError_t launch_router_logits(const Layer &L, const float *x, int T, float *logits, hipStream_t s)
 {
 	const int d = L.d, E = L.E;
-	// the selection kernel keeps 32 tokens' logits in LDS: E <= 128
-	const bool tiled = T > 64 && E % RT_EXP == 0 && E <= 128 && d % RT_KC == 0;
-	if (tiled) {
+	if (T <= RS_TOK) {
+		const size_t lds = sizeof(float) * (size_t)d * (1 + RS_TOK);
+		hipLaunchKernelGGL(router_small_kernel, dim3(E), dim3(RS_THREADS), lds, s, x, L.router, L.bias, T, d, E,
+				   logits);
+		return hipGetLastError();
+	}
+	if (T > 2 * RT_TOK && E % RT_EXP == 0 && d % RT_KC == 0) {
 		static bool attr = false;
 		if (!attr) {
 			const hipError_t err = hipFuncSetAttribute((const void *)router_logits_kernel,
@@ -483,16 +316,32 @@ hipError_t launch_router(const Layer &L, const float *x, int T, int k, float *lo
 		}
 		hipLaunchKernelGGL(router_logits_kernel, dim3((T + RT_TOK - 1) / RT_TOK, E / RT_EXP), dim3(RT_THREADS),
 				   RT_LDS, s, x, L.routerT, L.bias, T, d, E, logits);
-		hipLaunchKernelGGL(router_topk_kernel, dim3((T + RK_TOK - 1) / RK_TOK), dim3(RK_THREADS), 0, s, logits, T,
-				   E, k, topk_idx, topk_w);
 		return hipGetLastError();
 	}
-	const size_t lds = sizeof(float) * (size_t)d * (1 + RS_TOK);
-	const size_t lds_need = sizeof(float) * (size_t)(RS_THREADS / 64) * E;
-	hipLaunchKernelGGL(router_small_kernel, dim3(E, (T + RS_TOK - 1) / RS_TOK), dim3(RS_THREADS),
-			   lds > lds_need ? lds : lds_need, s, x, L.router, L.bias, T, d, E, k, logits, topk_idx,
-			   topk_w, counter);
+	hipLaunchKernelGGL(router_mid_kernel, dim3(E, (T + RM_TOK - 1) / RM_TOK), dim3(RM_THREADS),
+			   sizeof(float) * (size_t)d, s, x, L.router, L.bias, T, d, E, logits);
 	return hipGetLastError();
+}
+
+hipError_t launch_router_select(const Layer &L, int T, int k, const float *logits, int32_t *topk_idx, float *topk_w,
+				hipStream_t s)
+{
+	if (L.E <= 128)
+		hipLaunchKernelGGL(router_topk_kernel, dim3((T + RK_TOK - 1) / RK_TOK), dim3(RK_THREADS), 0, s, logits, T,
+				   L.E, k, topk_idx, topk_w);
+	else
+		hipLaunchKernelGGL(router_topk_wave_kernel, dim3((T + RW_THREADS / 64 - 1) / (RW_THREADS / 64)),
+				   dim3(RW_THREADS), 0, s, logits, T, L.E, k, topk_idx, topk_w);
+	return hipGetLastError();
+}
+
+hipError_t launch_router(const Layer &L, const float *x, int T, int k, float *logits, int32_t *topk_idx,
+			 float *topk_w, hipStream_t s)
+{
+	hipError_t err = launch_router_logits(L, x, T, logits, s);
+	if (err != hipSuccess)
+		return err;
+	return launch_router_select(L, T, k, logits, topk_idx, topk_w, s);
 }
 
 } // namespace tie
