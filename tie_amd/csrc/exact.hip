@@ -156,38 +156,53 @@ __device__ __forceinline__ void block_dots(const Q4KBlock &B, XP *const xs[PC], 
 #pragma unroll
 		for (int l = 0; l < 8; l++)
 			a0[p][l] = a1[p][l] = 0.0f;
+	// 32 steps s = (g, o, h) of 8 weights each; step s reads x[64g + 16o +
+	// 4h + i] and x[.. + 32].  The input pointers of step s + 1 are laundered
+	// at the top of step s, so their loads may be issued a step early.
+	XP *cur[PC];
 #pragma unroll
-	for (int g = 0; g < 4; g++) {
-		const float D1 = D[2 * g], M1 = nM[2 * g], D2 = D[2 * g + 1], M2 = nM[2 * g + 1];
+	for (int p = 0; p < PC; p++) {
+		cur[p] = xs[p];
+		launder(cur[p]);
+	}
 #pragma unroll
-		for (int o = 0; o < 2; o++) {
-			uint4 q = B.c[1 + 2 * g + o];
+	for (int st = 0; st < 32; st++) {
+		const int g = st >> 3, o = (st >> 2) & 1, h = st & 3;
+		step_fence<PC>(a0, a1);
+		XP *nxt[PC];
+		if (st + 1 < 32) {
+			const int g1 = (st + 1) >> 3, o1 = ((st + 1) >> 2) & 1, h1 = (st + 1) & 3;
 #pragma unroll
-			for (int h = 0; h < 4; h++) {
-				step_fence<PC>(a0, a1);
-				uint32_t w = word(q, h);
-				asm volatile("" : "+v"(w));
-				uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
-				float wl[4], wh[4];
-#pragma unroll
-				for (int i = 0; i < 4; i++) {
-					wl[i] = __builtin_fmaf(ubyte(lo, i), D1, M1);
-					wh[i] = __builtin_fmaf(ubyte(hi, i), D2, M2);
-				}
-#pragma unroll
-				for (int p = 0; p < PC; p++) {
-					XP *xl = xs[p] + 64 * g + 16 * o + 4 * h;
-					launder(xl);
-#pragma unroll
-					for (int i = 0; i < 4; i++) {
-						const int m = 4 * h + i;
-						float &A = (m < 8) ? a0[p][m & 7] : a1[p][m & 7];
-						A = __builtin_fmaf(xl[i], wl[i], A);
-						A = __builtin_fmaf(xl[32 + i], wh[i], A);
-					}
-				}
+			for (int p = 0; p < PC; p++) {
+				nxt[p] = xs[p] + 64 * g1 + 16 * o1 + 4 * h1;
+				launder(nxt[p]);
 			}
 		}
+		const float D1 = D[2 * g], M1 = nM[2 * g], D2 = D[2 * g + 1], M2 = nM[2 * g + 1];
+		uint32_t w = word(B.c[1 + 2 * g + o], h);
+		asm volatile("" : "+v"(w));
+		const uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
+		float wl[4], wh[4];
+#pragma unroll
+		for (int i = 0; i < 4; i++) {
+			wl[i] = __builtin_fmaf(ubyte(lo, i), D1, M1);
+			wh[i] = __builtin_fmaf(ubyte(hi, i), D2, M2);
+		}
+#pragma unroll
+		for (int p = 0; p < PC; p++) {
+			XP *xl = cur[p];
+#pragma unroll
+			for (int i = 0; i < 4; i++) {
+				const int m = 4 * h + i;
+				float &A = (m < 8) ? a0[p][m & 7] : a1[p][m & 7];
+				A = __builtin_fmaf(xl[i], wl[i], A);
+				A = __builtin_fmaf(xl[32 + i], wh[i], A);
+			}
+		}
+		if (st + 1 < 32)
+#pragma unroll
+			for (int p = 0; p < PC; p++)
+				cur[p] = nxt[p];
 	}
 #pragma unroll
 	for (int p = 0; p < PC; p++) {
@@ -213,54 +228,66 @@ __device__ __forceinline__ void block_dots(const Q6KBlock &B, XP *const xs[PC], 
 #pragma unroll
 		for (int l = 0; l < 8; l++)
 			a0[p][l] = a1[p][l] = 0.0f;
+	// 16 steps s = (n, l, hw) of 16 weights each; step s reads x[128n + l +
+	// 4hw + i + {0, 32, 64, 96}].  Pointers of step s + 1 are laundered at
+	// the top of step s, as in the Q4_K dot.
+	XP *cur[PC];
 #pragma unroll
-	for (int n = 0; n < 2; n++) {
+	for (int p = 0; p < PC; p++) {
+		cur[p] = xs[p];
+		launder(cur[p]);
+	}
+	auto sc = [&](int j) { return (float)(int8_t)((word(B.c[12], j >> 2) >> (8 * (j & 3))) & 0xffu); };
 #pragma unroll
-		for (int l = 0; l < 32; l += 8) {
-			const int is = (l >= 16) ? 1 : 0;
-			auto sc = [&](int j) {
-				return (float)(int8_t)((word(B.c[12], j >> 2) >> (8 * (j & 3))) & 0xffu);
-			};
-			const float W0 = d * sc(8 * n + is + 0);
-			const float W1 = d * sc(8 * n + is + 2);
-			const float W2 = d * sc(8 * n + is + 4);
-			const float W3 = d * sc(8 * n + is + 6);
-			const uint4 &cl = B.c[4 * n + (l >> 4)];
-			const uint4 &cl2 = B.c[4 * n + 2 + (l >> 4)];
-			const uint4 &chh = B.c[8 + 2 * n + (l >> 4)];
+	for (int st = 0; st < 16; st++) {
+		const int n = st >> 3, l = 8 * ((st >> 1) & 3), hw = st & 1;
+		const int is = (l >= 16) ? 1 : 0;
+		step_fence<PC>(a0, a1);
+		XP *nxt[PC];
+		if (st + 1 < 16) {
+			const int n1 = (st + 1) >> 3, l1 = 8 * (((st + 1) >> 1) & 3), hw1 = (st + 1) & 1;
 #pragma unroll
-			for (int hw = 0; hw < 2; hw++) {
-				const int dw = ((l & 8) >> 2) + hw;
-				step_fence<PC>(a0, a1);
-				uint32_t L = word(cl, dw), L2 = word(cl2, dw), H = word(chh, dw);
-				asm volatile("" : "+v"(L), "+v"(L2), "+v"(H));
-				const uint32_t q1 = (L & 0x0f0f0f0fu) | ((H & 0x03030303u) << 4);
-				const uint32_t q2 = (L2 & 0x0f0f0f0fu) | (((H >> 2) & 0x03030303u) << 4);
-				const uint32_t q3 = ((L >> 4) & 0x0f0f0f0fu) | (((H >> 4) & 0x03030303u) << 4);
-				const uint32_t q4 = ((L2 >> 4) & 0x0f0f0f0fu) | (((H >> 6) & 0x03030303u) << 4);
-				float f1[4], f2[4], f3[4], f4[4];
-#pragma unroll
-				for (int i = 0; i < 4; i++) {
-					f1[i] = ubyte(q1, i) - 32.0f;
-					f2[i] = ubyte(q2, i) - 32.0f;
-					f3[i] = ubyte(q3, i) - 32.0f;
-					f4[i] = ubyte(q4, i) - 32.0f;
-				}
-#pragma unroll
-				for (int p = 0; p < PC; p++) {
-					XP *xq = xs[p] + 128 * n + l + 4 * hw;
-					launder(xq);
-#pragma unroll
-					for (int i = 0; i < 4; i++) {
-						const int m = 4 * hw + i;
-						a0[p][m] = __builtin_fmaf(W0, f1[i] * xq[i], a0[p][m]);
-						a1[p][m] = __builtin_fmaf(W1, f2[i] * xq[32 + i], a1[p][m]);
-						a0[p][m] = __builtin_fmaf(W2, f3[i] * xq[64 + i], a0[p][m]);
-						a1[p][m] = __builtin_fmaf(W3, f4[i] * xq[96 + i], a1[p][m]);
-					}
-				}
+			for (int p = 0; p < PC; p++) {
+				nxt[p] = xs[p] + 128 * n1 + l1 + 4 * hw1;
+				launder(nxt[p]);
 			}
 		}
+		const float W0 = d * sc(8 * n + is + 0);
+		const float W1 = d * sc(8 * n + is + 2);
+		const float W2 = d * sc(8 * n + is + 4);
+		const float W3 = d * sc(8 * n + is + 6);
+		const int dw = ((l & 8) >> 2) + hw;
+		uint32_t L = word(B.c[4 * n + (l >> 4)], dw), L2 = word(B.c[4 * n + 2 + (l >> 4)], dw),
+			 H = word(B.c[8 + 2 * n + (l >> 4)], dw);
+		asm volatile("" : "+v"(L), "+v"(L2), "+v"(H));
+		const uint32_t q1 = (L & 0x0f0f0f0fu) | ((H & 0x03030303u) << 4);
+		const uint32_t q2 = (L2 & 0x0f0f0f0fu) | (((H >> 2) & 0x03030303u) << 4);
+		const uint32_t q3 = ((L >> 4) & 0x0f0f0f0fu) | (((H >> 4) & 0x03030303u) << 4);
+		const uint32_t q4 = ((L2 >> 4) & 0x0f0f0f0fu) | (((H >> 6) & 0x03030303u) << 4);
+		float f1[4], f2[4], f3[4], f4[4];
+#pragma unroll
+		for (int i = 0; i < 4; i++) {
+			f1[i] = ubyte(q1, i) - 32.0f;
+			f2[i] = ubyte(q2, i) - 32.0f;
+			f3[i] = ubyte(q3, i) - 32.0f;
+			f4[i] = ubyte(q4, i) - 32.0f;
+		}
+#pragma unroll
+		for (int p = 0; p < PC; p++) {
+			XP *xq = cur[p];
+#pragma unroll
+			for (int i = 0; i < 4; i++) {
+				const int m = 4 * hw + i;
+				a0[p][m] = __builtin_fmaf(W0, f1[i] * xq[i], a0[p][m]);
+				a1[p][m] = __builtin_fmaf(W1, f2[i] * xq[32 + i], a1[p][m]);
+				a0[p][m] = __builtin_fmaf(W2, f3[i] * xq[64 + i], a0[p][m]);
+				a1[p][m] = __builtin_fmaf(W3, f4[i] * xq[96 + i], a1[p][m]);
+			}
+		}
+		if (st + 1 < 16)
+#pragma unroll
+			for (int p = 0; p < PC; p++)
+				cur[p] = nxt[p];
 	}
 #pragma unroll
 	for (int p = 0; p < PC; p++) {
@@ -295,20 +322,32 @@ __device__ __forceinline__ void pairs_chunk(const Block &blk, int q, XF xrow, fl
 		part_b[(q + p) * 64 + lane] = out[p];
 }
 
-// All np pairs of a group against the lane's block, 4 / 2 / 1 at a time.
+// All np pairs of a group against the lane's block: up to TIE_EXACT_PCMAX
+// at a time, the remainder (1 .. PCMAX-1) in one chunk of its own size, so
+// an expert with at most PCMAX pairs dequantises each weight once.
 template <typename Block, typename XP, typename XF>
 __device__ __forceinline__ void block_all_pairs(const Block &blk, int np, XF xrow, float *part_b, int lane)
 {
+	constexpr int PM = TIE_EXACT_PCMAX;
 	int q = 0;
-	if (TIE_EXACT_PCMAX >= 4)
-		for (; q + 4 <= np; q += 4)
-			pairs_chunk<4, Block, XP>(blk, q, xrow, part_b, lane);
-	for (; q + 2 <= np;) {
-		pairs_chunk<2, Block, XP>(blk, q, xrow, part_b, lane);
-		q += 2;
+	for (; q + PM <= np; q += PM)
+		pairs_chunk<PM, Block, XP>(blk, q, xrow, part_b, lane);
+	switch (np - q) {
+	case 3:
+		if constexpr (PM > 3)
+			pairs_chunk<3, Block, XP>(blk, q, xrow, part_b, lane);
+		break;
+	case 2:
+		if constexpr (PM > 2)
+			pairs_chunk<2, Block, XP>(blk, q, xrow, part_b, lane);
+		break;
+	case 1:
+		if constexpr (PM > 1)
+			pairs_chunk<1, Block, XP>(blk, q, xrow, part_b, lane);
+		break;
+	default:
+		break;
 	}
-	if (q < np)
-		pairs_chunk<1, Block, XP>(blk, q, xrow, part_b, lane);
 }
 
 // ------------------------------------------------------------ routing
@@ -319,6 +358,7 @@ struct ExactArgs {
 	const float *x;       // [T][d] (gate/up)
 	float *sums[2];       // [pairs][F] gate and up row sums (gate/up output, down input)
 	float *y;             // [pairs][d] down output
+	float *hbuf;          // [pairs][F] SwiGLU output (fused gate/up -> down)
 	const float *silu;
 	const float *logits;  // [T][E] (inline routing)
 	int32_t *topk_idx;    // [T][k]
@@ -375,15 +415,19 @@ template <int NT> __device__ __forceinline__ void inline_route(const ExactArgs &
 }
 
 // ------------------------------------------------------------ gate / up
-// blockIdx = (64-row panel, active-expert slot, matrix).
-template <int TYPE>
+// blockIdx = (64-row panel, active-expert slot, matrix).  FUSED: one
+// workgroup per (panel, slot) runs both matrices (wave w: gate and up
+// column w, w + 8, ..) and applies TIE's table SwiGLU
+// (swiglu_activation_f32_f32_avx2) to the row sums, writing h; otherwise
+// blockIdx.z selects the matrix and the row sums are written.
+template <int TYPE, bool FUSED>
 __global__ __launch_bounds__(GU_THREADS) EXACT_OCC void exact_gu_kernel(ExactArgs a)
 {
 	using Block = typename BlockOf<TYPE>::type;
-	extern __shared__ float part[]; // [nb][pg_cap][64]
+	extern __shared__ float part[]; // [mats][nb][pg_cap][64]
 	__shared__ InlineRoute R;
 	const int32_t *offsets = a.offsets, *pairs = a.pairs, *active = a.active;
-	if (a.inline_route) {
+	if (!FUSED && a.inline_route) {
 		inline_route<GU_THREADS>(a, R);
 		offsets = R.offsets;
 		pairs = R.pairs;
@@ -392,15 +436,15 @@ __global__ __launch_bounds__(GU_THREADS) EXACT_OCC void exact_gu_kernel(ExactArg
 	const int slot = blockIdx.y;
 	if (slot >= active[a.E])
 		return;
-	const int m = blockIdx.z;
 	const int e = active[slot];
 	const int p0 = offsets[e], p1 = offsets[e + 1];
 	const int rt = blockIdx.x;
 	const int lane = threadIdx.x & 63;
 	const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 	const int nb = a.in / QK;
+	const int nmat = FUSED ? 2 : 1;
+	const int m0 = FUSED ? 0 : (int)blockIdx.z;
 	const size_t pb = panel_bytes(TYPE);
-	const uint8_t *panels = a.w[m] + (size_t)e * a.expert_bytes[m] + (size_t)rt * nb * pb;
 	const int pg_cap = a.pg_cap;
 	const int k = a.k, in = a.in;
 	const float *x = a.x;
@@ -408,24 +452,33 @@ __global__ __launch_bounds__(GU_THREADS) EXACT_OCC void exact_gu_kernel(ExactArg
 	for (int g0 = p0; g0 < p1; g0 += pg_cap) {
 		const int np = min(pg_cap, p1 - g0);
 		const int32_t *gp = pairs + g0;
-		auto xrow = [&](int q) {
-			const int pair = __builtin_amdgcn_readfirstlane(gp[q]);
-			return (cfloat *)(x + (size_t)(pair / k) * in);
-		};
-		for (int b = w; b < nb; b += GU_WAVES) {
+		for (int t = w; t < nmat * nb; t += GU_WAVES) {
+			const int mi = t / nb, b = t - mi * nb, m = m0 + mi;
+			const uint8_t *panel = a.w[m] + (size_t)e * a.expert_bytes[m] + ((size_t)rt * nb + b) * pb;
 			Block blk;
-			load_block(panels + (size_t)b * pb, lane, blk);
-			auto xrow_b = [&](int q) { return xrow(q) + QK * b; };
-			block_all_pairs<Block, cfloat>(blk, np, xrow_b, part + (size_t)b * pg_cap * 64, lane);
+			load_block(panel, lane, blk);
+			auto xrow_b = [&](int q) {
+				const int pair = __builtin_amdgcn_readfirstlane(gp[q]);
+				return (cfloat *)(x + (size_t)(pair / k) * in + QK * b);
+			};
+			block_all_pairs<Block, cfloat>(blk, np, xrow_b, part + (size_t)t * pg_cap * 64, lane);
 		}
 		__syncthreads();
-		// serial sum over super-blocks (math_avx2.c:762-766)
+		// serial sums over super-blocks (math_avx2.c:762-766)
 		for (int i = threadIdx.x; i < np * 64; i += GU_THREADS) {
 			const int q = i >> 6, r = i & 63;
-			float s = 0.0f;
+			const size_t o = (size_t)gp[q] * a.rows + rt * PANEL_ROWS + r;
+			float s0 = 0.0f;
 			for (int b = 0; b < nb; b++)
-				s = s + part[((size_t)b * pg_cap + q) * 64 + r];
-			a.sums[m][(size_t)gp[q] * a.rows + rt * PANEL_ROWS + r] = s;
+				s0 = s0 + part[((size_t)b * pg_cap + q) * 64 + r];
+			if (FUSED) {
+				float s1 = 0.0f;
+				for (int b = 0; b < nb; b++)
+					s1 = s1 + part[((size_t)(nb + b) * pg_cap + q) * 64 + r];
+				a.hbuf[o] = tie_swiglu(s0, s1, a.silu);
+			} else {
+				a.sums[m0][o] = s0;
+			}
 		}
 		__syncthreads();
 	}
@@ -491,8 +544,10 @@ __device__ __forceinline__ void stage_h(const ExactArgs &a, const int32_t *gp, i
 }
 
 // blockIdx = (64-row panel of d, active-expert slot); blockDim = 64 *
-// min(nb, 8).  Dynamic LDS: h [pg_cap][F] | part [nb][pg_cap][64].
-template <int TYPE>
+// min(nb, 8).  HG: h comes from hbuf (written by the fused gate/up kernel)
+// through scalar loads; otherwise the prologue forms h from the gate and up
+// row sums in LDS.  Dynamic LDS: [h [pg_cap][F] |] part [nb][pg_cap][64].
+template <int TYPE, bool HG>
 __global__ __launch_bounds__(512) EXACT_OCC void exact_down_kernel(ExactArgs a)
 {
 	using Block = typename BlockOf<TYPE>::type;
@@ -511,18 +566,28 @@ __global__ __launch_bounds__(512) EXACT_OCC void exact_down_kernel(ExactArgs a)
 	const uint8_t *panels = a.w[0] + (size_t)e * a.expert_bytes[0] + (size_t)rt * nb * pb;
 	const int pg_cap = a.pg_cap;
 	float *hs = lds;
-	float *part = lds + (size_t)pg_cap * F;
+	float *part = HG ? lds : lds + (size_t)pg_cap * F;
 
 	for (int g0 = p0; g0 < p1; g0 += pg_cap) {
 		const int np = min(pg_cap, p1 - g0);
 		const int32_t *gp = a.pairs + g0;
-		stage_h(a, gp, np, hs);
-		__syncthreads();
+		if (!HG) {
+			stage_h(a, gp, np, hs);
+			__syncthreads();
+		}
 		for (int b = w; b < nb; b += nw) {
 			Block blk;
 			load_block(panels + (size_t)b * pb, lane, blk);
-			auto xrow_b = [&](int q) { return (lfloat *)(hs + (size_t)q * F + QK * b); };
-			block_all_pairs<Block, lfloat>(blk, np, xrow_b, part + (size_t)b * pg_cap * 64, lane);
+			if (HG) {
+				auto xrow_b = [&](int q) {
+					const int pair = __builtin_amdgcn_readfirstlane(gp[q]);
+					return (cfloat *)(a.hbuf + (size_t)pair * F + QK * b);
+				};
+				block_all_pairs<Block, cfloat>(blk, np, xrow_b, part + (size_t)b * pg_cap * 64, lane);
+			} else {
+				auto xrow_b = [&](int q) { return (lfloat *)(hs + (size_t)q * F + QK * b); };
+				block_all_pairs<Block, lfloat>(blk, np, xrow_b, part + (size_t)b * pg_cap * 64, lane);
+			}
 		}
 		__syncthreads();
 		for (int i = threadIdx.x; i < np * 64; i += blockDim.x) {
@@ -586,8 +651,47 @@ static hipError_t set_lds_limit(const void *fn, size_t bytes)
 	return hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
 }
 
+static int clamp_pg(int v)
+{
+	return v > PG_MAX ? PG_MAX : v < 1 ? 1 : v;
+}
+
+// Launch a quantised kernel template instance with `lds` bytes of dynamic
+// LDS (raising the function's limit first).
+template <typename K>
+static hipError_t launch_q(K kernel, dim3 grid, dim3 block, size_t lds, size_t static_lds, hipStream_t s,
+			   const ExactArgs &a)
+{
+	hipError_t err = set_lds_limit((const void *)kernel, lds + static_lds);
+	if (err != hipSuccess)
+		return err;
+	hipLaunchKernelGGL(kernel, grid, block, lds, s, a);
+	return hipGetLastError();
+}
+
+// gate/up of one quantised type; fused (both matrices, h out) or one
+// matrix per blockIdx.z (row sums out)
+static hipError_t launch_gu_q(int type, bool fused, int nmat, int rows, int in, int max_active, ExactArgs g,
+			      hipStream_t s)
+{
+	const int nb = in / QK;
+	const int mats = fused ? 2 : 1;
+	g.pg_cap = clamp_pg(PART_FLOATS / (mats * nb * 64));
+	g.rows = rows;
+	g.in = in;
+	const size_t lds = sizeof(float) * (size_t)mats * nb * g.pg_cap * 64;
+	const dim3 grid(rows / PANEL_ROWS, max_active, fused ? 1 : nmat), block(GU_THREADS);
+	const size_t st = sizeof(InlineRoute);
+	if (type == TIE_GGML_Q4_K)
+		return fused ? launch_q(exact_gu_kernel<TIE_GGML_Q4_K, true>, grid, block, lds, st, s, g)
+			     : launch_q(exact_gu_kernel<TIE_GGML_Q4_K, false>, grid, block, lds, st, s, g);
+	return fused ? launch_q(exact_gu_kernel<TIE_GGML_Q6_K, true>, grid, block, lds, st, s, g)
+		     : launch_q(exact_gu_kernel<TIE_GGML_Q6_K, false>, grid, block, lds, st, s, g);
+}
+
 // Routing (logits, selection, grouping) and the expert GEMVs of the exact
-// path.  ws.h holds two [pairs][F] planes: the gate and the up row sums.
+// path.  ws.h holds two [pairs][F] planes: the gate and the up row sums, or
+// (fused gate/up) h in the first.
 hipError_t launch_exact_block(const Layer &L, const float *x, int T, int k, const float *silu, Workspace &ws,
 			      hipStream_t s)
 {
@@ -601,7 +705,13 @@ hipError_t launch_exact_block(const Layer &L, const float *x, int T, int k, cons
 	prof_end(s);
 	if (err != hipSuccess)
 		return err;
-	const bool inl = T <= INLINE_T && L.E <= INLINE_E && L.gate.type == L.up.type;
+	const bool same = L.gate.type == L.up.type;
+	const bool quant = L.gate.type != TIE_GGML_BF16 && L.up.type != TIE_GGML_BF16;
+	const bool inl = T <= INLINE_T && L.E <= INLINE_E && same;
+	// Small T: gate and up in separate workgroups (twice the parallelism),
+	// h formed in the down prologue.  Otherwise one workgroup per panel runs
+	// both and writes h, which the down kernel reads through scalar loads.
+	const bool fused = !inl && same && quant && L.down.type != TIE_GGML_BF16;
 	if (!inl) {
 		prof_begin("route_group", s);
 		if (npairs <= 4096)
@@ -623,6 +733,7 @@ hipError_t launch_exact_block(const Layer &L, const float *x, int T, int k, cons
 	a.x = x;
 	a.sums[0] = ws.h;
 	a.sums[1] = ws.h + (size_t)npairs * L.F;
+	a.hbuf = ws.h;
 	a.y = ws.y;
 	a.silu = silu;
 	a.logits = ws.logits;
@@ -634,76 +745,41 @@ hipError_t launch_exact_block(const Layer &L, const float *x, int T, int k, cons
 	a.inline_route = inl ? 1 : 0;
 
 	prof_begin("exact_gate_up", s);
-	if (L.gate.type == L.up.type) {
+	{
 		ExactArgs g = a;
-		g.sums[0] = a.sums[0];
-		g.sums[1] = a.sums[1];
-		// blockIdx.z selects the matrix: gate (0) or up (1)
 		g.w[0] = L.gate.data;
 		g.w[1] = L.up.data;
 		g.expert_bytes[0] = L.gate.expert_bytes;
 		g.expert_bytes[1] = L.up.expert_bytes;
-		g.rows = L.F;
-		g.in = L.d;
-		dim3 grid(L.F / PANEL_ROWS, max_active, 2);
-		if (L.gate.type == TIE_GGML_BF16) {
-			hipLaunchKernelGGL(exact_gu_bf16_kernel, grid, dim3(BF_THREADS), 0, s, g);
+		if (same && L.gate.type == TIE_GGML_BF16) {
+			g.rows = L.F;
+			g.in = L.d;
+			hipLaunchKernelGGL(exact_gu_bf16_kernel, dim3(L.F / PANEL_ROWS, max_active, 2), dim3(BF_THREADS), 0,
+					   s, g);
+			err = hipGetLastError();
+		} else if (same) {
+			err = launch_gu_q(L.gate.type, fused, 2, L.F, L.d, max_active, g, s);
 		} else {
-			const int nb = L.d / QK;
-			g.pg_cap = PG_MAX < PART_FLOATS / (nb * 64) ? PG_MAX : PART_FLOATS / (nb * 64);
-			if (g.pg_cap < 1)
-				g.pg_cap = 1;
-			const size_t lds = sizeof(float) * (size_t)nb * g.pg_cap * 64;
-			if (L.gate.type == TIE_GGML_Q4_K) {
-				err = set_lds_limit((const void *)exact_gu_kernel<TIE_GGML_Q4_K>, lds + sizeof(InlineRoute));
-				if (err == hipSuccess)
-					hipLaunchKernelGGL(exact_gu_kernel<TIE_GGML_Q4_K>, grid, dim3(GU_THREADS), lds, s, g);
-			} else {
-				err = set_lds_limit((const void *)exact_gu_kernel<TIE_GGML_Q6_K>, lds + sizeof(InlineRoute));
-				if (err == hipSuccess)
-					hipLaunchKernelGGL(exact_gu_kernel<TIE_GGML_Q6_K>, grid, dim3(GU_THREADS), lds, s, g);
-			}
-		}
-	} else {
-		// gate and up of different types: one launch per matrix, each with
-		// its matrix in slot 0 of the arguments
-		for (int mat = 0; mat < 2 && err == hipSuccess; mat++) {
-			ExactArgs g = a;
-			const ExpertTensor &t = mat == 0 ? L.gate : L.up;
-			g.w[0] = t.data;
-			g.expert_bytes[0] = t.expert_bytes;
-			g.sums[0] = a.sums[mat];
-			g.rows = t.rows;
-			g.in = t.in;
-			dim3 grid(t.rows / PANEL_ROWS, max_active, 1);
-			if (t.type == TIE_GGML_BF16) {
-				hipLaunchKernelGGL(exact_gu_bf16_kernel, grid, dim3(BF_THREADS), 0, s, g);
-			} else {
-				const int nb = t.in / QK;
-				g.pg_cap = PG_MAX < PART_FLOATS / (nb * 64) ? PG_MAX : PART_FLOATS / (nb * 64);
-				if (g.pg_cap < 1)
-					g.pg_cap = 1;
-				const size_t lds = sizeof(float) * (size_t)nb * g.pg_cap * 64;
-				if (t.type == TIE_GGML_Q4_K) {
-					err = set_lds_limit((const void *)exact_gu_kernel<TIE_GGML_Q4_K>,
-							    lds + sizeof(InlineRoute));
-					if (err == hipSuccess)
-						hipLaunchKernelGGL(exact_gu_kernel<TIE_GGML_Q4_K>, grid, dim3(GU_THREADS), lds,
-								   s, g);
+			// gate and up of different types: one launch per matrix, each
+			// with its matrix in slot 0 of the arguments
+			for (int mat = 0; mat < 2 && err == hipSuccess; mat++) {
+				const ExpertTensor &t = mat == 0 ? L.gate : L.up;
+				ExactArgs h = g;
+				h.w[0] = t.data;
+				h.expert_bytes[0] = t.expert_bytes;
+				h.sums[0] = a.sums[mat];
+				if (t.type == TIE_GGML_BF16) {
+					h.rows = t.rows;
+					h.in = t.in;
+					hipLaunchKernelGGL(exact_gu_bf16_kernel, dim3(t.rows / PANEL_ROWS, max_active, 1),
+							   dim3(BF_THREADS), 0, s, h);
+					err = hipGetLastError();
 				} else {
-					err = set_lds_limit((const void *)exact_gu_kernel<TIE_GGML_Q6_K>,
-							    lds + sizeof(InlineRoute));
-					if (err == hipSuccess)
-						hipLaunchKernelGGL(exact_gu_kernel<TIE_GGML_Q6_K>, grid, dim3(GU_THREADS), lds,
-								   s, g);
+					err = launch_gu_q(t.type, false, 1, t.rows, t.in, max_active, h, s);
 				}
 			}
-			if (err == hipSuccess)
-				err = hipGetLastError();
 		}
 	}
-	if (err == hipSuccess)
-		err = hipGetLastError();
 	prof_end(s);
 	if (err != hipSuccess)
 		return err;
@@ -715,36 +791,28 @@ hipError_t launch_exact_block(const Layer &L, const float *x, int T, int k, cons
 		g.expert_bytes[0] = L.down.expert_bytes;
 		g.rows = L.d;
 		g.in = L.F;
-		dim3 grid(L.d / PANEL_ROWS, max_active);
+		const dim3 grid(L.d / PANEL_ROWS, max_active);
 		const int F = L.F, nb = F / QK;
 		if (L.down.type == TIE_GGML_BF16) {
-			g.pg_cap = PART_FLOATS / F < PG_MAX ? PART_FLOATS / F : PG_MAX;
-			if (g.pg_cap < 1)
-				g.pg_cap = 1;
+			g.pg_cap = clamp_pg(PART_FLOATS / F);
 			const size_t lds = sizeof(float) * (size_t)g.pg_cap * F;
-			err = set_lds_limit((const void *)exact_down_bf16_kernel, lds);
-			if (err == hipSuccess)
-				hipLaunchKernelGGL(exact_down_bf16_kernel, grid, dim3(BF_THREADS), lds, s, g);
+			err = launch_q(exact_down_bf16_kernel, grid, dim3(BF_THREADS), lds, 0, s, g);
 		} else {
-			g.pg_cap = PART_FLOATS / (F + nb * 64);
-			if (g.pg_cap > PG_MAX)
-				g.pg_cap = PG_MAX;
-			if (g.pg_cap < 1)
-				g.pg_cap = 1;
-			const size_t lds = sizeof(float) * (size_t)g.pg_cap * (F + nb * 64);
-			const int nw = nb < 8 ? nb : 8;
-			const void *fn = L.down.type == TIE_GGML_Q4_K ? (const void *)exact_down_kernel<TIE_GGML_Q4_K>
-								      : (const void *)exact_down_kernel<TIE_GGML_Q6_K>;
-			err = set_lds_limit(fn, lds);
-			if (err == hipSuccess) {
-				if (L.down.type == TIE_GGML_Q4_K)
-					hipLaunchKernelGGL(exact_down_kernel<TIE_GGML_Q4_K>, grid, dim3(64 * nw), lds, s, g);
-				else
-					hipLaunchKernelGGL(exact_down_kernel<TIE_GGML_Q6_K>, grid, dim3(64 * nw), lds, s, g);
+			const dim3 block(64 * (nb < 8 ? nb : 8));
+			if (fused) {
+				g.pg_cap = clamp_pg(PART_FLOATS / (nb * 64));
+				const size_t lds = sizeof(float) * (size_t)g.pg_cap * nb * 64;
+				err = L.down.type == TIE_GGML_Q4_K
+					      ? launch_q(exact_down_kernel<TIE_GGML_Q4_K, true>, grid, block, lds, 0, s, g)
+					      : launch_q(exact_down_kernel<TIE_GGML_Q6_K, true>, grid, block, lds, 0, s, g);
+			} else {
+				g.pg_cap = clamp_pg(PART_FLOATS / (F + nb * 64));
+				const size_t lds = sizeof(float) * (size_t)g.pg_cap * (F + nb * 64);
+				err = L.down.type == TIE_GGML_Q4_K
+					      ? launch_q(exact_down_kernel<TIE_GGML_Q4_K, false>, grid, block, lds, 0, s, g)
+					      : launch_q(exact_down_kernel<TIE_GGML_Q6_K, false>, grid, block, lds, 0, s, g);
 			}
 		}
-		if (err == hipSuccess)
-			err = hipGetLastError();
 	}
 	prof_end(s);
 	return err;
