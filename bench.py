@@ -90,8 +90,9 @@ class Workload:
 
 
 def expert_bytes(cfg):
+    """HBM bytes of one expert: gate + up together, and down."""
     from tie_amd import synth
-    gu = cfg["F"] * synth.row_bytes(cfg["gu_type"], cfg["d"])
+    gu = 2 * cfg["F"] * synth.row_bytes(cfg["gu_type"], cfg["d"])
     dn = cfg["d"] * synth.row_bytes(cfg["down_type"], cfg["F"])
     return gu, dn
 
@@ -220,14 +221,24 @@ def cpu_baseline(cfg, k, budget_s=12.0):
     use_ref = bind.ref_available() and cpu_has("avx512f") and cpu_has("avx2")
     fn = (lambda: bind.ref_moe_block(layer, x, k, nthreads=threads)) if use_ref else \
         (lambda: bind.moe_block(layer, x, k, nthreads=threads))
-    fn()  # warm-up (also builds the reference's thread pool)
-    n, t0 = 0, time.perf_counter()
-    while True:
-        fn()
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s:
-            break
+    # the reference prints progress on stdout (math_dispatch.c:657): send
+    # the C-level stdout to stderr meanwhile, so that stdout carries only the
+    # result line
+    sys.stdout.flush()
+    saved = os.dup(1)
+    os.dup2(2, 1)
+    try:
+        fn()  # warm-up (also builds the reference's thread pool)
+        n, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= budget_s:
+                break
+    finally:
+        os.dup2(saved, 1)
+        os.close(saved)
     return {"value": round(n * T / el, 2), "unit": "tokens/s", "cores": threads,
             "kind": "reference" if use_ref else "port",
             "sample": "%d calls of T=%d tokens (%s weights, one layer) in %.1f s on %d host threads; nproc=%d" % (
@@ -245,6 +256,9 @@ def main():
     ap.add_argument("--layers", type=int, default=0, help="weight layers cycled (0 = auto)")
     ap.add_argument("--path", default="auto", choices=["auto", "exact", "mfma"])
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-mb", type=int, default=0,
+                    help="only run a plain device copy of this many MiB 5 times (the reference kernel for "
+                         "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (collectives are out of scope); "
@@ -252,6 +266,16 @@ def main():
         sys.exit(2)
 
     import torch
+    if args.copy_mb:
+        n = args.copy_mb << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_per_launch": n, "launches": 5}), flush=True)
+        return
     import tie_amd
     from tie_amd import synth
     tie_amd.init(0)
