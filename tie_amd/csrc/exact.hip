@@ -80,9 +80,28 @@ template <int PC> __device__ __forceinline__ void step_fence(float (&a0)[PC][8],
 #else
 #define EXACT_OCC
 #endif
+#ifdef TIE_GU_WPE
+#define GU_OCC __attribute__((amdgpu_waves_per_eu(TIE_GU_WPE)))
+#else
+#define GU_OCC
+#endif
 
-constexpr int GU_WAVES = 8;       // waves of a gate/up workgroup
+// waves per gate/up workgroup: split (one matrix, small T) and fused
+#ifndef TIE_GU_WAVES
+#define TIE_GU_WAVES 8
+#endif
+#ifndef TIE_GUF_WAVES
+#define TIE_GUF_WAVES 4
+#endif
+#ifndef TIE_GU_PG
+#define TIE_GU_PG 8
+#endif
+#ifndef TIE_GU_PREFETCH
+#define TIE_GU_PREFETCH 0
+#endif
+constexpr int GU_WAVES = TIE_GU_WAVES;
 constexpr int GU_THREADS = 64 * GU_WAVES;
+constexpr int GUF_WAVES = TIE_GUF_WAVES;
 constexpr int PG_MAX = 16;        // pairs per LDS group
 constexpr int PART_FLOATS = 16384; // LDS budget of the per-block partial dots (64 KiB)
 constexpr int INLINE_T = 8;       // routing in the gate/up prologue up to this T (E <= 128)
@@ -157,52 +176,46 @@ __device__ __forceinline__ void block_dots(const Q4KBlock &B, XP *const xs[PC], 
 		for (int l = 0; l < 8; l++)
 			a0[p][l] = a1[p][l] = 0.0f;
 	// 32 steps s = (g, o, h) of 8 weights each; step s reads x[64g + 16o +
-	// 4h + i] and x[.. + 32].  The input pointers of step s + 1 are laundered
-	// at the top of step s, so their loads may be issued a step early.
-	XP *cur[PC];
-#pragma unroll
-	for (int p = 0; p < PC; p++) {
-		cur[p] = xs[p];
-		launder(cur[p]);
-	}
+	// 4h + i] and x[.. + 32].  The inputs are loaded for a super-step of XS
+	// steps at once (two runs of 4*XS floats per pair, in SGPRs), so one
+	// wait for scalar loads covers XS steps of FMAs.
+	constexpr int XS = PC == 1 ? 4 : PC == 2 ? 2 : 1;
+	XP *xb[PC];
 #pragma unroll
 	for (int st = 0; st < 32; st++) {
 		const int g = st >> 3, o = (st >> 2) & 1, h = st & 3;
 		step_fence<PC>(a0, a1);
-		XP *nxt[PC];
-		if (st + 1 < 32) {
-			const int g1 = (st + 1) >> 3, o1 = ((st + 1) >> 2) & 1, h1 = (st + 1) & 3;
+		if (st % XS == 0) {
 #pragma unroll
 			for (int p = 0; p < PC; p++) {
-				nxt[p] = xs[p] + 64 * g1 + 16 * o1 + 4 * h1;
-				launder(nxt[p]);
+				xb[p] = xs[p] + 64 * g + 16 * o + 4 * h;
+				launder(xb[p]);
 			}
 		}
 		const float D1 = D[2 * g], M1 = nM[2 * g], D2 = D[2 * g + 1], M2 = nM[2 * g + 1];
 		uint32_t w = word(B.c[1 + 2 * g + o], h);
-		asm volatile("" : "+v"(w));
-		const uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
+		asm volatile("" : "+v"(w)); // the word is unpacked here, not hoisted
+		uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
+		// opaque: the nibbles are then converted by v_cvt_f32_ubyte0..3 on
+		// the masked words, one instruction per weight
+		asm volatile("" : "+v"(lo), "+v"(hi));
 		float wl[4], wh[4];
 #pragma unroll
 		for (int i = 0; i < 4; i++) {
 			wl[i] = __builtin_fmaf(ubyte(lo, i), D1, M1);
 			wh[i] = __builtin_fmaf(ubyte(hi, i), D2, M2);
 		}
+		const int xo = 4 * (st % XS);
 #pragma unroll
 		for (int p = 0; p < PC; p++) {
-			XP *xl = cur[p];
 #pragma unroll
 			for (int i = 0; i < 4; i++) {
 				const int m = 4 * h + i;
 				float &A = (m < 8) ? a0[p][m & 7] : a1[p][m & 7];
-				A = __builtin_fmaf(xl[i], wl[i], A);
-				A = __builtin_fmaf(xl[32 + i], wh[i], A);
+				A = __builtin_fmaf(xb[p][xo + i], wl[i], A);
+				A = __builtin_fmaf(xb[p][xo + 32 + i], wh[i], A);
 			}
 		}
-		if (st + 1 < 32)
-#pragma unroll
-			for (int p = 0; p < PC; p++)
-				cur[p] = nxt[p];
 	}
 #pragma unroll
 	for (int p = 0; p < PC; p++) {
@@ -229,27 +242,22 @@ __device__ __forceinline__ void block_dots(const Q6KBlock &B, XP *const xs[PC], 
 		for (int l = 0; l < 8; l++)
 			a0[p][l] = a1[p][l] = 0.0f;
 	// 16 steps s = (n, l, hw) of 16 weights each; step s reads x[128n + l +
-	// 4hw + i + {0, 32, 64, 96}].  Pointers of step s + 1 are laundered at
-	// the top of step s, as in the Q4_K dot.
-	XP *cur[PC];
-#pragma unroll
-	for (int p = 0; p < PC; p++) {
-		cur[p] = xs[p];
-		launder(cur[p]);
-	}
+	// 4hw + i + {0, 32, 64, 96}].  For PC <= 2 the inputs of both hw steps of
+	// an (n, l) are loaded at once (four runs of 8 floats per pair, in SGPRs),
+	// so one wait for scalar loads covers two steps.
+	constexpr int XS = PC == 1 ? 2 : 1;
 	auto sc = [&](int j) { return (float)(int8_t)((word(B.c[12], j >> 2) >> (8 * (j & 3))) & 0xffu); };
+	XP *xb[PC];
 #pragma unroll
 	for (int st = 0; st < 16; st++) {
 		const int n = st >> 3, l = 8 * ((st >> 1) & 3), hw = st & 1;
 		const int is = (l >= 16) ? 1 : 0;
 		step_fence<PC>(a0, a1);
-		XP *nxt[PC];
-		if (st + 1 < 16) {
-			const int n1 = (st + 1) >> 3, l1 = 8 * (((st + 1) >> 1) & 3), hw1 = (st + 1) & 1;
+		if (st % XS == 0) {
 #pragma unroll
 			for (int p = 0; p < PC; p++) {
-				nxt[p] = xs[p] + 128 * n1 + l1 + 4 * hw1;
-				launder(nxt[p]);
+				xb[p] = xs[p] + 128 * n + l + 4 * hw;
+				launder(xb[p]);
 			}
 		}
 		const float W0 = d * sc(8 * n + is + 0);
@@ -260,10 +268,11 @@ __device__ __forceinline__ void block_dots(const Q6KBlock &B, XP *const xs[PC], 
 		uint32_t L = word(B.c[4 * n + (l >> 4)], dw), L2 = word(B.c[4 * n + 2 + (l >> 4)], dw),
 			 H = word(B.c[8 + 2 * n + (l >> 4)], dw);
 		asm volatile("" : "+v"(L), "+v"(L2), "+v"(H));
-		const uint32_t q1 = (L & 0x0f0f0f0fu) | ((H & 0x03030303u) << 4);
-		const uint32_t q2 = (L2 & 0x0f0f0f0fu) | (((H >> 2) & 0x03030303u) << 4);
-		const uint32_t q3 = ((L >> 4) & 0x0f0f0f0fu) | (((H >> 4) & 0x03030303u) << 4);
-		const uint32_t q4 = ((L2 >> 4) & 0x0f0f0f0fu) | (((H >> 6) & 0x03030303u) << 4);
+		uint32_t q1 = (L & 0x0f0f0f0fu) | ((H & 0x03030303u) << 4);
+		uint32_t q2 = (L2 & 0x0f0f0f0fu) | (((H >> 2) & 0x03030303u) << 4);
+		uint32_t q3 = ((L >> 4) & 0x0f0f0f0fu) | (((H >> 4) & 0x03030303u) << 4);
+		uint32_t q4 = ((L2 >> 4) & 0x0f0f0f0fu) | (((H >> 6) & 0x03030303u) << 4);
+		asm volatile("" : "+v"(q1), "+v"(q2), "+v"(q3), "+v"(q4));
 		float f1[4], f2[4], f3[4], f4[4];
 #pragma unroll
 		for (int i = 0; i < 4; i++) {
@@ -272,22 +281,19 @@ __device__ __forceinline__ void block_dots(const Q6KBlock &B, XP *const xs[PC], 
 			f3[i] = ubyte(q3, i) - 32.0f;
 			f4[i] = ubyte(q4, i) - 32.0f;
 		}
+		const int xo = 4 * (st % XS);
 #pragma unroll
 		for (int p = 0; p < PC; p++) {
-			XP *xq = cur[p];
 #pragma unroll
 			for (int i = 0; i < 4; i++) {
 				const int m = 4 * hw + i;
-				a0[p][m] = __builtin_fmaf(W0, f1[i] * xq[i], a0[p][m]);
-				a1[p][m] = __builtin_fmaf(W1, f2[i] * xq[32 + i], a1[p][m]);
-				a0[p][m] = __builtin_fmaf(W2, f3[i] * xq[64 + i], a0[p][m]);
-				a1[p][m] = __builtin_fmaf(W3, f4[i] * xq[96 + i], a1[p][m]);
+				XP *xq = xb[p] + xo + i;
+				a0[p][m] = __builtin_fmaf(W0, f1[i] * xq[0], a0[p][m]);
+				a1[p][m] = __builtin_fmaf(W1, f2[i] * xq[32], a1[p][m]);
+				a0[p][m] = __builtin_fmaf(W2, f3[i] * xq[64], a0[p][m]);
+				a1[p][m] = __builtin_fmaf(W3, f4[i] * xq[96], a1[p][m]);
 			}
 		}
-		if (st + 1 < 16)
-#pragma unroll
-			for (int p = 0; p < PC; p++)
-				cur[p] = nxt[p];
 	}
 #pragma unroll
 	for (int p = 0; p < PC; p++) {
@@ -421,17 +427,21 @@ template <int NT> __device__ __forceinline__ void inline_route(const ExactArgs &
 // (swiglu_activation_f32_f32_avx2) to the row sums, writing h; otherwise
 // blockIdx.z selects the matrix and the row sums are written.
 template <int TYPE, bool FUSED>
-__global__ __launch_bounds__(GU_THREADS) EXACT_OCC void exact_gu_kernel(ExactArgs a)
+__global__ __launch_bounds__(GU_THREADS) GU_OCC void exact_gu_kernel(ExactArgs a)
 {
+	constexpr int NW = FUSED ? GUF_WAVES : GU_WAVES;
 	using Block = typename BlockOf<TYPE>::type;
 	extern __shared__ float part[]; // [mats][nb][pg_cap][64]
-	__shared__ InlineRoute R;
 	const int32_t *offsets = a.offsets, *pairs = a.pairs, *active = a.active;
-	if (!FUSED && a.inline_route) {
-		inline_route<GU_THREADS>(a, R);
-		offsets = R.offsets;
-		pairs = R.pairs;
-		active = R.active;
+	if constexpr (!FUSED) {
+		// the fused kernel never routes inline: no LDS reserved for it
+		__shared__ InlineRoute R;
+		if (a.inline_route) {
+			inline_route<GU_THREADS>(a, R);
+			offsets = R.offsets;
+			pairs = R.pairs;
+			active = R.active;
+		}
 	}
 	const int slot = blockIdx.y;
 	if (slot >= active[a.E])
@@ -452,20 +462,35 @@ __global__ __launch_bounds__(GU_THREADS) EXACT_OCC void exact_gu_kernel(ExactArg
 	for (int g0 = p0; g0 < p1; g0 += pg_cap) {
 		const int np = min(pg_cap, p1 - g0);
 		const int32_t *gp = pairs + g0;
-		for (int t = w; t < nmat * nb; t += GU_WAVES) {
-			const int mi = t / nb, b = t - mi * nb, m = m0 + mi;
-			const uint8_t *panel = a.w[m] + (size_t)e * a.expert_bytes[m] + ((size_t)rt * nb + b) * pb;
-			Block blk;
-			load_block(panel, lane, blk);
+		const int ntask = nmat * nb;
+		auto panel_of = [&](int t) {
+			const int mi = t / nb, b = t - mi * nb;
+			return a.w[m0 + mi] + (size_t)e * a.expert_bytes[m0 + mi] + ((size_t)rt * nb + b) * pb;
+		};
+		Block blk;
+		if (TIE_GU_PREFETCH && w < ntask)
+			load_block(panel_of(w), lane, blk);
+		for (int t = w; t < ntask; t += NW) {
+			const int b = t % nb;
+			Block nxt;
+			if (TIE_GU_PREFETCH) {
+				// the next task's block is in flight while this one computes
+				if (t + NW < ntask)
+					load_block(panel_of(t + NW), lane, nxt);
+			} else {
+				load_block(panel_of(t), lane, blk);
+			}
 			auto xrow_b = [&](int q) {
 				const int pair = __builtin_amdgcn_readfirstlane(gp[q]);
 				return (cfloat *)(x + (size_t)(pair / k) * in + QK * b);
 			};
 			block_all_pairs<Block, cfloat>(blk, np, xrow_b, part + (size_t)t * pg_cap * 64, lane);
+			if (TIE_GU_PREFETCH)
+				blk = nxt;
 		}
 		__syncthreads();
 		// serial sums over super-blocks (math_avx2.c:762-766)
-		for (int i = threadIdx.x; i < np * 64; i += GU_THREADS) {
+		for (int i = threadIdx.x; i < np * 64; i += 64 * NW) {
 			const int q = i >> 6, r = i & 63;
 			const size_t o = (size_t)gp[q] * a.rows + rt * PANEL_ROWS + r;
 			float s0 = 0.0f;
@@ -676,12 +701,16 @@ static hipError_t launch_gu_q(int type, bool fused, int nmat, int rows, int in, 
 {
 	const int nb = in / QK;
 	const int mats = fused ? 2 : 1;
+	// small pair groups: the LDS of a workgroup stays small enough for
+	// several workgroups per CU (experts with more pairs run more groups)
 	g.pg_cap = clamp_pg(PART_FLOATS / (mats * nb * 64));
+	if (g.pg_cap > TIE_GU_PG)
+		g.pg_cap = TIE_GU_PG;
 	g.rows = rows;
 	g.in = in;
 	const size_t lds = sizeof(float) * (size_t)mats * nb * g.pg_cap * 64;
-	const dim3 grid(rows / PANEL_ROWS, max_active, fused ? 1 : nmat), block(GU_THREADS);
-	const size_t st = sizeof(InlineRoute);
+	const dim3 grid(rows / PANEL_ROWS, max_active, fused ? 1 : nmat), block(64 * (fused ? GUF_WAVES : GU_WAVES));
+	const size_t st = fused ? 0 : sizeof(InlineRoute);
 	if (type == TIE_GGML_Q4_K)
 		return fused ? launch_q(exact_gu_kernel<TIE_GGML_Q4_K, true>, grid, block, lds, st, s, g)
 			     : launch_q(exact_gu_kernel<TIE_GGML_Q4_K, false>, grid, block, lds, st, s, g);
