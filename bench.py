@@ -281,7 +281,7 @@ def main():
     tie_amd.init(0)
     flags = {"auto": tie_amd.PATH_AUTO, "exact": tie_amd.PATH_EXACT, "mfma": tie_amd.PATH_MFMA}[args.path]
 
-    names = [args.config] + [c for c in args.extra.split(",") if c and c != args.config]
+    names = [args.config] + [c for c in args.extra.split(",") if c and c not in (args.config, "none")]
     workloads = {}
     results = {}
     for name in names:
