@@ -365,12 +365,13 @@ static int forward(tie_hip_layer *layer, const float *x, int T, int k, float *ou
 		HIP_TRY(launch_dispatch(L, T, k, ws.topk_idx, ws, s));
 		prof_end(s);
 		HIP_TRY(launch_mfma_experts(L, x, T, k, g.silu, ws, s));
+		prof_begin("combine", s);
+		HIP_TRY(launch_combine(T, L.d, k, ws.topk_w, ws.topk_idx, ws.y, out, s));
+		prof_end(s);
 	} else {
-		HIP_TRY(launch_exact_block(L, x, T, k, g.silu, ws, s));
+		// routing, experts and the combine
+		HIP_TRY(launch_exact_block(L, x, T, k, g.silu, ws, out, s));
 	}
-	prof_begin("combine", s);
-	HIP_TRY(launch_combine(T, L.d, k, ws.topk_w, ws.topk_idx, ws.y, out, s));
-	prof_end(s);
 	if (idx_out)
 		HIP_TRY(hipMemcpyAsync(idx_out, ws.topk_idx, (size_t)T * k * 4, hipMemcpyDeviceToDevice, s));
 	if (w_out)

@@ -89,7 +89,7 @@ hipError_t launch_router_transpose(const Layer &L, hipStream_t s);
 hipError_t launch_dispatch(const Layer &L, int T, int k, const int32_t *topk_idx, Workspace &ws, hipStream_t s);
 hipError_t launch_route_group(const Layer &L, int T, int k, const float *logits, Workspace &ws, hipStream_t s);
 hipError_t launch_exact_block(const Layer &L, const float *x, int T, int k, const float *silu, Workspace &ws,
-			      hipStream_t s);
+			      float *out, hipStream_t s);
 hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, const float *silu, Workspace &ws,
 			       hipStream_t s);
 int mfma_max_tiles(int npairs, int E);

@@ -372,11 +372,13 @@ struct ExactArgs {
 	int32_t *offsets, *pairs, *active; // grouping (global)
 	int pg_cap;           // pairs per LDS group
 	int inline_route;
+	int single;           // T = 1 mode: slot j = pair j of expert topk_idx[j], no grouping
 };
 
 // Selection and grouping of all T <= INLINE_T tokens by one workgroup of NT
 // threads (E <= INLINE_E <= NT); workgroup (0,0,0) also publishes them for
-// the later kernels.  Results land in the LDS arrays of `R`.
+// the later kernels.  Results land in the LDS arrays of `R`.  With T = 1
+// there is no grouping: slot j of the token is a group of its own.
 struct InlineRoute {
 	float lg[INLINE_T * INLINE_E];
 	float sel[INLINE_T * MAX_K];
@@ -405,6 +407,18 @@ template <int NT> __device__ __forceinline__ void inline_route(const ExactArgs &
 		topk_softmax_group8(R.lg + t * E, E, k, R.sel + t * MAX_K, R.etab, R.idx + t * k, R.w + t * k);
 	}
 	__syncthreads();
+	if (a.single) {
+		// one token: slot j is its own group (expert idx[j], pair j); the
+		// later kernels of this mode read only the selection
+		if (tid < k)
+			R.pairs[tid] = tid;
+		if (blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 && tid < k) {
+			a.topk_idx[tid] = R.idx[tid];
+			a.topk_w[tid] = R.w[tid];
+		}
+		__syncthreads();
+		return;
+	}
 	group_pairs<NT>(R.idx, T * k, E, R.cnt, R.cur, R.wsum, R.offsets, R.pairs, R.active, nullptr, nullptr,
 			nullptr);
 	if (blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0) {
@@ -433,6 +447,7 @@ __global__ __launch_bounds__(GU_THREADS) GU_OCC void exact_gu_kernel(ExactArgs a
 	using Block = typename BlockOf<TYPE>::type;
 	extern __shared__ float part[]; // [mats][nb][pg_cap][64]
 	const int32_t *offsets = a.offsets, *pairs = a.pairs, *active = a.active;
+	const int32_t *sel_idx = nullptr;
 	if constexpr (!FUSED) {
 		// the fused kernel never routes inline: no LDS reserved for it
 		__shared__ InlineRoute R;
@@ -441,13 +456,26 @@ __global__ __launch_bounds__(GU_THREADS) GU_OCC void exact_gu_kernel(ExactArgs a
 			offsets = R.offsets;
 			pairs = R.pairs;
 			active = R.active;
+			sel_idx = R.idx;
 		}
 	}
+	auto single_expert = [&](const ExactArgs &, const int32_t *, int j) { return j < a.k ? sel_idx[j] : -1; };
 	const int slot = blockIdx.y;
-	if (slot >= active[a.E])
-		return;
-	const int e = active[slot];
-	const int p0 = offsets[e], p1 = offsets[e + 1];
+	int e, p0, p1;
+	if (!FUSED && a.single) {
+		// one token: the slot's selected expert, the slot's own pair
+		e = __builtin_amdgcn_readfirstlane(single_expert(a, pairs, slot));
+		if (e < 0)
+			return;
+		p0 = slot;
+		p1 = slot + 1;
+	} else {
+		if (slot >= active[a.E])
+			return;
+		e = active[slot];
+		p0 = offsets[e];
+		p1 = offsets[e + 1];
+	}
 	const int rt = blockIdx.x;
 	const int lane = threadIdx.x & 63;
 	const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -578,10 +606,23 @@ __global__ __launch_bounds__(512) EXACT_OCC void exact_down_kernel(ExactArgs a)
 	using Block = typename BlockOf<TYPE>::type;
 	extern __shared__ float lds[];
 	const int slot = blockIdx.y;
-	if (slot >= a.active[a.E])
-		return;
-	const int e = a.active[slot];
-	const int p0 = a.offsets[e], p1 = a.offsets[e + 1];
+	int e, p0, p1;
+	const int32_t *pairs = a.pairs;
+	if (a.single) {
+		// one token: the slot's selected expert and its own pair
+		e = slot < a.k ? a.topk_idx[slot] : -1;
+		if (e < 0)
+			return;
+		p0 = slot;
+		p1 = slot + 1;
+		pairs = nullptr;
+	} else {
+		if (slot >= a.active[a.E])
+			return;
+		e = a.active[slot];
+		p0 = a.offsets[e];
+		p1 = a.offsets[e + 1];
+	}
 	const int rt = blockIdx.x;
 	const int lane = threadIdx.x & 63;
 	const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -593,9 +634,15 @@ __global__ __launch_bounds__(512) EXACT_OCC void exact_down_kernel(ExactArgs a)
 	float *hs = lds;
 	float *part = HG ? lds : lds + (size_t)pg_cap * F;
 
+	// single mode: the group is the slot's own pair, listed in LDS
+	__shared__ int32_t own_pair[1];
+	if (!pairs) {
+		own_pair[0] = p0;
+		__syncthreads();
+	}
 	for (int g0 = p0; g0 < p1; g0 += pg_cap) {
 		const int np = min(pg_cap, p1 - g0);
-		const int32_t *gp = a.pairs + g0;
+		const int32_t *gp = pairs ? pairs + g0 : own_pair;
 		if (!HG) {
 			stage_h(a, gp, np, hs);
 			__syncthreads();
@@ -722,7 +769,7 @@ static hipError_t launch_gu_q(int type, bool fused, int nmat, int rows, int in, 
 // path.  ws.h holds two [pairs][F] planes: the gate and the up row sums, or
 // (fused gate/up) h in the first.
 hipError_t launch_exact_block(const Layer &L, const float *x, int T, int k, const float *silu, Workspace &ws,
-			      hipStream_t s)
+			      float *out, hipStream_t s)
 {
 	const int npairs = T * k;
 	if (npairs == 0)
@@ -741,6 +788,8 @@ hipError_t launch_exact_block(const Layer &L, const float *x, int T, int k, cons
 	// h formed in the down prologue.  Otherwise one workgroup per panel runs
 	// both and writes h, which the down kernel reads through scalar loads.
 	const bool fused = !inl && same && quant && L.down.type != TIE_GGML_BF16;
+	// one token: slot j is pair j of expert topk_idx[j]; no grouping
+	const bool single = T == 1 && inl && quant && L.down.type != TIE_GGML_BF16;
 	if (!inl) {
 		prof_begin("route_group", s);
 		if (npairs <= 4096)
@@ -772,6 +821,7 @@ hipError_t launch_exact_block(const Layer &L, const float *x, int T, int k, cons
 	a.pairs = ws.pairs;
 	a.active = ws.active;
 	a.inline_route = inl ? 1 : 0;
+	a.single = single ? 1 : 0;
 
 	prof_begin("exact_gate_up", s);
 	{
@@ -843,6 +893,11 @@ hipError_t launch_exact_block(const Layer &L, const float *x, int T, int k, cons
 			}
 		}
 	}
+	prof_end(s);
+	if (err != hipSuccess)
+		return err;
+	prof_begin("combine", s);
+	err = launch_combine(T, L.d, k, ws.topk_w, ws.topk_idx, ws.y, out, s);
 	prof_end(s);
 	return err;
 }
