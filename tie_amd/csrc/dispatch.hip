@@ -31,7 +31,8 @@ __global__ __launch_bounds__(DSP_THREADS) void dispatch_kernel(const int32_t *__
 							       int32_t *__restrict__ tile_m0,
 							       int32_t *__restrict__ ntiles)
 {
-	__shared__ int32_t cnt[MAX_E], cur[MAX_E];
+	__shared__ __attribute__((aligned(16))) int32_t cnt[MAX_E];
+	__shared__ int32_t cur[MAX_E];
 	__shared__ int wsum[DSP_THREADS / 64];
 	group_pairs<DSP_THREADS>(topk_idx, npairs, E, cnt, cur, wsum, offsets, pairs, active, tile_e, tile_m0, ntiles);
 }
@@ -55,11 +56,13 @@ __global__ __launch_bounds__(DSP_THREADS) void route_group_kernel(const float *_
 								  int32_t *__restrict__ pairs,
 								  int32_t *__restrict__ active)
 {
-	__shared__ int32_t cnt[MAX_E], cur[MAX_E];
+	__shared__ __attribute__((aligned(16))) int32_t cnt[MAX_E];
+	__shared__ int32_t cur[MAX_E];
 	__shared__ int wsum[DSP_THREADS / 64];
 	__shared__ float sel[(DSP_THREADS / 8) * MAX_K];
 	__shared__ uint64_t etab[32];
 	__shared__ int32_t sidx[RG_MAX_PAIRS];
+	__shared__ int lpt[2 * LPT_BINS];
 	const int tid = threadIdx.x;
 	if (tid < 32) {
 		const uint64_t tab[32] = TIE_EXP2_TABLE;
@@ -81,7 +84,8 @@ __global__ __launch_bounds__(DSP_THREADS) void route_group_kernel(const float *_
 	const int npairs = T * k;
 	for (int p = tid; p < npairs; p += DSP_THREADS)
 		topk_idx[p] = sidx[p];
-	group_pairs<DSP_THREADS>(sidx, npairs, E, cnt, cur, wsum, offsets, pairs, active, nullptr, nullptr, nullptr);
+	group_pairs<DSP_THREADS>(sidx, npairs, E, cnt, cur, wsum, offsets, pairs, active, nullptr, nullptr, nullptr,
+				 lpt);
 }
 
 hipError_t launch_route_group(const Layer &L, int T, int k, const float *logits, Workspace &ws, hipStream_t s)

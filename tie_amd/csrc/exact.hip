@@ -379,12 +379,13 @@ struct ExactArgs {
 // threads (E <= INLINE_E <= NT); workgroup (0,0,0) also publishes them for
 // the later kernels.  Results land in the LDS arrays of `R`.  With T = 1
 // there is no grouping: slot j of the token is a group of its own.
-struct InlineRoute {
+struct alignas(16) InlineRoute {
 	float lg[INLINE_T * INLINE_E];
 	float sel[INLINE_T * MAX_K];
 	float w[INLINE_T * MAX_K];
 	int32_t idx[INLINE_T * MAX_K];
-	int32_t cnt[INLINE_E], cur[INLINE_E];
+	alignas(16) int32_t cnt[INLINE_E];
+	int32_t cur[INLINE_E];
 	int32_t offsets[INLINE_E + 1], active[INLINE_E + 1];
 	int32_t pairs[INLINE_T * MAX_K];
 	int wsum[16];
@@ -419,6 +420,8 @@ template <int NT> __device__ __forceinline__ void inline_route(const ExactArgs &
 		__syncthreads();
 		return;
 	}
+	// every workgroup groups on its own and must reach the same expert order:
+	// ascending expert index (the count order breaks ties by LDS atomics)
 	group_pairs<NT>(R.idx, T * k, E, R.cnt, R.cur, R.wsum, R.offsets, R.pairs, R.active, nullptr, nullptr,
 			nullptr);
 	if (blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0) {

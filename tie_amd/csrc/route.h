@@ -7,6 +7,8 @@
 
 namespace tie {
 
+constexpr int LPT_BINS = 256; // pair-count buckets of the launch order
+
 // top-k (engine.c:891-914 semantics) + softmax (engine.c:864-888) for one
 // token, by one wave.  `lg` holds the token's E logits.  The k winners are
 // extracted one at a time by a wave-wide argmax under the order (value
@@ -231,8 +233,9 @@ template <int NT> __device__ __forceinline__ int block_exclusive_scan(int v, int
 // Writes offsets[0..E] (exclusive prefix sum of the per-expert counts;
 // offsets[E] = valid pairs), pairs[] (pair ids grouped by expert; the order
 // inside an expert is not fixed: every pair is computed on its own row, so
-// results do not depend on it) and active[0..E] (experts with pairs, in
-// ascending order; active[E] = their number).  With tile_e non-null it
+// results do not depend on it) and active[0..E] (experts with pairs, by
+// descending pair count with lpt -- ties in any order --, else ascending;
+// active[E] = their number).  With tile_e non-null it
 // also writes the MFMA work list: each active expert's pairs split evenly
 // over ceil(count / MFMA_MT) tiles.  cnt / cur: LDS scratch of E ints
 // each; wsum: LDS scratch of NT/64 ints.  Output pointers may be LDS or
@@ -240,7 +243,7 @@ template <int NT> __device__ __forceinline__ int block_exclusive_scan(int v, int
 template <int NT>
 __device__ __forceinline__ void group_pairs(const int32_t *idx, int npairs, int E, int32_t *cnt, int32_t *cur,
 					    int *wsum, int32_t *offsets, int32_t *pairs, int32_t *active,
-					    int32_t *tile_e, int32_t *tile_m0, int32_t *ntiles)
+					    int32_t *tile_e, int32_t *tile_m0, int32_t *ntiles, int *lpt = nullptr)
 {
 	const int tid = threadIdx.x;
 	for (int e = tid; e < E; e += NT)
@@ -257,11 +260,39 @@ __device__ __forceinline__ void group_pairs(const int32_t *idx, int npairs, int 
 	int total, nact;
 	const int off = block_exclusive_scan<NT>(c, wsum, total);
 	const int aidx = block_exclusive_scan<NT>(c > 0 ? 1 : 0, wsum, nact);
+	// lpt (LDS scratch of 2 * LPT_BINS ints, or null): active experts
+	// ordered by pair count, largest first, ties in no fixed order (so only
+	// for a grouping made once and shared by all readers): the expert
+	// kernels launch one workgroup per active slot in this order, so the
+	// longest workgroups start first.  Otherwise ascending expert index.
+	int rank = aidx;
+	if (lpt) {
+		// bucket the experts by pair count (larger counts first; counts past
+		// the last bucket share it), then take slots inside a bucket by an
+		// LDS atomic: that order only decides which workgroup launches
+		// first, never a result
+		constexpr int NBIN = NT < LPT_BINS ? NT : LPT_BINS;
+		int *lpt_hist = lpt, *lpt_cur = lpt + NBIN;
+		for (int i = tid; i < NBIN; i += NT)
+			lpt_hist[i] = 0;
+		__syncthreads();
+		const int bin = NBIN - 1 - (c < NBIN - 1 ? c : NBIN - 1);
+		if (e < E && c > 0)
+			atomicAdd(&lpt_hist[bin], 1);
+		__syncthreads();
+		int nb_tot;
+		const int base = block_exclusive_scan<NT>(tid < NBIN ? lpt_hist[tid] : 0, wsum, nb_tot);
+		if (tid < NBIN)
+			lpt_cur[tid] = base;
+		__syncthreads();
+		if (e < E && c > 0)
+			rank = atomicAdd(&lpt_cur[bin], 1);
+	}
 	if (e < E) {
 		offsets[e] = off;
 		cur[e] = off;
 		if (c > 0)
-			active[aidx] = e;
+			active[rank] = e;
 	}
 	if (tile_e) {
 		int ntot;
