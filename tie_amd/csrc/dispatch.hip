@@ -23,6 +23,7 @@ constexpr int DSP_THREADS = 1024;
 
 // One workgroup groups all pairs (group_pairs) and writes the MFMA work
 // list.
+constexpr int DSP_STAGE_MAX = 16384; // pairs staged in LDS at most (selections + list: 128 KiB)
 __global__ __launch_bounds__(DSP_THREADS) void dispatch_kernel(const int32_t *__restrict__ topk_idx, int npairs,
 							       int E, int32_t *__restrict__ offsets,
 							       int32_t *__restrict__ pairs,
@@ -31,15 +32,50 @@ __global__ __launch_bounds__(DSP_THREADS) void dispatch_kernel(const int32_t *__
 							       int32_t *__restrict__ tile_m0,
 							       int32_t *__restrict__ ntiles)
 {
+	extern __shared__ __attribute__((aligned(16))) int32_t sidx[];
 	__shared__ __attribute__((aligned(16))) int32_t cnt[MAX_E];
 	__shared__ int32_t cur[MAX_E];
 	__shared__ int wsum[DSP_THREADS / 64];
-	group_pairs<DSP_THREADS>(topk_idx, npairs, E, cnt, cur, wsum, offsets, pairs, active, tile_e, tile_m0, ntiles);
+	if (npairs > DSP_STAGE_MAX) {
+		group_pairs<DSP_THREADS>(topk_idx, npairs, E, cnt, cur, wsum, offsets, pairs, active, tile_e, tile_m0,
+					 ntiles);
+		return;
+	}
+	// selections in, pair list out, both through LDS: the scattered
+	// placement stores hit LDS, and global memory sees only coalesced
+	// 16-byte loads and stores
+	int32_t *spairs = sidx + ((npairs + 3) & ~3);
+	const int n4 = npairs >> 2;
+	for (int i = threadIdx.x; i < n4; i += DSP_THREADS)
+		reinterpret_cast<int4 *>(sidx)[i] = reinterpret_cast<const int4 *>(topk_idx)[i];
+	for (int i = 4 * n4 + threadIdx.x; i < npairs; i += DSP_THREADS)
+		sidx[i] = topk_idx[i];
+	__syncthreads();
+	// pairs[0 .. valid): experts' lists back to back (the invalid selections,
+	// if any, were not placed)
+	const int valid =
+		group_pairs<DSP_THREADS>(sidx, npairs, E, cnt, cur, wsum, offsets, spairs, active, tile_e, tile_m0, ntiles);
+	const int v4 = valid >> 2;
+	for (int i = threadIdx.x; i < v4; i += DSP_THREADS)
+		reinterpret_cast<int4 *>(pairs)[i] = reinterpret_cast<const int4 *>(spairs)[i];
+	for (int i = 4 * v4 + threadIdx.x; i < valid; i += DSP_THREADS)
+		pairs[i] = spairs[i];
 }
 
 hipError_t launch_dispatch(const Layer &L, int T, int k, const int32_t *topk_idx, Workspace &ws, hipStream_t s)
 {
-	hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(DSP_THREADS), 0, s, topk_idx, T * k, L.E, ws.offsets,
+	const int npairs = T * k;
+	const size_t lds = npairs <= DSP_STAGE_MAX ? sizeof(int32_t) * 2 * (size_t)((npairs + 3) & ~3) : 0;
+	static bool attr = false;
+	if (!attr) {
+		const hipError_t err = hipFuncSetAttribute((const void *)dispatch_kernel,
+							   hipFuncAttributeMaxDynamicSharedMemorySize,
+							   (int)(sizeof(int32_t) * 2 * DSP_STAGE_MAX));
+		if (err != hipSuccess)
+			return err;
+		attr = true;
+	}
+	hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(DSP_THREADS), lds, s, topk_idx, npairs, L.E, ws.offsets,
 			   ws.pairs, ws.active, ws.tile_e, ws.tile_m0, ws.ntiles);
 	return hipGetLastError();
 }

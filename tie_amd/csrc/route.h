@@ -229,7 +229,7 @@ template <int NT> __device__ __forceinline__ int block_exclusive_scan(int v, int
 }
 
 // Groups the pairs p = t*k + j by expert, by one workgroup of NT >= E
-// threads.  `idx` holds the selected expert of every pair (-1: none).
+// threads, and returns the number of valid pairs.  `idx` holds the selected expert of every pair (-1: none).
 // Writes offsets[0..E] (exclusive prefix sum of the per-expert counts;
 // offsets[E] = valid pairs), pairs[] (pair ids grouped by expert; the order
 // inside an expert is not fixed: every pair is computed on its own row, so
@@ -241,7 +241,7 @@ template <int NT> __device__ __forceinline__ int block_exclusive_scan(int v, int
 // each; wsum: LDS scratch of NT/64 ints.  Output pointers may be LDS or
 // global memory.
 template <int NT>
-__device__ __forceinline__ void group_pairs(const int32_t *idx, int npairs, int E, int32_t *cnt, int32_t *cur,
+__device__ __forceinline__ int group_pairs(const int32_t *idx, int npairs, int E, int32_t *cnt, int32_t *cur,
 					    int *wsum, int32_t *offsets, int32_t *pairs, int32_t *active,
 					    int32_t *tile_e, int32_t *tile_m0, int32_t *ntiles, int *lpt = nullptr)
 {
@@ -319,6 +319,7 @@ __device__ __forceinline__ void group_pairs(const int32_t *idx, int npairs, int 
 			pairs[atomicAdd(&cur[ex], 1)] = p;
 	}
 	__syncthreads();
+	return total;
 }
 
 } // namespace tie

@@ -229,7 +229,10 @@ __global__ __launch_bounds__(RT_THREADS) void router_logits_kernel(const float *
 
 // ------------------------------------------------------------ router_topk
 // 32 tokens per workgroup, 8 lanes per token (E <= 128).
-constexpr int RK_TOK = 32, RK_THREADS = 8 * RK_TOK;
+#ifndef TIE_RK_TOK
+#define TIE_RK_TOK 32
+#endif
+constexpr int RK_TOK = TIE_RK_TOK, RK_THREADS = 8 * RK_TOK;
 
 __global__ __launch_bounds__(RK_THREADS) void router_topk_kernel(const float *__restrict__ logits, int T, int E,
 								 int k, int32_t *__restrict__ topk_idx,
