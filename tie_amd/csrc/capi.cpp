@@ -200,7 +200,7 @@ static int ensure_workspace(int T, int k, int d, int F, int E)
 		     o_hb = take(P * FF * 2), o_y = take(P * DD * 4), o_xb = take(Tcap * DD * 2),
 		     o_hlo = take(P * FF * 2), o_xlo = take(Tcap * DD * 2);
 	const size_t max_tiles = (size_t)mfma_max_tiles((int)P, (int)EE);
-	const size_t o_te = take(max_tiles * 4), o_tm = take(max_tiles * 4), o_nt = take(4);
+	const size_t o_te = take(2 * max_tiles * 4), o_tm = take(2 * max_tiles * 4), o_nt = take(8);
 	void *mem = nullptr;
 	if (w.alloc) {
 		HIP_TRY(hipStreamSynchronize(g.stream));
@@ -227,6 +227,7 @@ static int ensure_workspace(int T, int k, int d, int F, int E)
 	w.tile_e = (int32_t *)(b + o_te);
 	w.tile_m0 = (int32_t *)(b + o_tm);
 	w.ntiles = (int32_t *)(b + o_nt);
+	w.tile_cap = (int32_t)max_tiles;
 	w.cap_pairs = P;
 	w.cap_F = FF;
 	w.cap_d = DD;

@@ -19,7 +19,17 @@ constexpr size_t Q6K_PANEL = (size_t)PANEL_ROWS * Q6K_BYTES; // 13440
 constexpr int MAX_K = 32;
 constexpr int MAX_E = 1024;
 constexpr int SILU_N = TIE_SILU_TABLE_SIZE;
-constexpr int MFMA_MT = 192; // pair rows per MFMA work tile at most
+// MFMA work tiles: pair rows of one expert per tile at most, gate/up and
+// down (each kernel has its own tile list; MFMA_MT is the larger)
+#ifndef TIE_MFMA_MT_GU
+#define TIE_MFMA_MT_GU 160
+#endif
+#ifndef TIE_MFMA_MT_DN
+#define TIE_MFMA_MT_DN 192
+#endif
+constexpr int MFMA_MT_GU = TIE_MFMA_MT_GU;
+constexpr int MFMA_MT_DN = TIE_MFMA_MT_DN;
+constexpr int MFMA_MT = MFMA_MT_GU > MFMA_MT_DN ? MFMA_MT_GU : MFMA_MT_DN;
 
 // Device layout of one stacked expert tensor [E][rows][in].
 //
@@ -72,9 +82,10 @@ struct Workspace {
 	uint16_t *hlo = nullptr;      // [T*k][F] SwiGLU activations, bf16 remainder (MFMA path, BF16 weights)
 	uint16_t *xb = nullptr;       // [T][d]   x as bf16 (MFMA path)
 	uint16_t *xlo = nullptr;      // [T][d]   x - bf16(x) as bf16 (MFMA path, BF16 weights)
-	int32_t *tile_e = nullptr;    // [max tiles] MFMA work list: expert of each MFMA_MT-pair tile
-	int32_t *tile_m0 = nullptr;   // [max tiles] first pair of the tile within the expert
-	int32_t *ntiles = nullptr;    // [1]
+	int32_t *tile_e = nullptr;    // [2][max tiles] MFMA work lists (gate/up, down): expert of each tile
+	int32_t *tile_m0 = nullptr;   // [2][max tiles] first pair of the tile within the expert
+	int32_t *ntiles = nullptr;    // [2]
+	int32_t tile_cap = 0;         // max tiles per list
 	size_t cap_pairs = 0, cap_F = 0, cap_d = 0, cap_E = 0;
 	void *alloc = nullptr;
 };
@@ -92,7 +103,7 @@ hipError_t launch_exact_block(const Layer &L, const float *x, int T, int k, cons
 			      float *out, hipStream_t s);
 hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, const float *silu, Workspace &ws,
 			       hipStream_t s);
-int mfma_max_tiles(int npairs, int E);
+int mfma_max_tiles(int npairs, int E); // per list
 hipError_t launch_combine(int T, int d, int k, const float *topk_w, const int32_t *topk_idx, const float *y,
 			  float *out, hipStream_t s);
 hipError_t launch_repack(const ExpertTensor &dst, const uint8_t *src, int E, int literal_bf16_stride, hipStream_t s);

@@ -56,7 +56,17 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int MT = MFMA_MT;   // pair rows per work tile at most (192)
+// Q4_K K per stage (64: one 64-weight group), and waves per SIMD of the
+// gate/up and down kernels
+#ifndef TIE_Q4K_KST
+#define TIE_Q4K_KST 64
+#endif
+#ifndef TIE_MFMA_GU_WPE
+#define TIE_MFMA_GU_WPE 2
+#endif
+#ifndef TIE_MFMA_DN_WPE
+#define TIE_MFMA_DN_WPE 1
+#endif
 constexpr int NWAVES = 4;
 constexpr int MF_THREADS = 64 * NWAVES;
 constexpr int GU_COLS = 32 * NWAVES; // gate/up: F columns per tile (128)
@@ -94,9 +104,12 @@ struct MfmaArgs {
 	float *y;                // down out [pair][d]
 };
 
-template <int TYPE> struct Cfg {
+template <int TYPE, bool DOWN = false> struct Cfg {
+	static constexpr int MT = DOWN ? MFMA_MT_DN : MFMA_MT_GU; // pair rows per work tile at most
 	static constexpr bool SPLIT = TYPE == TIE_GGML_BF16; // bf16 weights take activations as hi + lo planes
-	static constexpr int KST = SPLIT ? 64 : 128;         // K per stage
+	// K per stage (Q4_K optionally 64: one 64-weight group per stage)
+	static constexpr int KST = SPLIT ? 64 : (TYPE == TIE_GGML_Q4_K && TIE_Q4K_KST == 64 ? 64 : 128);
+	static constexpr int SPB = QK / KST;                 // stages per 256-weight block (quantised)
 	static constexpr int NPL = SPLIT ? 2 : 1;            // activation planes
 	static constexpr int RB = KST * 2;                   // bytes per A row, plane and stage
 	static constexpr int CPR = RB / 16;                  // 16-byte slots per row
@@ -109,14 +122,14 @@ template <int TYPE> struct Cfg {
 	// stage, by direct loads): no registers hold the next stage's weights.
 	// BF16 weights are prefetched into registers.
 	static constexpr bool B_LDS = !SPLIT;
-	static constexpr int NCH = TYPE == TIE_GGML_Q4_K ? 5 : 7; // 1 KiB chunks per panel and stage
+	static constexpr int NCH = TYPE == TIE_GGML_Q4_K ? 1 + KST / 32 : 7; // 1 KiB chunks per panel and stage
 	static constexpr int PB = NCH * 1024;                     // bytes per panel and stage
 	static constexpr int BBUF = B_LDS ? 4 * PB + (TYPE == TIE_GGML_Q6_K ? 4 * 128 : 0) : 0; // + Q6_K d planes
 	static constexpr int LDS_A = 2 * ABUF, LDS_B = 2 * BBUF;
 	// The slot of 16-byte chunk c of row r is c ^ swz(r): the rows of a
 	// fragment read then spread over all LDS banks without row padding
 	// (which the direct global->LDS loads cannot make).
-	__device__ static int swz(int r) { return SPLIT ? (r >> 1) & 7 : r & 15; }
+	__device__ static int swz(int r) { return CPR == 8 ? (r >> 1) & 7 : r & 15; }
 };
 
 // ------------------------------------------------------------------ B registers
@@ -194,12 +207,12 @@ template <int TYPE, bool DOWN>
 __device__ __forceinline__ void dma_b(const MfmaArgs &a, int e, int slab, int st, int w, uint8_t *B)
 {
 	using C = Cfg<TYPE>;
-	const int lane = threadIdx.x & 63, half = st & 1;
+	const int lane = threadIdx.x & 63, half = st & 1, part = st % C::SPB;
 	const size_t pbytes = panel_bytes(TYPE);
 	auto panel = [&](int p) {
 		const int mat = DOWN ? 0 : p >> 1;
 		const int rt = DOWN ? 4 * slab + p : 2 * slab + (p & 1);
-		return a.w[mat] + (size_t)e * a.expert_bytes[mat] + ((size_t)rt * (a.in / QK) + (st >> 1)) * pbytes;
+		return a.w[mat] + (size_t)e * a.expert_bytes[mat] + ((size_t)rt * (a.in / QK) + st / C::SPB) * pbytes;
 	};
 #pragma unroll
 	for (int c = 0; c < C::NCH; c++) {
@@ -207,7 +220,7 @@ __device__ __forceinline__ void dma_b(const MfmaArgs &a, int e, int slab, int st
 		const int p = it / C::NCH, s = it % C::NCH;
 		int chunk;
 		if constexpr (TYPE == TIE_GGML_Q4_K)
-			chunk = s == 0 ? 0 : 4 * half + s;
+			chunk = s == 0 ? 0 : (C::NCH - 1) * part + s;
 		else
 			chunk = s < 4 ? 4 * half + s : (s < 6 ? 8 + 2 * half + (s - 4) : 12);
 		dma16(panel(p) + chunk * 1024 + 16 * lane, __builtin_amdgcn_readfirstlane(lds_addr(B + p * C::PB + s * 1024)));
@@ -230,7 +243,7 @@ __device__ __forceinline__ void lds_b(const uint8_t *B, const int p[2], const in
 		const uint8_t *pb = B + p[j] * C::PB + i[j] * 16;
 		if constexpr (TYPE == TIE_GGML_Q4_K) {
 #pragma unroll
-			for (int q = 0; q < 4; q++)
+			for (int q = 0; q < C::NCH - 1; q++)
 				b.q[j][q] = *reinterpret_cast<const u32x2 *>(pb + (1 + q) * 1024 + 8 * h);
 			b.sc[j] = *reinterpret_cast<const u32x4 *>(pb);
 		} else if constexpr (TYPE == TIE_GGML_Q6_K) {
@@ -290,7 +303,7 @@ __device__ __forceinline__ void group_factors(const BRegs<TYPE> &b, int st, int 
 #pragma unroll
 	for (int j = 0; j < 2; j++) {
 		if constexpr (TYPE == TIE_GGML_Q4_K) {
-			const int g = 2 * (st & 1) + gi;
+			const int g = (4 / Cfg<TYPE>::SPB) * (st % Cfg<TYPE>::SPB) + gi;
 			const float d = f16_to_f32(b.sc[j].x & 0xffffu), dmin = f16_to_f32(b.sc[j].x >> 16);
 #pragma unroll
 			for (int u = 0; u < 2; u++) {
@@ -369,10 +382,10 @@ __device__ __forceinline__ void dma16(const void *g, uint32_t lds)
 	asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
 }
 
-template <int TYPE>
+template <int TYPE, bool DOWN>
 __device__ __forceinline__ void dma_a(const ASrc &s, int st, int w, const uint8_t *buf)
 {
-	using C = Cfg<TYPE>;
+	using C = Cfg<TYPE, DOWN>;
 	const size_t ko = (size_t)st * C::RB;
 	uint32_t off[(C::NDMA + 3) / 4 * 4]; // whole 16-byte reads (the lane slot holds ROFF_STRIDE entries)
 	static_assert(C::NDMA <= ROFF_STRIDE, "row offset slot too small");
@@ -405,11 +418,11 @@ __device__ __forceinline__ void stage_barrier()
 // step s+1 are read from LDS and its B fragments dequantised while the
 // MFMAs of step s run (a single wave per SIMD: the MFMAs' 32-cycle issue
 // slots are where its VALU and LDS instructions go).
-template <int TYPE, int NMT>
+template <int TYPE, bool DOWN, int NMT>
 __device__ __forceinline__ void stage_mfma(const BRegs<TYPE> &b, int st, const uint8_t *__restrict__ A,
 					   f32x16 acc[6][2])
 {
-	using C = Cfg<TYPE>;
+	using C = Cfg<TYPE, DOWN>;
 	constexpr int NA = NMT * C::NPL; // fragments per step (hi [+ lo] per tile)
 	const int lane = threadIdx.x & 63;
 	// fragment row r = 32 mt + lane%32 (swz(r) = swz(lane%32)), chunk 2s + lane/32
@@ -452,7 +465,7 @@ template <int TYPE, bool DOWN, int NMT>
 __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_t *roff, int e, int pbase, int nrows,
 					 int slab)
 {
-	using C = Cfg<TYPE>;
+	using C = Cfg<TYPE, DOWN>;
 	const int nk = a.in / C::KST;
 	const int t = threadIdx.x;
 	const int w = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -466,7 +479,7 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 		as.base[1] = (const char *)a.a16lo + 16 * chunk;
 		// row r = RPI (NWAVES c + w') + rsub' is entry c of lane slot RPI w' + rsub'
 		as.roff = roff + (C::RPI * w + rsub) * ROFF_STRIDE;
-		if (t < MT) {
+		if (t < C::MT) {
 			const int r = t < nrows ? t : 0;
 			const int row = DOWN ? pbase + r : a.pairs[pbase + r] / a.k;
 			const int c = t / (C::RPI * NWAVES), ls = t % (C::RPI * NWAVES);
@@ -512,7 +525,7 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 		dma_b<TYPE, DOWN>(a, e, slab, 0, w, Bs);
 	else
 		load_b<TYPE>(bs, 0, h, b0);
-	dma_a<TYPE>(as, 0, w, As);
+	dma_a<TYPE, DOWN>(as, 0, w, As);
 	stage_barrier();
 
 	// stage st: the weights and activations of st+1 are fetched (into the
@@ -524,11 +537,11 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 				dma_b<TYPE, DOWN>(a, e, slab, st + 1, w, Bs + ((st + 1) & 1) * C::BBUF);
 			else
 				load_b<TYPE>(bs, st + 1, h, nxt);
-			dma_a<TYPE>(as, st + 1, w, As + ((st + 1) & 1) * C::ABUF);
+			dma_a<TYPE, DOWN>(as, st + 1, w, As + ((st + 1) & 1) * C::ABUF);
 		}
 		if constexpr (C::B_LDS)
 			lds_b<TYPE>(Bs + (st & 1) * C::BBUF, bp, bi, st, h, cur);
-		stage_mfma<TYPE, NMT>(cur, st, As + (st & 1) * C::ABUF, acc);
+		stage_mfma<TYPE, DOWN, NMT>(cur, st, As + (st & 1) * C::ABUF, acc);
 		stage_barrier();
 	};
 	if constexpr (C::B_LDS) {
@@ -584,12 +597,22 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 	}
 }
 
+// waves per SIMD: the quantised gate/up kernel keeps its LDS and registers
+// small enough for two workgroups per CU; the down and BF16 kernels use
+// larger tiles with one wave per SIMD
+constexpr int mf_wpe(int type, bool down)
+{
+	return down || type == TIE_GGML_BF16 ? TIE_MFMA_DN_WPE : TIE_MFMA_GU_WPE;
+}
+
 template <int TYPE, bool DOWN>
-__global__ __launch_bounds__(MF_THREADS) __attribute__((amdgpu_waves_per_eu(1, 1))) void
+__global__ __launch_bounds__(MF_THREADS) __attribute__((amdgpu_waves_per_eu(mf_wpe(TYPE, DOWN), mf_wpe(TYPE, DOWN)))) void
 mfma_experts_kernel(MfmaArgs a)
 {
+	using C = Cfg<TYPE, DOWN>;
+	constexpr int MT = C::MT, MT_TILES = C::MT / 32;
 	extern __shared__ __attribute__((aligned(16))) uint8_t As[]; // A [2][ABUF] | B [2][BBUF] | row offsets
-	uint32_t *roff = reinterpret_cast<uint32_t *>(As + Cfg<TYPE>::LDS_A + Cfg<TYPE>::LDS_B);
+	uint32_t *roff = reinterpret_cast<uint32_t *>(As + C::LDS_A + C::LDS_B);
 
 	// XCD-aware tile order.  Consecutive workgroup ids are spread round-robin
 	// over the 8 XCDs, each with its own L2.  The id is remapped so that each
@@ -625,10 +648,12 @@ mfma_experts_kernel(MfmaArgs a)
 		run_tile<TYPE, DOWN, 4>(a, As, roff, e, pbase, nrows, slab);
 		break;
 	case 5:
-		run_tile<TYPE, DOWN, 5>(a, As, roff, e, pbase, nrows, slab);
+		if constexpr (MT_TILES >= 5)
+			run_tile<TYPE, DOWN, (MT_TILES >= 5 ? 5 : 1)>(a, As, roff, e, pbase, nrows, slab);
 		break;
 	default:
-		run_tile<TYPE, DOWN, 6>(a, As, roff, e, pbase, nrows, slab);
+		if constexpr (MT_TILES >= 6)
+			run_tile<TYPE, DOWN, (MT_TILES >= 6 ? 6 : 1)>(a, As, roff, e, pbase, nrows, slab);
 	}
 }
 
@@ -657,7 +682,8 @@ template <int TYPE, bool DOWN>
 static hipError_t launch_type(const MfmaArgs &a, dim3 grid, hipStream_t s)
 {
 	// the double-buffered A tile exceeds the default 64 KiB of dynamic LDS
-	constexpr size_t lds = (size_t)Cfg<TYPE>::LDS_A + Cfg<TYPE>::LDS_B + 4 * (size_t)(Cfg<TYPE>::RPI * NWAVES * ROFF_STRIDE);
+	using C = Cfg<TYPE, DOWN>;
+	constexpr size_t lds = (size_t)C::LDS_A + C::LDS_B + 4 * (size_t)(C::RPI * NWAVES * ROFF_STRIDE);
 	static_assert(lds <= 160 * 1024, "LDS budget");
 	static bool attr = false;
 	if (!attr) {
@@ -683,7 +709,8 @@ static hipError_t launch_one(const MfmaArgs &a, int type, dim3 grid, hipStream_t
 
 int mfma_max_tiles(int npairs, int E)
 {
-	return (npairs + MT - 1) / MT + E;
+	constexpr int mt = MFMA_MT_GU < MFMA_MT_DN ? MFMA_MT_GU : MFMA_MT_DN;
+	return (npairs + mt - 1) / mt + E;
 }
 
 hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, const float *silu, Workspace &ws,
@@ -706,6 +733,7 @@ hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, con
 	a.k = k;
 	a.offsets = ws.offsets;
 	a.pairs = ws.pairs;
+	// gate/up tile list (list 0)
 	a.tile_e = ws.tile_e;
 	a.tile_m0 = ws.tile_m0;
 	a.ntiles = ws.ntiles;
@@ -738,6 +766,10 @@ hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, con
 		return err;
 
 	prof_begin("mfma_down", s);
+	// down tile list (list 1)
+	a.tile_e = ws.tile_e + ws.tile_cap;
+	a.tile_m0 = ws.tile_m0 + ws.tile_cap;
+	a.ntiles = ws.ntiles + 1;
 	a.w[0] = a.w[1] = L.down.data;
 	a.expert_bytes[0] = a.expert_bytes[1] = L.down.expert_bytes;
 	a.rows = L.d;
