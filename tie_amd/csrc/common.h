@@ -25,7 +25,7 @@ constexpr int SILU_N = TIE_SILU_TABLE_SIZE;
 #define TIE_MFMA_MT_GU 160
 #endif
 #ifndef TIE_MFMA_MT_DN
-#define TIE_MFMA_MT_DN 192
+#define TIE_MFMA_MT_DN 128
 #endif
 constexpr int MFMA_MT_GU = TIE_MFMA_MT_GU;
 constexpr int MFMA_MT_DN = TIE_MFMA_MT_DN;

@@ -61,11 +61,17 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 #ifndef TIE_Q4K_KST
 #define TIE_Q4K_KST 64
 #endif
+// Q6_K K per stage: 128 (one block half), or 64 (quarters {p, p + 2} of a
+// half, which share their ql / qh bytes; the activations' K order is
+// permuted to match)
+#ifndef TIE_Q6K_KST
+#define TIE_Q6K_KST 64
+#endif
 #ifndef TIE_MFMA_GU_WPE
 #define TIE_MFMA_GU_WPE 2
 #endif
 #ifndef TIE_MFMA_DN_WPE
-#define TIE_MFMA_DN_WPE 1
+#define TIE_MFMA_DN_WPE 2
 #endif
 constexpr int NWAVES = 4;
 constexpr int MF_THREADS = 64 * NWAVES;
@@ -108,7 +114,10 @@ template <int TYPE, bool DOWN = false> struct Cfg {
 	static constexpr int MT = DOWN ? MFMA_MT_DN : MFMA_MT_GU; // pair rows per work tile at most
 	static constexpr bool SPLIT = TYPE == TIE_GGML_BF16; // bf16 weights take activations as hi + lo planes
 	// K per stage (Q4_K optionally 64: one 64-weight group per stage)
-	static constexpr int KST = SPLIT ? 64 : (TYPE == TIE_GGML_Q4_K && TIE_Q4K_KST == 64 ? 64 : 128);
+	static constexpr int KST = SPLIT ? 64
+				    : (TYPE == TIE_GGML_Q4_K ? TIE_Q4K_KST : TYPE == TIE_GGML_Q6_K ? TIE_Q6K_KST : 128);
+	// Q6_K 64-K stages hold quarters p and p + 2 of a block half
+	static constexpr bool APERM = TYPE == TIE_GGML_Q6_K && KST == 64;
 	static constexpr int SPB = QK / KST;                 // stages per 256-weight block (quantised)
 	static constexpr int NPL = SPLIT ? 2 : 1;            // activation planes
 	static constexpr int RB = KST * 2;                   // bytes per A row, plane and stage
@@ -122,7 +131,7 @@ template <int TYPE, bool DOWN = false> struct Cfg {
 	// stage, by direct loads): no registers hold the next stage's weights.
 	// BF16 weights are prefetched into registers.
 	static constexpr bool B_LDS = !SPLIT;
-	static constexpr int NCH = TYPE == TIE_GGML_Q4_K ? 1 + KST / 32 : 7; // 1 KiB chunks per panel and stage
+	static constexpr int NCH = TYPE == TIE_GGML_Q4_K ? 1 + KST / 32 : (KST == 64 ? 5 : 7); // 1 KiB chunks per panel and stage
 	static constexpr int PB = NCH * 1024;                     // bytes per panel and stage
 	static constexpr int BBUF = B_LDS ? 4 * PB + (TYPE == TIE_GGML_Q6_K ? 4 * 128 : 0) : 0; // + Q6_K d planes
 	static constexpr int LDS_A = 2 * ABUF, LDS_B = 2 * BBUF;
@@ -221,7 +230,11 @@ __device__ __forceinline__ void dma_b(const MfmaArgs &a, int e, int slab, int st
 		int chunk;
 		if constexpr (TYPE == TIE_GGML_Q4_K)
 			chunk = s == 0 ? 0 : (C::NCH - 1) * part + s;
-		else
+		else if constexpr (C::APERM) {
+			// ql chunks of quarters q, q + 2 of half n; the half's qh; scales
+			const int n = (st >> 1) & 1, q = st & 1;
+			chunk = s < 2 ? 4 * n + 2 * q + s : (s < 4 ? 8 + 2 * n + (s - 2) : 12);
+		} else
 			chunk = s < 4 ? 4 * half + s : (s < 6 ? 8 + 2 * half + (s - 4) : 12);
 		dma16(panel(p) + chunk * 1024 + 16 * lane, __builtin_amdgcn_readfirstlane(lds_addr(B + p * C::PB + s * 1024)));
 	}
@@ -247,13 +260,15 @@ __device__ __forceinline__ void lds_b(const uint8_t *B, const int p[2], const in
 				b.q[j][q] = *reinterpret_cast<const u32x2 *>(pb + (1 + q) * 1024 + 8 * h);
 			b.sc[j] = *reinterpret_cast<const u32x4 *>(pb);
 		} else if constexpr (TYPE == TIE_GGML_Q6_K) {
+			constexpr int NQL = C::APERM ? 2 : 4; // ql chunk slots
 #pragma unroll
-			for (int q = 0; q < 4; q++)
+			for (int q = 0; q < NQL; q++)
 				b.ql[j][q] = *reinterpret_cast<const u32x2 *>(pb + q * 1024 + 8 * h);
 #pragma unroll
 			for (int q = 0; q < 2; q++)
-				b.qh[j][q] = *reinterpret_cast<const u32x2 *>(pb + (4 + q) * 1024 + 8 * h);
-			b.sc[j] = *reinterpret_cast<const u32x2 *>(pb + 6 * 1024 + 8 * (st & 1));
+				b.qh[j][q] = *reinterpret_cast<const u32x2 *>(pb + (NQL + q) * 1024 + 8 * h);
+			const int half = C::APERM ? (st >> 1) & 1 : st & 1;
+			b.sc[j] = *reinterpret_cast<const u32x2 *>(pb + (NQL + 2) * 1024 + 8 * half);
 			b.d[j] = *reinterpret_cast<const uint16_t *>(B + 4 * C::PB + p[j] * 128 + 2 * i[j]);
 		}
 	}
@@ -325,7 +340,7 @@ __device__ __forceinline__ void group_factors(const BRegs<TYPE> &b, int st, int 
 // l = 16*(s%2) + 8h + i, code q = ql nibble | qh bits << 4 with scale
 // 8*half + l/16 + 2r (TIE's block_q6_k).
 template <int TYPE>
-__device__ __forceinline__ void deq_step(const BRegs<TYPE> &b, const Fac &f, int s, bf16x8 out[2])
+__device__ __forceinline__ void deq_step(const BRegs<TYPE> &b, const Fac &f, int st, int s, bf16x8 out[2])
 {
 #pragma unroll
 	for (int j = 0; j < 2; j++) {
@@ -336,8 +351,9 @@ __device__ __forceinline__ void deq_step(const BRegs<TYPE> &b, const Fac &f, int
 			const u32x2 q = b.q[j][2 * gi + (sub & 1)];
 			out[j] = deq8((q.x >> (4 * u)) & 0x0f0f0f0fu, (q.y >> (4 * u)) & 0x0f0f0f0fu, f.D[j][u], f.M[j][u]);
 		} else {
-			const int r = s >> 1, lh = s & 1;
-			const u32x2 ql = b.ql[j][2 * (r & 1) + lh];
+			// quarter r; 64-K stages: quarter p for steps 0, 1 and p + 2 for 2, 3
+			const int r = Cfg<TYPE>::APERM ? (st & 1) + 2 * (s >> 1) : s >> 1, lh = s & 1;
+			const u32x2 ql = b.ql[j][Cfg<TYPE>::APERM ? lh : 2 * (r & 1) + lh];
 			const u32x2 qh = b.qh[j][lh];
 			const int nsh = 4 * (r >> 1), hsh = 2 * r;
 			const uint32_t lo = ((ql.x >> nsh) & 0x0f0f0f0fu) | (((qh.x >> hsh) & 0x03030303u) << 4);
@@ -386,7 +402,10 @@ template <int TYPE, bool DOWN>
 __device__ __forceinline__ void dma_a(const ASrc &s, int st, int w, const uint8_t *buf)
 {
 	using C = Cfg<TYPE, DOWN>;
-	const size_t ko = (size_t)st * C::RB;
+	// byte offset of the stage in an A row (APERM: block, half, quarter p;
+	// the lane's chunk offset in base covers the quarter p + 2 part)
+	const size_t ko = C::APERM ? (size_t)512 * (st >> 2) + 256 * ((st >> 1) & 1) + 64 * (st & 1)
+				   : (size_t)st * C::RB;
 	uint32_t off[(C::NDMA + 3) / 4 * 4]; // whole 16-byte reads (the lane slot holds ROFF_STRIDE entries)
 	static_assert(C::NDMA <= ROFF_STRIDE, "row offset slot too small");
 #pragma unroll
@@ -439,7 +458,7 @@ __device__ __forceinline__ void stage_mfma(const BRegs<TYPE> &b, int st, const u
 	group_factors<TYPE>(b, st, 0, f);
 	bf16x8 fa[2][NA], fb[2][2];
 	read(0, fa[0]);
-	deq_step<TYPE>(b, f, 0, fb[0]);
+	deq_step<TYPE>(b, f, st, 0, fb[0]);
 #pragma unroll
 	for (int s = 0; s < C::NSTEP; s++) {
 		const int cur = s & 1;
@@ -453,7 +472,7 @@ __device__ __forceinline__ void stage_mfma(const BRegs<TYPE> &b, int st, const u
 			read(s + 1, fa[cur ^ 1]);
 			if (TYPE == TIE_GGML_Q4_K && (s + 1) % 4 == 0)
 				group_factors<TYPE>(b, st, (s + 1) / 4, f);
-			deq_step<TYPE>(b, f, s + 1, fb[cur ^ 1]);
+			deq_step<TYPE>(b, f, st, s + 1, fb[cur ^ 1]);
 		}
 		__builtin_amdgcn_sched_barrier(0);
 	}
@@ -475,8 +494,10 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 	{
 		const int rsub = lane / C::CPR, slot = lane % C::CPR;
 		const int chunk = slot ^ C::swz(C::RPI * w + rsub);
-		as.base[0] = (const char *)a.a16 + 16 * chunk;
-		as.base[1] = (const char *)a.a16lo + 16 * chunk;
+		// APERM: chunks 0..3 are K 32p + 8c of the half, chunks 4..7 K 64 + 32p + 8(c - 4)
+		const int cofs = C::APERM ? 128 * (chunk >> 2) + 16 * (chunk & 3) : 16 * chunk;
+		as.base[0] = (const char *)a.a16 + cofs;
+		as.base[1] = (const char *)a.a16lo + cofs;
 		// row r = RPI (NWAVES c + w') + rsub' is entry c of lane slot RPI w' + rsub'
 		as.roff = roff + (C::RPI * w + rsub) * ROFF_STRIDE;
 		if (t < C::MT) {
@@ -597,12 +618,12 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 	}
 }
 
-// waves per SIMD: the quantised gate/up kernel keeps its LDS and registers
-// small enough for two workgroups per CU; the down and BF16 kernels use
-// larger tiles with one wave per SIMD
+// waves per SIMD: the quantised kernels keep their LDS and registers small
+// enough for two workgroups per CU; the BF16 kernels (weights prefetched
+// into registers) run one wave per SIMD
 constexpr int mf_wpe(int type, bool down)
 {
-	return down || type == TIE_GGML_BF16 ? TIE_MFMA_DN_WPE : TIE_MFMA_GU_WPE;
+	return type == TIE_GGML_BF16 ? 1 : down ? TIE_MFMA_DN_WPE : TIE_MFMA_GU_WPE;
 }
 
 template <int TYPE, bool DOWN>
