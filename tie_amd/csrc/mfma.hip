@@ -10,32 +10,37 @@
 //   gate/up:  G = X_e Wg_e^T, U = X_e Wu_e^T, h = silu_tab(G) * U  (fused)
 //   down:     Y = h_e Wd_e^T, scattered to the pairs' rows of y
 //
-// Work tile: up to MT = 192 pair rows of one expert (an expert with more
-// pairs is split evenly over several tiles; the usual prefill load is
-// ~T*k/E rows, one tile) x 128 F columns (gate/up: of gate and of up) or
-// 256 output columns (down).  A workgroup is 4 waves,
-// one per SIMD; wave w owns two 32-wide column tiles -- gate/up: the gate
-// and the up tile of F columns 32w..32w+31, so TIE's table SwiGLU
+// Work tile: up to MT pair rows of one expert (MFMA_MT_GU = 160 for
+// gate/up, MFMA_MT_DN = 128 for down; an expert with more pairs is split
+// evenly over several tiles) x 128 F columns (gate/up: of gate and of up)
+// or 256 output columns (down).  A workgroup is 4 waves, one per SIMD;
+// wave w owns two 32-wide column tiles -- gate/up: the gate and the up tile
+// of F columns 32w..32w+31, so TIE's table SwiGLU
 // (swiglu_activation_f32_f32_avx2) is applied to the accumulators in
-// registers; down: columns 64w..64w+63 -- against all rows of the tile
-// (up to 6 x 2 accumulator tiles of 32x32, in the accumulation registers;
-// more rows would not leave the 256 architectural registers the
-// dequantisation pipeline needs).
+// registers; down: columns 64w..64w+63 -- against all rows of the tile (up
+// to MT/32 x 2 accumulator tiles of 32x32).
 //
-// Both operands are staged per K stage of 128 by direct global->LDS loads
+// Both operands are staged per K stage by direct global->LDS loads
 // (global_load_lds_dwordx4) into double-buffered LDS tiles, one stage
 // ahead: the activations (A, bf16 rows gathered by pair) and, for Q4_K /
 // Q6_K, the raw panel chunks of the workgroup's 4 weight panels (1 KiB
-// each: the panel layout of common.h).  No register holds a prefetched
-// stage, so the pipeline costs no registers, and the compiler's wait-count
-// pass never sees (and never waits for) the prefetch: the stage barrier is
-// the wait.  In the 32x32x16 B-operand layout a lane holds 8 consecutive K
-// values of one weight row -- 8 consecutive quant bytes of its lane-row in
-// the panel -- which it reads from LDS and dequantises between the MFMAs:
-// every weight of the tile is dequantised exactly once, and each B fragment
-// feeds up to 6 MFMAs (one per 32-row M tile).  BF16 weights (already
-// MFMA operands) are prefetched into registers instead.  An A fragment
-// (1 KiB) feeds two MFMAs: 64 B of LDS reads per CU per clock.
+// each: the panel layout of common.h).  Quantised stages are 64 K: a Q4_K
+// stage is one 64-weight group (scale chunk + 2 quant chunks); a Q6_K stage
+// is quarters p and p + 2 of a 128-weight half, which share their ql / qh
+// bytes (low / high nibbles, qh bits 2p and 2p + 4), so a stage needs 5
+// chunks, and the activations' K order inside the stage is permuted to
+// match.  Small stages and tiles keep a workgroup at about 64-75 KiB of LDS
+// and 256 registers per lane: two workgroups share a CU (two waves per
+// SIMD), so one's stalls and pipeline fill / drain overlap the other's
+// MFMAs.  No register holds a prefetched stage, and the compiler's
+// wait-count pass never sees (and never waits for) the prefetch: the stage
+// barrier is the wait.  In the 32x32x16 B-operand layout a lane holds 8
+// consecutive K values of one weight row -- 8 consecutive quant bytes of
+// its lane-row in the panel -- which it reads from LDS and dequantises
+// between the MFMAs: every weight of the tile is dequantised exactly once,
+// and each B fragment feeds one MFMA per 32-row M tile.  BF16 weights
+// (already MFMA operands) are prefetched into registers instead (one wave
+// per SIMD, 64-K stages).  An A fragment (1 KiB) feeds two MFMAs.
 //
 // Numerics: fp32 accumulation of bf16 products.  Q4_K/Q6_K weights are
 // dequantised in fp32 (fma(q, d*sc, -dmin*m); d*sc*(q-32), both as TIE's
