@@ -171,15 +171,17 @@ def run_config(torch, tie_amd, wl, T, k, steps, warmup, flags):
                 block_TFLOPs=block_flops / (ms * 1e-3) / 1e12, kernels=kernels, layers=nL)
 
 
-def roofline(m):
-    """Roofline object for the dominant (longest) kernel of a measurement."""
+def roofline(m, config):
+    """Roofline object for the dominant (longest) kernel of a measurement of one
+    workload; traffic is the copy-scaled HBM bytes per launch measured for that
+    kernel on that workload (None when not profiled)."""
     name, kd = max(m["kernels"].items(), key=lambda kv: kv[1]["avg_us"])
     traffic = None
     tfile = os.path.join(ROOT, "profiles", "traffic.json")
     if os.path.exists(tfile):
         with open(tfile) as f:
             t = json.load(f)
-        traffic = t.get("%s@T%d" % (name, m["T"]))
+        traffic = t.get("%s@%s" % (name, config))
     # bound: MFMA when the kernel runs on the matrix cores and its algorithmic
     # intensity is above the MI355X ridge point (2.5 PFLOP/s / 8 TB/s)
     ridge = BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
@@ -310,7 +312,7 @@ def main():
         r = results[name]
         extra[name] = {"tokens_per_s": round(r["tokens_per_s"], 1), "ms_per_step": round(r["ms"], 4),
                        "block_GBps": round(r["block_GBps"], 1), "block_TFLOPs": round(r["block_TFLOPs"], 3),
-                       "roofline": roofline(r), "kernels": r["kernels"]}
+                       "roofline": roofline(r, name), "kernels": r["kernels"]}
     line = {
         "metric": "MoE block tokens/s (Qwen3-30B-A3B shape)",
         "value": round(m["tokens_per_s"], 1),
@@ -328,7 +330,7 @@ def main():
         "config": {"workload": "%s: d=%d F=%d E=%d k=%d T=%d, gate/up %s, down %s" % (
             main_name, cfg["d"], cfg["F"], cfg["E"], cfg["k"], cfg["T"], synth.TYPE_NAMES[cfg["gu_type"]],
             synth.TYPE_NAMES[cfg["down_type"]]), "T": cfg["T"], "path": args.path},
-        "roofline": roofline(m),
+        "roofline": roofline(m, main_name),
         "cpu_baseline": cpu,
         "block_GBps": round(m["block_GBps"], 1),
         "distinct_experts_per_step": round(m["U"], 2),

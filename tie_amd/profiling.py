@@ -6,13 +6,13 @@
         and grid shape.
 
     python -m tie_amd.profiling traffic --fetch F.csv --write W.csv
-            --copy-fetch CF.csv --copy-write CW.csv --copy-bytes N --T T
+            --copy-fetch CF.csv --copy-write CW.csv --copy-bytes N --config NAME
             [--out profiles/traffic.json]
         HBM bytes per forward of each block kernel from two --pmc runs
         (FETCH_SIZE, WRITE_SIZE; KiB per dispatch), each scaled by the
         factor that makes the same counter read N bytes for a plain device
         copy of N bytes (bench.py --copy-mb).  Merged into the JSON file
-        under "<kernel>@T<T>", which bench.py reports as roofline.traffic.
+        under "<kernel>@<config>", which bench.py reports as roofline.traffic.
 """
 import argparse
 import collections
@@ -126,9 +126,9 @@ _DEFAULT_JSON = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__f
 def traffic_markdown(path):
     with open(path) as f:
         t = json.load(f)
-    out = ["| kernel @ T | fetch MB | write MB | total MB per forward | dispatches | forwards |",
+    out = ["| kernel @ config | fetch MB | write MB | total MB per forward | dispatches | forwards |",
            "|---|---|---|---|---|---|"]
-    for k, v in sorted(t["detail"].items(), key=lambda kv: (int(kv[0].split("@T")[1]), kv[0])):
+    for k, v in sorted(t["detail"].items(), key=lambda kv: (kv[0].split("@")[1], kv[0])):
         out.append("| %s | %.2f | %.2f | %.2f | %d | %d |" % (k, v["fetch_bytes"] / 1e6, v["write_bytes"] / 1e6,
                                                              v["bytes"] / 1e6, v["dispatches"], v.get("forwards", 0)))
     out.append("")
@@ -150,7 +150,7 @@ def main():
     t.add_argument("--copy-fetch", required=True)
     t.add_argument("--copy-write", required=True)
     t.add_argument("--copy-bytes", type=int, required=True)
-    t.add_argument("--T", type=int, required=True)
+    t.add_argument("--config", required=True)
     t.add_argument("--out", default=_DEFAULT_JSON)
     m = sub.add_parser("traffic-md")
     m.add_argument("--json", default=_DEFAULT_JSON)
@@ -167,9 +167,9 @@ def main():
         with open(a.out) as f:
             data = json.load(f)
     for block, v in res.items():
-        data["%s@T%d" % (block, a.T)] = v["bytes"]
+        data["%s@%s" % (block, a.config)] = v["bytes"]
         data["detail"] = data.get("detail", {})
-        data["detail"]["%s@T%d" % (block, a.T)] = v
+        data["detail"]["%s@%s" % (block, a.config)] = v
     data["scales"] = scales
     with open(a.out, "w") as f:
         json.dump(data, f, indent=1, sort_keys=True)
