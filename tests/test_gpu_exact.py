@@ -88,7 +88,7 @@ def test_golden_bf16_zipf_device_api(name, literal):
     L.close()
 
 
-@pytest.mark.parametrize("cfg", ["30b_t1", "30b_t32", "235b_t1"])
+@pytest.mark.parametrize("cfg", ["30b_t1", "30b_t8", "30b_t32", "235b_t1"])
 def test_full_size_configs(cfg):
     c = synth.CONFIGS[cfg]
     layer = synth_layer(c["seed"], c["d"], c["F"], c["E"], c["gu_type"], c["down_type"], c["zipf"])
@@ -96,11 +96,48 @@ def test_full_size_configs(cfg):
     run_both(layer, x, c["k"])
 
 
+@pytest.mark.parametrize("gu,dn", [(synth.BF16, synth.BF16), (synth.Q4_K, synth.BF16), (synth.BF16, synth.Q6_K)])
+def test_one_token_other_types(gu, dn):
+    """One token with BF16 on either side: routing in the gate/up prologue
+    with a one-pair grouping (BF16 gate/up), or the separate grouping
+    kernel."""
+    layer = synth_layer(26, 512, 256, 32, gu, dn, None)
+    for k in (1, 8):
+        run_both(layer, synth.make_input(26 + k, 1, 512), k)
+
+
 def test_ragged_token_counts_and_k():
     layer = synth_layer(21, 512, 512, 24, synth.Q4_K, synth.Q6_K, None)
     for T, k in [(1, 1), (3, 2), (5, 7), (9, 24), (13, 8)]:
         x = synth.make_input(21 + T, T, 512)
         run_both(layer, x, k)
+
+
+@pytest.mark.parametrize("E", [200, 1024])
+def test_wide_expert_counts(E):
+    """Selection over more than 128 experts (several logits per lane, E not
+    a multiple of 64), on the grouping kernel (T*k <= 4096) and on the
+    separate selection + dispatch kernels (T*k > 4096)."""
+    import torch
+    layer = synth_layer(24 + E, 256, 256, E, synth.Q4_K, synth.Q6_K, None)
+    for T, k in [(1, 8), (5, 32), (40, 8)]:
+        x = synth.make_input(24 + T, T, 256)
+        run_both(layer, x, k)
+    T, k = 160, 32
+    x = synth.make_input(25, T, 256)
+    L = tie_amd.Layer.from_synth(layer)
+    xd = torch.from_numpy(x).cuda()
+    out = torch.empty_like(xd)
+    idx = torch.empty((T, k), dtype=torch.int32, device="cuda")
+    w = torch.empty((T, k), dtype=torch.float32, device="cuda")
+    print("case E=%d T=%d k=%d forced exact" % (E, T, k), flush=True)
+    L.forward(xd, T, k, out, idx, w, flags=tie_amd.PATH_EXACT)
+    torch.cuda.synchronize()
+    ro, ri, rw = bind.moe_block(layer, x, k)
+    assert_same(idx.cpu().numpy(), ri, "topk_idx")
+    assert_same(w.cpu().numpy(), rw, "topk_w")
+    assert_same(out.cpu().numpy(), ro, "out")
+    L.close()
 
 
 def test_zero_tokens_and_nan_rows():

@@ -96,7 +96,6 @@ __global__ __launch_bounds__(DSP_THREADS) void route_group_kernel(const float *_
 	__shared__ __attribute__((aligned(16))) int32_t cnt[MAX_E];
 	__shared__ int32_t cur[MAX_E];
 	__shared__ int wsum[DSP_THREADS / 64];
-	__shared__ float sel[(DSP_THREADS / 8) * MAX_K];
 	__shared__ uint64_t etab[32];
 	__shared__ int32_t sidx[RG_MAX_PAIRS];
 	__shared__ int lpt[2 * LPT_BINS];
@@ -106,17 +105,8 @@ __global__ __launch_bounds__(DSP_THREADS) void route_group_kernel(const float *_
 		etab[tid] = tab[tid];
 	}
 	__syncthreads();
-	if (E <= 128) {
-		for (int t0 = 0; t0 < T; t0 += DSP_THREADS / 8) {
-			const int t = t0 + tid / 8;
-			if (t < T)
-				topk_softmax_group8(logits + (size_t)t * E, E, k, sel + (tid / 8) * MAX_K, etab,
-						    sidx + t * k, topk_w + (size_t)t * k);
-		}
-	} else {
-		for (int t = tid >> 6; t < T; t += DSP_THREADS / 64)
-			topk_softmax_wave(logits + (size_t)t * E, E, k, etab, sidx + t * k, topk_w + (size_t)t * k);
-	}
+	for (int t = tid >> 6; t < T; t += DSP_THREADS / 64)
+		topk_softmax(logits + (size_t)t * E, E, k, etab, sidx + t * k, topk_w + (size_t)t * k);
 	__syncthreads();
 	const int npairs = T * k;
 	for (int p = tid; p < npairs; p += DSP_THREADS)

@@ -21,9 +21,9 @@
 //                      address per wave), so it reaches the FMAs as SGPR
 //                      operands.  Per-block dots meet in LDS and are added
 //                      in block order.  Writes the gate and up row sums.
-//                      For T <= 8 (E <= 128) every workgroup first selects
-//                      the experts of all tokens itself (top-k, softmax,
-//                      grouping): no separate routing launch.
+//                      For one token (E <= 128) every workgroup first
+//                      selects the token's experts itself (top-k,
+//                      softmax): no separate routing launch.
 //   exact_down_kernel  one workgroup per (64-row panel of d, active
 //                      expert).  The prologue forms h = silu_tab(gate) * up
 //                      (swiglu_activation_f32_f32_avx2) for its pairs in
@@ -104,7 +104,11 @@ constexpr int GU_THREADS = 64 * GU_WAVES;
 constexpr int GUF_WAVES = TIE_GUF_WAVES;
 constexpr int PG_MAX = 16;        // pairs per LDS group
 constexpr int PART_FLOATS = 16384; // LDS budget of the per-block partial dots (64 KiB)
-constexpr int INLINE_T = 8;       // routing in the gate/up prologue up to this T (E <= 128)
+// Routing in the gate/up prologue up to this T (E <= 128).  Only one token:
+// for T = 2..8 every workgroup repeating the selection and grouping of all
+// tokens costs more (T = 8: 64 us of gate/up against 33 us plus a 9.5 us
+// grouping launch) than the launch it saves.
+constexpr int INLINE_T = 1;
 constexpr int INLINE_E = 128;
 
 // ------------------------------------------------------------------ blocks
@@ -328,13 +332,11 @@ __device__ __forceinline__ void pairs_chunk(const Block &blk, int q, XF xrow, fl
 		part_b[(q + p) * 64 + lane] = out[p];
 }
 
-// All np pairs of a group against the lane's block: up to TIE_EXACT_PCMAX
-// at a time, the remainder (1 .. PCMAX-1) in one chunk of its own size, so
+// All np pairs of a group against the lane's block: up to PM at a time, the remainder (1 .. PCMAX-1) in one chunk of its own size, so
 // an expert with at most PCMAX pairs dequantises each weight once.
-template <typename Block, typename XP, typename XF>
+template <int PM, typename Block, typename XP, typename XF>
 __device__ __forceinline__ void block_all_pairs(const Block &blk, int np, XF xrow, float *part_b, int lane)
 {
-	constexpr int PM = TIE_EXACT_PCMAX;
 	int q = 0;
 	for (; q + PM <= np; q += PM)
 		pairs_chunk<PM, Block, XP>(blk, q, xrow, part_b, lane);
@@ -376,12 +378,11 @@ struct ExactArgs {
 };
 
 // Selection and grouping of all T <= INLINE_T tokens by one workgroup of NT
-// threads (E <= INLINE_E <= NT); workgroup (0,0,0) also publishes them for
-// the later kernels.  Results land in the LDS arrays of `R`.  With T = 1
+// threads (E <= INLINE_E <= NT; a wave per token reads its logits from
+// global memory); workgroup (0,0,0) also publishes them for the later
+// kernels.  Results land in the LDS arrays of `R`.  With T = 1
 // there is no grouping: slot j of the token is a group of its own.
 struct alignas(16) InlineRoute {
-	float lg[INLINE_T * INLINE_E];
-	float sel[INLINE_T * MAX_K];
 	float w[INLINE_T * MAX_K];
 	int32_t idx[INLINE_T * MAX_K];
 	alignas(16) int32_t cnt[INLINE_E];
@@ -400,13 +401,9 @@ template <int NT> __device__ __forceinline__ void inline_route(const ExactArgs &
 		const uint64_t tab[32] = TIE_EXP2_TABLE;
 		R.etab[tid] = tab[tid];
 	}
-	for (int i = tid; i < T * E; i += NT)
-		R.lg[i] = a.logits[i];
 	__syncthreads();
-	if (tid < 8 * T) {
-		const int t = tid >> 3;
-		topk_softmax_group8(R.lg + t * E, E, k, R.sel + t * MAX_K, R.etab, R.idx + t * k, R.w + t * k);
-	}
+	for (int t = tid >> 6; t < T; t += NT / 64)
+		topk_softmax_wave<INLINE_E / 64>(a.logits + (size_t)t * E, E, k, R.etab, R.idx + t * k, R.w + t * k);
 	__syncthreads();
 	if (a.single) {
 		// one token: slot j is its own group (expert idx[j], pair j); the
@@ -443,7 +440,7 @@ template <int NT> __device__ __forceinline__ void inline_route(const ExactArgs &
 // column w, w + 8, ..) and applies TIE's table SwiGLU
 // (swiglu_activation_f32_f32_avx2) to the row sums, writing h; otherwise
 // blockIdx.z selects the matrix and the row sums are written.
-template <int TYPE, bool FUSED>
+template <int TYPE, bool FUSED, int PM>
 __global__ __launch_bounds__(GU_THREADS) GU_OCC void exact_gu_kernel(ExactArgs a)
 {
 	constexpr int NW = FUSED ? GUF_WAVES : GU_WAVES;
@@ -515,7 +512,7 @@ __global__ __launch_bounds__(GU_THREADS) GU_OCC void exact_gu_kernel(ExactArgs a
 				const int pair = __builtin_amdgcn_readfirstlane(gp[q]);
 				return (cfloat *)(x + (size_t)(pair / k) * in + QK * b);
 			};
-			block_all_pairs<Block, cfloat>(blk, np, xrow_b, part + (size_t)t * pg_cap * 64, lane);
+			block_all_pairs<PM, Block, cfloat>(blk, np, xrow_b, part + (size_t)t * pg_cap * 64, lane);
 			if (TIE_GU_PREFETCH)
 				blk = nxt;
 		}
@@ -603,7 +600,7 @@ __device__ __forceinline__ void stage_h(const ExactArgs &a, const int32_t *gp, i
 // min(nb, 8).  HG: h comes from hbuf (written by the fused gate/up kernel)
 // through scalar loads; otherwise the prologue forms h from the gate and up
 // row sums in LDS.  Dynamic LDS: [h [pg_cap][F] |] part [nb][pg_cap][64].
-template <int TYPE, bool HG>
+template <int TYPE, bool HG, int PM>
 __global__ __launch_bounds__(512) EXACT_OCC void exact_down_kernel(ExactArgs a)
 {
 	using Block = typename BlockOf<TYPE>::type;
@@ -658,10 +655,10 @@ __global__ __launch_bounds__(512) EXACT_OCC void exact_down_kernel(ExactArgs a)
 					const int pair = __builtin_amdgcn_readfirstlane(gp[q]);
 					return (cfloat *)(a.hbuf + (size_t)pair * F + QK * b);
 				};
-				block_all_pairs<Block, cfloat>(blk, np, xrow_b, part + (size_t)b * pg_cap * 64, lane);
+				block_all_pairs<PM, Block, cfloat>(blk, np, xrow_b, part + (size_t)b * pg_cap * 64, lane);
 			} else {
 				auto xrow_b = [&](int q) { return (lfloat *)(hs + (size_t)q * F + QK * b); };
-				block_all_pairs<Block, lfloat>(blk, np, xrow_b, part + (size_t)b * pg_cap * 64, lane);
+				block_all_pairs<PM, Block, lfloat>(blk, np, xrow_b, part + (size_t)b * pg_cap * 64, lane);
 			}
 		}
 		__syncthreads();
@@ -761,11 +758,17 @@ static hipError_t launch_gu_q(int type, bool fused, int nmat, int rows, int in, 
 	const size_t lds = sizeof(float) * (size_t)mats * nb * g.pg_cap * 64;
 	const dim3 grid(rows / PANEL_ROWS, max_active, fused ? 1 : nmat), block(64 * (fused ? GUF_WAVES : GU_WAVES));
 	const size_t st = fused ? 0 : sizeof(InlineRoute);
+	constexpr int PM = TIE_EXACT_PCMAX;
+	// one token (one pair per group): a one-pair instance, whose register
+	// budget, and so occupancy, is not set by the multi-pair dot products
+	if (g.single)
+		return type == TIE_GGML_Q4_K ? launch_q(exact_gu_kernel<TIE_GGML_Q4_K, false, 1>, grid, block, lds, st, s, g)
+					     : launch_q(exact_gu_kernel<TIE_GGML_Q6_K, false, 1>, grid, block, lds, st, s, g);
 	if (type == TIE_GGML_Q4_K)
-		return fused ? launch_q(exact_gu_kernel<TIE_GGML_Q4_K, true>, grid, block, lds, st, s, g)
-			     : launch_q(exact_gu_kernel<TIE_GGML_Q4_K, false>, grid, block, lds, st, s, g);
-	return fused ? launch_q(exact_gu_kernel<TIE_GGML_Q6_K, true>, grid, block, lds, st, s, g)
-		     : launch_q(exact_gu_kernel<TIE_GGML_Q6_K, false>, grid, block, lds, st, s, g);
+		return fused ? launch_q(exact_gu_kernel<TIE_GGML_Q4_K, true, PM>, grid, block, lds, st, s, g)
+			     : launch_q(exact_gu_kernel<TIE_GGML_Q4_K, false, PM>, grid, block, lds, st, s, g);
+	return fused ? launch_q(exact_gu_kernel<TIE_GGML_Q6_K, true, PM>, grid, block, lds, st, s, g)
+		     : launch_q(exact_gu_kernel<TIE_GGML_Q6_K, false, PM>, grid, block, lds, st, s, g);
 }
 
 // Routing (logits, selection, grouping) and the expert GEMVs of the exact
@@ -868,6 +871,7 @@ hipError_t launch_exact_block(const Layer &L, const float *x, int T, int k, cons
 
 	prof_begin("exact_down", s);
 	{
+		constexpr int PM = TIE_EXACT_PCMAX;
 		ExactArgs g = a;
 		g.w[0] = L.down.data;
 		g.expert_bytes[0] = L.down.expert_bytes;
@@ -885,14 +889,19 @@ hipError_t launch_exact_block(const Layer &L, const float *x, int T, int k, cons
 				g.pg_cap = clamp_pg(PART_FLOATS / (nb * 64));
 				const size_t lds = sizeof(float) * (size_t)g.pg_cap * nb * 64;
 				err = L.down.type == TIE_GGML_Q4_K
-					      ? launch_q(exact_down_kernel<TIE_GGML_Q4_K, true>, grid, block, lds, 0, s, g)
-					      : launch_q(exact_down_kernel<TIE_GGML_Q6_K, true>, grid, block, lds, 0, s, g);
+					      ? launch_q(exact_down_kernel<TIE_GGML_Q4_K, true, PM>, grid, block, lds, 0, s, g)
+					      : launch_q(exact_down_kernel<TIE_GGML_Q6_K, true, PM>, grid, block, lds, 0, s, g);
 			} else {
 				g.pg_cap = clamp_pg(PART_FLOATS / (F + nb * 64));
 				const size_t lds = sizeof(float) * (size_t)g.pg_cap * (F + nb * 64);
-				err = L.down.type == TIE_GGML_Q4_K
-					      ? launch_q(exact_down_kernel<TIE_GGML_Q4_K, false>, grid, block, lds, 0, s, g)
-					      : launch_q(exact_down_kernel<TIE_GGML_Q6_K, false>, grid, block, lds, 0, s, g);
+				if (single)
+					err = L.down.type == TIE_GGML_Q4_K
+						      ? launch_q(exact_down_kernel<TIE_GGML_Q4_K, false, 1>, grid, block, lds, 0, s, g)
+						      : launch_q(exact_down_kernel<TIE_GGML_Q6_K, false, 1>, grid, block, lds, 0, s, g);
+				else
+					err = L.down.type == TIE_GGML_Q4_K
+						      ? launch_q(exact_down_kernel<TIE_GGML_Q4_K, false, PM>, grid, block, lds, 0, s, g)
+						      : launch_q(exact_down_kernel<TIE_GGML_Q6_K, false, PM>, grid, block, lds, 0, s, g);
 			}
 		}
 	}

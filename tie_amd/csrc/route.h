@@ -9,77 +9,6 @@ namespace tie {
 
 constexpr int LPT_BINS = 256; // pair-count buckets of the launch order
 
-// top-k (engine.c:891-914 semantics) + softmax (engine.c:864-888) for one
-// token, by one wave.  `lg` holds the token's E logits.  The k winners are
-// extracted one at a time by a wave-wide argmax under the order (value
-// descending, index ascending) -- the order find_top_k's strict-greater
-// insertion produces; NaN and -inf never qualify; unfilled slots are
-// {-1, -inf}.  Slot j's exponential is computed by lane j, the sum is
-// formed serially in slot order, and every weight is e_j * (1 / sum).
-__device__ __forceinline__ void topk_softmax_wave(const float *lg, int E, int k, const uint64_t *etab, int32_t *out_idx,
-				  float *out_w)
-{
-	const int lane = threadIdx.x & 63;
-	constexpr int PER = MAX_E / 64;
-	float v[PER];
-#pragma unroll
-	for (int q = 0; q < PER; q++) {
-		const int e = q * 64 + lane;
-		const float x = e < E ? lg[e] : -__builtin_inff();
-		v[q] = (x > -__builtin_inff()) ? x : -__builtin_inff(); // NaN -> never selected
-	}
-	float my_s = -__builtin_inff();
-	int my_i = -1;
-	for (int j = 0; j < k; j++) {
-		// lane-local best: first (lowest index) maximum
-		float bv = -__builtin_inff();
-		int be = 0x7fffffff;
-#pragma unroll
-		for (int q = 0; q < PER; q++)
-			if (v[q] > bv) {
-				bv = v[q];
-				be = q * 64 + lane;
-			}
-		// wave argmax by (value desc, index asc)
-#pragma unroll
-		for (int off = 32; off > 0; off >>= 1) {
-			const float ov = __shfl_xor(bv, off);
-			const int oe = __shfl_xor(be, off);
-			if (ov > bv || (ov == bv && oe < be)) {
-				bv = ov;
-				be = oe;
-			}
-		}
-		const bool found = bv > -__builtin_inff();
-		if (lane == j) {
-			my_s = found ? bv : -__builtin_inff();
-			my_i = found ? be : -1;
-		}
-		if (found && (be & 63) == lane) {
-#pragma unroll
-			for (int q = 0; q < PER; q++)
-				if (q == (be >> 6))
-					v[q] = -__builtin_inff();
-		}
-	}
-	// softmax over the k selected logits: max is slot 0 (or -inf), exp per lane
-	float mx = __shfl(my_s, 0);
-	for (int j = 1; j < k; j++) {
-		const float sj = __shfl(my_s, j);
-		if (sj > mx)
-			mx = sj;
-	}
-	const float ev = lane < k ? tie_expf_tab(my_s - mx, etab) : 0.0f;
-	float sum = 0.0f;
-	for (int j = 0; j < k; j++)
-		sum = sum + __shfl(ev, j);
-	const float inv = __fdiv_rn(1.0f, sum);
-	if (lane < k) {
-		out_w[lane] = ev * inv;
-		out_idx[lane] = my_i;
-	}
-}
-
 // DPP lane moves inside rows of 16 lanes (v_mov_b32 with a DPP control)
 template <int CTRL> __device__ __forceinline__ float dppf(float v)
 {
@@ -92,6 +21,7 @@ template <int CTRL> __device__ __forceinline__ int dppi(int v)
 constexpr int DPP_XOR1 = 0xb1;        // quad_perm [1,0,3,2]
 constexpr int DPP_XOR2 = 0x4e;        // quad_perm [2,3,0,1]
 constexpr int DPP_HALF_MIRROR = 0x141; // lane i <- lane 7-i within each 8
+constexpr int DPP_MIRROR = 0x140;      // lane i <- lane 15-i within each 16
 constexpr int DPP_SHL1 = 0x101, DPP_SHL2 = 0x102, DPP_SHL4 = 0x104; // lane i <- lane i+n (row of 16)
 
 // hsum_f32_avx2's tree over the 8 lanes l = lane%8 of a group, on lane l = 0:
@@ -103,95 +33,120 @@ __device__ __forceinline__ float hsum8_lanes(float v)
 	return a + dppf<DPP_SHL2>(a);          // lane 0: (s0 + s1) + (s2 + s3)
 }
 
-// The same selection and softmax for 8 tokens per wave: 8 lanes per token
-// (E <= 128, 16 logits per lane).  Identical order of selection (value
-// descending, index ascending; NaN and -inf never qualify) and identical
-// softmax arithmetic: the maximum over the slots, e_j = expf(s_j - max),
-// the sum formed serially in slot order, w_j = e_j * (1 / sum).  The
-// argmax runs over DPP lane moves.  `lg` is the group's token's E logits,
-// `sel` LDS scratch of MAX_K floats for that token.
-__device__ __forceinline__ void topk_softmax_group8(const float *lg, int E, int k, float *sel, const uint64_t *etab,
-						    int32_t *out_idx, float *out_w)
+__device__ __forceinline__ uint32_t umax32(uint32_t a, uint32_t b)
 {
-	constexpr int G = 8, V = 16;
-	const int lig = threadIdx.x & (G - 1);
-	float v[V];
+	return a > b ? a : b;
+}
+
+// Order-preserving integer key of a logit: larger float, larger key.  NaN
+// maps to the key of -inf (never selected, like find_top_k's strict
+// comparison) and -0 to +0 (they compare equal as floats, so they must tie
+// and fall back to the index order).  Every key of a selectable value is
+// above KEY_NINF; a removed entry gets key 0.
+constexpr uint32_t KEY_NINF = 0x007fffffu;
+__device__ __forceinline__ uint32_t logit_key(float x)
+{
+	if (!(x > -__builtin_inff()))
+		return KEY_NINF;
+	const uint32_t b = __builtin_bit_cast(uint32_t, x + 0.0f); // -0 -> +0
+	return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ float key_logit(uint32_t k)
+{
+	return __builtin_bit_cast(float, (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+// top-k (engine.c:891-914 semantics) + softmax (engine.c:864-888) for one
+// token, by one wave; PER logits per lane (E <= 64 * PER), entry e = 64q +
+// lane in register q.  The k winners are extracted one at a time by a
+// wave-wide argmax under the order (value descending, index ascending) --
+// the order find_top_k's strict-greater insertion produces: the maximum
+// key comes from a DPP reduction inside each row of 16 lanes and a scalar
+// maximum over the four rows, and the lowest index holding it from a
+// ballot per register (register q holds indices 64q ..).  NaN and -inf
+// never qualify; unfilled slots are {-1, -inf}.  Slot j's exponential is
+// computed by lane j, the sum is formed serially in slot order, and every
+// weight is e_j * (1 / sum).  `lg` may be global or LDS memory.
+template <int PER>
+__device__ __forceinline__ void topk_softmax_wave(const float *lg, int E, int k, const uint64_t *etab,
+						  int32_t *out_idx, float *out_w)
+{
+	const int lane = threadIdx.x & 63;
+	uint32_t key[PER];
 #pragma unroll
-	for (int q = 0; q < V; q++) {
-		const int e = q * G + lig;
-		const float x = e < E ? lg[e] : -__builtin_inff();
-		v[q] = (x > -__builtin_inff()) ? x : -__builtin_inff();
+	for (int q = 0; q < PER; q++) {
+		const int e = q * 64 + lane;
+		key[q] = e < E ? logit_key(lg[e]) : KEY_NINF;
 	}
-	auto better = [](float ov, int oe, float bv, int be) { return ov > bv || (ov == bv && oe < be); };
+	float my_s = -__builtin_inff();
+	int my_i = -1;
 	for (int j = 0; j < k; j++) {
-		float bv = -__builtin_inff();
-		int be = 0x7fffffff;
+		uint32_t m = key[0];
 #pragma unroll
-		for (int q = 0; q < V; q++)
-			if (v[q] > bv) {
-				bv = v[q];
-				be = q * G + lig;
-			}
-		float ov = dppf<DPP_XOR1>(bv);
-		int oe = dppi<DPP_XOR1>(be);
-		if (better(ov, oe, bv, be)) {
-			bv = ov;
-			be = oe;
-		}
-		ov = dppf<DPP_XOR2>(bv);
-		oe = dppi<DPP_XOR2>(be);
-		if (better(ov, oe, bv, be)) {
-			bv = ov;
-			be = oe;
-		}
-		ov = dppf<DPP_HALF_MIRROR>(bv);
-		oe = dppi<DPP_HALF_MIRROR>(be);
-		if (better(ov, oe, bv, be)) {
-			bv = ov;
-			be = oe;
-		}
-		const bool found = bv > -__builtin_inff();
-		if (lig == 0) {
-			sel[j] = found ? bv : -__builtin_inff();
-			out_idx[j] = found ? be : -1;
-		}
-		if (found && (be & (G - 1)) == lig) {
+		for (int q = 1; q < PER; q++)
+			m = m > key[q] ? m : key[q];
+		m = umax32(m, (uint32_t)dppi<DPP_XOR1>((int)m));
+		m = umax32(m, (uint32_t)dppi<DPP_XOR2>((int)m));
+		m = umax32(m, (uint32_t)dppi<DPP_HALF_MIRROR>((int)m));
+		m = umax32(m, (uint32_t)dppi<DPP_MIRROR>((int)m));
+		uint32_t best = (uint32_t)__builtin_amdgcn_readlane((int)m, 0);
 #pragma unroll
-			for (int q = 0; q < V; q++)
-				if (q == be / G)
-					v[q] = -__builtin_inff();
+		for (int r = 16; r < 64; r += 16) {
+			const uint32_t o = (uint32_t)__builtin_amdgcn_readlane((int)m, r);
+			best = best > o ? best : o;
+		}
+		if (best <= KEY_NINF)
+			break; // nothing selectable left: the remaining slots stay unfilled
+		int be = 0;
+#pragma unroll
+		for (int q = PER - 1; q >= 0; q--) {
+			const uint64_t bal = __builtin_amdgcn_ballot_w64(key[q] == best);
+			if (bal)
+				be = 64 * q + (int)__builtin_ctzll(bal);
+		}
+		if (lane == j) {
+			my_s = key_logit(best);
+			my_i = be;
+		}
+		if (lane == (be & 63)) {
+#pragma unroll
+			for (int q = 0; q < PER; q++)
+				if (q == (be >> 6))
+					key[q] = 0;
 		}
 	}
-	__builtin_amdgcn_wave_barrier();
-	float mx = sel[0];
-	for (int j = 1; j < k; j++)
-		if (sel[j] > mx)
-			mx = sel[j];
-	// e_j on lane j % 8, then the serial sum on lane 0
-	float ev[MAX_K / G];
-#pragma unroll
-	for (int q = 0; q < MAX_K / G; q++) {
-		const int j = q * G + lig;
-		ev[q] = j < k ? tie_expf_tab(sel[j] - mx, etab) : 0.0f;
+	// softmax over the k selected logits: max over the slots, exp per lane
+	float mx = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_s), 0));
+	for (int j = 1; j < k; j++) {
+		const float sj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_s), j));
+		if (sj > mx)
+			mx = sj;
 	}
-	__builtin_amdgcn_wave_barrier();
-#pragma unroll
-	for (int q = 0; q < MAX_K / G; q++) {
-		const int j = q * G + lig;
-		if (j < k)
-			sel[j] = ev[q];
-	}
-	__builtin_amdgcn_wave_barrier();
+	const float ev = lane < k ? tie_expf_tab(my_s - mx, etab) : 0.0f;
 	float sum = 0.0f;
 	for (int j = 0; j < k; j++)
-		sum = sum + sel[j];
+		sum = sum + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ev), j));
 	const float inv = __fdiv_rn(1.0f, sum);
-#pragma unroll
-	for (int q = 0; q < MAX_K / G; q++) {
-		const int j = q * G + lig;
-		if (j < k)
-			out_w[j] = ev[q] * inv;
+	if (lane < k) {
+		out_w[lane] = ev * inv;
+		out_idx[lane] = my_i;
 	}
+}
+
+// topk_softmax_wave with PER chosen for E (E <= MAX_E)
+__device__ __forceinline__ void topk_softmax(const float *lg, int E, int k, const uint64_t *etab, int32_t *out_idx,
+					     float *out_w)
+{
+	if (E <= 64)
+		topk_softmax_wave<1>(lg, E, k, etab, out_idx, out_w);
+	else if (E <= 128)
+		topk_softmax_wave<2>(lg, E, k, etab, out_idx, out_w);
+	else if (E <= 256)
+		topk_softmax_wave<4>(lg, E, k, etab, out_idx, out_w);
+	else if (E <= 512)
+		topk_softmax_wave<8>(lg, E, k, etab, out_idx, out_w);
+	else
+		topk_softmax_wave<16>(lg, E, k, etab, out_idx, out_w);
 }
 
 // Exclusive prefix sum over a workgroup of NT threads (one value each);

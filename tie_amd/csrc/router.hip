@@ -17,8 +17,8 @@
 //   router_logits  large T: 32 tokens x 32 experts per workgroup over the
 //                  transposed router matrix staged by direct global->LDS
 //                  loads.
-// Selection kernels: router_topk (8 lanes per token, E <= 128) and
-// router_topk_wave (a wave per token, E <= 1024).  Small batches select
+// Selection kernel: router_topk (a wave per token, E <= 1024).  Small
+// batches select
 // and group in one workgroup instead (route_group_kernel, dispatch.hip).
 #include "common.h"
 #include "route.h"
@@ -227,36 +227,6 @@ __global__ __launch_bounds__(RT_THREADS) void router_logits_kernel(const float *
 	}
 }
 
-// ------------------------------------------------------------ router_topk
-// 32 tokens per workgroup, 8 lanes per token (E <= 128).
-#ifndef TIE_RK_TOK
-#define TIE_RK_TOK 32
-#endif
-constexpr int RK_TOK = TIE_RK_TOK, RK_THREADS = 8 * RK_TOK;
-
-__global__ __launch_bounds__(RK_THREADS) void router_topk_kernel(const float *__restrict__ logits, int T, int E,
-								 int k, int32_t *__restrict__ topk_idx,
-								 float *__restrict__ topk_w)
-{
-	__shared__ float lg[RK_TOK * 128];
-	__shared__ float sel[RK_TOK * MAX_K];
-	__shared__ uint64_t etab[32];
-	const int tid = threadIdx.x;
-	const int t0 = blockIdx.x * RK_TOK;
-	const int nt = min(RK_TOK, T - t0);
-	if (tid < 32) {
-		const uint64_t tab[32] = TIE_EXP2_TABLE;
-		etab[tid] = tab[tid];
-	}
-	for (int i = tid; i < nt * E; i += RK_THREADS)
-		lg[i] = logits[(size_t)t0 * E + i];
-	__syncthreads();
-	const int t = tid / 8;
-	if (t < nt)
-		topk_softmax_group8(lg + t * E, E, k, sel + t * MAX_K, etab, topk_idx + (size_t)(t0 + t) * k,
-				    topk_w + (size_t)(t0 + t) * k);
-}
-
 // W [E][d] -> W^T [d][E] (once, at layer creation)
 __global__ void transpose_kernel(const float *__restrict__ W, float *__restrict__ WT, int E, int d)
 {
@@ -281,10 +251,10 @@ hipError_t launch_router_transpose(const Layer &L, hipStream_t s)
 	return hipGetLastError();
 }
 
-// ------------------------------------------------------------ router_topk_wave
-// E > 128: one wave per token (topk_softmax_wave, E <= MAX_E).
+// ------------------------------------------------------------ router_topk
+// one wave per token (topk_softmax, E <= MAX_E)
 constexpr int RW_THREADS = 256;
-__global__ __launch_bounds__(RW_THREADS) void router_topk_wave_kernel(const float *__restrict__ logits, int T, int E,
+__global__ __launch_bounds__(RW_THREADS) void router_topk_kernel(const float *__restrict__ logits, int T, int E,
 								      int k, int32_t *__restrict__ topk_idx,
 								      float *__restrict__ topk_w)
 {
@@ -296,7 +266,7 @@ __global__ __launch_bounds__(RW_THREADS) void router_topk_wave_kernel(const floa
 	__syncthreads();
 	const int t = blockIdx.x * (RW_THREADS / 64) + (threadIdx.x >> 6);
 	if (t < T)
-		topk_softmax_wave(logits + (size_t)t * E, E, k, etab, topk_idx + (size_t)t * k, topk_w + (size_t)t * k);
+		topk_softmax(logits + (size_t)t * E, E, k, etab, topk_idx + (size_t)t * k, topk_w + (size_t)t * k);
 }
 
 hipError_t launch_router_logits(const Layer &L, const float *x, int T, float *logits, hipStream_t s)
@@ -329,12 +299,8 @@ hipError_t launch_router_logits(const Layer &L, const float *x, int T, float *lo
 hipError_t launch_router_select(const Layer &L, int T, int k, const float *logits, int32_t *topk_idx, float *topk_w,
 				hipStream_t s)
 {
-	if (L.E <= 128)
-		hipLaunchKernelGGL(router_topk_kernel, dim3((T + RK_TOK - 1) / RK_TOK), dim3(RK_THREADS), 0, s, logits, T,
-				   L.E, k, topk_idx, topk_w);
-	else
-		hipLaunchKernelGGL(router_topk_wave_kernel, dim3((T + RW_THREADS / 64 - 1) / (RW_THREADS / 64)),
-				   dim3(RW_THREADS), 0, s, logits, T, L.E, k, topk_idx, topk_w);
+	hipLaunchKernelGGL(router_topk_kernel, dim3((T + RW_THREADS / 64 - 1) / (RW_THREADS / 64)), dim3(RW_THREADS), 0,
+			   s, logits, T, L.E, k, topk_idx, topk_w);
 	return hipGetLastError();
 }
 

@@ -125,6 +125,9 @@ def make_input(seed, T, d):
 # The workload configs of the MoE block benchmark (30B-A3B / 235B-A22B shapes).
 CONFIGS = {
     "30b_t1": dict(d=2048, F=768, E=128, k=8, T=1, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1234),
+    "30b_t2": dict(d=2048, F=768, E=128, k=8, T=2, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1242),
+    "30b_t4": dict(d=2048, F=768, E=128, k=8, T=4, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1244),
+    "30b_t8": dict(d=2048, F=768, E=128, k=8, T=8, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1240),
     "30b_t32": dict(d=2048, F=768, E=128, k=8, T=32, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1235),
     "30b_t2048": dict(d=2048, F=768, E=128, k=8, T=2048, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1236),
     "30b_bf16_zipf_t512": dict(d=2048, F=768, E=128, k=8, T=512, gu_type=BF16, down_type=BF16, zipf=1.2,
