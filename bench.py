@@ -67,10 +67,12 @@ def gen_device_layer(torch, cfg, seed):
     gate = expert(cfg["gu_type"], F, d)
     up = expert(cfg["gu_type"], F, d)
     down = expert(cfg["down_type"], d, F)
-    bias = None
+    bias = pbias = None
     if cfg.get("zipf"):
         bias = torch.from_numpy(synth.zipf_bias(E, s=cfg["zipf"], seed=seed + 7)).to(dev)
-    return router, gate, up, down, bias
+    if cfg.get("probs_bias"):
+        pbias = torch.randn(E, generator=g, device=dev) * cfg["probs_bias"]
+    return router, gate, up, down, bias, pbias
 
 
 class Workload:
@@ -79,9 +81,10 @@ class Workload:
         self.layers = []
         self.layer_bytes = 0
         for i in range(n_layers):
-            r, g, u, dn, b = gen_device_layer(torch, cfg, seed0 + 17 * i)
+            r, g, u, dn, b, pb = gen_device_layer(torch, cfg, seed0 + 17 * i)
             L = tie_amd.Layer(cfg["d"], cfg["F"], cfg["E"], r, g, u, dn, cfg["gu_type"], cfg["gu_type"],
-                              cfg["down_type"], bias=b, on_device=True)
+                              cfg["down_type"], bias=b, on_device=True, routing=cfg.get("routing", 0),
+                              probs_bias=pb)
             self.layer_bytes = L.nbytes()
             self.layers.append(L)
             del r, g, u, dn
@@ -216,7 +219,8 @@ def cpu_baseline(cfg, k, budget_s=12.0):
     from oracle import bind
     from tie_amd import synth
     layer = synth.make_layer(cfg["seed"], cfg["d"], cfg["F"], cfg["E"], cfg["gu_type"], cfg["down_type"],
-                             zipf=cfg.get("zipf"))
+                             zipf=cfg.get("zipf"), routing=cfg.get("routing", 0),
+                             probs_bias=cfg.get("probs_bias"))
     T = min(cfg["T"], 32)
     x = synth.make_input(cfg["seed"], T, cfg["d"])
     threads = 8  # TIE runs the k = 8 experts of a token as 8 pool tasks (model_qwen3.c:446-456)

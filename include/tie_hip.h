@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define TIE_HIP_ABI_VERSION 1
+#define TIE_HIP_ABI_VERSION 2
 
 /* GGML type ids as in gguf.h:8-36 */
 #define TIE_GGML_F32 0
@@ -44,6 +44,11 @@ extern "C" {
 #define TIE_HIP_PATH_AUTO 0x0  /* exact fp32 GEMV path for small T, bf16 MFMA grouped GEMM above */
 #define TIE_HIP_PATH_EXACT 0x1 /* always the fp32 path that reproduces TIE's arithmetic bit for bit */
 #define TIE_HIP_PATH_MFMA 0x2  /* always the grouped-GEMM path */
+
+/* Routing modes (tie_hip_layer_desc.routing) */
+#define TIE_HIP_ROUTE_SOFTMAX 0 /* Qwen3: top-k of the logits, softmax over the k (model_qwen3.c:431-443) */
+#define TIE_HIP_ROUTE_SIGMOID 1 /* LFM2: sigmoid, top-k of sigmoid + bias, L1-normalised sigmoid of the k
+				   (model_lfm2.c:437-467) */
 
 typedef struct tie_hip_layer tie_hip_layer;
 
@@ -76,6 +81,18 @@ int tie_hip_moe_ffn(const float *x, int T, int d, int F, int E, int k, const voi
 		    const void *gate_exps, int gate_type, const void *up_exps, int up_type, const void *down_exps,
 		    int down_type, float *out, int32_t *topk_idx_opt, float *topk_w_opt);
 
+/* Drop-in for the MoE branch of transformer_layer_lfm2
+ * (model_lfm2.c:414-497).  Same arguments as tie_hip_moe_ffn plus
+ *   probs_bias_opt  exp_probs_b_bias, F32 [E] host array, or NULL (the
+ *                   branch at model_lfm2.c:446-454)
+ * Routing is TIE_HIP_ROUTE_SIGMOID: p_e = 1/(1+expf(-logit_e)), top-k of
+ * p_e + bias_e, weights p_j / (sum_j p_j + 1e-6); the experts and the
+ * combine are those of tie_hip_moe_ffn. */
+int tie_hip_moe_ffn_lfm2(const float *x, int T, int d, int F, int E, int k, const void *router_w, int router_type,
+			 const float *probs_bias_opt, const void *gate_exps, int gate_type, const void *up_exps,
+			 int up_type, const void *down_exps, int down_type, float *out, int32_t *topk_idx_opt,
+			 float *topk_w_opt);
+
 /* Replace the SiLU lookup table with the caller's (TIE's own silu_table,
  * engine.c:12, as filled by silu_table_init, engine.c:297-303). */
 int tie_hip_set_silu_table(const float *table, int n);
@@ -102,6 +119,9 @@ typedef struct tie_hip_layer_desc {
 	int src_on_device;        /* 1: the pointers above are device memory (GGUF layout) */
 	int literal_bf16_stride;  /* 1: BF16 experts start at e*rows*(in/256)*2 bytes, as
 				     process_expert_task computes it (engine.c:929-942) */
+	int routing;              /* TIE_HIP_ROUTE_SOFTMAX (0, Qwen3) or TIE_HIP_ROUTE_SIGMOID (LFM2) */
+	const float *probs_bias;  /* optional [E]: LFM2's exp_probs_b_bias, added to the sigmoid
+				     scores for the selection only (ROUTE_SIGMOID) */
 } tie_hip_layer_desc;
 
 /* Upload (or copy on device) and repack one layer's weights into the

@@ -51,8 +51,9 @@ def oracle():
         lib.orc_find_top_k.argtypes = [_P, _I, _I, _P, _P]
         lib.orc_softmax.argtypes = [_P, _I]
         lib.orc_moe_block.restype = _I
-        lib.orc_moe_block.argtypes = [_P, _I, _I, _I, _I, _I, _P, _P, _P, _I, _P, _I, _P, _I, _I, _P, _P, _P,
-                                      _P, _P, _I]
+        lib.orc_moe_block.argtypes = [_P, _I, _I, _I, _I, _I, _P, _P, _I, _P, _P, _I, _P, _I, _P, _I, _I, _P,
+                                      _P, _P, _P, _P, _I]
+        lib.orc_sigmoid_route.argtypes = [_P, _I, _I, _P, _P, _P]
         lib.orc_dequant_q4k.argtypes = [_P, _I, _P]
         lib.orc_dequant_q6k.argtypes = [_P, _I, _P]
         lib.orc_expf_array.argtypes = [_P, _P, ctypes.c_size_t]
@@ -74,8 +75,8 @@ def ref():
         lib.ref_silu_table.argtypes = [_P, _I]
         lib.ref_pool_threads.restype = _I
         lib.ref_moe_block.restype = _I
-        lib.ref_moe_block.argtypes = [_P, _I, _I, _I, _I, _I, _P, _P, _P, _I, _P, _I, _P, _I, _I, _P, _P, _P,
-                                      _P, _I]
+        lib.ref_moe_block.argtypes = [_P, _I, _I, _I, _I, _I, _P, _P, _I, _P, _P, _I, _P, _I, _P, _I, _I, _P,
+                                      _P, _P, _P, _I]
         _ref = lib
     return _ref
 
@@ -98,6 +99,7 @@ def moe_block(layer, x, k, silu_tab=None, literal_bf16_stride=False, nthreads=8,
     w = np.empty((T, k), np.float32)
     logits = np.empty((T, layer.E), np.float32) if with_logits else None
     rc = oracle().orc_moe_block(_ptr(x), T, d, layer.F, layer.E, k, _ptr(layer.router), _ptr(layer.bias),
+                                int(getattr(layer, "routing", 0)), _ptr(getattr(layer, "probs_bias", None)),
                                 _ptr(layer.gate), layer.gate_type, _ptr(layer.up), layer.up_type,
                                 _ptr(layer.down), layer.down_type, int(literal_bf16_stride), _ptr(silu_tab),
                                 _ptr(out), _ptr(idx), _ptr(w), _ptr(logits), nthreads)
@@ -115,6 +117,7 @@ def ref_moe_block(layer, x, k, literal_bf16_stride=False, nthreads=8, with_logit
     w = np.empty((T, k), np.float32)
     logits = np.empty((T, layer.E), np.float32) if with_logits else None
     rc = ref().ref_moe_block(_ptr(x), T, d, layer.F, layer.E, k, _ptr(layer.router), _ptr(layer.bias),
+                             int(getattr(layer, "routing", 0)), _ptr(getattr(layer, "probs_bias", None)),
                              _ptr(layer.gate), layer.gate_type, _ptr(layer.up), layer.up_type, _ptr(layer.down),
                              layer.down_type, int(literal_bf16_stride), _ptr(out), _ptr(idx), _ptr(w),
                              _ptr(logits), nthreads)

@@ -15,6 +15,11 @@
  * own dispatch_mat_vec, find_top_k, softmax, process_expert_task and
  * dispatch_convert.
  *
+ * routing == 1 runs the LFM2 selection of model_lfm2.c:437-467 instead
+ * (sigmoid, optional exp_probs_b_bias for the selection, L1-normalised
+ * weights), restated here over the reference's find_top_k, compiled with
+ * the reference's flags so the sigmoid and sum loops vectorise as TIE's do.
+ *
  * Two harness extensions, both off by default:
  *   router_bias  -- added to the router logits before top-k (the Zipf
  *                   routing config; TIE's Qwen3 path has no router bias);
@@ -98,7 +103,7 @@ static void expert_task_exact_stride(void *arg)
 }
 
 int ref_moe_block(const float *x, int T, int d, int F, int E, int k, const float *router_w, const float *router_bias,
-		  const void *gate_w, int gate_type, const void *up_w, int up_type, const void *down_w, int down_type,
+		  int routing, const float *probs_bias, const void *gate_w, int gate_type, const void *up_w, int up_type, const void *down_w, int down_type,
 		  int literal_bf16_stride, float *out, int32_t *topk_idx, float *topk_w, float *logits_out,
 		  int nthreads)
 {
@@ -158,11 +163,33 @@ int ref_moe_block(const float *x, int T, int d, int F, int E, int k, const float
 			memcpy(logits_out + (size_t)i * E, scores, sizeof(float) * E);
 
 		ExpertChoice top[k];
-		find_top_k(scores, E, k, top);
 		float gv[k];
-		for (int j = 0; j < k; j++)
-			gv[j] = top[j].score;
-		softmax(gv, k);
+		if (routing == 1) {
+			/* model_lfm2.c:437-467 */
+			for (int e = 0; e < E; e++)
+				scores[e] = 1.0f / (1.0f + expf(-scores[e]));
+			float selection_scores[E];
+			if (probs_bias) {
+				for (int e = 0; e < E; e++)
+					selection_scores[e] = scores[e] + probs_bias[e];
+			} else {
+				memcpy(selection_scores, scores, E * sizeof(float));
+			}
+			find_top_k(selection_scores, E, k, top);
+			float sum_weights = 0.0f;
+			for (int j = 0; j < k; j++) {
+				gv[j] = top[j].index >= 0 ? scores[top[j].index] : 0.0f;
+				sum_weights += gv[j];
+			}
+			float inv_sum = 1.0f / (sum_weights + 1e-6f);
+			for (int j = 0; j < k; j++)
+				gv[j] *= inv_sum;
+		} else {
+			find_top_k(scores, E, k, top);
+			for (int j = 0; j < k; j++)
+				gv[j] = top[j].score;
+			softmax(gv, k);
+		}
 
 		for (int j = 0; j < k; j++) {
 			tasks[j] = (expert_task_t){

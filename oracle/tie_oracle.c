@@ -447,6 +447,30 @@ void orc_softmax(float *v, int n)
 		v[i] = v[i] * inv;
 }
 
+/* LFM2 routing (model_lfm2.c:437-467): p_e = 1 / (1 + expf(-l_e)) (libm
+ * expf, IEEE division); top-k (find_top_k) over p_e + bias_e (bias
+ * optional); the weights are the unbiased p of the selected experts over
+ * their serial sum + 1e-6, as a multiply by the reciprocal.  Unfilled
+ * slots (index -1) get weight 0 (TIE would read scores[-1]). */
+void orc_sigmoid_route(const float *logits, int E, int k, const float *probs_bias, int32_t *idx, float *w)
+{
+	float p[1024], sel[1024];
+	for (int e = 0; e < E; e++) {
+		p[e] = 1.0f / (1.0f + expf(-logits[e]));
+		sel[e] = probs_bias ? p[e] + probs_bias[e] : p[e];
+	}
+	float score[ORC_MAX_K];
+	orc_find_top_k(sel, E, k, idx, score);
+	float sum = 0.0f;
+	for (int j = 0; j < k; j++) {
+		w[j] = idx[j] >= 0 ? p[idx[j]] : 0.0f;
+		sum = sum + w[j];
+	}
+	float inv = 1.0f / (sum + 1e-6f);
+	for (int j = 0; j < k; j++)
+		w[j] = w[j] * inv;
+}
+
 /* ------------------------------------------------------------------ */
 /* the block                                                            */
 /* ------------------------------------------------------------------ */
@@ -468,11 +492,13 @@ static int type_ok(int t)
 }
 
 int orc_moe_block(const float *x, int T, int d, int F, int E, int k, const float *router_w,
-		  const float *router_bias, const void *gate_w, int gate_type, const void *up_w, int up_type,
+		  const float *router_bias, int routing, const float *probs_bias, const void *gate_w, int gate_type, const void *up_w, int up_type,
 		  const void *down_w, int down_type, int literal_bf16_stride, const float *silu_tab, float *out,
 		  int32_t *topk_idx, float *topk_w, float *logits_out, int nthreads)
 {
-	if (T < 0 || d <= 0 || F <= 0 || E <= 0 || k <= 0 || k > E || k > ORC_MAX_K)
+	if (T < 0 || d <= 0 || F <= 0 || E <= 0 || E > 1024 || k <= 0 || k > E || k > ORC_MAX_K)
+		return -1;
+	if (routing != 0 && routing != 1)
 		return -1;
 	if (d % 256 || F % 256)
 		return -1;
@@ -500,8 +526,12 @@ int orc_moe_block(const float *x, int T, int d, int F, int E, int k, const float
 
 		int32_t sel[ORC_MAX_K];
 		float g[ORC_MAX_K];
-		orc_find_top_k(logits, E, k, sel, g);
-		orc_softmax(g, k);
+		if (routing == 1) {
+			orc_sigmoid_route(logits, E, k, probs_bias, sel, g);
+		} else {
+			orc_find_top_k(logits, E, k, sel, g);
+			orc_softmax(g, k);
+		}
 
 		memset(acc, 0, sizeof(float) * d);
 		for (int j = 0; j < k; j++) {

@@ -34,9 +34,10 @@ void orc_swiglu(float *gate, const float *up, int n, const float *tab);
 
 void orc_find_top_k(const float *logits, int E, int k, int32_t *idx, float *score);
 void orc_softmax(float *v, int n);
+void orc_sigmoid_route(const float *logits, int E, int k, const float *probs_bias, int32_t *idx, float *w);
 
 int orc_moe_block(const float *x, int T, int d, int F, int E, int k, const float *router_w,
-		  const float *router_bias, const void *gate_w, int gate_type, const void *up_w, int up_type,
+		  const float *router_bias, int routing, const float *probs_bias, const void *gate_w, int gate_type, const void *up_w, int up_type,
 		  const void *down_w, int down_type, int literal_bf16_stride, const float *silu_tab, float *out,
 		  int32_t *topk_idx, float *topk_w, float *logits_out, int nthreads);
 

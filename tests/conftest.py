@@ -22,23 +22,28 @@ def load_golden(name):
 
 
 @functools.lru_cache(maxsize=None)
-def synth_layer(seed, d, F, E, gu, dn, zipf):
+def synth_layer(seed, d, F, E, gu, dn, zipf, routing=0, probs_bias=None):
     from tie_amd import synth
-    return synth.make_layer(seed, d, F, E, gu, dn, zipf=zipf)
+    return synth.make_layer(seed, d, F, E, gu, dn, zipf=zipf, routing=routing, probs_bias=probs_bias)
 
 
 def golden_layer(g):
     """Regenerate the weights of a golden case (cached per session)."""
     import copy
     zipf = float(g["zipf"]) or None
+    routing = int(g["routing"]) if "routing" in g else 0
+    pb = float(g["probs_bias"]) if "probs_bias" in g else 0.0
     layer = synth_layer(int(g["seed"]), int(g["d"]), int(g["F"]), int(g["E"]), int(g["gu_type"]),
-                        int(g["down_type"]), zipf)
+                        int(g["down_type"]), zipf, routing, pb or None)
     ties = g["tie_rows"].reshape(-1, 2)
-    if len(ties):
+    sat = g["sat_rows"] if "sat_rows" in g else np.zeros(0, np.int32)
+    if len(ties) or len(sat):
         layer = copy.copy(layer)
         layer.router = layer.router.copy()
         for a, b in ties:
             layer.router[b] = layer.router[a]
+        for r in sat:
+            layer.router[r] *= np.float32(100.0)
     return layer
 
 

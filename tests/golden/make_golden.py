@@ -26,7 +26,10 @@ from tie_amd import synth  # noqa: E402
 
 OUT = os.path.dirname(os.path.abspath(__file__))
 
-# name: (d, F, E, k, T, gate/up type, down type, zipf, seed, literal_bf16_stride, tie_rows)
+# name: (d, F, E, k, T, gate/up type, down type, zipf, seed, literal_bf16_stride, tie_rows[, lfm2])
+# lfm2 = (probs_bias std or 0, rows scaled by 100): sigmoid routing (model_lfm2.c:437-467); the
+# scaled rows give logits far outside [-20, 20], whose sigmoids saturate to
+# 1.0 (or 0.0) and tie, exercising find_top_k's index order on equal p.
 CASES = {
     "g30b_q4k_t4": (2048, 768, 128, 8, 4, synth.Q4_K, synth.Q6_K, None, 1234, 0, None),
     "g235b_e16_t2": (4096, 1536, 16, 8, 2, synth.Q4_K, synth.Q6_K, None, 1238, 0, None),
@@ -35,6 +38,8 @@ CASES = {
     "gtiny_ties_t6": (256, 256, 16, 4, 6, synth.Q4_K, synth.Q6_K, None, 9, 0, ((3, 5), (5, 11), (0, 1))),
     "g30b_bf16_zipf_t4": (2048, 768, 128, 8, 4, synth.BF16, synth.BF16, 1.2, 1237, 0, None),
     "g30b_bf16_zipf_literal_t4": (2048, 768, 128, 8, 4, synth.BF16, synth.BF16, 1.2, 1237, 1, None),
+    "glfm2_t4": (2048, 1792, 32, 4, 4, synth.Q4_K, synth.Q6_K, None, 1250, 0, None, (0.05, ())),
+    "glfm2_sat_t6": (512, 512, 32, 4, 6, synth.Q4_K, synth.Q6_K, None, 1252, 0, None, (0.0, (2, 9, 17, 30))),
 }
 
 
@@ -53,24 +58,36 @@ def cpu_identity():
 
 
 def build_case(name, spec):
-    d, F, E, k, T, gu, dn, zipf, seed, literal, tie_rows = spec
-    layer = synth.make_layer(seed, d, F, E, gu, dn, zipf=zipf)
+    d, F, E, k, T, gu, dn, zipf, seed, literal, tie_rows = spec[:11]
+    pb, sat = spec[11] if len(spec) > 11 else (None, ())
+    lfm2 = len(spec) > 11
+    layer = synth.make_layer(seed, d, F, E, gu, dn, zipf=zipf, routing=1 if lfm2 else 0, probs_bias=pb or None)
     if tie_rows:
         # identical router rows -> identical logits: exercises find_top_k's tie order
         for a, b in tie_rows:
             layer.router[b] = layer.router[a]
+    for r in sat:
+        layer.router[r] *= np.float32(100.0)
     x = synth.make_input(seed, T, d)
     out, idx, w, logits = bind.ref_moe_block(layer, x, k, literal_bf16_stride=bool(literal), with_logits=True)
-    return dict(name=name, d=d, F=F, E=E, k=k, T=T, gu_type=gu, down_type=dn, zipf=zipf or 0.0, seed=seed,
-                literal=literal, tie_rows=np.array(tie_rows or [], np.int32).reshape(-1, 2),
-                digest=layer.digest(), x=x, out=out, topk_idx=idx, topk_w=w, logits=logits,
-                cpu=cpu_identity())
+    c = dict(name=name, d=d, F=F, E=E, k=k, T=T, gu_type=gu, down_type=dn, zipf=zipf or 0.0, seed=seed,
+             literal=literal, tie_rows=np.array(tie_rows or [], np.int32).reshape(-1, 2),
+             digest=layer.digest(), x=x, out=out, topk_idx=idx, topk_w=w, logits=logits,
+             cpu=cpu_identity())
+    if lfm2:
+        c.update(routing=1, probs_bias=pb or 0.0, sat_rows=np.array(sat, np.int32))
+    return c
 
 
 def main():
-    tab = bind.ref_silu_table()
-    np.savez_compressed(os.path.join(OUT, "silu_table.npz"), table=tab, cpu=cpu_identity())
-    for name, spec in CASES.items():
+    """python make_golden.py [case ...]: the named cases (default: all, and
+    the SiLU table)."""
+    names = sys.argv[1:] or list(CASES)
+    if not sys.argv[1:]:
+        tab = bind.ref_silu_table()
+        np.savez_compressed(os.path.join(OUT, "silu_table.npz"), table=tab, cpu=cpu_identity())
+    for name in names:
+        spec = CASES[name]
         c = build_case(name, spec)
         np.savez_compressed(os.path.join(OUT, name + ".npz"), **c)
         print(name, "max|out| = %.4g" % np.abs(c["out"]).max())

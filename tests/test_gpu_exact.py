@@ -66,6 +66,30 @@ def test_golden_cases(name):
         assert_same(out, g["out"], "golden out")
 
 
+@pytest.mark.parametrize("name", ["glfm2_t4", "glfm2_sat_t6"])
+def test_lfm2_golden_cases(name):
+    """Sigmoid routing (tie_hip_moe_ffn_lfm2): bit-exact against the oracle
+    (both use the scalar expf and IEEE division); against the compiled
+    reference's vectors within the LFM2 bar (its sigmoid loop is vectorised
+    under -ffast-math): selection equal, weights within 1e-6 relative."""
+    g = load_golden(name)
+    layer = golden_layer(g)
+    out, idx, w = run_both(layer, g["x"], int(g["k"]))
+    assert_same(idx, g["topk_idx"], "golden topk_idx")
+    np.testing.assert_allclose(w, g["topk_w"], rtol=1e-6, atol=0)
+    if str(g["cpu"]) == host_cpu_identity():
+        assert np.abs(out - g["out"]).max() <= 1e-6 * np.abs(g["out"]).max()
+
+
+def test_lfm2_one_token_without_bias():
+    """One token routes inside the gate/up workgroups (sigmoid mode, no
+    selection bias), and E > 128 goes through the grouping kernel."""
+    for E in (32, 200):
+        layer = synth_layer(27 + E, 512, 256, E, synth.Q4_K, synth.Q6_K, None, 1, None)
+        for T, k in [(1, 4), (1, 8), (7, 4)]:
+            run_both(layer, synth.make_input(27 + T, T, 512), k)
+
+
 @pytest.mark.parametrize("name,literal", [("g30b_bf16_zipf_t4", False), ("g30b_bf16_zipf_literal_t4", True)])
 def test_golden_bf16_zipf_device_api(name, literal):
     import torch
@@ -88,10 +112,11 @@ def test_golden_bf16_zipf_device_api(name, literal):
     L.close()
 
 
-@pytest.mark.parametrize("cfg", ["30b_t1", "30b_t8", "30b_t32", "235b_t1"])
+@pytest.mark.parametrize("cfg", ["30b_t1", "30b_t8", "30b_t32", "235b_t1", "lfm2_t1", "lfm2_t32"])
 def test_full_size_configs(cfg):
     c = synth.CONFIGS[cfg]
-    layer = synth_layer(c["seed"], c["d"], c["F"], c["E"], c["gu_type"], c["down_type"], c["zipf"])
+    layer = synth_layer(c["seed"], c["d"], c["F"], c["E"], c["gu_type"], c["down_type"], c["zipf"],
+                        c.get("routing", 0), c.get("probs_bias"))
     x = synth.make_input(c["seed"], c["T"], c["d"])
     run_both(layer, x, c["k"])
 

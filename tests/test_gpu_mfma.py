@@ -147,3 +147,20 @@ def test_full_prefill_30b_routing_exact_and_sampled_outputs():
     e = rel_l2(out[sample], ro)
     print("T=2048 sampled rel L2 vs oracle %.3g" % e, flush=True)
     assert e <= 2e-2
+
+
+def test_lfm2_prefill_routing_exact():
+    """Sigmoid routing on the MFMA path (separate selection kernel at large
+    T): selection and weights bit-exact against the oracle, outputs within
+    the bf16 bound."""
+    c = synth.CONFIGS["lfm2_t32"]
+    layer = synth_layer(c["seed"], c["d"], c["F"], c["E"], c["gu_type"], c["down_type"], None, 1, c["probs_bias"])
+    T = 300
+    x = synth.make_input(c["seed"] + 5, T, c["d"])
+    out, idx, w = run_mfma(layer, x, c["k"])
+    ro, ri, rw = bind.moe_block(layer, x, c["k"])
+    np.testing.assert_array_equal(idx, ri)
+    np.testing.assert_array_equal(bits(w), bits(rw))
+    e = rel_l2(out, ro)
+    print("lfm2 T=300 rel L2 vs oracle %.3g" % e, flush=True)
+    assert e <= 2e-2

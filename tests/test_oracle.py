@@ -63,6 +63,96 @@ def test_oracle_matches_reference_fresh_inputs(seed):
         np.testing.assert_array_equal(bits(p), bits(q))
 
 
+def near_tie_tokens(sel_scores, k):
+    """Tokens whose k-th and (k+1)-th selection scores differ by less than
+    1e-5 (the tolerance band of the selection parity)."""
+    s = -np.sort(-sel_scores.astype(np.float64), axis=1)
+    if s.shape[1] <= k:
+        return np.zeros(s.shape[0], bool)
+    return np.abs(s[:, k - 1] - s[:, k]) < 1e-5
+
+
+def assert_lfm2_close(a, b, k, sel_scores, what):
+    """LFM2 parity bar: the oracle computes the sigmoid with scalar libm
+    expf and IEEE division, TIE's compiled loop with the vectorised expf of
+    -ffast-math.  Selection equal except near-tie tokens (reported), gate
+    weights within 1e-6 relative, outputs within 1e-6 of max|out|."""
+    (oa, ia, wa), (ob, ib, wb) = a[:3], b[:3]
+    tie = near_tie_tokens(sel_scores, k)
+    print("%s: %d near-tie token(s) of %d" % (what, int(tie.sum()), len(tie)))
+    np.testing.assert_array_equal(ia[~tie], ib[~tie])
+    np.testing.assert_allclose(wa[~tie], wb[~tie], rtol=1e-6, atol=0)
+    ok = ~tie
+    scale = float(np.abs(ob[ok]).max()) if ok.any() else 1.0
+    err = float(np.abs(oa[ok] - ob[ok]).max()) if ok.any() else 0.0
+    rel_l2 = float(np.linalg.norm(oa[ok] - ob[ok]) / max(np.linalg.norm(ob[ok]), 1e-30)) if ok.any() else 0.0
+    print("%s: max|diff| %.3g of max|out| %.3g, rel L2 %.3g" % (what, err, scale, rel_l2))
+    assert err <= 1e-6 * scale
+
+
+def lfm2_selection_scores(layer, logits):
+    p = 1.0 / (1.0 + np.exp(-logits.astype(np.float64)))
+    return p + (layer.probs_bias if layer.probs_bias is not None else 0.0)
+
+
+@pytest.mark.parametrize("name", ["glfm2_t4", "glfm2_sat_t6"])
+def test_lfm2_oracle_matches_reference_golden(name):
+    g = load_golden(name)
+    layer = golden_layer(g)
+    assert layer.digest() == str(g["digest"]), "synthetic generator changed"
+    k = int(g["k"])
+    res = bind.moe_block(layer, g["x"], k, with_logits=True)
+    np.testing.assert_array_equal(bits(res[3]), bits(g["logits"]))
+    if str(g["cpu"]) != host_cpu_identity():
+        # outputs depend on the host's SiLU table; selection and weights do not
+        tie = near_tie_tokens(lfm2_selection_scores(layer, g["logits"]), k)
+        np.testing.assert_array_equal(res[1][~tie], g["topk_idx"][~tie])
+        np.testing.assert_allclose(res[2][~tie], g["topk_w"][~tie], rtol=1e-6, atol=0)
+        pytest.skip("outputs depend on the SiLU table of %s" % g["cpu"])
+    assert_lfm2_close(res, (g["out"], g["topk_idx"], g["topk_w"]), k,
+                      lfm2_selection_scores(layer, g["logits"]), name)
+
+
+@pytest.mark.skipif(not bind.ref_available(), reason="reference build absent")
+@pytest.mark.parametrize("seed,pb", [(13, 0.05), (14, None)])
+def test_lfm2_oracle_matches_reference_fresh_inputs(seed, pb):
+    layer = synth.make_layer(seed, 512, 512, 32, synth.Q4_K, synth.Q6_K, routing=1, probs_bias=pb)
+    x = synth.make_input(seed, 24, 512)
+    a = bind.moe_block(layer, x, 4, with_logits=True)
+    b = bind.ref_moe_block(layer, x, 4, with_logits=True)
+    np.testing.assert_array_equal(bits(a[3]), bits(b[3]))
+    assert_lfm2_close(a, b, 4, lfm2_selection_scores(layer, a[3]), "lfm2 seed %d" % seed)
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_sigmoid_route_closed_form(seed):
+    """orc_sigmoid_route against float64: selection = stable descending sort
+    of sigmoid + bias (away from near ties), weights = p / (sum p + 1e-6),
+    and saturated logits tie at p = 1 and fall back to the index order."""
+    rng = np.random.default_rng(100 + seed)
+    E = int(rng.integers(4, 160))
+    k = int(rng.integers(1, min(E, 16) + 1))
+    logits = rng.normal(0, 3, size=E).astype(np.float32)
+    logits[rng.integers(0, E, 3)] = 40.0  # sigmoid(40) == 1.0f
+    bias = rng.normal(0, 0.05, size=E).astype(np.float32) if seed % 2 else None
+    idx = np.empty(k, np.int32)
+    w = np.empty(k, np.float32)
+    bind.oracle().orc_sigmoid_route(logits.ctypes.data, E, k, None if bias is None else bias.ctypes.data,
+                                    idx.ctypes.data, w.ctypes.data)
+    p32 = (1.0 / (1.0 + np.exp(-logits.astype(np.float64)))).astype(np.float32)
+    sel = p32 + (bias if bias is not None else np.float32(0.0))
+    order = sorted(range(E), key=lambda e: (-float(sel[e]), e))
+    # a float64 sigmoid can differ from libm's expf by an ulp: compare the
+    # order where no two of the top k+1 scores are within 1e-6 (exact ties,
+    # such as the saturated p = 1, are computed exactly by both)
+    gap = np.abs(np.diff(-np.sort(-sel.astype(np.float64))))[:k]
+    if not ((gap > 0) & (gap < 1e-6)).any():
+        assert list(idx) == order[:k]
+    p = p32[idx].astype(np.float64)
+    np.testing.assert_allclose(w, p / (p.sum() + 1e-6), rtol=1e-6)
+    assert abs(float(w.astype(np.float64).sum()) - p.sum() / (p.sum() + 1e-6)) < 1e-6
+
+
 # ---------------------------------------------------------------- closed forms
 def test_fp16_conversion_all_values():
     h = np.arange(65536, dtype=np.uint32)

@@ -18,11 +18,13 @@ LIB_PATH = os.environ.get("TIE_AMD_LIB") or os.path.join(HERE, "libtie_hip.so")
 F32, Q4_K, Q6_K, BF16 = 0, 12, 14, 30
 OK, EINVAL, EHIP, ENOMEM, ENOINIT = 0, -1, -2, -3, -4
 PATH_AUTO, PATH_EXACT, PATH_MFMA = 0, 1, 2
+ROUTE_SOFTMAX, ROUTE_SIGMOID = 0, 1
 SILU_TABLE_SIZE = 8192
 
 # every symbol include/tie_hip.h declares
 EXPORTS = (
-    "tie_hip_init", "tie_hip_shutdown", "tie_hip_last_error", "tie_hip_moe_ffn", "tie_hip_set_silu_table",
+    "tie_hip_init", "tie_hip_shutdown", "tie_hip_last_error", "tie_hip_moe_ffn", "tie_hip_moe_ffn_lfm2",
+    "tie_hip_set_silu_table",
     "tie_hip_silu_table_host", "tie_hip_layer_create", "tie_hip_layer_destroy", "tie_hip_layer_bytes",
     "tie_hip_moe_forward", "tie_hip_exact_max_tokens", "tie_hip_set_exact_max_tokens",
     "tie_hip_debug_fail_alloc", "tie_hip_host_expf", "tie_hip_profile_enable", "tie_hip_profile_read",
@@ -45,6 +47,8 @@ class LayerDesc(ctypes.Structure):
         ("router_bias", ctypes.c_void_p),
         ("src_on_device", ctypes.c_int),
         ("literal_bf16_stride", ctypes.c_int),
+        ("routing", ctypes.c_int),
+        ("probs_bias", ctypes.c_void_p),
     ]
 
 
@@ -65,6 +69,8 @@ def lib():
         L.tie_hip_last_error.restype = ctypes.c_char_p
         L.tie_hip_moe_ffn.argtypes = [P, I, I, I, I, I, P, I, P, I, P, I, P, I, P, P, P]
         L.tie_hip_moe_ffn.restype = I
+        L.tie_hip_moe_ffn_lfm2.argtypes = [P, I, I, I, I, I, P, I, P, P, I, P, I, P, I, P, P, P]
+        L.tie_hip_moe_ffn_lfm2.restype = I
         L.tie_hip_set_silu_table.argtypes = [P, I]
         L.tie_hip_set_silu_table.restype = I
         L.tie_hip_silu_table_host.argtypes = [P, I]
@@ -155,18 +161,26 @@ def profile_read(max_kernels=32):
 
 
 def moe_ffn(x, layer, k, with_topk=True):
-    """tie_hip_moe_ffn on host arrays (the drop-in for model_qwen3.c:404-471).
-    `layer` is a tie_amd.synth.MoELayer (GGUF-layout host arrays)."""
+    """tie_hip_moe_ffn on host arrays (the drop-in for model_qwen3.c:404-471),
+    or tie_hip_moe_ffn_lfm2 (model_lfm2.c:414-497) for a layer with sigmoid
+    routing.  `layer` is a tie_amd.synth.MoELayer (GGUF-layout host arrays)."""
     x = np.ascontiguousarray(x, np.float32)
     T, d = x.shape
     out = np.empty((T, d), np.float32)
     idx = np.empty((T, k), np.int32) if with_topk else None
     w = np.empty((T, k), np.float32) if with_topk else None
     if layer.bias is not None:
-        raise ValueError("tie_hip_moe_ffn has no router bias (TIE has none); use Layer for biased routing")
-    check(lib().tie_hip_moe_ffn(_p(x), T, d, layer.F, layer.E, k, _p(layer.router), F32, _p(layer.gate),
-                                layer.gate_type, _p(layer.up), layer.up_type, _p(layer.down), layer.down_type,
-                                _p(out), _p(idx), _p(w)))
+        raise ValueError("the host drop-ins take no logit bias (TIE has none); use Layer for biased routing")
+    if getattr(layer, "routing", ROUTE_SOFTMAX) == ROUTE_SIGMOID:
+        # tie_hip_moe_ffn_lfm2: the drop-in for model_lfm2.c:414-497
+        check(lib().tie_hip_moe_ffn_lfm2(_p(x), T, d, layer.F, layer.E, k, _p(layer.router), F32,
+                                         _p(layer.probs_bias), _p(layer.gate), layer.gate_type, _p(layer.up),
+                                         layer.up_type, _p(layer.down), layer.down_type, _p(out), _p(idx),
+                                         _p(w)))
+    else:
+        check(lib().tie_hip_moe_ffn(_p(x), T, d, layer.F, layer.E, k, _p(layer.router), F32, _p(layer.gate),
+                                    layer.gate_type, _p(layer.up), layer.up_type, _p(layer.down),
+                                    layer.down_type, _p(out), _p(idx), _p(w)))
     return out, idx, w
 
 
@@ -175,10 +189,10 @@ class Layer:
     host numpy arrays or device tensors (anything with data_ptr())."""
 
     def __init__(self, d, F, E, router, gate, up, down, gate_type, up_type, down_type, bias=None,
-                 on_device=False, literal_bf16_stride=False):
+                 on_device=False, literal_bf16_stride=False, routing=ROUTE_SOFTMAX, probs_bias=None):
         self.d, self.F, self.E = d, F, E
         desc = LayerDesc(d, F, E, _p(router), F32, _p(gate), gate_type, _p(up), up_type, _p(down), down_type,
-                         _p(bias), int(on_device), int(literal_bf16_stride))
+                         _p(bias), int(on_device), int(literal_bf16_stride), int(routing), _p(probs_bias))
         h = ctypes.c_void_p()
         check(lib().tie_hip_layer_create(ctypes.byref(desc), ctypes.byref(h)))
         self.handle = h
@@ -186,7 +200,8 @@ class Layer:
     @classmethod
     def from_synth(cls, s, literal_bf16_stride=False):
         return cls(s.d, s.F, s.E, s.router, s.gate, s.up, s.down, s.gate_type, s.up_type, s.down_type,
-                   bias=s.bias, literal_bf16_stride=literal_bf16_stride)
+                   bias=s.bias, literal_bf16_stride=literal_bf16_stride,
+                   routing=getattr(s, "routing", ROUTE_SOFTMAX), probs_bias=getattr(s, "probs_bias", None))
 
     def nbytes(self):
         return lib().tie_hip_layer_bytes(self.handle)

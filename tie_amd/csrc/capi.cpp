@@ -29,7 +29,8 @@ struct Ctx {
 	float *silu = nullptr;
 	Workspace ws;
 	// host-pointer API: cached layers and staging buffers
-	std::map<std::tuple<const void *, const void *, const void *, const void *, int, int, int, int, int, int>,
+	std::map<std::tuple<const void *, const void *, const void *, const void *, int, int, int, int, int, int, int,
+			    const void *>,
 		 tie_hip_layer *>
 		cache;
 	float *x_dev = nullptr, *out_dev = nullptr, *w_dev = nullptr;
@@ -257,6 +258,10 @@ static int create_layer(const tie_hip_layer_desc *ds, tie_hip_layer **out)
 				 ds->up_type, ds->down_type);
 	if (!ds->router_w || !ds->gate_exps || !ds->up_exps || !ds->down_exps)
 		return set_error(TIE_HIP_EINVAL, "null weight pointer");
+	if (ds->routing != TIE_HIP_ROUTE_SOFTMAX && ds->routing != TIE_HIP_ROUTE_SIGMOID)
+		return set_error(TIE_HIP_EINVAL, "routing mode %d unknown", ds->routing);
+	if (ds->probs_bias && ds->routing != TIE_HIP_ROUTE_SIGMOID)
+		return set_error(TIE_HIP_EINVAL, "probs_bias needs TIE_HIP_ROUTE_SIGMOID");
 
 	const int d = ds->d, F = ds->F, E = ds->E;
 	tie_hip_layer *l = new tie_hip_layer();
@@ -278,7 +283,8 @@ static int create_layer(const tie_hip_layer_desc *ds, tie_hip_layer **out)
 	const size_t b_router = align256((size_t)E * d * 4), b_bias = align256((size_t)E * 4);
 	const size_t b_gate = align256(E * L.gate.expert_bytes), b_up = align256(E * L.up.expert_bytes),
 		     b_down = align256(E * L.down.expert_bytes);
-	L.bytes = 2 * b_router + b_bias + b_gate + b_up + b_down;
+	// [router | router bias | selection bias | transposed router | gate | up | down]
+	L.bytes = 2 * b_router + 2 * b_bias + b_gate + b_up + b_down;
 	rc = dev_malloc(&L.alloc, L.bytes, "layer weights");
 	if (rc) {
 		delete l;
@@ -287,8 +293,10 @@ static int create_layer(const tie_hip_layer_desc *ds, tie_hip_layer **out)
 	uint8_t *base = (uint8_t *)L.alloc;
 	L.router = (const float *)base;
 	L.bias = ds->router_bias ? (const float *)(base + b_router) : nullptr;
-	L.routerT = (const float *)(base + b_router + b_bias);
-	L.gate.data = base + 2 * b_router + b_bias;
+	L.routing = ds->routing;
+	L.pbias = ds->probs_bias ? (const float *)(base + b_router + b_bias) : nullptr;
+	L.routerT = (const float *)(base + b_router + 2 * b_bias);
+	L.gate.data = base + 2 * b_router + 2 * b_bias;
 	L.up.data = L.gate.data + b_gate;
 	L.down.data = L.up.data + b_up;
 
@@ -296,6 +304,8 @@ static int create_layer(const tie_hip_layer_desc *ds, tie_hip_layer **out)
 	hipError_t e = hipMemcpyAsync((void *)L.router, ds->router_w, (size_t)E * d * 4, kind, g.stream);
 	if (e == hipSuccess && ds->router_bias)
 		e = hipMemcpyAsync((void *)L.bias, ds->router_bias, (size_t)E * 4, kind, g.stream);
+	if (e == hipSuccess && ds->probs_bias)
+		e = hipMemcpyAsync((void *)L.pbias, ds->probs_bias, (size_t)E * 4, kind, g.stream);
 	if (e == hipSuccess)
 		e = launch_router_transpose(L, g.stream);
 	struct Src {
@@ -490,10 +500,13 @@ extern "C" int tie_hip_moe_forward(tie_hip_layer *layer, const float *x_dev, int
 	return forward(layer, x_dev, T, k, out_dev, topk_idx_dev, topk_w_dev, flags, s);
 }
 
-extern "C" int tie_hip_moe_ffn(const float *x, int T, int d, int F, int E, int k, const void *router_w,
-			       int router_type, const void *gate_exps, int gate_type, const void *up_exps, int up_type,
-			       const void *down_exps, int down_type, float *out, int32_t *topk_idx_opt,
-			       float *topk_w_opt)
+// The host-buffer drop-ins: the layer comes from the weight cache (uploaded
+// at the first call with these weights), x goes up, out and the selection
+// come back, and the call returns after the stream has drained.
+static int moe_ffn_host(const float *x, int T, int d, int F, int E, int k, const void *router_w, int router_type,
+			int routing, const float *probs_bias, const void *gate_exps, int gate_type, const void *up_exps,
+			int up_type, const void *down_exps, int down_type, float *out, int32_t *topk_idx_opt,
+			float *topk_w_opt)
 {
 	std::lock_guard<std::recursive_mutex> lk(g.mu);
 	clear_error();
@@ -506,7 +519,7 @@ extern "C" int tie_hip_moe_ffn(const float *x, int T, int d, int F, int E, int k
 	if (T < 0 || (T > 0 && (!x || !out)))
 		return set_error(TIE_HIP_EINVAL, "bad T=%d or null x/out", T);
 	auto key = std::make_tuple(router_w, gate_exps, up_exps, down_exps, router_type, gate_type, up_type, down_type,
-				   d * 4096 + (F >> 8), E);
+				   d * 4096 + (F >> 8), E, routing, (const void *)probs_bias);
 	tie_hip_layer *layer = nullptr;
 	auto it = g.cache.find(key);
 	if (it != g.cache.end()) {
@@ -528,6 +541,8 @@ extern "C" int tie_hip_moe_ffn(const float *x, int T, int d, int F, int E, int k
 		ds.up_type = up_type;
 		ds.down_exps = down_exps;
 		ds.down_type = down_type;
+		ds.routing = routing;
+		ds.probs_bias = probs_bias;
 		rc = create_layer(&ds, &layer);
 		if (rc)
 			return rc;
@@ -567,6 +582,25 @@ extern "C" int tie_hip_moe_ffn(const float *x, int T, int d, int F, int E, int k
 		HIP_TRY(hipMemcpyAsync(topk_w_opt, g.w_dev, (size_t)T * k * 4, hipMemcpyDeviceToHost, g.stream));
 	HIP_TRY(hipStreamSynchronize(g.stream));
 	return TIE_HIP_OK;
+}
+
+extern "C" int tie_hip_moe_ffn(const float *x, int T, int d, int F, int E, int k, const void *router_w,
+			       int router_type, const void *gate_exps, int gate_type, const void *up_exps, int up_type,
+			       const void *down_exps, int down_type, float *out, int32_t *topk_idx_opt,
+			       float *topk_w_opt)
+{
+	return moe_ffn_host(x, T, d, F, E, k, router_w, router_type, TIE_HIP_ROUTE_SOFTMAX, nullptr, gate_exps,
+			    gate_type, up_exps, up_type, down_exps, down_type, out, topk_idx_opt, topk_w_opt);
+}
+
+extern "C" int tie_hip_moe_ffn_lfm2(const float *x, int T, int d, int F, int E, int k, const void *router_w,
+				    int router_type, const float *probs_bias_opt, const void *gate_exps, int gate_type,
+				    const void *up_exps, int up_type, const void *down_exps, int down_type, float *out,
+				    int32_t *topk_idx_opt, float *topk_w_opt)
+{
+	return moe_ffn_host(x, T, d, F, E, k, router_w, router_type, TIE_HIP_ROUTE_SIGMOID, probs_bias_opt,
+			    gate_exps, gate_type, up_exps, up_type, down_exps, down_type, out, topk_idx_opt,
+			    topk_w_opt);
 }
 
 extern "C" int tie_hip_exact_max_tokens(void)

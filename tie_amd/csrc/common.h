@@ -62,7 +62,9 @@ struct Layer {
 	int d = 0, F = 0, E = 0;
 	const float *router = nullptr; // [E][d]
 	const float *routerT = nullptr; // [d][E] (the tiled router kernel's layout)
-	const float *bias = nullptr;   // [E] or null
+	const float *bias = nullptr;   // [E] or null, added to the logits
+	int routing = 0;               // ROUTE_SOFTMAX (Qwen3) or ROUTE_SIGMOID (LFM2)
+	const float *pbias = nullptr;  // [E] or null: LFM2 selection bias (exp_probs_b_bias)
 	ExpertTensor gate, up, down;
 	void *alloc = nullptr;         // one device allocation holding everything
 	size_t bytes = 0;

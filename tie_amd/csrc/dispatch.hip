@@ -91,7 +91,8 @@ __global__ __launch_bounds__(DSP_THREADS) void route_group_kernel(const float *_
 								  float *__restrict__ topk_w,
 								  int32_t *__restrict__ offsets,
 								  int32_t *__restrict__ pairs,
-								  int32_t *__restrict__ active)
+								  int32_t *__restrict__ active, int routing,
+								  const float *__restrict__ pbias)
 {
 	__shared__ __attribute__((aligned(16))) int32_t cnt[MAX_E];
 	__shared__ int32_t cur[MAX_E];
@@ -106,7 +107,7 @@ __global__ __launch_bounds__(DSP_THREADS) void route_group_kernel(const float *_
 	}
 	__syncthreads();
 	for (int t = tid >> 6; t < T; t += DSP_THREADS / 64)
-		topk_softmax(logits + (size_t)t * E, E, k, etab, sidx + t * k, topk_w + (size_t)t * k);
+		topk_softmax(logits + (size_t)t * E, E, k, etab, sidx + t * k, topk_w + (size_t)t * k, routing, pbias);
 	__syncthreads();
 	const int npairs = T * k;
 	for (int p = tid; p < npairs; p += DSP_THREADS)
@@ -118,7 +119,7 @@ __global__ __launch_bounds__(DSP_THREADS) void route_group_kernel(const float *_
 hipError_t launch_route_group(const Layer &L, int T, int k, const float *logits, Workspace &ws, hipStream_t s)
 {
 	hipLaunchKernelGGL(route_group_kernel, dim3(1), dim3(DSP_THREADS), 0, s, logits, T, L.E, k, ws.topk_idx,
-			   ws.topk_w, ws.offsets, ws.pairs, ws.active);
+			   ws.topk_w, ws.offsets, ws.pairs, ws.active, L.routing, L.pbias);
 	return hipGetLastError();
 }
 

@@ -32,6 +32,8 @@
 //                      eight lane accumulators.
 // No kernel waits on another workgroup: the only ordering is the launch
 // order on the stream.
+#include <cmath>
+
 #include "common.h"
 #include "route.h"
 
@@ -86,22 +88,20 @@ template <int PC> __device__ __forceinline__ void step_fence(float (&a0)[PC][8],
 #define GU_OCC
 #endif
 
-// waves per gate/up workgroup: split (one matrix, small T) and fused
+// waves per split gate/up workgroup (one matrix, one token); the fused
+// gate/up and the down kernels take their wave count from the launch
 #ifndef TIE_GU_WAVES
 #define TIE_GU_WAVES 8
-#endif
-#ifndef TIE_GUF_WAVES
-#define TIE_GUF_WAVES 4
 #endif
 #ifndef TIE_GU_PG
 #define TIE_GU_PG 8
 #endif
+
 #ifndef TIE_GU_PREFETCH
 #define TIE_GU_PREFETCH 0
 #endif
 constexpr int GU_WAVES = TIE_GU_WAVES;
 constexpr int GU_THREADS = 64 * GU_WAVES;
-constexpr int GUF_WAVES = TIE_GUF_WAVES;
 constexpr int PG_MAX = 16;        // pairs per LDS group
 constexpr int PART_FLOATS = 16384; // LDS budget of the per-block partial dots (64 KiB)
 // Routing in the gate/up prologue up to this T (E <= 128).  Only one token:
@@ -375,6 +375,8 @@ struct ExactArgs {
 	int pg_cap;           // pairs per LDS group
 	int inline_route;
 	int single;           // T = 1 mode: slot j = pair j of expert topk_idx[j], no grouping
+	int routing;          // ROUTE_SOFTMAX / ROUTE_SIGMOID (inline routing)
+	const float *pbias;   // [E] selection bias of ROUTE_SIGMOID, or null
 };
 
 // Selection and grouping of all T <= INLINE_T tokens by one workgroup of NT
@@ -403,7 +405,8 @@ template <int NT> __device__ __forceinline__ void inline_route(const ExactArgs &
 	}
 	__syncthreads();
 	for (int t = tid >> 6; t < T; t += NT / 64)
-		topk_softmax_wave<INLINE_E / 64>(a.logits + (size_t)t * E, E, k, R.etab, R.idx + t * k, R.w + t * k);
+		topk_softmax_wave<INLINE_E / 64>(a.logits + (size_t)t * E, E, k, R.etab, R.idx + t * k, R.w + t * k,
+						 a.routing, a.pbias);
 	__syncthreads();
 	if (a.single) {
 		// one token: slot j is its own group (expert idx[j], pair j); the
@@ -443,7 +446,8 @@ template <int NT> __device__ __forceinline__ void inline_route(const ExactArgs &
 template <int TYPE, bool FUSED, int PM>
 __global__ __launch_bounds__(GU_THREADS) GU_OCC void exact_gu_kernel(ExactArgs a)
 {
-	constexpr int NW = FUSED ? GUF_WAVES : GU_WAVES;
+	// fused: as many waves as the launch chose; split: GU_WAVES
+	const int NW = FUSED ? __builtin_amdgcn_readfirstlane(blockDim.x >> 6) : GU_WAVES;
 	using Block = typename BlockOf<TYPE>::type;
 	extern __shared__ float part[]; // [mats][nb][pg_cap][64]
 	const int32_t *offsets = a.offsets, *pairs = a.pairs, *active = a.active;
@@ -596,8 +600,8 @@ __device__ __forceinline__ void stage_h(const ExactArgs &a, const int32_t *gp, i
 	}
 }
 
-// blockIdx = (64-row panel of d, active-expert slot); blockDim = 64 *
-// min(nb, 8).  HG: h comes from hbuf (written by the fused gate/up kernel)
+// blockIdx = (64-row panel of d, active-expert slot); blockDim = 64 * nb
+// up to nb = 6, else 64 * min(ceil(nb / 2), 8) (waves stride the blocks).  HG: h comes from hbuf (written by the fused gate/up kernel)
 // through scalar loads; otherwise the prologue forms h from the gate and up
 // row sums in LDS.  Dynamic LDS: [h [pg_cap][F] |] part [nb][pg_cap][64].
 template <int TYPE, bool HG, int PM>
@@ -741,6 +745,49 @@ static hipError_t launch_q(K kernel, dim3 grid, dim3 block, size_t lds, size_t s
 	return hipGetLastError();
 }
 
+// Waves per workgroup for a launch of n_wg workgroups that each run `tasks`
+// super-block columns, wave w taking columns w, w + nw, ..: the count in
+// [1, 8] that minimises rounds * ceil(tasks / nw), where a round is one
+// workgroup on every resident slot of the chip (the occupancy API's
+// workgroups per CU, which counts registers and LDS, times the CUs).  The
+// grids here are often only slightly larger than one round, so a wave count
+// that packs more workgroups per CU, or gives each fewer columns, shortens
+// the last, partly filled round.  Ties go to more waves (at most `tasks`).
+static int pick_waves(const void *fn, size_t lds, int n_wg, int tasks)
+{
+	static int ncu = 0;
+	if (!ncu) {
+		int dev = 0;
+		if (hipGetDevice(&dev) != hipSuccess ||
+		    hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0)
+			ncu = 256;
+	}
+	const int wmax = tasks < 8 ? tasks : 8;
+	int best = wmax;
+	long best_cost = -1;
+	for (int w = wmax; w >= 1; w--) {
+		int occ = 0;
+		if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, 64 * w, lds) != hipSuccess || occ <= 0)
+			continue;
+		const long slots = (long)ncu * occ;
+		const long cost = (long)((n_wg + slots - 1) / slots) * ((tasks + w - 1) / w);
+		if (best_cost < 0 || cost < best_cost) {
+			best_cost = cost;
+			best = w;
+		}
+	}
+	return best;
+}
+
+// Expected number of experts with at least one pair: E (1 - (1 - k/E)^T)
+// for independent uniform selections, at most max_active.
+static int expected_active(int E, int k, int T, int max_active)
+{
+	const double a = E * (1.0 - std::pow(1.0 - (double)k / E, (double)T));
+	const int n = (int)std::ceil(a);
+	return n < 1 ? 1 : n > max_active ? max_active : n;
+}
+
 // gate/up of one quantised type; fused (both matrices, h out) or one
 // matrix per blockIdx.z (row sums out)
 static hipError_t launch_gu_q(int type, bool fused, int nmat, int rows, int in, int max_active, ExactArgs g,
@@ -756,7 +803,8 @@ static hipError_t launch_gu_q(int type, bool fused, int nmat, int rows, int in, 
 	g.rows = rows;
 	g.in = in;
 	const size_t lds = sizeof(float) * (size_t)mats * nb * g.pg_cap * 64;
-	const dim3 grid(rows / PANEL_ROWS, max_active, fused ? 1 : nmat), block(64 * (fused ? GUF_WAVES : GU_WAVES));
+	const dim3 grid(rows / PANEL_ROWS, max_active, fused ? 1 : nmat);
+	dim3 block(64 * GU_WAVES);
 	const size_t st = fused ? 0 : sizeof(InlineRoute);
 	constexpr int PM = TIE_EXACT_PCMAX;
 	// one token (one pair per group): a one-pair instance, whose register
@@ -764,6 +812,15 @@ static hipError_t launch_gu_q(int type, bool fused, int nmat, int rows, int in, 
 	if (g.single)
 		return type == TIE_GGML_Q4_K ? launch_q(exact_gu_kernel<TIE_GGML_Q4_K, false, 1>, grid, block, lds, st, s, g)
 					     : launch_q(exact_gu_kernel<TIE_GGML_Q6_K, false, 1>, grid, block, lds, st, s, g);
+	if (fused) {
+		const void *fn = type == TIE_GGML_Q4_K ? (const void *)exact_gu_kernel<TIE_GGML_Q4_K, true, PM>
+						      : (const void *)exact_gu_kernel<TIE_GGML_Q6_K, true, PM>;
+		hipError_t err = set_lds_limit(fn, lds);
+		if (err != hipSuccess)
+			return err;
+		block.x = 64 * pick_waves(fn, lds, (rows / PANEL_ROWS) * expected_active(g.E, g.k, g.T, max_active),
+					  2 * nb);
+	}
 	if (type == TIE_GGML_Q4_K)
 		return fused ? launch_q(exact_gu_kernel<TIE_GGML_Q4_K, true, PM>, grid, block, lds, st, s, g)
 			     : launch_q(exact_gu_kernel<TIE_GGML_Q4_K, false, PM>, grid, block, lds, st, s, g);
@@ -827,6 +884,8 @@ hipError_t launch_exact_block(const Layer &L, const float *x, int T, int k, cons
 	a.pairs = ws.pairs;
 	a.active = ws.active;
 	a.inline_route = inl ? 1 : 0;
+	a.routing = L.routing;
+	a.pbias = L.pbias;
 	a.single = single ? 1 : 0;
 
 	prof_begin("exact_gate_up", s);
@@ -884,16 +943,33 @@ hipError_t launch_exact_block(const Layer &L, const float *x, int T, int k, cons
 			const size_t lds = sizeof(float) * (size_t)g.pg_cap * F;
 			err = launch_q(exact_down_bf16_kernel, grid, dim3(BF_THREADS), lds, 0, s, g);
 		} else {
-			const dim3 block(64 * (nb < 8 ? nb : 8));
+			dim3 block(64);
+			const int n_wg = (L.d / PANEL_ROWS) * expected_active(L.E, k, T, max_active);
 			if (fused) {
 				g.pg_cap = clamp_pg(PART_FLOATS / (nb * 64));
 				const size_t lds = sizeof(float) * (size_t)g.pg_cap * nb * 64;
+				const void *fn = L.down.type == TIE_GGML_Q4_K ? (const void *)exact_down_kernel<TIE_GGML_Q4_K, true, PM>
+									       : (const void *)exact_down_kernel<TIE_GGML_Q6_K, true, PM>;
+				err = set_lds_limit(fn, lds);
+				if (err != hipSuccess)
+					return err;
+				block.x = 64 * pick_waves(fn, lds, n_wg, nb);
 				err = L.down.type == TIE_GGML_Q4_K
 					      ? launch_q(exact_down_kernel<TIE_GGML_Q4_K, true, PM>, grid, block, lds, 0, s, g)
 					      : launch_q(exact_down_kernel<TIE_GGML_Q6_K, true, PM>, grid, block, lds, 0, s, g);
 			} else {
 				g.pg_cap = clamp_pg(PART_FLOATS / (F + nb * 64));
 				const size_t lds = sizeof(float) * (size_t)g.pg_cap * (F + nb * 64);
+				const void *fn = single ? (L.down.type == TIE_GGML_Q4_K
+								   ? (const void *)exact_down_kernel<TIE_GGML_Q4_K, false, 1>
+								   : (const void *)exact_down_kernel<TIE_GGML_Q6_K, false, 1>)
+							: (L.down.type == TIE_GGML_Q4_K
+								   ? (const void *)exact_down_kernel<TIE_GGML_Q4_K, false, PM>
+								   : (const void *)exact_down_kernel<TIE_GGML_Q6_K, false, PM>);
+				err = set_lds_limit(fn, lds);
+				if (err != hipSuccess)
+					return err;
+				block.x = 64 * pick_waves(fn, lds, single ? (L.d / PANEL_ROWS) * k : n_wg, nb);
 				if (single)
 					err = L.down.type == TIE_GGML_Q4_K
 						      ? launch_q(exact_down_kernel<TIE_GGML_Q4_K, false, 1>, grid, block, lds, 0, s, g)

@@ -56,27 +56,48 @@ __device__ __forceinline__ float key_logit(uint32_t k)
 	return __builtin_bit_cast(float, (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
 
-// top-k (engine.c:891-914 semantics) + softmax (engine.c:864-888) for one
-// token, by one wave; PER logits per lane (E <= 64 * PER), entry e = 64q +
-// lane in register q.  The k winners are extracted one at a time by a
-// wave-wide argmax under the order (value descending, index ascending) --
-// the order find_top_k's strict-greater insertion produces: the maximum
-// key comes from a DPP reduction inside each row of 16 lanes and a scalar
-// maximum over the four rows, and the lowest index holding it from a
-// ballot per register (register q holds indices 64q ..).  NaN and -inf
-// never qualify; unfilled slots are {-1, -inf}.  Slot j's exponential is
-// computed by lane j, the sum is formed serially in slot order, and every
-// weight is e_j * (1 / sum).  `lg` may be global or LDS memory.
+// Expert selection of one token, by one wave; PER logits per lane (E <= 64
+// * PER), entry e = 64q + lane in register q.
+//
+// ROUTE_SOFTMAX (Qwen3, model_qwen3.c:431-443): top-k over the logits
+// (find_top_k, engine.c:891-914), then softmax over the k selected
+// (engine.c:864-888): the maximum over the slots, e_j = expf(s_j - max) on
+// lane j, the sum formed serially in slot order, w_j = e_j * (1 / sum).
+//
+// ROUTE_SIGMOID (LFM2, model_lfm2.c:437-467): p_e = 1 / (1 + expf(-l_e));
+// top-k over p_e + bias_e (bias optional, selection only); the weights are
+// the unbiased p of the selected experts, L1-normalised: the sum formed
+// serially in slot order, w_j = p_j * (1 / (sum + 1e-6)).
+//
+// The k winners are extracted one at a time by a wave-wide argmax under
+// the order (value descending, index ascending) -- the order find_top_k's
+// strict-greater insertion produces: the maximum key comes from a DPP
+// reduction inside each row of 16 lanes and a scalar maximum over the
+// four rows, and the lowest index holding it from a ballot per register
+// (register q holds indices 64q ..).  NaN and -inf never qualify;
+// unfilled slots are {-1, -inf} with weight 0.  `lg` and `pbias` may be
+// global or LDS memory.
+constexpr int ROUTE_SOFTMAX = 0, ROUTE_SIGMOID = 1;
+
 template <int PER>
 __device__ __forceinline__ void topk_softmax_wave(const float *lg, int E, int k, const uint64_t *etab,
-						  int32_t *out_idx, float *out_w)
+						  int32_t *out_idx, float *out_w, int routing = ROUTE_SOFTMAX,
+						  const float *pbias = nullptr)
 {
 	const int lane = threadIdx.x & 63;
+	const bool sig = routing == ROUTE_SIGMOID;
 	uint32_t key[PER];
+	float prob[PER]; // sigmoid routing: the unbiased p of each entry
 #pragma unroll
 	for (int q = 0; q < PER; q++) {
 		const int e = q * 64 + lane;
-		key[q] = e < E ? logit_key(lg[e]) : KEY_NINF;
+		float v = e < E ? lg[e] : -__builtin_inff();
+		prob[q] = 0.0f;
+		if (sig && e < E) {
+			prob[q] = __fdiv_rn(1.0f, 1.0f + tie_expf_tab(-v, etab));
+			v = pbias ? prob[q] + pbias[e] : prob[q];
+		}
+		key[q] = logit_key(v);
 	}
 	float my_s = -__builtin_inff();
 	int my_i = -1;
@@ -104,8 +125,18 @@ __device__ __forceinline__ void topk_softmax_wave(const float *lg, int E, int k,
 			if (bal)
 				be = 64 * q + (int)__builtin_ctzll(bal);
 		}
+		float sv = key_logit(best);
+		if (sig) {
+			// the winner's unbiased p, from its lane
+			float pv = prob[0];
+#pragma unroll
+			for (int q = 1; q < PER; q++)
+				if (q == (be >> 6))
+					pv = prob[q];
+			sv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pv), be & 63));
+		}
 		if (lane == j) {
-			my_s = key_logit(best);
+			my_s = sv;
 			my_i = be;
 		}
 		if (lane == (be & 63)) {
@@ -114,6 +145,19 @@ __device__ __forceinline__ void topk_softmax_wave(const float *lg, int E, int k,
 				if (q == (be >> 6))
 					key[q] = 0;
 		}
+	}
+	if (sig) {
+		// L1 normalisation of the selected p (unfilled slots add nothing)
+		const float pj = my_i >= 0 ? my_s : 0.0f;
+		float sum = 0.0f;
+		for (int j = 0; j < k; j++)
+			sum = sum + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pj), j));
+		const float inv = __fdiv_rn(1.0f, sum + 1e-6f);
+		if (lane < k) {
+			out_w[lane] = pj * inv;
+			out_idx[lane] = my_i;
+		}
+		return;
 	}
 	// softmax over the k selected logits: max over the slots, exp per lane
 	float mx = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_s), 0));
@@ -135,18 +179,18 @@ __device__ __forceinline__ void topk_softmax_wave(const float *lg, int E, int k,
 
 // topk_softmax_wave with PER chosen for E (E <= MAX_E)
 __device__ __forceinline__ void topk_softmax(const float *lg, int E, int k, const uint64_t *etab, int32_t *out_idx,
-					     float *out_w)
+					     float *out_w, int routing, const float *pbias)
 {
 	if (E <= 64)
-		topk_softmax_wave<1>(lg, E, k, etab, out_idx, out_w);
+		topk_softmax_wave<1>(lg, E, k, etab, out_idx, out_w, routing, pbias);
 	else if (E <= 128)
-		topk_softmax_wave<2>(lg, E, k, etab, out_idx, out_w);
+		topk_softmax_wave<2>(lg, E, k, etab, out_idx, out_w, routing, pbias);
 	else if (E <= 256)
-		topk_softmax_wave<4>(lg, E, k, etab, out_idx, out_w);
+		topk_softmax_wave<4>(lg, E, k, etab, out_idx, out_w, routing, pbias);
 	else if (E <= 512)
-		topk_softmax_wave<8>(lg, E, k, etab, out_idx, out_w);
+		topk_softmax_wave<8>(lg, E, k, etab, out_idx, out_w, routing, pbias);
 	else
-		topk_softmax_wave<16>(lg, E, k, etab, out_idx, out_w);
+		topk_softmax_wave<16>(lg, E, k, etab, out_idx, out_w, routing, pbias);
 }
 
 // Exclusive prefix sum over a workgroup of NT threads (one value each);

@@ -256,7 +256,8 @@ hipError_t launch_router_transpose(const Layer &L, hipStream_t s)
 constexpr int RW_THREADS = 256;
 __global__ __launch_bounds__(RW_THREADS) void router_topk_kernel(const float *__restrict__ logits, int T, int E,
 								      int k, int32_t *__restrict__ topk_idx,
-								      float *__restrict__ topk_w)
+								      float *__restrict__ topk_w, int routing,
+								      const float *__restrict__ pbias)
 {
 	__shared__ uint64_t etab[32];
 	if (threadIdx.x < 32) {
@@ -266,7 +267,8 @@ __global__ __launch_bounds__(RW_THREADS) void router_topk_kernel(const float *__
 	__syncthreads();
 	const int t = blockIdx.x * (RW_THREADS / 64) + (threadIdx.x >> 6);
 	if (t < T)
-		topk_softmax(logits + (size_t)t * E, E, k, etab, topk_idx + (size_t)t * k, topk_w + (size_t)t * k);
+		topk_softmax(logits + (size_t)t * E, E, k, etab, topk_idx + (size_t)t * k, topk_w + (size_t)t * k, routing,
+			     pbias);
 }
 
 hipError_t launch_router_logits(const Layer &L, const float *x, int T, float *logits, hipStream_t s)
@@ -300,7 +302,7 @@ hipError_t launch_router_select(const Layer &L, int T, int k, const float *logit
 				hipStream_t s)
 {
 	hipLaunchKernelGGL(router_topk_kernel, dim3((T + RW_THREADS / 64 - 1) / (RW_THREADS / 64)), dim3(RW_THREADS), 0,
-			   s, logits, T, L.E, k, topk_idx, topk_w);
+			   s, logits, T, L.E, k, topk_idx, topk_w, L.routing, L.pbias);
 	return hipGetLastError();
 }
 

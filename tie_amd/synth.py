@@ -93,12 +93,17 @@ def zipf_bias(n_exp, s=1.2, c=1.0, seed=0):
 class MoELayer:
     """One MoE FFN layer's weights in host memory, GGUF layout."""
 
-    def __init__(self, d, F, E, gate, up, down, router, gu_type, down_type, bias=None):
+    def __init__(self, d, F, E, gate, up, down, router, gu_type, down_type, bias=None, routing=0,
+                 probs_bias=None):
         self.d, self.F, self.E = d, F, E
         self.gate, self.up, self.down, self.router = gate, up, down, router
         self.gate_type = self.up_type = gu_type
         self.down_type = down_type
         self.bias = bias
+        # 0: softmax routing (Qwen3); 1: sigmoid routing with an optional
+        # selection bias (LFM2's exp_probs_b_bias)
+        self.routing = routing
+        self.probs_bias = probs_bias
 
     def digest(self):
         h = hashlib.sha256()
@@ -107,14 +112,19 @@ class MoELayer:
         return h.hexdigest()
 
 
-def make_layer(seed, d, F, E, gu_type=Q4_K, down_type=Q6_K, zipf=None):
+def make_layer(seed, d, F, E, gu_type=Q4_K, down_type=Q6_K, zipf=None, routing=0, probs_bias=None):
+    """probs_bias: None, or the standard deviation of a seeded N(0, s)
+    selection bias for sigmoid routing (LFM2's exp_probs_b_bias)."""
     rng = np.random.default_rng(seed)
     router = rng.normal(0.0, 0.02, size=(E, d)).astype(np.float32)
     gate = expert_tensor(rng, gu_type, E, F, d)
     up = expert_tensor(rng, gu_type, E, F, d)
     down = expert_tensor(rng, down_type, E, d, F)
     bias = zipf_bias(E, s=zipf, seed=seed + 7) if zipf else None
-    return MoELayer(d, F, E, gate, up, down, router, gu_type, down_type, bias)
+    pb = None
+    if probs_bias:
+        pb = np.random.default_rng(seed + 11).normal(0.0, probs_bias, size=E).astype(np.float32)
+    return MoELayer(d, F, E, gate, up, down, router, gu_type, down_type, bias, routing, pb)
 
 
 def make_input(seed, T, d):
@@ -122,7 +132,8 @@ def make_input(seed, T, d):
     return rng.normal(0.0, 1.0, size=(T, d)).astype(np.float32)
 
 
-# The workload configs of the MoE block benchmark (30B-A3B / 235B-A22B shapes).
+# The workload configs of the MoE block benchmark (30B-A3B / 235B-A22B shapes;
+# lfm2_*: LFM2-8B-A1B-shaped blocks with sigmoid routing and a selection bias).
 CONFIGS = {
     "30b_t1": dict(d=2048, F=768, E=128, k=8, T=1, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1234),
     "30b_t2": dict(d=2048, F=768, E=128, k=8, T=2, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1242),
@@ -133,5 +144,9 @@ CONFIGS = {
     "30b_bf16_zipf_t512": dict(d=2048, F=768, E=128, k=8, T=512, gu_type=BF16, down_type=BF16, zipf=1.2,
                                seed=1237),
     "235b_t1": dict(d=4096, F=1536, E=128, k=8, T=1, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1238),
+    "lfm2_t1": dict(d=2048, F=1792, E=32, k=4, T=1, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1250,
+                    routing=1, probs_bias=0.05),
+    "lfm2_t32": dict(d=2048, F=1792, E=32, k=4, T=32, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1251,
+                     routing=1, probs_bias=0.05),
     "235b_t1024": dict(d=4096, F=1536, E=128, k=8, T=1024, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1239),
 }
