@@ -15,8 +15,11 @@
 //                      matrix); wave w owns super-block columns w, w+8, ..;
 //                      lane i owns row i.  The lane's super-block is read
 //                      once per group of up to 16 pairs with coalesced
-//                      16-byte panel loads and dequantised once per 8
-//                      weights for up to 4 pairs at a time; the input row
+//                      16-byte panel loads (in stages: the next 64-weight
+//                      group's chunks in flight while one computes, so
+//                      a third of the block is in registers) and
+//                      dequantised once per 8 weights for up to 4 pairs
+//                      at a time; the input row
 //                      of each pair comes in through scalar loads (one
 //                      address per wave), so it reaches the FMAs as SGPR
 //                      operands.  Per-block dots meet in LDS and are added
@@ -33,6 +36,7 @@
 // No kernel waits on another workgroup: the only ordering is the launch
 // order on the stream.
 #include <cmath>
+#include <type_traits>
 
 #include "common.h"
 #include "route.h"
@@ -231,6 +235,120 @@ __device__ __forceinline__ void block_dots(const Q4KBlock &B, XP *const xs[PC], 
 	}
 }
 
+// The Q4_K block read in stages instead of at once: the scale chunk and
+// the two quant chunks of 64-weight group 0 first, then the chunks of group
+// g + 1 while group g computes.  That keeps 12 of the block's 36 dwords in
+// registers at a time (vector loads return in order, so the wait for group
+// g leaves group g + 1 in flight).
+struct Q4KStream {
+	const uint4 *p; // the lane's first chunk; chunk c at p[64 c]
+};
+
+__device__ __forceinline__ void load_block(const uint8_t *__restrict__ panel, int lane, Q4KStream &S)
+{
+	S.p = reinterpret_cast<const uint4 *>(panel) + lane;
+}
+
+__device__ __forceinline__ void launder(const uint4 *&p)
+{
+	asm volatile("" : "+v"(p));
+}
+
+// Sub-block scale and negated minimum of Q4_K sub-block j (get_scale_min_k4,
+// math_scalar.c:91-100) from the 12 packed bytes s[0..2].
+__device__ __forceinline__ void q4k_sub_scale(const uint32_t s[3], int j, float d, float dmin, float &D, float &nM)
+{
+	auto sb = [&](int i) { return (s[i >> 2] >> (8 * (i & 3))) & 0xffu; };
+	uint32_t sc, m;
+	if (j < 4) {
+		sc = sb(j) & 63u;
+		m = sb(j + 4) & 63u;
+	} else {
+		sc = (sb(j + 4) & 15u) | ((sb(j - 4) >> 6) << 4);
+		m = (sb(j + 4) >> 4) | ((sb(j) >> 6) << 4);
+	}
+	D = d * (float)sc;
+	nM = -(dmin * (float)m);
+}
+
+template <int PC, typename XP>
+__device__ __forceinline__ void block_dots(const Q4KStream &S, XP *const xs[PC], float out[PC])
+{
+	const uint4 c0 = S.p[0];
+	uint4 cur[2] = {S.p[64], S.p[128]};
+	const float d = half_bits_to_float(c0.x & 0xffffu);
+	const float dmin = half_bits_to_float(c0.x >> 16);
+	const uint32_t s[3] = {c0.y, c0.z, c0.w};
+	float a0[PC][8], a1[PC][8];
+#pragma unroll
+	for (int p = 0; p < PC; p++)
+#pragma unroll
+		for (int l = 0; l < 8; l++)
+			a0[p][l] = a1[p][l] = 0.0f;
+	constexpr int XS = PC == 1 ? 4 : PC == 2 ? 2 : 1;
+	XP *xb[PC];
+#pragma unroll
+	for (int g = 0; g < 4; g++) {
+		step_fence<PC>(a0, a1);
+		uint4 nxt[2];
+		if (g < 3) {
+			const uint4 *q = S.p + 64 * (3 + 2 * g);
+			launder(q);
+			nxt[0] = q[0];
+			nxt[1] = q[64];
+			__builtin_amdgcn_sched_barrier(0);
+		}
+		float D1, M1, D2, M2;
+		q4k_sub_scale(s, 2 * g, d, dmin, D1, M1);
+		q4k_sub_scale(s, 2 * g + 1, d, dmin, D2, M2);
+#pragma unroll
+		for (int ss = 0; ss < 8; ss++) {
+			const int st = 8 * g + ss, o = ss >> 2, h = ss & 3;
+			step_fence<PC>(a0, a1);
+			if (st % XS == 0) {
+#pragma unroll
+				for (int p = 0; p < PC; p++) {
+					xb[p] = xs[p] + 64 * g + 16 * o + 4 * h;
+					launder(xb[p]);
+				}
+			}
+			uint32_t w = word(cur[o], h);
+			asm volatile("" : "+v"(w));
+			uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
+			asm volatile("" : "+v"(lo), "+v"(hi));
+			float wl[4], wh[4];
+#pragma unroll
+			for (int i = 0; i < 4; i++) {
+				wl[i] = __builtin_fmaf(ubyte(lo, i), D1, M1);
+				wh[i] = __builtin_fmaf(ubyte(hi, i), D2, M2);
+			}
+			const int xo = 4 * (st % XS);
+#pragma unroll
+			for (int p = 0; p < PC; p++) {
+#pragma unroll
+				for (int i = 0; i < 4; i++) {
+					const int m = 4 * h + i;
+					float &A = (m < 8) ? a0[p][m & 7] : a1[p][m & 7];
+					A = __builtin_fmaf(xb[p][xo + i], wl[i], A);
+					A = __builtin_fmaf(xb[p][xo + 32 + i], wh[i], A);
+				}
+			}
+		}
+		if (g < 3) {
+			cur[0] = nxt[0];
+			cur[1] = nxt[1];
+		}
+	}
+#pragma unroll
+	for (int p = 0; p < PC; p++) {
+		float v[8];
+#pragma unroll
+		for (int l = 0; l < 8; l++)
+			v[l] = a0[p][l] + a1[p][l];
+		out[p] = hsum8(v);
+	}
+}
+
 // dot_product_f32_q6k_avx2 (math_avx2.c:411-495) of the lane's block with
 // PC input rows.  Panel chunks: 0-7 ql[0..127], 8-11 qh[0..63], 12 the
 // int8 scales.  q - 32 is formed once per weight; per pair TIE's
@@ -309,12 +427,133 @@ __device__ __forceinline__ void block_dots(const Q6KBlock &B, XP *const xs[PC], 
 	}
 }
 
+// The Q6_K block read in stages: the scale chunk, d and the three quant
+// chunks (ql low/high nibble sources and qh) of quarter (n, l >> 4) first,
+// then those of the next quarter while one quarter computes.
+struct Q6KStream {
+	const uint4 *p;      // the lane's first chunk; chunk c at p[64 c]
+	const uint16_t *dp;  // the lane's d
+};
+
+__device__ __forceinline__ void load_block(const uint8_t *__restrict__ panel, int lane, Q6KStream &S)
+{
+	S.p = reinterpret_cast<const uint4 *>(panel) + lane;
+	S.dp = reinterpret_cast<const uint16_t *>(panel + Q6K_CHUNKS * 1024) + lane;
+}
+
+template <int PC, typename XP>
+__device__ __forceinline__ void block_dots(const Q6KStream &S, XP *const xs[PC], float out[PC])
+{
+	const uint4 sc4 = S.p[64 * 12];
+	const float d = half_bits_to_float(*S.dp);
+	// quarter qt = (n, hl): chunks 4n + hl (ql, low nibbles), 4n + 2 + hl
+	// (ql, high nibbles), 8 + 2n + hl (qh)
+	auto quarter = [&](int qt, uint4 (&c)[3]) {
+		const int n = qt >> 1, hl = qt & 1;
+		const uint4 *q = S.p + 64 * (4 * n + hl);
+		launder(q);
+		c[0] = q[0];
+		c[1] = q[128];
+		c[2] = q[64 * (8 + 2 * n + hl) - 64 * (4 * n + hl)];
+	};
+	uint4 cur[3];
+	quarter(0, cur);
+	float a0[PC][8], a1[PC][8];
+#pragma unroll
+	for (int p = 0; p < PC; p++)
+#pragma unroll
+		for (int l = 0; l < 8; l++)
+			a0[p][l] = a1[p][l] = 0.0f;
+	constexpr int XS = PC == 1 ? 2 : 1;
+	auto sc = [&](int j) { return (float)(int8_t)((word(sc4, j >> 2) >> (8 * (j & 3))) & 0xffu); };
+	XP *xb[PC];
+#pragma unroll
+	for (int qt = 0; qt < 4; qt++) {
+		step_fence<PC>(a0, a1);
+		uint4 nxt[3];
+		if (qt < 3) {
+			quarter(qt + 1, nxt);
+			__builtin_amdgcn_sched_barrier(0);
+		}
+#pragma unroll
+		for (int ss = 0; ss < 4; ss++) {
+			const int st = 4 * qt + ss;
+			const int n = st >> 3, l = 8 * ((st >> 1) & 3), hw = st & 1;
+			const int is = (l >= 16) ? 1 : 0;
+			step_fence<PC>(a0, a1);
+			if (st % XS == 0) {
+#pragma unroll
+				for (int p = 0; p < PC; p++) {
+					xb[p] = xs[p] + 128 * n + l + 4 * hw;
+					launder(xb[p]);
+				}
+			}
+			const float W0 = d * sc(8 * n + is + 0);
+			const float W1 = d * sc(8 * n + is + 2);
+			const float W2 = d * sc(8 * n + is + 4);
+			const float W3 = d * sc(8 * n + is + 6);
+			const int dw = ((l & 8) >> 2) + hw;
+			uint32_t L = word(cur[0], dw), L2 = word(cur[1], dw), H = word(cur[2], dw);
+			asm volatile("" : "+v"(L), "+v"(L2), "+v"(H));
+			uint32_t q1 = (L & 0x0f0f0f0fu) | ((H & 0x03030303u) << 4);
+			uint32_t q2 = (L2 & 0x0f0f0f0fu) | (((H >> 2) & 0x03030303u) << 4);
+			uint32_t q3 = ((L >> 4) & 0x0f0f0f0fu) | (((H >> 4) & 0x03030303u) << 4);
+			uint32_t q4 = ((L2 >> 4) & 0x0f0f0f0fu) | (((H >> 6) & 0x03030303u) << 4);
+			// two halves: words 1, 2 (accumulators a0, a1 via runs 0 and
+			// 32), then words 3, 4 (runs 64 and 96); every accumulator keeps
+			// TIE's order, and only eight converted weights are live
+			const int xo = 4 * (st % XS);
+#pragma unroll
+			for (int half = 0; half < 2; half++) {
+				uint32_t qa = half ? q3 : q1, qb = half ? q4 : q2;
+				asm volatile("" : "+v"(qa), "+v"(qb));
+				const float Wa = half ? W2 : W0, Wb = half ? W3 : W1;
+				float fa[4], fb[4];
+#pragma unroll
+				for (int i = 0; i < 4; i++) {
+					fa[i] = ubyte(qa, i) - 32.0f;
+					fb[i] = ubyte(qb, i) - 32.0f;
+				}
+#pragma unroll
+				for (int p = 0; p < PC; p++) {
+#pragma unroll
+					for (int i = 0; i < 4; i++) {
+						const int m = 4 * hw + i;
+						XP *xq = xb[p] + xo + i + 64 * half;
+						a0[p][m] = __builtin_fmaf(Wa, fa[i] * xq[0], a0[p][m]);
+						a1[p][m] = __builtin_fmaf(Wb, fb[i] * xq[32], a1[p][m]);
+					}
+				}
+				if (half == 0)
+					step_fence<PC>(a0, a1);
+			}
+		}
+		if (qt < 3) {
+#pragma unroll
+			for (int i = 0; i < 3; i++)
+				cur[i] = nxt[i];
+		}
+	}
+#pragma unroll
+	for (int p = 0; p < PC; p++) {
+		float v[8];
+#pragma unroll
+		for (int l = 0; l < 8; l++)
+			v[l] = a0[p][l] + a1[p][l];
+		out[p] = hsum8(v);
+	}
+}
+
 template <int TYPE> struct BlockOf;
+// quantised blocks read in stages (Q4KStream, Q6KStream) or at once
+#ifndef TIE_Q4K_STREAM
+#define TIE_Q4K_STREAM 1
+#endif
 template <> struct BlockOf<TIE_GGML_Q4_K> {
-	using type = Q4KBlock;
+	using type = std::conditional<TIE_Q4K_STREAM, Q4KStream, Q4KBlock>::type;
 };
 template <> struct BlockOf<TIE_GGML_Q6_K> {
-	using type = Q6KBlock;
+	using type = std::conditional<TIE_Q4K_STREAM, Q6KStream, Q6KBlock>::type;
 };
 
 // PC pairs of the group against the lane's block; part[(b*pg_cap + q) * 64 + lane]
