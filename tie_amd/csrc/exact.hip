@@ -240,16 +240,27 @@ __device__ __forceinline__ void block_dots(const Q4KBlock &B, XP *const xs[PC], 
 // g + 1 while group g computes.  That keeps 12 of the block's 36 dwords in
 // registers at a time (vector loads return in order, so the wait for group
 // g leaves group g + 1 in flight).
+// Panel chunks through a global-address-space pointer: after a launder the
+// loads stay global loads (a generic pointer would make them flat loads,
+// which also count as LDS/scalar operations, so every wait for the scalar
+// input loads would also wait for the next group's chunks).
+typedef const uint4 __attribute__((address_space(1))) guint4;
+typedef const uint16_t __attribute__((address_space(1))) guint16;
+__device__ __forceinline__ uint4 ld(guint4 *p)
+{
+	return *(const uint4 *)p;
+}
+
 struct Q4KStream {
-	const uint4 *p; // the lane's first chunk; chunk c at p[64 c]
+	guint4 *p; // the lane's first chunk; chunk c at p[64 c]
 };
 
 __device__ __forceinline__ void load_block(const uint8_t *__restrict__ panel, int lane, Q4KStream &S)
 {
-	S.p = reinterpret_cast<const uint4 *>(panel) + lane;
+	S.p = (guint4 *)reinterpret_cast<const uint4 *>(panel) + lane;
 }
 
-__device__ __forceinline__ void launder(const uint4 *&p)
+__device__ __forceinline__ void launder(guint4 *&p)
 {
 	asm volatile("" : "+v"(p));
 }
@@ -274,8 +285,8 @@ __device__ __forceinline__ void q4k_sub_scale(const uint32_t s[3], int j, float 
 template <int PC, typename XP>
 __device__ __forceinline__ void block_dots(const Q4KStream &S, XP *const xs[PC], float out[PC])
 {
-	const uint4 c0 = S.p[0];
-	uint4 cur[2] = {S.p[64], S.p[128]};
+	const uint4 c0 = ld(S.p);
+	uint4 cur[2] = {ld(S.p + 64), ld(S.p + 128)};
 	const float d = half_bits_to_float(c0.x & 0xffffu);
 	const float dmin = half_bits_to_float(c0.x >> 16);
 	const uint32_t s[3] = {c0.y, c0.z, c0.w};
@@ -292,10 +303,10 @@ __device__ __forceinline__ void block_dots(const Q4KStream &S, XP *const xs[PC],
 		step_fence<PC>(a0, a1);
 		uint4 nxt[2];
 		if (g < 3) {
-			const uint4 *q = S.p + 64 * (3 + 2 * g);
+			guint4 *q = S.p + 64 * (3 + 2 * g);
 			launder(q);
-			nxt[0] = q[0];
-			nxt[1] = q[64];
+			nxt[0] = ld(q);
+			nxt[1] = ld(q + 64);
 			__builtin_amdgcn_sched_barrier(0);
 		}
 		float D1, M1, D2, M2;
@@ -431,30 +442,30 @@ __device__ __forceinline__ void block_dots(const Q6KBlock &B, XP *const xs[PC], 
 // chunks (ql low/high nibble sources and qh) of quarter (n, l >> 4) first,
 // then those of the next quarter while one quarter computes.
 struct Q6KStream {
-	const uint4 *p;      // the lane's first chunk; chunk c at p[64 c]
-	const uint16_t *dp;  // the lane's d
+	guint4 *p;    // the lane's first chunk; chunk c at p[64 c]
+	guint16 *dp;  // the lane's d
 };
 
 __device__ __forceinline__ void load_block(const uint8_t *__restrict__ panel, int lane, Q6KStream &S)
 {
-	S.p = reinterpret_cast<const uint4 *>(panel) + lane;
-	S.dp = reinterpret_cast<const uint16_t *>(panel + Q6K_CHUNKS * 1024) + lane;
+	S.p = (guint4 *)reinterpret_cast<const uint4 *>(panel) + lane;
+	S.dp = (guint16 *)reinterpret_cast<const uint16_t *>(panel + Q6K_CHUNKS * 1024) + lane;
 }
 
 template <int PC, typename XP>
 __device__ __forceinline__ void block_dots(const Q6KStream &S, XP *const xs[PC], float out[PC])
 {
-	const uint4 sc4 = S.p[64 * 12];
-	const float d = half_bits_to_float(*S.dp);
+	const uint4 sc4 = ld(S.p + 64 * 12);
+	const float d = half_bits_to_float(*(const uint16_t *)S.dp);
 	// quarter qt = (n, hl): chunks 4n + hl (ql, low nibbles), 4n + 2 + hl
 	// (ql, high nibbles), 8 + 2n + hl (qh)
 	auto quarter = [&](int qt, uint4 (&c)[3]) {
 		const int n = qt >> 1, hl = qt & 1;
-		const uint4 *q = S.p + 64 * (4 * n + hl);
+		guint4 *q = S.p + 64 * (4 * n + hl);
 		launder(q);
-		c[0] = q[0];
-		c[1] = q[128];
-		c[2] = q[64 * (8 + 2 * n + hl) - 64 * (4 * n + hl)];
+		c[0] = ld(q);
+		c[1] = ld(q + 128);
+		c[2] = ld(q + 64 * (8 + 2 * n + hl) - 64 * (4 * n + hl));
 	};
 	uint4 cur[3];
 	quarter(0, cur);
