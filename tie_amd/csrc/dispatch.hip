@@ -86,6 +86,10 @@ hipError_t launch_dispatch(const Layer &L, int T, int k, const int32_t *topk_idx
 // token when E <= 128, else a wave per token), then group_pairs.  Saves
 // the separate selection launch.
 constexpr int RG_MAX_PAIRS = 4096;
+constexpr int RG_LDS_LOGITS = 8192; // T * E up to this: logits staged in LDS
+// G8: 8 tokens per wave (E <= 128 and more tokens than waves), else one
+// wave per token; separate instances keep each one's registers small
+template <bool G8, bool SIG>
 __global__ __launch_bounds__(DSP_THREADS) void route_group_kernel(const float *__restrict__ logits, int T, int E,
 								  int k, int32_t *__restrict__ topk_idx,
 								  float *__restrict__ topk_w,
@@ -100,14 +104,40 @@ __global__ __launch_bounds__(DSP_THREADS) void route_group_kernel(const float *_
 	__shared__ uint64_t etab[32];
 	__shared__ int32_t sidx[RG_MAX_PAIRS];
 	__shared__ int lpt[2 * LPT_BINS];
+	// the logits of all tokens in LDS (one coalesced copy: a wave that
+	// selects for several tokens then waits for global memory once)
+	__shared__ __attribute__((aligned(16))) float slg[RG_LDS_LOGITS];
+	__shared__ float gsel[(DSP_THREADS / 8) * MAX_K]; // per-token scratch of the 8-lane selection
 	const int tid = threadIdx.x;
 	if (tid < 32) {
 		const uint64_t tab[32] = TIE_EXP2_TABLE;
 		etab[tid] = tab[tid];
 	}
+	const float *lg = logits;
+	if (T * E <= RG_LDS_LOGITS) {
+		const int n = T * E;
+		for (int i = 4 * tid; i < n; i += 4 * DSP_THREADS) {
+			if (i + 4 <= n)
+				*reinterpret_cast<float4 *>(slg + i) = *reinterpret_cast<const float4 *>(logits + i);
+			else
+				for (int j = i; j < n; j++)
+					slg[j] = logits[j];
+		}
+		lg = slg;
+	}
 	__syncthreads();
-	for (int t = tid >> 6; t < T; t += DSP_THREADS / 64)
-		topk_softmax(logits + (size_t)t * E, E, k, etab, sidx + t * k, topk_w + (size_t)t * k, routing, pbias);
+	if constexpr (G8) {
+		for (int t0 = 0; t0 < T; t0 += DSP_THREADS / 8) {
+			const int t = t0 + tid / 8;
+			if (t < T)
+				topk_softmax_group8<SIG>(lg + (size_t)t * E, E, k, gsel + (tid / 8) * MAX_K, etab,
+							 sidx + t * k, topk_w + (size_t)t * k, pbias);
+		}
+	} else {
+		for (int t = tid >> 6; t < T; t += DSP_THREADS / 64)
+			topk_softmax(lg + (size_t)t * E, E, k, etab, sidx + t * k, topk_w + (size_t)t * k, routing,
+				     pbias);
+	}
 	__syncthreads();
 	const int npairs = T * k;
 	for (int p = tid; p < npairs; p += DSP_THREADS)
@@ -118,8 +148,11 @@ __global__ __launch_bounds__(DSP_THREADS) void route_group_kernel(const float *_
 
 hipError_t launch_route_group(const Layer &L, int T, int k, const float *logits, Workspace &ws, hipStream_t s)
 {
-	hipLaunchKernelGGL(route_group_kernel, dim3(1), dim3(DSP_THREADS), 0, s, logits, T, L.E, k, ws.topk_idx,
-			   ws.topk_w, ws.offsets, ws.pairs, ws.active, L.routing, L.pbias);
+	const bool g8 = L.E <= 128 && T > DSP_THREADS / 64, sig = L.routing == ROUTE_SIGMOID;
+	auto kern = g8 ? (sig ? route_group_kernel<true, true> : route_group_kernel<true, false>)
+		       : route_group_kernel<false, false>;
+	hipLaunchKernelGGL(kern, dim3(1), dim3(DSP_THREADS), 0, s, logits, T, L.E, k, ws.topk_idx, ws.topk_w, ws.offsets,
+			   ws.pairs, ws.active, L.routing, L.pbias);
 	return hipGetLastError();
 }
 

@@ -37,6 +37,34 @@ __device__ __forceinline__ uint32_t umax32(uint32_t a, uint32_t b)
 {
 	return a > b ? a : b;
 }
+__device__ __forceinline__ uint32_t umin32(uint32_t a, uint32_t b)
+{
+	return a < b ? a : b;
+}
+
+// Wave-wide maximum / minimum, returned in every lane: DPP inside rows of
+// 16 lanes (quad swaps, half-row and row mirrors), then v_permlane16_swap
+// (rows 0<->1, 2<->3) and v_permlane32_swap (halves).
+template <bool MAX> __device__ __forceinline__ uint32_t wave_all(uint32_t m)
+{
+	auto op = [](uint32_t a, uint32_t b) { return MAX ? umax32(a, b) : umin32(a, b); };
+	m = op(m, (uint32_t)dppi<DPP_XOR1>((int)m));
+	m = op(m, (uint32_t)dppi<DPP_XOR2>((int)m));
+	m = op(m, (uint32_t)dppi<DPP_HALF_MIRROR>((int)m));
+	m = op(m, (uint32_t)dppi<DPP_MIRROR>((int)m));
+	const auto r16 = __builtin_amdgcn_permlane16_swap(m, m, false, false);
+	m = op(r16[0], r16[1]);
+	const auto r32 = __builtin_amdgcn_permlane32_swap(m, m, false, false);
+	return op(r32[0], r32[1]);
+}
+__device__ __forceinline__ uint32_t wave_all_umax(uint32_t m)
+{
+	return wave_all<true>(m);
+}
+__device__ __forceinline__ uint32_t wave_all_umin(uint32_t m)
+{
+	return wave_all<false>(m);
+}
 
 // Order-preserving integer key of a logit: larger float, larger key.  NaN
 // maps to the key of -inf (never selected, like find_top_k's strict
@@ -69,13 +97,13 @@ __device__ __forceinline__ float key_logit(uint32_t k)
 // the unbiased p of the selected experts, L1-normalised: the sum formed
 // serially in slot order, w_j = p_j * (1 / (sum + 1e-6)).
 //
-// The k winners are extracted one at a time by a wave-wide argmax under
-// the order (value descending, index ascending) -- the order find_top_k's
-// strict-greater insertion produces: the maximum key comes from a DPP
-// reduction inside each row of 16 lanes and a scalar maximum over the
-// four rows, and the lowest index holding it from a ballot per register
-// (register q holds indices 64q ..).  NaN and -inf never qualify;
-// unfilled slots are {-1, -inf} with weight 0.  `lg` and `pbias` may be
+// The k winners are extracted one at a time under the order (value
+// descending, index ascending) -- the order find_top_k's strict-greater
+// insertion produces -- by wave-wide maximum of the keys and minimum of
+// the indices holding it, both kept in the vector unit (DPP inside rows,
+// then gfx950's row-pair and half swaps), so a round has no vector-to-
+// scalar round trip.  NaN and -inf never qualify; unfilled slots are
+// {-1, -inf} with weight 0.  `lg` and `pbias` may be
 // global or LDS memory.
 constexpr int ROUTE_SOFTMAX = 0, ROUTE_SIGMOID = 1;
 
@@ -102,49 +130,42 @@ __device__ __forceinline__ void topk_softmax_wave(const float *lg, int E, int k,
 	float my_s = -__builtin_inff();
 	int my_i = -1;
 	for (int j = 0; j < k; j++) {
+		// wave maximum of the keys, in every lane: lane-local, then DPP
+		// inside rows of 16, then the row-pair and half swaps
 		uint32_t m = key[0];
 #pragma unroll
 		for (int q = 1; q < PER; q++)
-			m = m > key[q] ? m : key[q];
-		m = umax32(m, (uint32_t)dppi<DPP_XOR1>((int)m));
-		m = umax32(m, (uint32_t)dppi<DPP_XOR2>((int)m));
-		m = umax32(m, (uint32_t)dppi<DPP_HALF_MIRROR>((int)m));
-		m = umax32(m, (uint32_t)dppi<DPP_MIRROR>((int)m));
-		uint32_t best = (uint32_t)__builtin_amdgcn_readlane((int)m, 0);
+			m = umax32(m, key[q]);
+		const uint32_t best = wave_all_umax(m);
+		// lowest index holding it (the lowest register first: register q
+		// holds indices 64q + lane)
+		uint32_t ci = 0xffffffffu;
 #pragma unroll
-		for (int r = 16; r < 64; r += 16) {
-			const uint32_t o = (uint32_t)__builtin_amdgcn_readlane((int)m, r);
-			best = best > o ? best : o;
-		}
-		if (best <= KEY_NINF)
-			break; // nothing selectable left: the remaining slots stay unfilled
-		int be = 0;
-#pragma unroll
-		for (int q = PER - 1; q >= 0; q--) {
-			const uint64_t bal = __builtin_amdgcn_ballot_w64(key[q] == best);
-			if (bal)
-				be = 64 * q + (int)__builtin_ctzll(bal);
-		}
+		for (int q = PER - 1; q >= 0; q--)
+			if (key[q] == best)
+				ci = 64 * q + lane;
+		const uint32_t be = wave_all_umin(ci);
+		const bool found = best > KEY_NINF; // wave-uniform
 		float sv = key_logit(best);
 		if (sig) {
-			// the winner's unbiased p, from its lane
-			float pv = prob[0];
-#pragma unroll
-			for (int q = 1; q < PER; q++)
-				if (q == (be >> 6))
-					pv = prob[q];
-			sv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pv), be & 63));
-		}
-		if (lane == j) {
-			my_s = sv;
-			my_i = be;
-		}
-		if (lane == (be & 63)) {
+			// the winner's unbiased p, from its lane: every lane holds its
+			// own candidate's p, the winner's reaches all lanes by the
+			// same minimum (only the winner offers a finite index)
+			float pv = 0.0f;
 #pragma unroll
 			for (int q = 0; q < PER; q++)
-				if (q == (be >> 6))
-					key[q] = 0;
+				if ((uint32_t)(64 * q + lane) == be)
+					pv = prob[q];
+			sv = __builtin_bit_cast(float, wave_all_umax(ci == be ? __builtin_bit_cast(uint32_t, pv) : 0u));
 		}
+		if (found && lane == j) {
+			my_s = sv;
+			my_i = (int)be;
+		}
+#pragma unroll
+		for (int q = 0; q < PER; q++)
+			if ((uint32_t)(64 * q + lane) == be)
+				key[q] = 0;
 	}
 	if (sig) {
 		// L1 normalisation of the selected p (unfilled slots add nothing)
@@ -191,6 +212,123 @@ __device__ __forceinline__ void topk_softmax(const float *lg, int E, int k, cons
 		topk_softmax_wave<8>(lg, E, k, etab, out_idx, out_w, routing, pbias);
 	else
 		topk_softmax_wave<16>(lg, E, k, etab, out_idx, out_w, routing, pbias);
+}
+
+// The same selection for 8 tokens per wave: 8 lanes per token (E <= 128,
+// 16 entries per lane, entry e = 8q + lane % 8 in register q), so a wave
+// runs the rounds of 8 tokens at once (a round is a chain of dependent
+// vector operations; one token per wave leaves the SIMD mostly idle).
+// Identical order of selection (the same keys: value descending, index
+// ascending; NaN and -inf never qualify) and identical weight arithmetic
+// for both routings.  The argmax of a round runs over DPP lane moves
+// inside the 8 lanes.  `sel`: LDS scratch of MAX_K floats for the token.
+template <bool SIG>
+__device__ __forceinline__ void topk_softmax_group8(const float *lg, int E, int k, float *sel, const uint64_t *etab,
+						    int32_t *out_idx, float *out_w, const float *pbias)
+{
+	constexpr int G = 8, V = 16;
+	const int lig = threadIdx.x & (G - 1);
+	constexpr bool sig = SIG;
+	uint32_t key[V];
+	float prob[V];
+#pragma unroll
+	for (int q = 0; q < V; q++) {
+		const int e = q * G + lig;
+		float v = e < E ? lg[e] : -__builtin_inff();
+		prob[q] = 0.0f;
+		if constexpr (SIG) {
+			if (e < E) {
+				prob[q] = __fdiv_rn(1.0f, 1.0f + tie_expf_tab(-v, etab));
+				v = pbias ? prob[q] + pbias[e] : prob[q];
+			}
+		}
+		key[q] = logit_key(v);
+	}
+	auto better = [](uint32_t ok, int oe, uint32_t bk, int be) { return ok > bk || (ok == bk && oe < be); };
+	for (int j = 0; j < k; j++) {
+		uint32_t bk = 0;
+		int be = 0x7fffffff;
+#pragma unroll
+		for (int q = 0; q < V; q++)
+			if (key[q] > bk) {
+				bk = key[q];
+				be = q * G + lig;
+			}
+		uint32_t ok = (uint32_t)dppi<DPP_XOR1>((int)bk);
+		int oe = dppi<DPP_XOR1>(be);
+		if (better(ok, oe, bk, be)) {
+			bk = ok;
+			be = oe;
+		}
+		ok = (uint32_t)dppi<DPP_XOR2>((int)bk);
+		oe = dppi<DPP_XOR2>(be);
+		if (better(ok, oe, bk, be)) {
+			bk = ok;
+			be = oe;
+		}
+		ok = (uint32_t)dppi<DPP_HALF_MIRROR>((int)bk);
+		oe = dppi<DPP_HALF_MIRROR>(be);
+		if (better(ok, oe, bk, be)) {
+			bk = ok;
+			be = oe;
+		}
+		const bool found = bk > KEY_NINF;
+		if (found && (be & (G - 1)) == lig) {
+			// the winner's lane records the slot and removes the entry
+			float pv = 0.0f;
+#pragma unroll
+			for (int q = 0; q < V; q++)
+				if (q == be / G) {
+					pv = prob[q];
+					key[q] = 0;
+				}
+			sel[j] = sig ? pv : key_logit(bk);
+			out_idx[j] = be;
+		} else if (!found && lig == 0) {
+			sel[j] = -__builtin_inff();
+			out_idx[j] = -1;
+		}
+	}
+	__builtin_amdgcn_wave_barrier();
+	if constexpr (SIG) {
+		// L1 normalisation of the selected p (unfilled slots add nothing)
+		float sum = 0.0f;
+		for (int j = 0; j < k; j++)
+			sum = sum + (sel[j] > -__builtin_inff() ? sel[j] : 0.0f);
+		const float inv = __fdiv_rn(1.0f, sum + 1e-6f);
+		for (int j = lig; j < k; j += G)
+			out_w[j] = (sel[j] > -__builtin_inff() ? sel[j] : 0.0f) * inv;
+		return;
+	}
+	float mx = sel[0];
+	for (int j = 1; j < k; j++)
+		if (sel[j] > mx)
+			mx = sel[j];
+	// e_j on lane j % 8, then the serial sum
+	float ev[MAX_K / G];
+#pragma unroll
+	for (int q = 0; q < MAX_K / G; q++) {
+		const int j = q * G + lig;
+		ev[q] = j < k ? tie_expf_tab(sel[j] - mx, etab) : 0.0f;
+	}
+	__builtin_amdgcn_wave_barrier();
+#pragma unroll
+	for (int q = 0; q < MAX_K / G; q++) {
+		const int j = q * G + lig;
+		if (j < k)
+			sel[j] = ev[q];
+	}
+	__builtin_amdgcn_wave_barrier();
+	float sum = 0.0f;
+	for (int j = 0; j < k; j++)
+		sum = sum + sel[j];
+	const float inv = __fdiv_rn(1.0f, sum);
+#pragma unroll
+	for (int q = 0; q < MAX_K / G; q++) {
+		const int j = q * G + lig;
+		if (j < k)
+			out_w[j] = ev[q] * inv;
+	}
 }
 
 // Exclusive prefix sum over a workgroup of NT threads (one value each);
