@@ -100,9 +100,10 @@ def expert_bytes(cfg):
     return gu, dn
 
 
-def run_config(torch, tie_amd, wl, T, k, steps, warmup, flags):
-    """Times `steps` forwards of T tokens; returns the measurement dict."""
-    cfg = wl.cfg
+def run_config(torch, tie_amd, wl, T, k, steps, warmup, flags, cfg=None):
+    """Times `steps` forwards of T tokens; returns the measurement dict.
+    cfg: the workload config (default: the one the layers were made for)."""
+    cfg = cfg or wl.cfg
     d, F, E = cfg["d"], cfg["F"], cfg["E"]
     nL = len(wl.layers)
     gen = torch.Generator(device="cuda")
@@ -112,8 +113,19 @@ def run_config(torch, tie_amd, wl, T, k, steps, warmup, flags):
     idx = torch.empty(nL, T, k, dtype=torch.int32, device="cuda")
     w = torch.empty(nL, T, k, device="cuda")
 
+    residual = bool(cfg.get("residual"))
+    if residual:
+        # the FFN half of the layer: out = X[l] + block(rms_norm(X[l])) (out
+        # of place, so every step sees the same inputs)
+        from tie_amd import synth
+        norm = torch.from_numpy(synth.make_norm_weight(cfg["seed"], d)).cuda()
+
     def step(s, record_topk=False):
         l = s % nL
+        if residual:
+            wl.layers[l].forward_residual(X[l], norm, 1e-6, T, k, out, idx[l] if record_topk else None,
+                                          w[l] if record_topk else None, flags=flags)
+            return
         wl.layers[l].forward(X[l], T, k, out, idx[l] if record_topk else None, w[l] if record_topk else None,
                              flags=flags)
 
@@ -145,7 +157,8 @@ def run_config(torch, tie_amd, wl, T, k, steps, warmup, flags):
         "router": E * d * 4 + T * d * 4,
         "exact_gate_up": U_avg * gu_b + T * d * 4 + pairs * F * 4,
         "exact_down": U_avg * dn_b + pairs * F * 4 + pairs * d * 4,
-        "combine": pairs * d * 4 + T * d * 4,
+        "combine": pairs * d * 4 + T * d * 4 * (3 if residual else 1),
+        "rmsnorm": 2 * T * d * 4 + d * 4,
         "dispatch": pairs * 4 * 2,
         "mfma_gate_up": U_avg * gu_b + T * d * 4 + pairs * F * 2,
         "mfma_down": U_avg * dn_b + pairs * F * 2 + pairs * d * 4,
@@ -292,7 +305,8 @@ def main():
     results = {}
     for name in names:
         cfg = dict(synth.CONFIGS[name])
-        key = (cfg["d"], cfg["F"], cfg["E"], cfg["gu_type"], cfg["down_type"], cfg.get("zipf"))
+        key = (cfg["d"], cfg["F"], cfg["E"], cfg["gu_type"], cfg["down_type"], cfg.get("zipf"), cfg.get("routing", 0),
+               cfg.get("probs_bias"))
         if key not in workloads:
             per_layer = cfg["E"] * sum(expert_bytes(cfg))
             nL = args.layers or max(8, min(40, int(16e9 // per_layer)))
@@ -301,7 +315,7 @@ def main():
         steps = args.steps if name == args.config else max(10, args.steps // 4)
         warm = args.warmup if name == args.config else max(2, args.warmup // 4)
         log("timing %s: T=%d, %d warm-up + %d steps" % (name, cfg["T"], warm, steps))
-        results[name] = run_config(torch, tie_amd, workloads[key], cfg["T"], cfg["k"], steps, warm, flags)
+        results[name] = run_config(torch, tie_amd, workloads[key], cfg["T"], cfg["k"], steps, warm, flags, cfg)
         log(json.dumps({name: results[name]}))
 
     main_name = args.config

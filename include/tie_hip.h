@@ -93,6 +93,20 @@ int tie_hip_moe_ffn_lfm2(const float *x, int T, int d, int F, int E, int k, cons
 			 int up_type, const void *down_exps, int down_type, float *out, int32_t *topk_idx_opt,
 			 float *topk_w_opt);
 
+/* Drop-in for the whole FFN half of transformer_layer_qwen3 (the RMSNorm at
+ * model_qwen3.c:392-401, the MoE branch at :404-471 and the residual add at
+ * :491): hidden += MoE(rms_norm(hidden, ffn_norm, eps)).
+ *   hidden    ctx->mem.hidden_state, [T][d] F32, read and updated in place
+ *   ffn_norm  LayerWeights.ffn_norm (engine.h:72), F32 [d]
+ *   eps       ctx->model->norm_eps
+ * The RMSNorm reproduces rms_norm_f32_f32_f32_avx2 (math_avx2.c:56-96) as
+ * TIE's build computes it, including the host CPU's RSQRTSS approximation
+ * (tabulated on this host at the first call).  Other arguments as
+ * tie_hip_moe_ffn. */
+int tie_hip_qwen3_ffn(float *hidden, int T, int d, int F, int E, int k, const float *ffn_norm, float eps,
+		      const void *router_w, int router_type, const void *gate_exps, int gate_type, const void *up_exps,
+		      int up_type, const void *down_exps, int down_type, int32_t *topk_idx_opt, float *topk_w_opt);
+
 /* Replace the SiLU lookup table with the caller's (TIE's own silu_table,
  * engine.c:12, as filled by silu_table_init, engine.c:297-303). */
 int tie_hip_set_silu_table(const float *table, int n);
@@ -137,6 +151,14 @@ size_t tie_hip_layer_bytes(const tie_hip_layer *layer);
  * optional [T][k].  Returns once enqueued; the caller synchronises. */
 int tie_hip_moe_forward(tie_hip_layer *layer, const float *x_dev, int T, int k, float *out_dev,
 			int32_t *topk_idx_dev, float *topk_w_dev, int flags, void *stream);
+
+/* The same FFN half on device pointers: out_dev = hidden_dev +
+ * block(rms_norm(hidden_dev)), both [T][d] F32; out_dev may be hidden_dev
+ * (TIE's in-place update).  ffn_norm_dev [d] F32.  Enqueued on `stream` like
+ * tie_hip_moe_forward. */
+int tie_hip_moe_forward_residual(tie_hip_layer *layer, const float *hidden_dev, const float *ffn_norm_dev, float eps,
+				 int T, int k, float *out_dev, int32_t *topk_idx_dev, float *topk_w_dev, int flags,
+				 void *stream);
 
 /* The largest T that TIE_HIP_PATH_AUTO sends down the exact path. */
 int tie_hip_exact_max_tokens(void);

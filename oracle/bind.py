@@ -57,6 +57,10 @@ def oracle():
         lib.orc_dequant_q4k.argtypes = [_P, _I, _P]
         lib.orc_dequant_q6k.argtypes = [_P, _I, _P]
         lib.orc_expf_array.argtypes = [_P, _P, ctypes.c_size_t]
+        lib.orc_rms_norm.argtypes = [_P, _P, _I, ctypes.c_float, _P]
+        lib.orc_qwen3_ffn.restype = _I
+        lib.orc_qwen3_ffn.argtypes = [_P, _I, _I, _I, _I, _I, _P, ctypes.c_float, _P, _P, _I, _P, _I, _P, _I, _P,
+                                      _P, _P, _I]
         _oracle = lib
     return _oracle
 
@@ -74,6 +78,10 @@ def ref():
         lib.ref_silu_table.restype = _I
         lib.ref_silu_table.argtypes = [_P, _I]
         lib.ref_pool_threads.restype = _I
+        lib.ref_rms_norm.restype = _I
+        lib.ref_rms_norm.argtypes = [_P, _P, _I, ctypes.c_float, _P, _I]
+        lib.ref_apply_residual.restype = _I
+        lib.ref_apply_residual.argtypes = [_P, _P, _I, _I]
         lib.ref_moe_block.restype = _I
         lib.ref_moe_block.argtypes = [_P, _I, _I, _I, _I, _I, _P, _P, _I, _P, _P, _I, _P, _I, _P, _I, _I, _P,
                                       _P, _P, _P, _I]
@@ -124,6 +132,45 @@ def ref_moe_block(layer, x, k, literal_bf16_stride=False, nthreads=8, with_logit
     if rc != 0:
         raise ValueError("reference driver failed")
     return (out, idx, w, logits) if with_logits else (out, idx, w)
+
+
+def rms_norm(x, w, eps):
+    """Oracle RMSNorm of every row of x (TIE's rms_norm with this host's RSQRTSS)."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    out = np.empty_like(x)
+    for t in range(x.shape[0]):
+        oracle().orc_rms_norm(_ptr(x[t]), _ptr(w), x.shape[1], eps, _ptr(out[t]))
+    return out
+
+
+def ref_rms_norm(x, w, eps, nthreads=8):
+    """The compiled reference's dispatch_rms_norm on every row of x."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    out = np.empty_like(x)
+    for t in range(x.shape[0]):
+        if ref().ref_rms_norm(_ptr(x[t]), _ptr(w), x.shape[1], eps, _ptr(out[t]), nthreads) != 0:
+            raise RuntimeError("reference rms_norm failed")
+    return out
+
+
+def qwen3_ffn(layer, hidden, k, ffn_norm, eps, silu_tab=None, nthreads=8):
+    """Oracle FFN half of the layer: hidden + block(rms_norm(hidden)).
+    Returns (new hidden, topk_idx, topk_w); the input array is not changed."""
+    h = np.array(hidden, np.float32, copy=True, order="C")
+    T, d = h.shape
+    if silu_tab is None:
+        silu_tab = silu_table()
+    idx = np.empty((T, k), np.int32)
+    w = np.empty((T, k), np.float32)
+    norm = np.ascontiguousarray(ffn_norm, np.float32)
+    rc = oracle().orc_qwen3_ffn(_ptr(h), T, d, layer.F, layer.E, k, _ptr(norm), eps, _ptr(layer.router),
+                                _ptr(layer.gate), layer.gate_type, _ptr(layer.up), layer.up_type, _ptr(layer.down),
+                                layer.down_type, _ptr(silu_tab), _ptr(idx), _ptr(w), nthreads)
+    if rc != 0:
+        raise ValueError("oracle rejected the block shape/types")
+    return h, idx, w
 
 
 def ref_silu_table(nthreads=8):

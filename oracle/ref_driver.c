@@ -68,6 +68,31 @@ int ref_silu_table(float *tab, int nthreads)
 	return 0;
 }
 
+/* TIE's own dispatch_rms_norm (math_dispatch.c:198) on one row */
+int ref_rms_norm(const float *x, const float *w, int size, float eps, float *out, int nthreads)
+{
+	if (ref_init(nthreads) < 0)
+		return -1;
+	MemType xi = {.type = GGML_TYPE_F32, .data = (void *)x};
+	MemType oi = {.type = GGML_TYPE_F32, .data = out};
+	Tensor wt;
+	memset(&wt, 0, sizeof(wt));
+	wt.mem = (MemType){.type = GGML_TYPE_F32, .data = (void *)w};
+	dispatch_rms_norm(&xi, &wt, &oi, size, eps);
+	return 0;
+}
+
+/* TIE's own dispatch_apply_residual (math_dispatch.c:468): acc += residual */
+int ref_apply_residual(float *acc, const float *residual, int size, int nthreads)
+{
+	if (ref_init(nthreads) < 0)
+		return -1;
+	MemType a = {.type = GGML_TYPE_F32, .data = acc};
+	MemType r = {.type = GGML_TYPE_F32, .data = (void *)residual};
+	dispatch_apply_residual(&a, &r, size);
+	return 0;
+}
+
 static size_t row_bytes(int type, int in_dim)
 {
 	switch (type) {

@@ -564,6 +564,54 @@ int orc_moe_block(const float *x, int T, int d, int F, int E, int k, const float
 	return 0;
 }
 
+/* rms_norm_f32_f32_f32_avx2 (math_avx2.c:56-96) as TIE's build computes it
+ * (our build of the reference sources, read back): eight FMA chains over
+ * x[8i + l], the hsum tree, ss / size + eps, then 1/sqrtf as GCC emits it
+ * under -ffast-math: y0 = RSQRTSS(a) on this host (the instruction itself,
+ * as TIE runs it) and one Newton step fma(a*y0, y0, -3) * (y0 * -0.5);
+ * out = (x * w) * inv. */
+__attribute__((target("avx2,fma"))) void orc_rms_norm(const float *x, const float *w, int size, float eps, float *o)
+{
+	float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+	int i = 0;
+	for (; i <= size - 8; i += 8)
+		for (int l = 0; l < 8; l++)
+			acc[l] = fmaf(x[i + l], x[i + l], acc[l]);
+	float ss = hsum8(acc);
+	for (; i < size; i++)
+		ss = fmaf(x[i], x[i], ss);
+	const float a = ss / (float)size + eps;
+	const float y0 = _mm_cvtss_f32(_mm_rsqrt_ss(_mm_set_ss(a)));
+	const float inv = fmaf(a * y0, y0, -3.0f) * (y0 * -0.5f);
+	for (i = 0; i < size; i++)
+		o[i] = (x[i] * w[i]) * inv;
+}
+
+/* The FFN half of transformer_layer_qwen3: RMSNorm of every token
+ * (model_qwen3.c:392-401), the MoE block (:404-471), then the residual add
+ * hidden += ffn_down_output (:491, apply_residual_f32_f32_avx2,
+ * math_avx2.c:731-751).  hidden is updated in place. */
+int orc_qwen3_ffn(float *hidden, int T, int d, int F, int E, int k, const float *ffn_norm, float eps,
+		  const float *router_w, const void *gate_w, int gate_type, const void *up_w, int up_type,
+		  const void *down_w, int down_type, const float *silu_tab, int32_t *topk_idx, float *topk_w,
+		  int nthreads)
+{
+	if (T < 0 || d <= 0)
+		return -1;
+	float *normed = (float *)calloc((size_t)(T > 0 ? T : 1) * d, sizeof(float));
+	float *out = (float *)calloc((size_t)(T > 0 ? T : 1) * d, sizeof(float));
+	for (int t = 0; t < T; t++)
+		orc_rms_norm(hidden + (size_t)t * d, ffn_norm, d, eps, normed + (size_t)t * d);
+	int rc = orc_moe_block(normed, T, d, F, E, k, router_w, NULL, 0, NULL, gate_w, gate_type, up_w, up_type,
+			       down_w, down_type, 0, silu_tab, out, topk_idx, topk_w, NULL, nthreads);
+	if (rc == 0)
+		for (size_t i = 0; i < (size_t)T * d; i++)
+			hidden[i] = hidden[i] + out[i];
+	free(normed);
+	free(out);
+	return rc;
+}
+
 /* ------------------------------------------------------------------ */
 /* dequantisers (closed-form checks)                                    */
 /* ------------------------------------------------------------------ */

@@ -41,6 +41,11 @@ int orc_moe_block(const float *x, int T, int d, int F, int E, int k, const float
 		  const void *down_w, int down_type, int literal_bf16_stride, const float *silu_tab, float *out,
 		  int32_t *topk_idx, float *topk_w, float *logits_out, int nthreads);
 
+void orc_rms_norm(const float *x, const float *w, int size, float eps, float *o);
+int orc_qwen3_ffn(float *hidden, int T, int d, int F, int E, int k, const float *ffn_norm, float eps,
+		  const float *router_w, const void *gate_w, int gate_type, const void *up_w, int up_type,
+		  const void *down_w, int down_type, const float *silu_tab, int32_t *topk_idx, float *topk_w,
+		  int nthreads);
 void orc_dequant_q4k(const uint8_t *blocks, int n, float *y);
 void orc_dequant_q6k(const uint8_t *blocks, int n, float *y);
 void orc_expf_array(const float *in, float *out, size_t n);

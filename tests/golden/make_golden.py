@@ -79,14 +79,45 @@ def build_case(name, spec):
     return c
 
 
+# The FFN half of a Qwen3 layer through the compiled reference: RMSNorm of
+# each token (dispatch_rms_norm), the MoE block, the residual add
+# (dispatch_apply_residual).  name: (d, F, E, k, T, seed, eps)
+FFN_CASES = {
+    "gffn_qwen3_t3": (2048, 768, 128, 8, 3, 1260, 1e-6),
+    "gffn_tiny_t5": (512, 256, 16, 4, 5, 1261, 1e-6),
+}
+
+
+def build_ffn_case(name, spec):
+    d, F, E, k, T, seed, eps = spec
+    layer = synth.make_layer(seed, d, F, E, synth.Q4_K, synth.Q6_K)
+    hidden = synth.make_input(seed, T, d) * np.float32(3.0)
+    norm = synth.make_norm_weight(seed, d)
+    normed = bind.ref_rms_norm(hidden, norm, eps)
+    out, idx, w = bind.ref_moe_block(layer, normed, k)
+    new = hidden.copy()
+    for t in range(T):
+        if bind.ref().ref_apply_residual(bind._ptr(new[t]), bind._ptr(out[t]), d, 8) != 0:
+            raise RuntimeError("reference residual failed")
+    return dict(name=name, d=d, F=F, E=E, k=k, T=T, seed=seed, eps=np.float32(eps), gu_type=synth.Q4_K,
+                down_type=synth.Q6_K, zipf=0.0, literal=0, tie_rows=np.zeros((0, 2), np.int32),
+                digest=layer.digest(), hidden=hidden, ffn_norm=norm, normed=normed, hidden_out=new, topk_idx=idx,
+                topk_w=w, cpu=cpu_identity())
+
+
 def main():
     """python make_golden.py [case ...]: the named cases (default: all, and
     the SiLU table)."""
-    names = sys.argv[1:] or list(CASES)
+    names = sys.argv[1:] or list(CASES) + list(FFN_CASES)
     if not sys.argv[1:]:
         tab = bind.ref_silu_table()
         np.savez_compressed(os.path.join(OUT, "silu_table.npz"), table=tab, cpu=cpu_identity())
     for name in names:
+        if name in FFN_CASES:
+            c = build_ffn_case(name, FFN_CASES[name])
+            np.savez_compressed(os.path.join(OUT, name + ".npz"), **c)
+            print(name, "max|hidden_out| = %.4g" % np.abs(c["hidden_out"]).max())
+            continue
         spec = CASES[name]
         c = build_case(name, spec)
         np.savez_compressed(os.path.join(OUT, name + ".npz"), **c)

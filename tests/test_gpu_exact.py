@@ -90,6 +90,62 @@ def test_lfm2_one_token_without_bias():
             run_both(layer, synth.make_input(27 + T, T, 512), k)
 
 
+@pytest.mark.parametrize("name", ["gffn_qwen3_t3", "gffn_tiny_t5"])
+def test_qwen3_ffn_residual(name):
+    """tie_hip_qwen3_ffn: RMSNorm (with the host RSQRTSS table), block and
+    residual add, bit-exact against the oracle; against the compiled
+    reference's vectors on the CPU they were made on."""
+    g = load_golden(name)
+    layer = golden_layer(g)
+    k, eps = int(g["k"]), float(g["eps"])
+    print("qwen3 ffn case %s" % name, flush=True)
+    h, idx, w = tie_amd.qwen3_ffn(g["hidden"], layer, k, g["ffn_norm"], eps)
+    rh, ri, rw = bind.qwen3_ffn(layer, g["hidden"], k, g["ffn_norm"], eps)
+    assert_same(idx, ri, "topk_idx")
+    assert_same(w, rw, "topk_w")
+    assert_same(h, rh, "hidden")
+    if str(g["cpu"]) == host_cpu_identity():
+        assert_same(h, g["hidden_out"], "golden hidden")
+
+
+@pytest.mark.parametrize("T,flags", [(32, None), (200, "mfma")])
+def test_qwen3_ffn_residual_device(T, flags):
+    """Layer.forward_residual on device memory, in place (and out of place
+    on a second call, which must give the same bits): the exact path
+    bit-exact, the MFMA path with exact routing and bf16-bounded outputs."""
+    import torch
+    c = synth.CONFIGS["30b_t32"]
+    layer = synth_layer(c["seed"], c["d"], c["F"], c["E"], c["gu_type"], c["down_type"], None)
+    hidden = synth.make_input(c["seed"] + T, T, c["d"]) * np.float32(3.0)
+    norm = synth.make_norm_weight(c["seed"], c["d"])
+    L = tie_amd.Layer.from_synth(layer)
+    mode = tie_amd.PATH_MFMA if flags else tie_amd.PATH_EXACT
+    hin = torch.from_numpy(hidden).cuda()
+    hout = torch.empty_like(hin)
+    L.forward_residual(hin, torch.from_numpy(norm).cuda(), 1e-6, T, 8, hout, flags=mode)
+    hd = torch.from_numpy(hidden).cuda()
+    nd = torch.from_numpy(norm).cuda()
+    idx = torch.empty((T, 8), dtype=torch.int32, device="cuda")
+    w = torch.empty((T, 8), dtype=torch.float32, device="cuda")
+    print("residual device case T=%d %s" % (T, flags), flush=True)
+    L.forward_residual(hd, nd, 1e-6, T, 8, None, idx, w, flags=tie_amd.PATH_MFMA if flags else tie_amd.PATH_EXACT)
+    torch.cuda.synchronize()
+    rh, ri, rw = bind.qwen3_ffn(layer, hidden, 8, norm, 1e-6)
+    assert_same(idx.cpu().numpy(), ri, "topk_idx")
+    assert_same(w.cpu().numpy(), rw, "topk_w")
+    got = hd.cpu().numpy()
+    assert_same(hout.cpu().numpy(), got, "out of place vs in place")
+    assert_same(hin.cpu().numpy(), hidden, "input untouched out of place")
+    if flags:
+        d_got, d_want = got - hidden, rh - hidden  # the block's contribution
+        e = float(np.linalg.norm(d_got - d_want) / np.linalg.norm(d_want))
+        print("residual MFMA rel L2 of the block output %.3g" % e, flush=True)
+        assert e <= 2e-2
+    else:
+        assert_same(got, rh, "hidden")
+    L.close()
+
+
 @pytest.mark.parametrize("name,literal", [("g30b_bf16_zipf_t4", False), ("g30b_bf16_zipf_literal_t4", True)])
 def test_golden_bf16_zipf_device_api(name, literal):
     import torch

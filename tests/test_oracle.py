@@ -153,6 +153,54 @@ def test_sigmoid_route_closed_form(seed):
     assert abs(float(w.astype(np.float64).sum()) - p.sum() / (p.sum() + 1e-6)) < 1e-6
 
 
+@pytest.mark.skipif(not bind.ref_available(), reason="reference build absent")
+@pytest.mark.parametrize("d", [8, 256, 2048, 4104])
+def test_rms_norm_matches_reference(d):
+    """orc_rms_norm against the compiled rms_norm_f32_f32_f32_avx2 (through
+    TIE's dispatch_rms_norm), bit for bit: rows of very different scales,
+    a zero row, and a length with a tail past the 8-lane loop."""
+    rng = np.random.default_rng(d)
+    x = rng.normal(0, 1, size=(12, d)).astype(np.float32)
+    x[1] *= np.float32(1e-4)
+    x[2] *= np.float32(1e5)
+    x[3] = 0.0
+    w = rng.normal(1, 0.1, size=d).astype(np.float32)
+    for eps in (1e-6, 1e-5):
+        np.testing.assert_array_equal(bits(bind.rms_norm(x, w, eps)), bits(bind.ref_rms_norm(x, w, eps)))
+
+
+def test_rms_norm_closed_form():
+    """x * w / sqrt(mean(x^2) + eps) in fp64: the host's approximate
+    reciprocal square root plus one Newton step is good to ~1e-7."""
+    rng = np.random.default_rng(5)
+    x = rng.normal(0, 2, size=(20, 2048)).astype(np.float32)
+    w = rng.normal(1, 0.1, size=2048).astype(np.float32)
+    got = bind.rms_norm(x, w, 1e-6).astype(np.float64)
+    x64 = x.astype(np.float64)
+    want = x64 * w / np.sqrt((x64 * x64).mean(axis=1, keepdims=True) + 1e-6)
+    np.testing.assert_allclose(got, want, rtol=2e-6, atol=0)
+
+
+@pytest.mark.parametrize("name", ["gffn_qwen3_t3", "gffn_tiny_t5"])
+def test_qwen3_ffn_oracle_matches_reference_golden(name):
+    """RMSNorm + block + residual against the compiled reference's vectors.
+    The RMSNorm uses the host's RSQRTSS and the block the host's SiLU
+    table, so the bits are compared on the CPU they were made on."""
+    g = load_golden(name)
+    layer = golden_layer(g)
+    assert layer.digest() == str(g["digest"]), "synthetic generator changed"
+    h, idx, w = bind.qwen3_ffn(layer, g["hidden"], int(g["k"]), g["ffn_norm"], float(g["eps"]))
+    if str(g["cpu"]) != host_cpu_identity():
+        normed = bind.rms_norm(g["hidden"], g["ffn_norm"], float(g["eps"]))
+        np.testing.assert_allclose(normed, g["normed"], rtol=1e-6, atol=0)
+        pytest.skip("bits depend on the RSQRTSS/SiLU of %s" % g["cpu"])
+    np.testing.assert_array_equal(bits(bind.rms_norm(g["hidden"], g["ffn_norm"], float(g["eps"]))),
+                                  bits(g["normed"]))
+    np.testing.assert_array_equal(idx, g["topk_idx"])
+    np.testing.assert_array_equal(bits(w), bits(g["topk_w"]))
+    np.testing.assert_array_equal(bits(h), bits(g["hidden_out"]))
+
+
 # ---------------------------------------------------------------- closed forms
 def test_fp16_conversion_all_values():
     h = np.arange(65536, dtype=np.uint32)

@@ -24,7 +24,7 @@ SILU_TABLE_SIZE = 8192
 # every symbol include/tie_hip.h declares
 EXPORTS = (
     "tie_hip_init", "tie_hip_shutdown", "tie_hip_last_error", "tie_hip_moe_ffn", "tie_hip_moe_ffn_lfm2",
-    "tie_hip_set_silu_table",
+    "tie_hip_qwen3_ffn", "tie_hip_moe_forward_residual", "tie_hip_set_silu_table",
     "tie_hip_silu_table_host", "tie_hip_layer_create", "tie_hip_layer_destroy", "tie_hip_layer_bytes",
     "tie_hip_moe_forward", "tie_hip_exact_max_tokens", "tie_hip_set_exact_max_tokens",
     "tie_hip_debug_fail_alloc", "tie_hip_host_expf", "tie_hip_profile_enable", "tie_hip_profile_read",
@@ -71,6 +71,10 @@ def lib():
         L.tie_hip_moe_ffn.restype = I
         L.tie_hip_moe_ffn_lfm2.argtypes = [P, I, I, I, I, I, P, I, P, P, I, P, I, P, I, P, P, P]
         L.tie_hip_moe_ffn_lfm2.restype = I
+        L.tie_hip_qwen3_ffn.argtypes = [P, I, I, I, I, I, P, ctypes.c_float, P, I, P, I, P, I, P, I, P, P]
+        L.tie_hip_qwen3_ffn.restype = I
+        L.tie_hip_moe_forward_residual.argtypes = [P, P, P, ctypes.c_float, I, I, P, P, P, I, P]
+        L.tie_hip_moe_forward_residual.restype = I
         L.tie_hip_set_silu_table.argtypes = [P, I]
         L.tie_hip_set_silu_table.restype = I
         L.tie_hip_silu_table_host.argtypes = [P, I]
@@ -184,6 +188,21 @@ def moe_ffn(x, layer, k, with_topk=True):
     return out, idx, w
 
 
+def qwen3_ffn(hidden, layer, k, ffn_norm, eps, with_topk=True):
+    """tie_hip_qwen3_ffn on host arrays: the FFN half of transformer_layer_qwen3
+    (RMSNorm, MoE block, residual add; model_qwen3.c:392-491).  Returns the
+    new hidden state (the input array is not changed) and the selection."""
+    h = np.array(hidden, np.float32, copy=True, order="C")
+    T, d = h.shape
+    idx = np.empty((T, k), np.int32) if with_topk else None
+    w = np.empty((T, k), np.float32) if with_topk else None
+    norm = np.ascontiguousarray(ffn_norm, np.float32)
+    check(lib().tie_hip_qwen3_ffn(_p(h), T, d, layer.F, layer.E, k, _p(norm), eps, _p(layer.router), F32,
+                                  _p(layer.gate), layer.gate_type, _p(layer.up), layer.up_type, _p(layer.down),
+                                  layer.down_type, _p(idx), _p(w)))
+    return h, idx, w
+
+
 class Layer:
     """A device-resident layer (tie_hip_layer_create).  Weight sources are
     host numpy arrays or device tensors (anything with data_ptr())."""
@@ -210,6 +229,14 @@ class Layer:
         """Enqueue the block on device pointers (torch tensors or ints)."""
         check(lib().tie_hip_moe_forward(self.handle, _p(x_dev), T, k, _p(out_dev), _p(topk_idx_dev),
                                         _p(topk_w_dev), flags, stream))
+
+    def forward_residual(self, hidden_dev, ffn_norm_dev, eps, T, k, out_dev=None, topk_idx_dev=None,
+                         topk_w_dev=None, flags=PATH_AUTO, stream=None):
+        """out = hidden + block(rms_norm(hidden)) on device pointers (out
+        defaults to hidden: the in-place update)."""
+        check(lib().tie_hip_moe_forward_residual(self.handle, _p(hidden_dev), _p(ffn_norm_dev), eps, T, k,
+                                                 _p(hidden_dev if out_dev is None else out_dev), _p(topk_idx_dev),
+                                                 _p(topk_w_dev), flags, stream))
 
     def close(self):
         if self.handle:

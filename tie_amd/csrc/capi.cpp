@@ -15,6 +15,7 @@ namespace tie {
 int set_error(int code, const char *fmt, ...);
 void clear_error();
 int silu_table_host(float *tab, int n);
+int rsqrt_table_host(std::vector<uint32_t> &tab, int &nbits);
 } // namespace tie
 
 struct tie_hip_layer {
@@ -35,7 +36,10 @@ struct Ctx {
 		cache;
 	float *x_dev = nullptr, *out_dev = nullptr, *w_dev = nullptr;
 	int32_t *idx_dev = nullptr;
+	float *norm_dev = nullptr; // [io_d] RMSNorm weights of the host-pointer residual call
 	size_t io_tokens = 0, io_d = 0, io_k = 0;
+	uint32_t *rsq = nullptr;   // host RSQRTSS table (built at the first residual call)
+	int rsq_bits = 0;
 	int exact_max_t = 64;
 	std::recursive_mutex mu;
 };
@@ -199,7 +203,7 @@ static int ensure_workspace(int T, int k, int d, int F, int E)
 	const size_t o_idx = take(P * 4), o_w = take(P * 4), o_off = take((EE + 1) * 4), o_pairs = take(P * 4),
 		     o_act = take((EE + 1) * 4), o_logits = take(Tcap * EE * 4), o_h = take(2 * P * FF * 4),
 		     o_hb = take(P * FF * 2), o_y = take(P * DD * 4), o_xb = take(Tcap * DD * 2),
-		     o_hlo = take(P * FF * 2), o_xlo = take(Tcap * DD * 2);
+		     o_hlo = take(P * FF * 2), o_xlo = take(Tcap * DD * 2), o_nm = take(Tcap * DD * 4);
 	const size_t max_tiles = (size_t)mfma_max_tiles((int)P, (int)EE);
 	const size_t o_te = take(2 * max_tiles * 4), o_tm = take(2 * max_tiles * 4), o_nt = take(8);
 	void *mem = nullptr;
@@ -222,6 +226,7 @@ static int ensure_workspace(int T, int k, int d, int F, int E)
 	w.h = (float *)(b + o_h);
 	w.hb = (uint16_t *)(b + o_hb);
 	w.y = (float *)(b + o_y);
+	w.normed = (float *)(b + o_nm);
 	w.xb = (uint16_t *)(b + o_xb);
 	w.hlo = (uint16_t *)(b + o_hlo);
 	w.xlo = (uint16_t *)(b + o_xlo);
@@ -344,8 +349,10 @@ static int create_layer(const tie_hip_layer_desc *ds, tie_hip_layer **out)
 	return TIE_HIP_OK;
 }
 
+// The block on device pointers; res (optional) is added to the combine
+// (out = res + block, the residual add after the FFN).
 static int forward(tie_hip_layer *layer, const float *x, int T, int k, float *out, int32_t *idx_out,
-		   float *w_out, int flags, hipStream_t s)
+		   float *w_out, int flags, hipStream_t s, const float *res = nullptr)
 {
 	if (!layer)
 		return set_error(TIE_HIP_EINVAL, "null layer");
@@ -377,17 +384,65 @@ static int forward(tie_hip_layer *layer, const float *x, int T, int k, float *ou
 		prof_end(s);
 		HIP_TRY(launch_mfma_experts(L, x, T, k, g.silu, ws, s));
 		prof_begin("combine", s);
-		HIP_TRY(launch_combine(T, L.d, k, ws.topk_w, ws.topk_idx, ws.y, out, s));
+		HIP_TRY(launch_combine(T, L.d, k, ws.topk_w, ws.topk_idx, ws.y, out, s, res));
 		prof_end(s);
 	} else {
 		// routing, experts and the combine
-		HIP_TRY(launch_exact_block(L, x, T, k, g.silu, ws, out, s));
+		HIP_TRY(launch_exact_block(L, x, T, k, g.silu, ws, out, s, res));
 	}
 	if (idx_out)
 		HIP_TRY(hipMemcpyAsync(idx_out, ws.topk_idx, (size_t)T * k * 4, hipMemcpyDeviceToDevice, s));
 	if (w_out)
 		HIP_TRY(hipMemcpyAsync(w_out, ws.topk_w, (size_t)T * k * 4, hipMemcpyDeviceToDevice, s));
 	return TIE_HIP_OK;
+}
+
+// The host CPU's RSQRTSS table on the device (built once).
+static int ensure_rsqrt()
+{
+	if (g.rsq)
+		return TIE_HIP_OK;
+	std::vector<uint32_t> tab;
+	int nbits = 0;
+	int rc = rsqrt_table_host(tab, nbits);
+	if (rc)
+		return rc;
+	uint32_t *dev = nullptr;
+	rc = dev_malloc((void **)&dev, tab.size() * 4, "rsqrt table");
+	if (rc)
+		return rc;
+	HIP_TRY(hipMemcpy(dev, tab.data(), tab.size() * 4, hipMemcpyHostToDevice));
+	g.rsq = dev;
+	g.rsq_bits = nbits;
+	return TIE_HIP_OK;
+}
+
+// out = hidden + block(rms_norm(hidden)): model_qwen3.c:392-401, 404-471,
+// 491 (out may be hidden: TIE updates its hidden state in place).
+static int forward_residual(tie_hip_layer *layer, const float *hidden, const float *norm_w, float eps, int T, int k,
+			    float *out, int32_t *idx_out, float *w_out, int flags, hipStream_t s)
+{
+	if (!layer)
+		return set_error(TIE_HIP_EINVAL, "null layer");
+	const Layer &L = layer->L;
+	if (T < 0)
+		return set_error(TIE_HIP_EINVAL, "T=%d < 0", T);
+	if (k < 1 || k > L.E || k > MAX_K)
+		return set_error(TIE_HIP_EINVAL, "k=%d outside [1, min(E=%d, %d)]", k, L.E, MAX_K);
+	if (T == 0)
+		return TIE_HIP_OK;
+	if (!hidden || !norm_w || !out)
+		return set_error(TIE_HIP_EINVAL, "null hidden/ffn_norm/out");
+	int rc = ensure_rsqrt();
+	if (rc)
+		return rc;
+	rc = ensure_workspace(T, k, L.d, L.F, L.E);
+	if (rc)
+		return rc;
+	prof_begin("rmsnorm", s);
+	HIP_TRY(launch_rmsnorm(hidden, norm_w, eps, T, L.d, g.ws.normed, g.rsq, g.rsq_bits, s));
+	prof_end(s);
+	return forward(layer, g.ws.normed, T, k, out, idx_out, w_out, flags, s, hidden);
 }
 
 } // namespace tie
@@ -434,12 +489,15 @@ extern "C" void tie_hip_shutdown(void)
 	if (g.ws.alloc)
 		(void)hipFree(g.ws.alloc);
 	g.ws = Workspace();
-	for (void *p : {(void *)g.x_dev, (void *)g.out_dev, (void *)g.w_dev, (void *)g.idx_dev, (void *)g.silu})
+	for (void *p : {(void *)g.x_dev, (void *)g.out_dev, (void *)g.w_dev, (void *)g.idx_dev, (void *)g.silu,
+			(void *)g.norm_dev, (void *)g.rsq})
 		if (p)
 			(void)hipFree(p);
-	g.x_dev = g.out_dev = g.w_dev = nullptr;
+	g.x_dev = g.out_dev = g.w_dev = g.norm_dev = nullptr;
 	g.idx_dev = nullptr;
 	g.silu = nullptr;
+	g.rsq = nullptr;
+	g.rsq_bits = 0;
 	g.io_tokens = g.io_d = g.io_k = 0;
 	(void)hipStreamDestroy(g.stream);
 	g.stream = nullptr;
@@ -503,10 +561,12 @@ extern "C" int tie_hip_moe_forward(tie_hip_layer *layer, const float *x_dev, int
 // The host-buffer drop-ins: the layer comes from the weight cache (uploaded
 // at the first call with these weights), x goes up, out and the selection
 // come back, and the call returns after the stream has drained.
+// With ffn_norm: the residual form, out = x + block(rms_norm(x)) (x and out
+// may be the same buffer: TIE's hidden state).
 static int moe_ffn_host(const float *x, int T, int d, int F, int E, int k, const void *router_w, int router_type,
 			int routing, const float *probs_bias, const void *gate_exps, int gate_type, const void *up_exps,
 			int up_type, const void *down_exps, int down_type, float *out, int32_t *topk_idx_opt,
-			float *topk_w_opt)
+			float *topk_w_opt, const float *ffn_norm = nullptr, float eps = 0.0f)
 {
 	std::lock_guard<std::recursive_mutex> lk(g.mu);
 	clear_error();
@@ -554,34 +614,55 @@ static int moe_ffn_host(const float *x, int T, int d, int F, int E, int k, const
 		return set_error(TIE_HIP_EINVAL, "k=%d outside [1, min(E=%d, %d)]", k, E, MAX_K);
 	if ((size_t)T > g.io_tokens || (size_t)d > g.io_d || (size_t)k > g.io_k) {
 		HIP_TRY(hipStreamSynchronize(g.stream));
-		for (void *p : {(void *)g.x_dev, (void *)g.out_dev, (void *)g.w_dev, (void *)g.idx_dev})
+		for (void *p : {(void *)g.x_dev, (void *)g.out_dev, (void *)g.w_dev, (void *)g.idx_dev, (void *)g.norm_dev})
 			if (p)
 				(void)hipFree(p);
-		g.x_dev = g.out_dev = g.w_dev = nullptr;
+		g.x_dev = g.out_dev = g.w_dev = g.norm_dev = nullptr;
 		g.idx_dev = nullptr;
 		g.io_tokens = g.io_d = g.io_k = 0;
 		const size_t nt = T, nd = d, nk = k;
 		if ((rc = dev_malloc((void **)&g.x_dev, nt * nd * 4, "x staging")) ||
 		    (rc = dev_malloc((void **)&g.out_dev, nt * nd * 4, "out staging")) ||
 		    (rc = dev_malloc((void **)&g.w_dev, nt * nk * 4, "topk staging")) ||
-		    (rc = dev_malloc((void **)&g.idx_dev, nt * nk * 4, "topk staging")))
+		    (rc = dev_malloc((void **)&g.idx_dev, nt * nk * 4, "topk staging")) ||
+		    (rc = dev_malloc((void **)&g.norm_dev, nd * 4, "ffn_norm staging")))
 			return rc;
 		g.io_tokens = nt;
 		g.io_d = nd;
 		g.io_k = nk;
 	}
 	HIP_TRY(hipMemcpyAsync(g.x_dev, x, (size_t)T * d * 4, hipMemcpyHostToDevice, g.stream));
-	rc = forward(layer, g.x_dev, T, k, g.out_dev, topk_idx_opt ? g.idx_dev : nullptr,
-		     topk_w_opt ? g.w_dev : nullptr, TIE_HIP_PATH_AUTO, g.stream);
+	if (ffn_norm) {
+		HIP_TRY(hipMemcpyAsync(g.norm_dev, ffn_norm, (size_t)d * 4, hipMemcpyHostToDevice, g.stream));
+		rc = forward_residual(layer, g.x_dev, g.norm_dev, eps, T, k, g.x_dev, topk_idx_opt ? g.idx_dev : nullptr,
+				      topk_w_opt ? g.w_dev : nullptr, TIE_HIP_PATH_AUTO, g.stream);
+	} else {
+		rc = forward(layer, g.x_dev, T, k, g.out_dev, topk_idx_opt ? g.idx_dev : nullptr,
+			     topk_w_opt ? g.w_dev : nullptr, TIE_HIP_PATH_AUTO, g.stream);
+	}
 	if (rc)
 		return rc;
-	HIP_TRY(hipMemcpyAsync(out, g.out_dev, (size_t)T * d * 4, hipMemcpyDeviceToHost, g.stream));
+	HIP_TRY(hipMemcpyAsync(out, ffn_norm ? g.x_dev : g.out_dev, (size_t)T * d * 4, hipMemcpyDeviceToHost, g.stream));
 	if (topk_idx_opt)
 		HIP_TRY(hipMemcpyAsync(topk_idx_opt, g.idx_dev, (size_t)T * k * 4, hipMemcpyDeviceToHost, g.stream));
 	if (topk_w_opt)
 		HIP_TRY(hipMemcpyAsync(topk_w_opt, g.w_dev, (size_t)T * k * 4, hipMemcpyDeviceToHost, g.stream));
 	HIP_TRY(hipStreamSynchronize(g.stream));
 	return TIE_HIP_OK;
+}
+
+extern "C" int tie_hip_moe_forward_residual(tie_hip_layer *layer, const float *hidden_dev, const float *ffn_norm_dev,
+					    float eps, int T, int k, float *out_dev, int32_t *topk_idx_dev, float *topk_w_dev,
+					    int flags, void *stream)
+{
+	std::lock_guard<std::recursive_mutex> lk(g.mu);
+	clear_error();
+	int rc = ensure_init();
+	if (rc)
+		return rc;
+	hipStream_t s = stream ? (hipStream_t)stream : g.stream;
+	return forward_residual(layer, hidden_dev, ffn_norm_dev, eps, T, k, out_dev, topk_idx_dev, topk_w_dev, flags,
+				s);
 }
 
 extern "C" int tie_hip_moe_ffn(const float *x, int T, int d, int F, int E, int k, const void *router_w,
@@ -601,6 +682,18 @@ extern "C" int tie_hip_moe_ffn_lfm2(const float *x, int T, int d, int F, int E, 
 	return moe_ffn_host(x, T, d, F, E, k, router_w, router_type, TIE_HIP_ROUTE_SIGMOID, probs_bias_opt,
 			    gate_exps, gate_type, up_exps, up_type, down_exps, down_type, out, topk_idx_opt,
 			    topk_w_opt);
+}
+
+extern "C" int tie_hip_qwen3_ffn(float *hidden, int T, int d, int F, int E, int k, const float *ffn_norm, float eps,
+				 const void *router_w, int router_type, const void *gate_exps, int gate_type,
+				 const void *up_exps, int up_type, const void *down_exps, int down_type,
+				 int32_t *topk_idx_opt, float *topk_w_opt)
+{
+	if (!ffn_norm && T > 0)
+		return set_error(TIE_HIP_EINVAL, "null ffn_norm");
+	return moe_ffn_host(hidden, T, d, F, E, k, router_w, router_type, TIE_HIP_ROUTE_SOFTMAX, nullptr, gate_exps,
+			    gate_type, up_exps, up_type, down_exps, down_type, hidden, topk_idx_opt, topk_w_opt, ffn_norm,
+			    eps);
 }
 
 extern "C" int tie_hip_exact_max_tokens(void)

@@ -81,6 +81,7 @@ struct Workspace {
 	float *h = nullptr;           // [2][T*k][F] gate and up row sums (exact path)
 	uint16_t *hb = nullptr;       // [T*k][F] SwiGLU activations (bf16 hi/lo, MFMA path)
 	float *y = nullptr;           // [T*k][d] expert outputs
+	float *normed = nullptr;      // [T][d]   RMSNorm of the hidden state (residual forward)
 	uint16_t *hlo = nullptr;      // [T*k][F] SwiGLU activations, bf16 remainder (MFMA path, BF16 weights)
 	uint16_t *xb = nullptr;       // [T][d]   x as bf16 (MFMA path)
 	uint16_t *xlo = nullptr;      // [T][d]   x - bf16(x) as bf16 (MFMA path, BF16 weights)
@@ -102,12 +103,16 @@ hipError_t launch_router_transpose(const Layer &L, hipStream_t s);
 hipError_t launch_dispatch(const Layer &L, int T, int k, const int32_t *topk_idx, Workspace &ws, hipStream_t s);
 hipError_t launch_route_group(const Layer &L, int T, int k, const float *logits, Workspace &ws, hipStream_t s);
 hipError_t launch_exact_block(const Layer &L, const float *x, int T, int k, const float *silu, Workspace &ws,
-			      float *out, hipStream_t s);
+			      float *out, hipStream_t s, const float *res = nullptr);
 hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, const float *silu, Workspace &ws,
 			       hipStream_t s);
 int mfma_max_tiles(int npairs, int E); // per list
+// res (optional): out = res + combine (the residual add after the block)
 hipError_t launch_combine(int T, int d, int k, const float *topk_w, const int32_t *topk_idx, const float *y,
-			  float *out, hipStream_t s);
+			  float *out, hipStream_t s, const float *res = nullptr);
+// TIE's RMSNorm of each row of x into out; tab/nbits: the host RSQRTSS table
+hipError_t launch_rmsnorm(const float *x, const float *w, float eps, int T, int d, float *out, const uint32_t *tab,
+			  int nbits, hipStream_t s);
 hipError_t launch_repack(const ExpertTensor &dst, const uint8_t *src, int E, int literal_bf16_stride, hipStream_t s);
 
 // Per-kernel timing (tie_hip_profile_enable): HIP events recorded on the

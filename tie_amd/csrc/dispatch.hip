@@ -156,10 +156,13 @@ hipError_t launch_route_group(const Layer &L, int T, int k, const float *logits,
 	return hipGetLastError();
 }
 
-// out[t][c] = fma(g_j, y[t*k+j][c], acc) for j = 0..k-1 (model_qwen3.c:459-467)
+// out[t][c] = fma(g_j, y[t*k+j][c], acc) for j = 0..k-1 (model_qwen3.c:459-467);
+// with res: out[t][c] = res[t][c] + acc, the residual add that follows the
+// block (dispatch_apply_residual, model_qwen3.c:491, apply_residual_f32_f32_avx2
+// math_avx2.c:731-751).  res may be out (the hidden state updated in place).
 __global__ __launch_bounds__(256) void combine_kernel(int T, int d, int k, const float *__restrict__ topk_w,
 						      const int32_t *__restrict__ topk_idx,
-						      const float *__restrict__ y, float *__restrict__ out)
+						      const float *__restrict__ y, const float *res, float *out)
 {
 	const int t = blockIdx.y;
 	const int c4 = blockIdx.x * blockDim.x + threadIdx.x; // float4 column
@@ -176,17 +179,24 @@ __global__ __launch_bounds__(256) void combine_kernel(int T, int d, int k, const
 		acc.z = __builtin_fmaf(g, v.z, acc.z);
 		acc.w = __builtin_fmaf(g, v.w, acc.w);
 	}
+	if (res) {
+		const float4 h = reinterpret_cast<const float4 *>(res + (size_t)t * d)[c4];
+		acc.x = h.x + acc.x;
+		acc.y = h.y + acc.y;
+		acc.z = h.z + acc.z;
+		acc.w = h.w + acc.w;
+	}
 	reinterpret_cast<float4 *>(out + (size_t)t * d)[c4] = acc;
 }
 
 hipError_t launch_combine(int T, int d, int k, const float *topk_w, const int32_t *topk_idx, const float *y,
-			  float *out, hipStream_t s)
+			  float *out, hipStream_t s, const float *res)
 {
 	if (T == 0)
 		return hipSuccess;
 	const int n4 = d / 4;
 	hipLaunchKernelGGL(combine_kernel, dim3((n4 + 255) / 256, T), dim3(256), 0, s, T, d, k, topk_w, topk_idx, y,
-			   out);
+			   res, out);
 	return hipGetLastError();
 }
 

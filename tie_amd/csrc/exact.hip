@@ -1082,7 +1082,7 @@ static hipError_t launch_gu_q(int type, bool fused, int nmat, int rows, int in, 
 // path.  ws.h holds two [pairs][F] planes: the gate and the up row sums, or
 // (fused gate/up) h in the first.
 hipError_t launch_exact_block(const Layer &L, const float *x, int T, int k, const float *silu, Workspace &ws,
-			      float *out, hipStream_t s)
+			      float *out, hipStream_t s, const float *res)
 {
 	const int npairs = T * k;
 	if (npairs == 0)
@@ -1235,7 +1235,7 @@ hipError_t launch_exact_block(const Layer &L, const float *x, int T, int k, cons
 	if (err != hipSuccess)
 		return err;
 	prof_begin("combine", s);
-	err = launch_combine(T, L.d, k, ws.topk_w, ws.topk_idx, ws.y, out, s);
+	err = launch_combine(T, L.d, k, ws.topk_w, ws.topk_idx, ws.y, out, s, res);
 	prof_end(s);
 	return err;
 }

@@ -6,6 +6,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <vector>
+
 #include "../../include/tie_hip.h"
 #include "tie_expf.h"
 
@@ -93,6 +95,76 @@ int silu_table_host(float *tab, int n)
 	if (!__builtin_cpu_supports("avx2") || !__builtin_cpu_supports("fma"))
 		return set_error(TIE_HIP_EINVAL, "host CPU lacks AVX2/FMA (TIE requires AVX2, engine.c:17-21)");
 	silu_table_build(tab, __builtin_cpu_supports("avx512f"));
+	return TIE_HIP_OK;
+}
+
+// ----------------------------------------------------------- rsqrt table
+// TIE's rms_norm (rms_norm_f32_f32_f32_avx2, math_avx2.c:56-96) computes
+// 1.0f / sqrtf(ss / size + eps).  Under -ffast-math GCC emits RSQRTSS and
+// one Newton step: y0 = rsqrtss(a), inv = fma(a * y0, y0, -3) * (y0 * -0.5)
+// (ix86's software rsqrt).  The approximate y0 is a property of the CPU, so
+// the library tabulates the host's RSQRTSS: its output for a and for a * 4^s
+// differ only in the exponent (checked below), so it is a function of the
+// exponent parity and of the mantissa, and on the CPUs seen so far of only
+// its top few bits (10 on current Intel server parts).  The table holds,
+// for parity p (biased exponent 126 + p) and the top `nbits` mantissa bits
+// j, the bits of rsqrtss(2^(p-1) * 1.j).
+
+__attribute__((target("sse"))) static float rsqrtss(float a)
+{
+	return _mm_cvtss_f32(_mm_rsqrt_ss(_mm_set_ss(a)));
+}
+
+static uint32_t fbits(float f)
+{
+	uint32_t u;
+	memcpy(&u, &f, 4);
+	return u;
+}
+
+static float bitsf(uint32_t u)
+{
+	float f;
+	memcpy(&f, &u, 4);
+	return f;
+}
+
+int rsqrt_table_host(std::vector<uint32_t> &tab, int &nbits)
+{
+	constexpr uint32_t M = 1u << 23;
+	std::vector<uint32_t> all(2 * M);
+	for (uint32_t p = 0; p < 2; p++)
+		for (uint32_t m = 0; m < M; m++)
+			all[p * M + m] = fbits(rsqrtss(bitsf(((126u + p) << 23) | m)));
+	// the fewest leading mantissa bits the output depends on
+	int n = 0;
+	for (uint32_t p = 0; p < 2; p++)
+		for (uint32_t m = 1; m < M; m++)
+			if (all[p * M + m] != all[p * M + m - 1]) {
+				const int need = 23 - __builtin_ctz(m);
+				n = need > n ? need : n;
+			}
+	// exponent scaling: rsqrtss(a * 4^s) = rsqrtss(a) * 2^-s over the normal
+	// range, on every mantissa of a stride that visits all index values
+	for (int s = -62; s <= 64; s++) {
+		for (uint32_t p = 0; p < 2; p++) {
+			const int eb = 126 + (int)p + 2 * s;
+			if (eb < 1 || eb > 254)
+				continue;
+			for (uint32_t m = 0; m < M; m += 1021) {
+				const uint32_t want = all[p * M + m] - (uint32_t)(s * (1 << 23));
+				if (fbits(rsqrtss(bitsf(((uint32_t)eb << 23) | m))) != want)
+					return set_error(TIE_HIP_EINVAL,
+							 "host RSQRTSS does not scale with the exponent (exponent %d, mantissa %u)",
+							 eb, m);
+			}
+		}
+	}
+	nbits = n;
+	tab.assign(2u << n, 0);
+	for (uint32_t p = 0; p < 2; p++)
+		for (uint32_t j = 0; j < (1u << n); j++)
+			tab[(p << n) + j] = all[p * M + (j << (23 - n))];
 	return TIE_HIP_OK;
 }
 

@@ -35,6 +35,7 @@ _NAMES = (
     ("tie::route_group_kernel", "route_group"),
     ("tie::dispatch_kernel", "dispatch"),
     ("tie::combine_kernel", "combine"),
+    ("tie::rmsnorm_kernel", "rmsnorm"),
     ("tie::to_bf16_kernel", "mfma_gate_up"),
     ("tie::to_split_kernel", "mfma_gate_up"),
 )

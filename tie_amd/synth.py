@@ -127,19 +127,28 @@ def make_layer(seed, d, F, E, gu_type=Q4_K, down_type=Q6_K, zipf=None, routing=0
     return MoELayer(d, F, E, gate, up, down, router, gu_type, down_type, bias, routing, pb)
 
 
+def make_norm_weight(seed, d):
+    """RMSNorm weight (ffn_norm) ~ N(1, 0.1), seeded."""
+    rng = np.random.default_rng(seed + 2000003)
+    return rng.normal(1.0, 0.1, size=d).astype(np.float32)
+
+
 def make_input(seed, T, d):
     rng = np.random.default_rng(seed + 1000003)
     return rng.normal(0.0, 1.0, size=(T, d)).astype(np.float32)
 
 
 # The workload configs of the MoE block benchmark (30B-A3B / 235B-A22B shapes;
-# lfm2_*: LFM2-8B-A1B-shaped blocks with sigmoid routing and a selection bias).
+# lfm2_*: LFM2-8B-A1B-shaped blocks with sigmoid routing and a selection bias;
+# *_ffn: the FFN half of the layer, RMSNorm before and the residual add after).
 CONFIGS = {
     "30b_t1": dict(d=2048, F=768, E=128, k=8, T=1, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1234),
     "30b_t2": dict(d=2048, F=768, E=128, k=8, T=2, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1242),
     "30b_t4": dict(d=2048, F=768, E=128, k=8, T=4, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1244),
     "30b_t8": dict(d=2048, F=768, E=128, k=8, T=8, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1240),
     "30b_t32": dict(d=2048, F=768, E=128, k=8, T=32, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1235),
+    "30b_t32_ffn": dict(d=2048, F=768, E=128, k=8, T=32, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1235,
+                        residual=True),
     "30b_t2048": dict(d=2048, F=768, E=128, k=8, T=2048, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1236),
     "30b_bf16_zipf_t512": dict(d=2048, F=768, E=128, k=8, T=512, gu_type=BF16, down_type=BF16, zipf=1.2,
                                seed=1237),
