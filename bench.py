@@ -92,6 +92,57 @@ class Workload:
         torch.cuda.empty_cache()
 
 
+def run_dense(torch, tie_amd, cfg, steps, warmup, n_copies):
+    """dispatch_mat_mat through tie_hip_mat_mat: T rows of x times one
+    [rows][in] weight matrix, cycling `n_copies` matrices so the MALL does
+    not hold the weights.  Same result fields as run_config."""
+    from tie_amd import synth
+    rows, in_dim, T, wtype = cfg["rows"], cfg["in"], cfg["T"], cfg["wtype"]
+    g = torch.Generator(device="cuda")
+    g.manual_seed(cfg["seed"])
+    mats = []
+    for i in range(n_copies):
+        if wtype == synth.F32:
+            w = torch.randn(rows * in_dim, generator=g, device="cuda") * 0.02
+        else:
+            rng = np.random.default_rng(cfg["seed"] + i)
+            w = torch.from_numpy(synth.expert_tensor(rng, wtype, 1, rows, in_dim)).cuda()
+        mats.append(tie_amd.Matrix(w, wtype, rows, in_dim, on_device=True))
+        del w
+    X = torch.randn(n_copies, T, in_dim, generator=g, device="cuda")
+    out = torch.empty(T, rows, device="cuda")
+
+    def step(s):
+        mats[s % n_copies].mat_mat(X[s % n_copies], T, out)
+
+    for s in range(warmup):
+        step(s)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(steps):
+        step(s)
+    torch.cuda.synchronize()
+    ms = 1e3 * (time.perf_counter() - t0) / steps
+    tie_amd.profile_enable(True)
+    for s in range(steps):
+        step(s)
+    prof = tie_amd.profile_read()
+    tie_amd.profile_enable(False)
+    wbytes = rows * synth.row_bytes(wtype, in_dim)
+    nbytes = wbytes + T * in_dim * 4 + T * rows * 4
+    flops = 2.0 * T * rows * in_dim
+    tot, n = prof.get("dense", (0.0, 0))
+    avg_ms = tot / n if n else ms
+    kernels = {"dense": {"avg_us": round(1e3 * avg_ms, 3), "launches": n, "alg_bytes": nbytes,
+                         "GBps": round(nbytes / (avg_ms * 1e-3) / 1e9, 1), "alg_flops": flops,
+                         "TFLOPs": round(flops / (avg_ms * 1e-3) / 1e12, 2)}}
+    for mt in mats:
+        mt.close()
+    return dict(T=T, k=0, ms=ms, tokens_per_s=T / (ms * 1e-3), U=1, block_bytes=nbytes, block_flops=flops,
+                block_GBps=nbytes / (ms * 1e-3) / 1e9, block_TFLOPs=flops / (ms * 1e-3) / 1e12, kernels=kernels,
+                layers=n_copies)
+
+
 def expert_bytes(cfg):
     """HBM bytes of one expert: gate + up together, and down."""
     from tie_amd import synth
@@ -305,6 +356,14 @@ def main():
     results = {}
     for name in names:
         cfg = dict(synth.CONFIGS[name])
+        if cfg.get("kind") == "dense":
+            steps = max(10, args.steps // 4)
+            wbytes = cfg["rows"] * synth.row_bytes(cfg["wtype"], cfg["in"])
+            ncp = max(2, min(64, int(1.2e9 // wbytes)))
+            log("timing dense %s: %d x %d, T=%d, %d matrices" % (name, cfg["rows"], cfg["in"], cfg["T"], ncp))
+            results[name] = run_dense(torch, tie_amd, cfg, steps, max(2, args.warmup // 4), ncp)
+            log(json.dumps({name: results[name]}))
+            continue
         key = (cfg["d"], cfg["F"], cfg["E"], cfg["gu_type"], cfg["down_type"], cfg.get("zipf"), cfg.get("routing", 0),
                cfg.get("probs_bias"))
         if key not in workloads:

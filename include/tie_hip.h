@@ -160,6 +160,27 @@ int tie_hip_moe_forward_residual(tie_hip_layer *layer, const float *hidden_dev, 
 				 int T, int k, float *out_dev, int32_t *topk_idx_dev, float *topk_w_dev, int flags,
 				 void *stream);
 
+/* ------------------------------------------------------------------ */
+/* Dense matrices (dispatch_mat_mat with F32 input)                     */
+/* ------------------------------------------------------------------ */
+
+typedef struct tie_hip_matrix tie_hip_matrix;
+
+/* Upload one GGUF weight matrix [rows][in_dim] (ne = [in_dim, rows]) of type
+ * TIE_GGML_F32, Q4_K, Q6_K or BF16 (repacked into the panel layout); rows a
+ * multiple of 64, in_dim a multiple of 256 up to 16384.  The source may be
+ * freed afterwards. */
+int tie_hip_matrix_create(const void *w, int type, int rows, int in_dim, int src_on_device, tie_hip_matrix **out);
+void tie_hip_matrix_destroy(tie_hip_matrix *m);
+
+/* dispatch_mat_mat (math_dispatch.c:304-359) on device pointers:
+ * out_dev[t][r] = W[r] . x_dev[t] for t < T, x [T][in_dim] F32, out
+ * [T][rows] F32, with TIE's row kernels (mat_vec_row_f32_{f32,q4k,q6k,
+ * bf16}_f32_avx2) bit for bit; flags must not ask for TIE_HIP_PATH_MFMA.
+ * Enqueued on `stream`.  The attention projections, the dense FFN and the LM
+ * head of transformer_layer_qwen3 / main.c use it. */
+int tie_hip_mat_mat(tie_hip_matrix *m, const float *x_dev, int T, float *out_dev, int flags, void *stream);
+
 /* The largest T that TIE_HIP_PATH_AUTO sends down the exact path. */
 int tie_hip_exact_max_tokens(void);
 void tie_hip_set_exact_max_tokens(int t);

@@ -173,6 +173,17 @@ def qwen3_ffn(layer, hidden, k, ffn_norm, eps, silu_tab=None, nthreads=8):
     return h, idx, w
 
 
+def mat_mat(x, w, wtype, rows):
+    """Oracle dispatch_mat_mat with F32 input: every row of x through TIE's
+    row kernel for the weight type."""
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty((x.shape[0], rows), np.float32)
+    for t in range(x.shape[0]):
+        if oracle().orc_matvec(_ptr(x[t]), _ptr(w), wtype, x.shape[1], rows, _ptr(out[t])) != 0:
+            raise ValueError("oracle rejected the matrix type")
+    return out
+
+
 def ref_silu_table(nthreads=8):
     t = np.empty(SILU_N, np.float32)
     if ref().ref_silu_table(_ptr(t), nthreads) != 0:

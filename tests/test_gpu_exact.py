@@ -90,6 +90,29 @@ def test_lfm2_one_token_without_bias():
             run_both(layer, synth.make_input(27 + T, T, 512), k)
 
 
+@pytest.mark.parametrize("wtype", [synth.Q4_K, synth.Q6_K, synth.BF16, synth.F32])
+def test_dense_mat_mat(wtype):
+    """tie_hip_mat_mat (dispatch_mat_mat with F32 input) against the oracle's
+    row kernels, bit for bit, for ragged token counts."""
+    import torch
+    rows, in_dim = 512, 1024
+    rng = np.random.default_rng(40 + wtype)
+    if wtype == synth.F32:
+        w = rng.normal(0, 0.02, size=rows * in_dim).astype(np.float32)
+    else:
+        w = synth.expert_tensor(rng, wtype, 1, rows, in_dim)
+    M = tie_amd.Matrix(w, wtype, rows, in_dim)
+    for T in (1, 5, 37, 200):
+        x = synth.make_input(41 + T, T, in_dim)
+        print("dense case type=%d T=%d" % (wtype, T), flush=True)
+        xd = torch.from_numpy(x).cuda()
+        out = torch.empty((T, rows), device="cuda")
+        M.mat_mat(xd, T, out)
+        torch.cuda.synchronize()
+        assert_same(out.cpu().numpy(), bind.mat_mat(x, w, wtype, rows), "dense out")
+    M.close()
+
+
 @pytest.mark.parametrize("name", ["gffn_qwen3_t3", "gffn_tiny_t5"])
 def test_qwen3_ffn_residual(name):
     """tie_hip_qwen3_ffn: RMSNorm (with the host RSQRTSS table), block and

@@ -24,7 +24,8 @@ SILU_TABLE_SIZE = 8192
 # every symbol include/tie_hip.h declares
 EXPORTS = (
     "tie_hip_init", "tie_hip_shutdown", "tie_hip_last_error", "tie_hip_moe_ffn", "tie_hip_moe_ffn_lfm2",
-    "tie_hip_qwen3_ffn", "tie_hip_moe_forward_residual", "tie_hip_set_silu_table",
+    "tie_hip_qwen3_ffn", "tie_hip_moe_forward_residual", "tie_hip_matrix_create", "tie_hip_matrix_destroy",
+    "tie_hip_mat_mat", "tie_hip_set_silu_table",
     "tie_hip_silu_table_host", "tie_hip_layer_create", "tie_hip_layer_destroy", "tie_hip_layer_bytes",
     "tie_hip_moe_forward", "tie_hip_exact_max_tokens", "tie_hip_set_exact_max_tokens",
     "tie_hip_debug_fail_alloc", "tie_hip_host_expf", "tie_hip_profile_enable", "tie_hip_profile_read",
@@ -75,6 +76,12 @@ def lib():
         L.tie_hip_qwen3_ffn.restype = I
         L.tie_hip_moe_forward_residual.argtypes = [P, P, P, ctypes.c_float, I, I, P, P, P, I, P]
         L.tie_hip_moe_forward_residual.restype = I
+        L.tie_hip_matrix_create.argtypes = [P, I, I, I, I, ctypes.POINTER(ctypes.c_void_p)]
+        L.tie_hip_matrix_create.restype = I
+        L.tie_hip_matrix_destroy.argtypes = [P]
+        L.tie_hip_matrix_destroy.restype = None
+        L.tie_hip_mat_mat.argtypes = [P, P, I, P, I, P]
+        L.tie_hip_mat_mat.restype = I
         L.tie_hip_set_silu_table.argtypes = [P, I]
         L.tie_hip_set_silu_table.restype = I
         L.tie_hip_silu_table_host.argtypes = [P, I]
@@ -201,6 +208,32 @@ def qwen3_ffn(hidden, layer, k, ffn_norm, eps, with_topk=True):
                                   _p(layer.gate), layer.gate_type, _p(layer.up), layer.up_type, _p(layer.down),
                                   layer.down_type, _p(idx), _p(w)))
     return h, idx, w
+
+
+class Matrix:
+    """A device-resident dense weight matrix (tie_hip_matrix_create):
+    GGUF layout [rows][in_dim] of type F32, Q4_K, Q6_K or BF16."""
+
+    def __init__(self, w, wtype, rows, in_dim, on_device=False):
+        self.rows, self.in_dim = rows, in_dim
+        h = ctypes.c_void_p()
+        check(lib().tie_hip_matrix_create(_p(w), wtype, rows, in_dim, int(on_device), ctypes.byref(h)))
+        self.handle = h
+
+    def mat_mat(self, x_dev, T, out_dev, flags=PATH_EXACT, stream=None):
+        """out[t][r] = W[r] . x[t] on device pointers (dispatch_mat_mat)."""
+        check(lib().tie_hip_mat_mat(self.handle, _p(x_dev), T, _p(out_dev), flags, stream))
+
+    def close(self):
+        if self.handle:
+            lib().tie_hip_matrix_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 class Layer:

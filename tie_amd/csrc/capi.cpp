@@ -22,6 +22,13 @@ struct tie_hip_layer {
 	tie::Layer L;
 };
 
+struct tie_hip_matrix {
+	tie::ExpertTensor W; // quantised / BF16 weights in the panel layout
+	tie::Layer F;        // F32 weights: the router kernels' [rows][in] matrix
+	void *alloc = nullptr;
+	size_t bytes = 0;
+};
+
 namespace tie {
 
 struct Ctx {
@@ -648,6 +655,119 @@ static int moe_ffn_host(const float *x, int T, int d, int F, int E, int k, const
 	if (topk_w_opt)
 		HIP_TRY(hipMemcpyAsync(topk_w_opt, g.w_dev, (size_t)T * k * 4, hipMemcpyDeviceToHost, g.stream));
 	HIP_TRY(hipStreamSynchronize(g.stream));
+	return TIE_HIP_OK;
+}
+
+extern "C" int tie_hip_matrix_create(const void *w, int type, int rows, int in_dim, int src_on_device,
+				     tie_hip_matrix **out)
+{
+	std::lock_guard<std::recursive_mutex> lk(g.mu);
+	clear_error();
+	if (!out || !w)
+		return set_error(TIE_HIP_EINVAL, "null argument");
+	*out = nullptr;
+	int rc = ensure_init();
+	if (rc)
+		return rc;
+	if (rows <= 0 || in_dim <= 0 || rows % PANEL_ROWS)
+		return set_error(TIE_HIP_EINVAL, "rows=%d must be a positive multiple of %d, in=%d", rows, PANEL_ROWS, in_dim);
+	if (type != TIE_GGML_F32 && !expert_type_ok(type))
+		return set_error(TIE_HIP_EINVAL, "matrix type %d unsupported (F32, Q4_K, Q6_K, BF16)", type);
+	if (in_dim % QK || in_dim > 64 * QK)
+		return set_error(TIE_HIP_EINVAL, "in=%d must be a multiple of 256 up to 16384", in_dim);
+	tie_hip_matrix *m = new tie_hip_matrix();
+	const size_t bytes = (size_t)rows * row_bytes(type, in_dim);
+	rc = dev_malloc(&m->alloc, bytes, "matrix weights");
+	if (rc) {
+		delete m;
+		return rc;
+	}
+	m->bytes = bytes;
+	const hipMemcpyKind kind = src_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
+	hipError_t e = hipSuccess;
+	if (type == TIE_GGML_F32) {
+		e = hipMemcpyAsync(m->alloc, w, bytes, kind, g.stream);
+		m->F.d = in_dim;
+		m->F.E = rows;
+		m->F.router = (const float *)m->alloc;
+	} else {
+		ExpertTensor &t = m->W;
+		t.type = type;
+		t.rows = rows;
+		t.in = in_dim;
+		t.nb = in_dim / QK;
+		t.rt = rows / PANEL_ROWS;
+		t.expert_bytes = bytes;
+		t.data = (const uint8_t *)m->alloc;
+		void *tmp = nullptr;
+		const uint8_t *src = (const uint8_t *)w;
+		if (!src_on_device) {
+			rc = dev_malloc(&tmp, bytes, "upload staging");
+			if (!rc)
+				e = hipMemcpyAsync(tmp, w, bytes, hipMemcpyHostToDevice, g.stream);
+			src = (const uint8_t *)tmp;
+		}
+		if (!rc && e == hipSuccess)
+			e = launch_repack(t, src, 1, 0, g.stream);
+		if (e == hipSuccess)
+			e = hipStreamSynchronize(g.stream);
+		if (tmp)
+			(void)hipFree(tmp);
+	}
+	if (e == hipSuccess && !rc)
+		e = hipStreamSynchronize(g.stream);
+	if (rc || e != hipSuccess) {
+		(void)hipFree(m->alloc);
+		delete m;
+		if (rc)
+			return rc;
+		return set_error(TIE_HIP_EHIP, "matrix upload failed: %s", hipGetErrorString(e));
+	}
+	*out = m;
+	return TIE_HIP_OK;
+}
+
+extern "C" void tie_hip_matrix_destroy(tie_hip_matrix *m)
+{
+	std::lock_guard<std::recursive_mutex> lk(g.mu);
+	if (!m)
+		return;
+	if (g.device >= 0)
+		(void)hipStreamSynchronize(g.stream);
+	if (m->alloc)
+		(void)hipFree(m->alloc);
+	delete m;
+}
+
+extern "C" int tie_hip_mat_mat(tie_hip_matrix *m, const float *x_dev, int T, float *out_dev, int flags, void *stream)
+{
+	std::lock_guard<std::recursive_mutex> lk(g.mu);
+	clear_error();
+	int rc = ensure_init();
+	if (rc)
+		return rc;
+	if (!m)
+		return set_error(TIE_HIP_EINVAL, "null matrix");
+	if (T < 0)
+		return set_error(TIE_HIP_EINVAL, "T=%d < 0", T);
+	if (T == 0)
+		return TIE_HIP_OK;
+	if (!x_dev || !out_dev)
+		return set_error(TIE_HIP_EINVAL, "null x/out");
+	if (flags & TIE_HIP_PATH_MFMA)
+		return set_error(TIE_HIP_EINVAL, "tie_hip_mat_mat runs TIE's row kernels only (TIE_HIP_PATH_EXACT)");
+	hipStream_t s = stream ? (hipStream_t)stream : g.stream;
+	prof_begin("dense", s);
+	if (m->F.router) {
+		HIP_TRY(launch_router_logits(m->F, x_dev, T, out_dev, s));
+	} else {
+		const int G = dense_groups(T);
+		rc = ensure_workspace(T, 1, m->W.in, QK, G);
+		if (rc)
+			return rc;
+		HIP_TRY(launch_dense(m->W, x_dev, T, out_dev, g.ws, s));
+	}
+	prof_end(s);
 	return TIE_HIP_OK;
 }
 

@@ -107,6 +107,11 @@ hipError_t launch_exact_block(const Layer &L, const float *x, int T, int k, cons
 hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, const float *silu, Workspace &ws,
 			       hipStream_t s);
 int mfma_max_tiles(int npairs, int E); // per list
+// Dense F32-input matrix product through the expert GEMV kernels: out[t][r]
+// = W[r] . x[t] (W one "expert": rows, in, panel layout); dense_groups(T)
+// token groups (the workspace needs that many experts and T pairs)
+hipError_t launch_dense(const ExpertTensor &W, const float *x, int T, float *out, Workspace &ws, hipStream_t s);
+int dense_groups(int T);
 // res (optional): out = res + combine (the residual add after the block)
 hipError_t launch_combine(int T, int d, int k, const float *topk_w, const int32_t *topk_idx, const float *y,
 			  float *out, hipStream_t s, const float *res = nullptr);

@@ -1240,4 +1240,62 @@ hipError_t launch_exact_block(const Layer &L, const float *x, int T, int k, cons
 	return err;
 }
 
+// ------------------------------------------------------------ dense
+// dispatch_mat_mat (math_dispatch.c:304-359) with F32 input: every token row
+// through the same row kernel as the experts (mat_vec_row_f32_{q4k,q6k,
+// bf16}_f32_avx2), so the expert GEMV kernels run it unchanged: the tokens
+// are split into groups of DENSE_GROUP, and each group is an "expert" of
+// stride 0 (every group reads the one matrix), so groups spread over the
+// grid's y dimension and each workgroup computes one 64-row panel for one
+// group.  out[t][r], [T][rows].
+constexpr int DENSE_GROUP = 8;
+
+__global__ void dense_groups_kernel(int T, int G, int32_t *offsets, int32_t *pairs, int32_t *active)
+{
+	const int i = blockIdx.x * blockDim.x + threadIdx.x;
+	if (i < T)
+		pairs[i] = i;
+	if (i <= G) {
+		offsets[i] = i * DENSE_GROUP < T ? i * DENSE_GROUP : T;
+		active[i] = i < G ? i : G;
+	}
+}
+
+int dense_groups(int T)
+{
+	return (T + DENSE_GROUP - 1) / DENSE_GROUP;
+}
+
+hipError_t launch_dense(const ExpertTensor &W, const float *x, int T, float *out, Workspace &ws, hipStream_t s)
+{
+	if (T == 0)
+		return hipSuccess;
+	const int G = dense_groups(T);
+	hipLaunchKernelGGL(dense_groups_kernel, dim3((T + 1 + 255) / 256 > (G + 1 + 255) / 256 ? (T + 1 + 255) / 256
+											  : (G + 1 + 255) / 256),
+			   dim3(256), 0, s, T, G, ws.offsets, ws.pairs, ws.active);
+	hipError_t err = hipGetLastError();
+	if (err != hipSuccess)
+		return err;
+	ExactArgs a;
+	memset(&a, 0, sizeof a);
+	a.w[0] = W.data;
+	a.expert_bytes[0] = 0;
+	a.k = 1;
+	a.E = G;
+	a.T = T;
+	a.x = x;
+	a.sums[0] = out;
+	a.offsets = ws.offsets;
+	a.pairs = ws.pairs;
+	a.active = ws.active;
+	a.rows = W.rows;
+	a.in = W.in;
+	if (W.type == TIE_GGML_BF16) {
+		hipLaunchKernelGGL(exact_gu_bf16_kernel, dim3(W.rows / PANEL_ROWS, G, 1), dim3(BF_THREADS), 0, s, a);
+		return hipGetLastError();
+	}
+	return launch_gu_q(W.type, false, 1, W.rows, W.in, G, a, s);
+}
+
 } // namespace tie

@@ -274,13 +274,13 @@ __global__ __launch_bounds__(RW_THREADS) void router_topk_kernel(const float *__
 hipError_t launch_router_logits(const Layer &L, const float *x, int T, float *logits, hipStream_t s)
 {
 	const int d = L.d, E = L.E;
-	if (T <= RS_TOK) {
+	if (T <= RS_TOK && sizeof(float) * (size_t)d * (1 + RS_TOK) <= 160 * 1024) {
 		const size_t lds = sizeof(float) * (size_t)d * (1 + RS_TOK);
 		hipLaunchKernelGGL(router_small_kernel, dim3(E), dim3(RS_THREADS), lds, s, x, L.router, L.bias, T, d, E,
 				   logits);
 		return hipGetLastError();
 	}
-	if (T > 2 * RT_TOK && E % RT_EXP == 0 && d % RT_KC == 0) {
+	if (T > 2 * RT_TOK && E % RT_EXP == 0 && d % RT_KC == 0 && L.routerT) {
 		static bool attr = false;
 		if (!attr) {
 			const hipError_t err = hipFuncSetAttribute((const void *)router_logits_kernel,

@@ -157,5 +157,10 @@ CONFIGS = {
                     routing=1, probs_bias=0.05),
     "lfm2_t32": dict(d=2048, F=1792, E=32, k=4, T=32, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1251,
                      routing=1, probs_bias=0.05),
+    # dense matrices (dispatch_mat_mat): a q_proj-shaped Q4_K matrix and a
+    # Q6_K LM head (151936 x 2048) of the 30B model
+    "dense_q4k_t1": dict(kind="dense", rows=4096, **{"in": 2048}, wtype=Q4_K, T=1, seed=1270),
+    "dense_q4k_t32": dict(kind="dense", rows=4096, **{"in": 2048}, wtype=Q4_K, T=32, seed=1271),
+    "lmhead_q6k_t1": dict(kind="dense", rows=151936, **{"in": 2048}, wtype=Q6_K, T=1, seed=1272),
     "235b_t1024": dict(d=4096, F=1536, E=128, k=8, T=1024, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1239),
 }
