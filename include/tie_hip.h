@@ -181,6 +181,38 @@ void tie_hip_matrix_destroy(tie_hip_matrix *m);
  * head of transformer_layer_qwen3 / main.c use it. */
 int tie_hip_mat_mat(tie_hip_matrix *m, const float *x_dev, int T, float *out_dev, int flags, void *stream);
 
+/* ------------------------------------------------------------------ */
+/* GGUF models: every MoE layer uploaded once                           */
+/* ------------------------------------------------------------------ */
+
+typedef struct tie_hip_model_info {
+	char architecture[32]; /* general.architecture */
+	int d, F, E, k;        /* embedding_length, expert_feed_forward_length, expert_count, expert_used_count */
+	int n_layers;          /* block_count */
+	int first_moe_layer;   /* leading_dense_block_count (LFM2), else 0 */
+	float norm_eps;        /* attention.layer_norm_rms_epsilon */
+	int routing;           /* TIE_HIP_ROUTE_SIGMOID for LFM2, else TIE_HIP_ROUTE_SOFTMAX */
+} tie_hip_model_info;
+
+typedef struct tie_hip_model tie_hip_model;
+
+/* Read the MoE shape of a GGUF file (host only, no GPU needed). */
+int tie_hip_gguf_inspect(const char *path, tie_hip_model_info *info);
+
+/* Map a GGUF file and upload the MoE FFN of every layer from
+ * first_moe_layer on: blk.N.ffn_gate_inp / ffn_gate_exps / ffn_up_exps /
+ * ffn_down_exps (and exp_probs_b.bias for LFM2) into a tie_hip_layer, and
+ * blk.N.ffn_norm.weight to the device, as TIE's model loading maps them
+ * (gguf_model_map_weights, gguf.c:892-966; model_load_tensor, model.c:198-235).
+ * The file is unmapped before returning. */
+int tie_hip_gguf_load(const char *path, tie_hip_model **out);
+void tie_hip_model_info_get(const tie_hip_model *m, tie_hip_model_info *info);
+/* Layer n's block (NULL for a dense layer) and its device ffn_norm [d] (NULL
+ * when the file has none). */
+tie_hip_layer *tie_hip_model_layer(tie_hip_model *m, int n);
+const float *tie_hip_model_ffn_norm(const tie_hip_model *m, int n);
+void tie_hip_model_close(tie_hip_model *m);
+
 /* The largest T that TIE_HIP_PATH_AUTO sends down the exact path. */
 int tie_hip_exact_max_tokens(void);
 void tie_hip_set_exact_max_tokens(int t);

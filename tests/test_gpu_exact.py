@@ -287,3 +287,47 @@ def test_argument_errors_and_injected_oom():
         tie_amd.moe_ffn(x, other, 4)  # first call uploads: that allocation fails
     assert e.value.code == tie_amd.ENOMEM
     run_both(other, x, 4)  # and the library recovers
+
+
+def test_gguf_model_load(tmp_path):
+    """tie_hip_gguf_load: a qwen3moe file's layers run the FFN half
+    (RMSNorm with the file's ffn_norm, block, residual) bit-exact against the
+    oracle on the same tensors; an lfm2 file's layer routes by sigmoid with
+    its exp_probs_b bias and skips the leading dense layers."""
+    import torch
+    from gguf_write import moe_model_file
+    d, F, E, k, T = 512, 256, 16, 4, 6
+    layers = [synth.make_layer(70 + i, d, F, E, synth.Q4_K, synth.Q6_K) for i in range(2)]
+    norms = [synth.make_norm_weight(70 + i, d) for i in range(2)]
+    p = str(tmp_path / "q.gguf")
+    moe_model_file(p, "qwen3moe", layers, d, F, E, k, eps=1e-6, norms=norms)
+    M = tie_amd.Model(p)
+    assert (M.info.n_layers, M.info.routing) == (2, tie_amd.ROUTE_SOFTMAX)
+    for n in range(2):
+        hidden = synth.make_input(80 + n, T, d) * np.float32(2.0)
+        hd = torch.from_numpy(hidden).cuda()
+        print("gguf qwen3moe layer %d" % n, flush=True)
+        M.layer(n).forward_residual(hd, M.ffn_norm(n), M.info.norm_eps, T, k, None, flags=tie_amd.PATH_EXACT)
+        torch.cuda.synchronize()
+        rh, _, _ = bind.qwen3_ffn(layers[n], hidden, k, norms[n], float(M.info.norm_eps))
+        assert_same(hd.cpu().numpy(), rh, "gguf layer %d hidden" % n)
+    M.close()
+
+    lay = synth.make_layer(75, d, F, E, synth.Q4_K, synth.Q6_K, routing=1, probs_bias=0.05)
+    p2 = str(tmp_path / "l.gguf")
+    moe_model_file(p2, "lfm2", [lay], d, F, E, k, pbias=[lay.probs_bias], lead=1)
+    M = tie_amd.Model(p2)
+    assert M.layer(0) is None and M.layer(1) is not None
+    x = synth.make_input(85, T, d)
+    xd = torch.from_numpy(x).cuda()
+    out = torch.empty_like(xd)
+    idx = torch.empty((T, k), dtype=torch.int32, device="cuda")
+    w = torch.empty((T, k), dtype=torch.float32, device="cuda")
+    print("gguf lfm2 layer 1", flush=True)
+    M.layer(1).forward(xd, T, k, out, idx, w, flags=tie_amd.PATH_EXACT)
+    torch.cuda.synchronize()
+    ro, ri, rw = bind.moe_block(lay, x, k)
+    assert_same(idx.cpu().numpy(), ri, "lfm2 topk_idx")
+    assert_same(w.cpu().numpy(), rw, "lfm2 topk_w")
+    assert_same(out.cpu().numpy(), ro, "lfm2 out")
+    M.close()

@@ -25,7 +25,8 @@ SILU_TABLE_SIZE = 8192
 EXPORTS = (
     "tie_hip_init", "tie_hip_shutdown", "tie_hip_last_error", "tie_hip_moe_ffn", "tie_hip_moe_ffn_lfm2",
     "tie_hip_qwen3_ffn", "tie_hip_moe_forward_residual", "tie_hip_matrix_create", "tie_hip_matrix_destroy",
-    "tie_hip_mat_mat", "tie_hip_set_silu_table",
+    "tie_hip_mat_mat", "tie_hip_gguf_inspect", "tie_hip_gguf_load", "tie_hip_model_info_get", "tie_hip_model_layer",
+    "tie_hip_model_ffn_norm", "tie_hip_model_close", "tie_hip_set_silu_table",
     "tie_hip_silu_table_host", "tie_hip_layer_create", "tie_hip_layer_destroy", "tie_hip_layer_bytes",
     "tie_hip_moe_forward", "tie_hip_exact_max_tokens", "tie_hip_set_exact_max_tokens",
     "tie_hip_debug_fail_alloc", "tie_hip_host_expf", "tie_hip_profile_enable", "tie_hip_profile_read",
@@ -50,6 +51,15 @@ class LayerDesc(ctypes.Structure):
         ("literal_bf16_stride", ctypes.c_int),
         ("routing", ctypes.c_int),
         ("probs_bias", ctypes.c_void_p),
+    ]
+
+
+class ModelInfo(ctypes.Structure):
+    _fields_ = [
+        ("architecture", ctypes.c_char * 32),
+        ("d", ctypes.c_int), ("F", ctypes.c_int), ("E", ctypes.c_int), ("k", ctypes.c_int),
+        ("n_layers", ctypes.c_int), ("first_moe_layer", ctypes.c_int),
+        ("norm_eps", ctypes.c_float), ("routing", ctypes.c_int),
     ]
 
 
@@ -82,6 +92,18 @@ def lib():
         L.tie_hip_matrix_destroy.restype = None
         L.tie_hip_mat_mat.argtypes = [P, P, I, P, I, P]
         L.tie_hip_mat_mat.restype = I
+        L.tie_hip_gguf_inspect.argtypes = [ctypes.c_char_p, ctypes.POINTER(ModelInfo)]
+        L.tie_hip_gguf_inspect.restype = I
+        L.tie_hip_gguf_load.argtypes = [ctypes.c_char_p, ctypes.POINTER(ctypes.c_void_p)]
+        L.tie_hip_gguf_load.restype = I
+        L.tie_hip_model_info_get.argtypes = [P, ctypes.POINTER(ModelInfo)]
+        L.tie_hip_model_info_get.restype = None
+        L.tie_hip_model_layer.argtypes = [P, I]
+        L.tie_hip_model_layer.restype = P
+        L.tie_hip_model_ffn_norm.argtypes = [P, I]
+        L.tie_hip_model_ffn_norm.restype = P
+        L.tie_hip_model_close.argtypes = [P]
+        L.tie_hip_model_close.restype = None
         L.tie_hip_set_silu_table.argtypes = [P, I]
         L.tie_hip_set_silu_table.restype = I
         L.tie_hip_silu_table_host.argtypes = [P, I]
@@ -208,6 +230,53 @@ def qwen3_ffn(hidden, layer, k, ffn_norm, eps, with_topk=True):
                                   _p(layer.gate), layer.gate_type, _p(layer.up), layer.up_type, _p(layer.down),
                                   layer.down_type, _p(idx), _p(w)))
     return h, idx, w
+
+
+def gguf_inspect(path):
+    """tie_hip_gguf_inspect: the MoE shape of a GGUF file (no GPU needed)."""
+    info = ModelInfo()
+    check(lib().tie_hip_gguf_inspect(os.fsencode(path), ctypes.byref(info)))
+    return info
+
+
+class _LayerRef:
+    """A layer owned by a Model (forward/forward_residual of Layer, no close)."""
+
+    def __init__(self, handle):
+        self.handle = handle
+
+    forward = lambda self, *a, **kw: Layer.forward(self, *a, **kw)  # noqa: E731
+    forward_residual = lambda self, *a, **kw: Layer.forward_residual(self, *a, **kw)  # noqa: E731
+
+
+class Model:
+    """tie_hip_gguf_load: every MoE layer of a GGUF file on the device."""
+
+    def __init__(self, path):
+        h = ctypes.c_void_p()
+        check(lib().tie_hip_gguf_load(os.fsencode(path), ctypes.byref(h)))
+        self.handle = h
+        self.info = ModelInfo()
+        lib().tie_hip_model_info_get(h, ctypes.byref(self.info))
+
+    def layer(self, n):
+        h = lib().tie_hip_model_layer(self.handle, n)
+        return _LayerRef(ctypes.c_void_p(h)) if h else None
+
+    def ffn_norm(self, n):
+        """Device pointer (int) of layer n's ffn_norm, or None."""
+        return lib().tie_hip_model_ffn_norm(self.handle, n)
+
+    def close(self):
+        if self.handle:
+            lib().tie_hip_model_close(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 class Matrix:

@@ -10,6 +10,7 @@
 #include <vector>
 
 #include "common.h"
+#include "gguf.h"
 
 namespace tie {
 int set_error(int code, const char *fmt, ...);
@@ -20,6 +21,12 @@ int rsqrt_table_host(std::vector<uint32_t> &tab, int &nbits);
 
 struct tie_hip_layer {
 	tie::Layer L;
+};
+
+struct tie_hip_model {
+	tie_hip_model_info info;
+	std::vector<tie_hip_layer *> layers; // [n_layers], NULL for dense layers
+	std::vector<float *> norms;          // [n_layers] device ffn_norm
 };
 
 struct tie_hip_matrix {
@@ -656,6 +663,117 @@ static int moe_ffn_host(const float *x, int T, int d, int F, int E, int k, const
 		HIP_TRY(hipMemcpyAsync(topk_w_opt, g.w_dev, (size_t)T * k * 4, hipMemcpyDeviceToHost, g.stream));
 	HIP_TRY(hipStreamSynchronize(g.stream));
 	return TIE_HIP_OK;
+}
+
+extern "C" void tie_hip_model_close(tie_hip_model *m)
+{
+	std::lock_guard<std::recursive_mutex> lk(g.mu);
+	if (!m)
+		return;
+	if (g.device >= 0)
+		(void)hipStreamSynchronize(g.stream);
+	for (auto *l : m->layers)
+		free_layer(l);
+	for (float *p : m->norms)
+		if (p)
+			(void)hipFree(p);
+	delete m;
+}
+
+extern "C" int tie_hip_gguf_load(const char *path, tie_hip_model **out)
+{
+	std::lock_guard<std::recursive_mutex> lk(g.mu);
+	clear_error();
+	if (!path || !out)
+		return set_error(TIE_HIP_EINVAL, "null argument");
+	*out = nullptr;
+	int rc = ensure_init();
+	if (rc)
+		return rc;
+	GGUFFile f;
+	rc = f.open(path);
+	if (rc)
+		return rc;
+	tie_hip_model *m = new tie_hip_model();
+	rc = f.moe_info(m->info);
+	if (rc) {
+		delete m;
+		return rc;
+	}
+	const tie_hip_model_info &I = m->info;
+	m->layers.assign(I.n_layers, nullptr);
+	m->norms.assign(I.n_layers, nullptr);
+	auto fail = [&](int code) {
+		tie_hip_model_close(m);
+		return code;
+	};
+	auto dims = [](const GGUFTensor *t, uint64_t a, uint64_t b, uint64_t c) {
+		return t->ne[0] == a && t->ne[1] == b && t->ne[2] == c && t->ne[3] == 1;
+	};
+	for (int n = I.first_moe_layer; n < I.n_layers; n++) {
+		char name[96];
+		auto get = [&](const char *what) {
+			snprintf(name, sizeof name, "blk.%d.%s", n, what);
+			return f.tensor(name);
+		};
+		const GGUFTensor *router = get("ffn_gate_inp.weight"), *gate = get("ffn_gate_exps.weight"),
+				 *up = get("ffn_up_exps.weight"), *down = get("ffn_down_exps.weight"),
+				 *norm = get("ffn_norm.weight"), *pbias = get("exp_probs_b.bias");
+		if (!router || !gate || !up || !down)
+			return fail(set_error(TIE_HIP_EINVAL, "layer %d: missing MoE FFN tensors", n));
+		const uint64_t d = I.d, F = I.F, E = I.E;
+		if (router->type != TIE_GGML_F32 || !dims(router, d, E, 1) || !dims(gate, d, F, E) || !dims(up, d, F, E) ||
+		    !dims(down, F, d, E))
+			return fail(set_error(TIE_HIP_EINVAL, "layer %d: MoE tensor shapes do not match d=%d F=%d E=%d", n,
+					      I.d, I.F, I.E));
+		if ((norm && (norm->type != TIE_GGML_F32 || !dims(norm, d, 1, 1))) ||
+		    (pbias && (pbias->type != TIE_GGML_F32 || !dims(pbias, E, 1, 1))))
+			return fail(set_error(TIE_HIP_EINVAL, "layer %d: ffn_norm / exp_probs_b shape or type", n));
+		tie_hip_layer_desc ds;
+		memset(&ds, 0, sizeof ds);
+		ds.d = I.d;
+		ds.F = I.F;
+		ds.E = I.E;
+		ds.router_w = router->data;
+		ds.router_type = TIE_GGML_F32;
+		ds.gate_exps = gate->data;
+		ds.gate_type = gate->type;
+		ds.up_exps = up->data;
+		ds.up_type = up->type;
+		ds.down_exps = down->data;
+		ds.down_type = down->type;
+		ds.routing = I.routing;
+		ds.probs_bias = I.routing == TIE_HIP_ROUTE_SIGMOID && pbias ? (const float *)pbias->data : nullptr;
+		rc = create_layer(&ds, &m->layers[n]);
+		if (rc)
+			return fail(rc);
+		if (norm) {
+			rc = dev_malloc((void **)&m->norms[n], d * 4, "ffn_norm");
+			if (rc)
+				return fail(rc);
+			const hipError_t e = hipMemcpy(m->norms[n], norm->data, d * 4, hipMemcpyHostToDevice);
+			if (e != hipSuccess)
+				return fail(set_error(TIE_HIP_EHIP, "ffn_norm upload: %s", hipGetErrorString(e)));
+		}
+	}
+	*out = m;
+	return TIE_HIP_OK;
+}
+
+extern "C" void tie_hip_model_info_get(const tie_hip_model *m, tie_hip_model_info *info)
+{
+	if (m && info)
+		*info = m->info;
+}
+
+extern "C" tie_hip_layer *tie_hip_model_layer(tie_hip_model *m, int n)
+{
+	return m && n >= 0 && n < (int)m->layers.size() ? m->layers[n] : nullptr;
+}
+
+extern "C" const float *tie_hip_model_ffn_norm(const tie_hip_model *m, int n)
+{
+	return m && n >= 0 && n < (int)m->norms.size() ? m->norms[n] : nullptr;
 }
 
 extern "C" int tie_hip_matrix_create(const void *w, int type, int rows, int in_dim, int src_on_device,
