@@ -112,20 +112,29 @@ __global__ __launch_bounds__(RM_THREADS) void router_mid_kernel(const float *__r
 }
 
 // ------------------------------------------------------------ router_logits
-// One workgroup (8 waves, two per SIMD) per 32 tokens x 32 experts.  Thread
-// (l, eg, tg) runs the 16 lane-l chains of experts 4eg..4eg+3 x tokens
-// 4tg..4tg+3, each in TIE's order (i ascending): per step one 16-byte LDS
-// read of the 4 weights and 4 reads of x feed 16 FMAs.  K advances 256 at
-// a time through a double-buffered LDS pipeline filled by direct
-// global->LDS loads (global_load_lds_dwordx4): the x rows as they are
-// (token-major) and the matching 256 rows x 32 experts of the transposed
-// router matrix, whose 16-byte column groups are XOR-swizzled by row
-// (conflict-free reads).
-constexpr int RT_TOK = 32, RT_EXP = 32, RT_KC = 256, RT_THREADS = 512, RT_NW = RT_THREADS / 64;
-constexpr int RT_WBYTES = RT_KC * RT_EXP * 4;   // W^T chunk (32 KiB)
-constexpr int RT_XBYTES = RT_TOK * RT_KC * 4;   // x chunk (32 KiB)
+// One workgroup (8 waves) per RT_TOK tokens x 32 experts.  Thread (l, eg,
+// tg) runs the lane-l chains of experts 4eg..4eg+3 x tokens RT_TPT*tg..,
+// each in TIE's order (i ascending): per step one 16-byte LDS read of the 4
+// weights and RT_TPT reads of x feed 4*RT_TPT FMAs.  K advances RT_KC at a
+// time through a double-buffered LDS pipeline filled by direct global->LDS
+// loads (global_load_lds_dwordx4): the x rows as they are (token-major) and
+// the matching RT_KC rows x 32 experts of the transposed router matrix,
+// whose 16-byte column groups are XOR-swizzled by row (conflict-free
+// reads).  16 tokens and 128-wide K chunks keep the LDS at 48 KiB (three
+// workgroups per CU); 32 x 256 (128 KiB, one per CU) took 33 us at T = 512
+// against 26 us.
+#ifndef TIE_RT_TOK
+#define TIE_RT_TOK 16
+#endif
+#ifndef TIE_RT_KC
+#define TIE_RT_KC 128
+#endif
+constexpr int RT_TOK = TIE_RT_TOK, RT_EXP = 32, RT_KC = TIE_RT_KC, RT_THREADS = 512, RT_NW = RT_THREADS / 64;
+constexpr int RT_TPT = RT_TOK / 8;              // tokens per thread
+constexpr int RT_WBYTES = RT_KC * RT_EXP * 4;   // W^T chunk (16 KiB)
+constexpr int RT_XBYTES = RT_TOK * RT_KC * 4;   // x chunk (8 KiB)
 constexpr int RT_BUF = RT_WBYTES + RT_XBYTES;
-constexpr int RT_LDS = 2 * RT_BUF;              // double-buffered (128 KiB)
+constexpr int RT_LDS = 2 * RT_BUF;              // double-buffered (48 KiB: three workgroups per CU)
 
 __device__ __forceinline__ uint32_t rt_lds_addr(const void *p)
 {
@@ -155,7 +164,7 @@ __device__ __forceinline__ void rt_dma_chunk(const float *__restrict__ x, const 
 #pragma unroll
 	for (int c = 0; c < RT_TOK / RT_NW; c++) {
 		const int t = RT_NW * c + w;
-		if (t < nt)
+		if (t < nt && lane < RT_KC / 4)
 			rt_dma16(x + (size_t)(t0 + t) * d + kc + 4 * lane,
 				 __builtin_amdgcn_readfirstlane(rt_lds_addr(buf + RT_WBYTES + t * RT_KC * 4)));
 	}
@@ -180,11 +189,11 @@ __global__ __launch_bounds__(RT_THREADS) void router_logits_kernel(const float *
 	const int nkc = d / RT_KC;
 	// float index of experts 4eg.. in W^T row r: slot eg ^ (r%8), r % 8 == l
 	const int wcol = 4 * (eg ^ l);
-	const int xo = (4 * tg) * RT_KC + l;
+	const int xo = (RT_TPT * tg) * RT_KC + l;
 
-	float acc[4][4];
+	float acc[RT_TPT][4];
 #pragma unroll
-	for (int a = 0; a < 4; a++)
+	for (int a = 0; a < RT_TPT; a++)
 #pragma unroll
 		for (int b = 0; b < 4; b++)
 			acc[a][b] = 0.0f;
@@ -200,7 +209,7 @@ __global__ __launch_bounds__(RT_THREADS) void router_logits_kernel(const float *
 		for (int i = 0; i < RT_KC / 8; i++) {
 			const float4 w4 = *reinterpret_cast<const float4 *>(ws + (8 * i + l) * RT_EXP + wcol);
 #pragma unroll
-			for (int a = 0; a < 4; a++) {
+			for (int a = 0; a < RT_TPT; a++) {
 				const float xv = xs[xo + a * RT_KC + 8 * i];
 				acc[a][0] = __builtin_fmaf(xv, w4.x, acc[a][0]);
 				acc[a][1] = __builtin_fmaf(xv, w4.y, acc[a][1]);
@@ -213,11 +222,11 @@ __global__ __launch_bounds__(RT_THREADS) void router_logits_kernel(const float *
 
 	// hsum8 over the 8 lanes l of each chain group (math_avx2.c:14-21 order)
 #pragma unroll
-	for (int a = 0; a < 4; a++) {
+	for (int a = 0; a < RT_TPT; a++) {
 #pragma unroll
 		for (int b = 0; b < 4; b++) {
 			float r = hsum8_lanes(acc[a][b]);
-			const int t = 4 * tg + a, e = e0 + 4 * eg + b;
+			const int t = RT_TPT * tg + a, e = e0 + 4 * eg + b;
 			if (l == 0 && t < nt) {
 				if (bias)
 					r = r + bias[e];
@@ -280,7 +289,9 @@ hipError_t launch_router_logits(const Layer &L, const float *x, int T, float *lo
 				   logits);
 		return hipGetLastError();
 	}
-	if (T > 2 * RT_TOK && E % RT_EXP == 0 && d % RT_KC == 0 && L.routerT) {
+	// the tiled kernel above 256 tokens: below that its one chunk in flight
+	// per K step leaves it waiting on memory, and router_mid is faster
+	if (T > 256 && E % RT_EXP == 0 && d % RT_KC == 0 && L.routerT) {
 		static bool attr = false;
 		if (!attr) {
 			const hipError_t err = hipFuncSetAttribute((const void *)router_logits_kernel,

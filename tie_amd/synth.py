@@ -147,6 +147,10 @@ CONFIGS = {
     "30b_t4": dict(d=2048, F=768, E=128, k=8, T=4, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1244),
     "30b_t8": dict(d=2048, F=768, E=128, k=8, T=8, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1240),
     "30b_t32": dict(d=2048, F=768, E=128, k=8, T=32, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1235),
+    "30b_t64": dict(d=2048, F=768, E=128, k=8, T=64, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1243),
+    "30b_t128": dict(d=2048, F=768, E=128, k=8, T=128, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1245),
+    "30b_t256": dict(d=2048, F=768, E=128, k=8, T=256, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1246),
+    "30b_t512": dict(d=2048, F=768, E=128, k=8, T=512, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1247),
     "30b_t32_ffn": dict(d=2048, F=768, E=128, k=8, T=32, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1235,
                         residual=True),
     "30b_t2048": dict(d=2048, F=768, E=128, k=8, T=2048, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1236),
