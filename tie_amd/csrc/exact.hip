@@ -101,9 +101,6 @@ template <int PC> __device__ __forceinline__ void step_fence(float (&a0)[PC][8],
 #define TIE_GU_PG 8
 #endif
 
-#ifndef TIE_GU_PREFETCH
-#define TIE_GU_PREFETCH 0
-#endif
 constexpr int GU_WAVES = TIE_GU_WAVES;
 constexpr int GU_THREADS = 64 * GU_WAVES;
 constexpr int PG_MAX = 16;        // pairs per LDS group
@@ -116,31 +113,6 @@ constexpr int INLINE_T = 1;
 constexpr int INLINE_E = 128;
 
 // ------------------------------------------------------------------ blocks
-struct Q4KBlock {
-	uint4 c[Q4K_CHUNKS];
-};
-struct Q6KBlock {
-	uint4 c[Q6K_CHUNKS];
-	uint32_t d;
-};
-
-__device__ __forceinline__ void load_block(const uint8_t *__restrict__ panel, int lane, Q4KBlock &B)
-{
-	const uint4 *p = reinterpret_cast<const uint4 *>(panel) + lane;
-#pragma unroll
-	for (int c = 0; c < Q4K_CHUNKS; c++)
-		B.c[c] = p[c * 64];
-}
-
-__device__ __forceinline__ void load_block(const uint8_t *__restrict__ panel, int lane, Q6KBlock &B)
-{
-	const uint4 *p = reinterpret_cast<const uint4 *>(panel) + lane;
-#pragma unroll
-	for (int c = 0; c < Q6K_CHUNKS; c++)
-		B.c[c] = p[c * 64];
-	B.d = reinterpret_cast<const uint16_t *>(panel + Q6K_CHUNKS * 1024)[lane];
-}
-
 __device__ __forceinline__ uint32_t word(const uint4 &v, int i)
 {
 	return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
@@ -154,88 +126,12 @@ __device__ __forceinline__ float ubyte(uint32_t w, int i)
 // dot_product_f32_q4k_avx2 (math_avx2.c:535-604) of the lane's block with
 // PC input rows at once.  Each weight w = fma(q, d*sc, -(dmin*m)) is formed
 // once and used by the PC pairs; every pair keeps its own 16 accumulators
-// and sees exactly TIE's sequence of FMAs.
-template <int PC, typename XP>
-__device__ __forceinline__ void block_dots(const Q4KBlock &B, XP *const xs[PC], float out[PC])
-{
-	const uint32_t w0 = B.c[0].x;
-	const float d = half_bits_to_float(w0 & 0xffffu);
-	const float dmin = half_bits_to_float(w0 >> 16);
-	const uint32_t s[3] = {B.c[0].y, B.c[0].z, B.c[0].w}; // 12 packed scale/min bytes
-	float D[8], nM[8];
-#pragma unroll
-	for (int j = 0; j < 8; j++) {
-		auto sb = [&](int i) { return (s[i >> 2] >> (8 * (i & 3))) & 0xffu; };
-		uint32_t sc, m;
-		if (j < 4) {
-			sc = sb(j) & 63u;
-			m = sb(j + 4) & 63u;
-		} else {
-			sc = (sb(j + 4) & 15u) | ((sb(j - 4) >> 6) << 4);
-			m = (sb(j + 4) >> 4) | ((sb(j) >> 6) << 4);
-		}
-		D[j] = d * (float)sc;
-		nM[j] = -(dmin * (float)m);
-	}
-	float a0[PC][8], a1[PC][8];
-#pragma unroll
-	for (int p = 0; p < PC; p++)
-#pragma unroll
-		for (int l = 0; l < 8; l++)
-			a0[p][l] = a1[p][l] = 0.0f;
-	// 32 steps s = (g, o, h) of 8 weights each; step s reads x[64g + 16o +
-	// 4h + i] and x[.. + 32].  The inputs are loaded for a super-step of XS
-	// steps at once (two runs of 4*XS floats per pair, in SGPRs), so one
-	// wait for scalar loads covers XS steps of FMAs.
-	constexpr int XS = PC == 1 ? 4 : PC == 2 ? 2 : 1;
-	XP *xb[PC];
-#pragma unroll
-	for (int st = 0; st < 32; st++) {
-		const int g = st >> 3, o = (st >> 2) & 1, h = st & 3;
-		step_fence<PC>(a0, a1);
-		if (st % XS == 0) {
-#pragma unroll
-			for (int p = 0; p < PC; p++) {
-				xb[p] = xs[p] + 64 * g + 16 * o + 4 * h;
-				launder(xb[p]);
-			}
-		}
-		const float D1 = D[2 * g], M1 = nM[2 * g], D2 = D[2 * g + 1], M2 = nM[2 * g + 1];
-		uint32_t w = word(B.c[1 + 2 * g + o], h);
-		asm volatile("" : "+v"(w)); // the word is unpacked here, not hoisted
-		uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
-		// opaque: the nibbles are then converted by v_cvt_f32_ubyte0..3 on
-		// the masked words, one instruction per weight
-		asm volatile("" : "+v"(lo), "+v"(hi));
-		float wl[4], wh[4];
-#pragma unroll
-		for (int i = 0; i < 4; i++) {
-			wl[i] = __builtin_fmaf(ubyte(lo, i), D1, M1);
-			wh[i] = __builtin_fmaf(ubyte(hi, i), D2, M2);
-		}
-		const int xo = 4 * (st % XS);
-#pragma unroll
-		for (int p = 0; p < PC; p++) {
-#pragma unroll
-			for (int i = 0; i < 4; i++) {
-				const int m = 4 * h + i;
-				float &A = (m < 8) ? a0[p][m & 7] : a1[p][m & 7];
-				A = __builtin_fmaf(xb[p][xo + i], wl[i], A);
-				A = __builtin_fmaf(xb[p][xo + 32 + i], wh[i], A);
-			}
-		}
-	}
-#pragma unroll
-	for (int p = 0; p < PC; p++) {
-		float v[8];
-#pragma unroll
-		for (int l = 0; l < 8; l++)
-			v[l] = a0[p][l] + a1[p][l];
-		out[p] = hsum8(v);
-	}
-}
-
-// The Q4_K block read in stages instead of at once: the scale chunk and
+// and sees exactly TIE's sequence of FMAs.  32 steps s = (g, o, h) of 8
+// weights each; step s reads x[64g + 16o + 4h + i] and x[.. + 32], loaded
+// for a super-step of XS steps at once (two runs of 4*XS floats per pair, in
+// SGPRs), so one wait for scalar loads covers XS steps of FMAs.
+//
+// The block is read in stages instead of at once: the scale chunk and
 // the two quant chunks of 64-weight group 0 first, then the chunks of group
 // g + 1 while group g computes.  That keeps 12 of the block's 36 dwords in
 // registers at a time (vector loads return in order, so the wait for group
@@ -364,81 +260,10 @@ __device__ __forceinline__ void block_dots(const Q4KStream &S, XP *const xs[PC],
 // PC input rows.  Panel chunks: 0-7 ql[0..127], 8-11 qh[0..63], 12 the
 // int8 scales.  q - 32 is formed once per weight; per pair TIE's
 // fma(d*sc, (q - 32) * x, acc) follows, the product rounded on its own.
-template <int PC, typename XP>
-__device__ __forceinline__ void block_dots(const Q6KBlock &B, XP *const xs[PC], float out[PC])
-{
-	const float d = half_bits_to_float(B.d);
-	float a0[PC][8], a1[PC][8];
-#pragma unroll
-	for (int p = 0; p < PC; p++)
-#pragma unroll
-		for (int l = 0; l < 8; l++)
-			a0[p][l] = a1[p][l] = 0.0f;
-	// 16 steps s = (n, l, hw) of 16 weights each; step s reads x[128n + l +
-	// 4hw + i + {0, 32, 64, 96}].  For PC <= 2 the inputs of both hw steps of
-	// an (n, l) are loaded at once (four runs of 8 floats per pair, in SGPRs),
-	// so one wait for scalar loads covers two steps.
-	constexpr int XS = PC == 1 ? 2 : 1;
-	auto sc = [&](int j) { return (float)(int8_t)((word(B.c[12], j >> 2) >> (8 * (j & 3))) & 0xffu); };
-	XP *xb[PC];
-#pragma unroll
-	for (int st = 0; st < 16; st++) {
-		const int n = st >> 3, l = 8 * ((st >> 1) & 3), hw = st & 1;
-		const int is = (l >= 16) ? 1 : 0;
-		step_fence<PC>(a0, a1);
-		if (st % XS == 0) {
-#pragma unroll
-			for (int p = 0; p < PC; p++) {
-				xb[p] = xs[p] + 128 * n + l + 4 * hw;
-				launder(xb[p]);
-			}
-		}
-		const float W0 = d * sc(8 * n + is + 0);
-		const float W1 = d * sc(8 * n + is + 2);
-		const float W2 = d * sc(8 * n + is + 4);
-		const float W3 = d * sc(8 * n + is + 6);
-		const int dw = ((l & 8) >> 2) + hw;
-		uint32_t L = word(B.c[4 * n + (l >> 4)], dw), L2 = word(B.c[4 * n + 2 + (l >> 4)], dw),
-			 H = word(B.c[8 + 2 * n + (l >> 4)], dw);
-		asm volatile("" : "+v"(L), "+v"(L2), "+v"(H));
-		uint32_t q1 = (L & 0x0f0f0f0fu) | ((H & 0x03030303u) << 4);
-		uint32_t q2 = (L2 & 0x0f0f0f0fu) | (((H >> 2) & 0x03030303u) << 4);
-		uint32_t q3 = ((L >> 4) & 0x0f0f0f0fu) | (((H >> 4) & 0x03030303u) << 4);
-		uint32_t q4 = ((L2 >> 4) & 0x0f0f0f0fu) | (((H >> 6) & 0x03030303u) << 4);
-		asm volatile("" : "+v"(q1), "+v"(q2), "+v"(q3), "+v"(q4));
-		float f1[4], f2[4], f3[4], f4[4];
-#pragma unroll
-		for (int i = 0; i < 4; i++) {
-			f1[i] = ubyte(q1, i) - 32.0f;
-			f2[i] = ubyte(q2, i) - 32.0f;
-			f3[i] = ubyte(q3, i) - 32.0f;
-			f4[i] = ubyte(q4, i) - 32.0f;
-		}
-		const int xo = 4 * (st % XS);
-#pragma unroll
-		for (int p = 0; p < PC; p++) {
-#pragma unroll
-			for (int i = 0; i < 4; i++) {
-				const int m = 4 * hw + i;
-				XP *xq = xb[p] + xo + i;
-				a0[p][m] = __builtin_fmaf(W0, f1[i] * xq[0], a0[p][m]);
-				a1[p][m] = __builtin_fmaf(W1, f2[i] * xq[32], a1[p][m]);
-				a0[p][m] = __builtin_fmaf(W2, f3[i] * xq[64], a0[p][m]);
-				a1[p][m] = __builtin_fmaf(W3, f4[i] * xq[96], a1[p][m]);
-			}
-		}
-	}
-#pragma unroll
-	for (int p = 0; p < PC; p++) {
-		float v[8];
-#pragma unroll
-		for (int l = 0; l < 8; l++)
-			v[l] = a0[p][l] + a1[p][l];
-		out[p] = hsum8(v);
-	}
-}
-
-// The Q6_K block read in stages: the scale chunk, d and the three quant
+// 16 steps s = (n, l, hw) of 16 weights each; step s reads x[128n + l +
+// 4hw + i + {0, 32, 64, 96}].
+//
+// The block is read in stages: the scale chunk, d and the three quant
 // chunks (ql low/high nibble sources and qh) of quarter (n, l >> 4) first,
 // then those of the next quarter while one quarter computes.
 struct Q6KStream {
@@ -556,15 +381,11 @@ __device__ __forceinline__ void block_dots(const Q6KStream &S, XP *const xs[PC],
 }
 
 template <int TYPE> struct BlockOf;
-// quantised blocks read in stages (Q4KStream, Q6KStream) or at once
-#ifndef TIE_Q4K_STREAM
-#define TIE_Q4K_STREAM 1
-#endif
 template <> struct BlockOf<TIE_GGML_Q4_K> {
-	using type = std::conditional<TIE_Q4K_STREAM, Q4KStream, Q4KBlock>::type;
+	using type = Q4KStream;
 };
 template <> struct BlockOf<TIE_GGML_Q6_K> {
-	using type = std::conditional<TIE_Q4K_STREAM, Q6KStream, Q6KBlock>::type;
+	using type = Q6KStream;
 };
 
 // PC pairs of the group against the lane's block; part[(b*pg_cap + q) * 64 + lane]
@@ -749,26 +570,15 @@ __global__ __launch_bounds__(GU_THREADS) GU_OCC void exact_gu_kernel(ExactArgs a
 			const int mi = t / nb, b = t - mi * nb;
 			return a.w[m0 + mi] + (size_t)e * a.expert_bytes[m0 + mi] + ((size_t)rt * nb + b) * pb;
 		};
-		Block blk;
-		if (TIE_GU_PREFETCH && w < ntask)
-			load_block(panel_of(w), lane, blk);
 		for (int t = w; t < ntask; t += NW) {
 			const int b = t % nb;
-			Block nxt;
-			if (TIE_GU_PREFETCH) {
-				// the next task's block is in flight while this one computes
-				if (t + NW < ntask)
-					load_block(panel_of(t + NW), lane, nxt);
-			} else {
-				load_block(panel_of(t), lane, blk);
-			}
+			Block blk;
+			load_block(panel_of(t), lane, blk);
 			auto xrow_b = [&](int q) {
 				const int pair = __builtin_amdgcn_readfirstlane(gp[q]);
 				return (cfloat *)(x + (size_t)(pair / k) * in + QK * b);
 			};
 			block_all_pairs<PM, Block, cfloat>(blk, np, xrow_b, part + (size_t)t * pg_cap * 64, lane);
-			if (TIE_GU_PREFETCH)
-				blk = nxt;
 		}
 		__syncthreads();
 		// serial sums over super-blocks (math_avx2.c:762-766)
