@@ -42,10 +42,11 @@ def _half_abs_normal(rng, n, scale):
 
 
 def f32_to_bf16_bits(a):
+    """Round-to-nearest-even bf16 bits of finite float32 values."""
     a = np.ascontiguousarray(a, dtype=np.float32)
-    u = a.view(np.uint32).astype(np.uint64)
-    r = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
-    return r.astype(np.uint16)
+    u = a.view(np.uint32)
+    r = u + np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1))  # no wrap for finite values
+    return (r >> np.uint32(16)).astype(np.uint16)
 
 
 def bf16_bits_to_f32(b):
@@ -77,8 +78,14 @@ def expert_tensor(rng, wtype, n_exp, rows, in_dim):
     if wtype == Q6_K:
         return q6k_blocks(rng, n_exp * rows * (in_dim // QK_K)).reshape(-1)
     if wtype == BF16:
-        w = rng.normal(0.0, 0.02, size=n_exp * rows * in_dim).astype(np.float32)
-        return f32_to_bf16_bits(w).view(np.uint8)
+        # drawn in chunks: the same stream of normals as one draw, in less memory
+        n = n_exp * rows * in_dim
+        out = np.empty(n, np.uint16)
+        step = 1 << 24
+        for i in range(0, n, step):
+            m = min(step, n - i)
+            out[i:i + m] = f32_to_bf16_bits(rng.normal(0.0, 0.02, size=m).astype(np.float32))
+        return out.view(np.uint8)
     raise ValueError("unsupported expert type %r" % (wtype,))
 
 
