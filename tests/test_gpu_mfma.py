@@ -66,6 +66,8 @@ def model(layer, x, k, idx, w, tab, split):
             bind.oracle().orc_swiglu(g.ctypes.data, u.ctypes.data, F, tab.ctypes.data)
             h = g if split else bf16(g)
             y = Wd[e].astype(np.float64) @ h.astype(np.float64)
+            if not split:
+                y = bf16(y.astype(np.float32)).astype(np.float64)  # stored as bf16 for the combine
             out[t] += float(w[t, j]) * y
     return out
 

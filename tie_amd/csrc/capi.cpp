@@ -398,7 +398,8 @@ static int forward(tie_hip_layer *layer, const float *x, int T, int k, float *ou
 		prof_end(s);
 		HIP_TRY(launch_mfma_experts(L, x, T, k, g.silu, ws, s));
 		prof_begin("combine", s);
-		HIP_TRY(launch_combine(T, L.d, k, ws.topk_w, ws.topk_idx, ws.y, out, s, res));
+		HIP_TRY(launch_combine(T, L.d, k, ws.topk_w, ws.topk_idx, ws.y, out, s, res,
+				       L.down.type != TIE_GGML_BF16));
 		prof_end(s);
 	} else {
 		// routing, experts and the combine

@@ -156,10 +156,12 @@ hipError_t launch_route_group(const Layer &L, int T, int k, const float *logits,
 	return hipGetLastError();
 }
 
-// out[t][c] = fma(g_j, y[t*k+j][c], acc) for j = 0..k-1 (model_qwen3.c:459-467);
+// out[t][c] = fma(g_j, y[t*k+j][c], acc) for j = 0..k-1 (model_qwen3.c:459-467),
+// y fp32 or (Y16, the MFMA path with quantised weights) bf16;
 // with res: out[t][c] = res[t][c] + acc, the residual add that follows the
 // block (dispatch_apply_residual, model_qwen3.c:491, apply_residual_f32_f32_avx2
 // math_avx2.c:731-751).  res may be out (the hidden state updated in place).
+template <bool Y16>
 __global__ __launch_bounds__(256) void combine_kernel(int T, int d, int k, const float *__restrict__ topk_w,
 						      const int32_t *__restrict__ topk_idx,
 						      const float *__restrict__ y, const float *res, float *out)
@@ -173,7 +175,15 @@ __global__ __launch_bounds__(256) void combine_kernel(int T, int d, int k, const
 		if (topk_idx[t * k + j] < 0)
 			continue;
 		const float g = topk_w[t * k + j];
-		const float4 v = reinterpret_cast<const float4 *>(y + ((size_t)t * k + j) * d)[c4];
+		float4 v;
+		if (Y16) {
+			const uint2 b = reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(y) +
+									((size_t)t * k + j) * d)[c4];
+			v = make_float4(__builtin_bit_cast(float, b.x << 16), __builtin_bit_cast(float, b.x & 0xffff0000u),
+					__builtin_bit_cast(float, b.y << 16), __builtin_bit_cast(float, b.y & 0xffff0000u));
+		} else {
+			v = reinterpret_cast<const float4 *>(y + ((size_t)t * k + j) * d)[c4];
+		}
 		acc.x = __builtin_fmaf(g, v.x, acc.x);
 		acc.y = __builtin_fmaf(g, v.y, acc.y);
 		acc.z = __builtin_fmaf(g, v.z, acc.z);
@@ -190,13 +200,13 @@ __global__ __launch_bounds__(256) void combine_kernel(int T, int d, int k, const
 }
 
 hipError_t launch_combine(int T, int d, int k, const float *topk_w, const int32_t *topk_idx, const float *y,
-			  float *out, hipStream_t s, const float *res)
+			  float *out, hipStream_t s, const float *res, bool y16)
 {
 	if (T == 0)
 		return hipSuccess;
 	const int n4 = d / 4;
-	hipLaunchKernelGGL(combine_kernel, dim3((n4 + 255) / 256, T), dim3(256), 0, s, T, d, k, topk_w, topk_idx, y,
-			   res, out);
+	hipLaunchKernelGGL(y16 ? combine_kernel<true> : combine_kernel<false>, dim3((n4 + 255) / 256, T), dim3(256), 0, s,
+			   T, d, k, topk_w, topk_idx, y, res, out);
 	return hipGetLastError();
 }
 

@@ -112,7 +112,8 @@ struct MfmaArgs {
 	const float *silu;
 	uint16_t *h16;           // gate/up out (bf16, by position)
 	uint16_t *h16lo;         // gate/up out, split mode: bf16 remainder plane
-	float *y;                // down out [pair][d]
+	float *y;                // down out [pair][d] (BF16 weights: fp32)
+	uint16_t *y16;           // down out [pair][d] (quantised weights: bf16)
 };
 
 template <int TYPE, bool DOWN = false> struct Cfg {
@@ -612,10 +613,16 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 				a.h16[(size_t)p * a.rows + col] = hi;
 				if (C::SPLIT)
 					a.h16lo[(size_t)p * a.rows + col] = bf16_bits(hv - bf16_bits_to_float(hi));
-			} else {
+			} else if (C::SPLIT) {
 				float *yr = a.y + (size_t)a.pairs[p] * a.rows + slab * DN_COLS + 64 * w + (lane & 31);
 				yr[0] = acc[mt][0][i];
 				yr[32] = acc[mt][1][i];
+			} else {
+				// quantised weights: y as bf16 (the path's products already
+				// take bf16 operands; half the bytes to the combine)
+				uint16_t *yr = a.y16 + (size_t)a.pairs[p] * a.rows + slab * DN_COLS + 64 * w + (lane & 31);
+				yr[0] = bf16_bits(acc[mt][0][i]);
+				yr[32] = bf16_bits(acc[mt][1][i]);
 			}
 		}
 		// one M tile at a time: only its accumulators move to VGPRs
@@ -765,6 +772,7 @@ hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, con
 	a.ntiles = ws.ntiles;
 	a.silu = silu;
 	a.y = ws.y;
+	a.y16 = reinterpret_cast<uint16_t *>(ws.y);
 	const int max_tiles = mfma_max_tiles(npairs, L.E);
 
 	prof_begin("mfma_gate_up", s);
