@@ -153,6 +153,7 @@ template <int TYPE, bool DOWN = false> struct Cfg {
 template <int TYPE> struct BRegs;
 __device__ __forceinline__ uint32_t lds_addr(const void *p);
 __device__ __forceinline__ void dma16(const void *g, uint32_t lds);
+__device__ __forceinline__ void dma16s(const void *base, uint32_t voff, uint32_t lds);
 template <> struct BRegs<TIE_GGML_Q4_K> {
 	u32x2 q[2][4];  // quant bytes 8h..8h+7 of the stage's 4 quant chunks
 	u32x4 sc[2];    // chunk 0: d, dmin, 12 scale bytes
@@ -218,21 +219,55 @@ __device__ __forceinline__ void load_b(const BSrc &s, int st, int h, BRegs<TYPE>
 // Q4_K slots: 0 scales, 1..4 the stage's quant chunks 1+4h..4+4h.  Q6_K
 // slots: 0..3 ql chunks 4h..4h+3, 4, 5 qh chunks 8+2h, 9+2h, 6 the scales;
 // then the 4 panels' d planes (128 B each).  h = st % 2 (the block half).
+// Wave w moves items 4c + w (panel (4c + w) / NCH, slot (4c + w) % NCH);
+// their bases and panel offsets are set once per tile (BDma).
+template <int TYPE> struct BDma {
+	static constexpr int NCH = Cfg<TYPE>::NCH;
+	const uint8_t *base[NCH]; // expert base of the item's matrix (wave-uniform)
+	uint32_t pofs[NCH];       // the item's panel row offset in the expert (wave-uniform)
+	int slot[NCH];            // the item's LDS slot
+	uint32_t lofs[NCH];       // the item's LDS offset in a B buffer
+	uint32_t lane16;          // 16 * lane
+	const uint8_t *dbase;     // Q6_K: expert base of panel w's matrix
+	uint32_t dpofs;           // Q6_K: offset of panel w's d plane in its first block column
+};
+
 template <int TYPE, bool DOWN>
-__device__ __forceinline__ void dma_b(const MfmaArgs &a, int e, int slab, int st, int w, uint8_t *B)
+__device__ __forceinline__ void bdma_init(const MfmaArgs &a, int e, int slab, int w, BDma<TYPE> &d)
 {
 	using C = Cfg<TYPE>;
-	const int lane = threadIdx.x & 63, half = st & 1, part = st % C::SPB;
-	const size_t pbytes = panel_bytes(TYPE);
-	auto panel = [&](int p) {
-		const int mat = DOWN ? 0 : p >> 1;
-		const int rt = DOWN ? 4 * slab + p : 2 * slab + (p & 1);
-		return a.w[mat] + (size_t)e * a.expert_bytes[mat] + ((size_t)rt * (a.in / QK) + st / C::SPB) * pbytes;
-	};
+	const uint32_t pbytes = (uint32_t)panel_bytes(TYPE);
+	const uint32_t nkb = (uint32_t)(a.in / QK);
 #pragma unroll
 	for (int c = 0; c < C::NCH; c++) {
-		const int it = NWAVES * c + w; // item: panel it / NCH, slot it % NCH; NWAVES == 4 panels
+		const int it = NWAVES * c + w; // NWAVES == 4 panels
 		const int p = it / C::NCH, s = it % C::NCH;
+		const int mat = DOWN ? 0 : p >> 1;
+		const int rt = DOWN ? 4 * slab + p : 2 * slab + (p & 1);
+		d.base[c] = a.w[mat] + (size_t)e * a.expert_bytes[mat];
+		d.pofs[c] = (uint32_t)rt * nkb * pbytes;
+		d.slot[c] = s;
+		d.lofs[c] = (uint32_t)(p * C::PB + s * 1024);
+	}
+	d.lane16 = 16u * (threadIdx.x & 63);
+	{
+		const int mat = DOWN ? 0 : w >> 1;
+		const int rt = DOWN ? 4 * slab + w : 2 * slab + (w & 1);
+		d.dbase = a.w[mat] + (size_t)e * a.expert_bytes[mat];
+		d.dpofs = (uint32_t)rt * nkb * pbytes + Q6K_CHUNKS * 1024;
+	}
+}
+
+template <int TYPE, bool DOWN>
+__device__ __forceinline__ void dma_b(const BDma<TYPE> &d, int slab, int st, int w, uint8_t *B)
+{
+	using C = Cfg<TYPE>;
+	const int half = st & 1, part = st % C::SPB;
+	const uint32_t kofs = (uint32_t)(st / C::SPB) * (uint32_t)panel_bytes(TYPE);
+	const uint32_t lb = lds_addr(B);
+#pragma unroll
+	for (int c = 0; c < C::NCH; c++) {
+		const int s = d.slot[c];
 		int chunk;
 		if constexpr (TYPE == TIE_GGML_Q4_K)
 			chunk = s == 0 ? 0 : (C::NCH - 1) * part + s;
@@ -242,12 +277,13 @@ __device__ __forceinline__ void dma_b(const MfmaArgs &a, int e, int slab, int st
 			chunk = s < 2 ? 4 * n + 2 * q + s : (s < 4 ? 8 + 2 * n + (s - 2) : 12);
 		} else
 			chunk = s < 4 ? 4 * half + s : (s < 6 ? 8 + 2 * half + (s - 4) : 12);
-		dma16(panel(p) + chunk * 1024 + 16 * lane, __builtin_amdgcn_readfirstlane(lds_addr(B + p * C::PB + s * 1024)));
+		dma16s(d.base[c], d.lane16 + (d.pofs[c] + kofs + (uint32_t)chunk * 1024),
+		       __builtin_amdgcn_readfirstlane(lb + d.lofs[c]));
 	}
 	if constexpr (TYPE == TIE_GGML_Q6_K) {
-		if (lane < 8)
-			dma16(panel(w) + Q6K_CHUNKS * 1024 + 16 * lane,
-			      __builtin_amdgcn_readfirstlane(lds_addr(B + 4 * C::PB + w * 128)));
+		// the d plane of panel w (128 B)
+		if ((threadIdx.x & 63) < 8)
+			dma16s(d.dbase, d.lane16 + (d.dpofs + kofs), __builtin_amdgcn_readfirstlane(lb + 4 * C::PB + w * 128));
 	}
 }
 
@@ -387,7 +423,8 @@ __device__ __forceinline__ void deq_step(const BRegs<TYPE> &b, const Fac &f, int
 // output rows the epilogue drops).
 constexpr int ROFF_STRIDE = 16; // offsets per lane slot (>= NDMA, multiple of 4)
 struct ASrc {
-	const char *base[2];   // planes + this lane's chunk offset
+	const char *base[2];   // planes (wave-uniform)
+	uint32_t cofs;         // this lane's chunk offset in a row
 	const uint32_t *roff;  // LDS: this lane's ROFF_STRIDE row byte offsets
 };
 
@@ -404,26 +441,34 @@ __device__ __forceinline__ void dma16(const void *g, uint32_t lds)
 	asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
 }
 
+// The same from a wave-uniform base (SGPR pair) plus a 32-bit per-lane byte
+// offset: no 64-bit address arithmetic per load.
+__device__ __forceinline__ void dma16s(const void *base, uint32_t voff, uint32_t lds)
+{
+	asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds)
+		     : "memory", "m0");
+}
+
 template <int TYPE, bool DOWN>
 __device__ __forceinline__ void dma_a(const ASrc &s, int st, int w, const uint8_t *buf)
 {
 	using C = Cfg<TYPE, DOWN>;
 	// byte offset of the stage in an A row (APERM: block, half, quarter p;
-	// the lane's chunk offset in base covers the quarter p + 2 part)
-	const size_t ko = C::APERM ? (size_t)512 * (st >> 2) + 256 * ((st >> 1) & 1) + 64 * (st & 1)
-				   : (size_t)st * C::RB;
+	// the lane's chunk offset covers the quarter p + 2 part)
+	const uint32_t ko = C::APERM ? 512u * (st >> 2) + 256u * ((st >> 1) & 1) + 64u * (st & 1) : (uint32_t)st * C::RB;
 	uint32_t off[(C::NDMA + 3) / 4 * 4]; // whole 16-byte reads (the lane slot holds ROFF_STRIDE entries)
 	static_assert(C::NDMA <= ROFF_STRIDE, "row offset slot too small");
 #pragma unroll
 	for (int c = 0; c < C::NDMA; c += 4)
 		*reinterpret_cast<u32x4 *>(off + c) = *reinterpret_cast<const u32x4 *>(s.roff + c);
+	const uint32_t lk = s.cofs + ko;
 #pragma unroll
 	for (int pl = 0; pl < C::NPL; pl++)
 #pragma unroll
 		for (int c = 0; c < C::NDMA; c++) {
 			const int r0 = C::RPI * (NWAVES * c + w);
 			const uint32_t dst = lds_addr(buf + pl * C::A_TILE + r0 * C::RB);
-			dma16(s.base[pl] + off[c] + ko, __builtin_amdgcn_readfirstlane(dst));
+			dma16s(s.base[pl], off[c] + lk, __builtin_amdgcn_readfirstlane(dst));
 		}
 }
 
@@ -502,8 +547,9 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 		const int chunk = slot ^ C::swz(C::RPI * w + rsub);
 		// APERM: chunks 0..3 are K 32p + 8c of the half, chunks 4..7 K 64 + 32p + 8(c - 4)
 		const int cofs = C::APERM ? 128 * (chunk >> 2) + 16 * (chunk & 3) : 16 * chunk;
-		as.base[0] = (const char *)a.a16 + cofs;
-		as.base[1] = (const char *)a.a16lo + cofs;
+		as.base[0] = (const char *)a.a16;
+		as.base[1] = (const char *)a.a16lo;
+		as.cofs = cofs;
 		// row r = RPI (NWAVES c + w') + rsub' is entry c of lane slot RPI w' + rsub'
 		as.roff = roff + (C::RPI * w + rsub) * ROFF_STRIDE;
 		if (t < C::MT) {
@@ -548,8 +594,11 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 	uint8_t *Bs = As + C::LDS_A;
 
 	BRegs<TYPE> b0, b1;
-	if constexpr (C::B_LDS)
-		dma_b<TYPE, DOWN>(a, e, slab, 0, w, Bs);
+	BDma<TYPE> bd;
+	if constexpr (C::B_LDS) {
+		bdma_init<TYPE, DOWN>(a, e, slab, w, bd);
+		dma_b<TYPE, DOWN>(bd, slab, 0, w, Bs);
+	}
 	else
 		load_b<TYPE>(bs, 0, h, b0);
 	dma_a<TYPE, DOWN>(as, 0, w, As);
@@ -561,7 +610,7 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 	auto body = [&](int st, BRegs<TYPE> &cur, BRegs<TYPE> &nxt) {
 		if (st + 1 < nk) {
 			if constexpr (C::B_LDS)
-				dma_b<TYPE, DOWN>(a, e, slab, st + 1, w, Bs + ((st + 1) & 1) * C::BBUF);
+				dma_b<TYPE, DOWN>(bd, slab, st + 1, w, Bs + ((st + 1) & 1) * C::BBUF);
 			else
 				load_b<TYPE>(bs, st + 1, h, nxt);
 			dma_a<TYPE, DOWN>(as, st + 1, w, As + ((st + 1) & 1) * C::ABUF);
