@@ -5,9 +5,11 @@ so selected experts and gate weights must equal the oracle bit for bit.  The
 expert products run on bf16 matrix cores, so outputs are checked two ways:
 
   * against a float64 model of the same arithmetic (weights dequantised in
-    fp32 as TIE does, rounded to bf16; activations rounded to bf16; TIE's
-    table SwiGLU) -- this pins the kernels' tiling, operand layouts and
-    epilogue: relative L2 error <= 2e-3;
+    fp32 as TIE does, rounded to bf16 -- to f16 for Q4_K gate/up, which run
+    on the f16 matrix cores with x in f16; activations rounded to bf16;
+    TIE's table SwiGLU) -- this pins the kernels' tiling, operand layouts
+    (including the f16 path's K permutation) and epilogue: relative L2
+    error <= 2e-3;
   * against the fp32 oracle (TIE's own arithmetic) -- the bf16 rounding
     error, reported and bounded: relative L2 error <= 2e-2 for Q4_K/Q6_K
     weights, and max |err| <= 1e-3 for BF16 weights (activations split into
@@ -37,6 +39,40 @@ def bf16(a):
     return synth.bf16_bits_to_f32(synth.f32_to_bf16_bits(np.asarray(a, np.float32)))
 
 
+def f16(a):
+    return np.asarray(a, np.float32).astype(np.float16).astype(np.float32)
+
+
+def q4k_f16(buf):
+    """Q4_K weights as the f16 gate/up kernels form them, divided by their
+    factor 256: per sub-block D = d*sc and M = -dmin*m in fp32 (exact), times
+    256 rounded to f16, then code*D16 + M16 rounded once to f16 (v_pk_fma_f16).
+    Super-block layout (TIE's block_q4_K): d, dmin (f16), 12 scale bytes, 128
+    code bytes; sub-block 2g holds the low and 2g+1 the high nibbles of code
+    bytes 32g..32g+31."""
+    b = np.frombuffer(np.ascontiguousarray(buf).tobytes(), np.uint8).reshape(-1, 144)
+    nb = b.shape[0]
+    d = b[:, 0:2].copy().view(np.float16).astype(np.float32)[:, 0]
+    dmin = b[:, 2:4].copy().view(np.float16).astype(np.float32)[:, 0]
+    s = b[:, 4:16].astype(np.int32)
+    sc = np.empty((nb, 8), np.int32)
+    mn = np.empty((nb, 8), np.int32)
+    for j in range(4):
+        sc[:, j] = s[:, j] & 63
+        mn[:, j] = s[:, j + 4] & 63
+    for j in range(4, 8):
+        sc[:, j] = (s[:, j + 4] & 15) | ((s[:, j - 4] >> 6) << 4)
+        mn[:, j] = (s[:, j + 4] >> 4) | ((s[:, j] >> 6) << 4)
+    D = (d[:, None] * sc.astype(np.float32)).astype(np.float32)
+    M = -(dmin[:, None] * mn.astype(np.float32)).astype(np.float32)
+    D16 = f16(D * 256).astype(np.float64)
+    M16 = f16(M * 256).astype(np.float64)
+    qs = b[:, 16:].reshape(nb, 4, 32)
+    q = np.stack([qs & 15, qs >> 4], axis=2).reshape(nb, 8, 32).astype(np.float64)
+    W = (q * D16[:, :, None] + M16[:, :, None]).astype(np.float16)  # exact in float64, one rounding
+    return W.astype(np.float32).reshape(-1) / 256
+
+
 def dequant(buf, wtype, E, rows, inn):
     if wtype == synth.BF16:
         return synth.bf16_bits_to_f32(np.ascontiguousarray(buf).view(np.uint16)).reshape(E, rows, inn)
@@ -52,9 +88,16 @@ def model(layer, x, k, idx, w, tab, split):
     Wg = dequant(layer.gate, layer.gate_type, E, F, d)
     Wu = dequant(layer.up, layer.up_type, E, F, d)
     Wd = dequant(layer.down, layer.down_type, E, d, F)
+    xa = x
     if not split:
-        Wg, Wu, Wd = bf16(Wg), bf16(Wu), bf16(Wd)
-    xa = x if split else bf16(x)
+        if layer.gate_type == synth.Q4_K:
+            # f16 operands
+            Wg = q4k_f16(layer.gate).reshape(E, F, d)
+            Wu = q4k_f16(layer.up).reshape(E, F, d)
+            xa = f16(x)
+        else:
+            Wg, Wu, xa = bf16(Wg), bf16(Wu), bf16(x)
+        Wd = bf16(Wd)
     out = np.zeros(x.shape, np.float64)
     for t in range(x.shape[0]):
         for j in range(k):

@@ -56,6 +56,8 @@ namespace tie {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -71,6 +73,11 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // permuted to match)
 #ifndef TIE_Q6K_KST
 #define TIE_Q6K_KST 64
+#endif
+// Q4_K gate/up on the f16 matrix cores (weights dequantised with packed f16
+// math; 0 keeps bf16)
+#ifndef TIE_MFMA_F16
+#define TIE_MFMA_F16 1
 #endif
 #ifndef TIE_MFMA_GU_WPE
 #define TIE_MFMA_GU_WPE 2
@@ -119,6 +126,9 @@ struct MfmaArgs {
 template <int TYPE, bool DOWN = false> struct Cfg {
 	static constexpr int MT = DOWN ? MFMA_MT_DN : MFMA_MT_GU; // pair rows per work tile at most
 	static constexpr bool SPLIT = TYPE == TIE_GGML_BF16; // bf16 weights take activations as hi + lo planes
+	// Q4_K gate/up: f16 operands (x as f16, K order inside each 8-group
+	// 0,2,1,3,4,6,5,7; weights scaled by 2^F16_SHIFT)
+	static constexpr bool F16 = TIE_MFMA_F16 && TYPE == TIE_GGML_Q4_K && !DOWN;
 	// K per stage (Q4_K optionally 64: one 64-weight group per stage)
 	static constexpr int KST = SPLIT ? 64
 				    : (TYPE == TIE_GGML_Q4_K ? TIE_Q4K_KST : TYPE == TIE_GGML_Q6_K ? TIE_Q6K_KST : 128);
@@ -375,6 +385,73 @@ __device__ __forceinline__ void group_factors(const BRegs<TYPE> &b, int st, int 
 	}
 }
 
+// f16 path: weights carry a factor 2^F16_SHIFT so that the per-sub-block
+// scales D (d * sc, as small as 2^-24 * 63) and the weights stay in f16's
+// normal range; the gate/up epilogue takes the factor out (exact).
+constexpr int F16_SHIFT = 8;
+
+struct Fac16 {
+	f16x2 D[2][2], M[2][2]; // [row][sub-block]: D * 2^S (low nibbles) or D * 2^(S-4) (high), M * 2^S
+};
+
+__device__ __forceinline__ f16x2 splat16(float v)
+{
+	const _Float16 h = (_Float16)v;
+	return f16x2{h, h};
+}
+
+template <int TYPE>
+__device__ __forceinline__ void group_factors16(const BRegs<TYPE> &b, int st, int gi, Fac16 &f)
+{
+	Fac g;
+	group_factors<TYPE>(b, st, gi, g);
+#pragma unroll
+	for (int j = 0; j < 2; j++) {
+		f.D[j][0] = splat16(g.D[j][0] * (float)(1 << F16_SHIFT));
+		f.D[j][1] = splat16(g.D[j][1] * (float)(1 << (F16_SHIFT - 4)));
+		f.M[j][0] = splat16(g.M[j][0] * (float)(1 << F16_SHIFT));
+		f.M[j][1] = splat16(g.M[j][1] * (float)(1 << F16_SHIFT));
+	}
+}
+
+// Q4_K step s in f16: 8 weight codes of the lane's row (bytes of q.x, q.y,
+// low or high nibbles) -> f16 pairs (K 0,2), (1,3), (4,6), (5,7).  A code
+// lands in the mantissa of 1024.0 (0x6400): as q (low nibble, bits 0-3) or
+// 16 q (high nibble, bits 4-7); subtracting 1024 is exact, then one packed
+// fma applies the scale and offset (v_pk_fma_f16, one rounding).
+// The masks and the magic live in VGPRs (K16): a GFX9 VOP3 instruction takes
+// no literal, so only then is each pair one v_and_or_b32.
+struct K16 {
+	uint32_t lo, hi, magic;
+};
+
+__device__ __forceinline__ K16 k16_consts()
+{
+	K16 k = {0x000f000fu, 0x00f000f0u, 0x64006400u};
+	asm volatile("" : "+v"(k.lo), "+v"(k.hi), "+v"(k.magic));
+	return k;
+}
+
+__device__ __forceinline__ void deq_step16(const BRegs<TIE_GGML_Q4_K> &b, const Fac16 &f, const K16 &kc, int s,
+					   f16x8 out[2])
+{
+	const f16x2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+#pragma unroll
+	for (int j = 0; j < 2; j++) {
+		const int sub = s & 3, u = sub >> 1;
+		const u32x2 q = b.q[j][sub & 1];
+		const uint32_t msk = u ? kc.hi : kc.lo;
+		uint32_t w[4] = {q.x, q.x >> 8, q.y, q.y >> 8};
+		f16x2 r[4];
+#pragma unroll
+		for (int i = 0; i < 4; i++) {
+			const f16x2 v = __builtin_bit_cast(f16x2, (w[i] & msk) | kc.magic) - k1024;
+			r[i] = __builtin_elementwise_fma(v, f.D[j][u], f.M[j][u]);
+		}
+		out[j] = f16x8{r[0][0], r[0][1], r[1][0], r[1][1], r[2][0], r[2][1], r[3][0], r[3][1]};
+	}
+}
+
 // Dequantise the B fragments of 16-K step s of stage st for both rows.
 // Q4_K: step s is in group gi = s/4; steps 0, 1 of a group take the low
 // nibbles of its two chunks, steps 2, 3 the high nibbles.  Q6_K: the stage
@@ -505,6 +582,39 @@ __device__ __forceinline__ void stage_mfma(const BRegs<TYPE> &b, int st, const u
 			fr[i] = *reinterpret_cast<const bf16x8 *>(arow + (i / NMT) * C::A_TILE + (i % NMT) * 32 * C::RB +
 								  slot);
 	};
+	if constexpr (C::F16) {
+		Fac16 f;
+		group_factors16<TYPE>(b, st, 0, f);
+		f16x8 fa[2][NA], fb[2][2];
+		auto read16 = [&](int s, f16x8 fr[NA]) {
+			bf16x8 t[NA];
+			read(s, t);
+#pragma unroll
+			for (int i = 0; i < NA; i++)
+				fr[i] = __builtin_bit_cast(f16x8, t[i]);
+		};
+		const K16 kc = k16_consts();
+		read16(0, fa[0]);
+		deq_step16(b, f, kc, 0, fb[0]);
+#pragma unroll
+		for (int s = 0; s < C::NSTEP; s++) {
+			const int cur = s & 1;
+#pragma unroll
+			for (int i = 0; i < NA; i++) {
+				const int mt = i % NMT;
+				acc[mt][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[cur][i], fb[cur][0], acc[mt][0], 0, 0, 0);
+				acc[mt][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[cur][i], fb[cur][1], acc[mt][1], 0, 0, 0);
+			}
+			if (s + 1 < C::NSTEP) {
+				read16(s + 1, fa[cur ^ 1]);
+				if ((s + 1) % 4 == 0)
+					group_factors16<TYPE>(b, st, (s + 1) / 4, f);
+				deq_step16(b, f, kc, s + 1, fb[cur ^ 1]);
+			}
+			__builtin_amdgcn_sched_barrier(0);
+		}
+		return;
+	}
 	Fac f;
 	group_factors<TYPE>(b, st, 0, f);
 	bf16x8 fa[2][NA], fb[2][2];
@@ -657,7 +767,8 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 			const int p = pbase + mrow;
 			if (!DOWN) {
 				const int col = slab * GU_COLS + 32 * w + (lane & 31);
-				const float hv = tie_swiglu(acc[mt][0][i], acc[mt][1][i], silu);
+				constexpr float unscale = C::F16 ? 1.0f / (1 << F16_SHIFT) : 1.0f;
+				const float hv = tie_swiglu(acc[mt][0][i] * unscale, acc[mt][1][i] * unscale, silu);
 				const uint16_t hi = bf16_bits(hv);
 				a.h16[(size_t)p * a.rows + col] = hi;
 				if (C::SPLIT)
@@ -748,6 +859,19 @@ __global__ void to_bf16_kernel(const float *__restrict__ x, uint16_t *__restrict
 	}
 }
 
+// x (fp32) -> f16 rows for the f16 gate/up A operand, K order inside each
+// 8-group 0,2,1,3,4,6,5,7 (the order of the dequantised weight pairs)
+__global__ void to_f16_kernel(const float *__restrict__ x, uint16_t *__restrict__ y, size_t n8)
+{
+	for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n8; i += (size_t)gridDim.x * blockDim.x) {
+		const float4 a = reinterpret_cast<const float4 *>(x)[2 * i];
+		const float4 c = reinterpret_cast<const float4 *>(x)[2 * i + 1];
+		const f16x8 h = {(_Float16)a.x, (_Float16)a.z, (_Float16)a.y, (_Float16)a.w,
+				 (_Float16)c.x, (_Float16)c.z, (_Float16)c.y, (_Float16)c.w};
+		reinterpret_cast<f16x8 *>(y)[i] = h;
+	}
+}
+
 // x (fp32) -> bf16 high and remainder planes for the split gate/up A operand
 __global__ void to_split_kernel(const float *__restrict__ x, uint16_t *__restrict__ hi, uint16_t *__restrict__ lo,
 				size_t n4)
@@ -830,6 +954,8 @@ hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, con
 		const dim3 g((unsigned)((n4 + 255) / 256 < 4096 ? (n4 + 255) / 256 : 4096));
 		if (split)
 			hipLaunchKernelGGL(to_split_kernel, g, dim3(256), 0, s, x, ws.xb, ws.xlo, n4);
+		else if (TIE_MFMA_F16 && L.gate.type == TIE_GGML_Q4_K)
+			hipLaunchKernelGGL(to_f16_kernel, g, dim3(256), 0, s, x, ws.xb, n4 / 2);
 		else
 			hipLaunchKernelGGL(to_bf16_kernel, g, dim3(256), 0, s, x, ws.xb, n4);
 	}
