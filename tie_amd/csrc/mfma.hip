@@ -486,18 +486,18 @@ __device__ __forceinline__ void deq_step(const BRegs<TYPE> &b, const Fac &f, int
 }
 
 // ------------------------------------------------------------------ A staging
-// A stage: MT rows x KST K of each plane, RB bytes per row.  Direct
+// A stage: up to MT rows x KST K of each plane, RB bytes per row.  Direct
 // global->LDS loads (global_load_lds_dwordx4): one wave instruction writes
 // 64 consecutive 16-byte LDS slots = RPI whole rows; lane l fills slot l%CPR
 // of row l/CPR with the row's chunk slot ^ swz(row).  Wave w, instruction c
-// covers rows RPI*(NWAVES c + w) ..; swz(row) does not depend on c.  Rows
-// past the tile's end are not loaded: an MFMA output row depends only on its
-// own A row, and the epilogue drops those rows.
+// covers rows RPI*(NWAVES c + w) ..; swz(row) does not depend on c.  Only
+// the rows of the tile's live 32-row M tiles are loaded.
 // The byte offsets of the tile's rows sit in an LDS table written once per
 // tile, not in registers, ordered so that the NDMA offsets one lane needs
-// per stage are contiguous (one wait per stage).  Rows past the tile's end
-// read the tile's first row instead (no branch; those LDS rows feed only
-// output rows the epilogue drops).
+// per stage are contiguous (one wait per stage).  Rows of a live M tile past
+// the tile's end read the tile's first row instead (no branch; an MFMA
+// output row depends only on its own A row, and the epilogue drops those
+// rows).
 constexpr int ROFF_STRIDE = 16; // offsets per lane slot (>= NDMA, multiple of 4)
 struct ASrc {
 	const char *base[2];   // planes (wave-uniform)
@@ -526,23 +526,27 @@ __device__ __forceinline__ void dma16s(const void *base, uint32_t voff, uint32_t
 		     : "memory", "m0");
 }
 
-template <int TYPE, bool DOWN>
+// Only the rows of the NMT live 32-row M tiles are moved (the fragments of
+// the other rows are never read).
+template <int TYPE, bool DOWN, int NMT>
 __device__ __forceinline__ void dma_a(const ASrc &s, int st, int w, const uint8_t *buf)
 {
 	using C = Cfg<TYPE, DOWN>;
+	constexpr int NLIVE = (32 * NMT + NWAVES * C::RPI - 1) / (NWAVES * C::RPI); // DMA instructions per wave and plane
+	static_assert(NLIVE <= C::NDMA, "live rows exceed the tile");
 	// byte offset of the stage in an A row (APERM: block, half, quarter p;
 	// the lane's chunk offset covers the quarter p + 2 part)
 	const uint32_t ko = C::APERM ? 512u * (st >> 2) + 256u * ((st >> 1) & 1) + 64u * (st & 1) : (uint32_t)st * C::RB;
 	uint32_t off[(C::NDMA + 3) / 4 * 4]; // whole 16-byte reads (the lane slot holds ROFF_STRIDE entries)
 	static_assert(C::NDMA <= ROFF_STRIDE, "row offset slot too small");
 #pragma unroll
-	for (int c = 0; c < C::NDMA; c += 4)
+	for (int c = 0; c < NLIVE; c += 4)
 		*reinterpret_cast<u32x4 *>(off + c) = *reinterpret_cast<const u32x4 *>(s.roff + c);
 	const uint32_t lk = s.cofs + ko;
 #pragma unroll
 	for (int pl = 0; pl < C::NPL; pl++)
 #pragma unroll
-		for (int c = 0; c < C::NDMA; c++) {
+		for (int c = 0; c < NLIVE; c++) {
 			const int r0 = C::RPI * (NWAVES * c + w);
 			const uint32_t dst = lds_addr(buf + pl * C::A_TILE + r0 * C::RB);
 			dma16s(s.base[pl], off[c] + lk, __builtin_amdgcn_readfirstlane(dst));
@@ -711,7 +715,7 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 	}
 	else
 		load_b<TYPE>(bs, 0, h, b0);
-	dma_a<TYPE, DOWN>(as, 0, w, As);
+	dma_a<TYPE, DOWN, NMT>(as, 0, w, As);
 	stage_barrier();
 
 	// stage st: the weights and activations of st+1 are fetched (into the
@@ -723,7 +727,7 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 				dma_b<TYPE, DOWN>(bd, slab, st + 1, w, Bs + ((st + 1) & 1) * C::BBUF);
 			else
 				load_b<TYPE>(bs, st + 1, h, nxt);
-			dma_a<TYPE, DOWN>(as, st + 1, w, As + ((st + 1) & 1) * C::ABUF);
+			dma_a<TYPE, DOWN, NMT>(as, st + 1, w, As + ((st + 1) & 1) * C::ABUF);
 		}
 		if constexpr (C::B_LDS)
 			lds_b<TYPE>(Bs + (st & 1) * C::BBUF, bp, bi, st, h, cur);
