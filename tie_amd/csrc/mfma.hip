@@ -79,6 +79,15 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 #ifndef TIE_MFMA_F16
 #define TIE_MFMA_F16 1
 #endif
+// Tiles with at least this many 32-row M tiles run the cross-stage
+// software pipeline (fewer: each stage self-contained)
+#ifndef TIE_MFMA_PIPE_NMT
+#define TIE_MFMA_PIPE_NMT 3
+#endif
+// VALU instructions placed between two MFMAs of a stage's last step
+#ifndef TIE_MFMA_TAIL_VALU
+#define TIE_MFMA_TAIL_VALU 12
+#endif
 #ifndef TIE_MFMA_GU_WPE
 #define TIE_MFMA_GU_WPE 2
 #endif
@@ -339,20 +348,21 @@ __device__ __forceinline__ bf16x8 deq8(uint32_t lo, uint32_t hi, float D, float 
 	return __builtin_bit_cast(bf16x8, r);
 }
 
-// Q4_K 6-bit scale / min of sub-block j from the 12 scale bytes (words y, z, w of chunk 0)
+// Q4_K 6-bit scale / min of sub-block j from the 12 scale bytes s[0..11]
+// (words y, z, w of chunk 0), without branches (j is wave-uniform but not a
+// constant; branches would split the schedule).  With i = j % 4:
+//   j < 4:  sc = s[j] & 63,                       m = s[j+4] & 63
+//   j >= 4: sc = s[j+4] & 15 | (s[j-4] >> 6) << 4, m = s[j+4] >> 4 | (s[j] >> 6) << 4
+// s[j] / s[j+4] (j < 4) are byte i of y / z; s[j-4], s[j], s[j+4] (j >= 4)
+// byte i of y, z, w.  The high parts' width is 0 for j < 4.
 __device__ __forceinline__ void q4k_scale_min(const u32x4 &c0, int j, uint32_t &sc, uint32_t &mn)
 {
-	auto sb = [&](int i) {
-		const uint32_t wd = i < 4 ? c0.y : (i < 8 ? c0.z : c0.w);
-		return (wd >> (8 * (i & 3))) & 0xffu;
-	};
-	if (j < 4) {
-		sc = sb(j) & 63u;
-		mn = sb(j + 4) & 63u;
-	} else {
-		sc = (sb(j + 4) & 15u) | ((sb(j - 4) >> 6) << 4);
-		mn = (sb(j + 4) >> 4) | ((sb(j) >> 6) << 4);
-	}
+	const bool hi = j >= 4;
+	const uint32_t o = 8u * (uint32_t)(j & 3);
+	const uint32_t wlo = hi ? 4u : 6u, whi = hi ? 2u : 0u;
+	const uint32_t a = hi ? c0.w : c0.y, b = hi ? c0.w : c0.z;
+	sc = __builtin_amdgcn_ubfe(a, o, wlo) | (__builtin_amdgcn_ubfe(c0.y, o + 6u, whi) << 4);
+	mn = __builtin_amdgcn_ubfe(b, o + (hi ? 4u : 0u), wlo) | (__builtin_amdgcn_ubfe(c0.z, o + 6u, whi) << 4);
 }
 
 // Per-row dequantisation factors of the current 64-K group (Q4_K: scale D
@@ -565,10 +575,33 @@ __device__ __forceinline__ void stage_barrier()
 	__builtin_amdgcn_s_barrier();
 }
 
-// One stage of MFMAs over NMT live 32-row M tiles.  The A fragments of 16-K
-// step s+1 are read from LDS and its B fragments dequantised while the
-// MFMAs of step s run (a single wave per SIMD: the MFMAs' 32-cycle issue
-// slots are where its VALU and LDS instructions go).
+// Operand arithmetic of a quantised kernel: bf16 fragments, or f16 ones
+// (Q4_K gate/up).
+template <int TYPE, bool DOWN, bool F16 = Cfg<TYPE, DOWN>::F16> struct Ops;
+template <int TYPE, bool DOWN> struct Ops<TYPE, DOWN, false> {
+	using V = bf16x8;
+	using F = Fac;
+	__device__ static void factors(const BRegs<TYPE> &b, int st, int gi, F &f) { group_factors<TYPE>(b, st, gi, f); }
+	__device__ static void deq(const BRegs<TYPE> &b, const F &f, const K16 &, int st, int s, V out[2])
+	{
+		deq_step<TYPE>(b, f, st, s, out);
+	}
+	__device__ static f32x16 mma(V a, V b, f32x16 c) { return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0); }
+};
+template <int TYPE, bool DOWN> struct Ops<TYPE, DOWN, true> {
+	using V = f16x8;
+	using F = Fac16;
+	__device__ static void factors(const BRegs<TYPE> &b, int st, int gi, F &f) { group_factors16<TYPE>(b, st, gi, f); }
+	__device__ static void deq(const BRegs<TYPE> &b, const F &f, const K16 &kc, int, int s, V out[2])
+	{
+		deq_step16(b, f, kc, s, out);
+	}
+	__device__ static f32x16 mma(V a, V b, f32x16 c) { return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0); }
+};
+
+// One stage of MFMAs over NMT live 32-row M tiles (BF16 weights, held in
+// registers).  The A fragments of 16-K step s+1 are read from LDS while the
+// MFMAs of step s run.
 template <int TYPE, bool DOWN, int NMT>
 __device__ __forceinline__ void stage_mfma(const BRegs<TYPE> &b, int st, const uint8_t *__restrict__ A,
 					   f32x16 acc[6][2])
@@ -586,39 +619,6 @@ __device__ __forceinline__ void stage_mfma(const BRegs<TYPE> &b, int st, const u
 			fr[i] = *reinterpret_cast<const bf16x8 *>(arow + (i / NMT) * C::A_TILE + (i % NMT) * 32 * C::RB +
 								  slot);
 	};
-	if constexpr (C::F16) {
-		Fac16 f;
-		group_factors16<TYPE>(b, st, 0, f);
-		f16x8 fa[2][NA], fb[2][2];
-		auto read16 = [&](int s, f16x8 fr[NA]) {
-			bf16x8 t[NA];
-			read(s, t);
-#pragma unroll
-			for (int i = 0; i < NA; i++)
-				fr[i] = __builtin_bit_cast(f16x8, t[i]);
-		};
-		const K16 kc = k16_consts();
-		read16(0, fa[0]);
-		deq_step16(b, f, kc, 0, fb[0]);
-#pragma unroll
-		for (int s = 0; s < C::NSTEP; s++) {
-			const int cur = s & 1;
-#pragma unroll
-			for (int i = 0; i < NA; i++) {
-				const int mt = i % NMT;
-				acc[mt][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[cur][i], fb[cur][0], acc[mt][0], 0, 0, 0);
-				acc[mt][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[cur][i], fb[cur][1], acc[mt][1], 0, 0, 0);
-			}
-			if (s + 1 < C::NSTEP) {
-				read16(s + 1, fa[cur ^ 1]);
-				if ((s + 1) % 4 == 0)
-					group_factors16<TYPE>(b, st, (s + 1) / 4, f);
-				deq_step16(b, f, kc, s + 1, fb[cur ^ 1]);
-			}
-			__builtin_amdgcn_sched_barrier(0);
-		}
-		return;
-	}
 	Fac f;
 	group_factors<TYPE>(b, st, 0, f);
 	bf16x8 fa[2][NA], fb[2][2];
@@ -707,37 +707,125 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 	}
 	uint8_t *Bs = As + C::LDS_A;
 
-	BRegs<TYPE> b0, b1;
-	BDma<TYPE> bd;
 	if constexpr (C::B_LDS) {
+		// Quantised weights, software-pipelined over the stages: a stage's
+		// step s MFMAs run while the A fragments of step s+1 are read and its
+		// weights dequantised; the next stage's DMA is issued after step 0's
+		// MFMAs; the last step's MFMAs run after the stage barrier, while the
+		// next stage's weights are read from LDS and its step 0 prepared.
+		using O = Ops<TYPE, DOWN>;
+		using V = typename O::V;
+		constexpr int NA = NMT;
+		static_assert(C::NPL == 1 && C::NSTEP % 2 == 0, "one activation plane, even step count");
+		uint8_t *Bs = As + C::LDS_A;
+		BDma<TYPE> bd;
 		bdma_init<TYPE, DOWN>(a, e, slab, w, bd);
-		dma_b<TYPE, DOWN>(bd, slab, 0, w, Bs);
-	}
-	else
-		load_b<TYPE>(bs, 0, h, b0);
-	dma_a<TYPE, DOWN, NMT>(as, 0, w, As);
-	stage_barrier();
-
-	// stage st: the weights and activations of st+1 are fetched (into the
-	// other LDS buffers, or registers for BF16 weights), then the MFMAs of
-	// st run
-	auto body = [&](int st, BRegs<TYPE> &cur, BRegs<TYPE> &nxt) {
-		if (st + 1 < nk) {
-			if constexpr (C::B_LDS)
-				dma_b<TYPE, DOWN>(bd, slab, st + 1, w, Bs + ((st + 1) & 1) * C::BBUF);
-			else
-				load_b<TYPE>(bs, st + 1, h, nxt);
-			dma_a<TYPE, DOWN, NMT>(as, st + 1, w, As + ((st + 1) & 1) * C::ABUF);
-		}
-		if constexpr (C::B_LDS)
-			lds_b<TYPE>(Bs + (st & 1) * C::BBUF, bp, bi, st, h, cur);
-		stage_mfma<TYPE, DOWN, NMT>(cur, st, As + (st & 1) * C::ABUF, acc);
+		auto abuf = [&](int st) { return As + (st & 1) * C::ABUF; };
+		auto bbuf = [&](int st) { return Bs + (st & 1) * C::BBUF; };
+		auto issue = [&](int st) {
+			dma_b<TYPE, DOWN>(bd, slab, st, w, bbuf(st));
+			dma_a<TYPE, DOWN, NMT>(as, st, w, abuf(st));
+		};
+		// fragment row r = 32 mt + lane%32 (swz(r) = swz(lane%32)), chunk 2s + lane/32
+		const int arow = (lane & 31) * C::RB, key = C::swz(lane & 31);
+		V fa[2][NA], fb[2][2];
+		typename O::F f;
+		BRegs<TYPE> b;
+		const K16 kc = k16_consts();
+		auto read = [&](int st, int s, V fr[NA]) {
+			const uint8_t *A = abuf(st) + arow + ((2 * s + (lane >> 5)) ^ key) * 16;
+#pragma unroll
+			for (int i = 0; i < NA; i++)
+				fr[i] = *reinterpret_cast<const V *>(A + i * 32 * C::RB);
+		};
+		auto prep = [&](int st, int s, int slot) {
+			read(st, s, fa[slot]);
+			if (s == 0 || (TYPE == TIE_GGML_Q4_K && s % 4 == 0))
+				O::factors(b, st, s / 4, f);
+			O::deq(b, f, kc, st, s, fb[slot]);
+		};
+		auto mm = [&](int slot) {
+#pragma unroll
+			for (int i = 0; i < NA; i++) {
+				acc[i][0] = O::mma(fa[slot][i], fb[slot][0], acc[i][0]);
+				acc[i][1] = O::mma(fa[slot][i], fb[slot][1], acc[i][1]);
+			}
+		};
+		constexpr int L = (C::NSTEP - 1) & 1; // slot of a stage's last step
+		// all steps but the last of stage st (the next stage's DMA with more)
+		auto steps = [&](int st, bool more) {
+#pragma unroll
+			for (int s = 0; s + 1 < C::NSTEP; s++) {
+				mm(s & 1);
+				// the buffers written here were last read in stage st - 1,
+				// which every wave has left (its barrier)
+				if (s == 0 && more)
+					issue(st + 1);
+				prep(st, s + 1, (s & 1) ^ 1);
+				__builtin_amdgcn_sched_barrier(0);
+			}
+		};
+		issue(0);
 		stage_barrier();
-	};
-	if constexpr (C::B_LDS) {
-		for (int st = 0; st < nk; st++)
-			body(st, b0, b0);
+		if constexpr (NMT < TIE_MFMA_PIPE_NMT) {
+			// few MFMAs per step: each stage self-contained (its DMA first,
+			// then its weights from LDS, then the steps)
+			for (int st = 0; st < nk; st++) {
+				if (st + 1 < nk)
+					issue(st + 1);
+				lds_b<TYPE>(bbuf(st), bp, bi, st, h, b);
+				prep(st, 0, 0);
+#pragma unroll
+				for (int s = 0; s < C::NSTEP; s++) {
+					mm(s & 1);
+					if (s + 1 < C::NSTEP)
+						prep(st, s + 1, (s & 1) ^ 1);
+					__builtin_amdgcn_sched_barrier(0);
+				}
+				stage_barrier();
+			}
+		} else {
+			lds_b<TYPE>(bbuf(0), bp, bi, 0, h, b);
+			prep(0, 0, 0);
+			for (int st = 0; st + 1 < nk; st++) {
+				steps(st, true);
+				// the last step's fragments are in registers: the barrier only
+				// waits for stage st + 1's data and this stage's LDS reads
+				stage_barrier();
+				lds_b<TYPE>(bbuf(st + 1), bp, bi, st + 1, h, b);
+				mm(L);
+				prep(st + 1, 0, L ^ 1);
+				// order: the LDS reads, two MFMAs (their latency), then the
+				// preparation's VALU work spread between the other MFMAs
+				__builtin_amdgcn_sched_group_barrier(0x100, 32, 0);
+				__builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+#pragma unroll
+				for (int i = 2; i < 2 * NA; i++) {
+					__builtin_amdgcn_sched_group_barrier(0x002, TIE_MFMA_TAIL_VALU, 0);
+					__builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+				}
+				__builtin_amdgcn_sched_barrier(0);
+			}
+			steps(nk - 1, false);
+			stage_barrier(); // every wave's LDS reads done before the epilogue reuses the buffers
+			mm(L);
+		}
 	} else {
+		BRegs<TYPE> b0, b1;
+		load_b<TYPE>(bs, 0, h, b0);
+		dma_a<TYPE, DOWN, NMT>(as, 0, w, As);
+		stage_barrier();
+
+		// stage st: the weights (registers) and activations (the other LDS
+		// buffer) of st+1 are fetched, then the MFMAs of st run
+		auto body = [&](int st, BRegs<TYPE> &cur, BRegs<TYPE> &nxt) {
+			if (st + 1 < nk) {
+				load_b<TYPE>(bs, st + 1, h, nxt);
+				dma_a<TYPE, DOWN, NMT>(as, st + 1, w, As + ((st + 1) & 1) * C::ABUF);
+			}
+			stage_mfma<TYPE, DOWN, NMT>(cur, st, As + (st & 1) * C::ABUF, acc);
+			stage_barrier();
+		};
 		for (int st = 0; st < nk; st += 2) {
 			body(st, b0, b1);
 			if (st + 1 < nk)
