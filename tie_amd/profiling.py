@@ -37,6 +37,7 @@ _NAMES = (
     ("tie::combine_kernel", "combine"),
     ("tie::rmsnorm_kernel", "rmsnorm"),
     ("tie::to_bf16_kernel", "mfma_gate_up"),
+    ("tie::to_f16_kernel", "mfma_gate_up"),
     ("tie::to_split_kernel", "mfma_gate_up"),
 )
 
