@@ -30,6 +30,12 @@ constexpr int SILU_N = TIE_SILU_TABLE_SIZE;
 constexpr int MFMA_MT_GU = TIE_MFMA_MT_GU;
 constexpr int MFMA_MT_DN = TIE_MFMA_MT_DN;
 constexpr int MFMA_MT = MFMA_MT_GU > MFMA_MT_DN ? MFMA_MT_GU : MFMA_MT_DN;
+// gate/up tiles of the small-tile kernel (quantised weights, few pairs per
+// expert: more waves per SIMD), used up to TIE_MFMA_SMALL_AVG pairs per expert
+constexpr int MFMA_MT_GU_SMALL = 64;
+#ifndef TIE_MFMA_SMALL_AVG
+#define TIE_MFMA_SMALL_AVG 32
+#endif
 
 // Device layout of one stacked expert tensor [E][rows][in].
 //
@@ -107,6 +113,8 @@ hipError_t launch_exact_block(const Layer &L, const float *x, int T, int k, cons
 hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, const float *silu, Workspace &ws,
 			       hipStream_t s);
 int mfma_max_tiles(int npairs, int E); // per list
+struct Layer;
+int mfma_gu_rows(const Layer &L, int npairs); // rows per gate/up tile (the tile list's and the kernel's)
 // Dense F32-input matrix product through the expert GEMV kernels: out[t][r]
 // = W[r] . x[t] (W one "expert": rows, in, panel layout); dense_groups(T)
 // token groups (the workspace needs that many experts and T pairs)

@@ -30,7 +30,7 @@ __global__ __launch_bounds__(DSP_THREADS) void dispatch_kernel(const int32_t *__
 							       int32_t *__restrict__ active,
 							       int32_t *__restrict__ tile_e,
 							       int32_t *__restrict__ tile_m0,
-							       int32_t *__restrict__ ntiles, int tile_cap)
+							       int32_t *__restrict__ ntiles, int tile_cap, int mt_gu)
 {
 	extern __shared__ __attribute__((aligned(16))) int32_t sidx[];
 	__shared__ __attribute__((aligned(16))) int32_t cnt[MAX_E];
@@ -38,7 +38,7 @@ __global__ __launch_bounds__(DSP_THREADS) void dispatch_kernel(const int32_t *__
 	__shared__ int wsum[DSP_THREADS / 64];
 	if (npairs > DSP_STAGE_MAX) {
 		group_pairs<DSP_THREADS>(topk_idx, npairs, E, cnt, cur, wsum, offsets, pairs, active, tile_e, tile_m0,
-					 ntiles, nullptr, tile_cap);
+					 ntiles, nullptr, tile_cap, mt_gu);
 		return;
 	}
 	// selections in, pair list out, both through LDS: the scattered
@@ -55,7 +55,7 @@ __global__ __launch_bounds__(DSP_THREADS) void dispatch_kernel(const int32_t *__
 	// if any, were not placed)
 	const int valid =
 		group_pairs<DSP_THREADS>(sidx, npairs, E, cnt, cur, wsum, offsets, spairs, active, tile_e, tile_m0, ntiles,
-					 nullptr, tile_cap);
+					 nullptr, tile_cap, mt_gu);
 	const int v4 = valid >> 2;
 	for (int i = threadIdx.x; i < v4; i += DSP_THREADS)
 		reinterpret_cast<int4 *>(pairs)[i] = reinterpret_cast<const int4 *>(spairs)[i];
@@ -77,7 +77,7 @@ hipError_t launch_dispatch(const Layer &L, int T, int k, const int32_t *topk_idx
 		attr = true;
 	}
 	hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(DSP_THREADS), lds, s, topk_idx, npairs, L.E, ws.offsets,
-			   ws.pairs, ws.active, ws.tile_e, ws.tile_m0, ws.ntiles, ws.tile_cap);
+			   ws.pairs, ws.active, ws.tile_e, ws.tile_m0, ws.ntiles, ws.tile_cap, mfma_gu_rows(L, npairs));
 	return hipGetLastError();
 }
 

@@ -11,7 +11,8 @@
 //   down:     Y = h_e Wd_e^T, scattered to the pairs' rows of y
 //
 // Work tile: up to MT pair rows of one expert (MFMA_MT_GU = 160 for
-// gate/up, MFMA_MT_DN = 128 for down; an expert with more pairs is split
+// gate/up, MFMA_MT_GU_SMALL = 64 for gate/up with few pairs per expert,
+// MFMA_MT_DN = 128 for down; an expert with more pairs is split
 // evenly over several tiles) x 128 F columns (gate/up: of gate and of up)
 // or 256 output columns (down).  A workgroup is 4 waves, one per SIMD;
 // wave w owns two 32-wide column tiles -- gate/up: the gate and the up tile
@@ -132,8 +133,9 @@ struct MfmaArgs {
 	uint16_t *y16;           // down out [pair][d] (quantised weights: bf16)
 };
 
-template <int TYPE, bool DOWN = false> struct Cfg {
-	static constexpr int MT = DOWN ? MFMA_MT_DN : MFMA_MT_GU; // pair rows per work tile at most
+template <int TYPE, bool DOWN = false, int MTR = 0> struct Cfg {
+	// pair rows per work tile at most (MTR: the small-tile gate/up kernel's)
+	static constexpr int MT = MTR ? MTR : DOWN ? MFMA_MT_DN : MFMA_MT_GU;
 	static constexpr bool SPLIT = TYPE == TIE_GGML_BF16; // bf16 weights take activations as hi + lo planes
 	// Q4_K gate/up: f16 operands (x as f16, K order inside each 8-group
 	// 0,2,1,3,4,6,5,7; weights scaled by 2^F16_SHIFT)
@@ -538,10 +540,10 @@ __device__ __forceinline__ void dma16s(const void *base, uint32_t voff, uint32_t
 
 // Only the rows of the NMT live 32-row M tiles are moved (the fragments of
 // the other rows are never read).
-template <int TYPE, bool DOWN, int NMT>
+template <int TYPE, bool DOWN, int NMT, int MTR>
 __device__ __forceinline__ void dma_a(const ASrc &s, int st, int w, const uint8_t *buf)
 {
-	using C = Cfg<TYPE, DOWN>;
+	using C = Cfg<TYPE, DOWN, MTR>;
 	constexpr int NLIVE = (32 * NMT + NWAVES * C::RPI - 1) / (NWAVES * C::RPI); // DMA instructions per wave and plane
 	static_assert(NLIVE <= C::NDMA, "live rows exceed the tile");
 	// byte offset of the stage in an A row (APERM: block, half, quarter p;
@@ -602,11 +604,11 @@ template <int TYPE, bool DOWN> struct Ops<TYPE, DOWN, true> {
 // One stage of MFMAs over NMT live 32-row M tiles (BF16 weights, held in
 // registers).  The A fragments of 16-K step s+1 are read from LDS while the
 // MFMAs of step s run.
-template <int TYPE, bool DOWN, int NMT>
+template <int TYPE, bool DOWN, int NMT, int MTR>
 __device__ __forceinline__ void stage_mfma(const BRegs<TYPE> &b, int st, const uint8_t *__restrict__ A,
 					   f32x16 acc[6][2])
 {
-	using C = Cfg<TYPE, DOWN>;
+	using C = Cfg<TYPE, DOWN, MTR>;
 	constexpr int NA = NMT * C::NPL; // fragments per step (hi [+ lo] per tile)
 	const int lane = threadIdx.x & 63;
 	// fragment row r = 32 mt + lane%32 (swz(r) = swz(lane%32)), chunk 2s + lane/32
@@ -645,11 +647,11 @@ __device__ __forceinline__ void stage_mfma(const BRegs<TYPE> &b, int st, const u
 
 // ------------------------------------------------------------------ kernel
 // One work tile with NMT live 32-row M tiles (nrows <= 32 NMT).
-template <int TYPE, bool DOWN, int NMT>
+template <int TYPE, bool DOWN, int NMT, int MTR>
 __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_t *roff, int e, int pbase, int nrows,
 					 int slab)
 {
-	using C = Cfg<TYPE, DOWN>;
+	using C = Cfg<TYPE, DOWN, MTR>;
 	const int nk = a.in / C::KST;
 	const int t = threadIdx.x;
 	const int w = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -724,7 +726,7 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 		auto bbuf = [&](int st) { return Bs + (st & 1) * C::BBUF; };
 		auto issue = [&](int st) {
 			dma_b<TYPE, DOWN>(bd, slab, st, w, bbuf(st));
-			dma_a<TYPE, DOWN, NMT>(as, st, w, abuf(st));
+			dma_a<TYPE, DOWN, NMT, MTR>(as, st, w, abuf(st));
 		};
 		// fragment row r = 32 mt + lane%32 (swz(r) = swz(lane%32)), chunk 2s + lane/32
 		const int arow = (lane & 31) * C::RB, key = C::swz(lane & 31);
@@ -813,7 +815,7 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 	} else {
 		BRegs<TYPE> b0, b1;
 		load_b<TYPE>(bs, 0, h, b0);
-		dma_a<TYPE, DOWN, NMT>(as, 0, w, As);
+		dma_a<TYPE, DOWN, NMT, MTR>(as, 0, w, As);
 		stage_barrier();
 
 		// stage st: the weights (registers) and activations (the other LDS
@@ -821,9 +823,9 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 		auto body = [&](int st, BRegs<TYPE> &cur, BRegs<TYPE> &nxt) {
 			if (st + 1 < nk) {
 				load_b<TYPE>(bs, st + 1, h, nxt);
-				dma_a<TYPE, DOWN, NMT>(as, st + 1, w, As + ((st + 1) & 1) * C::ABUF);
+				dma_a<TYPE, DOWN, NMT, MTR>(as, st + 1, w, As + ((st + 1) & 1) * C::ABUF);
 			}
-			stage_mfma<TYPE, DOWN, NMT>(cur, st, As + (st & 1) * C::ABUF, acc);
+			stage_mfma<TYPE, DOWN, NMT, MTR>(cur, st, As + (st & 1) * C::ABUF, acc);
 			stage_barrier();
 		};
 		for (int st = 0; st < nk; st += 2) {
@@ -833,11 +835,11 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 		}
 	}
 
-	// gate/up: TIE's SiLU table (32 KiB) into the now idle A buffers, so the
-	// epilogue's table lookups are LDS reads
+	// gate/up: TIE's SiLU table (32 KiB) into the now idle stage buffers, so
+	// the epilogue's table lookups are LDS reads
 	const float *silu = a.silu;
 	if constexpr (!DOWN) {
-		static_assert(SILU_N * 4 <= 2 * C::ABUF, "SiLU table must fit the A buffers");
+		static_assert(SILU_N * 4 <= C::LDS_A + C::LDS_B, "SiLU table must fit the stage buffers");
 #pragma unroll
 		for (int c = 0; c < SILU_N * 4 / 1024 / NWAVES; c++) {
 			const int off = 1024 * (NWAVES * c + w);
@@ -885,16 +887,16 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 // waves per SIMD: the quantised kernels keep their LDS and registers small
 // enough for two workgroups per CU; the BF16 kernels (weights prefetched
 // into registers) run one wave per SIMD
-constexpr int mf_wpe(int type, bool down)
+constexpr int mf_wpe(int type, bool down, int mtr)
 {
-	return type == TIE_GGML_BF16 ? 1 : down ? TIE_MFMA_DN_WPE : TIE_MFMA_GU_WPE;
+	return type == TIE_GGML_BF16 ? 1 : mtr ? 3 : down ? TIE_MFMA_DN_WPE : TIE_MFMA_GU_WPE;
 }
 
-template <int TYPE, bool DOWN>
-__global__ __launch_bounds__(MF_THREADS) __attribute__((amdgpu_waves_per_eu(mf_wpe(TYPE, DOWN), mf_wpe(TYPE, DOWN)))) void
+template <int TYPE, bool DOWN, int MTR>
+__global__ __launch_bounds__(MF_THREADS) __attribute__((amdgpu_waves_per_eu(mf_wpe(TYPE, DOWN, MTR), mf_wpe(TYPE, DOWN, MTR)))) void
 mfma_experts_kernel(MfmaArgs a)
 {
-	using C = Cfg<TYPE, DOWN>;
+	using C = Cfg<TYPE, DOWN, MTR>;
 	constexpr int MT = C::MT, MT_TILES = C::MT / 32;
 	extern __shared__ __attribute__((aligned(16))) uint8_t As[]; // A [2][ABUF] | B [2][BBUF] | row offsets
 	uint32_t *roff = reinterpret_cast<uint32_t *>(As + C::LDS_A + C::LDS_B);
@@ -921,24 +923,26 @@ mfma_experts_kernel(MfmaArgs a)
 	const int nrows = min((cnt + ntl - 1) / ntl, cnt - m0);
 	switch ((nrows + 31) >> 5) {
 	case 1:
-		run_tile<TYPE, DOWN, 1>(a, As, roff, e, pbase, nrows, slab);
+		run_tile<TYPE, DOWN, 1, MTR>(a, As, roff, e, pbase, nrows, slab);
 		break;
 	case 2:
-		run_tile<TYPE, DOWN, 2>(a, As, roff, e, pbase, nrows, slab);
+		run_tile<TYPE, DOWN, 2, MTR>(a, As, roff, e, pbase, nrows, slab);
 		break;
 	case 3:
-		run_tile<TYPE, DOWN, 3>(a, As, roff, e, pbase, nrows, slab);
+		if constexpr (MT_TILES >= 3)
+			run_tile<TYPE, DOWN, (MT_TILES >= 3 ? 3 : 1), MTR>(a, As, roff, e, pbase, nrows, slab);
 		break;
 	case 4:
-		run_tile<TYPE, DOWN, 4>(a, As, roff, e, pbase, nrows, slab);
+		if constexpr (MT_TILES >= 4)
+			run_tile<TYPE, DOWN, (MT_TILES >= 4 ? 4 : 1), MTR>(a, As, roff, e, pbase, nrows, slab);
 		break;
 	case 5:
 		if constexpr (MT_TILES >= 5)
-			run_tile<TYPE, DOWN, (MT_TILES >= 5 ? 5 : 1)>(a, As, roff, e, pbase, nrows, slab);
+			run_tile<TYPE, DOWN, (MT_TILES >= 5 ? 5 : 1), MTR>(a, As, roff, e, pbase, nrows, slab);
 		break;
 	default:
 		if constexpr (MT_TILES >= 6)
-			run_tile<TYPE, DOWN, (MT_TILES >= 6 ? 6 : 1)>(a, As, roff, e, pbase, nrows, slab);
+			run_tile<TYPE, DOWN, (MT_TILES >= 6 ? 6 : 1), MTR>(a, As, roff, e, pbase, nrows, slab);
 	}
 }
 
@@ -976,28 +980,34 @@ __global__ void to_split_kernel(const float *__restrict__ x, uint16_t *__restric
 	}
 }
 
-template <int TYPE, bool DOWN>
+template <int TYPE, bool DOWN, int MTR = 0>
 static hipError_t launch_type(const MfmaArgs &a, dim3 grid, hipStream_t s)
 {
 	// the double-buffered A tile exceeds the default 64 KiB of dynamic LDS
-	using C = Cfg<TYPE, DOWN>;
+	using C = Cfg<TYPE, DOWN, MTR>;
 	constexpr size_t lds = (size_t)C::LDS_A + C::LDS_B + 4 * (size_t)(C::RPI * NWAVES * ROFF_STRIDE);
 	static_assert(lds <= 160 * 1024, "LDS budget");
 	static bool attr = false;
 	if (!attr) {
-		const hipError_t err = hipFuncSetAttribute((const void *)mfma_experts_kernel<TYPE, DOWN>,
+		const hipError_t err = hipFuncSetAttribute((const void *)mfma_experts_kernel<TYPE, DOWN, MTR>,
 							   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
 		if (err != hipSuccess)
 			return err;
 		attr = true;
 	}
-	hipLaunchKernelGGL((mfma_experts_kernel<TYPE, DOWN>), grid, dim3(MF_THREADS), lds, s, a);
+	hipLaunchKernelGGL((mfma_experts_kernel<TYPE, DOWN, MTR>), grid, dim3(MF_THREADS), lds, s, a);
 	return hipGetLastError();
 }
 
 template <bool DOWN>
-static hipError_t launch_one(const MfmaArgs &a, int type, dim3 grid, hipStream_t s)
+static hipError_t launch_one(const MfmaArgs &a, int type, dim3 grid, hipStream_t s, bool small = false)
 {
+	if constexpr (!DOWN) {
+		if (small && type == TIE_GGML_Q4_K)
+			return launch_type<TIE_GGML_Q4_K, false, MFMA_MT_GU_SMALL>(a, grid, s);
+		if (small && type == TIE_GGML_Q6_K)
+			return launch_type<TIE_GGML_Q6_K, false, MFMA_MT_GU_SMALL>(a, grid, s);
+	}
 	if (type == TIE_GGML_Q4_K)
 		return launch_type<TIE_GGML_Q4_K, DOWN>(a, grid, s);
 	if (type == TIE_GGML_Q6_K)
@@ -1007,8 +1017,18 @@ static hipError_t launch_one(const MfmaArgs &a, int type, dim3 grid, hipStream_t
 
 int mfma_max_tiles(int npairs, int E)
 {
-	constexpr int mt = MFMA_MT_GU < MFMA_MT_DN ? MFMA_MT_GU : MFMA_MT_DN;
+	constexpr int mt0 = MFMA_MT_GU < MFMA_MT_DN ? MFMA_MT_GU : MFMA_MT_DN;
+	constexpr int mt = mt0 < MFMA_MT_GU_SMALL ? mt0 : MFMA_MT_GU_SMALL;
 	return (npairs + mt - 1) / mt + E;
+}
+
+// Quantised gate/up with at most TIE_MFMA_SMALL_AVG pairs per expert on
+// average: 64-row tiles, three waves per SIMD (smaller accumulator and LDS
+// footprint); measured faster there, slower for large expert counts.
+int mfma_gu_rows(const Layer &L, int npairs)
+{
+	const bool quant = L.gate.type == TIE_GGML_Q4_K || L.gate.type == TIE_GGML_Q6_K;
+	return quant && npairs <= TIE_MFMA_SMALL_AVG * L.E ? MFMA_MT_GU_SMALL : MFMA_MT_GU;
 }
 
 hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, const float *silu, Workspace &ws,
@@ -1061,7 +1081,8 @@ hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, con
 	a.a16lo = ws.xlo;
 	a.h16 = ws.hb;
 	a.h16lo = ws.hlo;
-	hipError_t err = launch_one<false>(a, L.gate.type, dim3(L.F / GU_COLS, max_tiles), s);
+	hipError_t err = launch_one<false>(a, L.gate.type, dim3(L.F / GU_COLS, max_tiles), s,
+					   mfma_gu_rows(L, npairs) == MFMA_MT_GU_SMALL);
 	prof_end(s);
 	if (err != hipSuccess)
 		return err;

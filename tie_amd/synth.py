@@ -158,6 +158,7 @@ CONFIGS = {
     "30b_t128": dict(d=2048, F=768, E=128, k=8, T=128, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1245),
     "30b_t256": dict(d=2048, F=768, E=128, k=8, T=256, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1246),
     "30b_t512": dict(d=2048, F=768, E=128, k=8, T=512, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1247),
+    "30b_t1024": dict(d=2048, F=768, E=128, k=8, T=1024, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1248),
     "30b_t32_ffn": dict(d=2048, F=768, E=128, k=8, T=32, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1235,
                         residual=True),
     "30b_t2048": dict(d=2048, F=768, E=128, k=8, T=2048, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1236),
