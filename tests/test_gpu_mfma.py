@@ -5,11 +5,12 @@ so selected experts and gate weights must equal the oracle bit for bit.  The
 expert products run on bf16 matrix cores, so outputs are checked two ways:
 
   * against a float64 model of the same arithmetic (weights dequantised in
-    fp32 as TIE does, rounded to bf16 -- to f16 for Q4_K gate/up, which run
-    on the f16 matrix cores with x in f16; activations rounded to bf16;
-    TIE's table SwiGLU) -- this pins the kernels' tiling, operand layouts
-    (including the f16 path's K permutation) and epilogue: relative L2
-    error <= 2e-3;
+    fp32 as TIE does, rounded to bf16 -- Q4_K and Q6_K weights run on the
+    f16 matrix cores instead, emulated exactly, with x in f16 and h as
+    f16(h / 256) * 256; other activations rounded to bf16; TIE's table
+    SwiGLU; y rounded to bf16) -- this pins the kernels' tiling, operand
+    layouts (including the f16 path's K permutation) and epilogue: relative
+    L2 error <= 2e-3;
   * against the fp32 oracle (TIE's own arithmetic) -- the bf16 rounding
     error, reported and bounded: relative L2 error <= 2e-2 for Q4_K/Q6_K
     weights, and max |err| <= 1e-3 for BF16 weights (activations split into
@@ -73,6 +74,36 @@ def q4k_f16(buf):
     return W.astype(np.float32).reshape(-1) / 256
 
 
+def q6k_f16(buf):
+    """Q6_K weights as the f16 kernels form them, divided by their factor 256:
+    D = d*sc in fp32 (exact), D*256 rounded to f16, then (code - 32)*D16
+    rounded once to f16 (v_pk_mul_f16).  Super-block layout (TIE's
+    block_q6_K): ql[128], qh[64], int8 scales[16], d (f16); half n, l < 32:
+    weights 128n + l + 32i take ql nibble (ql[64n + l + 32(i%2)], low for
+    i < 2), qh bits 2i of qh[32n + l], scale 8n + l//16 + 2i."""
+    b = np.frombuffer(np.ascontiguousarray(buf).tobytes(), np.uint8).reshape(-1, 210)
+    nb = b.shape[0]
+    ql, qh = b[:, 0:128].astype(np.int32), b[:, 128:192].astype(np.int32)
+    sc = b[:, 192:208].copy().view(np.int8).astype(np.float32)
+    d = b[:, 208:210].copy().view(np.float16).astype(np.float32)[:, 0]
+    q = np.empty((nb, 256), np.int32)
+    s = np.empty((nb, 256), np.float32)
+    l = np.arange(32)
+    for n in range(2):
+        for i in range(4):
+            nib = ql[:, 64 * n + l + 32 * (i % 2)]
+            nib = nib & 15 if i < 2 else nib >> 4
+            q[:, 128 * n + 32 * i + l] = nib | (((qh[:, 32 * n + l] >> (2 * i)) & 3) << 4)
+            s[:, 128 * n + 32 * i + l] = sc[:, 8 * n + l // 16 + 2 * i]
+    D16 = f16((d[:, None] * s).astype(np.float32) * 256).astype(np.float64)
+    W = ((q - 32).astype(np.float64) * D16).astype(np.float16)  # exact in float64, one rounding
+    return W.astype(np.float32).reshape(-1) / 256
+
+
+def quant_f16(buf, wtype):
+    return q4k_f16(buf) if wtype == synth.Q4_K else q6k_f16(buf)
+
+
 def dequant(buf, wtype, E, rows, inn):
     if wtype == synth.BF16:
         return synth.bf16_bits_to_f32(np.ascontiguousarray(buf).view(np.uint16)).reshape(E, rows, inn)
@@ -89,14 +120,19 @@ def model(layer, x, k, idx, w, tab, split):
     Wu = dequant(layer.up, layer.up_type, E, F, d)
     Wd = dequant(layer.down, layer.down_type, E, d, F)
     xa = x
+    quant = (synth.Q4_K, synth.Q6_K)
+    h16 = layer.down_type in quant  # h as f16 * 2^-8 (down on f16 operands)
     if not split:
-        if layer.gate_type == synth.Q4_K:
+        if layer.gate_type in quant:
             # f16 operands
-            Wg = q4k_f16(layer.gate).reshape(E, F, d)
-            Wu = q4k_f16(layer.up).reshape(E, F, d)
+            Wg = quant_f16(layer.gate, layer.gate_type).reshape(E, F, d)
+            Wu = quant_f16(layer.up, layer.up_type).reshape(E, F, d)
             xa = f16(x)
         else:
             Wg, Wu, xa = bf16(Wg), bf16(Wu), bf16(x)
+    if h16:
+        Wd = quant_f16(layer.down, layer.down_type).reshape(E, d, F)
+    elif not split:
         Wd = bf16(Wd)
     out = np.zeros(x.shape, np.float64)
     for t in range(x.shape[0]):
@@ -107,7 +143,7 @@ def model(layer, x, k, idx, w, tab, split):
             g = (Wg[e].astype(np.float64) @ xa[t].astype(np.float64)).astype(np.float32)
             u = (Wu[e].astype(np.float64) @ xa[t].astype(np.float64)).astype(np.float32)
             bind.oracle().orc_swiglu(g.ctypes.data, u.ctypes.data, F, tab.ctypes.data)
-            h = g if split else bf16(g)
+            h = f16(g / 256) * 256 if h16 else g if split else bf16(g)
             y = Wd[e].astype(np.float64) @ h.astype(np.float64)
             if not split:
                 y = bf16(y.astype(np.float32)).astype(np.float64)  # stored as bf16 for the combine

@@ -53,6 +53,8 @@
 // extra MFMA work is hidden.
 #include "common.h"
 
+#include <type_traits>
+
 namespace tie {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -129,6 +131,7 @@ struct MfmaArgs {
 	const float *silu;
 	uint16_t *h16;           // gate/up out (bf16, by position)
 	uint16_t *h16lo;         // gate/up out, split mode: bf16 remainder plane
+	int h_f16;               // gate/up out: h as f16 * 2^-F16_SHIFT, pair-permuted K order (quantised down)
 	float *y;                // down out [pair][d] (BF16 weights: fp32)
 	uint16_t *y16;           // down out [pair][d] (quantised weights: bf16)
 };
@@ -137,9 +140,9 @@ template <int TYPE, bool DOWN = false, int MTR = 0> struct Cfg {
 	// pair rows per work tile at most (MTR: the small-tile gate/up kernel's)
 	static constexpr int MT = MTR ? MTR : DOWN ? MFMA_MT_DN : MFMA_MT_GU;
 	static constexpr bool SPLIT = TYPE == TIE_GGML_BF16; // bf16 weights take activations as hi + lo planes
-	// Q4_K gate/up: f16 operands (x as f16, K order inside each 8-group
-	// 0,2,1,3,4,6,5,7; weights scaled by 2^F16_SHIFT)
-	static constexpr bool F16 = TIE_MFMA_F16 && TYPE == TIE_GGML_Q4_K && !DOWN;
+	// Q4_K / Q6_K weights: f16 operands (activations as f16 with the K order
+	// inside each 8-group 0,2,1,3,4,6,5,7; weights scaled by 2^F16_SHIFT)
+	static constexpr bool F16 = TIE_MFMA_F16 && (TYPE == TIE_GGML_Q4_K || TYPE == TIE_GGML_Q6_K);
 	// K per stage (Q4_K optionally 64: one 64-weight group per stage)
 	static constexpr int KST = SPLIT ? 64
 				    : (TYPE == TIE_GGML_Q4_K ? TIE_Q4K_KST : TYPE == TIE_GGML_Q6_K ? TIE_Q6K_KST : 128);
@@ -434,13 +437,13 @@ __device__ __forceinline__ void group_factors16(const BRegs<TYPE> &b, int st, in
 // The masks and the magic live in VGPRs (K16): a GFX9 VOP3 instruction takes
 // no literal, so only then is each pair one v_and_or_b32.
 struct K16 {
-	uint32_t lo, hi, magic;
+	uint32_t lo, hi, magic, q6;
 };
 
 __device__ __forceinline__ K16 k16_consts()
 {
-	K16 k = {0x000f000fu, 0x00f000f0u, 0x64006400u};
-	asm volatile("" : "+v"(k.lo), "+v"(k.hi), "+v"(k.magic));
+	K16 k = {0x000f000fu, 0x00f000f0u, 0x64006400u, 0x003f003fu};
+	asm volatile("" : "+v"(k.lo), "+v"(k.hi), "+v"(k.magic), "+v"(k.q6));
 	return k;
 }
 
@@ -494,6 +497,34 @@ __device__ __forceinline__ void deq_step(const BRegs<TYPE> &b, const Fac &f, int
 			const float W = f.d6[j] * (float)(int8_t)((sw >> (8 * (si & 3))) & 0xffu);
 			out[j] = deq8(lo, hi, W, -32.0f * W);
 		}
+	}
+}
+
+// Q6_K step s in f16: the step's 8 six-bit codes of the lane's row (bytes of
+// lo, hi, as in deq_step) -> f16 pairs (K 0,2), (1,3), (4,6), (5,7): a code
+// in the mantissa of 1024.0, minus 1056 = code - 32 (exact), times
+// d * sc * 2^F16_SHIFT (v_pk_mul_f16, one rounding).
+__device__ __forceinline__ void deq_step16_q6k(const BRegs<TIE_GGML_Q6_K> &b, const Fac &f, const K16 &kc, int st, int s,
+					       f16x8 out[2])
+{
+	const f16x2 k1056 = {(_Float16)1056.0f, (_Float16)1056.0f};
+#pragma unroll
+	for (int j = 0; j < 2; j++) {
+		const int r = Cfg<TIE_GGML_Q6_K>::APERM ? (st & 1) + 2 * (s >> 1) : s >> 1, lh = s & 1;
+		const u32x2 ql = b.ql[j][Cfg<TIE_GGML_Q6_K>::APERM ? lh : 2 * (r & 1) + lh];
+		const u32x2 qh = b.qh[j][lh];
+		const int nsh = 4 * (r >> 1), hsh = 2 * r;
+		const uint32_t lo = ((ql.x >> nsh) & 0x0f0f0f0fu) | (((qh.x >> hsh) & 0x03030303u) << 4);
+		const uint32_t hi = ((ql.y >> nsh) & 0x0f0f0f0fu) | (((qh.y >> hsh) & 0x03030303u) << 4);
+		const int si = lh + 2 * r;
+		const uint32_t sw = si < 4 ? b.sc[j].x : b.sc[j].y;
+		const f16x2 D = splat16(f.d6[j] * (float)(int8_t)((sw >> (8 * (si & 3))) & 0xffu) * (float)(1 << F16_SHIFT));
+		const uint32_t w[4] = {lo, lo >> 8, hi, hi >> 8};
+		f16x2 q[4];
+#pragma unroll
+		for (int i = 0; i < 4; i++)
+			q[i] = (__builtin_bit_cast(f16x2, (w[i] & kc.q6) | kc.magic) - k1056) * D;
+		out[j] = f16x8{q[0][0], q[0][1], q[1][0], q[1][1], q[2][0], q[2][1], q[3][0], q[3][1]};
 	}
 }
 
@@ -592,11 +623,20 @@ template <int TYPE, bool DOWN> struct Ops<TYPE, DOWN, false> {
 };
 template <int TYPE, bool DOWN> struct Ops<TYPE, DOWN, true> {
 	using V = f16x8;
-	using F = Fac16;
-	__device__ static void factors(const BRegs<TYPE> &b, int st, int gi, F &f) { group_factors16<TYPE>(b, st, gi, f); }
-	__device__ static void deq(const BRegs<TYPE> &b, const F &f, const K16 &kc, int, int s, V out[2])
+	using F = typename std::conditional<TYPE == TIE_GGML_Q4_K, Fac16, Fac>::type;
+	__device__ static void factors(const BRegs<TYPE> &b, int st, int gi, F &f)
 	{
-		deq_step16(b, f, kc, s, out);
+		if constexpr (TYPE == TIE_GGML_Q4_K)
+			group_factors16<TYPE>(b, st, gi, f);
+		else
+			group_factors<TYPE>(b, st, gi, f);
+	}
+	__device__ static void deq(const BRegs<TYPE> &b, const F &f, const K16 &kc, int st, int s, V out[2])
+	{
+		if constexpr (TYPE == TIE_GGML_Q4_K)
+			deq_step16(b, f, kc, s, out);
+		else
+			deq_step16_q6k(b, f, kc, st, s, out);
 	}
 	__device__ static f32x16 mma(V a, V b, f32x16 c) { return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0); }
 };
@@ -863,10 +903,18 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 				const int col = slab * GU_COLS + 32 * w + (lane & 31);
 				constexpr float unscale = C::F16 ? 1.0f / (1 << F16_SHIFT) : 1.0f;
 				const float hv = tie_swiglu(acc[mt][0][i] * unscale, acc[mt][1][i] * unscale, silu);
-				const uint16_t hi = bf16_bits(hv);
-				a.h16[(size_t)p * a.rows + col] = hi;
-				if (C::SPLIT)
-					a.h16lo[(size_t)p * a.rows + col] = bf16_bits(hv - bf16_bits_to_float(hi));
+				if (a.h_f16) {
+					// f16 * 2^-F16_SHIFT (range), K positions 1, 2 (and 5, 6)
+					// of each 8-group swapped (the dequantised pairs' order)
+					const int pc = (col & ~3) | ((col & 1) << 1) | ((col >> 1) & 1);
+					a.h16[(size_t)p * a.rows + pc] =
+						__builtin_bit_cast(uint16_t, (_Float16)(hv * (1.0f / (1 << F16_SHIFT))));
+				} else {
+					const uint16_t hi = bf16_bits(hv);
+					a.h16[(size_t)p * a.rows + col] = hi;
+					if (C::SPLIT)
+						a.h16lo[(size_t)p * a.rows + col] = bf16_bits(hv - bf16_bits_to_float(hi));
+				}
 			} else if (C::SPLIT) {
 				float *yr = a.y + (size_t)a.pairs[p] * a.rows + slab * DN_COLS + 64 * w + (lane & 31);
 				yr[0] = acc[mt][0][i];
@@ -1058,6 +1106,7 @@ hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, con
 	a.silu = silu;
 	a.y = ws.y;
 	a.y16 = reinterpret_cast<uint16_t *>(ws.y);
+	a.h_f16 = TIE_MFMA_F16 && (L.down.type == TIE_GGML_Q4_K || L.down.type == TIE_GGML_Q6_K);
 	const int max_tiles = mfma_max_tiles(npairs, L.E);
 
 	prof_begin("mfma_gate_up", s);
@@ -1066,7 +1115,7 @@ hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, con
 		const dim3 g((unsigned)((n4 + 255) / 256 < 4096 ? (n4 + 255) / 256 : 4096));
 		if (split)
 			hipLaunchKernelGGL(to_split_kernel, g, dim3(256), 0, s, x, ws.xb, ws.xlo, n4);
-		else if (TIE_MFMA_F16 && L.gate.type == TIE_GGML_Q4_K)
+		else if (TIE_MFMA_F16 && (L.gate.type == TIE_GGML_Q4_K || L.gate.type == TIE_GGML_Q6_K))
 			hipLaunchKernelGGL(to_f16_kernel, g, dim3(256), 0, s, x, ws.xb, n4 / 2);
 		else
 			hipLaunchKernelGGL(to_bf16_kernel, g, dim3(256), 0, s, x, ws.xb, n4);
