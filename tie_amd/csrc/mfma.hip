@@ -5,7 +5,7 @@
 // weights across tokens.  For large T the pairs are grouped by expert
 // (dispatch.hip) and each expert's weights are dequantised once per work
 // tile and multiplied against all of the tile's tokens with
-// v_mfma_f32_32x32x16_bf16:
+// v_mfma_f32_32x32x16_f16 (Q4_K / Q6_K weights) or _bf16 (BF16 weights):
 //
 //   gate/up:  G = X_e Wg_e^T, U = X_e Wu_e^T, h = silu_tab(G) * U  (fused)
 //   down:     Y = h_e Wd_e^T, scattered to the pairs' rows of y
@@ -23,7 +23,7 @@
 //
 // Both operands are staged per K stage by direct global->LDS loads
 // (global_load_lds_dwordx4) into double-buffered LDS tiles, one stage
-// ahead: the activations (A, bf16 rows gathered by pair) and, for Q4_K /
+// ahead: the activations (A, 16-bit rows gathered by pair) and, for Q4_K /
 // Q6_K, the raw panel chunks of the workgroup's 4 weight panels (1 KiB
 // each: the panel layout of common.h).  Quantised stages are 64 K: a Q4_K
 // stage is one 64-weight group (scale chunk + 2 quant chunks); a Q6_K stage
@@ -33,24 +33,28 @@
 // match.  Small stages and tiles keep a workgroup at about 64-75 KiB of LDS
 // and 256 registers per lane: two workgroups share a CU (two waves per
 // SIMD), so one's stalls and pipeline fill / drain overlap the other's
-// MFMAs.  No register holds a prefetched stage, and the compiler's
+// MFMAs (the small-tile gate/up kernel: 40 KiB, 128 registers, three).  No register holds a prefetched stage, and the compiler's
 // wait-count pass never sees (and never waits for) the prefetch: the stage
 // barrier is the wait.  In the 32x32x16 B-operand layout a lane holds 8
 // consecutive K values of one weight row -- 8 consecutive quant bytes of
 // its lane-row in the panel -- which it reads from LDS and dequantises
 // between the MFMAs: every weight of the tile is dequantised exactly once,
-// and each B fragment feeds one MFMA per 32-row M tile.  BF16 weights
+// and each B fragment feeds one MFMA per 32-row M tile (an f16 lane holds
+// the pairs (0,2), (1,3), (4,6), (5,7) of those 8).  BF16 weights
 // (already MFMA operands) are prefetched into registers instead (one wave
 // per SIMD, 64-K stages).  An A fragment (1 KiB) feeds two MFMAs.
 //
-// Numerics: fp32 accumulation of bf16 products.  Q4_K/Q6_K weights are
-// dequantised in fp32 (fma(q, d*sc, -dmin*m); d*sc*(q-32), both as TIE's
-// dequantisation) then rounded to bf16; activations are rounded to bf16.
-// With BF16 expert weights (exact in bf16) the activations are split into a
-// bf16 high part and a bf16 remainder, stored as two bf16 planes (x by
-// to_split_kernel, h by the gate/up epilogue), two MFMAs per product; this
-// keeps the products to ~16 mantissa bits; that path is HBM-bound, so the
-// extra MFMA work is hidden.
+// Numerics: fp32 accumulation of 16-bit products.  Q4_K / Q6_K weights are
+// dequantised with packed f16 math (code in the mantissa of 1024.0, exact
+// subtraction, one v_pk_fma_f16 / v_pk_mul_f16 rounding) and carry a factor
+// 2^F16_SHIFT; x is rounded to f16, h is stored as f16 * 2^-F16_SHIFT, both
+// with the K order inside each 8-group 0,2,1,3,4,6,5,7 (the dequantised
+// pairs' order).  The expert outputs y are stored as bf16.  With BF16 expert
+// weights (exact in bf16) the activations are split into a bf16 high part
+// and a bf16 remainder, stored as two bf16 planes (x by to_split_kernel, h
+// by the gate/up epilogue), two MFMAs per product; this keeps the products
+// to ~16 mantissa bits; that path is HBM-bound, so the extra MFMA work is
+// hidden, and its y stays fp32.
 #include "common.h"
 
 #include <type_traits>
