@@ -410,7 +410,7 @@ __device__ __forceinline__ void group_factors(const BRegs<TYPE> &b, int st, int 
 constexpr int F16_SHIFT = 8;
 
 struct Fac16 {
-	f16x2 D[2][2], M[2][2]; // [row][sub-block]: D * 2^S (low nibbles) or D * 2^(S-4) (high), M * 2^S
+	f16x2 DM[2][2]; // [row][sub-block]: (D * 2^S or D * 2^(S-4) for the high nibbles, M * 2^S)
 };
 
 __device__ __forceinline__ f16x2 splat16(float v)
@@ -419,25 +419,29 @@ __device__ __forceinline__ f16x2 splat16(float v)
 	return f16x2{h, h};
 }
 
+// In packed f16: (d, dmin) * (2^S, -2^S) (exact), the sub-block's 6-bit
+// (sc, m) as f16 (in the mantissa of 1024.0, minus 1024), then one product:
+// (d*sc*2^S, -dmin*m*2^S), each rounded once from its exact value -- the
+// same f16 values as rounding the fp32 D and M.
 template <int TYPE>
 __device__ __forceinline__ void group_factors16(const BRegs<TYPE> &b, int st, int gi, Fac16 &f)
 {
-	Fac g;
-	group_factors<TYPE>(b, st, gi, g);
+	const f16x2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+	const f16x2 s0 = {(_Float16)(float)(1 << F16_SHIFT), (_Float16)(-(float)(1 << F16_SHIFT))};
+	const f16x2 s1 = {(_Float16)(float)(1 << (F16_SHIFT - 4)), (_Float16)(-(float)(1 << F16_SHIFT))};
 #pragma unroll
 	for (int j = 0; j < 2; j++) {
-		f.D[j][0] = splat16(g.D[j][0] * (float)(1 << F16_SHIFT));
-		f.D[j][1] = splat16(g.D[j][1] * (float)(1 << (F16_SHIFT - 4)));
-		f.M[j][0] = splat16(g.M[j][0] * (float)(1 << F16_SHIFT));
-		f.M[j][1] = splat16(g.M[j][1] * (float)(1 << F16_SHIFT));
+		const int g = (4 / Cfg<TYPE>::SPB) * (st % Cfg<TYPE>::SPB) + gi;
+		const f16x2 dd = __builtin_bit_cast(f16x2, b.sc[j].x);
+#pragma unroll
+		for (int u = 0; u < 2; u++) {
+			uint32_t sc, mn;
+			q4k_scale_min(b.sc[j], 2 * g + u, sc, mn);
+			const f16x2 sm = __builtin_bit_cast(f16x2, (sc | (mn << 16)) | 0x64006400u) - k1024;
+			f.DM[j][u] = sm * (dd * (u ? s1 : s0));
+		}
 	}
 }
-
-// Q4_K step s in f16: 8 weight codes of the lane's row (bytes of q.x, q.y,
-// low or high nibbles) -> f16 pairs (K 0,2), (1,3), (4,6), (5,7).  A code
-// lands in the mantissa of 1024.0 (0x6400): as q (low nibble, bits 0-3) or
-// 16 q (high nibble, bits 4-7); subtracting 1024 is exact, then one packed
-// fma applies the scale and offset (v_pk_fma_f16, one rounding).
 // The masks and the magic live in VGPRs (K16): a GFX9 VOP3 instruction takes
 // no literal, so only then is each pair one v_and_or_b32.
 struct K16 {
@@ -465,7 +469,8 @@ __device__ __forceinline__ void deq_step16(const BRegs<TIE_GGML_Q4_K> &b, const 
 #pragma unroll
 		for (int i = 0; i < 4; i++) {
 			const f16x2 v = __builtin_bit_cast(f16x2, (w[i] & msk) | kc.magic) - k1024;
-			r[i] = __builtin_elementwise_fma(v, f.D[j][u], f.M[j][u]);
+			const f16x2 dm = f.DM[j][u];
+			r[i] = __builtin_elementwise_fma(v, f16x2{dm[0], dm[0]}, f16x2{dm[1], dm[1]});
 		}
 		out[j] = f16x8{r[0][0], r[0][1], r[1][0], r[1][1], r[2][0], r[2][1], r[3][0], r[3][1]};
 	}
