@@ -41,7 +41,7 @@ extern "C" {
 #define TIE_SILU_TABLE_SIZE 8192 /* SILU_TABLE_SIZE, engine.h:10 */
 
 /* Forward flags */
-#define TIE_HIP_PATH_AUTO 0x0  /* exact fp32 GEMV path for small T, bf16 MFMA grouped GEMM above */
+#define TIE_HIP_PATH_AUTO 0x0  /* exact fp32 GEMV path for small T, 16-bit MFMA grouped GEMM above */
 #define TIE_HIP_PATH_EXACT 0x1 /* always the fp32 path that reproduces TIE's arithmetic bit for bit */
 #define TIE_HIP_PATH_MFMA 0x2  /* always the grouped-GEMM path */
 
