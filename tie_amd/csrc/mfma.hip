@@ -1116,7 +1116,12 @@ hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, con
 	a.y = ws.y;
 	a.y16 = reinterpret_cast<uint16_t *>(ws.y);
 	a.h_f16 = TIE_MFMA_F16 && (L.down.type == TIE_GGML_Q4_K || L.down.type == TIE_GGML_Q6_K);
-	const int max_tiles = mfma_max_tiles(npairs, L.E);
+	// grid rows: each list's tile bound for its own tile rows, plus 8 rows:
+	// the XCD remap in the kernel reaches every live item only with at least
+	// 8 * ceil(live / 8) workgroups (rows past the list exit at once)
+	const int mt_gu = mfma_gu_rows(L, npairs);
+	const int gu_tiles = (npairs + mt_gu - 1) / mt_gu + L.E + 8;
+	const int dn_tiles = (npairs + MFMA_MT_DN - 1) / MFMA_MT_DN + L.E + 8;
 
 	prof_begin("mfma_gate_up", s);
 	{
@@ -1139,8 +1144,7 @@ hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, con
 	a.a16lo = ws.xlo;
 	a.h16 = ws.hb;
 	a.h16lo = ws.hlo;
-	hipError_t err = launch_one<false>(a, L.gate.type, dim3(L.F / GU_COLS, max_tiles), s,
-					   mfma_gu_rows(L, npairs) == MFMA_MT_GU_SMALL);
+	hipError_t err = launch_one<false>(a, L.gate.type, dim3(L.F / GU_COLS, gu_tiles), s, mt_gu == MFMA_MT_GU_SMALL);
 	prof_end(s);
 	if (err != hipSuccess)
 		return err;
@@ -1160,7 +1164,7 @@ hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, con
 		prof_end(s);
 		return hipErrorInvalidValue; // h has no remainder plane for the split down path
 	}
-	err = launch_one<true>(a, L.down.type, dim3(L.d / DN_COLS, max_tiles), s);
+	err = launch_one<true>(a, L.down.type, dim3(L.d / DN_COLS, dn_tiles), s);
 	prof_end(s);
 	return err;
 }
