@@ -46,7 +46,9 @@ def block_kernel(name):
     """Block kernel a rocprof kernel name belongs to (None: set-up or foreign)."""
     base = name.replace("void ", "").split("(")[0]
     if base.startswith("tie::mfma_experts_kernel"):
-        return "mfma_down" if "true>" in base else "mfma_gate_up"
+        # template arguments <type, down, tile rows>
+        args = base[base.index("<") + 1:base.rindex(">")].split(",")
+        return "mfma_down" if args[1].strip() == "true" else "mfma_gate_up"
     for prefix, block in _NAMES:
         if base == prefix or base.startswith(prefix + "<"):
             return block
