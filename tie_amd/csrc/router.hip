@@ -135,6 +135,10 @@ constexpr int RT_WBYTES = RT_KC * RT_EXP * 4;   // W^T chunk (16 KiB)
 constexpr int RT_XBYTES = RT_TOK * RT_KC * 4;   // x chunk (8 KiB)
 constexpr int RT_BUF = RT_WBYTES + RT_XBYTES;
 constexpr int RT_LDS = 2 * RT_BUF;              // double-buffered (48 KiB: three workgroups per CU)
+#ifndef TIE_RT_IB
+#define TIE_RT_IB 16
+#endif
+constexpr int RT_IB = TIE_RT_IB;                // K steps whose operands are read ahead
 
 __device__ __forceinline__ uint32_t rt_lds_addr(const void *p)
 {
@@ -205,16 +209,27 @@ __global__ __launch_bounds__(RT_THREADS) void router_logits_kernel(const float *
 			rt_dma_chunk(x, WT, E, d, t0, e0, nt, (c + 1) * RT_KC, rt_lds + ((c + 1) & 1) * RT_BUF);
 		const float *ws = reinterpret_cast<const float *>(rt_lds + (c & 1) * RT_BUF);
 		const float *xs = reinterpret_cast<const float *>(rt_lds + (c & 1) * RT_BUF + RT_WBYTES);
-#pragma unroll 8
-		for (int i = 0; i < RT_KC / 8; i++) {
-			const float4 w4 = *reinterpret_cast<const float4 *>(ws + (8 * i + l) * RT_EXP + wcol);
+		// operands of RT_IB K steps read into registers first (their LDS
+		// latencies overlap), then the FMAs in K order
+		for (int i0 = 0; i0 < RT_KC / 8; i0 += RT_IB) {
+			float4 w4[RT_IB];
+			float xv[RT_IB][RT_TPT];
 #pragma unroll
-			for (int a = 0; a < RT_TPT; a++) {
-				const float xv = xs[xo + a * RT_KC + 8 * i];
-				acc[a][0] = __builtin_fmaf(xv, w4.x, acc[a][0]);
-				acc[a][1] = __builtin_fmaf(xv, w4.y, acc[a][1]);
-				acc[a][2] = __builtin_fmaf(xv, w4.z, acc[a][2]);
-				acc[a][3] = __builtin_fmaf(xv, w4.w, acc[a][3]);
+			for (int j = 0; j < RT_IB; j++) {
+				w4[j] = *reinterpret_cast<const float4 *>(ws + (8 * (i0 + j) + l) * RT_EXP + wcol);
+#pragma unroll
+				for (int a = 0; a < RT_TPT; a++)
+					xv[j][a] = xs[xo + a * RT_KC + 8 * (i0 + j)];
+			}
+#pragma unroll
+			for (int j = 0; j < RT_IB; j++) {
+#pragma unroll
+				for (int a = 0; a < RT_TPT; a++) {
+					acc[a][0] = __builtin_fmaf(xv[j][a], w4[j].x, acc[a][0]);
+					acc[a][1] = __builtin_fmaf(xv[j][a], w4[j].y, acc[a][1]);
+					acc[a][2] = __builtin_fmaf(xv[j][a], w4[j].z, acc[a][2]);
+					acc[a][3] = __builtin_fmaf(xv[j][a], w4[j].w, acc[a][3]);
+				}
 			}
 		}
 		rt_barrier();
