@@ -139,6 +139,10 @@ constexpr int RT_LDS = 2 * RT_BUF;              // double-buffered (48 KiB: thre
 #define TIE_RT_IB 16
 #endif
 constexpr int RT_IB = TIE_RT_IB;                // K steps whose operands are read ahead
+// the tiled kernel above this many tokens (below: router_mid)
+#ifndef TIE_RT_MIN_T
+#define TIE_RT_MIN_T 256
+#endif
 
 __device__ __forceinline__ uint32_t rt_lds_addr(const void *p)
 {
@@ -306,7 +310,7 @@ hipError_t launch_router_logits(const Layer &L, const float *x, int T, float *lo
 	}
 	// the tiled kernel above 256 tokens: below that its one chunk in flight
 	// per K step leaves it waiting on memory, and router_mid is faster
-	if (T > 256 && E % RT_EXP == 0 && d % RT_KC == 0 && L.routerT) {
+	if (T > TIE_RT_MIN_T && E % RT_EXP == 0 && d % RT_KC == 0 && L.routerT) {
 		static bool attr = false;
 		if (!attr) {
 			const hipError_t err = hipFuncSetAttribute((const void *)router_logits_kernel,
