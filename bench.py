@@ -77,14 +77,21 @@ def gen_device_layer(torch, cfg, seed):
 
 class Workload:
     def __init__(self, torch, tie_amd, cfg, n_layers, seed0=4242):
+        from tie_amd import synth
         self.cfg = cfg
         self.layers = []
         self.layer_bytes = 0
+        self.host_layer0 = None  # layer 0's GGUF-layout tensors on the host (the CPU leg's weights)
         for i in range(n_layers):
             r, g, u, dn, b, pb = gen_device_layer(torch, cfg, seed0 + 17 * i)
             L = tie_amd.Layer(cfg["d"], cfg["F"], cfg["E"], r, g, u, dn, cfg["gu_type"], cfg["gu_type"],
                               cfg["down_type"], bias=b, on_device=True, routing=cfg.get("routing", 0),
                               probs_bias=pb)
+            if i == 0:
+                host = lambda t: None if t is None else t.cpu().numpy()  # noqa: E731
+                self.host_layer0 = synth.MoELayer(cfg["d"], cfg["F"], cfg["E"], host(g), host(u), host(dn),
+                                                  host(r), cfg["gu_type"], cfg["down_type"], host(b),
+                                                  cfg.get("routing", 0), host(pb))
             self.layer_bytes = L.nbytes()
             self.layers.append(L)
             del r, g, u, dn
@@ -154,6 +161,7 @@ def expert_bytes(cfg):
 def run_config(torch, tie_amd, wl, T, k, steps, warmup, flags, cfg=None):
     """Times `steps` forwards of T tokens; returns the measurement dict.
     cfg: the workload config (default: the one the layers were made for)."""
+    from tie_amd import synth
     cfg = cfg or wl.cfg
     d, F, E = cfg["d"], cfg["F"], cfg["E"]
     nL = len(wl.layers)
@@ -168,7 +176,6 @@ def run_config(torch, tie_amd, wl, T, k, steps, warmup, flags, cfg=None):
     if residual:
         # the FFN half of the layer: out = X[l] + block(rms_norm(X[l])) (out
         # of place, so every step sees the same inputs)
-        from tie_amd import synth
         norm = torch.from_numpy(synth.make_norm_weight(cfg["seed"], d)).cuda()
 
     def step(s, record_topk=False):
@@ -182,6 +189,12 @@ def run_config(torch, tie_amd, wl, T, k, steps, warmup, flags, cfg=None):
 
     for s in range(nL):  # routing of every (layer, batch) pair, for the byte counts
         step(s, record_topk=True)
+    torch.cuda.synchronize()
+    # layer 0 on batch 0: the outputs the parity check compares with TIE's
+    # CPU path (step 0 wrote them last for layer 0 only when nL == 1)
+    step(0, record_topk=True)
+    torch.cuda.synchronize()
+    gpu_out0 = (X[0].cpu().numpy(), out.cpu().numpy(), idx[0].cpu().numpy(), w[0].cpu().numpy())
     for s in range(warmup):
         step(s)
     torch.cuda.synchronize()
@@ -204,21 +217,27 @@ def run_config(torch, tie_amd, wl, T, k, steps, warmup, flags, cfg=None):
     U_avg = float(np.mean([U[s % nL] for s in range(steps)]))
     gu_b, dn_b = expert_bytes(cfg)
     pairs = T * k
+    y_bytes = 2 if cfg["down_type"] != synth.BF16 else 4  # the MFMA path's y: bf16 with quantised weights
+    h_bytes = 2 if cfg["down_type"] != synth.BF16 else 4  # h: f16 (quantised down) or bf16 hi + lo
     kern_bytes = {
         "router": E * d * 4 + T * d * 4,
         "exact_gate_up": U_avg * gu_b + T * d * 4 + pairs * F * 4,
         "exact_down": U_avg * dn_b + pairs * F * 4 + pairs * d * 4,
+        "decode_gate_up": U_avg * gu_b + T * d * 4 + pairs * F * 4,
+        "decode_down": U_avg * dn_b + pairs * F * 4 + T * d * 4 * (2 if residual else 1),
         "combine": pairs * d * 4 + T * d * 4 * (3 if residual else 1),
         "rmsnorm": 2 * T * d * 4 + d * 4,
         "dispatch": pairs * 4 * 2,
-        "mfma_gate_up": U_avg * gu_b + T * d * 4 + pairs * F * 2,
-        "mfma_down": U_avg * dn_b + pairs * F * 2 + pairs * d * 4,
+        "mfma_gate_up": U_avg * gu_b + T * d * 4 + pairs * F * h_bytes,
+        "mfma_down": U_avg * dn_b + pairs * F * h_bytes + pairs * d * y_bytes,
     }
     kern_flops = {
         "mfma_gate_up": 2.0 * pairs * 2 * F * d,
         "mfma_down": 2.0 * pairs * F * d,
         "exact_gate_up": 2.0 * pairs * 2 * F * d,
         "exact_down": 2.0 * pairs * F * d,
+        "decode_gate_up": 2.0 * pairs * 2 * F * d,
+        "decode_down": 2.0 * pairs * F * d,
         "router": 2.0 * T * E * d,
     }
     block_bytes = E * d * 4 + U_avg * (gu_b + dn_b) + 2 * T * d * 4
@@ -235,7 +254,7 @@ def run_config(torch, tie_amd, wl, T, k, steps, warmup, flags, cfg=None):
                          "alg_flops": kf, "TFLOPs": round(kf / (avg_ms * 1e-3) / 1e12, 2) if kf else None}
     return dict(T=T, k=k, ms=ms, tokens_per_s=T / (ms * 1e-3), U=U_avg, block_bytes=block_bytes,
                 block_flops=block_flops, block_GBps=block_bytes / (ms * 1e-3) / 1e9,
-                block_TFLOPs=block_flops / (ms * 1e-3) / 1e12, kernels=kernels, layers=nL)
+                block_TFLOPs=block_flops / (ms * 1e-3) / 1e12, kernels=kernels, layers=nL, gpu_out0=gpu_out0)
 
 
 def roofline(m, config):
@@ -276,21 +295,40 @@ def cpu_has(flag):
     return False
 
 
-def cpu_baseline(cfg, k, budget_s=12.0):
-    """TIE's MoE path on the host cores: the reference's own sources compiled
-    (oracle/_ref, kind "reference") when its build can run on this CPU,
-    otherwise the C restatement (oracle/liboracle.so, kind "port")."""
+def cpu_pool_threads():
+    """TIE's thread-pool size for the CPU leg: min(nproc, 32), at least k = 8
+    (model_qwen3.c:413 indexes tasks[num_threads] by slot), and no more than
+    this process's CPU share (OMP_NUM_THREADS, which the GPU box sets to it)."""
+    try:
+        nproc = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        nproc = os.cpu_count() or 8
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or nproc
+    return max(8, min(nproc, share, 32)), nproc
+
+
+def cpu_baseline(cfg, layer, x_gpu, gpu, budget_s):
+    """TIE's MoE path on the host cores (the reference's own sources compiled,
+    oracle/_ref, kind "reference", when its build runs on this CPU; else the
+    C restatement, kind "port") on layer 0 of the GPU workload and a sample
+    of the GPU's batch-0 tokens: tokens/s over ~budget_s, and the parity of
+    the GPU's outputs for those tokens (from the same forward over the full
+    batch) against TIE's:
+      routing_mismatch  tokens whose selected experts differ, outside near ties
+      near_ties         tokens whose 8th and 9th logits differ by < 1e-5
+      max_abs, rel_l2   over the sampled output rows."""
     from oracle import bind
     from tie_amd import synth
-    layer = synth.make_layer(cfg["seed"], cfg["d"], cfg["F"], cfg["E"], cfg["gu_type"], cfg["down_type"],
-                             zipf=cfg.get("zipf"), routing=cfg.get("routing", 0),
-                             probs_bias=cfg.get("probs_bias"))
-    T = min(cfg["T"], 32)
-    x = synth.make_input(cfg["seed"], T, cfg["d"])
-    threads = 8  # TIE runs the k = 8 experts of a token as 8 pool tasks (model_qwen3.c:446-456)
+    k = cfg["k"]
+    T = cfg["T"]
+    S = min(T, 32 if cfg["d"] <= 2048 else 16)
+    # evenly spaced sample of the batch (the MFMA path groups all T tokens)
+    rows = np.unique(np.linspace(0, T - 1, S).round().astype(int))
+    xs = np.ascontiguousarray(x_gpu[rows])
+    threads, nproc = cpu_pool_threads()
     use_ref = bind.ref_available() and cpu_has("avx512f") and cpu_has("avx2")
-    fn = (lambda: bind.ref_moe_block(layer, x, k, nthreads=threads)) if use_ref else \
-        (lambda: bind.moe_block(layer, x, k, nthreads=threads))
+    fn = (lambda: bind.ref_moe_block(layer, xs, k, nthreads=threads, with_logits=True)) if use_ref else \
+        (lambda: bind.moe_block(layer, xs, k, nthreads=threads, with_logits=True))
     # the reference prints progress on stdout (math_dispatch.c:657): send
     # the C-level stdout to stderr meanwhile, so that stdout carries only the
     # result line
@@ -298,7 +336,7 @@ def cpu_baseline(cfg, k, budget_s=12.0):
     saved = os.dup(1)
     os.dup2(2, 1)
     try:
-        fn()  # warm-up (also builds the reference's thread pool)
+        ro, ri, rw, lg = fn()  # warm-up (also builds the reference's thread pool); its outputs are checked
         n, t0 = 0, time.perf_counter()
         while True:
             fn()
@@ -309,10 +347,23 @@ def cpu_baseline(cfg, k, budget_s=12.0):
     finally:
         os.dup2(saved, 1)
         os.close(saved)
-    return {"value": round(n * T / el, 2), "unit": "tokens/s", "cores": threads,
+    g_out, g_idx, g_w = gpu
+    g_out, g_idx = g_out[rows], g_idx[rows]
+    srt = -np.sort(-lg, axis=1)
+    near = np.abs(srt[:, k - 1] - srt[:, k]) < 1e-5 if lg.shape[1] > k else np.zeros(len(rows), bool)
+    differ = (g_idx != ri).any(axis=1)
+    err = np.abs(g_out.astype(np.float64) - ro)
+    parity = {"tokens": int(len(rows)), "routing_mismatch": int((differ & ~near).sum()),
+              "near_ties": int(near.sum()), "near_tie_mismatch": int((differ & near).sum()),
+              "max_abs": float(err.max()), "max_ref": float(np.abs(ro).max()),
+              "rel_l2": float(np.linalg.norm(err) / max(np.linalg.norm(ro), 1e-30)),
+              "against": "reference" if use_ref else "port"}
+    base = {"value": round(n * len(rows) / el, 2), "unit": "tokens/s", "cores": threads,
             "kind": "reference" if use_ref else "port",
-            "sample": "%d calls of T=%d tokens (%s weights, one layer) in %.1f s on %d host threads; nproc=%d" % (
-                n, T, synth.TYPE_NAMES[cfg["gu_type"]], el, threads, os.cpu_count() or 0)}
+            "sample": "%d calls of %d tokens (rows of the GPU batch; %s weights, layer 0 of the GPU workload) in "
+                      "%.1f s on a %d-thread pool; nproc=%d" % (n, len(rows), synth.TYPE_NAMES[cfg["gu_type"]],
+                                                               el, threads, nproc)}
+    return base, parity
 
 
 # ---------------------------------------------------------------- main
@@ -322,7 +373,9 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="30b_t32")
-    ap.add_argument("--extra", default="30b_t1,30b_t2048")
+    ap.add_argument("--extra", default="30b_t1,30b_t2048,30b_bf16_zipf_t512,235b_t1,235b_t1024")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="CPU-leg timing budget of the headline workload (the others get half)")
     ap.add_argument("--layers", type=int, default=0, help="weight layers cycled (0 = auto)")
     ap.add_argument("--path", default="auto", choices=["auto", "exact", "mfma"])
     ap.add_argument("--no-cpu", action="store_true")
@@ -354,6 +407,7 @@ def main():
     names = [args.config] + [c for c in args.extra.split(",") if c and c not in (args.config, "none")]
     workloads = {}
     results = {}
+    gpu_outs = {}
     for name in names:
         cfg = dict(synth.CONFIGS[name])
         if cfg.get("kind") == "dense":
@@ -375,23 +429,35 @@ def main():
         warm = args.warmup if name == args.config else max(2, args.warmup // 4)
         log("timing %s: T=%d, %d warm-up + %d steps" % (name, cfg["T"], warm, steps))
         results[name] = run_config(torch, tie_amd, workloads[key], cfg["T"], cfg["k"], steps, warm, flags, cfg)
+        gpu_outs[name] = (key, results[name].pop("gpu_out0"))
         log(json.dumps({name: results[name]}))
+
+    # CPU legs (TIE's path on the host cores, same weights and tokens) and
+    # the parity of the GPU outputs against it, per workload
+    cpu, parity = {}, {}
+    for name in names:
+        cfg = synth.CONFIGS[name]
+        if args.no_cpu or name not in gpu_outs or cfg.get("residual"):
+            cpu[name], parity[name] = None, None
+            continue
+        key, (x0, out0, idx0, w0) = gpu_outs[name]
+        budget = args.cpu_seconds if name == args.config else args.cpu_seconds / 2
+        log("cpu baseline %s ..." % name)
+        cpu[name], parity[name] = cpu_baseline(cfg, workloads[key].host_layer0, x0, (out0, idx0, w0), budget)
+        log(json.dumps({name: {"cpu_baseline": cpu[name], "parity": parity[name]}}))
 
     main_name = args.config
     m = results[main_name]
     cfg = synth.CONFIGS[main_name]
-    cpu = None
-    if not args.no_cpu:
-        log("cpu baseline ...")
-        cpu = cpu_baseline(cfg, cfg["k"])
     extra = {}
     for name in names[1:]:
         r = results[name]
         extra[name] = {"tokens_per_s": round(r["tokens_per_s"], 1), "ms_per_step": round(r["ms"], 4),
                        "block_GBps": round(r["block_GBps"], 1), "block_TFLOPs": round(r["block_TFLOPs"], 3),
-                       "roofline": roofline(r, name), "kernels": r["kernels"]}
+                       "roofline": roofline(r, name), "cpu_baseline": cpu.get(name), "parity": parity.get(name),
+                       "kernels": r["kernels"]}
     line = {
-        "metric": "MoE block tokens/s (Qwen3-30B-A3B shape)",
+        "metric": "MoE block tokens/s; HBM GB/s at T=1, MFMA TFLOP/s at T=2048 (30B-A3B)",
         "value": round(m["tokens_per_s"], 1),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -401,14 +467,15 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16" if any(k.startswith("mfma") for k in m["kernels"]) else "f32",
+        "dtype": "f16" if any(k.startswith("mfma") for k in m["kernels"]) else "f32",
         "data": "synthetic (seeded GGUF-layout Q4_K/Q6_K blocks, N(0,1) inputs; %d weight layers cycled)" % m[
             "layers"],
         "config": {"workload": "%s: d=%d F=%d E=%d k=%d T=%d, gate/up %s, down %s" % (
             main_name, cfg["d"], cfg["F"], cfg["E"], cfg["k"], cfg["T"], synth.TYPE_NAMES[cfg["gu_type"]],
             synth.TYPE_NAMES[cfg["down_type"]]), "T": cfg["T"], "path": args.path},
         "roofline": roofline(m, main_name),
-        "cpu_baseline": cpu,
+        "cpu_baseline": cpu.get(main_name),
+        "parity": parity.get(main_name),
         "block_GBps": round(m["block_GBps"], 1),
         "distinct_experts_per_step": round(m["U"], 2),
         "kernels": m["kernels"],

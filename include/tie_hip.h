@@ -148,7 +148,15 @@ size_t tie_hip_layer_bytes(const tie_hip_layer *layer);
 
 /* MoE block on device pointers, enqueued on `stream` (a hipStream_t; NULL =
  * the library stream).  x_dev/out_dev are [T][d] F32; topk outputs are
- * optional [T][k].  Returns once enqueued; the caller synchronises. */
+ * optional [T][k].  Returns once enqueued; the caller synchronises.
+ *
+ * Streams: the library keeps one scratch workspace per stream, so forwards
+ * enqueued on different streams never share scratch memory and may run
+ * concurrently (on distinct out buffers).  Forwards on one stream are
+ * ordered by that stream.  When a call needs a larger workspace than its
+ * stream holds, the library drains the whole device (hipDeviceSynchronize)
+ * before freeing the old one; a call made during HIP graph capture must
+ * therefore not grow it (warm the stream up with the largest T first). */
 int tie_hip_moe_forward(tie_hip_layer *layer, const float *x_dev, int T, int k, float *out_dev,
 			int32_t *topk_idx_dev, float *topk_w_dev, int flags, void *stream);
 

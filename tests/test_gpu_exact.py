@@ -27,6 +27,17 @@ def device():
     tie_amd.shutdown()
 
 
+def golden_host_check(g):
+    """Whether this host can compare against the golden outputs directly (its
+    CPU builds the same SiLU / RSQRTSS tables as the one that made them);
+    printed either way, so the log says which comparison ran."""
+    here, made = host_cpu_identity(), str(g["cpu"])
+    same = here == made
+    print("golden outputs %s (host %s, vectors from %s)" % ("compared" if same else "skipped: other CPU", here, made),
+          flush=True)
+    return same
+
+
 def assert_same(got, want, what):
     g, w = np.ascontiguousarray(got), np.ascontiguousarray(want)
     if g.dtype == np.float32:
@@ -62,7 +73,7 @@ def test_golden_cases(name):
     out, idx, w = run_both(layer, g["x"], int(g["k"]))
     assert_same(idx, g["topk_idx"], "golden topk_idx")
     assert_same(w, g["topk_w"], "golden topk_w")
-    if str(g["cpu"]) == host_cpu_identity():
+    if golden_host_check(g):
         assert_same(out, g["out"], "golden out")
 
 
@@ -77,7 +88,7 @@ def test_lfm2_golden_cases(name):
     out, idx, w = run_both(layer, g["x"], int(g["k"]))
     assert_same(idx, g["topk_idx"], "golden topk_idx")
     np.testing.assert_allclose(w, g["topk_w"], rtol=1e-6, atol=0)
-    if str(g["cpu"]) == host_cpu_identity():
+    if golden_host_check(g):
         assert np.abs(out - g["out"]).max() <= 1e-6 * np.abs(g["out"]).max()
 
 
@@ -127,7 +138,7 @@ def test_qwen3_ffn_residual(name):
     assert_same(idx, ri, "topk_idx")
     assert_same(w, rw, "topk_w")
     assert_same(h, rh, "hidden")
-    if str(g["cpu"]) == host_cpu_identity():
+    if golden_host_check(g):
         assert_same(h, g["hidden_out"], "golden hidden")
 
 
@@ -163,7 +174,7 @@ def test_qwen3_ffn_residual_device(T, flags):
         d_got, d_want = got - hidden, rh - hidden  # the block's contribution
         e = float(np.linalg.norm(d_got - d_want) / np.linalg.norm(d_want))
         print("residual MFMA rel L2 of the block output %.3g" % e, flush=True)
-        assert e <= 2e-2
+        assert e <= 4e-3
     else:
         assert_same(got, rh, "hidden")
     L.close()
@@ -331,3 +342,70 @@ def test_gguf_model_load(tmp_path):
     assert_same(w.cpu().numpy(), rw, "lfm2 topk_w")
     assert_same(out.cpu().numpy(), ro, "lfm2 out")
     M.close()
+
+
+def test_one_token_nan_row_and_residual():
+    """One token (the decode kernels): a NaN input selects no expert (output
+    0); the residual form at T = 1 in place and out of place."""
+    import torch
+    layer = synth_layer(23, 2048, 768, 128, synth.Q4_K, synth.Q6_K, None)
+    x = synth.make_input(27, 1, 2048)
+    x[0, 11] = np.nan
+    out, idx, w = tie_amd.moe_ffn(x, layer, 8)
+    ro, ri, rw = bind.moe_block(layer, x, 8)
+    assert_same(idx, ri, "topk_idx")
+    assert (idx == -1).all() and (out == 0).all() and (ro == 0).all()
+    hidden = synth.make_input(28, 1, 2048) * np.float32(2.0)
+    norm = synth.make_norm_weight(28, 2048)
+    rh, ri, rw = bind.qwen3_ffn(layer, hidden, 8, norm, 1e-6)
+    L = tie_amd.Layer.from_synth(layer)
+    hd = torch.from_numpy(hidden).cuda()
+    nd = torch.from_numpy(norm).cuda()
+    hout = torch.empty_like(hd)
+    idx_d = torch.empty((1, 8), dtype=torch.int32, device="cuda")
+    w_d = torch.empty((1, 8), dtype=torch.float32, device="cuda")
+    L.forward_residual(hd, nd, 1e-6, 1, 8, hout, idx_d, w_d)
+    L.forward_residual(hd, nd, 1e-6, 1, 8)  # in place
+    torch.cuda.synchronize()
+    assert_same(idx_d.cpu().numpy(), ri, "topk_idx")
+    assert_same(w_d.cpu().numpy(), rw, "topk_w")
+    assert_same(hout.cpu().numpy(), rh, "out of place")
+    assert_same(hd.cpu().numpy(), rh, "in place")
+    L.close()
+
+
+def test_workspace_per_caller_stream():
+    """Forwards on two caller streams (not the library's), each growing its
+    own workspace while the other stream's work may still be in flight:
+    every result equals the oracle.  (Each stream keeps its own scratch;
+    growing one drains the device before the old buffer is freed.)"""
+    import torch
+    layer = synth_layer(29, 512, 512, 16, synth.Q4_K, synth.Q6_K, None)
+    L = tie_amd.Layer.from_synth(layer)
+    k = 4
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    cases = []
+    for i, T in enumerate([3, 40, 150, 1, 300, 9]):  # growing and shrinking T per stream
+        s = streams[i % 2]
+        x = synth.make_input(29 + i, T, 512)
+        with torch.cuda.stream(s):
+            xd = torch.from_numpy(x).to("cuda", non_blocking=False)
+            out = torch.empty_like(xd)
+            idx = torch.empty((T, k), dtype=torch.int32, device="cuda")
+            w = torch.empty((T, k), dtype=torch.float32, device="cuda")
+        s.synchronize()
+        flags = tie_amd.PATH_MFMA if T > 64 else tie_amd.PATH_EXACT
+        print("stream case %d T=%d" % (i, T), flush=True)
+        L.forward(xd, T, k, out, idx, w, flags=flags, stream=s.cuda_stream)
+        cases.append((x, out, idx, w, flags))
+    torch.cuda.synchronize()
+    for x, out, idx, w, flags in cases:
+        ro, ri, rw = bind.moe_block(layer, x, k)
+        assert_same(idx.cpu().numpy(), ri, "topk_idx")
+        assert_same(w.cpu().numpy(), rw, "topk_w")
+        got = out.cpu().numpy()
+        if flags == tie_amd.PATH_EXACT:
+            assert_same(got, ro, "out")
+        else:
+            assert float(np.linalg.norm(got - ro) / np.linalg.norm(ro)) <= 4e-3
+    L.close()

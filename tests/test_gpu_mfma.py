@@ -1,20 +1,23 @@
-"""GPU parity of the MFMA (grouped bf16 GEMM) path, called through the C ABI.
+"""GPU parity of the MFMA (grouped matrix-core GEMM) path, called through the
+C ABI.
 
 Routing (logits, top-k, gate weights) is computed in exact fp32 on both paths,
 so selected experts and gate weights must equal the oracle bit for bit.  The
-expert products run on bf16 matrix cores, so outputs are checked two ways:
+expert products run on the 16-bit matrix cores, so outputs are checked two
+ways:
 
-  * against a float64 model of the same arithmetic (weights dequantised in
-    fp32 as TIE does, rounded to bf16 -- Q4_K and Q6_K weights run on the
-    f16 matrix cores instead, emulated exactly, with x in f16 and h as
-    f16(h / 256) * 256; other activations rounded to bf16; TIE's table
-    SwiGLU; y rounded to bf16) -- this pins the kernels' tiling, operand
-    layouts (including the f16 path's K permutation) and epilogue: relative
-    L2 error <= 2e-3;
-  * against the fp32 oracle (TIE's own arithmetic) -- the bf16 rounding
-    error, reported and bounded: relative L2 error <= 2e-2 for Q4_K/Q6_K
-    weights, and max |err| <= 1e-3 for BF16 weights (activations split into
-    two bf16 parts).
+  * against a float64 model of the same arithmetic (the kernels' operands
+    emulated exactly: Q4_K / Q6_K weights dequantised in packed f16 with
+    their factor 256, x rounded to f16, h rounded to an 11-bit significand
+    (f16 scaled by the layer's power of two), y rounded to bf16; BF16
+    weights with activations split into two bf16 parts; TIE's table SwiGLU)
+    -- this pins the kernels' tiling, operand layouts (including the K
+    permutation), pipelines and epilogues;
+  * against the fp32 oracle (TIE's own arithmetic): the 16-bit rounding
+    error, bounded at about twice what it measures.
+
+Tokens whose activations leave the f16 range are recomputed in TIE's exact
+arithmetic; their rows must equal the oracle bit for bit.
 """
 import numpy as np
 import pytest
@@ -25,6 +28,16 @@ from oracle import bind
 from tie_amd import synth
 
 pytestmark = pytest.mark.gpu
+
+# rel. L2 bounds: quantised weights against the fp32 oracle (measured
+# 1.71e-3 .. 1.81e-3 on these inputs), and against the float64 model of the
+# kernels' own operands (measured 2.4e-5 .. 1.26e-4)
+ORACLE_RL2 = 4e-3
+MODEL_RL2 = 3e-4
+# BF16 weights (activations split into two bf16 parts): the north star's max
+# |err| bound (values O(1)), and rel. L2 (measured 4.4e-6 .. 4.6e-6)
+BF16_MAXABS = 1e-3
+BF16_RL2 = 2e-5
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -44,13 +57,21 @@ def f16(a):
     return np.asarray(a, np.float32).astype(np.float16).astype(np.float32)
 
 
+def sig11(a):
+    """Round to an 11-bit significand (f16's), exponent unbounded: f16 of a
+    value scaled into f16's normal range by a power of two, scaled back."""
+    a = np.asarray(a, np.float64)
+    m, e = np.frexp(a)
+    return np.ldexp(np.round(m * 2048.0) / 2048.0, e)
+
+
 def q4k_f16(buf):
-    """Q4_K weights as the f16 gate/up kernels form them, divided by their
-    factor 256: per sub-block D = d*sc and M = -dmin*m in fp32 (exact), times
-    256 rounded to f16, then code*D16 + M16 rounded once to f16 (v_pk_fma_f16).
-    Super-block layout (TIE's block_q4_K): d, dmin (f16), 12 scale bytes, 128
-    code bytes; sub-block 2g holds the low and 2g+1 the high nibbles of code
-    bytes 32g..32g+31."""
+    """Q4_K weights as the f16 kernels form them, divided by their factor
+    256: per sub-block D = d*sc and M = -dmin*m in fp32 (exact), times 256
+    rounded to f16, then code*D16 + M16 rounded once to f16 (v_pk_fma_f16).
+    Super-block layout (TIE's block_q4_K): d, dmin (f16), 12 scale bytes,
+    128 code bytes; sub-block 2g holds the low and 2g+1 the high nibbles of
+    code bytes 32g..32g+31."""
     b = np.frombuffer(np.ascontiguousarray(buf).tobytes(), np.uint8).reshape(-1, 144)
     nb = b.shape[0]
     d = b[:, 0:2].copy().view(np.float16).astype(np.float32)[:, 0]
@@ -100,59 +121,69 @@ def q6k_f16(buf):
     return W.astype(np.float32).reshape(-1) / 256
 
 
-def quant_f16(buf, wtype):
-    return q4k_f16(buf) if wtype == synth.Q4_K else q6k_f16(buf)
+QUANT = (synth.Q4_K, synth.Q6_K)
 
 
-def dequant(buf, wtype, E, rows, inn):
+def expert_weights(buf, wtype, e, rows, inn, f16_ops):
+    """Expert e's [rows][inn] weights as the kernels' operands."""
+    nbytes = rows * synth.row_bytes(wtype, inn)
+    raw = np.ascontiguousarray(np.frombuffer(np.ascontiguousarray(buf).tobytes(), np.uint8,
+                                             count=nbytes, offset=e * nbytes))
     if wtype == synth.BF16:
-        return synth.bf16_bits_to_f32(np.ascontiguousarray(buf).view(np.uint16)).reshape(E, rows, inn)
-    out = np.empty(E * rows * inn, np.float32)
+        return synth.bf16_bits_to_f32(raw.view(np.uint16)).reshape(rows, inn)
+    if f16_ops:
+        return (q4k_f16(raw) if wtype == synth.Q4_K else q6k_f16(raw)).reshape(rows, inn)
+    out = np.empty(rows * inn, np.float32)
     fn = bind.oracle().orc_dequant_q4k if wtype == synth.Q4_K else bind.oracle().orc_dequant_q6k
-    fn(np.ascontiguousarray(buf).ctypes.data, E * rows * inn, out.ctypes.data)
-    return out.reshape(E, rows, inn)
+    fn(raw.ctypes.data, rows * inn, out.ctypes.data)
+    return bf16(out).reshape(rows, inn)
 
 
-def model(layer, x, k, idx, w, tab, split):
-    """float64 model of the MFMA path given the (exact) routing."""
-    d, F, E = layer.d, layer.F, layer.E
-    Wg = dequant(layer.gate, layer.gate_type, E, F, d)
-    Wu = dequant(layer.up, layer.up_type, E, F, d)
-    Wd = dequant(layer.down, layer.down_type, E, d, F)
-    xa = x
-    quant = (synth.Q4_K, synth.Q6_K)
-    h16 = layer.down_type in quant  # h as f16 * 2^-8 (down on f16 operands)
-    if not split:
-        if layer.gate_type in quant:
-            # f16 operands
-            Wg = quant_f16(layer.gate, layer.gate_type).reshape(E, F, d)
-            Wu = quant_f16(layer.up, layer.up_type).reshape(E, F, d)
-            xa = f16(x)
-        else:
-            Wg, Wu, xa = bf16(Wg), bf16(Wu), bf16(x)
-    if h16:
-        Wd = quant_f16(layer.down, layer.down_type).reshape(E, d, F)
-    elif not split:
-        Wd = bf16(Wd)
+def model(layer, x, idx, w, tab):
+    """float64 model of the MFMA path given the (exact) routing, grouped by
+    expert (matrix products per expert)."""
+    d, F = layer.d, layer.F
+    split = layer.gate_type == synth.BF16       # activations as bf16 hi + lo (exact to ~16 bits)
+    h16 = layer.down_type in QUANT               # h in f16 (scaled) for the f16 down kernels
+    if split:
+        xa = x.astype(np.float64)
+    elif layer.gate_type in QUANT:
+        xa = f16(x).astype(np.float64)
+    else:
+        xa = bf16(x).astype(np.float64)
     out = np.zeros(x.shape, np.float64)
-    for t in range(x.shape[0]):
-        for j in range(k):
-            e = idx[t, j]
-            if e < 0:
-                continue
-            g = (Wg[e].astype(np.float64) @ xa[t].astype(np.float64)).astype(np.float32)
-            u = (Wu[e].astype(np.float64) @ xa[t].astype(np.float64)).astype(np.float32)
-            bind.oracle().orc_swiglu(g.ctypes.data, u.ctypes.data, F, tab.ctypes.data)
-            h = f16(g / 256) * 256 if h16 else g if split else bf16(g)
-            y = Wd[e].astype(np.float64) @ h.astype(np.float64)
-            if not split:
-                y = bf16(y.astype(np.float32)).astype(np.float64)  # stored as bf16 for the combine
-            out[t] += float(w[t, j]) * y
+    for e in np.unique(idx[idx >= 0]):
+        t, j = np.nonzero(idx == e)
+        Wg = expert_weights(layer.gate, layer.gate_type, e, F, d, True)
+        Wu = expert_weights(layer.up, layer.up_type, e, F, d, True)
+        Wd = expert_weights(layer.down, layer.down_type, e, d, F, h16)
+        X = xa[t]
+        g = np.ascontiguousarray((X @ Wg.T.astype(np.float64)).astype(np.float32))
+        u = np.ascontiguousarray((X @ Wu.T.astype(np.float64)).astype(np.float32))
+        bind.oracle().orc_swiglu(g.ctypes.data, u.ctypes.data, g.size, tab.ctypes.data)
+        if h16:
+            h = sig11(g)
+        elif split:
+            h = g.astype(np.float64)
+        else:
+            h = bf16(g).astype(np.float64)
+        y = h @ Wd.T.astype(np.float64)
+        if h16:
+            y = bf16(y.astype(np.float32)).astype(np.float64)  # stored as bf16 for the combine
+        np.add.at(out, t, w[t, j].astype(np.float64)[:, None] * y)
     return out
 
 
 def rel_l2(a, b):
-    return float(np.linalg.norm((a - b).ravel()) / max(np.linalg.norm(np.asarray(b).ravel()), 1e-30))
+    return float(np.linalg.norm((np.asarray(a, np.float64) - b).ravel()) /
+                 max(np.linalg.norm(np.asarray(b, np.float64).ravel()), 1e-30))
+
+
+def report(tag, out, ro):
+    e = rel_l2(out, ro)
+    mx = float(np.abs(out - ro).max())
+    print("PARITY %s rel_l2=%.3e max_abs=%.3e max_ref=%.3e" % (tag, e, mx, float(np.abs(ro).max())), flush=True)
+    return e, mx
 
 
 def run_mfma(layer, x, k):
@@ -172,24 +203,30 @@ def run_mfma(layer, x, k):
     return res
 
 
-@pytest.mark.parametrize("shape", [(256, 256, 16, 4, 40), (512, 512, 8, 2, 300), (2048, 768, 128, 8, 64)])
+def check_routing(idx, w, ri, rw):
+    np.testing.assert_array_equal(idx, ri)
+    np.testing.assert_array_equal(bits(w), bits(rw))
+
+
+# (d, F, E, k, T): small shapes, the 30B shape at few pairs per expert, and
+# few experts at T = 1024 (256 pairs per expert: full 160-row gate/up tiles,
+# the cross-stage software pipeline, several tiles per expert)
+@pytest.mark.parametrize("shape", [(256, 256, 16, 4, 40), (512, 512, 8, 2, 300), (2048, 768, 128, 8, 64),
+                                   (2048, 768, 8, 2, 1024)])
 @pytest.mark.parametrize("types", [(synth.Q4_K, synth.Q6_K), (synth.Q6_K, synth.Q4_K)])
-def test_quantised_against_bf16_model_and_oracle(shape, types):
+def test_quantised_against_model_and_oracle(shape, types):
     d, F, E, k, T = shape
     layer = synth_layer(31 + d + T, d, F, E, types[0], types[1], None)
     x = synth.make_input(31 + T, T, d)
     out, idx, w = run_mfma(layer, x, k)
     ro, ri, rw = bind.moe_block(layer, x, k)
-    np.testing.assert_array_equal(idx, ri)
-    np.testing.assert_array_equal(bits(w), bits(rw))
-    tab = bind.silu_table()
-    m = model(layer, x, k, ri, rw, tab, split=False)
+    check_routing(idx, w, ri, rw)
+    m = model(layer, x, ri, rw, bind.silu_table())
     e_model = rel_l2(out, m)
-    e_oracle = rel_l2(out, ro)
-    print("rel L2 vs bf16 model %.3g, vs fp32 oracle %.3g; max|err|/max|ref| vs oracle %.3g" % (
-        e_model, e_oracle, np.abs(out - ro).max() / np.abs(ro).max()), flush=True)
-    assert e_model <= 2e-3
-    assert e_oracle <= 2e-2
+    print("rel L2 vs kernel model %.3e" % e_model, flush=True)
+    e_oracle, _ = report("q_%d_%d_%d_%d_%d_%d" % (d, F, E, k, T, types[0]), out, ro)
+    assert e_model <= MODEL_RL2
+    assert e_oracle <= ORACLE_RL2
 
 
 @pytest.mark.parametrize("T,zipf", [(48, None), (200, 1.2)])
@@ -208,40 +245,104 @@ def test_bf16_weights_split_activations(T, zipf):
     out, idx, w = out.cpu().numpy(), idx.cpu().numpy(), w.cpu().numpy()
     L.close()
     ro, ri, rw = bind.moe_block(layer, x, k)
-    np.testing.assert_array_equal(idx, ri)
-    np.testing.assert_array_equal(bits(w), bits(rw))
-    err = np.abs(out - ro).max()
-    print("bf16 weights: max|err| %.3g (max|out| %.3g), rel L2 %.3g" % (err, np.abs(ro).max(), rel_l2(out, ro)),
-          flush=True)
-    assert err <= 1e-3
+    check_routing(idx, w, ri, rw)
+    e, err = report("bf16_T%d" % T, out, ro)
+    assert err <= BF16_MAXABS and e <= BF16_RL2
 
 
-def test_full_prefill_30b_routing_exact_and_sampled_outputs():
-    c = synth.CONFIGS["30b_t2048"]
+@pytest.mark.parametrize("cfg", ["30b_t2048", "235b_t1024"])
+def test_full_prefill_all_tokens(cfg):
+    """The headline prefill shapes at full size: every token's selection
+    bit-exact, every output row within the 16-bit bound."""
+    c = synth.CONFIGS[cfg]
     layer = synth_layer(c["seed"], c["d"], c["F"], c["E"], c["gu_type"], c["down_type"], None)
     x = synth.make_input(c["seed"], c["T"], c["d"])
     out, idx, w = run_mfma(layer, x, c["k"])
-    sample = np.arange(0, c["T"], 32)  # every 32nd token through the oracle
-    ro, ri, rw = bind.moe_block(layer, x[sample], c["k"])
-    np.testing.assert_array_equal(idx[sample], ri)
-    np.testing.assert_array_equal(bits(w[sample]), bits(rw))
-    e = rel_l2(out[sample], ro)
-    print("T=2048 sampled rel L2 vs oracle %.3g" % e, flush=True)
-    assert e <= 2e-2
+    ro, ri, rw = bind.moe_block(layer, x, c["k"])
+    check_routing(idx, w, ri, rw)
+    e, _ = report(cfg, out, ro)
+    assert np.isfinite(out).all()
+    assert e <= ORACLE_RL2
+
+
+def test_full_bf16_zipf_t512():
+    """30B shape, BF16 experts, Zipf-biased routing, T = 512 on the matrix
+    cores (the split-activation kernels at d = 2048, E = 128 with imbalanced
+    tiles): selection bit-exact, max |err| <= 1e-3."""
+    c = synth.CONFIGS["30b_bf16_zipf_t512"]
+    layer = synth_layer(c["seed"], c["d"], c["F"], c["E"], c["gu_type"], c["down_type"], c["zipf"])
+    x = synth.make_input(c["seed"], c["T"], c["d"])
+    out, idx, w = run_mfma(layer, x, c["k"])
+    ro, ri, rw = bind.moe_block(layer, x, c["k"])
+    check_routing(idx, w, ri, rw)
+    counts = np.bincount(ri.ravel(), minlength=c["E"])
+    print("zipf: busiest expert %d pairs, %d experts idle" % (counts.max(), int((counts == 0).sum())), flush=True)
+    e, err = report("30b_bf16_zipf_t512", out, ro)
+    assert err <= BF16_MAXABS and e <= BF16_RL2
+
+
+def scaled_scales(buf, wtype, factor):
+    """A copy of a Q4_K / Q6_K tensor with every fp16 super-block scale
+    (Q4_K d and dmin, Q6_K d) multiplied by factor (a power of two)."""
+    size = 144 if wtype == synth.Q4_K else 210
+    b = np.frombuffer(np.ascontiguousarray(buf).tobytes(), np.uint8).reshape(-1, size).copy()
+    cols = [(0, 2), (2, 4)] if wtype == synth.Q4_K else [(208, 210)]
+    for a, z in cols:
+        v = b[:, a:z].copy().view(np.float16).astype(np.float32) * np.float32(factor)
+        b[:, a:z] = v.astype(np.float16).view(np.uint8)
+    return b.reshape(-1)
+
+
+def test_small_activations():
+    """Weights 64x smaller than the synthetic default (closer to real
+    models): |h| ~ 1e-3.  The layer's h scale keeps those values normal f16
+    numbers, so the error against the oracle stays at the 16-bit level."""
+    import copy
+    base = synth_layer(91, 2048, 768, 16, synth.Q4_K, synth.Q6_K, None)
+    layer = copy.copy(base)
+    layer.gate = scaled_scales(base.gate, synth.Q4_K, 1.0 / 64)
+    layer.up = scaled_scales(base.up, synth.Q4_K, 1.0 / 64)
+    x = synth.make_input(91, 256, 2048)
+    out, idx, w = run_mfma(layer, x, 4)
+    ro, ri, rw = bind.moe_block(layer, x, 4)
+    check_routing(idx, w, ri, rw)
+    e, _ = report("small_h", out, ro)
+    assert e <= ORACLE_RL2
+
+
+def test_out_of_range_tokens_recomputed_exactly():
+    """Tokens whose x (|x| >= 65504, NaN) or scaled h leave the f16 range
+    are recomputed in TIE's exact arithmetic: their rows equal the oracle
+    bit for bit, and no other row changes."""
+    layer = synth_layer(93, 512, 512, 16, synth.Q4_K, synth.Q6_K, None)
+    T, k = 160, 4
+    x = synth.make_input(93, T, 512)
+    base_out, _, _ = run_mfma(layer, x, k)
+    x2 = x.copy()
+    x2[5] *= np.float32(1e5)     # x beyond f16
+    x2[9] *= np.float32(200.0)   # x fits f16, h ~ 4e4 x typical: beyond
+    x2[17, 3] = np.nan           # NaN logits: no expert, output 0
+    out, idx, w = run_mfma(layer, x2, k)
+    ro, ri, rw = bind.moe_block(layer, x2, k)
+    check_routing(idx, w, ri, rw)
+    for t in (5, 9, 17):
+        np.testing.assert_array_equal(bits(out[t]), bits(ro[t]), err_msg="row %d" % t)
+    assert (out[17] == 0).all()
+    rest = np.setdiff1d(np.arange(T), [5, 9, 17])
+    np.testing.assert_array_equal(bits(out[rest]), bits(base_out[rest]))
+    assert np.isfinite(out[rest]).all()
 
 
 def test_lfm2_prefill_routing_exact():
     """Sigmoid routing on the MFMA path (separate selection kernel at large
     T): selection and weights bit-exact against the oracle, outputs within
-    the bf16 bound."""
+    the 16-bit bound."""
     c = synth.CONFIGS["lfm2_t32"]
     layer = synth_layer(c["seed"], c["d"], c["F"], c["E"], c["gu_type"], c["down_type"], None, 1, c["probs_bias"])
     T = 300
     x = synth.make_input(c["seed"] + 5, T, c["d"])
     out, idx, w = run_mfma(layer, x, c["k"])
     ro, ri, rw = bind.moe_block(layer, x, c["k"])
-    np.testing.assert_array_equal(idx, ri)
-    np.testing.assert_array_equal(bits(w), bits(rw))
-    e = rel_l2(out, ro)
-    print("lfm2 T=300 rel L2 vs oracle %.3g" % e, flush=True)
-    assert e <= 2e-2
+    check_routing(idx, w, ri, rw)
+    e, _ = report("lfm2_T300", out, ro)
+    assert e <= ORACLE_RL2

@@ -2,6 +2,7 @@
 // and cache, workspace, and the forward orchestration.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <map>
 #include <string>
 #include <mutex>
@@ -17,6 +18,7 @@ int set_error(int code, const char *fmt, ...);
 void clear_error();
 int silu_table_host(float *tab, int n);
 int rsqrt_table_host(std::vector<uint32_t> &tab, int &nbits);
+int h_shift_estimate(int type, const uint8_t *b, size_t n_bytes, int d);
 } // namespace tie
 
 struct tie_hip_layer {
@@ -42,7 +44,9 @@ struct Ctx {
 	int device = -1;
 	hipStream_t stream = nullptr;
 	float *silu = nullptr;
-	Workspace ws;
+	// per-forward scratch, one per stream that forwards were enqueued on:
+	// forwards on different streams never share a buffer
+	std::map<hipStream_t, Workspace> ws;
 	// host-pointer API: cached layers and staging buffers
 	std::map<std::tuple<const void *, const void *, const void *, const void *, int, int, int, int, int, int, int,
 			    const void *>,
@@ -196,10 +200,11 @@ static int ensure_init()
 	return TIE_HIP_OK;
 }
 
-// Grow the per-forward workspace to hold T tokens.
-static int ensure_workspace(int T, int k, int d, int F, int E)
+// Grow stream s's workspace to hold T tokens; *out = that workspace.
+static int ensure_workspace(hipStream_t s, int T, int k, int d, int F, int E, Workspace **out)
 {
-	Workspace &w = g.ws;
+	Workspace &w = g.ws[s];
+	*out = &w;
 	const size_t pairs = (size_t)(T > 0 ? T : 1) * k;
 	if (w.alloc && pairs <= w.cap_pairs && (size_t)F <= w.cap_F && (size_t)d <= w.cap_d && (size_t)E <= w.cap_E)
 		return TIE_HIP_OK;
@@ -220,9 +225,12 @@ static int ensure_workspace(int T, int k, int d, int F, int E)
 		     o_hlo = take(P * FF * 2), o_xlo = take(Tcap * DD * 2), o_nm = take(Tcap * DD * 4);
 	const size_t max_tiles = (size_t)mfma_max_tiles((int)P, (int)EE);
 	const size_t o_te = take(2 * max_tiles * 4), o_tm = take(2 * max_tiles * 4), o_nt = take(8);
+	const size_t o_fl = take(Tcap * 4), o_fx = take(Tcap * 4), o_fc = take(4);
 	void *mem = nullptr;
 	if (w.alloc) {
-		HIP_TRY(hipStreamSynchronize(g.stream));
+		// work still queued on s (or, through events, on any stream the
+		// caller chained to it) may read the old buffer: drain the device
+		HIP_TRY(hipDeviceSynchronize());
 		HIP_TRY(hipFree(w.alloc));
 		w = Workspace();
 	}
@@ -247,6 +255,9 @@ static int ensure_workspace(int T, int k, int d, int F, int E)
 	w.tile_e = (int32_t *)(b + o_te);
 	w.tile_m0 = (int32_t *)(b + o_tm);
 	w.ntiles = (int32_t *)(b + o_nt);
+	w.tok_flag = (int32_t *)(b + o_fl);
+	w.fix_list = (int32_t *)(b + o_fx);
+	w.fix_count = (int32_t *)(b + o_fc);
 	w.tile_cap = (int32_t)max_tiles;
 	w.cap_pairs = P;
 	w.cap_F = FF;
@@ -353,6 +364,15 @@ static int create_layer(const tie_hip_layer_desc *ds, tie_hip_layer **out)
 	}
 	if (e == hipSuccess && rc == 0)
 		e = hipStreamSynchronize(g.stream);
+	if (e == hipSuccess && rc == 0) {
+		// the f16 scale of h from a sample of the gate weights (host or
+		// device source: unified addressing)
+		const size_t n = std::min<size_t>(L.gate.expert_bytes * E, (size_t)1 << 20);
+		std::vector<uint8_t> smp(n);
+		e = hipMemcpy(smp.data(), ds->gate_exps, n, hipMemcpyDefault);
+		if (e == hipSuccess)
+			L.h_shift = h_shift_estimate(ds->gate_type, smp.data(), n, d);
+	}
 	if (rc || e != hipSuccess) {
 		free_layer(l);
 		if (rc)
@@ -380,15 +400,19 @@ static int forward(tie_hip_layer *layer, const float *x, int T, int k, float *ou
 	if (!x || !out)
 		return set_error(TIE_HIP_EINVAL, "null x/out");
 	const bool mfma = (flags & TIE_HIP_PATH_MFMA) || (!(flags & TIE_HIP_PATH_EXACT) && T > g.exact_max_t);
+	if (mfma && !decode_supported(L, k) && mfma_f16_operands(L))
+		return set_error(TIE_HIP_EINVAL, "the MFMA path needs the exact per-token kernels for its range guard "
+						 "(k * F too large for them: use TIE_HIP_PATH_EXACT)");
 	if (mfma && L.gate.type != L.up.type)
 		return set_error(TIE_HIP_EINVAL, "the MFMA path needs gate and up of one type (got %d, %d)", L.gate.type,
 				 L.up.type);
 	if (mfma && L.gate.type != TIE_GGML_BF16 && L.down.type == TIE_GGML_BF16)
 		return set_error(TIE_HIP_EINVAL, "the MFMA path needs a quantised down when gate/up are quantised");
-	int rc = ensure_workspace(T, k, L.d, L.F, L.E);
+	Workspace *wsp = nullptr;
+	int rc = ensure_workspace(s, T, k, L.d, L.F, L.E, &wsp);
 	if (rc)
 		return rc;
-	Workspace &ws = g.ws;
+	Workspace &ws = *wsp;
 	if (mfma) {
 		prof_begin("router", s);
 		HIP_TRY(launch_router(L, x, T, k, ws.logits, ws.topk_idx, ws.topk_w, s));
@@ -401,6 +425,27 @@ static int forward(tie_hip_layer *layer, const float *x, int T, int k, float *ou
 		HIP_TRY(launch_combine(T, L.d, k, ws.topk_w, ws.topk_idx, ws.y, out, s, res,
 				       L.down.type != TIE_GGML_BF16));
 		prof_end(s);
+		if (mfma_f16_operands(L)) {
+			// tokens whose activations left the f16 range (listed by the
+			// kernels above; usually none): recomputed exactly, their rows
+			// of out overwritten
+			HIP_TRY(launch_decode(L, x, k, g.silu, ws.logits, ws.topk_idx, ws.topk_w, ws.h, out, res, ws.fix_list,
+					      ws.fix_count, T, false, true, s));
+		}
+	} else if (T == 1 && decode_supported(L, k)) {
+		// one token: router logits, then the experts and the combine in two
+		// launches (the selection runs in the gate/up prologue for E <= 128)
+		prof_begin("router", s);
+		HIP_TRY(launch_router_logits(L, x, 1, ws.logits, s));
+		prof_end(s);
+		const bool inl = L.E <= 128;
+		if (!inl) {
+			prof_begin("router_topk", s);
+			HIP_TRY(launch_router_select(L, 1, k, ws.logits, ws.topk_idx, ws.topk_w, s));
+			prof_end(s);
+		}
+		HIP_TRY(launch_decode(L, x, k, g.silu, ws.logits, ws.topk_idx, ws.topk_w, ws.h, out, res, nullptr, nullptr,
+				      1, inl, false, s));
 	} else {
 		// routing, experts and the combine
 		HIP_TRY(launch_exact_block(L, x, T, k, g.silu, ws, out, s, res));
@@ -451,13 +496,14 @@ static int forward_residual(tie_hip_layer *layer, const float *hidden, const flo
 	int rc = ensure_rsqrt();
 	if (rc)
 		return rc;
-	rc = ensure_workspace(T, k, L.d, L.F, L.E);
+	Workspace *ws = nullptr;
+	rc = ensure_workspace(s, T, k, L.d, L.F, L.E, &ws);
 	if (rc)
 		return rc;
 	prof_begin("rmsnorm", s);
-	HIP_TRY(launch_rmsnorm(hidden, norm_w, eps, T, L.d, g.ws.normed, g.rsq, g.rsq_bits, s));
+	HIP_TRY(launch_rmsnorm(hidden, norm_w, eps, T, L.d, ws->normed, g.rsq, g.rsq_bits, s));
 	prof_end(s);
-	return forward(layer, g.ws.normed, T, k, out, idx_out, w_out, flags, s, hidden);
+	return forward(layer, ws->normed, T, k, out, idx_out, w_out, flags, s, hidden);
 }
 
 } // namespace tie
@@ -497,13 +543,14 @@ extern "C" void tie_hip_shutdown(void)
 	if (g.device < 0)
 		return;
 	(void)hipSetDevice(g.device);
-	(void)hipStreamSynchronize(g.stream);
+	(void)hipDeviceSynchronize();
 	for (auto &kv : g.cache)
 		free_layer(kv.second);
 	g.cache.clear();
-	if (g.ws.alloc)
-		(void)hipFree(g.ws.alloc);
-	g.ws = Workspace();
+	for (auto &kv : g.ws)
+		if (kv.second.alloc)
+			(void)hipFree(kv.second.alloc);
+	g.ws.clear();
 	for (void *p : {(void *)g.x_dev, (void *)g.out_dev, (void *)g.w_dev, (void *)g.idx_dev, (void *)g.silu,
 			(void *)g.norm_dev, (void *)g.rsq})
 		if (p)
@@ -552,7 +599,7 @@ extern "C" void tie_hip_layer_destroy(tie_hip_layer *layer)
 	if (!layer)
 		return;
 	if (g.device >= 0)
-		(void)hipStreamSynchronize(g.stream);
+		(void)hipDeviceSynchronize(); // forwards on any stream may still read it
 	free_layer(layer);
 }
 
@@ -672,7 +719,7 @@ extern "C" void tie_hip_model_close(tie_hip_model *m)
 	if (!m)
 		return;
 	if (g.device >= 0)
-		(void)hipStreamSynchronize(g.stream);
+		(void)hipDeviceSynchronize(); // forwards on any stream may still read it
 	for (auto *l : m->layers)
 		free_layer(l);
 	for (float *p : m->norms)
@@ -852,7 +899,7 @@ extern "C" void tie_hip_matrix_destroy(tie_hip_matrix *m)
 	if (!m)
 		return;
 	if (g.device >= 0)
-		(void)hipStreamSynchronize(g.stream);
+		(void)hipDeviceSynchronize(); // forwards on any stream may still read it
 	if (m->alloc)
 		(void)hipFree(m->alloc);
 	delete m;
@@ -881,10 +928,11 @@ extern "C" int tie_hip_mat_mat(tie_hip_matrix *m, const float *x_dev, int T, flo
 		HIP_TRY(launch_router_logits(m->F, x_dev, T, out_dev, s));
 	} else {
 		const int G = dense_groups(T);
-		rc = ensure_workspace(T, 1, m->W.in, QK, G);
+		Workspace *ws = nullptr;
+		rc = ensure_workspace(s, T, 1, m->W.in, QK, G, &ws);
 		if (rc)
 			return rc;
-		HIP_TRY(launch_dense(m->W, x_dev, T, out_dev, g.ws, s));
+		HIP_TRY(launch_dense(m->W, x_dev, T, out_dev, *ws, s));
 	}
 	prof_end(s);
 	return TIE_HIP_OK;

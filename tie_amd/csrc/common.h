@@ -72,6 +72,7 @@ struct Layer {
 	int routing = 0;               // ROUTE_SOFTMAX (Qwen3) or ROUTE_SIGMOID (LFM2)
 	const float *pbias = nullptr;  // [E] or null: LFM2 selection bias (exp_probs_b_bias)
 	ExpertTensor gate, up, down;
+	int h_shift = 0;               // MFMA path: h is stored as f16(h * 2^-h_shift)
 	void *alloc = nullptr;         // one device allocation holding everything
 	size_t bytes = 0;
 };
@@ -94,6 +95,9 @@ struct Workspace {
 	int32_t *tile_e = nullptr;    // [2][max tiles] MFMA work lists (gate/up, down): expert of each tile
 	int32_t *tile_m0 = nullptr;   // [2][max tiles] first pair of the tile within the expert
 	int32_t *ntiles = nullptr;    // [2]
+	int32_t *tok_flag = nullptr;  // [T]      f16 path: token's activations left the f16 range
+	int32_t *fix_list = nullptr;  // [T]      flagged tokens (recomputed exactly after the forward)
+	int32_t *fix_count = nullptr; // [1]
 	int32_t tile_cap = 0;         // max tiles per list
 	size_t cap_pairs = 0, cap_F = 0, cap_d = 0, cap_E = 0;
 	void *alloc = nullptr;
@@ -112,6 +116,17 @@ hipError_t launch_exact_block(const Layer &L, const float *x, int T, int k, cons
 			      float *out, hipStream_t s, const float *res = nullptr);
 hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, const float *silu, Workspace &ws,
 			       hipStream_t s);
+// True when the matrix-core path of this layer takes f16 operands, whose
+// range the forward guards (tokens outside it are recomputed exactly).
+bool mfma_f16_operands(const Layer &L);
+// The block for listed tokens in TIE's exact arithmetic (decode.hip): list
+// == null runs token 0 of a one-token call (routed from its logits when
+// inline_route, E <= 128); otherwise the *count tokens of list, with their
+// selection already in topk_idx / topk_w.  h: [entries][k][F] scratch.
+bool decode_supported(const Layer &L, int k);
+hipError_t launch_decode(const Layer &L, const float *x, int k, const float *silu, const float *logits,
+			 int32_t *topk_idx, float *topk_w, float *h, float *out, const float *res, const int32_t *list,
+			 const int32_t *count, int max_entries, bool inline_route, bool fixup, hipStream_t s);
 int mfma_max_tiles(int npairs, int E); // per list
 struct Layer;
 int mfma_gu_rows(const Layer &L, int npairs); // rows per gate/up tile (the tile list's and the kernel's)

@@ -1,0 +1,515 @@
+// decode.hip -- the block for one token at a time, in TIE's exact fp32
+// arithmetic: decode (T = 1), and the exact recomputation of listed tokens
+// of a large-T forward (tokens whose activations left the f16 range of the
+// matrix-core path).
+//
+// Reference: per token, TIE runs k process_expert_task jobs
+// (engine.c:916-964): gate and up GEMVs (mat_vec_row_f32_{q4k,q6k}_f32_avx2,
+// math_avx2.c:753-787, a serial fp32 sum over the row's super-block dots
+// dot_product_f32_{q4k,q6k}_avx2, :535-604 / :411-495), the table SwiGLU
+// (swiglu_activation_f32_f32_avx2, :908-950) and the down GEMV, then the
+// combine out = sum_j g_j y_j in slot order (model_qwen3.c:459-467).
+//
+// At one token nothing is shared between the k experts, so the work is a
+// set of independent (row, super-block) dot products.  Each lane owns one:
+// it issues the loads of its whole block (Q4_K 9, Q6_K 13 chunks of 16
+// bytes, all in flight at once) and runs TIE's dot with the input vector
+// read from LDS.  A workgroup holds every block of R rows, so the serial
+// per-row sums over the blocks, the SwiGLU (gate/up) and the combine over
+// the k experts (down) happen in its epilogue without another launch:
+//
+//   decode_gu_kernel    blockIdx = (R rows of F, slot j, list entry);
+//                       lane = (row, matrix, block): 2 nb R dots.  Writes
+//                       h = silu_tab(gate) * up of the slot's expert.
+//   decode_down_kernel  blockIdx = (R rows of d, -, list entry);
+//                       lane = (row, slot, block): k nb R dots.  Writes
+//                       out = [res +] sum_j g_j y_j, i.e. the combine.
+//
+// Rows are read from the panel layout (common.h): rows r0..r0+R-1 of a
+// panel are R consecutive 16-byte slots of every 1 KiB chunk.  The input
+// vector (x, or the k h vectors) sits in LDS as 256-float segments, each
+// padded by XPAD floats so that the segments a wave reads at once start in
+// different banks.
+#include "common.h"
+#include "route.h"
+
+namespace tie {
+
+constexpr int XPAD = 4;
+constexpr int XSEG = QK + XPAD;
+constexpr int DEC_MAX_THREADS = 512;
+constexpr size_t DEC_MAX_LDS = 150 * 1024; // dynamic LDS per workgroup at most (160 KiB per CU)
+
+typedef const float __attribute__((address_space(3))) dfloat; // LDS input rows
+typedef float vf4 __attribute__((ext_vector_type(4)));
+typedef const vf4 __attribute__((address_space(3))) dfloat4;
+
+__device__ __forceinline__ uint32_t dword_of(const uint4 &v, int i)
+{
+	return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
+// Make v opaque at this point of the instruction stream: the work that
+// depends on it cannot be hoisted above (the block's chunks are all loaded
+// up front, so without these the scheduler would dequantise the whole block
+// at once and run out of registers).
+__device__ __forceinline__ void pin(uint4 &v)
+{
+	asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w));
+}
+
+// Accumulator fence: an empty statement that reads and writes all 16
+// accumulators, so it cannot run before the FMAs issued ahead of it.  The
+// pins that follow it (volatile statements keep their order) therefore
+// hold the next group's work behind the previous group's FMAs.
+__device__ __forceinline__ void acc_fence(float (&a0)[8], float (&a1)[8])
+{
+	asm volatile("" : "+v"(a0[0]), "+v"(a0[1]), "+v"(a0[2]), "+v"(a0[3]), "+v"(a0[4]), "+v"(a0[5]), "+v"(a0[6]),
+			  "+v"(a0[7]));
+	asm volatile("" : "+v"(a1[0]), "+v"(a1[1]), "+v"(a1[2]), "+v"(a1[3]), "+v"(a1[4]), "+v"(a1[5]), "+v"(a1[6]),
+			  "+v"(a1[7]));
+}
+
+__device__ __forceinline__ float byte_f(uint32_t w, int i)
+{
+	return (float)((w >> (8 * i)) & 0xffu);
+}
+
+// get_scale_min_k4 (math_scalar.c:91-100) of sub-block j: D = d * sc,
+// nM = -(dmin * m)
+__device__ __forceinline__ void q4k_scale(const uint4 &c0, int j, float d, float dmin, float &D, float &nM)
+{
+	const uint32_t s[3] = {c0.y, c0.z, c0.w};
+	auto sb = [&](int i) { return (s[i >> 2] >> (8 * (i & 3))) & 0xffu; };
+	uint32_t sc, m;
+	if (j < 4) {
+		sc = sb(j) & 63u;
+		m = sb(j + 4) & 63u;
+	} else {
+		sc = (sb(j + 4) & 15u) | ((sb(j - 4) >> 6) << 4);
+		m = (sb(j + 4) >> 4) | ((sb(j) >> 6) << 4);
+	}
+	D = d * (float)sc;
+	nM = -(dmin * (float)m);
+}
+
+// dot_product_f32_q4k_avx2 (math_avx2.c:535-604) of one block (chunks c[0..8]
+// of the panel layout: c[0] = d, dmin, scales; c[1 + 2g + o] = code bytes
+// 64g + 16o .. +15) with 256 inputs x.  16 accumulators (two 8-lane AVX2
+// registers): weight w = fma(q, d*sc, -(dmin*m)); step (g, o, h) covers
+// codes 64g + 16o + 4h + i (low nibbles: x[64g + 16o + 4h + i], high: +32),
+// accumulator 4h + i; then lo + hi and hsum_f32_avx2.
+__device__ __forceinline__ float q4k_dot(uint4 (&c)[9], dfloat *x)
+{
+	const float d = half_bits_to_float(c[0].x & 0xffffu);
+	const float dmin = half_bits_to_float(c[0].x >> 16);
+	float a0[8], a1[8];
+#pragma unroll
+	for (int l = 0; l < 8; l++)
+		a0[l] = a1[l] = 0.0f;
+#pragma unroll
+	for (int g = 0; g < 4; g++) {
+		// one 64-weight group at a time
+		acc_fence(a0, a1);
+		asm volatile("" : "+v"(x));
+		pin(c[1 + 2 * g]);
+		pin(c[2 + 2 * g]);
+		float D1, M1, D2, M2;
+		q4k_scale(c[0], 2 * g, d, dmin, D1, M1);
+		q4k_scale(c[0], 2 * g + 1, d, dmin, D2, M2);
+#pragma unroll
+		for (int ss = 0; ss < 8; ss++) {
+			const int o = ss >> 2, h = ss & 3;
+			const uint32_t w = dword_of(c[1 + 2 * g + o], h);
+			const uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
+			dfloat *xb = x + 64 * g + 16 * o + 4 * h;
+			const vf4 xl = *(dfloat4 *)xb, xh = *(dfloat4 *)(xb + 32);
+			const float xlv[4] = {xl.x, xl.y, xl.z, xl.w}, xhv[4] = {xh.x, xh.y, xh.z, xh.w};
+#pragma unroll
+			for (int i = 0; i < 4; i++) {
+				const float wl = __builtin_fmaf(byte_f(lo, i), D1, M1);
+				const float wh = __builtin_fmaf(byte_f(hi, i), D2, M2);
+				const int m = 4 * h + i;
+				float &A = (m < 8) ? a0[m & 7] : a1[m & 7];
+				A = __builtin_fmaf(xlv[i], wl, A);
+				A = __builtin_fmaf(xhv[i], wh, A);
+			}
+		}
+	}
+	float v[8];
+#pragma unroll
+	for (int l = 0; l < 8; l++)
+		v[l] = a0[l] + a1[l];
+	return hsum8(v);
+}
+
+// dot_product_f32_q6k_avx2 (math_avx2.c:411-495) of one block (chunks
+// c[0..12] of the panel layout: 0-7 ql, 8-11 qh, 12 the int8 scales; d
+// the fp16 scale) with 256 inputs x.  Step (n, l, hw) forms the codes
+// q = ql nibble | qh bits << 4 of weights 128n + l + 4hw + i + 32r (r =
+// 0..3) and accumulates fma(d*sc, (q - 32) * x, acc) into accumulators
+// 4hw + i of a0 (r = 0, 2) and a1 (r = 1, 3), the product rounded on its
+// own.
+__device__ __forceinline__ float q6k_dot(uint4 (&c)[13], uint32_t dbits, dfloat *x)
+{
+	const float d = half_bits_to_float(dbits);
+	uint4 sc4 = c[12];
+	auto sc = [&](int j) { return (float)(int8_t)((dword_of(sc4, j >> 2) >> (8 * (j & 3))) & 0xffu); };
+	float a0[8], a1[8];
+#pragma unroll
+	for (int l = 0; l < 8; l++)
+		a0[l] = a1[l] = 0.0f;
+#pragma unroll
+	for (int st = 0; st < 16; st++) {
+		const int qt = st >> 2, n = st >> 3, l = 8 * ((st >> 1) & 3), hw = st & 1;
+		const int hl = qt & 1, is = (l >= 16) ? 1 : 0;
+		if ((st & 3) == 0) {
+			// one quarter at a time
+			acc_fence(a0, a1);
+			asm volatile("" : "+v"(x));
+			pin(sc4);
+			pin(c[4 * n + hl]);
+			pin(c[4 * n + 2 + hl]);
+			pin(c[8 + 2 * n + hl]);
+		}
+		// quarter qt = (n, hl): ql chunks 4n + hl (low nibbles) and 4n + 2 + hl
+		// (high nibbles), qh chunk 8 + 2n + hl
+		const uint4 &C0 = c[4 * n + hl], &C1 = c[4 * n + 2 + hl], &C2 = c[8 + 2 * n + hl];
+		const float W0 = d * sc(8 * n + is + 0), W1 = d * sc(8 * n + is + 2);
+		const float W2 = d * sc(8 * n + is + 4), W3 = d * sc(8 * n + is + 6);
+		const int dw = ((l & 8) >> 2) + hw;
+		const uint32_t L = dword_of(C0, dw), L2 = dword_of(C1, dw), H = dword_of(C2, dw);
+		const uint32_t q1 = (L & 0x0f0f0f0fu) | ((H & 0x03030303u) << 4);
+		const uint32_t q2 = (L2 & 0x0f0f0f0fu) | (((H >> 2) & 0x03030303u) << 4);
+		const uint32_t q3 = ((L >> 4) & 0x0f0f0f0fu) | (((H >> 4) & 0x03030303u) << 4);
+		const uint32_t q4 = ((L2 >> 4) & 0x0f0f0f0fu) | (((H >> 6) & 0x03030303u) << 4);
+		dfloat *xb = x + 128 * n + l + 4 * hw;
+#pragma unroll
+		for (int half = 0; half < 2; half++) {
+			const uint32_t qa = half ? q3 : q1, qb = half ? q4 : q2;
+			const float Wa = half ? W2 : W0, Wb = half ? W3 : W1;
+			const vf4 xa = *(dfloat4 *)(xb + 64 * half), xc = *(dfloat4 *)(xb + 64 * half + 32);
+			const float xav[4] = {xa.x, xa.y, xa.z, xa.w}, xcv[4] = {xc.x, xc.y, xc.z, xc.w};
+#pragma unroll
+			for (int i = 0; i < 4; i++) {
+				const int m = 4 * hw + i;
+				const float fa = byte_f(qa, i) - 32.0f, fb = byte_f(qb, i) - 32.0f;
+				a0[m] = __builtin_fmaf(Wa, fa * xav[i], a0[m]);
+				a1[m] = __builtin_fmaf(Wb, fb * xcv[i], a1[m]);
+			}
+		}
+	}
+	float v[8];
+#pragma unroll
+	for (int l = 0; l < 8; l++)
+		v[l] = a0[l] + a1[l];
+	return hsum8(v);
+}
+
+typedef const uint4 __attribute__((address_space(1))) g4;
+
+// The dot of one (row, block) of a quantised tensor: `blk` = the row's
+// 16-byte slot in chunk 0 of its panel's block column (chunk c at +1024 c);
+// `dp` (Q6_K) = the row's fp16 d.  All loads are issued before any use.
+template <int TYPE> __device__ __forceinline__ float row_block_dot(const uint8_t *blk, const uint8_t *dp, dfloat *x)
+{
+	if constexpr (TYPE == TIE_GGML_Q4_K) {
+		uint4 c[9];
+#pragma unroll
+		for (int i = 0; i < 9; i++)
+			c[i] = *(const uint4 *)(g4 *)(blk + 1024 * i);
+		return q4k_dot(c, x);
+	} else {
+		uint4 c[13];
+#pragma unroll
+		for (int i = 0; i < 13; i++)
+			c[i] = *(const uint4 *)(g4 *)(blk + 1024 * i);
+		const uint32_t db = *(const uint16_t *)dp;
+		return q6k_dot(c, db, x);
+	}
+}
+
+// address of row `row`, block column b of expert e (panel layout)
+__device__ __forceinline__ const uint8_t *panel_slot(const uint8_t *base, size_t expert_bytes, int e, int row, int b,
+						     int nb, size_t pbytes)
+{
+	return base + (size_t)e * expert_bytes + ((size_t)(row >> 6) * nb + b) * pbytes + (row & 63) * 16;
+}
+
+struct DecodeArgs {
+	const uint8_t *w[3];   // gate, up, down (panel layout)
+	size_t expert_bytes[3];
+	int d, F, E, k;
+	int R;                 // rows per workgroup (a power of two <= 64)
+	const float *x;        // [T][d]
+	const float *logits;   // [T][E] (inline routing)
+	int32_t *topk_idx;     // [T][k]
+	float *topk_w;         // [T][k]
+	float *h;              // [list entry][k][F] SwiGLU outputs
+	float *out;            // [T][d]
+	const float *res;      // [T][d] or null: out = res + block
+	const float *silu;
+	const int32_t *list;   // tokens to run (null: token 0 only)
+	const int32_t *count;  // number of list entries (device)
+	int routing;
+	const float *pbias;
+};
+
+__device__ __forceinline__ int list_count(const DecodeArgs &a)
+{
+	return a.list ? __builtin_amdgcn_readfirstlane(*a.count) : 1;
+}
+
+__device__ __forceinline__ int list_token(const DecodeArgs &a, int li)
+{
+	return a.list ? __builtin_amdgcn_readfirstlane(a.list[li]) : 0;
+}
+
+// Dynamic LDS: x [nb][XSEG] | part [2 nb][R] | (INLINE) selection
+template <int TG, int TU, bool INLINE>
+__global__ __launch_bounds__(DEC_MAX_THREADS) void decode_gu_kernel(DecodeArgs a)
+{
+	extern __shared__ __attribute__((aligned(16))) float dl[];
+	__shared__ int32_t sel_idx[MAX_K];
+	__shared__ float sel_w[MAX_K];
+	__shared__ uint64_t etab[32];
+	const int R = a.R, j = blockIdx.y;
+	const int nb = a.d / QK;
+	float *xs = dl;
+	float *part = dl + nb * XSEG;
+	const int tid = threadIdx.x;
+	const int ntask = 2 * nb;
+	const int n = list_count(a);
+	for (int li = blockIdx.z; li < n; li += gridDim.z) {
+		const int t = list_token(a, li);
+		// x of the token -> LDS (independent of the routing)
+		const float4 *x4 = reinterpret_cast<const float4 *>(a.x + (size_t)t * a.d);
+		for (int i = tid; i < a.d / 4; i += blockDim.x) {
+			const int f = 4 * i;
+			*reinterpret_cast<float4 *>(xs + (f / QK) * XSEG + (f % QK)) = x4[i];
+		}
+		int e;
+		if constexpr (INLINE) {
+			// the token's selection from its logits (one wave), published
+			// by workgroup (0, 0) for the down kernel
+			if (tid < 32) {
+				const uint64_t tab[32] = TIE_EXP2_TABLE;
+				etab[tid] = tab[tid];
+			}
+			__syncthreads();
+			if (tid < 64)
+				topk_softmax_wave<2>(a.logits + (size_t)t * a.E, a.E, a.k, etab, sel_idx, sel_w, a.routing,
+						     a.pbias);
+			__syncthreads();
+			if (blockIdx.x == 0 && j == 0 && tid < a.k) {
+				a.topk_idx[(size_t)t * a.k + tid] = sel_idx[tid];
+				a.topk_w[(size_t)t * a.k + tid] = sel_w[tid];
+			}
+			e = sel_idx[j];
+		} else {
+			e = __builtin_amdgcn_readfirstlane(a.topk_idx[(size_t)t * a.k + j]);
+			__syncthreads();
+		}
+		if (e < 0) // slot without an expert: its h is never read
+			continue;
+		const int r0 = blockIdx.x * R;
+		for (int u = tid; u < ntask * R; u += blockDim.x) {
+			const int r = u & (R - 1), task = u / R;
+			const int mat = task >= nb ? 1 : 0, b = task - mat * nb;
+			const uint8_t *blk = panel_slot(a.w[mat], a.expert_bytes[mat], e, r0 + r, b, nb,
+							panel_bytes(mat ? TU : TG));
+			float v;
+			if (mat == 0)
+				v = row_block_dot<TG>(blk, blk + Q6K_CHUNKS * 1024 - 14 * ((r0 + r) & 63), (dfloat *)(xs + b * XSEG));
+			else
+				v = row_block_dot<TU>(blk, blk + Q6K_CHUNKS * 1024 - 14 * ((r0 + r) & 63), (dfloat *)(xs + b * XSEG));
+			part[task * R + r] = v;
+		}
+		__syncthreads();
+		if (tid < R) {
+			// serial sums over the blocks (math_avx2.c:762-766), SwiGLU
+			float g = 0.0f, up = 0.0f;
+			for (int b = 0; b < nb; b++)
+				g = g + part[b * R + tid];
+			for (int b = 0; b < nb; b++)
+				up = up + part[(nb + b) * R + tid];
+			a.h[((size_t)li * a.k + j) * a.F + r0 + tid] = tie_swiglu(g, up, a.silu);
+		}
+		__syncthreads();
+	}
+}
+
+// Dynamic LDS: h [k][nb][XSEG] | part [k nb][R]
+template <int TD> __global__ __launch_bounds__(DEC_MAX_THREADS) void decode_down_kernel(DecodeArgs a)
+{
+	extern __shared__ __attribute__((aligned(16))) float dl[];
+	__shared__ int32_t sel_idx[MAX_K];
+	__shared__ float sel_w[MAX_K];
+	const int R = a.R, k = a.k;
+	const int nb = a.F / QK;
+	float *hs = dl;
+	float *part = dl + (size_t)k * nb * XSEG;
+	const int tid = threadIdx.x;
+	const int ntask = k * nb;
+	const int n = list_count(a);
+	const int r0 = blockIdx.x * R;
+	for (int li = blockIdx.z; li < n; li += gridDim.z) {
+		const int t = list_token(a, li);
+		if (tid < k) {
+			sel_idx[tid] = a.topk_idx[(size_t)t * k + tid];
+			sel_w[tid] = a.topk_w[(size_t)t * k + tid];
+		}
+		// the k h vectors -> LDS (independent of the selection)
+		const float4 *h4 = reinterpret_cast<const float4 *>(a.h + (size_t)li * k * a.F);
+		for (int i = tid; i < k * a.F / 4; i += blockDim.x) {
+			const int f = 4 * i; // = j F + b QK + m
+			*reinterpret_cast<float4 *>(hs + (f / QK) * XSEG + (f % QK)) = h4[i];
+		}
+		__syncthreads();
+		for (int u = tid; u < ntask * R; u += blockDim.x) {
+			const int r = u & (R - 1), task = u / R;
+			const int j = task / nb, b = task - j * nb;
+			const int e = sel_idx[j];
+			float v = 0.0f;
+			if (e >= 0) {
+				const uint8_t *blk = panel_slot(a.w[2], a.expert_bytes[2], e, r0 + r, b, nb, panel_bytes(TD));
+				v = row_block_dot<TD>(blk, blk + Q6K_CHUNKS * 1024 - 14 * ((r0 + r) & 63),
+						      (dfloat *)(hs + (size_t)task * XSEG));
+			}
+			part[task * R + r] = v;
+		}
+		__syncthreads();
+		if (tid < R) {
+			// y_j = serial sum over the blocks; out = sum_j fma(g_j, y_j, .)
+			// in slot order from +0 (model_qwen3.c:459-467); slots without an
+			// expert add nothing
+			float acc = 0.0f;
+			for (int j = 0; j < k; j++) {
+				if (sel_idx[j] < 0)
+					continue;
+				float y = 0.0f;
+				for (int b = 0; b < nb; b++)
+					y = y + part[(j * nb + b) * R + tid];
+				acc = __builtin_fmaf(sel_w[j], y, acc);
+			}
+			const size_t o = (size_t)t * a.d + r0 + tid;
+			a.out[o] = a.res ? a.res[o] + acc : acc;
+		}
+		__syncthreads();
+	}
+}
+
+// ---------------------------------------------------------------- launchers
+static int round64(int n)
+{
+	return (n + 63) & ~63;
+}
+
+// rows per workgroup: the largest power of two <= rmax (and <= 64) whose
+// tasks x rows fit one workgroup
+static int pick_rows(int ntask, int rmax)
+{
+	int R = rmax;
+	while (R > 1 && ntask * R > DEC_MAX_THREADS)
+		R >>= 1;
+	return R;
+}
+
+bool decode_supported(const Layer &L, int k)
+{
+	const bool q = (L.gate.type == TIE_GGML_Q4_K || L.gate.type == TIE_GGML_Q6_K) &&
+		       (L.up.type == TIE_GGML_Q4_K || L.up.type == TIE_GGML_Q6_K) &&
+		       (L.down.type == TIE_GGML_Q4_K || L.down.type == TIE_GGML_Q6_K);
+	const int nbd = L.d / QK, nbf = L.F / QK;
+	// LDS: x of one token, or the k h vectors, plus the partial dots
+	const size_t lds_gu = sizeof(float) * ((size_t)nbd * XSEG + 2 * nbd * 64);
+	const size_t lds_dn = sizeof(float) * ((size_t)k * nbf * XSEG + (size_t)k * nbf * 8);
+	return q && k <= MAX_K && 2 * nbd <= DEC_MAX_THREADS && k * nbf <= DEC_MAX_THREADS && lds_gu <= DEC_MAX_LDS &&
+	       lds_dn <= DEC_MAX_LDS;
+}
+
+template <typename K> static hipError_t dec_launch(K kern, dim3 grid, dim3 block, size_t lds, hipStream_t s,
+						     const DecodeArgs &a)
+{
+	hipError_t err = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+	if (err != hipSuccess)
+		return err;
+	hipLaunchKernelGGL(kern, grid, block, lds, s, a);
+	return hipGetLastError();
+}
+
+// The block for listed tokens (list == null: token 0 of a one-token call,
+// routed here from its logits when inline_route) in TIE's exact arithmetic.
+// h: [max_entries][k][F] scratch.  max_entries bounds the grid's list
+// dimension (entries beyond it are looped over).
+hipError_t launch_decode(const Layer &L, const float *x, int k, const float *silu, const float *logits,
+			 int32_t *topk_idx, float *topk_w, float *h, float *out, const float *res, const int32_t *list,
+			 const int32_t *count, int max_entries, bool inline_route, bool fixup, hipStream_t s)
+{
+	DecodeArgs a;
+	memset(&a, 0, sizeof a);
+	a.w[0] = L.gate.data;
+	a.w[1] = L.up.data;
+	a.w[2] = L.down.data;
+	a.expert_bytes[0] = L.gate.expert_bytes;
+	a.expert_bytes[1] = L.up.expert_bytes;
+	a.expert_bytes[2] = L.down.expert_bytes;
+	a.d = L.d;
+	a.F = L.F;
+	a.E = L.E;
+	a.k = k;
+	a.x = x;
+	a.logits = logits;
+	a.topk_idx = topk_idx;
+	a.topk_w = topk_w;
+	a.h = h;
+	a.out = out;
+	a.res = res;
+	a.silu = silu;
+	a.list = list;
+	a.count = count;
+	a.routing = L.routing;
+	a.pbias = L.pbias;
+	const int nz = max_entries < 1 ? 1 : max_entries > 64 ? 64 : max_entries;
+	const int nbd = L.d / QK, nbf = L.F / QK;
+	hipError_t err;
+	prof_begin(fixup ? "fixup_gate_up" : "decode_gate_up", s);
+	{
+		DecodeArgs g = a;
+		g.R = pick_rows(2 * nbd, 16);
+		const int threads = round64(2 * nbd * g.R);
+		const size_t lds = sizeof(float) * ((size_t)nbd * XSEG + 2 * nbd * g.R);
+		const dim3 grid(L.F / g.R, k, nz);
+		const int tg = L.gate.type, tu = L.up.type;
+#define DEC_GU(A, B)                                                                                                 \
+	(inline_route ? dec_launch(decode_gu_kernel<A, B, true>, grid, dim3(threads), lds, s, g)                        \
+		      : dec_launch(decode_gu_kernel<A, B, false>, grid, dim3(threads), lds, s, g))
+		if (tg == TIE_GGML_Q4_K && tu == TIE_GGML_Q4_K)
+			err = DEC_GU(TIE_GGML_Q4_K, TIE_GGML_Q4_K);
+		else if (tg == TIE_GGML_Q4_K)
+			err = DEC_GU(TIE_GGML_Q4_K, TIE_GGML_Q6_K);
+		else if (tu == TIE_GGML_Q4_K)
+			err = DEC_GU(TIE_GGML_Q6_K, TIE_GGML_Q4_K);
+		else
+			err = DEC_GU(TIE_GGML_Q6_K, TIE_GGML_Q6_K);
+#undef DEC_GU
+	}
+	prof_end(s);
+	if (err != hipSuccess)
+		return err;
+	prof_begin(fixup ? "fixup_down" : "decode_down", s);
+	{
+		DecodeArgs g = a;
+		g.R = pick_rows(k * nbf, 8);
+		const int threads = round64(k * nbf * g.R);
+		const size_t lds = sizeof(float) * ((size_t)k * nbf * XSEG + (size_t)k * nbf * g.R);
+		const dim3 grid(L.d / g.R, 1, nz);
+		err = L.down.type == TIE_GGML_Q4_K
+			      ? dec_launch(decode_down_kernel<TIE_GGML_Q4_K>, grid, dim3(threads), lds, s, g)
+			      : dec_launch(decode_down_kernel<TIE_GGML_Q6_K>, grid, dim3(threads), lds, s, g);
+	}
+	prof_end(s);
+	return err;
+}
+
+} // namespace tie

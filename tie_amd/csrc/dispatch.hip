@@ -30,8 +30,12 @@ __global__ __launch_bounds__(DSP_THREADS) void dispatch_kernel(const int32_t *__
 							       int32_t *__restrict__ active,
 							       int32_t *__restrict__ tile_e,
 							       int32_t *__restrict__ tile_m0,
-							       int32_t *__restrict__ ntiles, int tile_cap, int mt_gu)
+							       int32_t *__restrict__ ntiles, int tile_cap, int mt_gu,
+							       int32_t *__restrict__ fix_count)
 {
+	// the f16 path's list of tokens to recompute starts empty
+	if (fix_count && threadIdx.x == 0)
+		*fix_count = 0;
 	extern __shared__ __attribute__((aligned(16))) int32_t sidx[];
 	__shared__ __attribute__((aligned(16))) int32_t cnt[MAX_E];
 	__shared__ int32_t cur[MAX_E];
@@ -77,7 +81,8 @@ hipError_t launch_dispatch(const Layer &L, int T, int k, const int32_t *topk_idx
 		attr = true;
 	}
 	hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(DSP_THREADS), lds, s, topk_idx, npairs, L.E, ws.offsets,
-			   ws.pairs, ws.active, ws.tile_e, ws.tile_m0, ws.ntiles, ws.tile_cap, mfma_gu_rows(L, npairs));
+			   ws.pairs, ws.active, ws.tile_e, ws.tile_m0, ws.ntiles, ws.tile_cap, mfma_gu_rows(L, npairs),
+			   ws.fix_count);
 	return hipGetLastError();
 }
 

@@ -2,6 +2,8 @@
 // table builder, the host build of the device expf, and error reporting.
 #include <immintrin.h>
 #include <math.h>
+
+#include <cmath>
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
@@ -166,6 +168,88 @@ int rsqrt_table_host(std::vector<uint32_t> &tab, int &nbits)
 		for (uint32_t j = 0; j < (1u << n); j++)
 			tab[(p << n) + j] = all[p * M + (j << (23 - n))];
 	return TIE_HIP_OK;
+}
+
+// ------------------------------------------------------ f16 range of h
+// The matrix-core path stores the SwiGLU output h as f16 times 2^-shift.
+// The shift centres the layer's typical |h| at about 2^2 inside f16's
+// normal range [2^-14, 2^16): 14 octaves of headroom above it (a token
+// beyond them is recomputed exactly), and small activations stay normal
+// numbers instead of losing bits as subnormals.  Typical |h| follows from
+// the gate weights' RMS over a sample of their blocks: for inputs of unit
+// RMS (RMSNorm outputs) a row dot is ~ sqrt(d) RMS(w), and h = silu(g) u
+// is of the order of its square.
+
+static float f16_host(uint16_t h)
+{
+	const uint32_t e = (h >> 10) & 31u, m = h & 1023u;
+	const float v = e == 0 ? ldexpf((float)m, -24) : e == 31 ? INFINITY : ldexpf((float)(m | 1024u), (int)e - 25);
+	return (h & 0x8000u) ? -v : v;
+}
+
+int h_shift_estimate(int type, const uint8_t *b, size_t n_bytes, int d)
+{
+	double ss = 0.0;
+	size_t n = 0;
+	if (type == TIE_GGML_Q4_K) {
+		for (size_t o = 0; o + 144 <= n_bytes; o += 144) {
+			const uint8_t *blk = b + o;
+			uint16_t hd, hm;
+			memcpy(&hd, blk, 2);
+			memcpy(&hm, blk + 2, 2);
+			const float dd = f16_host(hd), dmin = f16_host(hm);
+			const uint8_t *sc = blk + 4, *qs = blk + 16;
+			for (int j = 0; j < 8; j++) {
+				int s, m;
+				if (j < 4) {
+					s = sc[j] & 63;
+					m = sc[j + 4] & 63;
+				} else {
+					s = (sc[j + 4] & 15) | ((sc[j - 4] >> 6) << 4);
+					m = (sc[j + 4] >> 4) | ((sc[j] >> 6) << 4);
+				}
+				for (int i = 0; i < 32; i++) {
+					const int q = (j & 1) ? qs[32 * (j >> 1) + i] >> 4 : qs[32 * (j >> 1) + i] & 15;
+					const double w = (double)dd * s * q - (double)dmin * m;
+					ss += w * w;
+				}
+			}
+			n += 256;
+		}
+	} else if (type == TIE_GGML_Q6_K) {
+		for (size_t o = 0; o + 210 <= n_bytes; o += 210) {
+			const uint8_t *blk = b + o;
+			uint16_t hd;
+			memcpy(&hd, blk + 208, 2);
+			const double dd = f16_host(hd);
+			for (int i = 0; i < 256; i++) {
+				// ql nibble and qh bits of weight i (block_q6_K order)
+				const int half = i >> 7, l = i & 127, r = l >> 5, li = l & 31;
+				const uint8_t ql = blk[64 * half + li + 32 * (r & 1)];
+				const int lo = r < 2 ? ql & 15 : ql >> 4;
+				const int hi = (blk[128 + 32 * half + li] >> (2 * r)) & 3;
+				const int sc = (int8_t)blk[192 + 8 * half + li / 16 + 2 * r];
+				const double w = dd * sc * ((lo | (hi << 4)) - 32);
+				ss += w * w;
+			}
+			n += 256;
+		}
+	} else if (type == TIE_GGML_BF16) {
+		for (size_t o = 0; o + 2 <= n_bytes; o += 2) {
+			uint16_t v;
+			memcpy(&v, b + o, 2);
+			uint32_t u = (uint32_t)v << 16;
+			float f;
+			memcpy(&f, &u, 4);
+			ss += (double)f * f;
+			n++;
+		}
+	}
+	if (n == 0 || !(ss > 0.0) || !std::isfinite(ss))
+		return 0;
+	const double h_typ = (double)d * (ss / (double)n); // (sqrt(d) rms)^2
+	int s = (int)lrint(log2(h_typ)) - 2;
+	return s < -24 ? -24 : s > 24 ? 24 : s;
 }
 
 } // namespace tie

@@ -47,9 +47,15 @@
 // Numerics: fp32 accumulation of 16-bit products.  Q4_K / Q6_K weights are
 // dequantised with packed f16 math (code in the mantissa of 1024.0, exact
 // subtraction, one v_pk_fma_f16 / v_pk_mul_f16 rounding) and carry a factor
-// 2^F16_SHIFT; x is rounded to f16, h is stored as f16 * 2^-F16_SHIFT, both
-// with the K order inside each 8-group 0,2,1,3,4,6,5,7 (the dequantised
-// pairs' order).  The expert outputs y are stored as bf16.  With BF16 expert
+// 2^F16_SHIFT, which the epilogues take out of the fp32 accumulators
+// (exact); x is rounded to f16 and h is stored as f16(h * 2^-h_shift), with
+// the layer's h_shift chosen at upload so its typical |h| sits near 2^2 (far
+// from both ends of f16's range), both with the K order inside each 8-group
+// 0,2,1,3,4,6,5,7 (the dequantised pairs' order).  A token whose x or scaled
+// h leaves the f16 range (|v| >= 65504, or not finite) is
+// listed by to_f16_kernel / the gate/up epilogue and recomputed afterwards
+// in TIE's exact arithmetic (decode.hip), which overwrites its output row.
+// The expert outputs y are stored as bf16.  With BF16 expert
 // weights (exact in bf16) the activations are split into a bf16 high part
 // and a bf16 remainder, stored as two bf16 planes (x by to_split_kernel, h
 // by the gate/up epilogue), two MFMAs per product; this keeps the products
@@ -135,10 +141,23 @@ struct MfmaArgs {
 	const float *silu;
 	uint16_t *h16;           // gate/up out (bf16, by position)
 	uint16_t *h16lo;         // gate/up out, split mode: bf16 remainder plane
-	int h_f16;               // gate/up out: h as f16 * 2^-F16_SHIFT, pair-permuted K order (quantised down)
+	int h_f16;               // gate/up out: h as f16(h * h_scale), pair-permuted K order (quantised down)
+	float h_scale;           // 2^-h_shift of the layer
+	float y_scale;           // down out (f16 operands): 2^(h_shift - F16_SHIFT) takes both factors out
 	float *y;                // down out [pair][d] (BF16 weights: fp32)
 	uint16_t *y16;           // down out [pair][d] (quantised weights: bf16)
+	int32_t *tok_flag;       // [T] gate/up, h_f16: tokens whose h left the f16 range
+	int32_t *fix_list;       //     are appended here (once each) ...
+	int32_t *fix_count;      //     ... and counted
 };
+
+// Token t's activations do not fit the f16 operands: list it (once) for
+// the exact recomputation that follows the forward.
+__device__ __forceinline__ void flag_token(int32_t *flag, int32_t *list, int32_t *count, int t)
+{
+	if (atomicCAS(flag + t, 0, 1) == 0)
+		list[atomicAdd(count, 1)] = t;
+}
 
 template <int TYPE, bool DOWN = false, int MTR = 0> struct Cfg {
 	// pair rows per work tile at most (MTR: the small-tile gate/up kernel's)
@@ -913,11 +932,14 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 				constexpr float unscale = C::F16 ? 1.0f / (1 << F16_SHIFT) : 1.0f;
 				const float hv = tie_swiglu(acc[mt][0][i] * unscale, acc[mt][1][i] * unscale, silu);
 				if (a.h_f16) {
-					// f16 * 2^-F16_SHIFT (range), K positions 1, 2 (and 5, 6)
-					// of each 8-group swapped (the dequantised pairs' order)
+					// f16, K positions 1, 2 (and 5, 6) of each 8-group swapped
+					// (the dequantised pairs' order).  A value outside the f16
+					// range sends the pair's token to the exact recomputation.
 					const int pc = (col & ~3) | ((col & 1) << 1) | ((col >> 1) & 1);
-					a.h16[(size_t)p * a.rows + pc] =
-						__builtin_bit_cast(uint16_t, (_Float16)(hv * (1.0f / (1 << F16_SHIFT))));
+					const float hs = hv * a.h_scale;
+					a.h16[(size_t)p * a.rows + pc] = __builtin_bit_cast(uint16_t, (_Float16)hs);
+					if (!(__builtin_fabsf(hs) < 65504.0f))
+						flag_token(a.tok_flag, a.fix_list, a.fix_count, a.pairs[p] / a.k);
 				} else {
 					const uint16_t hi = bf16_bits(hv);
 					a.h16[(size_t)p * a.rows + col] = hi;
@@ -930,10 +952,13 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 				yr[32] = acc[mt][1][i];
 			} else {
 				// quantised weights: y as bf16 (the path's products already
-				// take bf16 operands; half the bytes to the combine)
+				// take 16-bit operands; half the bytes to the combine); the
+				// f16 weights' factor 2^F16_SHIFT and h's scale come out here
+				// (a power of two: exact)
+				const float unscale = C::F16 ? a.y_scale : 1.0f;
 				uint16_t *yr = a.y16 + (size_t)a.pairs[p] * a.rows + slab * DN_COLS + 64 * w + (lane & 31);
-				yr[0] = bf16_bits(acc[mt][0][i]);
-				yr[32] = bf16_bits(acc[mt][1][i]);
+				yr[0] = bf16_bits(acc[mt][0][i] * unscale);
+				yr[32] = bf16_bits(acc[mt][1][i] * unscale);
 			}
 		}
 		// one M tile at a time: only its accumulators move to VGPRs
@@ -1013,15 +1038,38 @@ __global__ void to_bf16_kernel(const float *__restrict__ x, uint16_t *__restrict
 }
 
 // x (fp32) -> f16 rows for the f16 gate/up A operand, K order inside each
-// 8-group 0,2,1,3,4,6,5,7 (the order of the dequantised weight pairs)
-__global__ void to_f16_kernel(const float *__restrict__ x, uint16_t *__restrict__ y, size_t n8)
+// 8-group 0,2,1,3,4,6,5,7 (the order of the dequantised weight pairs).  One
+// workgroup per token row: flag[t] = 1 (and t listed for the exact
+// recomputation) when any x of the row is not finite or not below 65504 in
+// magnitude, else 0.
+constexpr int F16_THREADS = 256;
+__global__ __launch_bounds__(F16_THREADS) void to_f16_kernel(const float *__restrict__ x, uint16_t *__restrict__ y,
+							      int d, int32_t *__restrict__ flag,
+							      int32_t *__restrict__ list, int32_t *__restrict__ count)
 {
-	for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n8; i += (size_t)gridDim.x * blockDim.x) {
-		const float4 a = reinterpret_cast<const float4 *>(x)[2 * i];
-		const float4 c = reinterpret_cast<const float4 *>(x)[2 * i + 1];
+	const int t = blockIdx.x;
+	const float4 *xr = reinterpret_cast<const float4 *>(x + (size_t)t * d);
+	f16x8 *yr = reinterpret_cast<f16x8 *>(y + (size_t)t * d);
+	int bad = 0;
+	for (int i = threadIdx.x; i < d / 8; i += F16_THREADS) {
+		const float4 a = xr[2 * i], c = xr[2 * i + 1];
+		const float m = __builtin_fmaxf(__builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(a.x), __builtin_fabsf(a.y)),
+								__builtin_fmaxf(__builtin_fabsf(a.z), __builtin_fabsf(a.w))),
+						__builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(c.x), __builtin_fabsf(c.y)),
+								__builtin_fmaxf(__builtin_fabsf(c.z), __builtin_fabsf(c.w))));
+		// fmax drops NaN: test the values themselves for NaN
+		const bool nan = a.x != a.x || a.y != a.y || a.z != a.z || a.w != a.w || c.x != c.x || c.y != c.y ||
+				 c.z != c.z || c.w != c.w;
+		bad |= (nan || !(m < 65504.0f)) ? 1 : 0;
 		const f16x8 h = {(_Float16)a.x, (_Float16)a.z, (_Float16)a.y, (_Float16)a.w,
 				 (_Float16)c.x, (_Float16)c.z, (_Float16)c.y, (_Float16)c.w};
-		reinterpret_cast<f16x8 *>(y)[i] = h;
+		yr[i] = h;
+	}
+	bad = __syncthreads_or(bad);
+	if (threadIdx.x == 0) {
+		flag[t] = bad;
+		if (bad)
+			list[atomicAdd(count, 1)] = t;
 	}
 }
 
@@ -1072,6 +1120,13 @@ static hipError_t launch_one(const MfmaArgs &a, int type, dim3 grid, hipStream_t
 	return launch_type<TIE_GGML_BF16, DOWN>(a, grid, s);
 }
 
+bool mfma_f16_operands(const Layer &L)
+{
+	const bool q = L.gate.type == TIE_GGML_Q4_K || L.gate.type == TIE_GGML_Q6_K;
+	const bool qd = L.down.type == TIE_GGML_Q4_K || L.down.type == TIE_GGML_Q6_K;
+	return TIE_MFMA_F16 && (q || qd);
+}
+
 int mfma_max_tiles(int npairs, int E)
 {
 	constexpr int mt0 = MFMA_MT_GU < MFMA_MT_DN ? MFMA_MT_GU : MFMA_MT_DN;
@@ -1116,6 +1171,11 @@ hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, con
 	a.y = ws.y;
 	a.y16 = reinterpret_cast<uint16_t *>(ws.y);
 	a.h_f16 = TIE_MFMA_F16 && (L.down.type == TIE_GGML_Q4_K || L.down.type == TIE_GGML_Q6_K);
+	a.h_scale = ldexpf(1.0f, -L.h_shift);
+	a.y_scale = ldexpf(1.0f, L.h_shift - F16_SHIFT);
+	a.tok_flag = ws.tok_flag;
+	a.fix_list = ws.fix_list;
+	a.fix_count = ws.fix_count;
 	// grid rows: each list's tile bound for its own tile rows, plus 8 rows:
 	// the XCD remap in the kernel reaches every live item only with at least
 	// 8 * ceil(live / 8) workgroups (rows past the list exit at once)
@@ -1130,7 +1190,8 @@ hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, con
 		if (split)
 			hipLaunchKernelGGL(to_split_kernel, g, dim3(256), 0, s, x, ws.xb, ws.xlo, n4);
 		else if (TIE_MFMA_F16 && (L.gate.type == TIE_GGML_Q4_K || L.gate.type == TIE_GGML_Q6_K))
-			hipLaunchKernelGGL(to_f16_kernel, g, dim3(256), 0, s, x, ws.xb, n4 / 2);
+			hipLaunchKernelGGL(to_f16_kernel, dim3(T), dim3(F16_THREADS), 0, s, x, ws.xb, L.d, ws.tok_flag,
+					   ws.fix_list, ws.fix_count);
 		else
 			hipLaunchKernelGGL(to_bf16_kernel, g, dim3(256), 0, s, x, ws.xb, n4);
 	}
