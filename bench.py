@@ -1,18 +1,22 @@
 """Benchmark of the MI355X Qwen3-MoE FFN block (one GPU).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 30b_t32] [--extra 30b_t1,30b_t2048]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 30b_t32] [--extra 30b_t1,...] [--graph]
 
 A step is one MoE block forward (router, top-k, dispatch, experts, combine)
 over one batch of T tokens of synthetic input, with weights and inputs
 already resident in HBM.  Weights are cycled over L independently generated
 layers (and inputs over L token batches) so that no step finds its experts
-in the 256 MB MALL or the L2 left warm by the previous steps.
+in the 256 MB MALL or the L2 left warm by the previous steps.  The K timed
+steps are K library calls from a Python loop (eager: the way TIE's host
+loop calls the block), bracketed by device synchronisations.  --graph times
+one replay of a HIP graph that captured the same K calls instead.
 
 Prints one JSON line: the headline workload (`value`, tokens/s), the
 roofline of its dominant kernel (event-timed on the library's stream), the
 CPU baseline (TIE's own compiled MoE path on the host cores, or the C
-restatement when the reference build cannot run here), and the extra
-workloads named by --extra.
+restatement when the reference build cannot run here) with the parity of
+the GPU's outputs against it on the same tokens, and the same for the
+extra workloads named by --extra.
 """
 import argparse
 import json
@@ -158,9 +162,11 @@ def expert_bytes(cfg):
     return gu, dn
 
 
-def run_config(torch, tie_amd, wl, T, k, steps, warmup, flags, cfg=None):
+def run_config(torch, tie_amd, wl, T, k, steps, warmup, flags, cfg=None, graph=False):
     """Times `steps` forwards of T tokens; returns the measurement dict.
-    cfg: the workload config (default: the one the layers were made for)."""
+    cfg: the workload config (default: the one the layers were made for).
+    graph: also time the steps as one replay of a captured HIP graph and
+    report that (the eager loop's time is reported either way)."""
     from tie_amd import synth
     cfg = cfg or wl.cfg
     d, F, E = cfg["d"], cfg["F"], cfg["E"]
@@ -178,14 +184,14 @@ def run_config(torch, tie_amd, wl, T, k, steps, warmup, flags, cfg=None):
         # of place, so every step sees the same inputs)
         norm = torch.from_numpy(synth.make_norm_weight(cfg["seed"], d)).cuda()
 
-    def step(s, record_topk=False):
+    def step(s, record_topk=False, stream=None):
         l = s % nL
         if residual:
             wl.layers[l].forward_residual(X[l], norm, 1e-6, T, k, out, idx[l] if record_topk else None,
-                                          w[l] if record_topk else None, flags=flags)
+                                          w[l] if record_topk else None, flags=flags, stream=stream)
             return
         wl.layers[l].forward(X[l], T, k, out, idx[l] if record_topk else None, w[l] if record_topk else None,
-                             flags=flags)
+                             flags=flags, stream=stream)
 
     for s in range(nL):  # routing of every (layer, batch) pair, for the byte counts
         step(s, record_topk=True)
@@ -195,6 +201,8 @@ def run_config(torch, tie_amd, wl, T, k, steps, warmup, flags, cfg=None):
     step(0, record_topk=True)
     torch.cuda.synchronize()
     gpu_out0 = (X[0].cpu().numpy(), out.cpu().numpy(), idx[0].cpu().numpy(), w[0].cpu().numpy())
+    # eager: one library call per step from this Python loop (host launch
+    # overhead included)
     for s in range(warmup):
         step(s)
     torch.cuda.synchronize()
@@ -202,8 +210,28 @@ def run_config(torch, tie_amd, wl, T, k, steps, warmup, flags, cfg=None):
     for s in range(steps):
         step(s)
     torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    ms = 1e3 * elapsed / steps
+    ms_eager = 1e3 * (time.perf_counter() - t0) / steps
+    ms = ms_eager
+    if graph:
+        # the same `steps` forwards captured once as a HIP graph on a stream
+        # of their own (its workspace sized by the warm-up) and replayed: the
+        # GPU's time per step without the host's launch cost
+        gs = torch.cuda.Stream()
+        with torch.cuda.stream(gs):
+            for s in range(max(warmup, nL)):
+                step(s, stream=gs.cuda_stream)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=gs, capture_error_mode="thread_local"):
+            for s in range(steps):
+                step(s, stream=gs.cuda_stream)
+        g.replay()  # warm-up replay
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        g.replay()
+        torch.cuda.synchronize()
+        ms = 1e3 * (time.perf_counter() - t0) / steps
+        del g
 
     # per-kernel event timing over the same sequence of steps
     tie_amd.profile_enable(True)
@@ -225,6 +253,7 @@ def run_config(torch, tie_amd, wl, T, k, steps, warmup, flags, cfg=None):
         "exact_down": U_avg * dn_b + pairs * F * 4 + pairs * d * 4,
         "decode_gate_up": U_avg * gu_b + T * d * 4 + pairs * F * 4,
         "decode_down": U_avg * dn_b + pairs * F * 4 + T * d * 4 * (2 if residual else 1),
+        "decode_fused": E * d * 4 + U_avg * (gu_b + dn_b) + T * d * 4 * (3 if residual else 2),
         "combine": pairs * d * 4 + T * d * 4 * (3 if residual else 1),
         "rmsnorm": 2 * T * d * 4 + d * 4,
         "dispatch": pairs * 4 * 2,
@@ -238,6 +267,7 @@ def run_config(torch, tie_amd, wl, T, k, steps, warmup, flags, cfg=None):
         "exact_down": 2.0 * pairs * F * d,
         "decode_gate_up": 2.0 * pairs * 2 * F * d,
         "decode_down": 2.0 * pairs * F * d,
+        "decode_fused": 2.0 * T * (E * d + 3 * k * F * d),
         "router": 2.0 * T * E * d,
     }
     block_bytes = E * d * 4 + U_avg * (gu_b + dn_b) + 2 * T * d * 4
@@ -254,14 +284,18 @@ def run_config(torch, tie_amd, wl, T, k, steps, warmup, flags, cfg=None):
                          "alg_flops": kf, "TFLOPs": round(kf / (avg_ms * 1e-3) / 1e12, 2) if kf else None}
     return dict(T=T, k=k, ms=ms, tokens_per_s=T / (ms * 1e-3), U=U_avg, block_bytes=block_bytes,
                 block_flops=block_flops, block_GBps=block_bytes / (ms * 1e-3) / 1e9,
-                block_TFLOPs=block_flops / (ms * 1e-3) / 1e12, kernels=kernels, layers=nL, gpu_out0=gpu_out0)
+                block_TFLOPs=block_flops / (ms * 1e-3) / 1e12, kernels=kernels, layers=nL, gpu_out0=gpu_out0,
+                ms_eager=ms_eager, timing="graph" if graph else "eager")
 
 
 def roofline(m, config):
     """Roofline object for the dominant (longest) kernel of a measurement of one
     workload; traffic is the copy-scaled HBM bytes per launch measured for that
     kernel on that workload (None when not profiled)."""
-    name, kd = max(m["kernels"].items(), key=lambda kv: kv[1]["avg_us"])
+    # (kernels without an algorithmic byte count -- the exact recomputation
+    # of out-of-range tokens, which runs empty on these inputs -- are not
+    # candidates)
+    name, kd = max(((n, v) for n, v in m["kernels"].items() if v.get("alg_bytes")), key=lambda kv: kv[1]["avg_us"])
     traffic = None
     tfile = os.path.join(ROOT, "profiles", "traffic.json")
     if os.path.exists(tfile):
@@ -379,6 +413,9 @@ def main():
     ap.add_argument("--layers", type=int, default=0, help="weight layers cycled (0 = auto)")
     ap.add_argument("--path", default="auto", choices=["auto", "exact", "mfma"])
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--graph", action="store_true",
+                    help="time one replay of a HIP graph that captured the K steps instead of the eager loop (one "
+                         "library call per step); under capture one-token forwards take their three-launch form")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="only run a plain device copy of this many MiB 5 times (the reference kernel for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes) and exit")
@@ -428,7 +465,8 @@ def main():
         steps = args.steps if name == args.config else max(10, args.steps // 4)
         warm = args.warmup if name == args.config else max(2, args.warmup // 4)
         log("timing %s: T=%d, %d warm-up + %d steps" % (name, cfg["T"], warm, steps))
-        results[name] = run_config(torch, tie_amd, workloads[key], cfg["T"], cfg["k"], steps, warm, flags, cfg)
+        results[name] = run_config(torch, tie_amd, workloads[key], cfg["T"], cfg["k"], steps, warm, flags, cfg,
+                                   graph=args.graph)
         gpu_outs[name] = (key, results[name].pop("gpu_out0"))
         log(json.dumps({name: results[name]}))
 
@@ -453,6 +491,7 @@ def main():
     for name in names[1:]:
         r = results[name]
         extra[name] = {"tokens_per_s": round(r["tokens_per_s"], 1), "ms_per_step": round(r["ms"], 4),
+                       "ms_per_step_eager": round(r["ms_eager"], 4),
                        "block_GBps": round(r["block_GBps"], 1), "block_TFLOPs": round(r["block_TFLOPs"], 3),
                        "roofline": roofline(r, name), "cpu_baseline": cpu.get(name), "parity": parity.get(name),
                        "kernels": r["kernels"]}
@@ -464,6 +503,8 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(m["ms"], 4),
+        "ms_per_step_eager": round(m["ms_eager"], 4),
+        "timing": m["timing"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

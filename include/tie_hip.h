@@ -130,7 +130,9 @@ typedef struct tie_hip_layer_desc {
 	const void *down_exps;
 	int down_type;
 	const float *router_bias; /* optional [E], added to the logits before top-k; NULL in TIE */
-	int src_on_device;        /* 1: the pointers above are device memory (GGUF layout) */
+	int src_on_device;        /* 1: the pointers above are device memory (GGUF layout); the
+				     library drains the device before reading them, so work on any
+				     stream that writes them has finished */
 	int literal_bf16_stride;  /* 1: BF16 experts start at e*rows*(in/256)*2 bytes, as
 				     process_expert_task computes it (engine.c:929-942) */
 	int routing;              /* TIE_HIP_ROUTE_SOFTMAX (0, Qwen3) or TIE_HIP_ROUTE_SIGMOID (LFM2) */

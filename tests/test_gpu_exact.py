@@ -409,3 +409,55 @@ def test_workspace_per_caller_stream():
         else:
             assert float(np.linalg.norm(got - ro) / np.linalg.norm(ro)) <= 4e-3
     L.close()
+
+
+def test_one_token_repeat_calls_and_types():
+    """One-token forwards (router, then the decode gate/up and down+combine
+    kernels) many times in a row, for both routings and mixed types:
+    bit-exact against the oracle every time."""
+    cases = [(synth_layer(23, 2048, 768, 128, synth.Q4_K, synth.Q6_K, None), 8),
+             (synth_layer(41, 512, 256, 32, synth.Q6_K, synth.Q4_K, None), 4),
+             (synth_layer(42, 512, 512, 24, synth.Q4_K, synth.Q6_K, None, 1, 0.05), 6)]
+    for n, (layer, k) in enumerate(cases):
+        for rep in range(3):
+            x = synth.make_input(50 + rep, 1, layer.d)
+            print("one-token case %d rep %d" % (n, rep), flush=True)
+            run_both(layer, x, k)
+
+
+def test_one_token_graph_replays():
+    """One-token forwards captured in a HIP graph (three forwards on three
+    layers) and replayed with eager work in between: every replay equals
+    the eager result bit for bit."""
+    import torch
+    layers = [synth_layer(60 + i, 2048, 768, 128, synth.Q4_K, synth.Q6_K, None) for i in range(3)]
+    Ls = [tie_amd.Layer.from_synth(l) for l in layers]
+    xs = [torch.from_numpy(synth.make_input(61 + i, 1, 2048)).cuda() for i in range(3)]
+    outs = [torch.empty_like(x) for x in xs]
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        for L, x, o in zip(Ls, xs, outs):
+            L.forward(x, 1, 8, o, stream=s.cuda_stream)
+    torch.cuda.synchronize()
+    eager = [o.cpu().numpy() for o in outs]
+    for i, l in enumerate(layers):
+        ro, _, _ = bind.moe_block(l, xs[i].cpu().numpy(), 8)
+        assert_same(eager[i], ro, "eager vs oracle")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s, capture_error_mode="thread_local"):
+        for L, x, o in zip(Ls, xs, outs):
+            L.forward(x, 1, 8, o, stream=s.cuda_stream)
+    for rep in range(4):
+        for o in outs:
+            o.fill_(-1.0)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        print("graph replay %d" % rep, flush=True)
+        for i, o in enumerate(outs):
+            assert_same(o.cpu().numpy(), eager[i], "replay %d layer %d" % (rep, i))
+        # eager forwards between replays, on the library stream
+        tie_amd.moe_ffn(xs[rep % 3].cpu().numpy(), layers[rep % 3], 8)
+    del g
+    for L in Ls:
+        L.close()

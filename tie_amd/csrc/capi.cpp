@@ -6,6 +6,7 @@
 #include <map>
 #include <string>
 #include <mutex>
+#include <stdlib.h>
 #include <string.h>
 #include <tuple>
 #include <vector>
@@ -331,7 +332,11 @@ static int create_layer(const tie_hip_layer_desc *ds, tie_hip_layer **out)
 	L.down.data = L.up.data + b_up;
 
 	const hipMemcpyKind kind = ds->src_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
-	hipError_t e = hipMemcpyAsync((void *)L.router, ds->router_w, (size_t)E * d * 4, kind, g.stream);
+	// device sources may still be written by work on the caller's streams,
+	// which the library's (non-blocking) stream does not wait for
+	hipError_t e = ds->src_on_device ? hipDeviceSynchronize() : hipSuccess;
+	if (e == hipSuccess)
+		e = hipMemcpyAsync((void *)L.router, ds->router_w, (size_t)E * d * 4, kind, g.stream);
 	if (e == hipSuccess && ds->router_bias)
 		e = hipMemcpyAsync((void *)L.bias, ds->router_bias, (size_t)E * 4, kind, g.stream);
 	if (e == hipSuccess && ds->probs_bias)
@@ -850,9 +855,11 @@ extern "C" int tie_hip_matrix_create(const void *w, int type, int rows, int in_d
 	}
 	m->bytes = bytes;
 	const hipMemcpyKind kind = src_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
-	hipError_t e = hipSuccess;
+	// device sources may still be written by work on the caller's streams
+	hipError_t e = src_on_device ? hipDeviceSynchronize() : hipSuccess;
 	if (type == TIE_GGML_F32) {
-		e = hipMemcpyAsync(m->alloc, w, bytes, kind, g.stream);
+		if (e == hipSuccess)
+			e = hipMemcpyAsync(m->alloc, w, bytes, kind, g.stream);
 		m->F.d = in_dim;
 		m->F.E = rows;
 		m->F.router = (const float *)m->alloc;
@@ -869,7 +876,7 @@ extern "C" int tie_hip_matrix_create(const void *w, int type, int rows, int in_d
 		const uint8_t *src = (const uint8_t *)w;
 		if (!src_on_device) {
 			rc = dev_malloc(&tmp, bytes, "upload staging");
-			if (!rc)
+			if (!rc && e == hipSuccess)
 				e = hipMemcpyAsync(tmp, w, bytes, hipMemcpyHostToDevice, g.stream);
 			src = (const uint8_t *)tmp;
 		}

@@ -124,6 +124,7 @@ bool mfma_f16_operands(const Layer &L);
 // inline_route, E <= 128); otherwise the *count tokens of list, with their
 // selection already in topk_idx / topk_w.  h: [entries][k][F] scratch.
 bool decode_supported(const Layer &L, int k);
+
 hipError_t launch_decode(const Layer &L, const float *x, int k, const float *silu, const float *logits,
 			 int32_t *topk_idx, float *topk_w, float *h, float *out, const float *res, const int32_t *list,
 			 const int32_t *count, int max_entries, bool inline_route, bool fixup, hipStream_t s);
@@ -144,6 +145,10 @@ hipError_t launch_rmsnorm(const float *x, const float *w, float eps, int T, int 
 			  int nbits, hipStream_t s);
 hipError_t launch_repack(const ExpertTensor &dst, const uint8_t *src, int E, int literal_bf16_stride, hipStream_t s);
 
+// Raise a kernel's dynamic-LDS limit to at least `bytes` (remembered per
+// kernel: the attribute call runs only when a launch needs more)
+hipError_t ensure_lds_limit(const void *fn, size_t bytes);
+
 // Per-kernel timing (tie_hip_profile_enable): HIP events recorded on the
 // launch stream around each kernel; no-ops while profiling is off.
 void prof_begin(const char *name, hipStream_t s);
@@ -151,6 +156,29 @@ void prof_end(hipStream_t s);
 
 // ---------------------------------------------------------------- device helpers
 #if defined(__HIPCC__)
+// Copy n4 float4s from global memory with every thread of the workgroup,
+// dst(q, v) storing element q (to LDS): each thread issues a batch of BATCH
+// loads before the first store, so a copy of up to BATCH * blockDim.x
+// elements costs one memory round trip instead of one per element it holds.
+template <int BATCH, typename DST>
+__device__ __forceinline__ void copy_in(const float4 *__restrict__ src, int n4, DST dst)
+{
+	for (int base = threadIdx.x; base < n4; base += BATCH * (int)blockDim.x) {
+		float4 v[BATCH];
+#pragma unroll
+		for (int i = 0; i < BATCH; i++) {
+			const int q = base + i * (int)blockDim.x;
+			v[i] = src[q < n4 ? q : n4 - 1];
+		}
+#pragma unroll
+		for (int i = 0; i < BATCH; i++) {
+			const int q = base + i * (int)blockDim.x;
+			if (q < n4)
+				dst(q, v[i]);
+		}
+	}
+}
+
 // The 8-lane horizontal sum of an AVX2 accumulator (lo+hi, hadd, hadd).
 __device__ __forceinline__ float hsum8(const float v[8])
 {

@@ -33,9 +33,21 @@
 #include "common.h"
 #include "route.h"
 
+#include <algorithm>
+
 namespace tie {
 
 constexpr int XPAD = 4;
+constexpr int INLINE_E = 128; // inline routing: experts held by one wave (two per lane)
+
+// LDS scratch of topk_softmax_block for E <= INLINE_E
+struct TopkScratch {
+	alignas(16) uint32_t key[INLINE_E];
+	float prob[INLINE_E];
+	int rank[INLINE_E];
+	float sv[MAX_K];
+	int si[MAX_K];
+}; // gate/up workgroups of the one-launch decode at most (done words)
 constexpr int XSEG = QK + XPAD;
 constexpr int DEC_MAX_THREADS = 512;
 constexpr size_t DEC_MAX_LDS = 150 * 1024; // dynamic LDS per workgroup at most (160 KiB per CU)
@@ -121,7 +133,9 @@ __device__ __forceinline__ float q4k_dot(uint4 (&c)[9], dfloat *x)
 		for (int ss = 0; ss < 8; ss++) {
 			const int o = ss >> 2, h = ss & 3;
 			const uint32_t w = dword_of(c[1 + 2 * g + o], h);
-			const uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
+			uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
+			// byte-parallel words: each code is then one v_cvt_f32_ubyteN
+			asm volatile("" : "+v"(lo), "+v"(hi));
 			dfloat *xb = x + 64 * g + 16 * o + 4 * h;
 			const vf4 xl = *(dfloat4 *)xb, xh = *(dfloat4 *)(xb + 32);
 			const float xlv[4] = {xl.x, xl.y, xl.z, xl.w}, xhv[4] = {xh.x, xh.y, xh.z, xh.w};
@@ -186,7 +200,8 @@ __device__ __forceinline__ float q6k_dot(uint4 (&c)[13], uint32_t dbits, dfloat 
 		dfloat *xb = x + 128 * n + l + 4 * hw;
 #pragma unroll
 		for (int half = 0; half < 2; half++) {
-			const uint32_t qa = half ? q3 : q1, qb = half ? q4 : q2;
+			uint32_t qa = half ? q3 : q1, qb = half ? q4 : q2;
+			asm volatile("" : "+v"(qa), "+v"(qb)); // byte-parallel codes (v_cvt_f32_ubyteN)
 			const float Wa = half ? W2 : W0, Wb = half ? W3 : W1;
 			const vf4 xa = *(dfloat4 *)(xb + 64 * half), xc = *(dfloat4 *)(xb + 64 * half + 32);
 			const float xav[4] = {xa.x, xa.y, xa.z, xa.w}, xcv[4] = {xc.x, xc.y, xc.z, xc.w};
@@ -208,25 +223,48 @@ __device__ __forceinline__ float q6k_dot(uint4 (&c)[13], uint32_t dbits, dfloat 
 
 typedef const uint4 __attribute__((address_space(1))) g4;
 
-// The dot of one (row, block) of a quantised tensor: `blk` = the row's
-// 16-byte slot in chunk 0 of its panel's block column (chunk c at +1024 c);
-// `dp` (Q6_K) = the row's fp16 d.  All loads are issued before any use.
-template <int TYPE> __device__ __forceinline__ float row_block_dot(const uint8_t *blk, const uint8_t *dp, dfloat *x)
-{
-	if constexpr (TYPE == TIE_GGML_Q4_K) {
-		uint4 c[9];
+// One (row, block) of a quantised tensor held in registers: `blk` = the
+// row's 16-byte slot in chunk 0 of its panel's block column (chunk c at
+// +1024 c), `dp` (Q6_K) = the row's fp16 d.  load() issues every load of the
+// block; dot() waits for them as it goes.
+template <int TYPE> struct RowBlock;
+template <> struct RowBlock<TIE_GGML_Q4_K> {
+	uint4 c[9];
+	__device__ __forceinline__ void load(const uint8_t *blk, const uint8_t *)
+	{
 #pragma unroll
 		for (int i = 0; i < 9; i++)
 			c[i] = *(const uint4 *)(g4 *)(blk + 1024 * i);
-		return q4k_dot(c, x);
-	} else {
-		uint4 c[13];
+	}
+	__device__ __forceinline__ float dot(dfloat *x) { return q4k_dot(c, x); }
+};
+template <> struct RowBlock<TIE_GGML_Q6_K> {
+	uint4 c[13];
+	uint32_t db;
+	__device__ __forceinline__ void load(const uint8_t *blk, const uint8_t *dp)
+	{
 #pragma unroll
 		for (int i = 0; i < 13; i++)
 			c[i] = *(const uint4 *)(g4 *)(blk + 1024 * i);
-		const uint32_t db = *(const uint16_t *)dp;
-		return q6k_dot(c, db, x);
+		db = *(const uint16_t *)dp;
 	}
+	__device__ __forceinline__ float dot(dfloat *x) { return q6k_dot(c, db, x); }
+};
+
+
+// the row's fp16 d in a Q6_K panel (the d plane after the 13 chunks)
+__device__ __forceinline__ const uint8_t *q6k_d_of(const uint8_t *blk, int row)
+{
+	return blk + Q6K_CHUNKS * 1024 - 14 * (row & 63);
+}
+
+// The dot of one (row, block) with the input segment x (all loads issued
+// before any use).
+template <int TYPE> __device__ __forceinline__ float row_block_dot(const uint8_t *blk, const uint8_t *dp, dfloat *x)
+{
+	RowBlock<TYPE> rb;
+	rb.load(blk, dp);
+	return rb.dot(x);
 }
 
 // address of row `row`, block column b of expert e (panel layout)
@@ -266,6 +304,58 @@ __device__ __forceinline__ int list_token(const DecodeArgs &a, int li)
 }
 
 // Dynamic LDS: x [nb][XSEG] | part [2 nb][R] | (INLINE) selection
+// Row sums of the gate/up partial dots part[(m nb + b) R + r] (m = 0 gate,
+// 1 up): s = 0 + p_0 + p_1 + ... in block order (math_avx2.c:762-766), one
+// thread per (matrix, row), into part[m R + r] (after a barrier).
+__device__ __forceinline__ void row_sums(float *part, int nb, int R)
+{
+	float s = 0.0f;
+	const int t = threadIdx.x;
+	if (t < 2 * R) {
+		const int m = t / R, r = t - m * R;
+#pragma unroll 8
+		for (int b = 0; b < nb; b++)
+			s = s + part[(m * nb + b) * R + r];
+	}
+	__syncthreads();
+	if (t < 2 * R)
+		part[t] = s;
+	__syncthreads();
+}
+
+// The combine of R rows from the down partial dots part[(j nb + b) R + r]:
+// y_j = serial block sum per (slot, row) on k R threads, then per row
+// out = fma(g_j, y_j, .) in slot order from +0 (model_qwen3.c:459-467;
+// slots without an expert add nothing), [res +].
+__device__ __forceinline__ void combine_rows(float *part, int nb, int k, int R, const int32_t *sel_idx,
+					     const float *sel_w, float *out, const float *res)
+{
+	const int t = threadIdx.x;
+	float y = 0.0f;
+	if (t < k * R) {
+		const int j = t / R, r = t - j * R;
+#pragma unroll 8
+		for (int b = 0; b < nb; b++)
+			y = y + part[(j * nb + b) * R + r];
+	}
+	__syncthreads();
+	if (t < k * R)
+		part[t] = y;
+	__syncthreads();
+	if (t < R) {
+		float yv[MAX_K];
+#pragma unroll
+		for (int j = 0; j < MAX_K; j++)
+			yv[j] = j < k ? part[j * R + t] : 0.0f;
+		float acc = 0.0f;
+#pragma unroll
+		for (int j = 0; j < MAX_K; j++)
+			if (j < k && sel_idx[j] >= 0)
+				acc = __builtin_fmaf(sel_w[j], yv[j], acc);
+		out[t] = res ? res[t] + acc : acc;
+	}
+}
+
 template <int TG, int TU, bool INLINE>
 __global__ __launch_bounds__(DEC_MAX_THREADS) void decode_gu_kernel(DecodeArgs a)
 {
@@ -273,6 +363,7 @@ __global__ __launch_bounds__(DEC_MAX_THREADS) void decode_gu_kernel(DecodeArgs a
 	__shared__ int32_t sel_idx[MAX_K];
 	__shared__ float sel_w[MAX_K];
 	__shared__ uint64_t etab[32];
+	__shared__ float slg[INLINE_E]; // the token's logits (E <= INLINE_E with inline routing)
 	const int R = a.R, j = blockIdx.y;
 	const int nb = a.d / QK;
 	float *xs = dl;
@@ -282,12 +373,11 @@ __global__ __launch_bounds__(DEC_MAX_THREADS) void decode_gu_kernel(DecodeArgs a
 	const int n = list_count(a);
 	for (int li = blockIdx.z; li < n; li += gridDim.z) {
 		const int t = list_token(a, li);
-		// x of the token -> LDS (independent of the routing)
-		const float4 *x4 = reinterpret_cast<const float4 *>(a.x + (size_t)t * a.d);
-		for (int i = tid; i < a.d / 4; i += blockDim.x) {
-			const int f = 4 * i;
-			*reinterpret_cast<float4 *>(xs + (f / QK) * XSEG + (f % QK)) = x4[i];
-		}
+		// x of the token (and its logits) -> LDS in one round trip
+		copy_in<4>(reinterpret_cast<const float4 *>(a.x + (size_t)t * a.d), a.d / 4, [&](int q, float4 v) {
+			const int f = 4 * q;
+			*reinterpret_cast<float4 *>(xs + (f / QK) * XSEG + (f % QK)) = v;
+		});
 		int e;
 		if constexpr (INLINE) {
 			// the token's selection from its logits (one wave), published
@@ -296,10 +386,11 @@ __global__ __launch_bounds__(DEC_MAX_THREADS) void decode_gu_kernel(DecodeArgs a
 				const uint64_t tab[32] = TIE_EXP2_TABLE;
 				etab[tid] = tab[tid];
 			}
+			for (int i = tid; i < a.E; i += blockDim.x)
+				slg[i] = a.logits[(size_t)t * a.E + i];
 			__syncthreads();
 			if (tid < 64)
-				topk_softmax_wave<2>(a.logits + (size_t)t * a.E, a.E, a.k, etab, sel_idx, sel_w, a.routing,
-						     a.pbias);
+				topk_softmax_wave<2>(slg, a.E, a.k, etab, sel_idx, sel_w, a.routing, a.pbias);
 			__syncthreads();
 			if (blockIdx.x == 0 && j == 0 && tid < a.k) {
 				a.topk_idx[(size_t)t * a.k + tid] = sel_idx[tid];
@@ -320,21 +411,16 @@ __global__ __launch_bounds__(DEC_MAX_THREADS) void decode_gu_kernel(DecodeArgs a
 							panel_bytes(mat ? TU : TG));
 			float v;
 			if (mat == 0)
-				v = row_block_dot<TG>(blk, blk + Q6K_CHUNKS * 1024 - 14 * ((r0 + r) & 63), (dfloat *)(xs + b * XSEG));
+				v = row_block_dot<TG>(blk, q6k_d_of(blk, r0 + r), (dfloat *)(xs + b * XSEG));
 			else
-				v = row_block_dot<TU>(blk, blk + Q6K_CHUNKS * 1024 - 14 * ((r0 + r) & 63), (dfloat *)(xs + b * XSEG));
+				v = row_block_dot<TU>(blk, q6k_d_of(blk, r0 + r), (dfloat *)(xs + b * XSEG));
 			part[task * R + r] = v;
 		}
 		__syncthreads();
-		if (tid < R) {
-			// serial sums over the blocks (math_avx2.c:762-766), SwiGLU
-			float g = 0.0f, up = 0.0f;
-			for (int b = 0; b < nb; b++)
-				g = g + part[b * R + tid];
-			for (int b = 0; b < nb; b++)
-				up = up + part[(nb + b) * R + tid];
-			a.h[((size_t)li * a.k + j) * a.F + r0 + tid] = tie_swiglu(g, up, a.silu);
-		}
+		// serial sums over the blocks (math_avx2.c:762-766), SwiGLU
+		row_sums(part, nb, R);
+		if (tid < R)
+			a.h[((size_t)li * a.k + j) * a.F + r0 + tid] = tie_swiglu(part[tid], part[R + tid], a.silu);
 		__syncthreads();
 	}
 }
@@ -359,12 +445,11 @@ template <int TD> __global__ __launch_bounds__(DEC_MAX_THREADS) void decode_down
 			sel_idx[tid] = a.topk_idx[(size_t)t * k + tid];
 			sel_w[tid] = a.topk_w[(size_t)t * k + tid];
 		}
-		// the k h vectors -> LDS (independent of the selection)
-		const float4 *h4 = reinterpret_cast<const float4 *>(a.h + (size_t)li * k * a.F);
-		for (int i = tid; i < k * a.F / 4; i += blockDim.x) {
-			const int f = 4 * i; // = j F + b QK + m
-			*reinterpret_cast<float4 *>(hs + (f / QK) * XSEG + (f % QK)) = h4[i];
-		}
+		// the k h vectors -> LDS (independent of the selection), one round trip
+		copy_in<8>(reinterpret_cast<const float4 *>(a.h + (size_t)li * k * a.F), k * a.F / 4, [&](int q, float4 v) {
+			const int f = 4 * q; // = j F + b QK + m
+			*reinterpret_cast<float4 *>(hs + (f / QK) * XSEG + (f % QK)) = v;
+		});
 		__syncthreads();
 		for (int u = tid; u < ntask * R; u += blockDim.x) {
 			const int r = u & (R - 1), task = u / R;
@@ -373,28 +458,12 @@ template <int TD> __global__ __launch_bounds__(DEC_MAX_THREADS) void decode_down
 			float v = 0.0f;
 			if (e >= 0) {
 				const uint8_t *blk = panel_slot(a.w[2], a.expert_bytes[2], e, r0 + r, b, nb, panel_bytes(TD));
-				v = row_block_dot<TD>(blk, blk + Q6K_CHUNKS * 1024 - 14 * ((r0 + r) & 63),
-						      (dfloat *)(hs + (size_t)task * XSEG));
+				v = row_block_dot<TD>(blk, q6k_d_of(blk, r0 + r), (dfloat *)(hs + (size_t)task * XSEG));
 			}
 			part[task * R + r] = v;
 		}
 		__syncthreads();
-		if (tid < R) {
-			// y_j = serial sum over the blocks; out = sum_j fma(g_j, y_j, .)
-			// in slot order from +0 (model_qwen3.c:459-467); slots without an
-			// expert add nothing
-			float acc = 0.0f;
-			for (int j = 0; j < k; j++) {
-				if (sel_idx[j] < 0)
-					continue;
-				float y = 0.0f;
-				for (int b = 0; b < nb; b++)
-					y = y + part[(j * nb + b) * R + tid];
-				acc = __builtin_fmaf(sel_w[j], y, acc);
-			}
-			const size_t o = (size_t)t * a.d + r0 + tid;
-			a.out[o] = a.res ? a.res[o] + acc : acc;
-		}
+		combine_rows(part, nb, k, R, sel_idx, sel_w, a.out + (size_t)t * a.d + r0, a.res ? a.res + (size_t)t * a.d + r0 : nullptr);
 		__syncthreads();
 	}
 }
@@ -415,6 +484,16 @@ static int pick_rows(int ntask, int rmax)
 	return R;
 }
 
+// rows per gate/up and down workgroup of the one-token kernels
+static int gu_rows(int nbd)
+{
+	return pick_rows(2 * nbd, 16);
+}
+static int dn_rows(int k, int nbf)
+{
+	return pick_rows(k * nbf, 8);
+}
+
 bool decode_supported(const Layer &L, int k)
 {
 	const bool q = (L.gate.type == TIE_GGML_Q4_K || L.gate.type == TIE_GGML_Q6_K) &&
@@ -428,10 +507,10 @@ bool decode_supported(const Layer &L, int k)
 	       lds_dn <= DEC_MAX_LDS;
 }
 
-template <typename K> static hipError_t dec_launch(K kern, dim3 grid, dim3 block, size_t lds, hipStream_t s,
-						     const DecodeArgs &a)
+template <typename K, typename A> static hipError_t dec_launch(K kern, dim3 grid, dim3 block, size_t lds, hipStream_t s,
+								    const A &a)
 {
-	hipError_t err = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+	hipError_t err = ensure_lds_limit((const void *)kern, lds);
 	if (err != hipSuccess)
 		return err;
 	hipLaunchKernelGGL(kern, grid, block, lds, s, a);
@@ -470,13 +549,15 @@ hipError_t launch_decode(const Layer &L, const float *x, int k, const float *sil
 	a.count = count;
 	a.routing = L.routing;
 	a.pbias = L.pbias;
-	const int nz = max_entries < 1 ? 1 : max_entries > 64 ? 64 : max_entries;
+	// a token list runs with one workgroup row per slot and loops over its
+	// entries (usually none: the launch must stay cheap)
+	const int nz = list ? 1 : (max_entries < 1 ? 1 : max_entries > 64 ? 64 : max_entries);
 	const int nbd = L.d / QK, nbf = L.F / QK;
 	hipError_t err;
 	prof_begin(fixup ? "fixup_gate_up" : "decode_gate_up", s);
 	{
 		DecodeArgs g = a;
-		g.R = pick_rows(2 * nbd, 16);
+		g.R = gu_rows(nbd);
 		const int threads = round64(2 * nbd * g.R);
 		const size_t lds = sizeof(float) * ((size_t)nbd * XSEG + 2 * nbd * g.R);
 		const dim3 grid(L.F / g.R, k, nz);
@@ -500,7 +581,7 @@ hipError_t launch_decode(const Layer &L, const float *x, int k, const float *sil
 	prof_begin(fixup ? "fixup_down" : "decode_down", s);
 	{
 		DecodeArgs g = a;
-		g.R = pick_rows(k * nbf, 8);
+		g.R = dn_rows(k, nbf);
 		const int threads = round64(k * nbf * g.R);
 		const size_t lds = sizeof(float) * ((size_t)k * nbf * XSEG + (size_t)k * nbf * g.R);
 		const dim3 grid(L.d / g.R, 1, nz);
@@ -513,3 +594,5 @@ hipError_t launch_decode(const Layer &L, const float *x, int k, const float *sil
 }
 
 } // namespace tie
+
+

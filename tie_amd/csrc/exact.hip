@@ -36,7 +36,10 @@
 // No kernel waits on another workgroup: the only ordering is the launch
 // order on the stream.
 #include <cmath>
+#include <map>
+#include <tuple>
 #include <type_traits>
+#include <unordered_map>
 
 #include "common.h"
 #include "route.h"
@@ -782,9 +785,24 @@ __global__ __launch_bounds__(BF_THREADS) void exact_down_bf16_kernel(ExactArgs a
 }
 
 // ---------------------------------------------------------------- launcher
+// Raise a kernel's dynamic-LDS limit to at least `bytes`.  The limit is
+// remembered per kernel, so the attribute call (host work on every launch
+// otherwise) happens only when a launch needs more than before.
+hipError_t ensure_lds_limit(const void *fn, size_t bytes)
+{
+	static std::unordered_map<const void *, size_t> limit;
+	auto it = limit.find(fn);
+	if (it != limit.end() && it->second >= bytes)
+		return hipSuccess;
+	const hipError_t err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+	if (err == hipSuccess)
+		limit[fn] = bytes;
+	return err;
+}
+
 static hipError_t set_lds_limit(const void *fn, size_t bytes)
 {
-	return hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+	return ensure_lds_limit(fn, bytes);
 }
 
 static int clamp_pg(int v)
@@ -813,7 +831,7 @@ static hipError_t launch_q(K kernel, dim3 grid, dim3 block, size_t lds, size_t s
 // grids here are often only slightly larger than one round, so a wave count
 // that packs more workgroups per CU, or gives each fewer columns, shortens
 // the last, partly filled round.  Ties go to more waves (at most `tasks`).
-static int pick_waves(const void *fn, size_t lds, int n_wg, int tasks)
+static int pick_waves_uncached(const void *fn, size_t lds, int n_wg, int tasks)
 {
 	static int ncu = 0;
 	if (!ncu) {
@@ -837,6 +855,19 @@ static int pick_waves(const void *fn, size_t lds, int n_wg, int tasks)
 		}
 	}
 	return best;
+}
+
+// pick_waves, memoised (the occupancy queries are host work)
+static int pick_waves(const void *fn, size_t lds, int n_wg, int tasks)
+{
+	static std::map<std::tuple<const void *, size_t, int, int>, int> memo;
+	const auto key = std::make_tuple(fn, lds, n_wg, tasks);
+	auto it = memo.find(key);
+	if (it != memo.end())
+		return it->second;
+	const int w = pick_waves_uncached(fn, lds, n_wg, tasks);
+	memo[key] = w;
+	return w;
 }
 
 // Expected number of experts with at least one pair: E (1 - (1 - k/E)^T)

@@ -787,7 +787,6 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 		using V = typename O::V;
 		constexpr int NA = NMT;
 		static_assert(C::NPL == 1 && C::NSTEP % 2 == 0, "one activation plane, even step count");
-		uint8_t *Bs = As + C::LDS_A;
 		BDma<TYPE> bd;
 		bdma_init<TYPE, DOWN>(a, e, slab, w, bd);
 		auto abuf = [&](int st) { return As + (st & 1) * C::ABUF; };
@@ -938,8 +937,11 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 					const int pc = (col & ~3) | ((col & 1) << 1) | ((col >> 1) & 1);
 					const float hs = hv * a.h_scale;
 					a.h16[(size_t)p * a.rows + pc] = __builtin_bit_cast(uint16_t, (_Float16)hs);
-					if (!(__builtin_fabsf(hs) < 65504.0f))
-						flag_token(a.tok_flag, a.fix_list, a.fix_count, a.pairs[p] / a.k);
+					if (!(__builtin_fabsf(hs) < 65504.0f)) {
+						const int tok = a.pairs[p] / a.k;
+						if (a.tok_flag[tok] == 0) // listed already: no atomic
+							flag_token(a.tok_flag, a.fix_list, a.fix_count, tok);
+					}
 				} else {
 					const uint16_t hi = bf16_bits(hv);
 					a.h16[(size_t)p * a.rows + col] = hi;

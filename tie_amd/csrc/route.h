@@ -33,6 +33,70 @@ __device__ __forceinline__ float hsum8_lanes(float v)
 	return a + dppf<DPP_SHL2>(a);          // lane 0: (s0 + s1) + (s2 + s3)
 }
 
+// TIE's router chain for lane l of 8 (mat_vec_row_f32_f32_f32_avx2): acc
+// = fma(x[8i + l], w[8i + l], acc) for i ascending.  x and w sit in LDS
+// lane-major (stage_lane_major: lane l's elements 8i + l contiguous, rows
+// padded to start in different banks), so one 16-byte read brings 4 steps
+// and the reads of the next 16 steps are in flight while 16 FMAs run.
+__device__ __forceinline__ int lane_major_stride(int d)
+{
+	return d / 8 + 4;
+}
+__device__ __host__ __forceinline__ int lane_major_floats(int d)
+{
+	return 8 * (d / 8 + 4);
+}
+
+// x[0..d) (global) -> dst[(f % 8) * stride + f / 8] (LDS), all threads
+__device__ __forceinline__ void stage_lane_major(float *dst, const float *src, int d)
+{
+	const int st = lane_major_stride(d);
+	copy_in<4>(reinterpret_cast<const float4 *>(src), d / 4, [&](int q, float4 v) {
+		const int f = 4 * q, l = f & 7, i = f >> 3;
+		dst[(l + 0) * st + i] = v.x;
+		dst[(l + 1) * st + i] = v.y;
+		dst[(l + 2) * st + i] = v.z;
+		dst[(l + 3) * st + i] = v.w;
+	});
+}
+
+__device__ __forceinline__ float lane_chain(const float *xs, const float *ws, int d, int l)
+{
+	typedef float f4 __attribute__((ext_vector_type(4)));
+	const int st = lane_major_stride(d), n = d / 8;
+	const f4 *xl = reinterpret_cast<const f4 *>(xs + l * st);
+	const f4 *wl = reinterpret_cast<const f4 *>(ws + l * st);
+	float acc = 0.0f;
+	f4 xa[4], wa[4];
+#pragma unroll
+	for (int u = 0; u < 4; u++) {
+		xa[u] = xl[u];
+		wa[u] = wl[u];
+	}
+	for (int i = 0; i < n; i += 16) {
+		f4 xb[4], wb[4];
+		const int nx = (i + 16 < n ? i + 16 : i) / 4;
+#pragma unroll
+		for (int u = 0; u < 4; u++) {
+			xb[u] = xl[nx + u];
+			wb[u] = wl[nx + u];
+		}
+#pragma unroll
+		for (int u = 0; u < 4; u++) {
+			acc = __builtin_fmaf(xa[u].x, wa[u].x, acc);
+			acc = __builtin_fmaf(xa[u].y, wa[u].y, acc);
+			acc = __builtin_fmaf(xa[u].z, wa[u].z, acc);
+			acc = __builtin_fmaf(xa[u].w, wa[u].w, acc);
+		}
+#pragma unroll
+		for (int u = 0; u < 4; u++) {
+			xa[u] = xb[u];
+			wa[u] = wb[u];
+		}
+	}
+	return acc;
+}
+
 __device__ __forceinline__ uint32_t umax32(uint32_t a, uint32_t b)
 {
 	return a > b ? a : b;
@@ -84,6 +148,46 @@ __device__ __forceinline__ float key_logit(uint32_t k)
 	return __builtin_bit_cast(float, (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
 
+constexpr int ROUTE_SOFTMAX = 0, ROUTE_SIGMOID = 1;
+
+// The gate weights of the k selected slots, on lane j of the wave: my_s
+// is slot j's logit (softmax) or unbiased p (sigmoid), my_i its expert
+// (-inf / -1 on lanes of unfilled slots and lanes >= k).
+__device__ __forceinline__ void topk_weights_wave(float my_s, int my_i, int k, const uint64_t *etab, int32_t *out_idx,
+						  float *out_w, bool sig)
+{
+	const int lane = threadIdx.x & 63;
+	if (sig) {
+		// L1 normalisation of the selected p (unfilled slots add nothing)
+		const float pj = my_i >= 0 ? my_s : 0.0f;
+		float sum = 0.0f;
+		for (int j = 0; j < k; j++)
+			sum = sum + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pj), j));
+		const float inv = __fdiv_rn(1.0f, sum + 1e-6f);
+		if (lane < k) {
+			out_w[lane] = pj * inv;
+			out_idx[lane] = my_i;
+		}
+		return;
+	}
+	// softmax over the k selected logits: max over the slots, exp per lane
+	float mx = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_s), 0));
+	for (int j = 1; j < k; j++) {
+		const float sj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_s), j));
+		if (sj > mx)
+			mx = sj;
+	}
+	const float ev = lane < k ? tie_expf_tab(my_s - mx, etab) : 0.0f;
+	float sum = 0.0f;
+	for (int j = 0; j < k; j++)
+		sum = sum + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ev), j));
+	const float inv = __fdiv_rn(1.0f, sum);
+	if (lane < k) {
+		out_w[lane] = ev * inv;
+		out_idx[lane] = my_i;
+	}
+}
+
 // Expert selection of one token, by one wave; PER logits per lane (E <= 64
 // * PER), entry e = 64q + lane in register q.
 //
@@ -105,8 +209,6 @@ __device__ __forceinline__ float key_logit(uint32_t k)
 // scalar round trip.  NaN and -inf never qualify; unfilled slots are
 // {-1, -inf} with weight 0.  `lg` and `pbias` may be
 // global or LDS memory.
-constexpr int ROUTE_SOFTMAX = 0, ROUTE_SIGMOID = 1;
-
 template <int PER>
 __device__ __forceinline__ void topk_softmax_wave(const float *lg, int E, int k, const uint64_t *etab,
 						  int32_t *out_idx, float *out_w, int routing = ROUTE_SOFTMAX,
@@ -167,35 +269,7 @@ __device__ __forceinline__ void topk_softmax_wave(const float *lg, int E, int k,
 			if ((uint32_t)(64 * q + lane) == be)
 				key[q] = 0;
 	}
-	if (sig) {
-		// L1 normalisation of the selected p (unfilled slots add nothing)
-		const float pj = my_i >= 0 ? my_s : 0.0f;
-		float sum = 0.0f;
-		for (int j = 0; j < k; j++)
-			sum = sum + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pj), j));
-		const float inv = __fdiv_rn(1.0f, sum + 1e-6f);
-		if (lane < k) {
-			out_w[lane] = pj * inv;
-			out_idx[lane] = my_i;
-		}
-		return;
-	}
-	// softmax over the k selected logits: max over the slots, exp per lane
-	float mx = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_s), 0));
-	for (int j = 1; j < k; j++) {
-		const float sj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_s), j));
-		if (sj > mx)
-			mx = sj;
-	}
-	const float ev = lane < k ? tie_expf_tab(my_s - mx, etab) : 0.0f;
-	float sum = 0.0f;
-	for (int j = 0; j < k; j++)
-		sum = sum + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ev), j));
-	const float inv = __fdiv_rn(1.0f, sum);
-	if (lane < k) {
-		out_w[lane] = ev * inv;
-		out_idx[lane] = my_i;
-	}
+	topk_weights_wave(my_s, my_i, k, etab, out_idx, out_w, sig);
 }
 
 // topk_softmax_wave with PER chosen for E (E <= MAX_E)

@@ -38,33 +38,22 @@ __global__ __launch_bounds__(RS_THREADS) void router_small_kernel(const float *_
 								  const float *__restrict__ bias, int T, int d, int E,
 								  float *__restrict__ logits)
 {
-	extern __shared__ float lds[]; // W row [d] | x [RS_TOK][d]
+	extern __shared__ float lds[]; // W row | x [RS_TOK], lane-major (lane_chain)
 	float *ws = lds;
-	float *xs = lds + d;
+	float *xs = lds + lane_major_floats(d);
 	const int e = blockIdx.x;
 	const int nt = min(RS_TOK, T);
 	const int tid = threadIdx.x;
-	const int d4 = d >> 2;
 
-	const float4 *W4 = reinterpret_cast<const float4 *>(W + (size_t)e * d);
-	for (int i = tid; i < d4; i += RS_THREADS)
-		reinterpret_cast<float4 *>(ws)[i] = W4[i];
-	for (int t = 0; t < nt; t++) {
-		const float4 *x4 = reinterpret_cast<const float4 *>(x + (size_t)t * d);
-		for (int i = tid; i < d4; i += RS_THREADS)
-			reinterpret_cast<float4 *>(xs + (size_t)t * d)[i] = x4[i];
-	}
+	// the row and the tokens -> LDS, lane-major
+	stage_lane_major(ws, W + (size_t)e * d, d);
+	for (int t = 0; t < nt; t++)
+		stage_lane_major(xs + t * lane_major_floats(d), x + (size_t)t * d, d);
 	__syncthreads();
 	if (tid >= RS_TOK * 8)
 		return;
 	const int t = tid >> 3, l = tid & 7;
-	float acc = 0.0f;
-	if (t < nt) {
-		const float *xt = xs + (size_t)t * d;
-#pragma unroll 16
-		for (int i = 0; i < d; i += 8)
-			acc = __builtin_fmaf(xt[i + l], ws[i + l], acc);
-	}
+	const float acc = t < nt ? lane_chain(xs + (size_t)t * lane_major_floats(d), ws, d, l) : 0.0f;
 	const float r = hsum8_lanes(acc);
 	if (l == 0 && t < nt)
 		logits[(size_t)t * E + e] = bias ? r + bias[e] : r;
@@ -302,8 +291,8 @@ __global__ __launch_bounds__(RW_THREADS) void router_topk_kernel(const float *__
 hipError_t launch_router_logits(const Layer &L, const float *x, int T, float *logits, hipStream_t s)
 {
 	const int d = L.d, E = L.E;
-	if (T <= RS_TOK && sizeof(float) * (size_t)d * (1 + RS_TOK) <= 160 * 1024) {
-		const size_t lds = sizeof(float) * (size_t)d * (1 + RS_TOK);
+	if (T <= RS_TOK && sizeof(float) * (size_t)(8 * (d / 8 + 4)) * (1 + RS_TOK) <= 160 * 1024) {
+		const size_t lds = sizeof(float) * (size_t)(8 * (d / 8 + 4)) * (1 + RS_TOK);
 		hipLaunchKernelGGL(router_small_kernel, dim3(E), dim3(RS_THREADS), lds, s, x, L.router, L.bias, T, d, E,
 				   logits);
 		return hipGetLastError();
