@@ -59,3 +59,55 @@ def test_exact_threshold_setter():
     lib.tie_hip_set_exact_max_tokens(-3)
     assert lib.tie_hip_exact_max_tokens() == 0
     lib.tie_hip_set_exact_max_tokens(old)
+
+
+C_CALLER = r"""
+#include <stdio.h>
+#include <stdint.h>
+#include "tie_hip.h"
+
+/* the call site INTEGRATION.md shows, reduced to what runs without a GPU:
+ * every prototype used with TIE's own argument types */
+int main(void)
+{
+	static float table[TIE_SILU_TABLE_SIZE];
+	float in[2] = {0.0f, -1.5f}, out[2];
+	tie_hip_model_info info;
+	int32_t idx[8];
+	float w[8];
+	int rc;
+	tie_hip_host_expf(in, out, 2);
+	rc = tie_hip_silu_table_host(table, TIE_SILU_TABLE_SIZE);
+	if (rc != TIE_HIP_OK || out[0] != 1.0f)
+		return 1;
+	/* no device: a clear error code, no exit */
+	rc = tie_hip_moe_ffn(in, 0, 2048, 768, 128, 8, table, TIE_GGML_F32, table, TIE_GGML_Q4_K, table,
+			     TIE_GGML_Q4_K, table, TIE_GGML_Q6_K, out, idx, w);
+	if (rc != TIE_HIP_ENOINIT)
+		return 2;
+	rc = tie_hip_gguf_inspect("/nonexistent.gguf", &info);
+	if (rc == TIE_HIP_OK)
+		return 3;
+	printf("%s\n", tie_hip_last_error());
+	return 0;
+}
+"""
+
+
+def test_header_compiles_as_c99_and_links(tmp_path):
+    """A C translation unit compiled the way TIE compiles (gcc, C99, all
+    warnings as errors) against include/tie_hip.h, linked with
+    libtie_hip.so, and run: the prototypes INTEGRATION.md relies on are
+    plain C and the library answers without a GPU."""
+    import subprocess
+    src = tmp_path / "caller.c"
+    src.write_text(C_CALLER)
+    exe = tmp_path / "caller"
+    libdir = os.path.dirname(tie_amd.LIB_PATH)
+    cmd = ["gcc", "-std=c99", "-Wall", "-Wextra", "-Werror", "-pedantic", "-I", os.path.join(ROOT, "include"),
+           str(src), "-o", str(exe), "-L", libdir, "-ltie_hip", "-Wl,-rpath," + libdir]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    env = dict(os.environ, HIP_VISIBLE_DEVICES="", ROCR_VISIBLE_DEVICES="")
+    r = subprocess.run([str(exe)], capture_output=True, text=True, env=env, timeout=120)
+    assert r.returncode == 0, (r.returncode, r.stdout, r.stderr)
