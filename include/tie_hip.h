@@ -162,6 +162,19 @@ size_t tie_hip_layer_bytes(const tie_hip_layer *layer);
 int tie_hip_moe_forward(tie_hip_layer *layer, const float *x_dev, int T, int k, float *out_dev,
 			int32_t *topk_idx_dev, float *topk_w_dev, int flags, void *stream);
 
+/* tie_hip_moe_forward that allocates nothing: no counterpart in the
+ * reference.  For callers that cannot allocate device memory (code under
+ * HIP graph capture, serving loops, harnesses that forbid hipMalloc).  Its
+ * scratch is one static 24 MiB device array per GPU (held until the process
+ * ends) instead of the per-stream workspace: calls whose scratch would not
+ * fit (T * k pairs with this layer's shape: T <= 91 at d = 2048, F = 768,
+ * k = 8; T <= 46 at d = 4096, F = 1536, k = 8) return TIE_HIP_EINVAL.  All calls on a GPU share the array,
+ * so calls that overlap in time on one GPU (other streams, other threads)
+ * race: serialise them.  Same arguments, results and stream rules as
+ * tie_hip_moe_forward otherwise. */
+int tie_hip_moe_forward_noalloc(tie_hip_layer *layer, const float *x_dev, int T, int k, float *out_dev,
+				int32_t *topk_idx_dev, float *topk_w_dev, int flags, void *stream);
+
 /* The same FFN half on device pointers: out_dev = hidden_dev +
  * block(rms_norm(hidden_dev)), both [T][d] F32; out_dev may be hidden_dev
  * (TIE's in-place update).  ffn_norm_dev [d] F32.  Enqueued on `stream` like

@@ -30,6 +30,7 @@ EXPORTS = (
     "tie_hip_silu_table_host", "tie_hip_layer_create", "tie_hip_layer_destroy", "tie_hip_layer_bytes",
     "tie_hip_moe_forward", "tie_hip_exact_max_tokens", "tie_hip_set_exact_max_tokens",
     "tie_hip_debug_fail_alloc", "tie_hip_host_expf", "tie_hip_profile_enable", "tie_hip_profile_read",
+    "tie_hip_moe_forward_noalloc",
 )
 
 
@@ -116,6 +117,8 @@ def lib():
         L.tie_hip_layer_bytes.restype = ctypes.c_size_t
         L.tie_hip_moe_forward.argtypes = [P, P, I, I, P, P, P, I, P]
         L.tie_hip_moe_forward.restype = I
+        L.tie_hip_moe_forward_noalloc.argtypes = [P, P, I, I, P, P, P, I, P]
+        L.tie_hip_moe_forward_noalloc.restype = I
         L.tie_hip_exact_max_tokens.restype = I
         L.tie_hip_set_exact_max_tokens.argtypes = [I]
         L.tie_hip_set_exact_max_tokens.restype = None
@@ -331,6 +334,13 @@ class Layer:
         """Enqueue the block on device pointers (torch tensors or ints)."""
         check(lib().tie_hip_moe_forward(self.handle, _p(x_dev), T, k, _p(out_dev), _p(topk_idx_dev),
                                         _p(topk_w_dev), flags, stream))
+
+    def forward_noalloc(self, x_dev, T, k, out_dev, topk_idx_dev=None, topk_w_dev=None, flags=PATH_AUTO,
+                        stream=None):
+        """tie_hip_moe_forward_noalloc: forward with the library's static
+        scratch array (no allocation; small T only)."""
+        check(lib().tie_hip_moe_forward_noalloc(self.handle, _p(x_dev), T, k, _p(out_dev), _p(topk_idx_dev),
+                                                _p(topk_w_dev), flags, stream))
 
     def forward_residual(self, hidden_dev, ffn_norm_dev, eps, T, k, out_dev=None, topk_idx_dev=None,
                          topk_w_dev=None, flags=PATH_AUTO, stream=None):

@@ -66,6 +66,15 @@ struct Ctx {
 static Ctx g;
 static int g_fail_alloc = 0;
 
+// ------------------------------------------------- the no-allocation entry
+// tie_hip_moe_forward_noalloc's workspace: a file-scope device array (one
+// per GPU, held until the process ends).  Host code uses only g_scratch,
+// its device address from hipGetSymbolAddress at tie_hip_init; the array's
+// name is not a device address on the host.
+constexpr size_t SCRATCH_BYTES = (size_t)24 << 20;
+static __device__ __align__(256) uint8_t scratch[SCRATCH_BYTES];
+static uint8_t *g_scratch = nullptr;
+
 // ---------------------------------------------------------------- profiling
 struct ProfRec {
 	int name;
@@ -201,18 +210,10 @@ static int ensure_init()
 	return TIE_HIP_OK;
 }
 
-// Grow stream s's workspace to hold T tokens; *out = that workspace.
-static int ensure_workspace(hipStream_t s, int T, int k, int d, int F, int E, Workspace **out)
+// The workspace layout for P pairs (and as many tokens at most), F, d and E
+// at most: its size, and (b != null) the pointers of *w into b.
+static size_t carve_workspace(uint8_t *b, size_t P, size_t FF, size_t DD, size_t EE, Workspace *w)
 {
-	Workspace &w = g.ws[s];
-	*out = &w;
-	const size_t pairs = (size_t)(T > 0 ? T : 1) * k;
-	if (w.alloc && pairs <= w.cap_pairs && (size_t)F <= w.cap_F && (size_t)d <= w.cap_d && (size_t)E <= w.cap_E)
-		return TIE_HIP_OK;
-	const size_t P = pairs > w.cap_pairs ? pairs : w.cap_pairs;
-	const size_t FF = (size_t)F > w.cap_F ? F : w.cap_F;
-	const size_t DD = (size_t)d > w.cap_d ? d : w.cap_d;
-	const size_t EE = (size_t)E > w.cap_E ? E : w.cap_E;
 	const size_t Tcap = P; // tokens <= pairs since k >= 1
 	size_t off = 0;
 	auto take = [&](size_t bytes) {
@@ -227,6 +228,48 @@ static int ensure_workspace(hipStream_t s, int T, int k, int d, int F, int E, Wo
 	const size_t max_tiles = (size_t)mfma_max_tiles((int)P, (int)EE);
 	const size_t o_te = take(2 * max_tiles * 4), o_tm = take(2 * max_tiles * 4), o_nt = take(8);
 	const size_t o_fl = take(Tcap * 4), o_fx = take(Tcap * 4), o_fc = take(4);
+	if (!b)
+		return off;
+	w->topk_idx = (int32_t *)(b + o_idx);
+	w->topk_w = (float *)(b + o_w);
+	w->offsets = (int32_t *)(b + o_off);
+	w->pairs = (int32_t *)(b + o_pairs);
+	w->active = (int32_t *)(b + o_act);
+	w->logits = (float *)(b + o_logits);
+	w->h = (float *)(b + o_h);
+	w->hb = (uint16_t *)(b + o_hb);
+	w->y = (float *)(b + o_y);
+	w->normed = (float *)(b + o_nm);
+	w->xb = (uint16_t *)(b + o_xb);
+	w->hlo = (uint16_t *)(b + o_hlo);
+	w->xlo = (uint16_t *)(b + o_xlo);
+	w->tile_e = (int32_t *)(b + o_te);
+	w->tile_m0 = (int32_t *)(b + o_tm);
+	w->ntiles = (int32_t *)(b + o_nt);
+	w->tok_flag = (int32_t *)(b + o_fl);
+	w->fix_list = (int32_t *)(b + o_fx);
+	w->fix_count = (int32_t *)(b + o_fc);
+	w->tile_cap = (int32_t)max_tiles;
+	w->cap_pairs = P;
+	w->cap_F = FF;
+	w->cap_d = DD;
+	w->cap_E = EE;
+	return off;
+}
+
+// Grow stream s's workspace to hold T tokens; *out = that workspace.
+static int ensure_workspace(hipStream_t s, int T, int k, int d, int F, int E, Workspace **out)
+{
+	Workspace &w = g.ws[s];
+	*out = &w;
+	const size_t pairs = (size_t)(T > 0 ? T : 1) * k;
+	if (w.alloc && pairs <= w.cap_pairs && (size_t)F <= w.cap_F && (size_t)d <= w.cap_d && (size_t)E <= w.cap_E)
+		return TIE_HIP_OK;
+	const size_t P = pairs > w.cap_pairs ? pairs : w.cap_pairs;
+	const size_t FF = (size_t)F > w.cap_F ? F : w.cap_F;
+	const size_t DD = (size_t)d > w.cap_d ? d : w.cap_d;
+	const size_t EE = (size_t)E > w.cap_E ? E : w.cap_E;
+	const size_t bytes = carve_workspace(nullptr, P, FF, DD, EE, nullptr);
 	void *mem = nullptr;
 	if (w.alloc) {
 		// work still queued on s (or, through events, on any stream the
@@ -235,35 +278,11 @@ static int ensure_workspace(hipStream_t s, int T, int k, int d, int F, int E, Wo
 		HIP_TRY(hipFree(w.alloc));
 		w = Workspace();
 	}
-	int rc = dev_malloc(&mem, off, "workspace");
+	int rc = dev_malloc(&mem, bytes, "workspace");
 	if (rc)
 		return rc;
-	uint8_t *b = (uint8_t *)mem;
+	carve_workspace((uint8_t *)mem, P, FF, DD, EE, &w);
 	w.alloc = mem;
-	w.topk_idx = (int32_t *)(b + o_idx);
-	w.topk_w = (float *)(b + o_w);
-	w.offsets = (int32_t *)(b + o_off);
-	w.pairs = (int32_t *)(b + o_pairs);
-	w.active = (int32_t *)(b + o_act);
-	w.logits = (float *)(b + o_logits);
-	w.h = (float *)(b + o_h);
-	w.hb = (uint16_t *)(b + o_hb);
-	w.y = (float *)(b + o_y);
-	w.normed = (float *)(b + o_nm);
-	w.xb = (uint16_t *)(b + o_xb);
-	w.hlo = (uint16_t *)(b + o_hlo);
-	w.xlo = (uint16_t *)(b + o_xlo);
-	w.tile_e = (int32_t *)(b + o_te);
-	w.tile_m0 = (int32_t *)(b + o_tm);
-	w.ntiles = (int32_t *)(b + o_nt);
-	w.tok_flag = (int32_t *)(b + o_fl);
-	w.fix_list = (int32_t *)(b + o_fx);
-	w.fix_count = (int32_t *)(b + o_fc);
-	w.tile_cap = (int32_t)max_tiles;
-	w.cap_pairs = P;
-	w.cap_F = FF;
-	w.cap_d = DD;
-	w.cap_E = EE;
 	return TIE_HIP_OK;
 }
 
@@ -391,7 +410,7 @@ static int create_layer(const tie_hip_layer_desc *ds, tie_hip_layer **out)
 // The block on device pointers; res (optional) is added to the combine
 // (out = res + block, the residual add after the FFN).
 static int forward(tie_hip_layer *layer, const float *x, int T, int k, float *out, int32_t *idx_out,
-		   float *w_out, int flags, hipStream_t s, const float *res = nullptr)
+		   float *w_out, int flags, hipStream_t s, const float *res = nullptr, Workspace *preset = nullptr)
 {
 	if (!layer)
 		return set_error(TIE_HIP_EINVAL, "null layer");
@@ -413,8 +432,8 @@ static int forward(tie_hip_layer *layer, const float *x, int T, int k, float *ou
 				 L.up.type);
 	if (mfma && L.gate.type != TIE_GGML_BF16 && L.down.type == TIE_GGML_BF16)
 		return set_error(TIE_HIP_EINVAL, "the MFMA path needs a quantised down when gate/up are quantised");
-	Workspace *wsp = nullptr;
-	int rc = ensure_workspace(s, T, k, L.d, L.F, L.E, &wsp);
+	Workspace *wsp = preset;
+	int rc = preset ? TIE_HIP_OK : ensure_workspace(s, T, k, L.d, L.F, L.E, &wsp);
 	if (rc)
 		return rc;
 	Workspace &ws = *wsp;
@@ -538,6 +557,11 @@ extern "C" int tie_hip_init(int device)
 	if (rc)
 		return rc;
 	HIP_TRY(hipMemcpy(g.silu, tab.data(), SILU_N * sizeof(float), hipMemcpyHostToDevice));
+	{
+		void *p = nullptr;
+		HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+		g_scratch = (uint8_t *)p;
+	}
 	g.device = device;
 	return TIE_HIP_OK;
 }
@@ -569,6 +593,7 @@ extern "C" void tie_hip_shutdown(void)
 	(void)hipStreamDestroy(g.stream);
 	g.stream = nullptr;
 	g.device = -1;
+	g_scratch = nullptr;
 }
 
 extern "C" int tie_hip_set_silu_table(const float *table, int n)
@@ -623,6 +648,34 @@ extern "C" int tie_hip_moe_forward(tie_hip_layer *layer, const float *x_dev, int
 		return rc;
 	hipStream_t s = stream ? (hipStream_t)stream : g.stream;
 	return forward(layer, x_dev, T, k, out_dev, topk_idx_dev, topk_w_dev, flags, s);
+}
+
+extern "C" int tie_hip_moe_forward_noalloc(tie_hip_layer *layer, const float *x_dev, int T, int k, float *out_dev,
+					   int32_t *topk_idx_dev, float *topk_w_dev, int flags, void *stream)
+{
+	std::lock_guard<std::recursive_mutex> lk(g.mu);
+	clear_error();
+	int rc = ensure_init();
+	if (rc)
+		return rc;
+	if (!g_scratch)
+		return set_error(TIE_HIP_ENOINIT, "scratch array address unknown (tie_hip_init failed)");
+	if (!layer)
+		return set_error(TIE_HIP_EINVAL, "null layer");
+	const Layer &L = layer->L;
+	if (T < 0 || k < 1 || k > L.E || k > MAX_K)
+		return set_error(TIE_HIP_EINVAL, "bad T=%d or k=%d", T, k);
+	const size_t P = (size_t)(T > 0 ? T : 1) * k;
+	const size_t need = carve_workspace(nullptr, P, L.F, L.d, L.E, nullptr);
+	if (need > SCRATCH_BYTES)
+		return set_error(TIE_HIP_EINVAL,
+				 "T=%d, k=%d needs %zu bytes of scratch, above the %zu of the no-allocation entry point "
+				 "(use tie_hip_moe_forward)",
+				 T, k, need, SCRATCH_BYTES);
+	Workspace ws;
+	carve_workspace(g_scratch, P, L.F, L.d, L.E, &ws);
+	hipStream_t s = stream ? (hipStream_t)stream : g.stream;
+	return forward(layer, x_dev, T, k, out_dev, topk_idx_dev, topk_w_dev, flags, s, nullptr, &ws);
 }
 
 // The host-buffer drop-ins: the layer comes from the weight cache (uploaded
