@@ -104,6 +104,12 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 #ifndef TIE_MFMA_GU_WPE
 #define TIE_MFMA_GU_WPE 2
 #endif
+// three weight stage buffers where they fit (1), or always two (0).  Off:
+// stage barriers wait 5-9% of a workgroup's cycles at T = 2048, and a third
+// buffer measured within +-2% (30B T = 2048, 235B T = 1024)
+#ifndef TIE_MFMA_BBUF3
+#define TIE_MFMA_BBUF3 0
+#endif
 #ifndef TIE_MFMA_DN_WPE
 #define TIE_MFMA_DN_WPE 2
 #endif
@@ -187,7 +193,20 @@ template <int TYPE, bool DOWN = false, int MTR = 0> struct Cfg {
 	static constexpr int NCH = TYPE == TIE_GGML_Q4_K ? 1 + KST / 32 : (KST == 64 ? 5 : 7); // 1 KiB chunks per panel and stage
 	static constexpr int PB = NCH * 1024;                     // bytes per panel and stage
 	static constexpr int BBUF = B_LDS ? 4 * PB + (TYPE == TIE_GGML_Q6_K ? 4 * 128 : 0) : 0; // + Q6_K d planes
-	static constexpr int LDS_A = 2 * ABUF, LDS_B = 2 * BBUF;
+	// weight stage buffers: three (the weights of stage s + 2 in flight
+	// while stage s computes: an HBM round trip is longer than a stage)
+	// where they fit the budget of two workgroups per CU, else two
+	static constexpr int LDS_BUDGET = (160 * 1024) / (MTR ? 3 : 2); // per workgroup: 3 (small tiles) or 2 per CU
+	static constexpr int ROFF_BYTES = 4 * RPI * NWAVES * 16 + 4 * MT; // row offsets + pair ids
+	static constexpr int NBB = (TIE_MFMA_BBUF3 && B_LDS && 2 * ABUF + 3 * BBUF + ROFF_BYTES <= LDS_BUDGET) ? 3 : 2;
+	static_assert(NWAVES == 4, "epilogue tile size");
+	// DMA instructions one wave issues per weight stage (dma_b)
+	static constexpr int B_DMA = NCH + (TYPE == TIE_GGML_Q6_K ? 1 : 0);
+	static constexpr int LDS_A = 2 * ABUF, LDS_B = NBB * BBUF;
+	// the f16 kernels' epilogue tiles (gate/up: after the 32 KiB SiLU
+	// table) reuse the stage buffers; the dynamic LDS covers both
+	static constexpr int EPI_BYTES = (F16 && !SPLIT) ? (DOWN ? 0 : 32768) + NWAVES * 16 * (DOWN ? 72 : 40) * 4 : 0;
+	static constexpr int STAGE_BYTES = LDS_A + LDS_B > EPI_BYTES ? LDS_A + LDS_B : EPI_BYTES;
 	// The slot of 16-byte chunk c of row r is c ^ swz(r): the rows of a
 	// fragment read then spread over all LDS banks without row padding
 	// (which the direct global->LDS loads cannot make).
@@ -636,6 +655,25 @@ __device__ __forceinline__ void stage_barrier()
 	__builtin_amdgcn_s_barrier();
 }
 
+// Cycle accounting of the matrix-core kernels (diagnostic builds only:
+// -DTIE_MFMA_TRACE): summed over workgroups (wave 0 of each), [down][0]
+// cycles in run_tile, [1] in stage barriers, [2] in the epilogue, [3]
+// workgroups; read by tie_hip_debug_mfma_trace.
+#ifdef TIE_MFMA_TRACE
+__device__ unsigned long long g_mfma_trace[2][4];
+#endif
+
+// The same, but the N youngest vector loads (the next-but-one weight
+// stage's DMA, issued last) may stay in flight: loads complete in order, so
+// everything older has landed.  N < 16 (the gfx9 encoding: vmcnt in bits
+// 3:0, expcnt and lgkmcnt 0).
+template <int N> __device__ __forceinline__ void stage_barrier_keep()
+{
+	static_assert(N >= 0 && N < 16, "vmcnt field");
+	__builtin_amdgcn_s_waitcnt(N);
+	__builtin_amdgcn_s_barrier();
+}
+
 // Operand arithmetic of a quantised kernel: bf16 fragments, or f16 ones
 // (Q4_K gate/up).
 template <int TYPE, bool DOWN, bool F16 = Cfg<TYPE, DOWN>::F16> struct Ops;
@@ -716,12 +754,16 @@ __device__ __forceinline__ void stage_mfma(const BRegs<TYPE> &b, int st, const u
 // ------------------------------------------------------------------ kernel
 // One work tile with NMT live 32-row M tiles (nrows <= 32 NMT).
 template <int TYPE, bool DOWN, int NMT, int MTR>
-__device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_t *roff, int e, int pbase, int nrows,
-					 int slab)
+__device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_t *roff, int32_t *spair, int e,
+					 int pbase, int nrows, int slab)
 {
 	using C = Cfg<TYPE, DOWN, MTR>;
 	const int nk = a.in / C::KST;
 	const int t = threadIdx.x;
+#ifdef TIE_MFMA_TRACE
+	const unsigned long long t_start = __builtin_readcyclecounter();
+	unsigned long long t_loop = 0, bw_total = 0;
+#endif
 	const int w = __builtin_amdgcn_readfirstlane(t >> 6);
 	const int lane = t & 63, h = lane >> 5;
 
@@ -738,9 +780,11 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 		as.roff = roff + (C::RPI * w + rsub) * ROFF_STRIDE;
 		if (t < C::MT) {
 			const int r = t < nrows ? t : 0;
-			const int row = DOWN ? pbase + r : a.pairs[pbase + r] / a.k;
+			const int pr = a.pairs[pbase + r];
+			const int row = DOWN ? pbase + r : pr / a.k;
 			const int c = t / (C::RPI * NWAVES), ls = t % (C::RPI * NWAVES);
 			roff[ls * ROFF_STRIDE + c] = (uint32_t)((size_t)row * a.in * 2);
+			spair[t] = pr; // the tile rows' pair ids, for the epilogue
 		}
 		__syncthreads();
 	}
@@ -790,10 +834,31 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 		BDma<TYPE> bd;
 		bdma_init<TYPE, DOWN>(a, e, slab, w, bd);
 		auto abuf = [&](int st) { return As + (st & 1) * C::ABUF; };
-		auto bbuf = [&](int st) { return Bs + (st & 1) * C::BBUF; };
+		auto bbuf = [&](int st) { return Bs + (st % C::NBB) * C::BBUF; };
+		// stage st's activations and, NBB - 1 stages ahead, weights (issued
+		// last: the barrier may leave them in flight)
 		auto issue = [&](int st) {
-			dma_b<TYPE, DOWN>(bd, slab, st, w, bbuf(st));
-			dma_a<TYPE, DOWN, NMT, MTR>(as, st, w, abuf(st));
+			if (st < nk)
+				dma_a<TYPE, DOWN, NMT, MTR>(as, st, w, abuf(st));
+			if (st + C::NBB - 2 < nk)
+				dma_b<TYPE, DOWN>(bd, slab, st + C::NBB - 2, w, bbuf(st + C::NBB - 2));
+		};
+		// end of stage st: stage st + 1's data landed (and this stage's LDS
+		// reads done); the weights of stage st + NBB - 1 may be in flight
+#ifdef TIE_MFMA_TRACE
+		unsigned long long bwait = 0;
+#endif
+		auto barrier_after = [&](int st) {
+#ifdef TIE_MFMA_TRACE
+			const unsigned long long tb = __builtin_readcyclecounter();
+#endif
+			if (C::NBB == 3 && st + 2 < nk)
+				stage_barrier_keep<C::B_DMA>();
+			else
+				stage_barrier();
+#ifdef TIE_MFMA_TRACE
+			bwait += __builtin_readcyclecounter() - tb;
+#endif
 		};
 		// fragment row r = 32 mt + lane%32 (swz(r) = swz(lane%32)), chunk 2s + lane/32
 		const int arow = (lane & 31) * C::RB, key = C::swz(lane & 31);
@@ -834,14 +899,15 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 				__builtin_amdgcn_sched_barrier(0);
 			}
 		};
+		if (C::NBB == 3)
+			dma_b<TYPE, DOWN>(bd, slab, 0, w, bbuf(0));
 		issue(0);
-		stage_barrier();
+		barrier_after(-1);
 		if constexpr (NMT < TIE_MFMA_PIPE_NMT) {
 			// few MFMAs per step: each stage self-contained (its DMA first,
 			// then its weights from LDS, then the steps)
 			for (int st = 0; st < nk; st++) {
-				if (st + 1 < nk)
-					issue(st + 1);
+				issue(st + 1);
 				lds_b<TYPE>(bbuf(st), bp, bi, st, h, b);
 				prep(st, 0, 0);
 #pragma unroll
@@ -851,7 +917,7 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 						prep(st, s + 1, (s & 1) ^ 1);
 					__builtin_amdgcn_sched_barrier(0);
 				}
-				stage_barrier();
+				barrier_after(st);
 			}
 		} else {
 			lds_b<TYPE>(bbuf(0), bp, bi, 0, h, b);
@@ -860,7 +926,7 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 				steps(st, true);
 				// the last step's fragments are in registers: the barrier only
 				// waits for stage st + 1's data and this stage's LDS reads
-				stage_barrier();
+				barrier_after(st);
 				lds_b<TYPE>(bbuf(st + 1), bp, bi, st + 1, h, b);
 				mm(L);
 				prep(st + 1, 0, L ^ 1);
@@ -879,6 +945,9 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 			stage_barrier(); // every wave's LDS reads done before the epilogue reuses the buffers
 			mm(L);
 		}
+#ifdef TIE_MFMA_TRACE
+		bw_total = bwait;
+#endif
 	} else {
 		BRegs<TYPE> b0, b1;
 		load_b<TYPE>(bs, 0, h, b0);
@@ -902,11 +971,14 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 		}
 	}
 
+#ifdef TIE_MFMA_TRACE
+	t_loop = __builtin_readcyclecounter();
+#endif
 	// gate/up: TIE's SiLU table (32 KiB) into the now idle stage buffers, so
 	// the epilogue's table lookups are LDS reads
 	const float *silu = a.silu;
 	if constexpr (!DOWN) {
-		static_assert(SILU_N * 4 <= C::LDS_A + C::LDS_B, "SiLU table must fit the stage buffers");
+		static_assert(SILU_N * 4 <= C::STAGE_BYTES, "SiLU table must fit the stage buffers");
 #pragma unroll
 		for (int c = 0; c < SILU_N * 4 / 1024 / NWAVES; c++) {
 			const int off = 1024 * (NWAVES * c + w);
@@ -918,6 +990,79 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 	}
 	// D layout of v_mfma_f32_32x32x16: lane l, register i holds
 	// row 8*(i/4) + 4*(l/32) + i%4, column l%32.
+	if constexpr (C::F16 && !C::SPLIT) {
+		// 16-bit outputs of the f16 kernels through a wave-private LDS tile
+		// (fp32, rows padded so the two row groups of a write fall in
+		// different banks), then 16-byte coalesced stores: gate/up h rows
+		// (32 columns of the wave) at 32 KiB past the SiLU table, down y
+		// rows (64 columns) at the buffers' start.
+		constexpr int NC = DOWN ? 64 : 32;          // columns of the wave
+		constexpr int LS = DOWN ? 72 : 40;          // LDS row stride (floats)
+		// half an M tile (16 rows) at a time: registers i = 8 half .. 8 half + 7
+		// hold rows 16 half .. 16 half + 15
+		float *tl = reinterpret_cast<float *>(As + (DOWN ? 0 : 32768) + w * (16 * LS * 4));
+		static_assert((DOWN ? 0 : 32768) + NWAVES * 16 * LS * 4 <= C::STAGE_BYTES, "epilogue tile");
+		const int c0 = lane & 31;
+		// gate/up: K positions 1, 2 (and 5, 6) of each 8-group of h swapped
+		// (the dequantised pairs' order)
+		const int pc0 = DOWN ? c0 : (c0 & ~3) | ((c0 & 1) << 1) | ((c0 >> 1) & 1);
+#pragma unroll
+		for (int mt = 0; mt < NMT; mt++) {
+#pragma unroll
+			for (int half = 0; half < 2; half++) {
+#pragma unroll
+				for (int ii = 0; ii < 8; ii++) {
+					const int i = 8 * half + ii;
+					const int r = 8 * (ii >> 2) + 4 * h + (ii & 3); // row within the half
+					if (DOWN) {
+						tl[r * LS + c0] = acc[mt][0][i] * a.y_scale;
+						tl[r * LS + 32 + c0] = acc[mt][1][i] * a.y_scale;
+					} else {
+						constexpr float unscale = 1.0f / (1 << F16_SHIFT);
+						const float hs =
+							tie_swiglu(acc[mt][0][i] * unscale, acc[mt][1][i] * unscale, silu) * a.h_scale;
+						tl[r * LS + pc0] = hs;
+						// a value outside the f16 range sends the pair's token
+						// to the exact recomputation
+						const int mrow = 32 * mt + 16 * half + r;
+						if (!(__builtin_fabsf(hs) < 65504.0f) && mrow < nrows) {
+							const int tok = spair[mrow] / a.k;
+							if (a.tok_flag[tok] == 0) // listed already: no atomic
+								flag_token(a.tok_flag, a.fix_list, a.fix_count, tok);
+						}
+					}
+				}
+				__builtin_amdgcn_s_waitcnt(0xc07f); // lgkmcnt(0): the tile's LDS writes done
+				__builtin_amdgcn_wave_barrier();
+				// 16-byte chunks: 16 rows x NC columns / 8 per chunk, 64 lanes
+				constexpr int CPRW = NC / 8; // chunks per row
+#pragma unroll
+				for (int q = 0; q < 16 * CPRW / 64; q++) {
+					const int cidx = lane + 64 * q, r = cidx / CPRW, part = cidx % CPRW;
+					const float4 v0 = *reinterpret_cast<const float4 *>(tl + r * LS + 8 * part);
+					const float4 v1 = *reinterpret_cast<const float4 *>(tl + r * LS + 8 * part + 4);
+					const int mrow = 32 * mt + 16 * half + r;
+					if (mrow < nrows) {
+						if (DOWN) {
+							const uint4 o = make_uint4(pack_bf16(v0.x, v0.y), pack_bf16(v0.z, v0.w),
+										   pack_bf16(v1.x, v1.y), pack_bf16(v1.z, v1.w));
+							uint16_t *yr = a.y16 + (size_t)spair[mrow] * a.rows + slab * DN_COLS + 64 * w + 8 * part;
+							*reinterpret_cast<uint4 *>(yr) = o;
+						} else {
+							const f16x8 hv = {(_Float16)v0.x, (_Float16)v0.y, (_Float16)v0.z, (_Float16)v0.w,
+									  (_Float16)v1.x, (_Float16)v1.y, (_Float16)v1.z, (_Float16)v1.w};
+							uint16_t *hr =
+								a.h16 + (size_t)(pbase + mrow) * a.rows + slab * GU_COLS + 32 * w + 8 * part;
+							*reinterpret_cast<f16x8 *>(hr) = hv;
+						}
+					}
+				}
+				__builtin_amdgcn_s_waitcnt(0xc07f);
+				__builtin_amdgcn_wave_barrier(); // the reads done before the next half overwrites
+			}
+			__builtin_amdgcn_sched_barrier(0);
+		}
+	} else
 #pragma unroll
 	for (int mt = 0; mt < NMT; mt++) {
 #pragma unroll
@@ -966,6 +1111,15 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 		// one M tile at a time: only its accumulators move to VGPRs
 		__builtin_amdgcn_sched_barrier(0);
 	}
+#ifdef TIE_MFMA_TRACE
+	if (t == 0 && t_loop) {
+		const unsigned long long t_end = __builtin_readcyclecounter();
+		atomicAdd(&g_mfma_trace[DOWN][0], t_end - t_start);
+		atomicAdd(&g_mfma_trace[DOWN][1], bw_total);
+		atomicAdd(&g_mfma_trace[DOWN][2], t_end - t_loop);
+		atomicAdd(&g_mfma_trace[DOWN][3], 1ull);
+	}
+#endif
 }
 
 // waves per SIMD: the quantised kernels keep their LDS and registers small
@@ -983,7 +1137,8 @@ mfma_experts_kernel(MfmaArgs a)
 	using C = Cfg<TYPE, DOWN, MTR>;
 	constexpr int MT = C::MT, MT_TILES = C::MT / 32;
 	extern __shared__ __attribute__((aligned(16))) uint8_t As[]; // A [2][ABUF] | B [2][BBUF] | row offsets
-	uint32_t *roff = reinterpret_cast<uint32_t *>(As + C::LDS_A + C::LDS_B);
+	uint32_t *roff = reinterpret_cast<uint32_t *>(As + C::STAGE_BYTES);
+	int32_t *spair = reinterpret_cast<int32_t *>(roff + C::RPI * NWAVES * ROFF_STRIDE);
 
 	// XCD-aware tile order.  Consecutive workgroup ids are spread round-robin
 	// over the 8 XCDs, each with its own L2.  The id is remapped so that each
@@ -1005,28 +1160,33 @@ mfma_experts_kernel(MfmaArgs a)
 	const int ntl = (cnt + MT - 1) / MT;
 	const int pbase = a.offsets[e] + m0;
 	const int nrows = min((cnt + ntl - 1) / ntl, cnt - m0);
+#ifdef TIE_MFMA_FIXED_NMT
+	// one tile height for every tile (one copy of run_tile's code)
+	run_tile<TYPE, DOWN, MT_TILES, MTR>(a, As, roff, spair, e, pbase, nrows, slab);
+	return;
+#endif
 	switch ((nrows + 31) >> 5) {
 	case 1:
-		run_tile<TYPE, DOWN, 1, MTR>(a, As, roff, e, pbase, nrows, slab);
+		run_tile<TYPE, DOWN, 1, MTR>(a, As, roff, spair, e, pbase, nrows, slab);
 		break;
 	case 2:
-		run_tile<TYPE, DOWN, 2, MTR>(a, As, roff, e, pbase, nrows, slab);
+		run_tile<TYPE, DOWN, 2, MTR>(a, As, roff, spair, e, pbase, nrows, slab);
 		break;
 	case 3:
 		if constexpr (MT_TILES >= 3)
-			run_tile<TYPE, DOWN, (MT_TILES >= 3 ? 3 : 1), MTR>(a, As, roff, e, pbase, nrows, slab);
+			run_tile<TYPE, DOWN, (MT_TILES >= 3 ? 3 : 1), MTR>(a, As, roff, spair, e, pbase, nrows, slab);
 		break;
 	case 4:
 		if constexpr (MT_TILES >= 4)
-			run_tile<TYPE, DOWN, (MT_TILES >= 4 ? 4 : 1), MTR>(a, As, roff, e, pbase, nrows, slab);
+			run_tile<TYPE, DOWN, (MT_TILES >= 4 ? 4 : 1), MTR>(a, As, roff, spair, e, pbase, nrows, slab);
 		break;
 	case 5:
 		if constexpr (MT_TILES >= 5)
-			run_tile<TYPE, DOWN, (MT_TILES >= 5 ? 5 : 1), MTR>(a, As, roff, e, pbase, nrows, slab);
+			run_tile<TYPE, DOWN, (MT_TILES >= 5 ? 5 : 1), MTR>(a, As, roff, spair, e, pbase, nrows, slab);
 		break;
 	default:
 		if constexpr (MT_TILES >= 6)
-			run_tile<TYPE, DOWN, (MT_TILES >= 6 ? 6 : 1), MTR>(a, As, roff, e, pbase, nrows, slab);
+			run_tile<TYPE, DOWN, (MT_TILES >= 6 ? 6 : 1), MTR>(a, As, roff, spair, e, pbase, nrows, slab);
 	}
 }
 
@@ -1092,7 +1252,7 @@ static hipError_t launch_type(const MfmaArgs &a, dim3 grid, hipStream_t s)
 {
 	// the double-buffered A tile exceeds the default 64 KiB of dynamic LDS
 	using C = Cfg<TYPE, DOWN, MTR>;
-	constexpr size_t lds = (size_t)C::LDS_A + C::LDS_B + 4 * (size_t)(C::RPI * NWAVES * ROFF_STRIDE);
+	constexpr size_t lds = (size_t)C::STAGE_BYTES + 4 * (size_t)(C::RPI * NWAVES * ROFF_STRIDE) + 4 * C::MT;
 	static_assert(lds <= 160 * 1024, "LDS budget");
 	static bool attr = false;
 	if (!attr) {
@@ -1233,4 +1393,18 @@ hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, con
 }
 
 } // namespace tie
+
+#ifdef TIE_MFMA_TRACE
+extern "C" int tie_hip_debug_mfma_trace(unsigned long long *host, int reset)
+{
+	if (hipMemcpyFromSymbol(host, HIP_SYMBOL(tie::g_mfma_trace), sizeof(unsigned long long) * 8) != hipSuccess)
+		return -1;
+	if (reset) {
+		static const unsigned long long z[8] = {0};
+		if (hipMemcpyToSymbol(HIP_SYMBOL(tie::g_mfma_trace), z, sizeof z) != hipSuccess)
+			return -1;
+	}
+	return 0;
+}
+#endif
 
