@@ -151,7 +151,7 @@ def run_dense(torch, tie_amd, cfg, steps, warmup, n_copies):
         mt.close()
     return dict(T=T, k=0, ms=ms, tokens_per_s=T / (ms * 1e-3), U=1, block_bytes=nbytes, block_flops=flops,
                 block_GBps=nbytes / (ms * 1e-3) / 1e9, block_TFLOPs=flops / (ms * 1e-3) / 1e12, kernels=kernels,
-                layers=n_copies)
+                layers=n_copies, ms_eager=ms, timing="eager")
 
 
 def expert_bytes(cfg):

@@ -104,7 +104,8 @@ def test_lfm2_one_token_without_bias():
 @pytest.mark.parametrize("wtype", [synth.Q4_K, synth.Q6_K, synth.BF16, synth.F32])
 def test_dense_mat_mat(wtype):
     """tie_hip_mat_mat (dispatch_mat_mat with F32 input) against the oracle's
-    row kernels, bit for bit, for ragged token counts."""
+    row kernels, bit for bit, for ragged token counts (T <= 4 on the
+    row-block kernel, more on the grouped GEMV kernels)."""
     import torch
     rows, in_dim = 512, 1024
     rng = np.random.default_rng(40 + wtype)
@@ -113,7 +114,7 @@ def test_dense_mat_mat(wtype):
     else:
         w = synth.expert_tensor(rng, wtype, 1, rows, in_dim)
     M = tie_amd.Matrix(w, wtype, rows, in_dim)
-    for T in (1, 5, 37, 200):
+    for T in (1, 3, 4, 5, 37, 200):
         x = synth.make_input(41 + T, T, in_dim)
         print("dense case type=%d T=%d" % (wtype, T), flush=True)
         xd = torch.from_numpy(x).cuda()

@@ -424,7 +424,7 @@ static int forward(tie_hip_layer *layer, const float *x, int T, int k, float *ou
 	if (!x || !out)
 		return set_error(TIE_HIP_EINVAL, "null x/out");
 	const bool mfma = (flags & TIE_HIP_PATH_MFMA) || (!(flags & TIE_HIP_PATH_EXACT) && T > g.exact_max_t);
-	if (mfma && !decode_supported(L, k) && mfma_f16_operands(L))
+	if (mfma && !recompute_supported(L, k) && mfma_f16_operands(L))
 		return set_error(TIE_HIP_EINVAL, "the MFMA path needs the exact per-token kernels for its range guard "
 						 "(k * F too large for them: use TIE_HIP_PATH_EXACT)");
 	if (mfma && L.gate.type != L.up.type)
@@ -453,8 +453,8 @@ static int forward(tie_hip_layer *layer, const float *x, int T, int k, float *ou
 			// tokens whose activations left the f16 range (listed by the
 			// kernels above; usually none): recomputed exactly, their rows
 			// of out overwritten
-			HIP_TRY(launch_decode(L, x, k, g.silu, ws.logits, ws.topk_idx, ws.topk_w, ws.h, out, res, ws.fix_list,
-					      ws.fix_count, T, false, true, s));
+			HIP_TRY(launch_recompute(L, x, k, g.silu, ws.topk_idx, ws.topk_w, out, res, ws.fix_list, ws.fix_count, T,
+						 s));
 		}
 	} else if (T == 1 && decode_supported(L, k)) {
 		// one token: router logits, then the experts and the combine in two
@@ -986,6 +986,8 @@ extern "C" int tie_hip_mat_mat(tie_hip_matrix *m, const float *x_dev, int T, flo
 	prof_begin("dense", s);
 	if (m->F.router) {
 		HIP_TRY(launch_router_logits(m->F, x_dev, T, out_dev, s));
+	} else if (dense_rows_supported(m->W, T)) {
+		HIP_TRY(launch_dense_rows(m->W, x_dev, T, out_dev, s));
 	} else {
 		const int G = dense_groups(T);
 		Workspace *ws = nullptr;

@@ -124,6 +124,12 @@ bool mfma_f16_operands(const Layer &L);
 // inline_route, E <= 128); otherwise the *count tokens of list, with their
 // selection already in topk_idx / topk_w.  h: [entries][k][F] scratch.
 bool decode_supported(const Layer &L, int k);
+// The f16 path's listed tokens recomputed exactly, a workgroup per token,
+// in one launch (recompute_kernel); count on the device, T bounds it.
+bool recompute_supported(const Layer &L, int k);
+hipError_t launch_recompute(const Layer &L, const float *x, int k, const float *silu, const int32_t *topk_idx,
+			    const float *topk_w, float *out, const float *res, const int32_t *list,
+			    const int32_t *count, int T, hipStream_t s);
 
 hipError_t launch_decode(const Layer &L, const float *x, int k, const float *silu, const float *logits,
 			 int32_t *topk_idx, float *topk_w, float *h, float *out, const float *res, const int32_t *list,
@@ -135,6 +141,10 @@ int mfma_gu_rows(const Layer &L, int npairs); // rows per gate/up tile (the tile
 // = W[r] . x[t] (W one "expert": rows, in, panel layout); dense_groups(T)
 // token groups (the workspace needs that many experts and T pairs)
 hipError_t launch_dense(const ExpertTensor &W, const float *x, int T, float *out, Workspace &ws, hipStream_t s);
+// The same for a few tokens (T <= 4, Q4_K / Q6_K): a lane per (row, block),
+// the block loaded once for all tokens (decode.hip); needs no workspace
+bool dense_rows_supported(const ExpertTensor &W, int T);
+hipError_t launch_dense_rows(const ExpertTensor &W, const float *x, int T, float *out, hipStream_t s);
 int dense_groups(int T);
 // res (optional): out = res + combine (the residual add after the block)
 // y16: y holds bf16 values (the MFMA path's down output with quantised weights)

@@ -468,7 +468,71 @@ template <int TD> __global__ __launch_bounds__(DEC_MAX_THREADS) void decode_down
 	}
 }
 
+// ------------------------------------------------------------ recompute
+// Listed tokens of a large-T forward (their activations left the f16 range
+// of the matrix-core path; usually none), each recomputed whole in TIE's
+// exact arithmetic by one workgroup: thread per (row of F): for each slot,
+// the gate and up row sums over the blocks in order (each block's dot as
+// in decode_gu_kernel), SwiGLU into LDS; then thread per row of d: y_j =
+// serial block sum, out = [res +] sum_j fma(g_j, y_j, .) in slot order --
+// the same operations as decode_gu_kernel / decode_down_kernel, one kernel
+// instead of two, so the (usually empty) launch costs once.
+template <int TG, int TU, int TD>
+__global__ __launch_bounds__(DEC_MAX_THREADS) void recompute_kernel(DecodeArgs a)
+{
+	extern __shared__ __attribute__((aligned(16))) float dl[];
+	const int nbd = a.d / QK, nbf = a.F / QK, k = a.k;
+	float *xs = dl;                          // [nbd][XSEG]
+	float *hs = dl + (size_t)nbd * XSEG;     // [k][nbf][XSEG]
+	const int n = list_count(a);
+	for (int li = blockIdx.x; li < n; li += gridDim.x) {
+		const int t = list_token(a, li);
+		copy_in<4>(reinterpret_cast<const float4 *>(a.x + (size_t)t * a.d), a.d / 4, [&](int q, float4 v) {
+			const int f = 4 * q;
+			*reinterpret_cast<float4 *>(xs + (f / QK) * XSEG + (f % QK)) = v;
+		});
+		__syncthreads();
+		for (int u = threadIdx.x; u < k * a.F; u += blockDim.x) {
+			const int j = u / a.F, r = u - j * a.F;
+			const int e = a.topk_idx[(size_t)t * k + j];
+			float h = 0.0f;
+			if (e >= 0) {
+				float g = 0.0f, up = 0.0f;
+				for (int b = 0; b < nbd; b++) {
+					const uint8_t *bg = panel_slot(a.w[0], a.expert_bytes[0], e, r, b, nbd, panel_bytes(TG));
+					g = g + row_block_dot<TG>(bg, q6k_d_of(bg, r), (dfloat *)(xs + b * XSEG));
+				}
+				for (int b = 0; b < nbd; b++) {
+					const uint8_t *bu = panel_slot(a.w[1], a.expert_bytes[1], e, r, b, nbd, panel_bytes(TU));
+					up = up + row_block_dot<TU>(bu, q6k_d_of(bu, r), (dfloat *)(xs + b * XSEG));
+				}
+				h = tie_swiglu(g, up, a.silu);
+			}
+			hs[(j * nbf + r / QK) * XSEG + r % QK] = h;
+		}
+		__syncthreads();
+		for (int r = threadIdx.x; r < a.d; r += blockDim.x) {
+			float acc = 0.0f;
+			for (int j = 0; j < k; j++) {
+				const int e = a.topk_idx[(size_t)t * k + j];
+				if (e < 0)
+					continue;
+				float y = 0.0f;
+				for (int b = 0; b < nbf; b++) {
+					const uint8_t *bd = panel_slot(a.w[2], a.expert_bytes[2], e, r, b, nbf, panel_bytes(TD));
+					y = y + row_block_dot<TD>(bd, q6k_d_of(bd, r), (dfloat *)(hs + (size_t)(j * nbf + b) * XSEG));
+				}
+				acc = __builtin_fmaf(a.topk_w[(size_t)t * k + j], y, acc);
+			}
+			const size_t o = (size_t)t * a.d + r;
+			a.out[o] = a.res ? a.res[o] + acc : acc;
+		}
+		__syncthreads();
+	}
+}
+
 // ---------------------------------------------------------------- launchers
+
 static int round64(int n)
 {
 	return (n + 63) & ~63;
@@ -507,14 +571,67 @@ bool decode_supported(const Layer &L, int k)
 	       lds_dn <= DEC_MAX_LDS;
 }
 
-template <typename K, typename A> static hipError_t dec_launch(K kern, dim3 grid, dim3 block, size_t lds, hipStream_t s,
-								    const A &a)
+template <typename K, typename... A>
+static hipError_t dec_launch(K kern, dim3 grid, dim3 block, size_t lds, hipStream_t s, A... args)
 {
 	hipError_t err = ensure_lds_limit((const void *)kern, lds);
 	if (err != hipSuccess)
 		return err;
-	hipLaunchKernelGGL(kern, grid, block, lds, s, a);
+	hipLaunchKernelGGL(kern, grid, block, lds, s, args...);
 	return hipGetLastError();
+}
+
+bool recompute_supported(const Layer &L, int k)
+{
+	const size_t lds = sizeof(float) * ((size_t)(L.d / QK) + (size_t)k * (L.F / QK)) * XSEG;
+	return decode_supported(L, k) && lds <= DEC_MAX_LDS;
+}
+
+// The listed tokens (*count of them, their selection in topk_idx / topk_w)
+// recomputed exactly into out (recompute_kernel); T bounds the list.
+hipError_t launch_recompute(const Layer &L, const float *x, int k, const float *silu, const int32_t *topk_idx,
+			    const float *topk_w, float *out, const float *res, const int32_t *list,
+			    const int32_t *count, int T, hipStream_t s)
+{
+	DecodeArgs a;
+	memset(&a, 0, sizeof a);
+	a.w[0] = L.gate.data;
+	a.w[1] = L.up.data;
+	a.w[2] = L.down.data;
+	a.expert_bytes[0] = L.gate.expert_bytes;
+	a.expert_bytes[1] = L.up.expert_bytes;
+	a.expert_bytes[2] = L.down.expert_bytes;
+	a.d = L.d;
+	a.F = L.F;
+	a.E = L.E;
+	a.k = k;
+	a.x = x;
+	a.topk_idx = const_cast<int32_t *>(topk_idx);
+	a.topk_w = const_cast<float *>(topk_w);
+	a.out = out;
+	a.res = res;
+	a.silu = silu;
+	a.list = list;
+	a.count = count;
+	const size_t lds = sizeof(float) * ((size_t)(L.d / QK) + (size_t)k * (L.F / QK)) * XSEG;
+	const dim3 grid(T < 128 ? (T > 0 ? T : 1) : 128);
+	const int tg = L.gate.type, tu = L.up.type, td = L.down.type;
+	hipError_t err;
+	prof_begin("recompute", s);
+#define REC(A, B)                                                                                                    \
+	(td == TIE_GGML_Q4_K ? dec_launch(recompute_kernel<A, B, TIE_GGML_Q4_K>, grid, dim3(DEC_MAX_THREADS), lds, s, a) \
+			     : dec_launch(recompute_kernel<A, B, TIE_GGML_Q6_K>, grid, dim3(DEC_MAX_THREADS), lds, s, a))
+	if (tg == TIE_GGML_Q4_K && tu == TIE_GGML_Q4_K)
+		err = REC(TIE_GGML_Q4_K, TIE_GGML_Q4_K);
+	else if (tg == TIE_GGML_Q4_K)
+		err = REC(TIE_GGML_Q4_K, TIE_GGML_Q6_K);
+	else if (tu == TIE_GGML_Q4_K)
+		err = REC(TIE_GGML_Q6_K, TIE_GGML_Q4_K);
+	else
+		err = REC(TIE_GGML_Q6_K, TIE_GGML_Q6_K);
+#undef REC
+	prof_end(s);
+	return err;
 }
 
 // The block for listed tokens (list == null: token 0 of a one-token call,
@@ -591,6 +708,71 @@ hipError_t launch_decode(const Layer &L, const float *x, int k, const float *sil
 	}
 	prof_end(s);
 	return err;
+}
+
+// ------------------------------------------------------------ dense, few tokens
+// dispatch_mat_mat (math_dispatch.c:304-359) for T <= DENSE_ROWS_T tokens
+// through TIE's row kernel (mat_vec_row_f32_{q4k,q6k}_f32_avx2) as the
+// decode kernels do it: a lane per (row, block) of R rows of the matrix,
+// the block in registers (every load up front) and its dot taken with each
+// token's x from LDS; then the serial sums over the blocks, out[t][row].
+constexpr int DENSE_ROWS_T = 4;
+template <int TW> __global__ __launch_bounds__(DEC_MAX_THREADS) void dense_rows_kernel(const uint8_t *__restrict__ W,
+											  const float *__restrict__ x, int T,
+											  int in, int rows, int R,
+											  float *__restrict__ out)
+{
+	extern __shared__ __attribute__((aligned(16))) float dl[];
+	const int nb = in / QK;
+	float *xs = dl;                        // [T][nb][XSEG]
+	float *part = dl + (size_t)T * nb * XSEG; // [T][nb][R]
+	copy_in<4>(reinterpret_cast<const float4 *>(x), T * in / 4, [&](int q, float4 v) {
+		const int f = 4 * q, t = f / in, r = f - t * in;
+		*reinterpret_cast<float4 *>(xs + ((size_t)t * nb + r / QK) * XSEG + (r % QK)) = v;
+	});
+	__syncthreads();
+	const int r0 = blockIdx.x * R;
+	for (int u = threadIdx.x; u < nb * R; u += blockDim.x) {
+		const int r = u & (R - 1), b = u / R;
+		const uint8_t *blk = panel_slot(W, 0, 0, r0 + r, b, nb, panel_bytes(TW));
+		RowBlock<TW> rb;
+		rb.load(blk, q6k_d_of(blk, r0 + r));
+		for (int t = 0; t < T; t++)
+			part[((size_t)t * nb + b) * R + r] = rb.dot((dfloat *)(xs + ((size_t)t * nb + b) * XSEG));
+	}
+	__syncthreads();
+	for (int u = threadIdx.x; u < T * R; u += blockDim.x) {
+		const int t = u / R, r = u - t * R;
+		float acc = 0.0f;
+#pragma unroll 8
+		for (int b = 0; b < nb; b++)
+			acc = acc + part[((size_t)t * nb + b) * R + r];
+		out[(size_t)t * rows + r0 + r] = acc;
+	}
+}
+
+bool dense_rows_supported(const ExpertTensor &W, int T)
+{
+	const int nb = W.in / QK;
+	const size_t lds = sizeof(float) * ((size_t)DENSE_ROWS_T * nb * XSEG + (size_t)DENSE_ROWS_T * nb * 64);
+	return T <= DENSE_ROWS_T && (W.type == TIE_GGML_Q4_K || W.type == TIE_GGML_Q6_K) && nb <= DEC_MAX_THREADS &&
+	       lds <= DEC_MAX_LDS;
+}
+
+hipError_t launch_dense_rows(const ExpertTensor &W, const float *x, int T, float *out, hipStream_t s)
+{
+	const int nb = W.in / QK;
+	// rows per workgroup: at most 64 and a workgroup's worth of lanes, and
+	// few enough that the grid has ~512 workgroups (small matrices)
+	int R = 64;
+	while (R > 1 && (nb * R > DEC_MAX_THREADS || W.rows / R < 512))
+		R >>= 1;
+	const size_t lds = sizeof(float) * ((size_t)T * nb * XSEG + (size_t)T * nb * R);
+	const dim3 grid(W.rows / R);
+	const dim3 block((nb * R + 63) & ~63);
+	return W.type == TIE_GGML_Q4_K
+		       ? dec_launch(dense_rows_kernel<TIE_GGML_Q4_K>, grid, block, lds, s, W.data, x, T, W.in, W.rows, R, out)
+		       : dec_launch(dense_rows_kernel<TIE_GGML_Q6_K>, grid, block, lds, s, W.data, x, T, W.in, W.rows, R, out);
 }
 
 } // namespace tie
