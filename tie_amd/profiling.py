@@ -39,6 +39,11 @@ _NAMES = (
     ("tie::to_bf16_kernel", "mfma_gate_up"),
     ("tie::to_f16_kernel", "mfma_gate_up"),
     ("tie::to_split_kernel", "mfma_gate_up"),
+    ("tie::decode_gu_kernel", "decode_gate_up"),
+    ("tie::decode_down_kernel", "decode_down"),
+    ("tie::recompute_kernel", "recompute"),
+    ("tie::dense_rows_kernel", "dense"),
+    ("tie::dense_groups_kernel", "dense"),
 )
 
 
@@ -110,9 +115,12 @@ def traffic(fetch_csv, write_csv, copy_fetch_csv, copy_write_csv, copy_bytes):
     w_scale = copy_bytes / (max(cw) * 1024.0)
     fetch = _per_dispatch(fetch_csv, "FETCH_SIZE")
     write = _per_dispatch(write_csv, "WRITE_SIZE")
-    # one combine dispatch per forward: bytes per forward of a block kernel
-    # (some blocks are two kernels, e.g. router logits + selection)
-    steps = len(fetch["combine"])
+    # one combine (or, for one token, decode_down) dispatch per forward:
+    # bytes per forward of a block kernel (some blocks are two kernels,
+    # e.g. router logits + selection)
+    steps = len(fetch.get("combine") or fetch.get("decode_down") or [])
+    if not steps:
+        raise ValueError("no combine / decode_down dispatches: cannot count forwards")
     res = {}
     for block in fetch:
         if block == "copy" or block not in write:
@@ -130,7 +138,11 @@ _DEFAULT_JSON = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__f
 def traffic_markdown(path):
     with open(path) as f:
         t = json.load(f)
-    out = ["| kernel @ config | fetch MB | write MB | total MB per forward | dispatches | forwards |",
+    out = ["Kernels are grouped as the library's per-kernel timer groups them: mfma_gate_up includes the x conversion "
+           "(to_f16 / to_bf16 / to_split), router includes the separate selection kernel (router_topk) where one "
+           "runs, dense includes its grouping kernel.",
+           "",
+           "| kernel @ config | fetch MB | write MB | total MB per forward | dispatches | forwards |",
            "|---|---|---|---|---|---|"]
     for k, v in sorted(t["detail"].items(), key=lambda kv: (kv[0].split("@")[1], kv[0])):
         out.append("| %s | %.2f | %.2f | %.2f | %d | %d |" % (k, v["fetch_bytes"] / 1e6, v["write_bytes"] / 1e6,
