@@ -253,7 +253,7 @@ def run_config(torch, tie_amd, wl, T, k, steps, warmup, flags, cfg=None, graph=F
         "exact_down": U_avg * dn_b + pairs * F * 4 + pairs * d * 4,
         "decode_gate_up": U_avg * gu_b + T * d * 4 + pairs * F * 4,
         "decode_down": U_avg * dn_b + pairs * F * 4 + T * d * 4 * (2 if residual else 1),
-        "decode_fused": E * d * 4 + U_avg * (gu_b + dn_b) + T * d * 4 * (3 if residual else 2),
+        "decode_one": E * d * 4 + U_avg * (gu_b + dn_b) + T * d * 4 * (3 if residual else 2),
         "combine": pairs * d * 4 + T * d * 4 * (3 if residual else 1),
         "rmsnorm": 2 * T * d * 4 + d * 4,
         "dispatch": pairs * 4 * 2,
@@ -267,7 +267,7 @@ def run_config(torch, tie_amd, wl, T, k, steps, warmup, flags, cfg=None, graph=F
         "exact_down": 2.0 * pairs * F * d,
         "decode_gate_up": 2.0 * pairs * 2 * F * d,
         "decode_down": 2.0 * pairs * F * d,
-        "decode_fused": 2.0 * T * (E * d + 3 * k * F * d),
+        "decode_one": 2.0 * T * (E * d + 3 * k * F * d),
         "router": 2.0 * T * E * d,
     }
     block_bytes = E * d * 4 + U_avg * (gu_b + dn_b) + 2 * T * d * 4

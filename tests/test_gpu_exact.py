@@ -462,3 +462,41 @@ def test_one_token_graph_replays():
     del g
     for L in Ls:
         L.close()
+
+
+@pytest.mark.gpu
+def test_one_launch_back_to_back():
+    """Eager one-token forwards (the one-launch kernel: router, gate/up and
+    down workgroups handing over through sequence-stamped words) queued
+    back to back on one stream over three layers with no synchronisation in
+    between, then checked: each equals the oracle bit for bit, so no call
+    read a word left by the call before it."""
+    import torch
+    cases = [(synth_layer(70, 2048, 768, 128, synth.Q4_K, synth.Q6_K, None), 8),
+             (synth_layer(71, 512, 256, 32, synth.Q6_K, synth.Q4_K, None), 4),
+             (synth_layer(72, 4096, 1536, 128, synth.Q4_K, synth.Q6_K, None), 8)]
+    Ls = [tie_amd.Layer.from_synth(l) for l, _ in cases]
+    runs = []
+    tie_amd.profile_enable(True)
+    for i in range(12):
+        c = i % 3
+        layer, k = cases[c]
+        x = torch.from_numpy(synth.make_input(80 + i, 1, layer.d)).cuda()
+        out = torch.empty_like(x)
+        idx = torch.empty((1, k), dtype=torch.int32, device="cuda")
+        w = torch.empty((1, k), dtype=torch.float32, device="cuda")
+        Ls[c].forward(x, 1, k, out, idx, w)
+        runs.append((c, x, out, idx, w))
+    torch.cuda.synchronize()
+    prof = tie_amd.profile_read()
+    tie_amd.profile_enable(False)
+    assert prof.get("decode_one", (0, 0))[1] == 12, prof
+    for i, (c, x, out, idx, w) in enumerate(runs):
+        layer, k = cases[c]
+        print("back-to-back call %d (layer %d)" % (i, c), flush=True)
+        ro, ri, rw = bind.moe_block(layer, x.cpu().numpy(), k)
+        assert_same(idx.cpu().numpy(), ri, "topk_idx")
+        assert_same(w.cpu().numpy(), rw, "topk_w")
+        assert_same(out.cpu().numpy(), ro, "out")
+    for L in Ls:
+        L.close()

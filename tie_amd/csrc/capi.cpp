@@ -228,6 +228,7 @@ static size_t carve_workspace(uint8_t *b, size_t P, size_t FF, size_t DD, size_t
 	const size_t max_tiles = (size_t)mfma_max_tiles((int)P, (int)EE);
 	const size_t o_te = take(2 * max_tiles * 4), o_tm = take(2 * max_tiles * 4), o_nt = take(8);
 	const size_t o_fl = take(Tcap * 4), o_fx = take(Tcap * 4), o_fc = take(4);
+	const size_t o_lg = take(EE * 8), o_dn = take((size_t)MAX_K * FF * 8);
 	if (!b)
 		return off;
 	w->topk_idx = (int32_t *)(b + o_idx);
@@ -249,6 +250,9 @@ static size_t carve_workspace(uint8_t *b, size_t P, size_t FF, size_t DD, size_t
 	w->tok_flag = (int32_t *)(b + o_fl);
 	w->fix_list = (int32_t *)(b + o_fx);
 	w->fix_count = (int32_t *)(b + o_fc);
+	w->one_lg = (unsigned long long *)(b + o_lg);
+	w->one_h = (unsigned long long *)(b + o_dn);
+	w->one_seq = 0;
 	w->tile_cap = (int32_t)max_tiles;
 	w->cap_pairs = P;
 	w->cap_F = FF;
@@ -283,6 +287,10 @@ static int ensure_workspace(hipStream_t s, int T, int k, int d, int F, int E, Wo
 		return rc;
 	carve_workspace((uint8_t *)mem, P, FF, DD, EE, &w);
 	w.alloc = mem;
+	// the one-launch decode's words start at sequence 0 (every call uses a
+	// later one)
+	HIP_TRY(hipMemset(w.one_lg, 0, (size_t)EE * 8));
+	HIP_TRY(hipMemset(w.one_h, 0, (size_t)MAX_K * FF * 8));
 	return TIE_HIP_OK;
 }
 
@@ -407,6 +415,16 @@ static int create_layer(const tie_hip_layer_desc *ds, tie_hip_layer **out)
 	return TIE_HIP_OK;
 }
 
+static bool capturing(hipStream_t s)
+{
+	hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+	if (hipStreamIsCapturing(s, &st) != hipSuccess) {
+		(void)hipGetLastError();
+		return true; // unknown: take the path that works either way
+	}
+	return st != hipStreamCaptureStatusNone;
+}
+
 // The block on device pointers; res (optional) is added to the combine
 // (out = res + block, the residual add after the FFN).
 static int forward(tie_hip_layer *layer, const float *x, int T, int k, float *out, int32_t *idx_out,
@@ -456,6 +474,18 @@ static int forward(tie_hip_layer *layer, const float *x, int T, int k, float *ou
 			HIP_TRY(launch_recompute(L, x, k, g.silu, ws.topk_idx, ws.topk_w, out, res, ws.fix_list, ws.fix_count, T,
 						 s));
 		}
+	} else if (T == 1 && !preset && !capturing(s) && decode_one_supported(L, k)) {
+		// one token, one launch (eager calls on a workspace of their own:
+		// the sequence number lives on the host, so a captured graph could
+		// not advance it)
+		if (++ws.one_seq == 0) {
+			HIP_TRY(hipStreamSynchronize(s));
+			HIP_TRY(hipMemset(ws.one_lg, 0, (size_t)ws.cap_E * 8));
+			HIP_TRY(hipMemset(ws.one_h, 0, (size_t)MAX_K * ws.cap_F * 8));
+			ws.one_seq = 1;
+		}
+		HIP_TRY(launch_decode_one(L, x, k, g.silu, ws.topk_idx, ws.topk_w, out, res, ws.one_lg, ws.one_h, ws.one_seq,
+					  s));
 	} else if (T == 1 && decode_supported(L, k)) {
 		// one token: router logits, then the experts and the combine in two
 		// launches (the selection runs in the gate/up prologue for E <= 128)

@@ -98,6 +98,9 @@ struct Workspace {
 	int32_t *tok_flag = nullptr;  // [T]      f16 path: token's activations left the f16 range
 	int32_t *fix_list = nullptr;  // [T]      flagged tokens (recomputed exactly after the forward)
 	int32_t *fix_count = nullptr; // [1]
+	unsigned long long *one_lg = nullptr; // [E]  one-launch decode: {seq, logit} words
+	unsigned long long *one_h = nullptr; // [MAX_K * F] one-launch decode: {seq, h} words
+	uint32_t one_seq = 0;         // one-launch decode: sequence number of the last call
 	int32_t tile_cap = 0;         // max tiles per list
 	size_t cap_pairs = 0, cap_F = 0, cap_d = 0, cap_E = 0;
 	void *alloc = nullptr;
@@ -134,6 +137,12 @@ hipError_t launch_recompute(const Layer &L, const float *x, int k, const float *
 hipError_t launch_decode(const Layer &L, const float *x, int k, const float *silu, const float *logits,
 			 int32_t *topk_idx, float *topk_w, float *h, float *out, const float *res, const int32_t *list,
 			 const int32_t *count, int max_entries, bool inline_route, bool fixup, hipStream_t s);
+// T = 1 in one launch (router, gate/up and down + combine workgroups that
+// hand the logits and h over as sequence-stamped words in lg / hw; E <= 128)
+bool decode_one_supported(const Layer &L, int k);
+hipError_t launch_decode_one(const Layer &L, const float *x, int k, const float *silu, int32_t *topk_idx,
+			     float *topk_w, float *out, const float *res, unsigned long long *lg, unsigned long long *hw,
+			     uint32_t seq, hipStream_t s);
 int mfma_max_tiles(int npairs, int E); // per list
 struct Layer;
 int mfma_gu_rows(const Layer &L, int npairs); // rows per gate/up tile (the tile list's and the kernel's)

@@ -468,6 +468,238 @@ template <int TD> __global__ __launch_bounds__(DEC_MAX_THREADS) void decode_down
 	}
 }
 
+// ------------------------------------------------------------ one launch
+// T = 1 in a single launch.  Workgroups take one of three roles by index,
+// in dependency order (the dispatcher starts workgroups in index order, so a
+// workgroup only ever waits for workgroups started before it):
+//
+//   [0, nr)          router: rpr expert rows each, TIE's 8 lane chains and
+//                    hsum tree (as router_small_kernel).
+//   [nr, nr + ng)    gate/up: (slot j, rg rows of F): x staged while the
+//                    router runs, the logits read back, the token's
+//                    selection made in the prologue (as decode_gu_kernel),
+//                    h = silu_tab(gate) * up published.
+//   [nr + ng, ...)   down + combine: (rd rows of d): the selection made
+//                    again from the logits, every weight block of the
+//                    workgroup's rows loaded into registers BEFORE the wait
+//                    for h, then the dots and the combine (as
+//                    decode_down_kernel).
+//
+// Every value handed between workgroups (the E logits, the k F values of
+// h) travels as one 64-bit word {seq, value bits}, written and read with
+// agent-scope relaxed atomics (sc1: coherent across the XCDs' L2s with no
+// cache write-back, invalidate or separate flag); seq (one per call) tells
+// a word of this call from one left by an earlier call.  The waits are
+// bounded: a wait that gives up produces NaN outputs instead of hanging.
+constexpr int SPIN_MAX = 1 << 18;
+
+__device__ __forceinline__ unsigned long long ld_word(const unsigned long long *p)
+{
+	return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ unsigned long long wait_word64(const unsigned long long *p, uint32_t seq, int &bad)
+{
+	for (int i = 0; i < SPIN_MAX; i++) {
+		const unsigned long long v = ld_word(p);
+		if ((uint32_t)(v >> 32) == seq)
+			return v;
+		__builtin_amdgcn_s_sleep(1);
+	}
+	bad = 1;
+	return 0x7fc00000ull; // NaN
+}
+
+struct OneArgs {
+	DecodeArgs a;
+	const float *router;      // [E][d] F32 rows
+	const float *bias;        // [E] or null
+	unsigned long long *lg;   // [E] {seq, logit}
+	unsigned long long *hw;   // [k][F] {seq, h}
+	uint32_t seq;
+	int nr, ng;               // router, gate/up workgroups
+	int rpr, rg, rd;          // rows per router, gate/up, down workgroup
+};
+
+// The token's logits (published by the router workgroups), read back by
+// thread e, then its selection -> sel_idx / sel_w.  Ends with a barrier.
+__device__ __forceinline__ void one_select(const OneArgs &o, uint64_t *etab, int32_t *sel_idx, float *sel_w, int *sbad,
+					   RankScratch *rs)
+{
+	const int tid = threadIdx.x;
+	if (tid < 32) {
+		const uint64_t tab[32] = TIE_EXP2_TABLE;
+		etab[tid] = tab[tid];
+	}
+	__syncthreads();
+	if (tid < o.a.E) {
+		int bad = 0;
+		const float v = __uint_as_float((uint32_t)wait_word64(o.lg + tid, o.seq, bad));
+		if (bad)
+			*sbad = 1;
+		rank_key(v, tid, o.a.routing, o.a.pbias, etab, *rs);
+	}
+	topk_rank_block(o.a.E, o.a.k, etab, sel_idx, sel_w, o.a.routing, *rs);
+}
+
+template <int TG, int TU, int TD> __global__ __launch_bounds__(DEC_MAX_THREADS, 4) void decode_one_kernel(OneArgs o)
+{
+	extern __shared__ __attribute__((aligned(16))) float dl[];
+	__shared__ int32_t sel_idx[MAX_K];
+	__shared__ float sel_w[MAX_K];
+	__shared__ uint64_t etab[32];
+	__shared__ RankScratch rsc;
+	__shared__ int sbad;
+	const DecodeArgs &a = o.a;
+	const int tid = threadIdx.x, b = blockIdx.x, d = a.d;
+	if (tid == 0)
+		sbad = 0;
+	if (b < o.nr) {
+		// ---- router rows e0 .. e0 + ne - 1
+		const int e0 = b * o.rpr, ne = min(o.rpr, a.E - e0);
+		const int lmf = lane_major_floats(d), st = lane_major_stride(d), n4 = d / 4;
+		// x and the rows -> LDS lane-major, all loads of a thread in flight at once
+		for (int base = tid; base < (1 + ne) * n4; base += 8 * (int)blockDim.x) {
+			float4 v[8];
+#pragma unroll
+			for (int i = 0; i < 8; i++) {
+				const int q = base + i * (int)blockDim.x;
+				const int r = q / n4, c = q - r * n4;
+				const float *src = r == 0 ? a.x : o.router + (size_t)(e0 + r - 1) * d;
+				v[i] = q < (1 + ne) * n4 ? reinterpret_cast<const float4 *>(src)[c] : make_float4(0, 0, 0, 0);
+			}
+#pragma unroll
+			for (int i = 0; i < 8; i++) {
+				const int q = base + i * (int)blockDim.x;
+				if (q < (1 + ne) * n4) {
+					const int r = q / n4, f = 4 * (q - r * n4), l = f & 7, ii = f >> 3;
+					float *dst = dl + r * lmf;
+					dst[(l + 0) * st + ii] = v[i].x;
+					dst[(l + 1) * st + ii] = v[i].y;
+					dst[(l + 2) * st + ii] = v[i].z;
+					dst[(l + 3) * st + ii] = v[i].w;
+				}
+			}
+		}
+		__syncthreads();
+		if (tid < 8 * ne) {
+			const int r = tid >> 3, l = tid & 7;
+			const float s = hsum8_lanes(lane_chain(dl, dl + (1 + r) * lmf, d, l));
+			if (l == 0) {
+				const int e = e0 + r;
+				const float v = o.bias ? s + o.bias[e] : s;
+				const unsigned long long w = ((unsigned long long)o.seq << 32) | __float_as_uint(v);
+				__hip_atomic_store(o.lg + e, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+			}
+		}
+		return;
+	}
+	if (b < o.nr + o.ng) {
+		// ---- gate/up: slot j, rows r0 .. r0 + rg - 1 of F
+		const int gb = b - o.nr, nxg = a.F / o.rg, R = o.rg;
+		const int j = gb / nxg, r0 = (gb - j * nxg) * R;
+		const int nb = d / QK;
+		float *xs = dl;
+		float *part = dl + nb * XSEG;
+		copy_in<4>(reinterpret_cast<const float4 *>(a.x), d / 4, [&](int q, float4 v) {
+			const int f = 4 * q;
+			*reinterpret_cast<float4 *>(xs + (f / QK) * XSEG + (f % QK)) = v;
+		});
+		one_select(o, etab, sel_idx, sel_w, &sbad, &rsc);
+		if (gb == 0 && tid < a.k) {
+			a.topk_idx[tid] = sel_idx[tid];
+			a.topk_w[tid] = sel_w[tid];
+		}
+		const int e = sel_idx[j];
+		float hv = 0.0f; // a slot without an expert: its h is never used
+		if (e >= 0) {
+			for (int u = tid; u < 2 * nb * R; u += blockDim.x) {
+				const int task = u / R, r = u - task * R;
+				const int mat = task >= nb ? 1 : 0, bb = task - mat * nb;
+				const uint8_t *blk = panel_slot(a.w[mat], a.expert_bytes[mat], e, r0 + r, bb, nb,
+								panel_bytes(mat ? TU : TG));
+				float v;
+				if (mat == 0)
+					v = row_block_dot<TG>(blk, q6k_d_of(blk, r0 + r), (dfloat *)(xs + bb * XSEG));
+				else
+					v = row_block_dot<TU>(blk, q6k_d_of(blk, r0 + r), (dfloat *)(xs + bb * XSEG));
+				part[task * R + r] = v;
+			}
+			__syncthreads();
+			row_sums(part, nb, R);
+			if (tid < R)
+				hv = sbad ? __builtin_nanf("") : tie_swiglu(part[tid], part[R + tid], a.silu);
+		}
+		if (tid < R) {
+			const unsigned long long w = ((unsigned long long)o.seq << 32) | __float_as_uint(hv);
+			__hip_atomic_store(o.hw + (size_t)j * a.F + r0 + tid, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+		}
+		return;
+	}
+	// ---- down + combine: rows r0 .. r0 + rd - 1 of d; lane (task, row): the
+	// block dot of (row, slot j, block b), task = j nb + b
+	const int R = o.rd, k = a.k, nb = a.F / QK;
+	const int r0 = (b - o.nr - o.ng) * R;
+	float *hs = dl;                           // [k nb][XSEG]
+	float *part = dl + (size_t)k * nb * XSEG; // [k nb][R]
+	one_select(o, etab, sel_idx, sel_w, &sbad, &rsc);
+	const int ntask = k * nb;
+	const int task = tid / R, r = tid - task * R;
+	const bool live = task < ntask;
+	const int jj = live ? task / nb : 0, bb = task - jj * nb;
+	const int e = live ? sel_idx[jj] : -1;
+	RowBlock<TD> rb;
+	if (e >= 0) {
+		// the weights before the wait for h
+		const uint8_t *blk = panel_slot(a.w[2], a.expert_bytes[2], e, r0 + r, bb, nb, panel_bytes(TD));
+		rb.load(blk, q6k_d_of(blk, r0 + r));
+	}
+	// h (k F words of this call) -> LDS, 8 words of a thread polled at
+	// once, the ones not yet stamped again until all are
+	{
+		const int nw = k * a.F;
+		int bad = 0;
+		for (int base = tid; base < nw; base += 8 * (int)blockDim.x) {
+			unsigned long long v[8];
+			uint32_t pend = 0;
+#pragma unroll
+			for (int i = 0; i < 8; i++)
+				if (base + i * (int)blockDim.x < nw)
+					pend |= 1u << i;
+			int it = 0;
+			while (pend) {
+#pragma unroll
+				for (int i = 0; i < 8; i++)
+					if (pend & (1u << i))
+						v[i] = ld_word(o.hw + base + i * (int)blockDim.x);
+#pragma unroll
+				for (int i = 0; i < 8; i++)
+					if ((pend & (1u << i)) && (uint32_t)(v[i] >> 32) == o.seq) {
+						pend &= ~(1u << i);
+						const int f = base + i * (int)blockDim.x; // = (j nb + b) QK + m
+						hs[(f / QK) * XSEG + f % QK] = __uint_as_float((uint32_t)v[i]);
+					}
+				if (pend && ++it >= SPIN_MAX) {
+					bad = 1;
+					break;
+				}
+				if (pend)
+					__builtin_amdgcn_s_sleep(1);
+			}
+		}
+		if (bad)
+			sbad = 1;
+	}
+	__syncthreads();
+	if (live)
+		part[task * R + r] = e >= 0 ? rb.dot((dfloat *)(hs + (size_t)task * XSEG)) : 0.0f;
+	__syncthreads();
+	float *outp = a.out + r0;
+	combine_rows(part, nb, k, R, sel_idx, sel_w, outp, a.res ? a.res + r0 : nullptr);
+	if (sbad && tid < R)
+		outp[tid] = __builtin_nanf("");
+}
+
 // ------------------------------------------------------------ recompute
 // Listed tokens of a large-T forward (their activations left the f16 range
 // of the matrix-core path; usually none), each recomputed whole in TIE's
@@ -706,6 +938,96 @@ hipError_t launch_decode(const Layer &L, const float *x, int k, const float *sil
 			      ? dec_launch(decode_down_kernel<TIE_GGML_Q4_K>, grid, dim3(threads), lds, s, g)
 			      : dec_launch(decode_down_kernel<TIE_GGML_Q6_K>, grid, dim3(threads), lds, s, g);
 	}
+	prof_end(s);
+	return err;
+}
+
+// ------------------------------------------------------------ one launch: launcher
+static void one_shape(const Layer &L, int k, int &rpr, int &rg, int &rd, int &threads, size_t &lds)
+{
+	const int nbd = L.d / QK, nbf = L.F / QK;
+	// gate/up: rg rows, 2 nb tasks per row; down: rd rows, k nb tasks per
+	// row (powers of two); router: rpr rows
+	rg = gu_rows(nbd);
+	rd = pick_rows(k * nbf, 16);
+	threads = round64(std::max(std::max(2 * nbd * rg, k * nbf * rd), L.E));
+	rpr = L.d <= 2048 ? 2 : 1;
+	const size_t lds_r = sizeof(float) * (size_t)(1 + rpr) * lane_major_floats(L.d);
+	const size_t lds_g = sizeof(float) * ((size_t)nbd * XSEG + 2 * nbd * rg);
+	const size_t lds_d = sizeof(float) * ((size_t)k * nbf * XSEG + (size_t)k * nbf * rd);
+	lds = std::max(lds_r, std::max(lds_g, lds_d));
+}
+
+bool decode_one_supported(const Layer &L, int k)
+{
+	if (!decode_supported(L, k) || L.E > INLINE_E)
+		return false;
+	int rpr, rg, rd, threads;
+	size_t lds;
+	one_shape(L, k, rpr, rg, rd, threads, lds);
+	return threads <= DEC_MAX_THREADS && lds <= DEC_MAX_LDS && 8 * rpr <= threads;
+}
+
+int decode_one_gate_up_groups(const Layer &L, int k)
+{
+	int rpr, rg, rd, threads;
+	size_t lds;
+	one_shape(L, k, rpr, rg, rd, threads, lds);
+	return (L.F / rg) * k;
+}
+
+hipError_t launch_decode_one(const Layer &L, const float *x, int k, const float *silu, int32_t *topk_idx,
+			     float *topk_w, float *out, const float *res, unsigned long long *lg, unsigned long long *hw,
+			     uint32_t seq, hipStream_t s)
+{
+	OneArgs o;
+	memset(&o, 0, sizeof o);
+	DecodeArgs &a = o.a;
+	a.w[0] = L.gate.data;
+	a.w[1] = L.up.data;
+	a.w[2] = L.down.data;
+	a.expert_bytes[0] = L.gate.expert_bytes;
+	a.expert_bytes[1] = L.up.expert_bytes;
+	a.expert_bytes[2] = L.down.expert_bytes;
+	a.d = L.d;
+	a.F = L.F;
+	a.E = L.E;
+	a.k = k;
+	a.x = x;
+	a.topk_idx = topk_idx;
+	a.topk_w = topk_w;
+	a.out = out;
+	a.res = res;
+	a.silu = silu;
+	a.routing = L.routing;
+	a.pbias = L.pbias;
+	int threads;
+	size_t lds;
+	one_shape(L, k, o.rpr, o.rg, o.rd, threads, lds);
+	o.router = L.router;
+	o.bias = L.bias;
+	o.lg = lg;
+	o.hw = hw;
+	o.seq = seq;
+	o.nr = (L.E + o.rpr - 1) / o.rpr;
+	o.ng = (L.F / o.rg) * k;
+	const int nd = L.d / o.rd;
+	const dim3 grid(o.nr + o.ng + nd);
+	const int tg = L.gate.type, tu = L.up.type, td = L.down.type;
+	hipError_t err;
+	prof_begin("decode_one", s);
+#define ONE(A, B)                                                                                                    \
+	(td == TIE_GGML_Q4_K ? dec_launch(decode_one_kernel<A, B, TIE_GGML_Q4_K>, grid, dim3(threads), lds, s, o)        \
+			     : dec_launch(decode_one_kernel<A, B, TIE_GGML_Q6_K>, grid, dim3(threads), lds, s, o))
+	if (tg == TIE_GGML_Q4_K && tu == TIE_GGML_Q4_K)
+		err = ONE(TIE_GGML_Q4_K, TIE_GGML_Q4_K);
+	else if (tg == TIE_GGML_Q4_K)
+		err = ONE(TIE_GGML_Q4_K, TIE_GGML_Q6_K);
+	else if (tu == TIE_GGML_Q4_K)
+		err = ONE(TIE_GGML_Q6_K, TIE_GGML_Q4_K);
+	else
+		err = ONE(TIE_GGML_Q6_K, TIE_GGML_Q6_K);
+#undef ONE
 	prof_end(s);
 	return err;
 }

@@ -171,16 +171,36 @@ __device__ __forceinline__ void topk_weights_wave(float my_s, int my_i, int k, c
 		return;
 	}
 	// softmax over the k selected logits: max over the slots, exp per lane
-	float mx = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_s), 0));
-	for (int j = 1; j < k; j++) {
-		const float sj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_s), j));
-		if (sj > mx)
-			mx = sj;
+	// (lanes of constant index for k <= 8, the common case)
+	auto rl = [](float v, int j) {
+		return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), j));
+	};
+	float mx = rl(my_s, 0);
+	if (k <= 8) {
+#pragma unroll
+		for (int j = 1; j < 8; j++) {
+			const float sj = rl(my_s, j);
+			if (j < k && sj > mx)
+				mx = sj;
+		}
+	} else {
+		for (int j = 1; j < k; j++) {
+			const float sj = rl(my_s, j);
+			if (sj > mx)
+				mx = sj;
+		}
 	}
 	const float ev = lane < k ? tie_expf_tab(my_s - mx, etab) : 0.0f;
 	float sum = 0.0f;
-	for (int j = 0; j < k; j++)
-		sum = sum + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ev), j));
+	if (k <= 8) {
+#pragma unroll
+		for (int j = 0; j < 8; j++)
+			if (j < k)
+				sum = sum + rl(ev, j);
+	} else {
+		for (int j = 0; j < k; j++)
+			sum = sum + rl(ev, j);
+	}
 	const float inv = __fdiv_rn(1.0f, sum);
 	if (lane < k) {
 		out_w[lane] = ev * inv;
@@ -270,6 +290,94 @@ __device__ __forceinline__ void topk_softmax_wave(const float *lg, int E, int k,
 				key[q] = 0;
 	}
 	topk_weights_wave(my_s, my_i, k, etab, out_idx, out_w, sig);
+}
+
+// The same selection by a whole workgroup, by ranks instead of k rounds of
+// wave-wide maxima: entry e's rank is the number of entries before it in
+// the order (value descending, index ascending), i.e. with a larger
+// composite key {logit_key, ~e}; the entries of rank < k that qualify
+// (key above KEY_NINF) take slot = rank.  The E x E comparisons are spread
+// over the whole workgroup (P = blockDim / E threads per entry, each
+// counting a contiguous 1/P of the entries).  Then wave 0 forms the
+// weights (topk_weights_wave).  Usage, E <= RANK_MAX_E <= blockDim:
+//   rank_key(v, e, ...) by thread e < E with its logit v, then
+//   topk_rank_block(...) (which begins and ends with a barrier).
+constexpr int RANK_MAX_E = 128;
+struct RankScratch {
+	alignas(16) unsigned long long ck[RANK_MAX_E];
+	float prob[RANK_MAX_E];
+	int cnt[4][RANK_MAX_E];
+	float sv[MAX_K];
+	int si[MAX_K];
+};
+__device__ __forceinline__ void rank_key(float v, int e, int routing, const float *pbias, const uint64_t *etab,
+					 RankScratch &S)
+{
+	float p = 0.0f;
+	if (routing == ROUTE_SIGMOID) {
+		p = __fdiv_rn(1.0f, 1.0f + tie_expf_tab(-v, etab));
+		v = pbias ? p + pbias[e] : p;
+	}
+	S.ck[e] = ((unsigned long long)logit_key(v) << 32) | (uint32_t)~(uint32_t)e;
+	S.prob[e] = p;
+}
+__device__ __forceinline__ void topk_rank_block(int E, int k, const uint64_t *etab, int32_t *out_idx, float *out_w,
+						int routing, RankScratch &S)
+{
+	const int tid = threadIdx.x;
+	const bool sig = routing == ROUTE_SIGMOID;
+	if (tid < k) {
+		S.sv[tid] = -__builtin_inff();
+		S.si[tid] = -1;
+	}
+	__syncthreads();
+	int P = (int)blockDim.x / E;
+	P = P > 4 ? 4 : P;
+	if (E == RANK_MAX_E && P >= 2) {
+		// 2 x 64 comparisons per entry, wave-uniform halves (E = 128 is
+		// two waves), fully unrolled 16-byte broadcast reads
+		P = 2;
+		if (tid < 2 * E) {
+			const int p = tid / E, i = tid - p * E;
+			const unsigned long long c = S.ck[i];
+			const ulonglong2 *q = reinterpret_cast<const ulonglong2 *>(S.ck) + 32 * p;
+			int n = 0;
+#pragma unroll
+			for (int j = 0; j < 32; j++) {
+				const ulonglong2 v = q[j];
+				n += (v.x > c ? 1 : 0) + (v.y > c ? 1 : 0);
+			}
+			S.cnt[p][i] = n;
+		}
+	} else if (tid < P * E) {
+		const int p = tid / E, i = tid - p * E;
+		const int lo = p * E / P, hi = (p + 1) * E / P;
+		const unsigned long long c = S.ck[i];
+		int n = 0;
+#pragma unroll 8
+		for (int j = lo; j < hi; j++)
+			n += S.ck[j] > c ? 1 : 0;
+		S.cnt[p][i] = n;
+	}
+	__syncthreads();
+	if (tid < E) {
+		int n = 0;
+		for (int p = 0; p < P; p++)
+			n += S.cnt[p][tid];
+		const uint32_t key = (uint32_t)(S.ck[tid] >> 32);
+		if (n < k && key > KEY_NINF) {
+			S.sv[n] = sig ? S.prob[tid] : key_logit(key);
+			S.si[n] = tid;
+		}
+	}
+	__syncthreads();
+	if (tid < 64) {
+		const int lane = tid;
+		const float my_s = lane < k ? S.sv[lane] : -__builtin_inff();
+		const int my_i = lane < k ? S.si[lane] : -1;
+		topk_weights_wave(my_s, my_i, k, etab, out_idx, out_w, sig);
+	}
+	__syncthreads();
 }
 
 // topk_softmax_wave with PER chosen for E (E <= MAX_E)

@@ -41,6 +41,7 @@ _NAMES = (
     ("tie::to_split_kernel", "mfma_gate_up"),
     ("tie::decode_gu_kernel", "decode_gate_up"),
     ("tie::decode_down_kernel", "decode_down"),
+    ("tie::decode_one_kernel", "decode_one"),
     ("tie::recompute_kernel", "recompute"),
     ("tie::dense_rows_kernel", "dense"),
     ("tie::dense_groups_kernel", "dense"),
@@ -115,12 +116,12 @@ def traffic(fetch_csv, write_csv, copy_fetch_csv, copy_write_csv, copy_bytes):
     w_scale = copy_bytes / (max(cw) * 1024.0)
     fetch = _per_dispatch(fetch_csv, "FETCH_SIZE")
     write = _per_dispatch(write_csv, "WRITE_SIZE")
-    # one combine (or, for one token, decode_down) dispatch per forward:
+    # one combine (or, for one token, decode_one / decode_down) dispatch per forward:
     # bytes per forward of a block kernel (some blocks are two kernels,
     # e.g. router logits + selection)
-    steps = len(fetch.get("combine") or fetch.get("decode_down") or [])
+    steps = len(fetch.get("combine") or fetch.get("decode_one") or fetch.get("decode_down") or [])
     if not steps:
-        raise ValueError("no combine / decode_down dispatches: cannot count forwards")
+        raise ValueError("no combine / decode_one / decode_down dispatches: cannot count forwards")
     res = {}
     for block in fetch:
         if block == "copy" or block not in write:
