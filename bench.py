@@ -257,7 +257,7 @@ def run_config(torch, tie_amd, wl, T, k, steps, warmup, flags, cfg=None, graph=F
         "combine": pairs * d * 4 + T * d * 4 * (3 if residual else 1),
         "rmsnorm": 2 * T * d * 4 + d * 4,
         "dispatch": pairs * 4 * 2,
-        "mfma_gate_up": U_avg * gu_b + T * d * 4 + pairs * F * h_bytes,
+        "mfma_gate_up": U_avg * gu_b + T * d * 2 + pairs * F * h_bytes,
         "mfma_down": U_avg * dn_b + pairs * F * h_bytes + pairs * d * y_bytes,
     }
     kern_flops = {

@@ -225,8 +225,7 @@ static size_t carve_workspace(uint8_t *b, size_t P, size_t FF, size_t DD, size_t
 		     o_act = take((EE + 1) * 4), o_logits = take(Tcap * EE * 4), o_h = take(2 * P * FF * 4),
 		     o_hb = take(P * FF * 2), o_y = take(P * DD * 4), o_xb = take(Tcap * DD * 2),
 		     o_hlo = take(P * FF * 2), o_xlo = take(Tcap * DD * 2), o_nm = take(Tcap * DD * 4);
-	const size_t max_tiles = (size_t)mfma_max_tiles((int)P, (int)EE);
-	const size_t o_te = take(2 * max_tiles * 4), o_tm = take(2 * max_tiles * 4), o_nt = take(8);
+	const size_t o_bc = take(EE * 4), o_mk = take(EE * (size_t)T4((int)Tcap)), o_bk = take(EE * T4((int)Tcap) * 4);
 	const size_t o_fl = take(Tcap * 4), o_fx = take(Tcap * 4), o_fc = take(4);
 	const size_t o_lg = take(EE * 8), o_dn = take((size_t)MAX_K * FF * 8);
 	if (!b)
@@ -244,16 +243,15 @@ static size_t carve_workspace(uint8_t *b, size_t P, size_t FF, size_t DD, size_t
 	w->xb = (uint16_t *)(b + o_xb);
 	w->hlo = (uint16_t *)(b + o_hlo);
 	w->xlo = (uint16_t *)(b + o_xlo);
-	w->tile_e = (int32_t *)(b + o_te);
-	w->tile_m0 = (int32_t *)(b + o_tm);
-	w->ntiles = (int32_t *)(b + o_nt);
+	w->bucket_cnt = (int32_t *)(b + o_bc);
+	w->sel = b + o_mk;
+	w->bucket = (int32_t *)(b + o_bk);
 	w->tok_flag = (int32_t *)(b + o_fl);
 	w->fix_list = (int32_t *)(b + o_fx);
 	w->fix_count = (int32_t *)(b + o_fc);
 	w->one_lg = (unsigned long long *)(b + o_lg);
 	w->one_h = (unsigned long long *)(b + o_dn);
 	w->one_seq = 0;
-	w->tile_cap = (int32_t)max_tiles;
 	w->cap_pairs = P;
 	w->cap_F = FF;
 	w->cap_d = DD;
@@ -456,11 +454,19 @@ static int forward(tie_hip_layer *layer, const float *x, int T, int k, float *ou
 		return rc;
 	Workspace &ws = *wsp;
 	if (mfma) {
+		// logits (clearing the selection bytes and the recomputation
+		// count), then selection, selection bytes and the A operand in one
+		// launch, then the per-expert pair lists
 		prof_begin("router", s);
-		HIP_TRY(launch_router(L, x, T, k, ws.logits, ws.topk_idx, ws.topk_w, s));
+		ZeroArgs z;
+		z.p2 = reinterpret_cast<int32_t *>(ws.sel);
+		z.n2 = L.E * T4(T) / 4;
+		z.one = ws.fix_count;
+		HIP_TRY(launch_router_logits(L, x, T, ws.logits, s, z));
+		HIP_TRY(launch_route_bucket(L, x, T, k, ws, s));
 		prof_end(s);
 		prof_begin("dispatch", s);
-		HIP_TRY(launch_dispatch(L, T, k, ws.topk_idx, ws, s));
+		HIP_TRY(launch_bucket_plan(L, T, k, ws, s));
 		prof_end(s);
 		HIP_TRY(launch_mfma_experts(L, x, T, k, g.silu, ws, s));
 		prof_begin("combine", s);

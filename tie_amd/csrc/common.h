@@ -92,22 +92,39 @@ struct Workspace {
 	uint16_t *hlo = nullptr;      // [T*k][F] SwiGLU activations, bf16 remainder (MFMA path, BF16 weights)
 	uint16_t *xb = nullptr;       // [T][d]   x as bf16 (MFMA path)
 	uint16_t *xlo = nullptr;      // [T][d]   x - bf16(x) as bf16 (MFMA path, BF16 weights)
-	int32_t *tile_e = nullptr;    // [2][max tiles] MFMA work lists (gate/up, down): expert of each tile
-	int32_t *tile_m0 = nullptr;   // [2][max tiles] first pair of the tile within the expert
-	int32_t *ntiles = nullptr;    // [2]
+	int32_t *bucket_cnt = nullptr; // [E]   MFMA path: pairs per expert
+	uint8_t *sel = nullptr;       // [E][T4(T)] MFMA path: slot + 1 that chose the expert (0: none)
+	int32_t *bucket = nullptr;    // [E][T4(T)] MFMA path: each expert's pair ids in token order
 	int32_t *tok_flag = nullptr;  // [T]      f16 path: token's activations left the f16 range
 	int32_t *fix_list = nullptr;  // [T]      flagged tokens (recomputed exactly after the forward)
 	int32_t *fix_count = nullptr; // [1]
 	unsigned long long *one_lg = nullptr; // [E]  one-launch decode: {seq, logit} words
 	unsigned long long *one_h = nullptr; // [MAX_K * F] one-launch decode: {seq, h} words
 	uint32_t one_seq = 0;         // one-launch decode: sequence number of the last call
-	int32_t tile_cap = 0;         // max tiles per list
 	size_t cap_pairs = 0, cap_F = 0, cap_d = 0, cap_E = 0;
 	void *alloc = nullptr;
 };
 
 // ---------------------------------------------------------------- launchers
-hipError_t launch_router_logits(const Layer &L, const float *x, int T, float *logits, hipStream_t s);
+// T rounded up to a multiple of 4 (the row stride of the MFMA path's
+// per-expert selection bytes and pair lists)
+inline int T4(int T)
+{
+	return (T + 3) & ~3;
+}
+// words the router logits kernel clears before the kernels that follow
+// accumulate into them
+struct ZeroArgs {
+	int32_t *p = nullptr, *p2 = nullptr;
+	int n = 0, n2 = 0;
+	int32_t *one = nullptr;
+};
+hipError_t launch_router_logits(const Layer &L, const float *x, int T, float *logits, hipStream_t s,
+				ZeroArgs z = ZeroArgs());
+// the matrix-core path's selection, grouping into per-expert buckets and
+// A-operand conversion (mfma.hip)
+hipError_t launch_route_bucket(const Layer &L, const float *x, int T, int k, Workspace &ws, hipStream_t s);
+hipError_t launch_bucket_plan(const Layer &L, int T, int k, Workspace &ws, hipStream_t s);
 hipError_t launch_router_select(const Layer &L, int T, int k, const float *logits, int32_t *topk_idx, float *topk_w,
 				hipStream_t s);
 hipError_t launch_router(const Layer &L, const float *x, int T, int k, float *logits, int32_t *topk_idx,
@@ -143,7 +160,6 @@ bool decode_one_supported(const Layer &L, int k);
 hipError_t launch_decode_one(const Layer &L, const float *x, int k, const float *silu, int32_t *topk_idx,
 			     float *topk_w, float *out, const float *res, unsigned long long *lg, unsigned long long *hw,
 			     uint32_t seq, hipStream_t s);
-int mfma_max_tiles(int npairs, int E); // per list
 struct Layer;
 int mfma_gu_rows(const Layer &L, int npairs); // rows per gate/up tile (the tile list's and the kernel's)
 // Dense F32-input matrix product through the expert GEMV kernels: out[t][r]

@@ -21,28 +21,20 @@ namespace tie {
 
 constexpr int DSP_THREADS = 1024;
 
-// One workgroup groups all pairs (group_pairs) and writes the MFMA work
-// list.
+// One workgroup groups all pairs (group_pairs): the exact path's grouping
+// for batches too large for route_group_kernel.
 constexpr int DSP_STAGE_MAX = 16384; // pairs staged in LDS at most (selections + list: 128 KiB)
 __global__ __launch_bounds__(DSP_THREADS) void dispatch_kernel(const int32_t *__restrict__ topk_idx, int npairs,
 							       int E, int32_t *__restrict__ offsets,
 							       int32_t *__restrict__ pairs,
-							       int32_t *__restrict__ active,
-							       int32_t *__restrict__ tile_e,
-							       int32_t *__restrict__ tile_m0,
-							       int32_t *__restrict__ ntiles, int tile_cap, int mt_gu,
-							       int32_t *__restrict__ fix_count)
+							       int32_t *__restrict__ active)
 {
-	// the f16 path's list of tokens to recompute starts empty
-	if (fix_count && threadIdx.x == 0)
-		*fix_count = 0;
 	extern __shared__ __attribute__((aligned(16))) int32_t sidx[];
 	__shared__ __attribute__((aligned(16))) int32_t cnt[MAX_E];
 	__shared__ int32_t cur[MAX_E];
 	__shared__ int wsum[DSP_THREADS / 64];
 	if (npairs > DSP_STAGE_MAX) {
-		group_pairs<DSP_THREADS>(topk_idx, npairs, E, cnt, cur, wsum, offsets, pairs, active, tile_e, tile_m0,
-					 ntiles, nullptr, tile_cap, mt_gu);
+		group_pairs<DSP_THREADS>(topk_idx, npairs, E, cnt, cur, wsum, offsets, pairs, active);
 		return;
 	}
 	// selections in, pair list out, both through LDS: the scattered
@@ -57,9 +49,7 @@ __global__ __launch_bounds__(DSP_THREADS) void dispatch_kernel(const int32_t *__
 	__syncthreads();
 	// pairs[0 .. valid): experts' lists back to back (the invalid selections,
 	// if any, were not placed)
-	const int valid =
-		group_pairs<DSP_THREADS>(sidx, npairs, E, cnt, cur, wsum, offsets, spairs, active, tile_e, tile_m0, ntiles,
-					 nullptr, tile_cap, mt_gu);
+	const int valid = group_pairs<DSP_THREADS>(sidx, npairs, E, cnt, cur, wsum, offsets, spairs, active);
 	const int v4 = valid >> 2;
 	for (int i = threadIdx.x; i < v4; i += DSP_THREADS)
 		reinterpret_cast<int4 *>(pairs)[i] = reinterpret_cast<const int4 *>(spairs)[i];
@@ -81,8 +71,7 @@ hipError_t launch_dispatch(const Layer &L, int T, int k, const int32_t *topk_idx
 		attr = true;
 	}
 	hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(DSP_THREADS), lds, s, topk_idx, npairs, L.E, ws.offsets,
-			   ws.pairs, ws.active, ws.tile_e, ws.tile_m0, ws.ntiles, ws.tile_cap, mfma_gu_rows(L, npairs),
-			   ws.fix_count);
+			   ws.pairs, ws.active);
 	return hipGetLastError();
 }
 
@@ -147,8 +136,7 @@ __global__ __launch_bounds__(DSP_THREADS) void route_group_kernel(const float *_
 	const int npairs = T * k;
 	for (int p = tid; p < npairs; p += DSP_THREADS)
 		topk_idx[p] = sidx[p];
-	group_pairs<DSP_THREADS>(sidx, npairs, E, cnt, cur, wsum, offsets, pairs, active, nullptr, nullptr, nullptr,
-				 lpt);
+	group_pairs<DSP_THREADS>(sidx, npairs, E, cnt, cur, wsum, offsets, pairs, active, lpt);
 }
 
 hipError_t launch_route_group(const Layer &L, int T, int k, const float *logits, Workspace &ws, hipStream_t s)

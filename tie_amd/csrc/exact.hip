@@ -496,8 +496,7 @@ template <int NT> __device__ __forceinline__ void inline_route(const ExactArgs &
 	}
 	// every workgroup groups on its own and must reach the same expert order:
 	// ascending expert index (the count order breaks ties by LDS atomics)
-	group_pairs<NT>(R.idx, T * k, E, R.cnt, R.cur, R.wsum, R.offsets, R.pairs, R.active, nullptr, nullptr,
-			nullptr);
+	group_pairs<NT>(R.idx, T * k, E, R.cnt, R.cur, R.wsum, R.offsets, R.pairs, R.active);
 	if (blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0) {
 		for (int i = tid; i < T * k; i += NT) {
 			a.topk_idx[i] = R.idx[i];

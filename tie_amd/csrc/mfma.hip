@@ -53,15 +53,16 @@
 // from both ends of f16's range), both with the K order inside each 8-group
 // 0,2,1,3,4,6,5,7 (the dequantised pairs' order).  A token whose x or scaled
 // h leaves the f16 range (|v| >= 65504, or not finite) is
-// listed by to_f16_kernel / the gate/up epilogue and recomputed afterwards
+// listed by route_bucket_kernel / the gate/up epilogue and recomputed afterwards
 // in TIE's exact arithmetic (decode.hip), which overwrites its output row.
 // The expert outputs y are stored as bf16.  With BF16 expert
 // weights (exact in bf16) the activations are split into a bf16 high part
-// and a bf16 remainder, stored as two bf16 planes (x by to_split_kernel, h
+// and a bf16 remainder, stored as two bf16 planes (x by route_bucket_kernel, h
 // by the gate/up epilogue), two MFMAs per product; this keeps the products
 // to ~16 mantissa bits; that path is HBM-bound, so the extra MFMA work is
 // hidden, and its y stays fp32.
 #include "common.h"
+#include "route.h"
 
 #include <type_traits>
 
@@ -143,7 +144,10 @@ struct MfmaArgs {
 	const uint16_t *a16;     // A as bf16 rows (gate/up: x [T][d] by token; down: h [P][F] by position)
 	const uint16_t *a16lo;   // split mode: the bf16 remainder plane of A
 	int k;                   // experts per token (token = pair / k)
-	const int32_t *offsets, *pairs, *tile_e, *tile_m0, *ntiles;
+	int E;                   // experts
+	const int32_t *cnt;      // [E] pairs per expert
+	const int32_t *bucket;   // [E][bstride] the expert's pair ids in token order
+	int bstride;
 	const float *silu;
 	uint16_t *h16;           // gate/up out (bf16, by position)
 	uint16_t *h16lo;         // gate/up out, split mode: bf16 remainder plane
@@ -754,7 +758,7 @@ __device__ __forceinline__ void stage_mfma(const BRegs<TYPE> &b, int st, const u
 // ------------------------------------------------------------------ kernel
 // One work tile with NMT live 32-row M tiles (nrows <= 32 NMT).
 template <int TYPE, bool DOWN, int NMT, int MTR>
-__device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_t *roff, int32_t *spair, int e,
+__device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_t *roff, const int32_t *spair, int e,
 					 int pbase, int nrows, int slab)
 {
 	using C = Cfg<TYPE, DOWN, MTR>;
@@ -780,11 +784,10 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 		as.roff = roff + (C::RPI * w + rsub) * ROFF_STRIDE;
 		if (t < C::MT) {
 			const int r = t < nrows ? t : 0;
-			const int pr = a.pairs[pbase + r];
+			const int pr = spair[r];
 			const int row = DOWN ? pbase + r : pr / a.k;
 			const int c = t / (C::RPI * NWAVES), ls = t % (C::RPI * NWAVES);
 			roff[ls * ROFF_STRIDE + c] = (uint32_t)((size_t)row * a.in * 2);
-			spair[t] = pr; // the tile rows' pair ids, for the epilogue
 		}
 		__syncthreads();
 	}
@@ -1083,7 +1086,7 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 					const float hs = hv * a.h_scale;
 					a.h16[(size_t)p * a.rows + pc] = __builtin_bit_cast(uint16_t, (_Float16)hs);
 					if (!(__builtin_fabsf(hs) < 65504.0f)) {
-						const int tok = a.pairs[p] / a.k;
+						const int tok = spair[mrow] / a.k;
 						if (a.tok_flag[tok] == 0) // listed already: no atomic
 							flag_token(a.tok_flag, a.fix_list, a.fix_count, tok);
 					}
@@ -1094,7 +1097,7 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 						a.h16lo[(size_t)p * a.rows + col] = bf16_bits(hv - bf16_bits_to_float(hi));
 				}
 			} else if (C::SPLIT) {
-				float *yr = a.y + (size_t)a.pairs[p] * a.rows + slab * DN_COLS + 64 * w + (lane & 31);
+				float *yr = a.y + (size_t)spair[mrow] * a.rows + slab * DN_COLS + 64 * w + (lane & 31);
 				yr[0] = acc[mt][0][i];
 				yr[32] = acc[mt][1][i];
 			} else {
@@ -1103,7 +1106,7 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 				// f16 weights' factor 2^F16_SHIFT and h's scale come out here
 				// (a power of two: exact)
 				const float unscale = C::F16 ? a.y_scale : 1.0f;
-				uint16_t *yr = a.y16 + (size_t)a.pairs[p] * a.rows + slab * DN_COLS + 64 * w + (lane & 31);
+				uint16_t *yr = a.y16 + (size_t)spair[mrow] * a.rows + slab * DN_COLS + 64 * w + (lane & 31);
 				yr[0] = bf16_bits(acc[mt][0][i] * unscale);
 				yr[32] = bf16_bits(acc[mt][1][i] * unscale);
 			}
@@ -1140,26 +1143,67 @@ mfma_experts_kernel(MfmaArgs a)
 	uint32_t *roff = reinterpret_cast<uint32_t *>(As + C::STAGE_BYTES);
 	int32_t *spair = reinterpret_cast<int32_t *>(roff + C::RPI * NWAVES * ROFF_STRIDE);
 
-	// XCD-aware tile order.  Consecutive workgroup ids are spread round-robin
-	// over the 8 XCDs, each with its own L2.  The id is remapped so that each
-	// XCD takes a contiguous run of (tile, column slab) work items; the slabs
-	// of one expert tile then share an XCD and read the tile's gathered
-	// activation rows from that XCD's L2.
-	const int nslab = gridDim.x;
-	const int live = *a.ntiles * nslab;
-	const int per_xcd = (live + 7) / 8;
-	const int lin = blockIdx.y * gridDim.x + blockIdx.x;
-	const int v = (lin % 8) * per_xcd + lin / 8;
-	if (lin / 8 >= per_xcd || v >= live)
-		return;
-	const int tile = v / nslab;
-	const int slab = v % nslab;
-	// an expert's pairs are split evenly over ceil(count / MT) tiles
-	const int e = a.tile_e[tile], m0 = a.tile_m0[tile];
-	const int cnt = a.offsets[e + 1] - a.offsets[e];
+	// The work tiles: expert e's pairs (a.cnt[e] of them, bucket e) split
+	// evenly over ceil(cnt / MT) tiles, the tiles numbered in expert order.
+	// Every workgroup derives its tile from the counts: exclusive scans of
+	// the tile and pair counts over the experts (thread i owns experts
+	// 4i .. 4i + 3), in the idle stage buffers.
+	int e, li, off, slab;
+	{
+		int *sc = reinterpret_cast<int *>(As); // [MF_THREADS / 64] scan | e, li, off
+		const int t = threadIdx.x;
+		int c4[4], n4[4], csum = 0, nsum = 0;
+#pragma unroll
+		for (int i = 0; i < 4; i++) {
+			const int ex = 4 * t + i;
+			c4[i] = ex < a.E ? a.cnt[ex] : 0;
+			n4[i] = (c4[i] + MT - 1) / MT;
+			csum += c4[i];
+			nsum += n4[i];
+		}
+		int ntiles, ctot;
+		int nbase = block_exclusive_scan<MF_THREADS>(nsum, sc, ntiles);
+		int cbase = block_exclusive_scan<MF_THREADS>(csum, sc, ctot);
+		// this workgroup's item (XCD-aware order: consecutive workgroup ids
+		// go round-robin over the 8 XCDs, each with its own L2; the id is
+		// remapped so that each XCD takes a contiguous run of (tile, column
+		// slab) items, and the slabs of one expert tile share an XCD and read
+		// the tile's gathered activation rows from its L2)
+		const int nslab = gridDim.x;
+		const int live = ntiles * nslab;
+		const int per_xcd = (live + 7) / 8;
+		const int lin = blockIdx.y * gridDim.x + blockIdx.x;
+		const int v = (lin % 8) * per_xcd + lin / 8;
+		if (lin / 8 >= per_xcd || v >= live)
+			return;
+		const int tile = v / nslab;
+		slab = v % nslab;
+#pragma unroll
+		for (int i = 0; i < 4; i++) {
+			if (tile >= nbase && tile < nbase + n4[i]) {
+				sc[MF_THREADS / 64] = 4 * t + i;
+				sc[MF_THREADS / 64 + 1] = tile - nbase;
+				sc[MF_THREADS / 64 + 2] = cbase;
+			}
+			nbase += n4[i];
+			cbase += c4[i];
+		}
+		__syncthreads();
+		e = sc[MF_THREADS / 64];
+		li = sc[MF_THREADS / 64 + 1];
+		off = sc[MF_THREADS / 64 + 2];
+		__syncthreads(); // the stage buffers are free again
+	}
+	const int cnt = a.cnt[e];
 	const int ntl = (cnt + MT - 1) / MT;
-	const int pbase = a.offsets[e] + m0;
-	const int nrows = min((cnt + ntl - 1) / ntl, cnt - m0);
+	const int rpt = (cnt + ntl - 1) / ntl;
+	const int m0 = li * rpt;
+	const int pbase = off + m0; // the tile's first row in the dense h rows
+	const int nrows = min(rpt, cnt - m0);
+	// the tile's pair ids (rows m0 .. m0 + nrows - 1 of the expert's bucket)
+	if (threadIdx.x < nrows)
+		spair[threadIdx.x] = a.bucket[(size_t)e * a.bstride + m0 + threadIdx.x];
+	__syncthreads();
 #ifdef TIE_MFMA_FIXED_NMT
 	// one tile height for every tile (one copy of run_tile's code)
 	run_tile<TYPE, DOWN, MT_TILES, MTR>(a, As, roff, spair, e, pbase, nrows, slab);
@@ -1190,61 +1234,203 @@ mfma_experts_kernel(MfmaArgs a)
 	}
 }
 
-// x (fp32) -> bf16 rows for the gate/up A operand
-__global__ void to_bf16_kernel(const float *__restrict__ x, uint16_t *__restrict__ y, size_t n4)
-{
-	for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (size_t)gridDim.x * blockDim.x) {
-		const float4 v = reinterpret_cast<const float4 *>(x)[i];
-		reinterpret_cast<uint2 *>(y)[i] = make_uint2(pack_bf16(v.x, v.y), pack_bf16(v.z, v.w));
-	}
-}
+// ------------------------------------------------------------ routing
+// The matrix-core path's selection and grouping, one wave per token, after
+// the router logits: top-k + softmax (topk_softmax: find_top_k and softmax,
+// engine.c:864-914), then each selected expert e records the slot that
+// chose it, sel[e][t] = j + 1 (a byte of its own: no atomics; the array is
+// zeroed by the logits kernel).  bucket_plan_kernel turns these rows into
+// per-expert pair lists.  The same wave converts the token's x row into the
+// gate/up A operand:
+//   MODE 0: bf16
+//   MODE 1: f16 with the K order inside each 8-group 0,2,1,3,4,6,5,7 (the
+//           order of the dequantised weight pairs); the token is flagged
+//           and listed for the exact recomputation when any x is not finite
+//           or not below 65504 in magnitude
+//   MODE 2: bf16 high and remainder planes (BF16 weights)
+constexpr int RB_THREADS = 256;
+struct BucketArgs {
+	const float *logits;
+	int T, ts, E, k, d, routing; // ts: row stride of sel (T rounded up to 4)
+	const float *pbias;
+	int32_t *topk_idx;
+	float *topk_w;
+	uint8_t *sel;
+	const float *x;
+	uint16_t *xa, *xlo;
+	int32_t *flag, *list, *count;
+};
 
-// x (fp32) -> f16 rows for the f16 gate/up A operand, K order inside each
-// 8-group 0,2,1,3,4,6,5,7 (the order of the dequantised weight pairs).  One
-// workgroup per token row: flag[t] = 1 (and t listed for the exact
-// recomputation) when any x of the row is not finite or not below 65504 in
-// magnitude, else 0.
-constexpr int F16_THREADS = 256;
-__global__ __launch_bounds__(F16_THREADS) void to_f16_kernel(const float *__restrict__ x, uint16_t *__restrict__ y,
-							      int d, int32_t *__restrict__ flag,
-							      int32_t *__restrict__ list, int32_t *__restrict__ count)
+template <int MODE> __global__ __launch_bounds__(RB_THREADS) void route_bucket_kernel(BucketArgs r)
 {
-	const int t = blockIdx.x;
-	const float4 *xr = reinterpret_cast<const float4 *>(x + (size_t)t * d);
-	f16x8 *yr = reinterpret_cast<f16x8 *>(y + (size_t)t * d);
+	__shared__ uint64_t etab[32];
+	if (threadIdx.x < 32) {
+		const uint64_t tab[32] = TIE_EXP2_TABLE;
+		etab[threadIdx.x] = tab[threadIdx.x];
+	}
+	__syncthreads();
+	const int lane = threadIdx.x & 63;
+	const int t = blockIdx.x * (RB_THREADS / 64) + (threadIdx.x >> 6);
+	if (t >= r.T)
+		return;
+	// the token's x row in flight during the selection: RB_X float4 per
+	// lane per round (8 consecutive floats, one f16x8 of the A row, per
+	// pair of float4)
+	constexpr int RB_X = 8;
+	const float4 *xr = reinterpret_cast<const float4 *>(r.x + (size_t)t * r.d);
+	const int n4 = r.d / 4;
+	float4 xv[RB_X];
+#pragma unroll
+	for (int i = 0; i < RB_X / 2; i++) {
+		const int q = 2 * (lane + 64 * i);
+		xv[2 * i] = q < n4 ? xr[q] : make_float4(0, 0, 0, 0);
+		xv[2 * i + 1] = q < n4 ? xr[q + 1] : make_float4(0, 0, 0, 0);
+	}
+	topk_softmax(r.logits + (size_t)t * r.E, r.E, r.k, etab, r.topk_idx + (size_t)t * r.k, r.topk_w + (size_t)t * r.k,
+		     r.routing, r.pbias);
+	if (lane < r.k) {
+		// lane j wrote slot j above
+		const int e = r.topk_idx[(size_t)t * r.k + lane];
+		if (e >= 0)
+			r.sel[(size_t)e * r.ts + t] = (uint8_t)(lane + 1);
+	}
 	int bad = 0;
-	for (int i = threadIdx.x; i < d / 8; i += F16_THREADS) {
-		const float4 a = xr[2 * i], c = xr[2 * i + 1];
-		const float m = __builtin_fmaxf(__builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(a.x), __builtin_fabsf(a.y)),
-								__builtin_fmaxf(__builtin_fabsf(a.z), __builtin_fabsf(a.w))),
-						__builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(c.x), __builtin_fabsf(c.y)),
-								__builtin_fmaxf(__builtin_fabsf(c.z), __builtin_fabsf(c.w))));
-		// fmax drops NaN: test the values themselves for NaN
-		const bool nan = a.x != a.x || a.y != a.y || a.z != a.z || a.w != a.w || c.x != c.x || c.y != c.y ||
-				 c.z != c.z || c.w != c.w;
-		bad |= (nan || !(m < 65504.0f)) ? 1 : 0;
-		const f16x8 h = {(_Float16)a.x, (_Float16)a.z, (_Float16)a.y, (_Float16)a.w,
-				 (_Float16)c.x, (_Float16)c.z, (_Float16)c.y, (_Float16)c.w};
-		yr[i] = h;
+	for (int base = 0; base < n4; base += 128 * (RB_X / 2)) {
+		if (base > 0) {
+#pragma unroll
+			for (int i = 0; i < RB_X / 2; i++) {
+				const int q = base + 2 * (lane + 64 * i);
+				xv[2 * i] = q < n4 ? xr[q] : make_float4(0, 0, 0, 0);
+				xv[2 * i + 1] = q < n4 ? xr[q + 1] : make_float4(0, 0, 0, 0);
+			}
+		}
+#pragma unroll
+		for (int i = 0; i < RB_X / 2; i++) {
+			const int q = base + 2 * (lane + 64 * i); // float4 index of the pair's first half
+			if (q >= n4)
+				continue;
+			const float4 a = xv[2 * i], c = xv[2 * i + 1];
+			if constexpr (MODE == 1) {
+				const float m = __builtin_fmaxf(
+					__builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(a.x), __builtin_fabsf(a.y)),
+							__builtin_fmaxf(__builtin_fabsf(a.z), __builtin_fabsf(a.w))),
+					__builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(c.x), __builtin_fabsf(c.y)),
+							__builtin_fmaxf(__builtin_fabsf(c.z), __builtin_fabsf(c.w))));
+				// fmax drops NaN: test the values themselves for NaN
+				const bool nan = a.x != a.x || a.y != a.y || a.z != a.z || a.w != a.w || c.x != c.x ||
+						 c.y != c.y || c.z != c.z || c.w != c.w;
+				bad |= (nan || !(m < 65504.0f)) ? 1 : 0;
+				const f16x8 h = {(_Float16)a.x, (_Float16)a.z, (_Float16)a.y, (_Float16)a.w,
+						 (_Float16)c.x, (_Float16)c.z, (_Float16)c.y, (_Float16)c.w};
+				reinterpret_cast<f16x8 *>(r.xa + (size_t)t * r.d)[q / 2] = h;
+			} else if constexpr (MODE == 2) {
+				uint4 hi, lo;
+				const float h0 = (float)(__bf16)a.x, h1 = (float)(__bf16)a.y, h2 = (float)(__bf16)a.z,
+					    h3 = (float)(__bf16)a.w, h4 = (float)(__bf16)c.x, h5 = (float)(__bf16)c.y,
+					    h6 = (float)(__bf16)c.z, h7 = (float)(__bf16)c.w;
+				hi = make_uint4(pack_bf16(h0, h1), pack_bf16(h2, h3), pack_bf16(h4, h5), pack_bf16(h6, h7));
+				lo = make_uint4(pack_bf16(a.x - h0, a.y - h1), pack_bf16(a.z - h2, a.w - h3),
+						pack_bf16(c.x - h4, c.y - h5), pack_bf16(c.z - h6, c.w - h7));
+				reinterpret_cast<uint4 *>(r.xa + (size_t)t * r.d)[q / 2] = hi;
+				reinterpret_cast<uint4 *>(r.xlo + (size_t)t * r.d)[q / 2] = lo;
+			} else {
+				reinterpret_cast<uint4 *>(r.xa + (size_t)t * r.d)[q / 2] =
+					make_uint4(pack_bf16(a.x, a.y), pack_bf16(a.z, a.w), pack_bf16(c.x, c.y), pack_bf16(c.z, c.w));
+			}
+		}
 	}
-	bad = __syncthreads_or(bad);
-	if (threadIdx.x == 0) {
-		flag[t] = bad;
-		if (bad)
-			list[atomicAdd(count, 1)] = t;
+	if constexpr (MODE == 1) {
+		bad = __any(bad);
+		if (lane == 0) {
+			r.flag[t] = bad;
+			if (bad)
+				r.list[atomicAdd(r.count, 1)] = t;
+		}
 	}
 }
 
-// x (fp32) -> bf16 high and remainder planes for the split gate/up A operand
-__global__ void to_split_kernel(const float *__restrict__ x, uint16_t *__restrict__ hi, uint16_t *__restrict__ lo,
-				size_t n4)
+hipError_t launch_route_bucket(const Layer &L, const float *x, int T, int k, Workspace &ws, hipStream_t s)
 {
-	for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (size_t)gridDim.x * blockDim.x) {
-		const float4 v = reinterpret_cast<const float4 *>(x)[i];
-		const float h0 = (float)(__bf16)v.x, h1 = (float)(__bf16)v.y, h2 = (float)(__bf16)v.z, h3 = (float)(__bf16)v.w;
-		reinterpret_cast<uint2 *>(hi)[i] = make_uint2(pack_bf16(h0, h1), pack_bf16(h2, h3));
-		reinterpret_cast<uint2 *>(lo)[i] = make_uint2(pack_bf16(v.x - h0, v.y - h1), pack_bf16(v.z - h2, v.w - h3));
+	BucketArgs r;
+	r.logits = ws.logits;
+	r.T = T;
+	r.ts = T4(T);
+	r.E = L.E;
+	r.k = k;
+	r.d = L.d;
+	r.routing = L.routing;
+	r.pbias = L.pbias;
+	r.topk_idx = ws.topk_idx;
+	r.topk_w = ws.topk_w;
+	r.sel = ws.sel;
+	r.x = x;
+	r.xa = ws.xb;
+	r.xlo = ws.xlo;
+	r.flag = ws.tok_flag;
+	r.list = ws.fix_list;
+	r.count = ws.fix_count;
+	const dim3 grid((T + RB_THREADS / 64 - 1) / (RB_THREADS / 64));
+	if (L.gate.type == TIE_GGML_BF16)
+		hipLaunchKernelGGL(route_bucket_kernel<2>, grid, dim3(RB_THREADS), 0, s, r);
+	else if (TIE_MFMA_F16)
+		hipLaunchKernelGGL(route_bucket_kernel<1>, grid, dim3(RB_THREADS), 0, s, r);
+	else
+		hipLaunchKernelGGL(route_bucket_kernel<0>, grid, dim3(RB_THREADS), 0, s, r);
+	return hipGetLastError();
+}
+
+hipError_t launch_bucket_plan(const Layer &L, int T, int k, Workspace &ws, hipStream_t s);
+
+// Per-expert pair lists from the selection bytes, one workgroup per expert
+// e: the tokens t with sel[e][t] = j + 1 != 0 in token order (ranks by an
+// exclusive scan of each thread's count over 4 tokens per word): bucket[e]
+// [rank] = t k + j, cnt[e] = their number.  No atomics: the expert kernels
+// read the counts and their tiles' rows from here.
+constexpr int BP_THREADS = 256;
+__global__ __launch_bounds__(BP_THREADS) void bucket_plan_kernel(const uint8_t *__restrict__ sel, int k, int T,
+								  int32_t *__restrict__ cnt, int32_t *__restrict__ bucket)
+{
+	__shared__ int wsum[BP_THREADS / 64];
+	const int e = blockIdx.x, t = threadIdx.x;
+	const uint32_t *row = reinterpret_cast<const uint32_t *>(sel + (size_t)e * T); // T % 4 == 0
+	int32_t *bk = bucket + (size_t)e * T;
+	const int nw = T / 4;
+	int carry = 0;
+	for (int w0 = 0; w0 < nw; w0 += 4 * BP_THREADS) {
+		// 4 words (16 tokens) per thread
+		uint32_t wd[4];
+		int n = 0;
+#pragma unroll
+		for (int i = 0; i < 4; i++) {
+			const int wi = w0 + 4 * t + i;
+			wd[i] = wi < nw ? row[wi] : 0u;
+#pragma unroll
+			for (int b = 0; b < 4; b++)
+				n += ((wd[i] >> (8 * b)) & 0xffu) ? 1 : 0;
+		}
+		int tot;
+		int rk = carry + block_exclusive_scan<BP_THREADS>(n, wsum, tot);
+#pragma unroll
+		for (int i = 0; i < 4; i++)
+#pragma unroll
+			for (int b = 0; b < 4; b++) {
+				const uint32_t v = (wd[i] >> (8 * b)) & 0xffu;
+				if (v) {
+					const int tok = 4 * (w0 + 4 * t + i) + b;
+					bk[rk++] = tok * k + (int)v - 1;
+				}
+			}
+		carry += tot;
 	}
+	if (t == 0)
+		cnt[e] = carry;
+}
+
+hipError_t launch_bucket_plan(const Layer &L, int T, int k, Workspace &ws, hipStream_t s)
+{
+	hipLaunchKernelGGL(bucket_plan_kernel, dim3(L.E), dim3(BP_THREADS), 0, s, ws.sel, k, T4(T), ws.bucket_cnt,
+			   ws.bucket);
+	return hipGetLastError();
 }
 
 template <int TYPE, bool DOWN, int MTR = 0>
@@ -1289,13 +1475,6 @@ bool mfma_f16_operands(const Layer &L)
 	return TIE_MFMA_F16 && (q || qd);
 }
 
-int mfma_max_tiles(int npairs, int E)
-{
-	constexpr int mt0 = MFMA_MT_GU < MFMA_MT_DN ? MFMA_MT_GU : MFMA_MT_DN;
-	constexpr int mt = mt0 < MFMA_MT_GU_SMALL ? mt0 : MFMA_MT_GU_SMALL;
-	return (npairs + mt - 1) / mt + E;
-}
-
 // Quantised gate/up with at most TIE_MFMA_SMALL_AVG pairs per expert on
 // average: 64-row tiles, three waves per SIMD (smaller accumulator and LDS
 // footprint); measured faster there, slower for large expert counts.
@@ -1316,6 +1495,7 @@ hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, con
 		return hipErrorInvalidValue;
 	const bool split = L.gate.type == TIE_GGML_BF16;
 	const bool split_down = L.down.type == TIE_GGML_BF16;
+	(void)x;
 	// the kernels address activation rows with 32-bit byte offsets; tiles
 	// are GU_COLS gate/up and DN_COLS down columns wide
 	if ((size_t)T * L.d * 4 > 0xfffffffeu || (size_t)npairs * L.F * 4 > 0xfffffffeu || L.F % GU_COLS ||
@@ -1323,12 +1503,10 @@ hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, con
 		return hipErrorInvalidValue;
 	MfmaArgs a;
 	a.k = k;
-	a.offsets = ws.offsets;
-	a.pairs = ws.pairs;
-	// gate/up tile list (list 0)
-	a.tile_e = ws.tile_e;
-	a.tile_m0 = ws.tile_m0;
-	a.ntiles = ws.ntiles;
+	a.E = L.E;
+	a.cnt = ws.bucket_cnt;
+	a.bucket = ws.bucket;
+	a.bstride = T4(T);
 	a.silu = silu;
 	a.y = ws.y;
 	a.y16 = reinterpret_cast<uint16_t *>(ws.y);
@@ -1338,25 +1516,15 @@ hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, con
 	a.tok_flag = ws.tok_flag;
 	a.fix_list = ws.fix_list;
 	a.fix_count = ws.fix_count;
-	// grid rows: each list's tile bound for its own tile rows, plus 8 rows:
-	// the XCD remap in the kernel reaches every live item only with at least
-	// 8 * ceil(live / 8) workgroups (rows past the list exit at once)
+	// grid rows: a bound on each kernel's tiles (its own tile rows) plus 8
+	// rows: the XCD remap in the kernel reaches every live item only with
+	// at least 8 * ceil(live / 8) workgroups (rows past the tiles exit at
+	// once)
 	const int mt_gu = mfma_gu_rows(L, npairs);
 	const int gu_tiles = (npairs + mt_gu - 1) / mt_gu + L.E + 8;
 	const int dn_tiles = (npairs + MFMA_MT_DN - 1) / MFMA_MT_DN + L.E + 8;
 
 	prof_begin("mfma_gate_up", s);
-	{
-		const size_t n4 = (size_t)T * L.d / 4;
-		const dim3 g((unsigned)((n4 + 255) / 256 < 4096 ? (n4 + 255) / 256 : 4096));
-		if (split)
-			hipLaunchKernelGGL(to_split_kernel, g, dim3(256), 0, s, x, ws.xb, ws.xlo, n4);
-		else if (TIE_MFMA_F16 && (L.gate.type == TIE_GGML_Q4_K || L.gate.type == TIE_GGML_Q6_K))
-			hipLaunchKernelGGL(to_f16_kernel, dim3(T), dim3(F16_THREADS), 0, s, x, ws.xb, L.d, ws.tok_flag,
-					   ws.fix_list, ws.fix_count);
-		else
-			hipLaunchKernelGGL(to_bf16_kernel, g, dim3(256), 0, s, x, ws.xb, n4);
-	}
 	a.w[0] = L.gate.data;
 	a.w[1] = L.up.data;
 	a.expert_bytes[0] = L.gate.expert_bytes;
@@ -1373,10 +1541,6 @@ hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, con
 		return err;
 
 	prof_begin("mfma_down", s);
-	// down tile list (list 1)
-	a.tile_e = ws.tile_e + ws.tile_cap;
-	a.tile_m0 = ws.tile_m0 + ws.tile_cap;
-	a.ntiles = ws.ntiles + 1;
 	a.w[0] = a.w[1] = L.down.data;
 	a.expert_bytes[0] = a.expert_bytes[1] = L.down.expert_bytes;
 	a.rows = L.d;

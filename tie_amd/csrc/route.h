@@ -555,16 +555,12 @@ template <int NT> __device__ __forceinline__ int block_exclusive_scan(int v, int
 // is not fixed: every pair is computed on its own row, so results do not
 // depend on it) and active[0..E] (experts with pairs, by descending pair
 // count with lpt -- ties in any order --, else ascending; active[E] =
-// their number).  With tile_e non-null it also writes the two MFMA work
-// lists (list l at offset l * tile_cap): each active expert's pairs split
-// evenly over ceil(count / MT) tiles, MT = mt_gu (list 0, gate/up) or
-// MFMA_MT_DN (list 1, down).  cnt / cur: LDS scratch of E ints each; wsum:
+// their number).  cnt / cur: LDS scratch of E ints each; wsum:
 // LDS scratch of NT/64 ints.  Output pointers may be LDS or global memory.
 template <int NT>
 __device__ __forceinline__ int group_pairs(const int32_t *idx, int npairs, int E, int32_t *cnt, int32_t *cur,
 					    int *wsum, int32_t *offsets, int32_t *pairs, int32_t *active,
-					    int32_t *tile_e, int32_t *tile_m0, int32_t *ntiles, int *lpt = nullptr,
-					    int tile_cap = 0, int mt_gu = MFMA_MT_GU)
+					    int *lpt = nullptr)
 {
 	const int tid = threadIdx.x;
 	for (int e = tid; e < E; e += NT)
@@ -614,26 +610,6 @@ __device__ __forceinline__ int group_pairs(const int32_t *idx, int npairs, int E
 		cur[e] = off;
 		if (c > 0)
 			active[rank] = e;
-	}
-	if (tile_e) {
-		// two lists (gate/up tiles of mt_gu rows, down tiles of
-		// MFMA_MT_DN rows), list l at tile_e + l * tile_cap
-#pragma unroll
-		for (int l = 0; l < 2; l++) {
-			const int mt = l == 0 ? mt_gu : MFMA_MT_DN;
-			int ntot;
-			const int nt = (c + mt - 1) / mt;
-			const int toff = block_exclusive_scan<NT>(nt, wsum, ntot);
-			if (e < E) {
-				const int rpt = nt > 0 ? (c + nt - 1) / nt : 0;
-				for (int t = 0; t < nt; t++) {
-					tile_e[l * tile_cap + toff + t] = e;
-					tile_m0[l * tile_cap + toff + t] = t * rpt;
-				}
-			}
-			if (tid == 0)
-				ntiles[l] = ntot;
-		}
 	}
 	if (tid == 0) {
 		offsets[E] = total;

@@ -25,6 +25,20 @@
 
 namespace tie {
 
+// Words the next kernels accumulate into (the matrix-core path's per-expert
+// pair counts and token masks, and its recomputation count), cleared by
+// the logits kernel's workgroups (grid-strided)
+__device__ __forceinline__ void zero_words(const ZeroArgs &z)
+{
+	const int nb = gridDim.x * gridDim.y, b = blockIdx.y * gridDim.x + blockIdx.x;
+	for (int i = b * blockDim.x + threadIdx.x; i < z.n; i += nb * blockDim.x)
+		z.p[i] = 0;
+	for (int i = b * blockDim.x + threadIdx.x; i < z.n2; i += nb * blockDim.x)
+		z.p2[i] = 0;
+	if (z.one && b == 0 && threadIdx.x == 0)
+		*z.one = 0;
+}
+
 // ------------------------------------------------------------ router_small
 // T <= RS_TOK: one workgroup per expert row; the row and the tokens are
 // staged in LDS with coalesced 16-byte loads and thread (t, l) runs the
@@ -36,8 +50,9 @@ constexpr int RS_THREADS = 256;
 __global__ __launch_bounds__(RS_THREADS) void router_small_kernel(const float *__restrict__ x,
 								  const float *__restrict__ W,
 								  const float *__restrict__ bias, int T, int d, int E,
-								  float *__restrict__ logits)
+								  float *__restrict__ logits, ZeroArgs z)
 {
+	zero_words(z);
 	extern __shared__ float lds[]; // W row | x [RS_TOK], lane-major (lane_chain)
 	float *ws = lds;
 	float *xs = lds + lane_major_floats(d);
@@ -70,8 +85,9 @@ constexpr int RM_THREADS = RM_TOK * 8;
 __global__ __launch_bounds__(RM_THREADS) void router_mid_kernel(const float *__restrict__ x,
 								const float *__restrict__ W,
 								const float *__restrict__ bias, int T, int d, int E,
-								float *__restrict__ logits)
+								float *__restrict__ logits, ZeroArgs z)
 {
+	zero_words(z);
 	extern __shared__ float ws[]; // W row [d]
 	const int e = blockIdx.x;
 	const int t0 = blockIdx.y * RM_TOK;
@@ -175,8 +191,9 @@ __device__ __forceinline__ void rt_barrier()
 __global__ __launch_bounds__(RT_THREADS) void router_logits_kernel(const float *__restrict__ x,
 								   const float *__restrict__ WT,
 								   const float *__restrict__ bias, int T, int d, int E,
-								   float *__restrict__ logits)
+								   float *__restrict__ logits, ZeroArgs z)
 {
+	zero_words(z);
 	extern __shared__ __attribute__((aligned(16))) uint8_t rt_lds[];
 
 	const int tid = threadIdx.x;
@@ -288,13 +305,13 @@ __global__ __launch_bounds__(RW_THREADS) void router_topk_kernel(const float *__
 			     pbias);
 }
 
-hipError_t launch_router_logits(const Layer &L, const float *x, int T, float *logits, hipStream_t s)
+hipError_t launch_router_logits(const Layer &L, const float *x, int T, float *logits, hipStream_t s, ZeroArgs z)
 {
 	const int d = L.d, E = L.E;
 	if (T <= RS_TOK && sizeof(float) * (size_t)(8 * (d / 8 + 4)) * (1 + RS_TOK) <= 160 * 1024) {
 		const size_t lds = sizeof(float) * (size_t)(8 * (d / 8 + 4)) * (1 + RS_TOK);
 		hipLaunchKernelGGL(router_small_kernel, dim3(E), dim3(RS_THREADS), lds, s, x, L.router, L.bias, T, d, E,
-				   logits);
+				   logits, z);
 		return hipGetLastError();
 	}
 	// the tiled kernel above 256 tokens: below that its one chunk in flight
@@ -309,11 +326,11 @@ hipError_t launch_router_logits(const Layer &L, const float *x, int T, float *lo
 			attr = true;
 		}
 		hipLaunchKernelGGL(router_logits_kernel, dim3((T + RT_TOK - 1) / RT_TOK, E / RT_EXP), dim3(RT_THREADS),
-				   RT_LDS, s, x, L.routerT, L.bias, T, d, E, logits);
+				   RT_LDS, s, x, L.routerT, L.bias, T, d, E, logits, z);
 		return hipGetLastError();
 	}
 	hipLaunchKernelGGL(router_mid_kernel, dim3(E, (T + RM_TOK - 1) / RM_TOK), dim3(RM_THREADS),
-			   sizeof(float) * (size_t)d, s, x, L.router, L.bias, T, d, E, logits);
+			   sizeof(float) * (size_t)d, s, x, L.router, L.bias, T, d, E, logits, z);
 	return hipGetLastError();
 }
 

@@ -36,9 +36,8 @@ _NAMES = (
     ("tie::dispatch_kernel", "dispatch"),
     ("tie::combine_kernel", "combine"),
     ("tie::rmsnorm_kernel", "rmsnorm"),
-    ("tie::to_bf16_kernel", "mfma_gate_up"),
-    ("tie::to_f16_kernel", "mfma_gate_up"),
-    ("tie::to_split_kernel", "mfma_gate_up"),
+    ("tie::route_bucket_kernel", "router"),
+    ("tie::bucket_plan_kernel", "dispatch"),
     ("tie::decode_gu_kernel", "decode_gate_up"),
     ("tie::decode_down_kernel", "decode_down"),
     ("tie::decode_one_kernel", "decode_one"),
