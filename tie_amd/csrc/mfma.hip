@@ -662,9 +662,10 @@ __device__ __forceinline__ void stage_barrier()
 // Cycle accounting of the matrix-core kernels (diagnostic builds only:
 // -DTIE_MFMA_TRACE): summed over workgroups (wave 0 of each), [down][0]
 // cycles in run_tile, [1] in stage barriers, [2] in the epilogue, [3]
-// workgroups; read by tie_hip_debug_mfma_trace.
+// workgroups, [4] cycles from kernel entry to the tile's start (the tile
+// mapping); read by tie_hip_debug_mfma_trace.
 #ifdef TIE_MFMA_TRACE
-__device__ unsigned long long g_mfma_trace[2][4];
+__device__ unsigned long long g_mfma_trace[2][8];
 #endif
 
 // The same, but the N youngest vector loads (the next-but-one weight
@@ -1013,26 +1014,58 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 		for (int mt = 0; mt < NMT; mt++) {
 #pragma unroll
 			for (int half = 0; half < 2; half++) {
+				if constexpr (DOWN) {
 #pragma unroll
-				for (int ii = 0; ii < 8; ii++) {
-					const int i = 8 * half + ii;
-					const int r = 8 * (ii >> 2) + 4 * h + (ii & 3); // row within the half
-					if (DOWN) {
+					for (int ii = 0; ii < 8; ii++) {
+						const int i = 8 * half + ii;
+						const int r = 8 * (ii >> 2) + 4 * h + (ii & 3); // row within the half
 						tl[r * LS + c0] = acc[mt][0][i] * a.y_scale;
 						tl[r * LS + 32 + c0] = acc[mt][1][i] * a.y_scale;
-					} else {
-						constexpr float unscale = 1.0f / (1 << F16_SHIFT);
-						const float hs =
-							tie_swiglu(acc[mt][0][i] * unscale, acc[mt][1][i] * unscale, silu) * a.h_scale;
+					}
+				} else {
+					// TIE's table SwiGLU (tie_swiglu, the same operations) on
+					// the half's 8 values, all table reads issued together
+					constexpr float unscale = 1.0f / (1 << F16_SHIFT);
+					float pos[8], up[8], y1[8], y2[8];
+					int idx[8];
+#pragma unroll
+					for (int ii = 0; ii < 8; ii++) {
+						const int i = 8 * half + ii;
+						const float g = acc[mt][0][i] * unscale;
+						up[ii] = acc[mt][1][i] * unscale;
+						pos[ii] = ((g + 10.0f) * 8191.0f) * 0.05f;
+						int id = (pos[ii] >= -2147483648.0f && pos[ii] < 2147483648.0f)
+								 ? (int)__builtin_rintf(pos[ii])
+								 : (int)0x80000000;
+						id = id < 0 ? 0 : id;
+						idx[ii] = id > SILU_N - 2 ? SILU_N - 2 : id;
+					}
+#pragma unroll
+					for (int ii = 0; ii < 8; ii++) {
+						y1[ii] = silu[idx[ii]];
+						y2[ii] = silu[idx[ii] + 1];
+					}
+					uint32_t bad = 0;
+#pragma unroll
+					for (int ii = 0; ii < 8; ii++) {
+						const int r = 8 * (ii >> 2) + 4 * h + (ii & 3); // row within the half
+						const float frac = pos[ii] - (float)idx[ii];
+						const float sl = __builtin_fmaf(frac, y2[ii] - y1[ii], y1[ii]);
+						const float hs = (sl * up[ii]) * a.h_scale;
 						tl[r * LS + pc0] = hs;
-						// a value outside the f16 range sends the pair's token
-						// to the exact recomputation
 						const int mrow = 32 * mt + 16 * half + r;
-						if (!(__builtin_fabsf(hs) < 65504.0f) && mrow < nrows) {
-							const int tok = spair[mrow] / a.k;
-							if (a.tok_flag[tok] == 0) // listed already: no atomic
-								flag_token(a.tok_flag, a.fix_list, a.fix_count, tok);
-						}
+						bad |= (!(__builtin_fabsf(hs) < 65504.0f) && mrow < nrows) ? 1u << ii : 0u;
+					}
+					// a value outside the f16 range sends the pair's token to
+					// the exact recomputation (rare: off the common path)
+					if (bad) {
+						for (int ii = 0; ii < 8; ii++)
+							if (bad & (1u << ii)) {
+								const int r = 8 * (ii >> 2) + 4 * h + (ii & 3);
+								const int tok = spair[32 * mt + 16 * half + r] / a.k;
+								if (a.tok_flag[tok] == 0) // listed already: no atomic
+									flag_token(a.tok_flag, a.fix_list, a.fix_count, tok);
+							}
 					}
 				}
 				__builtin_amdgcn_s_waitcnt(0xc07f); // lgkmcnt(0): the tile's LDS writes done
@@ -1148,9 +1181,12 @@ mfma_experts_kernel(MfmaArgs a)
 	// Every workgroup derives its tile from the counts: exclusive scans of
 	// the tile and pair counts over the experts (thread i owns experts
 	// 4i .. 4i + 3), in the idle stage buffers.
+#ifdef TIE_MFMA_TRACE
+	const unsigned long long t_k0 = __builtin_readcyclecounter();
+#endif
 	int e, li, off, slab;
 	{
-		int *sc = reinterpret_cast<int *>(As); // [MF_THREADS / 64] scan | e, li, off
+		int *sc = reinterpret_cast<int *>(As); // [2 MF_THREADS / 64] scan | e, li, off
 		const int t = threadIdx.x;
 		int c4[4], n4[4], csum = 0, nsum = 0;
 #pragma unroll
@@ -1161,9 +1197,12 @@ mfma_experts_kernel(MfmaArgs a)
 			csum += c4[i];
 			nsum += n4[i];
 		}
-		int ntiles, ctot;
-		int nbase = block_exclusive_scan<MF_THREADS>(nsum, sc, ntiles);
-		int cbase = block_exclusive_scan<MF_THREADS>(csum, sc, ctot);
+		// one scan of both sums (tiles in the high word, pairs in the low)
+		long long tot;
+		const long long b2 = block_exclusive_scan64<MF_THREADS>(((long long)nsum << 32) | (long long)csum,
+									 reinterpret_cast<long long *>(sc), tot);
+		const int ntiles = (int)(tot >> 32);
+		int nbase = (int)(b2 >> 32), cbase = (int)(b2 & 0xffffffffll);
 		// this workgroup's item (XCD-aware order: consecutive workgroup ids
 		// go round-robin over the 8 XCDs, each with its own L2; the id is
 		// remapped so that each XCD takes a contiguous run of (tile, column
@@ -1181,17 +1220,17 @@ mfma_experts_kernel(MfmaArgs a)
 #pragma unroll
 		for (int i = 0; i < 4; i++) {
 			if (tile >= nbase && tile < nbase + n4[i]) {
-				sc[MF_THREADS / 64] = 4 * t + i;
-				sc[MF_THREADS / 64 + 1] = tile - nbase;
-				sc[MF_THREADS / 64 + 2] = cbase;
+				sc[2 * MF_THREADS / 64] = 4 * t + i;
+				sc[2 * MF_THREADS / 64 + 1] = tile - nbase;
+				sc[2 * MF_THREADS / 64 + 2] = cbase;
 			}
 			nbase += n4[i];
 			cbase += c4[i];
 		}
 		__syncthreads();
-		e = sc[MF_THREADS / 64];
-		li = sc[MF_THREADS / 64 + 1];
-		off = sc[MF_THREADS / 64 + 2];
+		e = sc[2 * MF_THREADS / 64];
+		li = sc[2 * MF_THREADS / 64 + 1];
+		off = sc[2 * MF_THREADS / 64 + 2];
 		__syncthreads(); // the stage buffers are free again
 	}
 	const int cnt = a.cnt[e];
@@ -1204,6 +1243,10 @@ mfma_experts_kernel(MfmaArgs a)
 	if (threadIdx.x < nrows)
 		spair[threadIdx.x] = a.bucket[(size_t)e * a.bstride + m0 + threadIdx.x];
 	__syncthreads();
+#ifdef TIE_MFMA_TRACE
+	if (threadIdx.x == 0)
+		atomicAdd(&g_mfma_trace[DOWN][4], __builtin_readcyclecounter() - t_k0);
+#endif
 #ifdef TIE_MFMA_FIXED_NMT
 	// one tile height for every tile (one copy of run_tile's code)
 	run_tile<TYPE, DOWN, MT_TILES, MTR>(a, As, roff, spair, e, pbase, nrows, slab);
@@ -1561,10 +1604,10 @@ hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, con
 #ifdef TIE_MFMA_TRACE
 extern "C" int tie_hip_debug_mfma_trace(unsigned long long *host, int reset)
 {
-	if (hipMemcpyFromSymbol(host, HIP_SYMBOL(tie::g_mfma_trace), sizeof(unsigned long long) * 8) != hipSuccess)
+	if (hipMemcpyFromSymbol(host, HIP_SYMBOL(tie::g_mfma_trace), sizeof(unsigned long long) * 16) != hipSuccess)
 		return -1;
 	if (reset) {
-		static const unsigned long long z[8] = {0};
+		static const unsigned long long z[16] = {0};
 		if (hipMemcpyToSymbol(HIP_SYMBOL(tie::g_mfma_trace), z, sizeof z) != hipSuccess)
 			return -1;
 	}

@@ -515,6 +515,36 @@ __device__ __forceinline__ void topk_softmax_group8(const float *lg, int E, int 
 
 // Exclusive prefix sum over a workgroup of NT threads (one value each);
 // `total` receives the sum.  wsum: LDS scratch of NT/64 ints.
+// The same over 64-bit values (two counts packed in one word: neither
+// half carries into the other while both stay non-negative and below 2^31
+// in total).
+template <int NT>
+__device__ __forceinline__ long long block_exclusive_scan64(long long v, long long *wsum, long long &total)
+{
+	const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+	constexpr int NW = NT / 64;
+	long long x = v;
+#pragma unroll
+	for (int off = 1; off < 64; off <<= 1) {
+		const long long y = __shfl_up(x, off);
+		if (lane >= off)
+			x += y;
+	}
+	if (lane == 63)
+		wsum[wave] = x;
+	__syncthreads();
+	long long prefix = 0;
+#pragma unroll
+	for (int i = 0; i < NW; i++)
+		prefix += i < wave ? wsum[i] : 0;
+	total = 0;
+#pragma unroll
+	for (int i = 0; i < NW; i++)
+		total += wsum[i];
+	__syncthreads();
+	return prefix + x - v;
+}
+
 template <int NT> __device__ __forceinline__ int block_exclusive_scan(int v, int *wsum, int &total)
 {
 	const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
