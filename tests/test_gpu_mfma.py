@@ -346,3 +346,32 @@ def test_lfm2_prefill_routing_exact():
     check_routing(idx, w, ri, rw)
     e, _ = report("lfm2_T300", out, ro)
     assert e <= ORACLE_RL2
+
+
+def test_out_of_range_residual_in_place():
+    """The FFN half (RMSNorm, block, residual) on the MFMA path with every
+    token's normed x beyond the f16 range (one huge ffn_norm weight): every
+    row is recomputed exactly, also when the residual add updates the
+    hidden state in place (the recomputation reads the hidden state as it
+    was, so the combine must leave those rows alone): bit-exact against the
+    oracle, in place and out of place."""
+    import torch
+    layer = synth_layer(95, 512, 512, 16, synth.Q4_K, synth.Q6_K, None)
+    T, k = 100, 4
+    hidden = synth.make_input(95, T, 512)
+    norm = synth.make_norm_weight(95, 512)
+    norm[7] = np.float32(1e6)
+    rh, ri, rw = bind.qwen3_ffn(layer, hidden, k, norm, 1e-6)
+    L = tie_amd.Layer.from_synth(layer)
+    nd = torch.from_numpy(norm).cuda()
+    for in_place in (False, True):
+        hd = torch.from_numpy(hidden).cuda()
+        out = hd if in_place else torch.empty_like(hd)
+        idx = torch.empty((T, k), dtype=torch.int32, device="cuda")
+        w = torch.empty((T, k), dtype=torch.float32, device="cuda")
+        L.forward_residual(hd, nd, 1e-6, T, k, None if in_place else out, idx, w, flags=tie_amd.PATH_MFMA)
+        torch.cuda.synchronize()
+        print("in place %s" % in_place, flush=True)
+        check_routing(idx.cpu().numpy(), w.cpu().numpy(), ri, rw)
+        np.testing.assert_array_equal(bits(out.cpu().numpy()), bits(rh), err_msg="in place %s" % in_place)
+    L.close()

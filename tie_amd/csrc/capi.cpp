@@ -470,8 +470,10 @@ static int forward(tie_hip_layer *layer, const float *x, int T, int k, float *ou
 		prof_end(s);
 		HIP_TRY(launch_mfma_experts(L, x, T, k, g.silu, ws, s));
 		prof_begin("combine", s);
-		HIP_TRY(launch_combine(T, L.d, k, ws.topk_w, ws.topk_idx, ws.y, out, s, res,
-				       L.down.type != TIE_GGML_BF16));
+		// tokens listed for the exact recomputation are skipped (their rows
+		// come from it, computed from res as it was: res may be out)
+		HIP_TRY(launch_combine(T, L.d, k, ws.topk_w, ws.topk_idx, ws.y, out, s, res, L.down.type != TIE_GGML_BF16,
+				       mfma_f16_operands(L) ? ws.tok_flag : nullptr));
 		prof_end(s);
 		if (mfma_f16_operands(L)) {
 			// tokens whose activations left the f16 range (listed by the

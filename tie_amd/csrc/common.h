@@ -174,7 +174,8 @@ int dense_groups(int T);
 // res (optional): out = res + combine (the residual add after the block)
 // y16: y holds bf16 values (the MFMA path's down output with quantised weights)
 hipError_t launch_combine(int T, int d, int k, const float *topk_w, const int32_t *topk_idx, const float *y,
-			  float *out, hipStream_t s, const float *res = nullptr, bool y16 = false);
+			  float *out, hipStream_t s, const float *res = nullptr, bool y16 = false,
+			  const int32_t *skip = nullptr);
 // TIE's RMSNorm of each row of x into out; tab/nbits: the host RSQRTSS table
 hipError_t launch_rmsnorm(const float *x, const float *w, float eps, int T, int d, float *out, const uint32_t *tab,
 			  int nbits, hipStream_t s);

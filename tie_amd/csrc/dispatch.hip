@@ -154,12 +154,17 @@ hipError_t launch_route_group(const Layer &L, int T, int k, const float *logits,
 // with res: out[t][c] = res[t][c] + acc, the residual add that follows the
 // block (dispatch_apply_residual, model_qwen3.c:491, apply_residual_f32_f32_avx2
 // math_avx2.c:731-751).  res may be out (the hidden state updated in place).
+// Tokens with skip[t] != 0 (skip optional) are left alone: the exact
+// recomputation writes their rows afterwards, from res as it was.
 template <bool Y16>
 __global__ __launch_bounds__(256) void combine_kernel(int T, int d, int k, const float *__restrict__ topk_w,
 						      const int32_t *__restrict__ topk_idx,
-						      const float *__restrict__ y, const float *res, float *out)
+						      const float *__restrict__ y, const float *res, float *out,
+						      const int32_t *__restrict__ skip)
 {
 	const int t = blockIdx.y;
+	if (skip && skip[t])
+		return;
 	const int c4 = blockIdx.x * blockDim.x + threadIdx.x; // float4 column
 	if (c4 * 4 >= d)
 		return;
@@ -193,13 +198,13 @@ __global__ __launch_bounds__(256) void combine_kernel(int T, int d, int k, const
 }
 
 hipError_t launch_combine(int T, int d, int k, const float *topk_w, const int32_t *topk_idx, const float *y,
-			  float *out, hipStream_t s, const float *res, bool y16)
+			  float *out, hipStream_t s, const float *res, bool y16, const int32_t *skip)
 {
 	if (T == 0)
 		return hipSuccess;
 	const int n4 = d / 4;
 	hipLaunchKernelGGL(y16 ? combine_kernel<true> : combine_kernel<false>, dim3((n4 + 255) / 256, T), dim3(256), 0, s,
-			   T, d, k, topk_w, topk_idx, y, res, out);
+			   T, d, k, topk_w, topk_idx, y, res, out, skip);
 	return hipGetLastError();
 }
 
