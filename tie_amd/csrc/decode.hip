@@ -949,7 +949,7 @@ static void one_shape(const Layer &L, int k, int &rpr, int &rg, int &rd, int &th
 	// gate/up: rg rows, 2 nb tasks per row; down: rd rows, k nb tasks per
 	// row (powers of two); router: rpr rows
 	rg = gu_rows(nbd);
-	rd = pick_rows(k * nbf, 16);
+	rd = pick_rows(k * nbf, 8);
 	threads = round64(std::max(std::max(2 * nbd * rg, k * nbf * rd), L.E));
 	rpr = L.d <= 2048 ? 2 : 1;
 	const size_t lds_r = sizeof(float) * (size_t)(1 + rpr) * lane_major_floats(L.d);
