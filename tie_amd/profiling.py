@@ -138,9 +138,10 @@ _DEFAULT_JSON = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__f
 def traffic_markdown(path):
     with open(path) as f:
         t = json.load(f)
-    out = ["Kernels are grouped as the library's per-kernel timer groups them: mfma_gate_up includes the x conversion "
-           "(to_f16 / to_bf16 / to_split), router includes the separate selection kernel (router_topk) where one "
-           "runs, dense includes its grouping kernel.",
+    out = ["Kernels are grouped as the library's per-kernel timer groups them: on the matrix-core path router is the "
+           "logits kernel plus route_bucket (selection, per-expert selection bytes, and x converted to the gate/up A "
+           "operand), dispatch is bucket_plan (per-expert pair lists); decode_one is the whole one-token block; "
+           "dense includes its grouping kernel.",
            "",
            "| kernel @ config | fetch MB | write MB | total MB per forward | dispatches | forwards |",
            "|---|---|---|---|---|---|"]
