@@ -469,18 +469,23 @@ static int forward(tie_hip_layer *layer, const float *x, int T, int k, float *ou
 		HIP_TRY(launch_bucket_plan(L, T, k, ws, s));
 		prof_end(s);
 		HIP_TRY(launch_mfma_experts(L, x, T, k, g.silu, ws, s));
-		prof_begin("combine", s);
-		// tokens listed for the exact recomputation are skipped (their rows
-		// come from it, computed from res as it was: res may be out)
-		HIP_TRY(launch_combine(T, L.d, k, ws.topk_w, ws.topk_idx, ws.y, out, s, res, L.down.type != TIE_GGML_BF16,
-				       mfma_f16_operands(L) ? ws.tok_flag : nullptr));
-		prof_end(s);
-		if (mfma_f16_operands(L)) {
-			// tokens whose activations left the f16 range (listed by the
-			// kernels above; usually none): recomputed exactly, their rows
-			// of out overwritten
-			HIP_TRY(launch_recompute(L, x, k, g.silu, ws.topk_idx, ws.topk_w, out, res, ws.fix_list, ws.fix_count, T,
-						 s));
+		if (mfma_f16_operands(L) && combine_fix_preferred(L)) {
+			// the combine of every token, except those whose activations
+			// left the f16 range (listed by the kernels above; usually
+			// none), which are recomputed exactly in the same launch, from
+			// res as it was (res may be out)
+			HIP_TRY(launch_combine_fix(L, x, k, g.silu, ws.topk_idx, ws.topk_w, reinterpret_cast<const uint16_t *>(ws.y),
+						   out, res, ws.tok_flag, ws.fix_list, ws.fix_count, T, s));
+		} else {
+			// the same in two launches (the recomputation's LDS would cost
+			// the combine occupancy); the combine skips the listed tokens
+			prof_begin("combine", s);
+			HIP_TRY(launch_combine(T, L.d, k, ws.topk_w, ws.topk_idx, ws.y, out, s, res, L.down.type != TIE_GGML_BF16,
+					       mfma_f16_operands(L) ? ws.tok_flag : nullptr));
+			prof_end(s);
+			if (mfma_f16_operands(L))
+				HIP_TRY(launch_recompute(L, x, k, g.silu, ws.topk_idx, ws.topk_w, out, res, ws.fix_list,
+							 ws.fix_count, T, s));
 		}
 	} else if (T == 1 && !preset && !capturing(s) && decode_one_supported(L, k)) {
 		// one token, one launch (eager calls on a workspace of their own:

@@ -150,6 +150,13 @@ bool recompute_supported(const Layer &L, int k);
 hipError_t launch_recompute(const Layer &L, const float *x, int k, const float *silu, const int32_t *topk_idx,
 			    const float *topk_w, float *out, const float *res, const int32_t *list,
 			    const int32_t *count, int T, hipStream_t s);
+// The matrix-core path's combine (bf16 y; tokens with skip[t] set left
+// alone) and the exact recomputation of the listed tokens in one launch,
+// when combine_fix_preferred
+bool combine_fix_preferred(const Layer &L);
+hipError_t launch_combine_fix(const Layer &L, const float *x, int k, const float *silu, const int32_t *topk_idx,
+			      const float *topk_w, const uint16_t *y, float *out, const float *res,
+			      const int32_t *skip, const int32_t *list, const int32_t *count, int T, hipStream_t s);
 
 hipError_t launch_decode(const Layer &L, const float *x, int k, const float *silu, const float *logits,
 			 int32_t *topk_idx, float *topk_w, float *h, float *out, const float *res, const int32_t *list,

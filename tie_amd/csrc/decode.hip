@@ -710,25 +710,29 @@ template <int TG, int TU, int TD> __global__ __launch_bounds__(DEC_MAX_THREADS, 
 // the same operations as decode_gu_kernel / decode_down_kernel, one kernel
 // instead of two, so the (usually empty) launch costs once.
 template <int TG, int TU, int TD>
-__global__ __launch_bounds__(DEC_MAX_THREADS) void recompute_kernel(DecodeArgs a)
+__device__ __forceinline__ void recompute_tokens(const DecodeArgs &a, float *dl, int first, int stride)
 {
-	extern __shared__ __attribute__((aligned(16))) float dl[];
 	const int nbd = a.d / QK, nbf = a.F / QK, k = a.k;
 	float *xs = dl;                          // [nbd][XSEG]
-	float *hs = dl + (size_t)nbd * XSEG;     // [k][nbf][XSEG]
+	float *hs = dl + (size_t)nbd * XSEG;     // [nbf][XSEG]: h of one slot
+	float *acc = hs + (size_t)nbf * XSEG;    // [d]: the combine of the slots so far
 	const int n = list_count(a);
-	for (int li = blockIdx.x; li < n; li += gridDim.x) {
+	for (int li = first; li < n; li += stride) {
 		const int t = list_token(a, li);
 		copy_in<4>(reinterpret_cast<const float4 *>(a.x + (size_t)t * a.d), a.d / 4, [&](int q, float4 v) {
 			const int f = 4 * q;
 			*reinterpret_cast<float4 *>(xs + (f / QK) * XSEG + (f % QK)) = v;
 		});
+		for (int r = threadIdx.x; r < a.d; r += blockDim.x)
+			acc[r] = 0.0f;
 		__syncthreads();
-		for (int u = threadIdx.x; u < k * a.F; u += blockDim.x) {
-			const int j = u / a.F, r = u - j * a.F;
+		// one slot at a time: h_j in LDS, then y_j and acc = fma(g_j, y_j,
+		// acc) per row (slot order, as the combine)
+		for (int j = 0; j < k; j++) {
 			const int e = a.topk_idx[(size_t)t * k + j];
-			float h = 0.0f;
-			if (e >= 0) {
+			if (e < 0)
+				continue;
+			for (int r = threadIdx.x; r < a.F; r += blockDim.x) {
 				float g = 0.0f, up = 0.0f;
 				for (int b = 0; b < nbd; b++) {
 					const uint8_t *bg = panel_slot(a.w[0], a.expert_bytes[0], e, r, b, nbd, panel_bytes(TG));
@@ -738,29 +742,88 @@ __global__ __launch_bounds__(DEC_MAX_THREADS) void recompute_kernel(DecodeArgs a
 					const uint8_t *bu = panel_slot(a.w[1], a.expert_bytes[1], e, r, b, nbd, panel_bytes(TU));
 					up = up + row_block_dot<TU>(bu, q6k_d_of(bu, r), (dfloat *)(xs + b * XSEG));
 				}
-				h = tie_swiglu(g, up, a.silu);
+				hs[(r / QK) * XSEG + r % QK] = tie_swiglu(g, up, a.silu);
 			}
-			hs[(j * nbf + r / QK) * XSEG + r % QK] = h;
-		}
-		__syncthreads();
-		for (int r = threadIdx.x; r < a.d; r += blockDim.x) {
-			float acc = 0.0f;
-			for (int j = 0; j < k; j++) {
-				const int e = a.topk_idx[(size_t)t * k + j];
-				if (e < 0)
-					continue;
+			__syncthreads();
+			const float gw = a.topk_w[(size_t)t * k + j];
+			for (int r = threadIdx.x; r < a.d; r += blockDim.x) {
 				float y = 0.0f;
 				for (int b = 0; b < nbf; b++) {
 					const uint8_t *bd = panel_slot(a.w[2], a.expert_bytes[2], e, r, b, nbf, panel_bytes(TD));
-					y = y + row_block_dot<TD>(bd, q6k_d_of(bd, r), (dfloat *)(hs + (size_t)(j * nbf + b) * XSEG));
+					y = y + row_block_dot<TD>(bd, q6k_d_of(bd, r), (dfloat *)(hs + (size_t)b * XSEG));
 				}
-				acc = __builtin_fmaf(a.topk_w[(size_t)t * k + j], y, acc);
+				acc[r] = __builtin_fmaf(gw, y, acc[r]);
 			}
+			__syncthreads();
+		}
+		for (int r = threadIdx.x; r < a.d; r += blockDim.x) {
 			const size_t o = (size_t)t * a.d + r;
-			a.out[o] = a.res ? a.res[o] + acc : acc;
+			a.out[o] = a.res ? a.res[o] + acc[r] : acc[r];
 		}
 		__syncthreads();
 	}
+}
+
+// LDS of recompute_tokens: x, one slot's h, the combine accumulators
+static size_t recompute_lds(const Layer &L)
+{
+	return sizeof(float) * (((size_t)(L.d / QK) + (size_t)(L.F / QK)) * XSEG + (size_t)L.d);
+}
+
+template <int TG, int TU, int TD>
+__global__ __launch_bounds__(DEC_MAX_THREADS) void recompute_kernel(DecodeArgs a)
+{
+	extern __shared__ __attribute__((aligned(16))) float dl[];
+	recompute_tokens<TG, TU, TD>(a, dl, blockIdx.x, gridDim.x);
+}
+
+// The matrix-core path's last launch: the combine of every token not listed
+// for recomputation (combine_kernel's operations: out[t][c] = [res +] sum_j
+// fma(g_j, y_j[c], .) in slot order, y bf16), and, in workgroups of their
+// own, the exact recomputation of the listed ones (usually none) -- one
+// launch instead of two.  Workgroups [0, ncomb): token b / cpt, 1024
+// columns each; [ncomb, ncomb + nfix): recomputation.
+struct CombineFixArgs {
+	int ncomb, cpt, nfix;
+	const float *topk_w;
+	const int32_t *topk_idx;
+	const uint16_t *y;
+	const int32_t *skip;
+};
+constexpr int CF_THREADS = 256;
+template <int TG, int TU, int TD>
+__global__ __launch_bounds__(CF_THREADS) void combine_fix_kernel(DecodeArgs a, CombineFixArgs c)
+{
+	extern __shared__ __attribute__((aligned(16))) float dl[];
+	const int b = blockIdx.x;
+	if (b >= c.ncomb) {
+		recompute_tokens<TG, TU, TD>(a, dl, b - c.ncomb, c.nfix);
+		return;
+	}
+	const int t = b / c.cpt;
+	const int c4 = (b - t * c.cpt) * CF_THREADS + threadIdx.x; // float4 column
+	if (c.skip[t] || c4 * 4 >= a.d)
+		return;
+	const int k = a.k;
+	float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+	for (int j = 0; j < k; j++) {
+		if (c.topk_idx[t * k + j] < 0)
+			continue;
+		const float g = c.topk_w[t * k + j];
+		const uint2 w = reinterpret_cast<const uint2 *>(c.y + ((size_t)t * k + j) * a.d)[c4];
+		acc.x = __builtin_fmaf(g, __builtin_bit_cast(float, w.x << 16), acc.x);
+		acc.y = __builtin_fmaf(g, __builtin_bit_cast(float, w.x & 0xffff0000u), acc.y);
+		acc.z = __builtin_fmaf(g, __builtin_bit_cast(float, w.y << 16), acc.z);
+		acc.w = __builtin_fmaf(g, __builtin_bit_cast(float, w.y & 0xffff0000u), acc.w);
+	}
+	if (a.res) {
+		const float4 h = reinterpret_cast<const float4 *>(a.res + (size_t)t * a.d)[c4];
+		acc.x = h.x + acc.x;
+		acc.y = h.y + acc.y;
+		acc.z = h.z + acc.z;
+		acc.w = h.w + acc.w;
+	}
+	reinterpret_cast<float4 *>(a.out + (size_t)t * a.d)[c4] = acc;
 }
 
 // ---------------------------------------------------------------- launchers
@@ -815,8 +878,7 @@ static hipError_t dec_launch(K kern, dim3 grid, dim3 block, size_t lds, hipStrea
 
 bool recompute_supported(const Layer &L, int k)
 {
-	const size_t lds = sizeof(float) * ((size_t)(L.d / QK) + (size_t)k * (L.F / QK)) * XSEG;
-	return decode_supported(L, k) && lds <= DEC_MAX_LDS;
+	return decode_supported(L, k) && recompute_lds(L) <= DEC_MAX_LDS;
 }
 
 // The listed tokens (*count of them, their selection in topk_idx / topk_w)
@@ -845,7 +907,7 @@ hipError_t launch_recompute(const Layer &L, const float *x, int k, const float *
 	a.silu = silu;
 	a.list = list;
 	a.count = count;
-	const size_t lds = sizeof(float) * ((size_t)(L.d / QK) + (size_t)k * (L.F / QK)) * XSEG;
+	const size_t lds = recompute_lds(L);
 	const dim3 grid(T < 128 ? (T > 0 ? T : 1) : 128);
 	const int tg = L.gate.type, tu = L.up.type, td = L.down.type;
 	hipError_t err;
@@ -862,6 +924,71 @@ hipError_t launch_recompute(const Layer &L, const float *x, int k, const float *
 	else
 		err = REC(TIE_GGML_Q6_K, TIE_GGML_Q6_K);
 #undef REC
+	prof_end(s);
+	return err;
+}
+
+// One launch for the combine and the recomputation when the latter's LDS
+// leaves the combine workgroups their occupancy (measured: 30B shapes gain
+// 6 us at T = 128 and 1.4 us at T = 2048; 235B T = 1024, 39 KiB, loses 2 us)
+bool combine_fix_preferred(const Layer &L)
+{
+	return recompute_lds(L) <= 24 * 1024;
+}
+
+// The combine of the matrix-core path's bf16 y (tokens listed in skip left
+// alone) and the exact recomputation of the listed tokens, in one launch.
+hipError_t launch_combine_fix(const Layer &L, const float *x, int k, const float *silu, const int32_t *topk_idx,
+			      const float *topk_w, const uint16_t *y, float *out, const float *res,
+			      const int32_t *skip, const int32_t *list, const int32_t *count, int T, hipStream_t s)
+{
+	if (T == 0)
+		return hipSuccess;
+	DecodeArgs a;
+	memset(&a, 0, sizeof a);
+	a.w[0] = L.gate.data;
+	a.w[1] = L.up.data;
+	a.w[2] = L.down.data;
+	a.expert_bytes[0] = L.gate.expert_bytes;
+	a.expert_bytes[1] = L.up.expert_bytes;
+	a.expert_bytes[2] = L.down.expert_bytes;
+	a.d = L.d;
+	a.F = L.F;
+	a.E = L.E;
+	a.k = k;
+	a.x = x;
+	a.topk_idx = const_cast<int32_t *>(topk_idx);
+	a.topk_w = const_cast<float *>(topk_w);
+	a.out = out;
+	a.res = res;
+	a.silu = silu;
+	a.list = list;
+	a.count = count;
+	CombineFixArgs c;
+	c.cpt = (L.d / 4 + CF_THREADS - 1) / CF_THREADS;
+	c.ncomb = T * c.cpt;
+	c.nfix = T < 64 ? T : 64;
+	c.topk_w = topk_w;
+	c.topk_idx = topk_idx;
+	c.y = y;
+	c.skip = skip;
+	const size_t lds = recompute_lds(L);
+	const dim3 grid(c.ncomb + c.nfix);
+	const int tg = L.gate.type, tu = L.up.type, td = L.down.type;
+	hipError_t err;
+	prof_begin("combine", s);
+#define CF(A, B)                                                                                                     \
+	(td == TIE_GGML_Q4_K ? dec_launch(combine_fix_kernel<A, B, TIE_GGML_Q4_K>, grid, dim3(CF_THREADS), lds, s, a, c) \
+			     : dec_launch(combine_fix_kernel<A, B, TIE_GGML_Q6_K>, grid, dim3(CF_THREADS), lds, s, a, c))
+	if (tg == TIE_GGML_Q4_K && tu == TIE_GGML_Q4_K)
+		err = CF(TIE_GGML_Q4_K, TIE_GGML_Q4_K);
+	else if (tg == TIE_GGML_Q4_K)
+		err = CF(TIE_GGML_Q4_K, TIE_GGML_Q6_K);
+	else if (tu == TIE_GGML_Q4_K)
+		err = CF(TIE_GGML_Q6_K, TIE_GGML_Q4_K);
+	else
+		err = CF(TIE_GGML_Q6_K, TIE_GGML_Q6_K);
+#undef CF
 	prof_end(s);
 	return err;
 }

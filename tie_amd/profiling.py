@@ -42,6 +42,7 @@ _NAMES = (
     ("tie::decode_down_kernel", "decode_down"),
     ("tie::decode_one_kernel", "decode_one"),
     ("tie::recompute_kernel", "recompute"),
+    ("tie::combine_fix_kernel", "combine"),
     ("tie::dense_rows_kernel", "dense"),
     ("tie::dense_groups_kernel", "dense"),
 )
