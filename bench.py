@@ -103,7 +103,7 @@ class Workload:
         torch.cuda.empty_cache()
 
 
-def run_dense(torch, tie_amd, cfg, steps, warmup, n_copies):
+def run_dense(torch, tie_amd, cfg, steps, warmup, n_copies, flags):
     """dispatch_mat_mat through tie_hip_mat_mat: T rows of x times one
     [rows][in] weight matrix, cycling `n_copies` matrices so the MALL does
     not hold the weights.  Same result fields as run_config."""
@@ -124,7 +124,7 @@ def run_dense(torch, tie_amd, cfg, steps, warmup, n_copies):
     out = torch.empty(T, rows, device="cuda")
 
     def step(s):
-        mats[s % n_copies].mat_mat(X[s % n_copies], T, out)
+        mats[s % n_copies].mat_mat(X[s % n_copies], T, out, flags=flags)
 
     for s in range(warmup):
         step(s)
@@ -142,9 +142,10 @@ def run_dense(torch, tie_amd, cfg, steps, warmup, n_copies):
     wbytes = rows * synth.row_bytes(wtype, in_dim)
     nbytes = wbytes + T * in_dim * 4 + T * rows * 4
     flops = 2.0 * T * rows * in_dim
-    tot, n = prof.get("dense", (0.0, 0))
+    key = "dense_mfma" if "dense_mfma" in prof else "dense"
+    tot, n = prof.get(key, (0.0, 0))
     avg_ms = tot / n if n else ms
-    kernels = {"dense": {"avg_us": round(1e3 * avg_ms, 3), "launches": n, "alg_bytes": nbytes,
+    kernels = {key: {"avg_us": round(1e3 * avg_ms, 3), "launches": n, "alg_bytes": nbytes,
                          "GBps": round(nbytes / (avg_ms * 1e-3) / 1e9, 1), "alg_flops": flops,
                          "TFLOPs": round(flops / (avg_ms * 1e-3) / 1e12, 2)}}
     for mt in mats:
@@ -305,7 +306,7 @@ def roofline(m, config):
     # bound: MFMA when the kernel runs on the matrix cores and its algorithmic
     # intensity is above the MI355X ridge point (2.5 PFLOP/s / 8 TB/s)
     ridge = BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
-    mfma = name.startswith("mfma") and kd.get("alg_flops") and kd["alg_flops"] / kd["alg_bytes"] > ridge
+    mfma = "mfma" in name and kd.get("alg_flops") and kd["alg_flops"] / kd["alg_bytes"] > ridge
     if mfma:
         return {"kernel": name, "bound": "mfma", "achieved": kd["TFLOPs"], "peak": BF16_PEAK_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(kd["TFLOPs"] / BF16_PEAK_TFLOPS, 4), "traffic": traffic,
@@ -452,7 +453,7 @@ def main():
             wbytes = cfg["rows"] * synth.row_bytes(cfg["wtype"], cfg["in"])
             ncp = max(2, min(64, int(1.2e9 // wbytes)))
             log("timing dense %s: %d x %d, T=%d, %d matrices" % (name, cfg["rows"], cfg["in"], cfg["T"], ncp))
-            results[name] = run_dense(torch, tie_amd, cfg, steps, max(2, args.warmup // 4), ncp)
+            results[name] = run_dense(torch, tie_amd, cfg, steps, max(2, args.warmup // 4), ncp, flags)
             log(json.dumps({name: results[name]}))
             continue
         key = (cfg["d"], cfg["F"], cfg["E"], cfg["gu_type"], cfg["down_type"], cfg.get("zipf"), cfg.get("routing", 0),

@@ -198,9 +198,14 @@ void tie_hip_matrix_destroy(tie_hip_matrix *m);
 
 /* dispatch_mat_mat (math_dispatch.c:304-359) on device pointers:
  * out_dev[t][r] = W[r] . x_dev[t] for t < T, x [T][in_dim] F32, out
- * [T][rows] F32, with TIE's row kernels (mat_vec_row_f32_{f32,q4k,q6k,
- * bf16}_f32_avx2) bit for bit; flags must not ask for TIE_HIP_PATH_MFMA.
- * Enqueued on `stream`.  The attention projections, the dense FFN and the LM
+ * [T][rows] F32.  TIE_HIP_PATH_EXACT, and TIE_HIP_PATH_AUTO for T up to the
+ * exact threshold (64), use TIE's row kernels (mat_vec_row_f32_{f32,q4k,q6k,
+ * bf16}_f32_avx2) bit for bit.  TIE_HIP_PATH_MFMA, and AUTO above the
+ * threshold where supported (Q4_K or Q6_K, rows a multiple of 256), run the
+ * f16 matrix cores with fp32 accumulation (relative L2 error about 3e-4 of
+ * TIE's result); rows whose input does not fit the f16 range are recomputed
+ * with the exact kernel.  TIE_HIP_PATH_MFMA on an unsupported matrix is an
+ * error.  Enqueued on `stream`.  The attention projections, the dense FFN and the LM
  * head of transformer_layer_qwen3 / main.c use it. */
 int tie_hip_mat_mat(tie_hip_matrix *m, const float *x_dev, int T, float *out_dev, int flags, void *stream);
 

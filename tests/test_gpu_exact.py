@@ -119,7 +119,7 @@ def test_dense_mat_mat(wtype):
         print("dense case type=%d T=%d" % (wtype, T), flush=True)
         xd = torch.from_numpy(x).cuda()
         out = torch.empty((T, rows), device="cuda")
-        M.mat_mat(xd, T, out)
+        M.mat_mat(xd, T, out, flags=tie_amd.PATH_EXACT)
         torch.cuda.synchronize()
         assert_same(out.cpu().numpy(), bind.mat_mat(x, w, wtype, rows), "dense out")
     M.close()

@@ -375,3 +375,56 @@ def test_out_of_range_residual_in_place():
         check_routing(idx.cpu().numpy(), w.cpu().numpy(), ri, rw)
         np.testing.assert_array_equal(bits(out.cpu().numpy()), bits(rh), err_msg="in place %s" % in_place)
     L.close()
+
+
+@pytest.mark.parametrize("wtype", QUANT)
+def test_dense_mat_mat_mfma(wtype):
+    """tie_hip_mat_mat on the matrix cores (TIE_HIP_PATH_MFMA, and the
+    default above the exact threshold): against the float64 model of its
+    operands (x in f16, the f16 weights of q4k_f16 / q6k_f16) and against
+    TIE's row kernels (the fp32 oracle); a token whose x leaves the f16 range
+    is computed exactly instead (bit-exact)."""
+    import torch
+    rows, in_dim = 512, 1024
+    rng = np.random.default_rng(60 + wtype)
+    w = synth.expert_tensor(rng, wtype, 1, rows, in_dim)
+    W16 = expert_weights(w, wtype, 0, rows, in_dim, True).astype(np.float64)
+    M = tie_amd.Matrix(w, wtype, rows, in_dim)
+    for T, flags in ((65, tie_amd.PATH_AUTO), (200, tie_amd.PATH_MFMA), (7, tie_amd.PATH_MFMA)):
+        x = synth.make_input(61 + T, T, in_dim)
+        x[3] *= np.float32(1e5)  # beyond f16: recomputed exactly
+        print("dense mfma type=%d T=%d" % (wtype, T), flush=True)
+        xd = torch.from_numpy(x).cuda()
+        out = torch.empty((T, rows), device="cuda")
+        M.mat_mat(xd, T, out, flags=flags)
+        torch.cuda.synchronize()
+        got = out.cpu().numpy()
+        ro = bind.mat_mat(x, w, wtype, rows)
+        np.testing.assert_array_equal(bits(got[3]), bits(ro[3]), err_msg="flagged row")
+        rest = np.setdiff1d(np.arange(T), [3])
+        ref = f16(x[rest]).astype(np.float64) @ W16.T
+        e_model = rel_l2(got[rest], ref)
+        e_oracle, _ = report("dense_mfma t%d T=%d" % (wtype, T), got[rest], ro[rest])
+        assert e_model <= MODEL_RL2, e_model
+        assert e_oracle <= ORACLE_RL2, e_oracle
+    M.close()
+
+
+def test_dense_mat_mat_mfma_limits():
+    """The matrix-core dense path is refused for what it cannot run (F32,
+    rows not a multiple of 256) when asked for, and not taken by default:
+    the default then runs TIE's row kernels (bit-exact)."""
+    import torch
+    rows, in_dim, T = 320, 512, 100
+    rng = np.random.default_rng(66)
+    w = synth.expert_tensor(rng, synth.Q4_K, 1, rows, in_dim)
+    M = tie_amd.Matrix(w, synth.Q4_K, rows, in_dim)
+    x = synth.make_input(66, T, in_dim)
+    xd = torch.from_numpy(x).cuda()
+    out = torch.empty((T, rows), device="cuda")
+    with pytest.raises(tie_amd.TieError):
+        M.mat_mat(xd, T, out, flags=tie_amd.PATH_MFMA)
+    M.mat_mat(xd, T, out, flags=tie_amd.PATH_AUTO)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(bits(out.cpu().numpy()), bits(bind.mat_mat(x, w, synth.Q4_K, rows)))
+    M.close()

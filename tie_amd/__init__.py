@@ -292,8 +292,10 @@ class Matrix:
         check(lib().tie_hip_matrix_create(_p(w), wtype, rows, in_dim, int(on_device), ctypes.byref(h)))
         self.handle = h
 
-    def mat_mat(self, x_dev, T, out_dev, flags=PATH_EXACT, stream=None):
-        """out[t][r] = W[r] . x[t] on device pointers (dispatch_mat_mat)."""
+    def mat_mat(self, x_dev, T, out_dev, flags=PATH_AUTO, stream=None):
+        """out[t][r] = W[r] . x[t] on device pointers (dispatch_mat_mat);
+        PATH_AUTO takes the matrix cores above the exact threshold where the
+        matrix allows them, PATH_EXACT always TIE's row kernels."""
         check(lib().tie_hip_mat_mat(self.handle, _p(x_dev), T, _p(out_dev), flags, stream))
 
     def close(self):

@@ -1023,11 +1023,21 @@ extern "C" int tie_hip_mat_mat(tie_hip_matrix *m, const float *x_dev, int T, flo
 		return TIE_HIP_OK;
 	if (!x_dev || !out_dev)
 		return set_error(TIE_HIP_EINVAL, "null x/out");
-	if (flags & TIE_HIP_PATH_MFMA)
-		return set_error(TIE_HIP_EINVAL, "tie_hip_mat_mat runs TIE's row kernels only (TIE_HIP_PATH_EXACT)");
 	hipStream_t s = stream ? (hipStream_t)stream : g.stream;
-	prof_begin("dense", s);
-	if (m->F.router) {
+	// the matrix cores: asked for, or by default above the exact threshold
+	// where the matrix allows them (Q4_K / Q6_K, rows a multiple of 256)
+	const bool mfma_ok = !m->F.router && mfma_dense_supported(m->W, T);
+	const bool mfma = (flags & TIE_HIP_PATH_MFMA) || (!(flags & TIE_HIP_PATH_EXACT) && T > g.exact_max_t && mfma_ok);
+	if (mfma && !mfma_ok)
+		return set_error(TIE_HIP_EINVAL, "the matrix-core path needs a Q4_K / Q6_K matrix with rows a multiple of 256");
+	prof_begin(mfma ? "dense_mfma" : "dense", s);
+	if (mfma) {
+		Workspace *ws = nullptr;
+		rc = ensure_workspace(s, T, 1, m->W.in, QK, 1, &ws);
+		if (rc)
+			return rc;
+		HIP_TRY(launch_mfma_dense(m->W, x_dev, T, out_dev, *ws, s));
+	} else if (m->F.router) {
 		HIP_TRY(launch_router_logits(m->F, x_dev, T, out_dev, s));
 	} else if (dense_rows_supported(m->W, T)) {
 		HIP_TRY(launch_dense_rows(m->W, x_dev, T, out_dev, s));

@@ -177,6 +177,13 @@ hipError_t launch_dense(const ExpertTensor &W, const float *x, int T, float *out
 // the block loaded once for all tokens (decode.hip); needs no workspace
 bool dense_rows_supported(const ExpertTensor &W, int T);
 hipError_t launch_dense_rows(const ExpertTensor &W, const float *x, int T, float *out, hipStream_t s);
+// TIE's exact rows of the tokens with flag[t] set (decode.hip)
+hipError_t launch_dense_fix(const ExpertTensor &W, const float *x, int T, float *out, const int32_t *flag,
+			    hipStream_t s);
+// Dense Q4_K / Q6_K matrix product on the f16 matrix cores (mfma.hip): rows
+// a multiple of 256; tokens whose x leaves the f16 range computed exactly
+bool mfma_dense_supported(const ExpertTensor &W, int T);
+hipError_t launch_mfma_dense(const ExpertTensor &W, const float *x, int T, float *out, Workspace &ws, hipStream_t s);
 int dense_groups(int T);
 // res (optional): out = res + combine (the residual add after the block)
 // y16: y holds bf16 values (the MFMA path's down output with quantised weights)

@@ -1166,12 +1166,10 @@ hipError_t launch_decode_one(const Layer &L, const float *x, int k, const float 
 // the block in registers (every load up front) and its dot taken with each
 // token's x from LDS; then the serial sums over the blocks, out[t][row].
 constexpr int DENSE_ROWS_T = 4;
-template <int TW> __global__ __launch_bounds__(DEC_MAX_THREADS) void dense_rows_kernel(const uint8_t *__restrict__ W,
-											  const float *__restrict__ x, int T,
-											  int in, int rows, int R,
-											  float *__restrict__ out)
+template <int TW>
+__device__ __forceinline__ void dense_rows_tile(const uint8_t *__restrict__ W, const float *__restrict__ x, int T, int in,
+						int rows, int R, float *__restrict__ out, int r0, float *dl)
 {
-	extern __shared__ __attribute__((aligned(16))) float dl[];
 	const int nb = in / QK;
 	float *xs = dl;                        // [T][nb][XSEG]
 	float *part = dl + (size_t)T * nb * XSEG; // [T][nb][R]
@@ -1180,7 +1178,6 @@ template <int TW> __global__ __launch_bounds__(DEC_MAX_THREADS) void dense_rows_
 		*reinterpret_cast<float4 *>(xs + ((size_t)t * nb + r / QK) * XSEG + (r % QK)) = v;
 	});
 	__syncthreads();
-	const int r0 = blockIdx.x * R;
 	for (int u = threadIdx.x; u < nb * R; u += blockDim.x) {
 		const int r = u & (R - 1), b = u / R;
 		const uint8_t *blk = panel_slot(W, 0, 0, r0 + r, b, nb, panel_bytes(TW));
@@ -1200,12 +1197,66 @@ template <int TW> __global__ __launch_bounds__(DEC_MAX_THREADS) void dense_rows_
 	}
 }
 
+template <int TW> __global__ __launch_bounds__(DEC_MAX_THREADS) void dense_rows_kernel(const uint8_t *__restrict__ W,
+											  const float *__restrict__ x, int T,
+											  int in, int rows, int R,
+											  float *__restrict__ out)
+{
+	extern __shared__ __attribute__((aligned(16))) float dl[];
+	dense_rows_tile<TW>(W, x, T, in, rows, R, out, blockIdx.x * R, dl);
+}
+
+// The exact rows (TIE's row kernel, as dense_rows_kernel) of the tokens
+// flagged by the matrix-core dense path (x outside the f16 range; usually
+// none), over R rows per workgroup: each workgroup walks the flags 64 at a
+// time and recomputes its rows of every flagged token.
+template <int TW> __global__ __launch_bounds__(DEC_MAX_THREADS) void dense_fix_kernel(const uint8_t *__restrict__ W,
+											 const float *__restrict__ x, int T,
+											 int in, int rows, int R,
+											 float *__restrict__ out,
+											 const int32_t *__restrict__ flag)
+{
+	extern __shared__ __attribute__((aligned(16))) float dl[];
+	__shared__ unsigned long long sbits;
+	for (int t0 = 0; t0 < T; t0 += 64) {
+		if (threadIdx.x < 64) {
+			const int t = t0 + threadIdx.x;
+			const unsigned long long m = __ballot(t < T && flag[t] != 0);
+			if (threadIdx.x == 0)
+				sbits = m;
+		}
+		__syncthreads();
+		unsigned long long m = sbits;
+		__syncthreads();
+		while (m) {
+			const int t = t0 + __builtin_ctzll(m);
+			m &= m - 1;
+			dense_rows_tile<TW>(W, x + (size_t)t * in, 1, in, rows, R, out + (size_t)t * rows, blockIdx.x * R, dl);
+			__syncthreads();
+		}
+	}
+}
+
 bool dense_rows_supported(const ExpertTensor &W, int T)
 {
 	const int nb = W.in / QK;
 	const size_t lds = sizeof(float) * ((size_t)DENSE_ROWS_T * nb * XSEG + (size_t)DENSE_ROWS_T * nb * 64);
 	return T <= DENSE_ROWS_T && (W.type == TIE_GGML_Q4_K || W.type == TIE_GGML_Q6_K) && nb <= DEC_MAX_THREADS &&
 	       lds <= DEC_MAX_LDS;
+}
+
+hipError_t launch_dense_fix(const ExpertTensor &W, const float *x, int T, float *out, const int32_t *flag, hipStream_t s)
+{
+	const int nb = W.in / QK;
+	int R = 64;
+	while (R > 1 && (nb * R > DEC_MAX_THREADS || W.rows / R < 512))
+		R >>= 1;
+	const size_t lds = sizeof(float) * ((size_t)nb * XSEG + (size_t)nb * R);
+	const dim3 grid(W.rows / R);
+	const dim3 block((nb * R + 63) & ~63);
+	return W.type == TIE_GGML_Q4_K
+		       ? dec_launch(dense_fix_kernel<TIE_GGML_Q4_K>, grid, block, lds, s, W.data, x, T, W.in, W.rows, R, out, flag)
+		       : dec_launch(dense_fix_kernel<TIE_GGML_Q6_K>, grid, block, lds, s, W.data, x, T, W.in, W.rows, R, out, flag);
 }
 
 hipError_t launch_dense_rows(const ExpertTensor &W, const float *x, int T, float *out, hipStream_t s)

@@ -156,6 +156,7 @@ struct MfmaArgs {
 	float y_scale;           // down out (f16 operands): 2^(h_shift - F16_SHIFT) takes both factors out
 	float *y;                // down out [pair][d] (BF16 weights: fp32)
 	uint16_t *y16;           // down out [pair][d] (quantised weights: bf16)
+	float *out32;            // down: fp32 rows [pair][rows] instead of y16 (dense matrices)
 	int32_t *tok_flag;       // [T] gate/up, h_f16: tokens whose h left the f16 range
 	int32_t *fix_list;       //     are appended here (once each) ...
 	int32_t *fix_count;      //     ... and counted
@@ -1079,7 +1080,11 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 					const float4 v1 = *reinterpret_cast<const float4 *>(tl + r * LS + 8 * part + 4);
 					const int mrow = 32 * mt + 16 * half + r;
 					if (mrow < nrows) {
-						if (DOWN) {
+						if (DOWN && a.out32) {
+							float *orow = a.out32 + (size_t)spair[mrow] * a.rows + slab * DN_COLS + 64 * w + 8 * part;
+							*reinterpret_cast<float4 *>(orow) = v0;
+							*reinterpret_cast<float4 *>(orow + 4) = v1;
+						} else if (DOWN) {
 							const uint4 o = make_uint4(pack_bf16(v0.x, v0.y), pack_bf16(v0.z, v0.w),
 										   pack_bf16(v1.x, v1.y), pack_bf16(v1.z, v1.w));
 							uint16_t *yr = a.y16 + (size_t)spair[mrow] * a.rows + slab * DN_COLS + 64 * w + 8 * part;
@@ -1559,6 +1564,7 @@ hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, con
 	a.tok_flag = ws.tok_flag;
 	a.fix_list = ws.fix_list;
 	a.fix_count = ws.fix_count;
+	a.out32 = nullptr;
 	// grid rows: a bound on each kernel's tiles (its own tile rows) plus 8
 	// rows: the XCD remap in the kernel reaches every live item only with
 	// at least 8 * ceil(live / 8) workgroups (rows past the tiles exit at
@@ -1597,6 +1603,85 @@ hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, con
 	err = launch_one<true>(a, L.down.type, dim3(L.d / DN_COLS, dn_tiles), s);
 	prof_end(s);
 	return err;
+}
+
+// ------------------------------------------------------------ dense matrices
+// dispatch_mat_mat (math_dispatch.c:304-359) on the f16 matrix cores: the
+// matrix is one "expert" whose pairs are the T tokens in order (k = 1), run
+// by the down kernel (A = x as f16 in the pair-permuted K order, unscaled;
+// fp32 output rows).  dense_prep_kernel converts x (one wave per token),
+// flags tokens whose x leaves the f16 range (their rows are recomputed in
+// TIE's exact arithmetic afterwards, launch_dense_fix), and writes the
+// one-expert pair list (cnt[0] = T, bucket[t] = t).
+__global__ __launch_bounds__(RB_THREADS) void dense_prep_kernel(const float *__restrict__ x, int T, int in,
+								 uint16_t *__restrict__ xa, int32_t *__restrict__ cnt,
+								 int32_t *__restrict__ bucket, int32_t *__restrict__ flag)
+{
+	const int lane = threadIdx.x & 63;
+	const int t = blockIdx.x * (RB_THREADS / 64) + (threadIdx.x >> 6);
+	if (t >= T)
+		return;
+	if (t == 0 && lane == 0)
+		cnt[0] = T;
+	if (lane == 0)
+		bucket[t] = t;
+	const float4 *xr = reinterpret_cast<const float4 *>(x + (size_t)t * in);
+	f16x8 *yr = reinterpret_cast<f16x8 *>(xa + (size_t)t * in);
+	int bad = 0;
+	for (int i = lane; i < in / 8; i += 64) {
+		const float4 a = xr[2 * i], c = xr[2 * i + 1];
+		const float m = __builtin_fmaxf(__builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(a.x), __builtin_fabsf(a.y)),
+								__builtin_fmaxf(__builtin_fabsf(a.z), __builtin_fabsf(a.w))),
+						__builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(c.x), __builtin_fabsf(c.y)),
+								__builtin_fmaxf(__builtin_fabsf(c.z), __builtin_fabsf(c.w))));
+		// fmax drops NaN: test the values themselves for NaN
+		const bool nan = a.x != a.x || a.y != a.y || a.z != a.z || a.w != a.w || c.x != c.x || c.y != c.y ||
+				 c.z != c.z || c.w != c.w;
+		bad |= (nan || !(m < 65504.0f)) ? 1 : 0;
+		yr[i] = f16x8{(_Float16)a.x, (_Float16)a.z, (_Float16)a.y, (_Float16)a.w,
+			      (_Float16)c.x, (_Float16)c.z, (_Float16)c.y, (_Float16)c.w};
+	}
+	bad = __any(bad);
+	if (lane == 0)
+		flag[t] = bad;
+}
+
+bool mfma_dense_supported(const ExpertTensor &W, int T)
+{
+	return TIE_MFMA_F16 && (W.type == TIE_GGML_Q4_K || W.type == TIE_GGML_Q6_K) && W.rows % DN_COLS == 0 &&
+	       (size_t)T * W.in * 2 <= 0xfffffffeu && (size_t)T * W.rows * 4 <= 0xfffffffeu;
+}
+
+hipError_t launch_mfma_dense(const ExpertTensor &W, const float *x, int T, float *out, Workspace &ws, hipStream_t s)
+{
+	if (T == 0)
+		return hipSuccess;
+	if (!mfma_dense_supported(W, T))
+		return hipErrorInvalidValue;
+	hipLaunchKernelGGL(dense_prep_kernel, dim3((T + RB_THREADS / 64 - 1) / (RB_THREADS / 64)), dim3(RB_THREADS), 0, s, x,
+			   T, W.in, ws.xb, ws.bucket_cnt, ws.bucket, ws.tok_flag);
+	hipError_t err = hipGetLastError();
+	if (err != hipSuccess)
+		return err;
+	MfmaArgs a;
+	memset(&a, 0, sizeof a);
+	a.k = 1;
+	a.E = 1;
+	a.cnt = ws.bucket_cnt;
+	a.bucket = ws.bucket;
+	a.bstride = T4(T);
+	a.y_scale = ldexpf(1.0f, -F16_SHIFT); // x unscaled; the weights' factor 2^F16_SHIFT out
+	a.out32 = out;
+	a.w[0] = a.w[1] = W.data;
+	a.expert_bytes[0] = a.expert_bytes[1] = W.expert_bytes;
+	a.rows = W.rows;
+	a.in = W.in;
+	a.a16 = ws.xb;
+	const int tiles = (T + MFMA_MT_DN - 1) / MFMA_MT_DN + 1 + 8;
+	err = launch_one<true>(a, W.type, dim3(W.rows / DN_COLS, tiles), s);
+	if (err != hipSuccess)
+		return err;
+	return launch_dense_fix(W, x, T, out, ws.tok_flag, s);
 }
 
 } // namespace tie
