@@ -289,6 +289,14 @@ def run_config(torch, tie_amd, wl, T, k, steps, warmup, flags, cfg=None, graph=F
                 ms_eager=ms_eager, timing="graph" if graph else "eager")
 
 
+def workload_name(synth, name, cfg):
+    if cfg.get("kind") == "dense":
+        return "%s: dense %s %d x %d, T=%d" % (name, synth.TYPE_NAMES[cfg["wtype"]], cfg["rows"], cfg["in"], cfg["T"])
+    return "%s: d=%d F=%d E=%d k=%d T=%d, gate/up %s, down %s" % (
+        name, cfg["d"], cfg["F"], cfg["E"], cfg["k"], cfg["T"], synth.TYPE_NAMES[cfg["gu_type"]],
+        synth.TYPE_NAMES[cfg["down_type"]])
+
+
 def roofline(m, config):
     """Roofline object for the dominant (longest) kernel of a measurement of one
     workload; traffic is the copy-scaled HBM bytes per launch measured for that
@@ -509,12 +517,10 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16" if any(k.startswith("mfma") for k in m["kernels"]) else "f32",
+        "dtype": "f16" if any("mfma" in k for k in m["kernels"]) else "f32",
         "data": "synthetic (seeded GGUF-layout Q4_K/Q6_K blocks, N(0,1) inputs; %d weight layers cycled)" % m[
             "layers"],
-        "config": {"workload": "%s: d=%d F=%d E=%d k=%d T=%d, gate/up %s, down %s" % (
-            main_name, cfg["d"], cfg["F"], cfg["E"], cfg["k"], cfg["T"], synth.TYPE_NAMES[cfg["gu_type"]],
-            synth.TYPE_NAMES[cfg["down_type"]]), "T": cfg["T"], "path": args.path},
+        "config": {"workload": workload_name(synth, main_name, cfg), "T": cfg["T"], "path": args.path},
         "roofline": roofline(m, main_name),
         "cpu_baseline": cpu.get(main_name),
         "parity": parity.get(main_name),

@@ -125,6 +125,31 @@ def test_dense_mat_mat(wtype):
     M.close()
 
 
+@pytest.mark.parametrize("wtype,rows,in_dim", [(synth.Q6_K, 33024, 2048), (synth.Q4_K, 33024, 2048),
+                                               (synth.Q6_K, 41024, 1536), (synth.Q4_K, 16448, 4096)])
+def test_dense_stream(wtype, rows, in_dim):
+    """One token through a tall matrix (the LM head's shape class): at
+    rows x blocks / 64 >= 4096 units tie_hip_mat_mat streams units of 64 /
+    nb rows through persistent waves (dense_stream_kernel), including block
+    counts that do not divide 64 (nb = 6: ten rows per unit, four lanes
+    idle) and a last unit past the matrix's end; bit for bit with the
+    oracle."""
+    import torch
+    rng = np.random.default_rng(50 + wtype + in_dim)
+    w = synth.expert_tensor(rng, wtype, 1, rows, in_dim)
+    M = tie_amd.Matrix(w, wtype, rows, in_dim)
+    x = synth.make_input(51 + in_dim, 1, in_dim)
+    x[0, 5] = -0.0
+    print("dense stream case type=%d rows=%d in=%d" % (wtype, rows, in_dim), flush=True)
+    xd = torch.from_numpy(x).cuda()
+    out = torch.full((1, rows), float("nan"), device="cuda")
+    for _ in range(2):
+        M.mat_mat(xd, 1, out)
+    torch.cuda.synchronize()
+    assert_same(out.cpu().numpy(), bind.mat_mat(x, w, wtype, rows), "dense stream out")
+    M.close()
+
+
 @pytest.mark.parametrize("name", ["gffn_qwen3_t3", "gffn_tiny_t5"])
 def test_qwen3_ffn_residual(name):
     """tie_hip_qwen3_ffn: RMSNorm (with the host RSQRTSS table), block and

@@ -1039,6 +1039,8 @@ extern "C" int tie_hip_mat_mat(tie_hip_matrix *m, const float *x_dev, int T, flo
 		HIP_TRY(launch_mfma_dense(m->W, x_dev, T, out_dev, *ws, s));
 	} else if (m->F.router) {
 		HIP_TRY(launch_router_logits(m->F, x_dev, T, out_dev, s));
+	} else if (dense_stream_supported(m->W, T)) {
+		HIP_TRY(launch_dense_stream(m->W, x_dev, out_dev, s));
 	} else if (dense_rows_supported(m->W, T)) {
 		HIP_TRY(launch_dense_rows(m->W, x_dev, T, out_dev, s));
 	} else {

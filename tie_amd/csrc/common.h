@@ -177,6 +177,8 @@ hipError_t launch_dense(const ExpertTensor &W, const float *x, int T, float *out
 // the block loaded once for all tokens (decode.hip); needs no workspace
 bool dense_rows_supported(const ExpertTensor &W, int T);
 hipError_t launch_dense_rows(const ExpertTensor &W, const float *x, int T, float *out, hipStream_t s);
+bool dense_stream_supported(const ExpertTensor &W, int T);
+hipError_t launch_dense_stream(const ExpertTensor &W, const float *x, float *out, hipStream_t s);
 // TIE's exact rows of the tokens with flag[t] set (decode.hip)
 hipError_t launch_dense_fix(const ExpertTensor &W, const float *x, int T, float *out, const int32_t *flag,
 			    hipStream_t s);
@@ -256,6 +258,24 @@ __device__ __forceinline__ float half_bits_to_float(uint32_t h)
 		bits = sign;
 	}
 	return __uint_as_float(bits);
+}
+
+// Q6_K codes q = ql nibble | (qh 2-bit field << 4) of four weights, as the
+// int8 bytes of q - 32 (exact: -32..31): the two high bits h select the
+// signed top nibble (h - 2) << 4 from a byte table with one v_perm_b32, the
+// nibble is or-ed in below it.  `hsh` is the field's shift in H (0, 2, 4,
+// 6), `lsh` the nibble's in L (0, 4).  Each byte converts to float in one
+// instruction (sbyte_f).
+__device__ __forceinline__ uint32_t q6_codes(uint32_t L, int lsh, uint32_t H, int hsh)
+{
+	const uint32_t top = __builtin_amdgcn_perm(0u, 0x1000f0e0u, (H >> hsh) & 0x03030303u);
+	return top | ((L >> lsh) & 0x0f0f0f0fu);
+}
+
+// signed byte i of w as a float
+__device__ __forceinline__ float sbyte_f(uint32_t w, int i)
+{
+	return (float)(int8_t)((w >> (8 * i)) & 0xffu);
 }
 
 __device__ __forceinline__ float bf16_bits_to_float(uint32_t b)

@@ -163,9 +163,21 @@ __device__ __forceinline__ float q4k_dot(uint4 (&c)[9], dfloat *x)
 // q = ql nibble | qh bits << 4 of weights 128n + l + 4hw + i + 32r (r =
 // 0..3) and accumulates fma(d*sc, (q - 32) * x, acc) into accumulators
 // 4hw + i of a0 (r = 0, 2) and a1 (r = 1, 3), the product rounded on its
-// own.
-__device__ __forceinline__ float q6k_dot(uint4 (&c)[13], uint32_t dbits, dfloat *x)
+// own.  PX: the input pairs of each half step are read from LDS one half
+// step ahead (streamed kernels, whose waves have no other LDS work to hide
+// the latency behind).
+template <bool PX = false> __device__ __forceinline__ float q6k_dot(uint4 (&c)[13], uint32_t dbits, dfloat *x)
 {
+	// inputs of half step hs = 2 st + half: x[128n + l + 4hw + 64 half + {0, 32} ..]
+	auto xat = [&](int hs) {
+		const int st = hs >> 1, half = hs & 1;
+		return x + 128 * (st >> 3) + 8 * ((st >> 1) & 3) + 4 * (st & 1) + 64 * half;
+	};
+	vf4 pa, pc;
+	if constexpr (PX) {
+		pa = *(dfloat4 *)xat(0);
+		pc = *(dfloat4 *)(xat(0) + 32);
+	}
 	const float d = half_bits_to_float(dbits);
 	uint4 sc4 = c[12];
 	auto sc = [&](int j) { return (float)(int8_t)((dword_of(sc4, j >> 2) >> (8 * (j & 3))) & 0xffu); };
@@ -180,7 +192,8 @@ __device__ __forceinline__ float q6k_dot(uint4 (&c)[13], uint32_t dbits, dfloat 
 		if ((st & 3) == 0) {
 			// one quarter at a time
 			acc_fence(a0, a1);
-			asm volatile("" : "+v"(x));
+			if constexpr (!PX)
+				asm volatile("" : "+v"(x));
 			pin(sc4);
 			pin(c[4 * n + hl]);
 			pin(c[4 * n + 2 + hl]);
@@ -193,22 +206,33 @@ __device__ __forceinline__ float q6k_dot(uint4 (&c)[13], uint32_t dbits, dfloat 
 		const float W2 = d * sc(8 * n + is + 4), W3 = d * sc(8 * n + is + 6);
 		const int dw = ((l & 8) >> 2) + hw;
 		const uint32_t L = dword_of(C0, dw), L2 = dword_of(C1, dw), H = dword_of(C2, dw);
-		const uint32_t q1 = (L & 0x0f0f0f0fu) | ((H & 0x03030303u) << 4);
-		const uint32_t q2 = (L2 & 0x0f0f0f0fu) | (((H >> 2) & 0x03030303u) << 4);
-		const uint32_t q3 = ((L >> 4) & 0x0f0f0f0fu) | (((H >> 4) & 0x03030303u) << 4);
-		const uint32_t q4 = ((L2 >> 4) & 0x0f0f0f0fu) | (((H >> 6) & 0x03030303u) << 4);
+		// bytes of q - 32
+		const uint32_t q1 = q6_codes(L, 0, H, 0), q2 = q6_codes(L2, 0, H, 2);
+		const uint32_t q3 = q6_codes(L, 4, H, 4), q4 = q6_codes(L2, 4, H, 6);
 		dfloat *xb = x + 128 * n + l + 4 * hw;
 #pragma unroll
 		for (int half = 0; half < 2; half++) {
 			uint32_t qa = half ? q3 : q1, qb = half ? q4 : q2;
-			asm volatile("" : "+v"(qa), "+v"(qb)); // byte-parallel codes (v_cvt_f32_ubyteN)
+			asm volatile("" : "+v"(qa), "+v"(qb)); // byte-parallel codes (one conversion each)
 			const float Wa = half ? W2 : W0, Wb = half ? W3 : W1;
-			const vf4 xa = *(dfloat4 *)(xb + 64 * half), xc = *(dfloat4 *)(xb + 64 * half + 32);
+			vf4 xa, xc;
+			if constexpr (PX) {
+				xa = pa;
+				xc = pc;
+				const int hs = 2 * st + half;
+				if (hs + 1 < 32) {
+					pa = *(dfloat4 *)xat(hs + 1);
+					pc = *(dfloat4 *)(xat(hs + 1) + 32);
+				}
+			} else {
+				xa = *(dfloat4 *)(xb + 64 * half);
+				xc = *(dfloat4 *)(xb + 64 * half + 32);
+			}
 			const float xav[4] = {xa.x, xa.y, xa.z, xa.w}, xcv[4] = {xc.x, xc.y, xc.z, xc.w};
 #pragma unroll
 			for (int i = 0; i < 4; i++) {
 				const int m = 4 * hw + i;
-				const float fa = byte_f(qa, i) - 32.0f, fb = byte_f(qb, i) - 32.0f;
+				const float fa = sbyte_f(qa, i), fb = sbyte_f(qb, i);
 				a0[m] = __builtin_fmaf(Wa, fa * xav[i], a0[m]);
 				a1[m] = __builtin_fmaf(Wb, fb * xcv[i], a1[m]);
 			}
@@ -236,7 +260,7 @@ template <> struct RowBlock<TIE_GGML_Q4_K> {
 		for (int i = 0; i < 9; i++)
 			c[i] = *(const uint4 *)(g4 *)(blk + 1024 * i);
 	}
-	__device__ __forceinline__ float dot(dfloat *x) { return q4k_dot(c, x); }
+	template <bool PX = false> __device__ __forceinline__ float dot(dfloat *x) { return q4k_dot(c, x); }
 };
 template <> struct RowBlock<TIE_GGML_Q6_K> {
 	uint4 c[13];
@@ -248,7 +272,7 @@ template <> struct RowBlock<TIE_GGML_Q6_K> {
 			c[i] = *(const uint4 *)(g4 *)(blk + 1024 * i);
 		db = *(const uint16_t *)dp;
 	}
-	__device__ __forceinline__ float dot(dfloat *x) { return q6k_dot(c, db, x); }
+	template <bool PX = false> __device__ __forceinline__ float dot(dfloat *x) { return q6k_dot<PX>(c, db, x); }
 };
 
 
@@ -1235,6 +1259,157 @@ template <int TW> __global__ __launch_bounds__(DEC_MAX_THREADS) void dense_fix_k
 			__syncthreads();
 		}
 	}
+}
+
+// ------------------------------------------------------------ dense, one token, many rows
+// dispatch_mat_mat (math_dispatch.c:304-359) at T = 1 for tall matrices (the
+// LM head): persistent waves stream units of `rpw` rows x nb blocks, one
+// lane per (row, block), and load the next unit's blocks into registers
+// while the current unit's are dotted (TIE's row kernel per block, as
+// dense_rows_kernel).  Each row's sum over its blocks (0 + p_0 + p_1 + ...,
+// math_avx2.c:762-766) is taken in block order by the row's block-0 lane.
+#ifndef TIE_STREAM_WAVES
+#define TIE_STREAM_WAVES 4
+#endif
+constexpr int STREAM_WAVES = TIE_STREAM_WAVES;
+#ifndef TIE_STREAM_PX
+#define TIE_STREAM_PX 1
+#endif
+constexpr bool STREAM_PX = TIE_STREAM_PX;
+
+// 0 + p_0 + p_1 + ... + p_{N-1} over lanes i .. i + N - 1 (on lane i, N <= 16
+// lanes inside one DPP row), with the values brought over by row shifts.
+template <int N> __device__ __forceinline__ float row_serial_sum(float p)
+{
+	float acc = 0.0f + p;
+	if constexpr (N > 1) acc = acc + dppf<0x101>(p);
+	if constexpr (N > 2) acc = acc + dppf<0x102>(p);
+	if constexpr (N > 3) acc = acc + dppf<0x103>(p);
+	if constexpr (N > 4) {
+		acc = acc + dppf<0x104>(p);
+		acc = acc + dppf<0x105>(p);
+		acc = acc + dppf<0x106>(p);
+		acc = acc + dppf<0x107>(p);
+	}
+	if constexpr (N > 8) {
+		acc = acc + dppf<0x108>(p);
+		acc = acc + dppf<0x109>(p);
+		acc = acc + dppf<0x10a>(p);
+		acc = acc + dppf<0x10b>(p);
+		acc = acc + dppf<0x10c>(p);
+		acc = acc + dppf<0x10d>(p);
+		acc = acc + dppf<0x10e>(p);
+		acc = acc + dppf<0x10f>(p);
+	}
+	return acc;
+}
+
+template <int TW>
+__device__ __forceinline__ void stream_unit(RowBlock<TW> &cur, RowBlock<TW> &nxt, const uint8_t *__restrict__ W,
+					    dfloat *xb, int u, int nu, int units, int rpw, int rl, int b, int nb, int rows,
+					    float *__restrict__ out)
+{
+	// (unconditional: past the end every wave reads the last unit again,
+	// from the cache; a conditional load would make the compiler move the
+	// whole block between registers)
+	const size_t pb = panel_bytes(TW);
+	int row = (nu < units ? nu : units - 1) * rpw + rl;
+	row = row < rows ? row : rows - 1;
+	const uint8_t *blk = panel_slot(W, 0, 0, row, b, nb, pb);
+	nxt.load(blk, q6k_d_of(blk, row));
+	const float p = cur.template dot<STREAM_PX>(xb);
+	float acc;
+	switch (nb) {
+	case 4: acc = row_serial_sum<4>(p); break;
+	case 8: acc = row_serial_sum<8>(p); break;
+	case 16: acc = row_serial_sum<16>(p); break;
+	default:
+		acc = 0.0f;
+		for (int j = 0; j < nb; j++)
+			acc = acc + __shfl(p, rl * nb + j);
+	}
+	row = u * rpw + rl;
+	if (b == 0 && rl < rpw && row < rows)
+		out[row] = acc;
+}
+
+template <int TW>
+__global__ __launch_bounds__(64 * STREAM_WAVES) void dense_stream_kernel(const uint8_t *__restrict__ W,
+									  const float *__restrict__ x, int in, int rows,
+									  int rpw, int units, float *__restrict__ out)
+{
+	extern __shared__ __attribute__((aligned(16))) float dl[];
+	const int nb = in / QK;
+	copy_in<4>(reinterpret_cast<const float4 *>(x), in / 4, [&](int q, float4 v) {
+		const int f = 4 * q;
+		*reinterpret_cast<float4 *>(dl + (f / QK) * XSEG + (f % QK)) = v;
+	});
+	__syncthreads();
+	const int lane = threadIdx.x & 63;
+	const int rl = lane / nb, b = lane - rl * nb;
+	dfloat *xb = (dfloat *)(dl + b * XSEG);
+	const int nw = gridDim.x * STREAM_WAVES;
+	// consecutive units to the waves of a workgroup, so that the waves with
+	// one unit more than the others sit on different SIMDs of few CUs
+	int u = blockIdx.x * STREAM_WAVES + (threadIdx.x >> 6);
+	if (u >= units)
+		return;
+	const size_t pb = panel_bytes(TW);
+	RowBlock<TW> A, B;
+	{
+		int row = u * rpw + rl;
+		row = row < rows ? row : rows - 1;
+		const uint8_t *blk = panel_slot(W, 0, 0, row, b, nb, pb);
+		A.load(blk, q6k_d_of(blk, row));
+	}
+	for (;;) {
+		stream_unit<TW>(A, B, W, xb, u, u + nw, units, rpw, rl, b, nb, rows, out);
+		u += nw;
+		if (u >= units)
+			break;
+		stream_unit<TW>(B, A, W, xb, u, u + nw, units, rpw, rl, b, nb, rows, out);
+		u += nw;
+		if (u >= units)
+			break;
+	}
+}
+
+// units of the streamed kernel at least (below it, dense_rows_kernel)
+constexpr int STREAM_MIN_UNITS = 4096;
+
+bool dense_stream_supported(const ExpertTensor &W, int T)
+{
+	const int nb = W.in / QK;
+	return T == 1 && (W.type == TIE_GGML_Q4_K || W.type == TIE_GGML_Q6_K) && nb <= 64 &&
+	       (long)W.rows * nb / 64 >= STREAM_MIN_UNITS;
+}
+
+hipError_t launch_dense_stream(const ExpertTensor &W, const float *x, float *out, hipStream_t s)
+{
+	const int nb = W.in / QK;
+	const int rpw = 64 / nb;
+	const int units = (W.rows + rpw - 1) / rpw;
+	const size_t lds = sizeof(float) * (size_t)nb * XSEG;
+	const void *fn = W.type == TIE_GGML_Q4_K ? (const void *)dense_stream_kernel<TIE_GGML_Q4_K>
+						 : (const void *)dense_stream_kernel<TIE_GGML_Q6_K>;
+	static int ncu = 0;
+	if (!ncu) {
+		int dev = 0;
+		if (hipGetDevice(&dev) != hipSuccess ||
+		    hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0)
+			ncu = 256;
+	}
+	int occ = 0;
+	if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, 64 * STREAM_WAVES, lds) != hipSuccess || occ <= 0)
+		occ = 1;
+	int grid = ncu * occ;
+	const int need = (units + STREAM_WAVES - 1) / STREAM_WAVES;
+	grid = grid < need ? grid : need;
+	return W.type == TIE_GGML_Q4_K
+		       ? dec_launch(dense_stream_kernel<TIE_GGML_Q4_K>, dim3(grid), dim3(64 * STREAM_WAVES), lds, s, W.data,
+				    x, W.in, W.rows, rpw, units, out)
+		       : dec_launch(dense_stream_kernel<TIE_GGML_Q6_K>, dim3(grid), dim3(64 * STREAM_WAVES), lds, s, W.data,
+				    x, W.in, W.rows, rpw, units, out);
 }
 
 bool dense_rows_supported(const ExpertTensor &W, int T)

@@ -261,7 +261,7 @@ __device__ __forceinline__ void block_dots(const Q4KStream &S, XP *const xs[PC],
 
 // dot_product_f32_q6k_avx2 (math_avx2.c:411-495) of the lane's block with
 // PC input rows.  Panel chunks: 0-7 ql[0..127], 8-11 qh[0..63], 12 the
-// int8 scales.  q - 32 is formed once per weight; per pair TIE's
+// int8 scales.  q - 32 is formed once per weight (q6_codes); per pair TIE's
 // fma(d*sc, (q - 32) * x, acc) follows, the product rounded on its own.
 // 16 steps s = (n, l, hw) of 16 weights each; step s reads x[128n + l +
 // 4hw + i + {0, 32, 64, 96}].
@@ -334,10 +334,9 @@ __device__ __forceinline__ void block_dots(const Q6KStream &S, XP *const xs[PC],
 			const int dw = ((l & 8) >> 2) + hw;
 			uint32_t L = word(cur[0], dw), L2 = word(cur[1], dw), H = word(cur[2], dw);
 			asm volatile("" : "+v"(L), "+v"(L2), "+v"(H));
-			uint32_t q1 = (L & 0x0f0f0f0fu) | ((H & 0x03030303u) << 4);
-			uint32_t q2 = (L2 & 0x0f0f0f0fu) | (((H >> 2) & 0x03030303u) << 4);
-			uint32_t q3 = ((L >> 4) & 0x0f0f0f0fu) | (((H >> 4) & 0x03030303u) << 4);
-			uint32_t q4 = ((L2 >> 4) & 0x0f0f0f0fu) | (((H >> 6) & 0x03030303u) << 4);
+			// bytes of q - 32
+			uint32_t q1 = q6_codes(L, 0, H, 0), q2 = q6_codes(L2, 0, H, 2);
+			uint32_t q3 = q6_codes(L, 4, H, 4), q4 = q6_codes(L2, 4, H, 6);
 			// two halves: words 1, 2 (accumulators a0, a1 via runs 0 and
 			// 32), then words 3, 4 (runs 64 and 96); every accumulator keeps
 			// TIE's order, and only eight converted weights are live
@@ -350,8 +349,8 @@ __device__ __forceinline__ void block_dots(const Q6KStream &S, XP *const xs[PC],
 				float fa[4], fb[4];
 #pragma unroll
 				for (int i = 0; i < 4; i++) {
-					fa[i] = ubyte(qa, i) - 32.0f;
-					fb[i] = ubyte(qb, i) - 32.0f;
+					fa[i] = sbyte_f(qa, i);
+					fb[i] = sbyte_f(qb, i);
 				}
 #pragma unroll
 				for (int p = 0; p < PC; p++) {

@@ -45,6 +45,7 @@ _NAMES = (
     ("tie::combine_fix_kernel", "combine"),
     ("tie::dense_rows_kernel", "dense"),
     ("tie::dense_groups_kernel", "dense"),
+    ("tie::dense_stream_kernel", "dense"),
     ("tie::dense_prep_kernel", "dense_mfma"),
     ("tie::dense_fix_kernel", "dense_mfma"),
 )
