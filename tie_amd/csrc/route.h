@@ -428,14 +428,26 @@ __device__ __forceinline__ void topk_softmax_group8(const float *lg, int E, int 
 	}
 	auto better = [](uint32_t ok, int oe, uint32_t bk, int be) { return ok > bk || (ok == bk && oe < be); };
 	for (int j = 0; j < k; j++) {
-		uint32_t bk = 0;
-		int be = 0x7fffffff;
+		// the lane's best (largest key, lowest index on ties) as a tree over
+		// adjacent ranges (the left range always holds the lower indices, so
+		// the right one wins only when strictly larger): depth 4, not 16
+		uint32_t tk[V];
+		int tq[V];
 #pragma unroll
-		for (int q = 0; q < V; q++)
-			if (key[q] > bk) {
-				bk = key[q];
-				be = q * G + lig;
-			}
+		for (int q = 0; q < V; q++) {
+			tk[q] = key[q];
+			tq[q] = q;
+		}
+#pragma unroll
+		for (int w = 1; w < V; w <<= 1)
+#pragma unroll
+			for (int q = 0; q < V; q += 2 * w)
+				if (tk[q + w] > tk[q]) {
+					tk[q] = tk[q + w];
+					tq[q] = tq[q + w];
+				}
+		uint32_t bk = tk[0];
+		int be = bk > 0 ? tq[0] * G + lig : 0x7fffffff;
 		uint32_t ok = (uint32_t)dppi<DPP_XOR1>((int)bk);
 		int oe = dppi<DPP_XOR1>(be);
 		if (better(ok, oe, bk, be)) {
@@ -602,6 +614,95 @@ __device__ __forceinline__ int group_pairs(const int32_t *idx, int npairs, int E
 			atomicAdd(&cnt[e], 1);
 	}
 	__syncthreads();
+	if (E <= 128 && npairs < 32768) {
+		// one wave: experts 2 lane, 2 lane + 1; counts and active flags
+		// scanned together (counts in the high half), then the LPT slots
+		if (tid < 64) {
+			const int e0 = 2 * tid, e1 = e0 + 1;
+			const int c0 = e0 < E ? cnt[e0] : 0, c1 = e1 < E ? cnt[e1] : 0;
+			const int v = ((c0 + c1) << 16) | ((c0 > 0) + (c1 > 0));
+			int inc = v;
+#pragma unroll
+			for (int o = 1; o < 64; o <<= 1) {
+				const int y = __shfl_up(inc, o);
+				if (tid >= o)
+					inc += y;
+			}
+			const int ex = inc - v, all = __shfl(inc, 63);
+			const int off0 = ex >> 16, off1 = off0 + c0;
+			int r0 = ex & 0xffff, r1 = r0 + (c0 > 0);
+			if (lpt) {
+				// rank by pair count, larger first: counts bucketed (the last
+				// bucket shared), slots inside a bucket by LDS atomics
+				int *hist = lpt, *bcur = lpt + LPT_BINS;
+				for (int i = tid; i < LPT_BINS; i += 64)
+					hist[i] = 0;
+				__builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+				__builtin_amdgcn_wave_barrier();
+				const int b0 = LPT_BINS - 1 - (c0 < LPT_BINS - 1 ? c0 : LPT_BINS - 1);
+				const int b1 = LPT_BINS - 1 - (c1 < LPT_BINS - 1 ? c1 : LPT_BINS - 1);
+				if (c0 > 0)
+					atomicAdd(&hist[b0], 1);
+				if (c1 > 0)
+					atomicAdd(&hist[b1], 1);
+				__builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
+				__builtin_amdgcn_wave_barrier();
+				// exclusive scan of the buckets, LPT_BINS / 64 per lane
+				constexpr int BPL = LPT_BINS / 64;
+				int h[BPL], hs = 0;
+#pragma unroll
+				for (int i = 0; i < BPL; i++) {
+					h[i] = hist[BPL * tid + i];
+					hs += h[i];
+				}
+				int hin = hs;
+#pragma unroll
+				for (int o = 1; o < 64; o <<= 1) {
+					const int y = __shfl_up(hin, o);
+					if (tid >= o)
+						hin += y;
+				}
+				int base = hin - hs;
+#pragma unroll
+				for (int i = 0; i < BPL; i++) {
+					bcur[BPL * tid + i] = base;
+					base += h[i];
+				}
+				__builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
+				__builtin_amdgcn_wave_barrier();
+				if (c0 > 0)
+					r0 = atomicAdd(&bcur[b0], 1);
+				if (c1 > 0)
+					r1 = atomicAdd(&bcur[b1], 1);
+			}
+			if (e0 < E) {
+				offsets[e0] = off0;
+				cur[e0] = off0;
+				if (c0 > 0)
+					active[r0] = e0;
+			}
+			if (e1 < E) {
+				offsets[e1] = off1;
+				cur[e1] = off1;
+				if (c1 > 0)
+					active[r1] = e1;
+			}
+			if (tid == 0) {
+				offsets[E] = all >> 16;
+				active[E] = all & 0xffff;
+				wsum[0] = all >> 16;
+			}
+		}
+		__syncthreads();
+		const int total = wsum[0];
+		for (int p = tid; p < npairs; p += NT) {
+			const int ex = idx[p];
+			if (ex >= 0 && ex < E)
+				pairs[atomicAdd(&cur[ex], 1)] = p;
+		}
+		__syncthreads();
+		return total;
+	}
 	const int e = tid;
 	const int c = e < E ? cnt[e] : 0;
 	int total, nact;

@@ -82,6 +82,8 @@ __global__ __launch_bounds__(RS_THREADS) void router_small_kernel(const float *_
 constexpr int RM_TOK = 32;
 constexpr int RM_THREADS = RM_TOK * 8;
 
+// U: inputs per lane and batch (d a multiple of 8 U)
+template <int U>
 __global__ __launch_bounds__(RM_THREADS) void router_mid_kernel(const float *__restrict__ x,
 								const float *__restrict__ W,
 								const float *__restrict__ bias, int T, int d, int E,
@@ -92,24 +94,42 @@ __global__ __launch_bounds__(RM_THREADS) void router_mid_kernel(const float *__r
 	const int e = blockIdx.x;
 	const int t0 = blockIdx.y * RM_TOK;
 	const int tid = threadIdx.x;
+	const int t = t0 + (tid >> 3), l = tid & 7;
+	const bool live = t < T;
+	const float *xt = x + (size_t)(live ? t : 0) * d + l;
+	// the token's inputs stream in batches of U per lane, the next batch
+	// loading while the current one is multiplied; the first batch is
+	// issued before the row's staging, so the two memory waits overlap
+	const int nbt = d / (8 * U);
+	float xa[U], xb[U];
+#pragma unroll
+	for (int u = 0; u < U; u++)
+		xa[u] = xt[8 * u];
 	const float4 *W4 = reinterpret_cast<const float4 *>(W + (size_t)e * d);
 	for (int i = tid; i < (d >> 2); i += RM_THREADS)
 		reinterpret_cast<float4 *>(ws)[i] = W4[i];
 	__syncthreads();
-	const int t = t0 + (tid >> 3), l = tid & 7;
-	const bool live = t < T;
-	const float *xt = x + (size_t)(live ? t : 0) * d + l;
 	const float *wl = ws + l;
 	float acc = 0.0f;
-	constexpr int U = 32;
-	for (int i = 0; i < d; i += 8 * U) {
-		float xv[U];
+	for (int bt = 0; bt < nbt; bt += 2) {
+		if (bt + 1 < nbt) {
+#pragma unroll
+			for (int u = 0; u < U; u++)
+				xb[u] = xt[8 * U * (bt + 1) + 8 * u];
+		}
 #pragma unroll
 		for (int u = 0; u < U; u++)
-			xv[u] = xt[i + 8 * u];
+			acc = __builtin_fmaf(xa[u], wl[8 * U * bt + 8 * u], acc);
+		if (bt + 1 >= nbt)
+			break;
+		if (bt + 2 < nbt) {
+#pragma unroll
+			for (int u = 0; u < U; u++)
+				xa[u] = xt[8 * U * (bt + 2) + 8 * u];
+		}
 #pragma unroll
 		for (int u = 0; u < U; u++)
-			acc = __builtin_fmaf(xv[u], wl[i + 8 * u], acc);
+			acc = __builtin_fmaf(xb[u], wl[8 * U * (bt + 1) + 8 * u], acc);
 	}
 	const float r = hsum8_lanes(acc);
 	if (l == 0 && live)
@@ -329,7 +349,7 @@ hipError_t launch_router_logits(const Layer &L, const float *x, int T, float *lo
 				   RT_LDS, s, x, L.routerT, L.bias, T, d, E, logits, z);
 		return hipGetLastError();
 	}
-	hipLaunchKernelGGL(router_mid_kernel, dim3(E, (T + RM_TOK - 1) / RM_TOK), dim3(RM_THREADS),
+	hipLaunchKernelGGL(d % 512 == 0 ? router_mid_kernel<64> : router_mid_kernel<32>, dim3(E, (T + RM_TOK - 1) / RM_TOK), dim3(RM_THREADS),
 			   sizeof(float) * (size_t)d, s, x, L.router, L.bias, T, d, E, logits, z);
 	return hipGetLastError();
 }
