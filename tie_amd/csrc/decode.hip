@@ -545,10 +545,26 @@ struct OneArgs {
 	int rpr, rg, rd;          // rows per router, gate/up, down workgroup
 };
 
+#ifdef TIE_ONE_TRACE
+// diagnostic timeline of the one-launch decode (s_memrealtime, 100 MHz):
+// [2i] earliest, [2i+1] latest time of event i over the workgroups
+constexpr int ONE_TRACE_WG = 8192;
+__device__ unsigned long long g_one_trace[ONE_TRACE_WG][6]; // role + 1, stamps
+__device__ __forceinline__ void one_mark(int i, unsigned long long t)
+{
+	if (blockIdx.x < ONE_TRACE_WG) {
+		g_one_trace[blockIdx.x][0] = 1 + (i >= 6 ? 2 : i >= 3 ? 1 : 0);
+		g_one_trace[blockIdx.x][1 + (i >= 6 ? i - 6 : i >= 3 ? i - 3 : i)] = t;
+	}
+}
+#define ONE_T(v) const unsigned long long v = __builtin_amdgcn_s_memrealtime()
+#else
+#define ONE_T(v)
+#endif
 // The token's logits (published by the router workgroups), read back by
 // thread e, then its selection -> sel_idx / sel_w.  Ends with a barrier.
 __device__ __forceinline__ void one_select(const OneArgs &o, uint64_t *etab, int32_t *sel_idx, float *sel_w, int *sbad,
-					   RankScratch *rs)
+					   RankScratch *rs, bool weights)
 {
 	const int tid = threadIdx.x;
 	if (tid < 32) {
@@ -563,11 +579,17 @@ __device__ __forceinline__ void one_select(const OneArgs &o, uint64_t *etab, int
 			*sbad = 1;
 		rank_key(v, tid, o.a.routing, o.a.pbias, etab, *rs);
 	}
-	topk_rank_block(o.a.E, o.a.k, etab, sel_idx, sel_w, o.a.routing, *rs);
+#ifdef TIE_ONE_TRACE
+	__syncthreads();
+	if (tid == 0 && blockIdx.x < ONE_TRACE_WG)
+		g_one_trace[blockIdx.x][5] = __builtin_amdgcn_s_memrealtime();
+#endif
+	topk_rank_block(o.a.E, o.a.k, etab, sel_idx, sel_w, o.a.routing, *rs, weights);
 }
 
 template <int TG, int TU, int TD> __global__ __launch_bounds__(DEC_MAX_THREADS, 4) void decode_one_kernel(OneArgs o)
 {
+	ONE_T(t_start);
 	extern __shared__ __attribute__((aligned(16))) float dl[];
 	__shared__ int32_t sel_idx[MAX_K];
 	__shared__ float sel_w[MAX_K];
@@ -606,6 +628,7 @@ template <int TG, int TU, int TD> __global__ __launch_bounds__(DEC_MAX_THREADS, 
 			}
 		}
 		__syncthreads();
+		ONE_T(t_staged);
 		if (tid < 8 * ne) {
 			const int r = tid >> 3, l = tid & 7;
 			const float s = hsum8_lanes(lane_chain(dl, dl + (1 + r) * lmf, d, l));
@@ -616,6 +639,14 @@ template <int TG, int TU, int TD> __global__ __launch_bounds__(DEC_MAX_THREADS, 
 				__hip_atomic_store(o.lg + e, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 			}
 		}
+#ifdef TIE_ONE_TRACE
+		if (tid == 0) {
+			ONE_T(t_end);
+			one_mark(0, t_start);
+			one_mark(1, t_staged);
+			one_mark(2, t_end);
+		}
+#endif
 		return;
 	}
 	if (b < o.nr + o.ng) {
@@ -629,11 +660,10 @@ template <int TG, int TU, int TD> __global__ __launch_bounds__(DEC_MAX_THREADS, 
 			const int f = 4 * q;
 			*reinterpret_cast<float4 *>(xs + (f / QK) * XSEG + (f % QK)) = v;
 		});
-		one_select(o, etab, sel_idx, sel_w, &sbad, &rsc);
-		if (gb == 0 && tid < a.k) {
-			a.topk_idx[tid] = sel_idx[tid];
-			a.topk_w[tid] = sel_w[tid];
-		}
+		// the experts only: their gate weights (topk_w, by the first
+		// gate/up workgroup) wait until its h is out
+		one_select(o, etab, sel_idx, sel_w, &sbad, &rsc, false);
+		ONE_T(t_sel);
 		const int e = sel_idx[j];
 		float hv = 0.0f; // a slot without an expert: its h is never used
 		if (e >= 0) {
@@ -658,6 +688,21 @@ template <int TG, int TU, int TD> __global__ __launch_bounds__(DEC_MAX_THREADS, 
 			const unsigned long long w = ((unsigned long long)o.seq << 32) | __float_as_uint(hv);
 			__hip_atomic_store(o.hw + (size_t)j * a.F + r0 + tid, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 		}
+		if (gb == 0) {
+			topk_rank_weights(a.k, etab, sel_idx, sel_w, a.routing, rsc);
+			if (tid < a.k) {
+				a.topk_idx[tid] = sel_idx[tid];
+				a.topk_w[tid] = sel_w[tid];
+			}
+		}
+#ifdef TIE_ONE_TRACE
+		if (tid == 0) {
+			ONE_T(t_end);
+			one_mark(3, t_start);
+			one_mark(4, t_sel);
+			one_mark(5, t_end);
+		}
+#endif
 		return;
 	}
 	// ---- down + combine: rows r0 .. r0 + rd - 1 of d; lane (task, row): the
@@ -666,18 +711,24 @@ template <int TG, int TU, int TD> __global__ __launch_bounds__(DEC_MAX_THREADS, 
 	const int r0 = (b - o.nr - o.ng) * R;
 	float *hs = dl;                           // [k nb][XSEG]
 	float *part = dl + (size_t)k * nb * XSEG; // [k nb][R]
-	one_select(o, etab, sel_idx, sel_w, &sbad, &rsc);
+	one_select(o, etab, sel_idx, sel_w, &sbad, &rsc, false);
+	ONE_T(t_sel);
 	const int ntask = k * nb;
 	const int task = tid / R, r = tid - task * R;
 	const bool live = task < ntask;
-	const int jj = live ? task / nb : 0, bb = task - jj * nb;
+	const int jj = live ? task / nb : 0, bb = live ? task - jj * nb : 0;
 	const int e = live ? sel_idx[jj] : -1;
 	RowBlock<TD> rb;
-	if (e >= 0) {
-		// the weights before the wait for h
-		const uint8_t *blk = panel_slot(a.w[2], a.expert_bytes[2], e, r0 + r, bb, nb, panel_bytes(TD));
-		rb.load(blk, q6k_d_of(blk, r0 + r));
+	{
+		// the weights before the wait for h (unconditional: a lane without
+		// an expert reads expert 0's block and never uses it; a conditional
+		// load would have the compiler wait for it at once)
+		const int rr = live ? r0 + r : r0;
+		const uint8_t *blk = panel_slot(a.w[2], a.expert_bytes[2], e >= 0 ? e : 0, rr, bb, nb, panel_bytes(TD));
+		rb.load(blk, q6k_d_of(blk, rr));
 	}
+	// the gate weights while those loads are in flight
+	topk_rank_weights(k, etab, sel_idx, sel_w, a.routing, rsc);
 	// h (k F words of this call) -> LDS, 8 words of a thread polled at
 	// once, the ones not yet stamped again until all are
 	{
@@ -715,6 +766,7 @@ template <int TG, int TU, int TD> __global__ __launch_bounds__(DEC_MAX_THREADS, 
 			sbad = 1;
 	}
 	__syncthreads();
+	ONE_T(t_h);
 	if (live)
 		part[task * R + r] = e >= 0 ? rb.dot((dfloat *)(hs + (size_t)task * XSEG)) : 0.0f;
 	__syncthreads();
@@ -722,6 +774,15 @@ template <int TG, int TU, int TD> __global__ __launch_bounds__(DEC_MAX_THREADS, 
 	combine_rows(part, nb, k, R, sel_idx, sel_w, outp, a.res ? a.res + r0 : nullptr);
 	if (sbad && tid < R)
 		outp[tid] = __builtin_nanf("");
+#ifdef TIE_ONE_TRACE
+	if (tid == 0) {
+		ONE_T(t_end);
+		one_mark(6, t_start);
+		one_mark(7, t_sel);
+		one_mark(8, t_h);
+		one_mark(9, t_end);
+	}
+#endif
 }
 
 // ------------------------------------------------------------ recompute
@@ -1453,3 +1514,18 @@ hipError_t launch_dense_rows(const ExpertTensor &W, const float *x, int T, float
 } // namespace tie
 
 
+
+#ifdef TIE_ONE_TRACE
+extern "C" int tie_hip_debug_one_trace(unsigned long long *host, int reset)
+{
+	const size_t n = sizeof(unsigned long long) * tie::ONE_TRACE_WG * 6;
+	if (hipMemcpyFromSymbol(host, HIP_SYMBOL(tie::g_one_trace), n) != hipSuccess)
+		return -1;
+	if (reset) {
+		static unsigned long long z[tie::ONE_TRACE_WG * 6];
+		if (hipMemcpyToSymbol(HIP_SYMBOL(tie::g_one_trace), z, n) != hipSuccess)
+			return -1;
+	}
+	return 0;
+}
+#endif

@@ -321,8 +321,23 @@ __device__ __forceinline__ void rank_key(float v, int e, int routing, const floa
 	S.ck[e] = ((unsigned long long)logit_key(v) << 32) | (uint32_t)~(uint32_t)e;
 	S.prob[e] = p;
 }
+// The gate weights of a selection made by topk_rank_block(..., false)
+// (whose slot values S.sv / S.si it reads): out_idx / out_w as
+// topk_rank_block(..., true) writes them.  Ends with a barrier.
+__device__ __forceinline__ void topk_rank_weights(int k, const uint64_t *etab, int32_t *out_idx, float *out_w,
+						  int routing, const RankScratch &S)
+{
+	const int tid = threadIdx.x;
+	if (tid < 64) {
+		const float my_s = tid < k ? S.sv[tid] : -__builtin_inff();
+		const int my_i = tid < k ? S.si[tid] : -1;
+		topk_weights_wave(my_s, my_i, k, etab, out_idx, out_w, routing == ROUTE_SIGMOID);
+	}
+	__syncthreads();
+}
+
 __device__ __forceinline__ void topk_rank_block(int E, int k, const uint64_t *etab, int32_t *out_idx, float *out_w,
-						int routing, RankScratch &S)
+						int routing, RankScratch &S, bool weights = true)
 {
 	const int tid = threadIdx.x;
 	const bool sig = routing == ROUTE_SIGMOID;
@@ -371,13 +386,14 @@ __device__ __forceinline__ void topk_rank_block(int E, int k, const uint64_t *et
 		}
 	}
 	__syncthreads();
-	if (tid < 64) {
-		const int lane = tid;
-		const float my_s = lane < k ? S.sv[lane] : -__builtin_inff();
-		const int my_i = lane < k ? S.si[lane] : -1;
-		topk_weights_wave(my_s, my_i, k, etab, out_idx, out_w, sig);
+	if (!weights) {
+		// the experts only (the weights later, by topk_rank_weights)
+		if (tid < k)
+			out_idx[tid] = S.si[tid];
+		__syncthreads();
+		return;
 	}
-	__syncthreads();
+	topk_rank_weights(k, etab, out_idx, out_w, routing, S);
 }
 
 // topk_softmax_wave with PER chosen for E (E <= MAX_E)
