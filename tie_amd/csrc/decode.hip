@@ -1303,6 +1303,16 @@ template <int TW> __global__ __launch_bounds__(DEC_MAX_THREADS) void dense_fix_k
 {
 	extern __shared__ __attribute__((aligned(16))) float dl[];
 	__shared__ unsigned long long sbits;
+	// usually nothing is flagged: one pass over all the flags first
+	int any = 0;
+	for (int i = threadIdx.x; i < T / 4; i += blockDim.x) {
+		const int4 f = reinterpret_cast<const int4 *>(flag)[i];
+		any |= f.x | f.y | f.z | f.w;
+	}
+	for (int t = (T & ~3) + threadIdx.x; t < T; t += blockDim.x)
+		any |= flag[t];
+	if (!__syncthreads_or(any))
+		return;
 	for (int t0 = 0; t0 < T; t0 += 64) {
 		if (threadIdx.x < 64) {
 			const int t = t0 + threadIdx.x;
