@@ -1258,6 +1258,16 @@ __device__ __forceinline__ void dense_rows_tile(const uint8_t *__restrict__ W, c
 	const int nb = in / QK;
 	float *xs = dl;                        // [T][nb][XSEG]
 	float *part = dl + (size_t)T * nb * XSEG; // [T][nb][R]
+	// the thread's first block is requested before the inputs are staged,
+	// so the two memory waits overlap (unconditionally: a conditional load
+	// would be waited for at once)
+	RowBlock<TW> rb;
+	{
+		const int u = (int)threadIdx.x < nb * R ? (int)threadIdx.x : nb * R - 1;
+		const int r = u & (R - 1), b = u / R;
+		const uint8_t *blk = panel_slot(W, 0, 0, r0 + r, b, nb, panel_bytes(TW));
+		rb.load(blk, q6k_d_of(blk, r0 + r));
+	}
 	copy_in<4>(reinterpret_cast<const float4 *>(x), T * in / 4, [&](int q, float4 v) {
 		const int f = 4 * q, t = f / in, r = f - t * in;
 		*reinterpret_cast<float4 *>(xs + ((size_t)t * nb + r / QK) * XSEG + (r % QK)) = v;
@@ -1265,9 +1275,10 @@ __device__ __forceinline__ void dense_rows_tile(const uint8_t *__restrict__ W, c
 	__syncthreads();
 	for (int u = threadIdx.x; u < nb * R; u += blockDim.x) {
 		const int r = u & (R - 1), b = u / R;
-		const uint8_t *blk = panel_slot(W, 0, 0, r0 + r, b, nb, panel_bytes(TW));
-		RowBlock<TW> rb;
-		rb.load(blk, q6k_d_of(blk, r0 + r));
+		if (u != (int)threadIdx.x) {
+			const uint8_t *blk = panel_slot(W, 0, 0, r0 + r, b, nb, panel_bytes(TW));
+			rb.load(blk, q6k_d_of(blk, r0 + r));
+		}
 		for (int t = 0; t < T; t++)
 			part[((size_t)t * nb + b) * R + r] = rb.dot((dfloat *)(xs + ((size_t)t * nb + b) * XSEG));
 	}
