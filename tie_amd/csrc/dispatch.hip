@@ -169,23 +169,38 @@ __global__ __launch_bounds__(256) void combine_kernel(int T, int d, int k, const
 	if (c4 * 4 >= d)
 		return;
 	float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-	for (int j = 0; j < k; j++) {
-		if (topk_idx[t * k + j] < 0)
-			continue;
-		const float g = topk_w[t * k + j];
-		float4 v;
-		if (Y16) {
-			const uint2 b = reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(y) +
-									((size_t)t * k + j) * d)[c4];
-			v = make_float4(__builtin_bit_cast(float, b.x << 16), __builtin_bit_cast(float, b.x & 0xffff0000u),
-					__builtin_bit_cast(float, b.y << 16), __builtin_bit_cast(float, b.y & 0xffff0000u));
-		} else {
-			v = reinterpret_cast<const float4 *>(y + ((size_t)t * k + j) * d)[c4];
+	constexpr int CG = 8;
+	// 8 slots at a time: every row of the group loaded before the first
+	// FMA (one memory wait per group, not one per slot), then the FMAs in
+	// slot order
+	for (int j0 = 0; j0 < k; j0 += CG) {
+		float4 v[CG];
+		float g[CG];
+#pragma unroll
+		for (int q = 0; q < CG; q++) {
+			const int j = j0 + q;
+			const bool on = j < k && topk_idx[t * k + (j < k ? j : 0)] >= 0;
+			g[q] = on ? topk_w[t * k + j] : 0.0f;
+			// a slot without an expert reads slot j0's row and adds nothing
+			const size_t row = (size_t)t * k + (on ? j : j0);
+			if (Y16) {
+				const uint2 b = reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(y) + row * d)[c4];
+				v[q] = make_float4(__builtin_bit_cast(float, b.x << 16), __builtin_bit_cast(float, b.x & 0xffff0000u),
+						   __builtin_bit_cast(float, b.y << 16), __builtin_bit_cast(float, b.y & 0xffff0000u));
+			} else {
+				v[q] = reinterpret_cast<const float4 *>(y + row * d)[c4];
+			}
 		}
-		acc.x = __builtin_fmaf(g, v.x, acc.x);
-		acc.y = __builtin_fmaf(g, v.y, acc.y);
-		acc.z = __builtin_fmaf(g, v.z, acc.z);
-		acc.w = __builtin_fmaf(g, v.w, acc.w);
+#pragma unroll
+		for (int q = 0; q < CG; q++) {
+			const int j = j0 + q;
+			if (j < k && topk_idx[t * k + j] >= 0) {
+				acc.x = __builtin_fmaf(g[q], v[q].x, acc.x);
+				acc.y = __builtin_fmaf(g[q], v[q].y, acc.y);
+				acc.z = __builtin_fmaf(g[q], v[q].z, acc.z);
+				acc.w = __builtin_fmaf(g[q], v[q].w, acc.w);
+			}
+		}
 	}
 	if (res) {
 		const float4 h = reinterpret_cast<const float4 *>(res + (size_t)t * d)[c4];
