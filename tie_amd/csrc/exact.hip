@@ -81,6 +81,14 @@ template <int PC> __device__ __forceinline__ void step_fence(float (&a0)[PC][8],
 
 // Tuning knobs (compile-time): the most pairs one dot product serves at a
 // time, and an optional occupancy target for the quantised kernels.
+// steps whose input values a block dot of 3 or more pairs requests at once
+// (scalar loads; 2 lets the compiler merge them and issue them earlier)
+#ifndef TIE_Q4K_XS4
+#define TIE_Q4K_XS4 2
+#endif
+#ifndef TIE_Q6K_XS
+#define TIE_Q6K_XS 2
+#endif
 #ifndef TIE_EXACT_PCMAX
 #define TIE_EXACT_PCMAX 4
 #endif
@@ -195,7 +203,7 @@ __device__ __forceinline__ void block_dots(const Q4KStream &S, XP *const xs[PC],
 #pragma unroll
 		for (int l = 0; l < 8; l++)
 			a0[p][l] = a1[p][l] = 0.0f;
-	constexpr int XS = PC == 1 ? 4 : PC == 2 ? 2 : 1;
+	constexpr int XS = PC == 1 ? 4 : PC == 2 ? 2 : TIE_Q4K_XS4;
 	XP *xb[PC];
 #pragma unroll
 	for (int g = 0; g < 4; g++) {
@@ -303,7 +311,7 @@ __device__ __forceinline__ void block_dots(const Q6KStream &S, XP *const xs[PC],
 #pragma unroll
 		for (int l = 0; l < 8; l++)
 			a0[p][l] = a1[p][l] = 0.0f;
-	constexpr int XS = PC == 1 ? 2 : 1;
+	constexpr int XS = PC == 1 ? 2 : TIE_Q6K_XS;
 	auto sc = [&](int j) { return (float)(int8_t)((word(sc4, j >> 2) >> (8 * (j & 3))) & 0xffu); };
 	XP *xb[PC];
 #pragma unroll
