@@ -89,6 +89,15 @@ template <int PC> __device__ __forceinline__ void step_fence(float (&a0)[PC][8],
 #ifndef TIE_Q6K_XS
 #define TIE_Q6K_XS 2
 #endif
+#ifndef TIE_Q4K_XS1
+#define TIE_Q4K_XS1 4
+#endif
+#ifndef TIE_Q4K_XS2
+#define TIE_Q4K_XS2 2
+#endif
+#ifndef TIE_Q6K_XS1
+#define TIE_Q6K_XS1 2
+#endif
 #ifndef TIE_EXACT_PCMAX
 #define TIE_EXACT_PCMAX 4
 #endif
@@ -203,7 +212,7 @@ __device__ __forceinline__ void block_dots(const Q4KStream &S, XP *const xs[PC],
 #pragma unroll
 		for (int l = 0; l < 8; l++)
 			a0[p][l] = a1[p][l] = 0.0f;
-	constexpr int XS = PC == 1 ? 4 : PC == 2 ? 2 : TIE_Q4K_XS4;
+	constexpr int XS = PC == 1 ? TIE_Q4K_XS1 : PC == 2 ? TIE_Q4K_XS2 : TIE_Q4K_XS4;
 	XP *xb[PC];
 #pragma unroll
 	for (int g = 0; g < 4; g++) {
@@ -311,7 +320,7 @@ __device__ __forceinline__ void block_dots(const Q6KStream &S, XP *const xs[PC],
 #pragma unroll
 		for (int l = 0; l < 8; l++)
 			a0[p][l] = a1[p][l] = 0.0f;
-	constexpr int XS = PC == 1 ? 2 : TIE_Q6K_XS;
+	constexpr int XS = PC == 1 ? TIE_Q6K_XS1 : TIE_Q6K_XS;
 	auto sc = [&](int j) { return (float)(int8_t)((word(sc4, j >> 2) >> (8 * (j & 3))) & 0xffu); };
 	XP *xb[PC];
 #pragma unroll
