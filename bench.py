@@ -470,7 +470,8 @@ def main():
             wbytes = cfg["rows"] * synth.row_bytes(cfg["wtype"], cfg["in"])
             ncp = max(2, min(64, int(1.2e9 // wbytes)))
             log("timing dense %s: %d x %d, T=%d, %d matrices" % (name, cfg["rows"], cfg["in"], cfg["T"], ncp))
-            results[name] = run_dense(torch, tie_amd, cfg, steps, max(2, args.warmup // 4), ncp, flags)
+            fl = {"exact": tie_amd.PATH_EXACT, "mfma": tie_amd.PATH_MFMA}.get(cfg.get("path"), flags)
+            results[name] = run_dense(torch, tie_amd, cfg, steps, max(2, args.warmup // 4), ncp, fl)
             log(json.dumps({name: results[name]}))
             continue
         key = (cfg["d"], cfg["F"], cfg["E"], cfg["gu_type"], cfg["down_type"], cfg.get("zipf"), cfg.get("routing", 0),

@@ -383,14 +383,17 @@ def test_dense_mat_mat_mfma(wtype):
     default above the exact threshold): against the float64 model of its
     operands (x in f16, the f16 weights of q4k_f16 / q6k_f16) and against
     TIE's row kernels (the fp32 oracle); a token whose x leaves the f16 range
-    is computed exactly instead (bit-exact)."""
+    is computed exactly instead (bit-exact).  The small matrix makes the
+    launcher shrink the tiles (32 to 128 rows: every token count here runs
+    tiles of fewer rows than the kernel's maximum, with ragged last tiles)."""
     import torch
     rows, in_dim = 512, 1024
     rng = np.random.default_rng(60 + wtype)
     w = synth.expert_tensor(rng, wtype, 1, rows, in_dim)
     W16 = expert_weights(w, wtype, 0, rows, in_dim, True).astype(np.float64)
     M = tie_amd.Matrix(w, wtype, rows, in_dim)
-    for T, flags in ((65, tie_amd.PATH_AUTO), (200, tie_amd.PATH_MFMA), (7, tie_amd.PATH_MFMA)):
+    for T, flags in ((65, tie_amd.PATH_AUTO), (200, tie_amd.PATH_MFMA), (7, tie_amd.PATH_MFMA), (32, tie_amd.PATH_MFMA),
+                     (130, tie_amd.PATH_AUTO)):
         x = synth.make_input(61 + T, T, in_dim)
         x[3] *= np.float32(1e5)  # beyond f16: recomputed exactly
         print("dense mfma type=%d T=%d" % (wtype, T), flush=True)

@@ -160,6 +160,7 @@ struct MfmaArgs {
 	float *y;                // down out [pair][d] (BF16 weights: fp32)
 	uint16_t *y16;           // down out [pair][d] (quantised weights: bf16)
 	float *out32;            // down: fp32 rows [pair][rows] instead of y16 (dense matrices)
+	int mt_cap;              // pair rows per tile at most, below MT (0: MT; dense matrices at small T)
 	int32_t *tok_flag;       // [T] gate/up, h_f16: tokens whose h left the f16 range
 	int32_t *fix_list;       //     are appended here (once each) ...
 	int32_t *fix_count;      //     ... and counted
@@ -1202,6 +1203,7 @@ mfma_experts_kernel(MfmaArgs a)
 #ifdef TIE_MFMA_TRACE
 	const unsigned long long t_k0 = __builtin_readcyclecounter();
 #endif
+	const int mtc = a.mt_cap > 0 && a.mt_cap < MT ? a.mt_cap : MT;
 	int e, li, off, slab;
 	{
 		int *sc = reinterpret_cast<int *>(As); // [2 MF_THREADS / 64] scan | e, li, off
@@ -1211,7 +1213,7 @@ mfma_experts_kernel(MfmaArgs a)
 		for (int i = 0; i < 4; i++) {
 			const int ex = 4 * t + i;
 			c4[i] = ex < a.E ? a.cnt[ex] : 0;
-			n4[i] = (c4[i] + MT - 1) / MT;
+			n4[i] = (c4[i] + mtc - 1) / mtc;
 			csum += c4[i];
 			nsum += n4[i];
 		}
@@ -1252,7 +1254,7 @@ mfma_experts_kernel(MfmaArgs a)
 		__syncthreads(); // the stage buffers are free again
 	}
 	const int cnt = a.cnt[e];
-	const int ntl = (cnt + MT - 1) / MT;
+	const int ntl = (cnt + mtc - 1) / mtc;
 	const int rpt = (cnt + ntl - 1) / ntl;
 	const int m0 = li * rpt;
 	const int pbase = off + m0; // the tile's first row in the dense h rows
@@ -1563,6 +1565,7 @@ hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, con
 	    L.d % DN_COLS)
 		return hipErrorInvalidValue;
 	MfmaArgs a;
+	memset(&a, 0, sizeof a);
 	a.k = k;
 	a.E = L.E;
 	a.cnt = ws.bucket_cnt;
@@ -1690,7 +1693,14 @@ hipError_t launch_mfma_dense(const ExpertTensor &W, const float *x, int T, float
 	a.rows = W.rows;
 	a.in = W.in;
 	a.a16 = ws.xb;
-	const int tiles = (T + MFMA_MT_DN - 1) / MFMA_MT_DN + 1 + 8;
+	// tiles of fewer rows while the matrix's column slabs alone leave CUs
+	// idle (each tile then dequantises its slab again, from the cache)
+	const int slabs = W.rows / DN_COLS;
+	int mt = MFMA_MT_DN;
+	while (mt > 32 && slabs * ((T + mt - 1) / mt) < 256)
+		mt >>= 1;
+	a.mt_cap = mt;
+	const int tiles = (T + mt - 1) / mt + 1 + 8;
 	err = launch_one<true>(a, W.type, dim3(W.rows / DN_COLS, tiles), s);
 	if (err != hipSuccess)
 		return err;
