@@ -126,14 +126,16 @@ def test_dense_mat_mat(wtype):
 
 
 @pytest.mark.parametrize("wtype,rows,in_dim", [(synth.Q6_K, 33024, 2048), (synth.Q4_K, 33024, 2048),
-                                               (synth.Q6_K, 41024, 1536), (synth.Q4_K, 16448, 4096)])
+                                               (synth.Q6_K, 41024, 1536), (synth.Q4_K, 16448, 4096),
+                                               (synth.Q4_K, 4096, 16384)])
 def test_dense_stream(wtype, rows, in_dim):
     """One token through a tall matrix (the LM head's shape class): at
     rows x blocks / 64 >= 4096 units tie_hip_mat_mat streams units of 64 /
     nb rows through persistent waves (dense_stream_kernel), including block
     counts that do not divide 64 (nb = 6: ten rows per unit, four lanes
-    idle) and a last unit past the matrix's end; bit for bit with the
-    oracle."""
+    idle), the largest input (nb = 64: one row per unit, the row sum by
+    lane shuffles) and a last unit past the matrix's end; bit for bit with
+    the oracle."""
     import torch
     rng = np.random.default_rng(50 + wtype + in_dim)
     w = synth.expert_tensor(rng, wtype, 1, rows, in_dim)
