@@ -93,9 +93,6 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 #ifndef TIE_MFMA_F16
 #define TIE_MFMA_F16 1
 #endif
-#ifndef TIE_Q6_BFI
-#define TIE_Q6_BFI 1
-#endif
 // Tiles with at least this many 32-row M tiles run the cross-stage
 // software pipeline (fewer: each stage self-contained)
 #ifndef TIE_MFMA_PIPE_NMT
@@ -570,7 +567,6 @@ __device__ __forceinline__ void deq_step16_q6k(const BRegs<TIE_GGML_Q6_K> &b, co
 		const u32x2 ql = b.ql[j][Cfg<TIE_GGML_Q6_K>::APERM ? lh : 2 * (r & 1) + lh];
 		const u32x2 qh = b.qh[j][lh];
 		const int nsh = 4 * (r >> 1), hsh = 2 * r;
-#if TIE_Q6_BFI
 		// the code bytes' bits 6, 7 may hold other qh bits: the f16 pairs
 		// below keep 6 bits of each (kc.q6), so a rotate (bits 2 hsh.. of
 		// each qh byte to bits 4, 5) and one bit-field insert per word put
@@ -578,10 +574,6 @@ __device__ __forceinline__ void deq_step16_q6k(const BRegs<TIE_GGML_Q6_K> &b, co
 		auto qhs = [&](uint32_t v) { return __builtin_amdgcn_alignbit(v, v, (uint32_t)(hsh + 28) & 31u); };
 		const uint32_t lo = ((ql.x >> nsh) & 0x0f0f0f0fu) | (qhs(qh.x) & 0xf0f0f0f0u);
 		const uint32_t hi = ((ql.y >> nsh) & 0x0f0f0f0fu) | (qhs(qh.y) & 0xf0f0f0f0u);
-#else
-		const uint32_t lo = ((ql.x >> nsh) & 0x0f0f0f0fu) | (((qh.x >> hsh) & 0x03030303u) << 4);
-		const uint32_t hi = ((ql.y >> nsh) & 0x0f0f0f0fu) | (((qh.y >> hsh) & 0x03030303u) << 4);
-#endif
 		const int si = lh + 2 * r;
 		const uint32_t sw = si < 4 ? b.sc[j].x : b.sc[j].y;
 		const f16x2 D = splat16(f.d6[j] * (float)(int8_t)((sw >> (8 * (si & 3))) & 0xffu) * (float)(1 << F16_SHIFT));
