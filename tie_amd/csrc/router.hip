@@ -163,7 +163,7 @@ constexpr int RT_LDS = 2 * RT_BUF;              // double-buffered (48 KiB: thre
 #ifndef TIE_RT_IB
 #define TIE_RT_IB 16
 #endif
-constexpr int RT_IB = TIE_RT_IB;                // K steps whose operands are read ahead
+constexpr int RT_IB = TIE_RT_IB < RT_KC / 8 ? TIE_RT_IB : RT_KC / 8; // K steps whose operands are read ahead
 // the tiled kernel above this many tokens (below: router_mid)
 #ifndef TIE_RT_MIN_T
 #define TIE_RT_MIN_T 256
