@@ -108,6 +108,9 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // three weight stage buffers where they fit (1), or always two (0).  Off:
 // stage barriers wait 5-9% of a workgroup's cycles at T = 2048, and a third
 // buffer measured within +-2% (30B T = 2048, 235B T = 1024)
+#ifndef TIE_BF16_B3
+#define TIE_BF16_B3 1
+#endif
 #ifndef TIE_MFMA_BBUF3
 #define TIE_MFMA_BBUF3 0
 #endif
@@ -959,6 +962,37 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 #ifdef TIE_MFMA_TRACE
 		bw_total = bwait;
 #endif
+	} else if constexpr (TIE_BF16_B3) {
+		// weights two stages ahead: the loads of stage st + 2 (issued last,
+		// 8 vector loads per lane) stay in flight across the stage barrier,
+		// so each stage's weights have two stages of MFMAs to arrive in
+		BRegs<TYPE> b0, b1, b2;
+		load_b<TYPE>(bs, 0, h, b0);
+		dma_a<TYPE, DOWN, NMT, MTR>(as, 0, w, As);
+		if (nk > 1) {
+			load_b<TYPE>(bs, 1, h, b1);
+			stage_barrier_keep<8>();
+		} else {
+			stage_barrier();
+		}
+		auto body = [&](int st, BRegs<TYPE> &cur, BRegs<TYPE> &n2) {
+			if (st + 1 < nk)
+				dma_a<TYPE, DOWN, NMT, MTR>(as, st + 1, w, As + ((st + 1) & 1) * C::ABUF);
+			if (st + 2 < nk)
+				load_b<TYPE>(bs, st + 2, h, n2);
+			stage_mfma<TYPE, DOWN, NMT, MTR>(cur, st, As + (st & 1) * C::ABUF, acc);
+			if (st + 2 < nk)
+				stage_barrier_keep<8>();
+			else
+				stage_barrier();
+		};
+		for (int st = 0; st < nk; st += 3) {
+			body(st, b0, b2);
+			if (st + 1 < nk)
+				body(st + 1, b1, b0);
+			if (st + 2 < nk)
+				body(st + 2, b2, b1);
+		}
 	} else {
 		BRegs<TYPE> b0, b1;
 		load_b<TYPE>(bs, 0, h, b0);
