@@ -680,12 +680,12 @@ __device__ unsigned long long g_mfma_trace[2][8];
 
 // The same, but the N youngest vector loads (the next-but-one weight
 // stage's DMA, issued last) may stay in flight: loads complete in order, so
-// everything older has landed.  N < 16 (the gfx9 encoding: vmcnt in bits
-// 3:0, expcnt and lgkmcnt 0).
+// everything older has landed.  N < 64 (expcnt and lgkmcnt 0).
 template <int N> __device__ __forceinline__ void stage_barrier_keep()
 {
-	static_assert(N >= 0 && N < 16, "vmcnt field");
-	__builtin_amdgcn_s_waitcnt(N);
+	static_assert(N >= 0 && N < 64, "vmcnt field");
+	// gfx9 s_waitcnt: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8
+	__builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14));
 	__builtin_amdgcn_s_barrier();
 }
 
