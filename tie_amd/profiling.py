@@ -35,6 +35,7 @@ _NAMES = (
     ("tie::route_group_kernel", "route_group"),
     ("tie::dispatch_kernel", "dispatch"),
     ("tie::combine_kernel", "combine"),
+    ("tie::combine16_kernel", "combine"),
     ("tie::rmsnorm_kernel", "rmsnorm"),
     ("tie::route_bucket_kernel", "router"),
     ("tie::bucket_plan_kernel", "dispatch"),
