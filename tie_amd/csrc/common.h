@@ -302,6 +302,56 @@ __device__ __forceinline__ float tie_swiglu(float g, float u, const float *__res
 	float s = __builtin_fmaf(frac, y2 - y1, y1);
 	return s * u;
 }
+// One token's combine over 8 columns (c8: 8-column group) of bf16 expert
+// outputs: out[t][c] = [res[t][c] +] sum_j fma(g_j, y[t*k+j][c], .) in slot
+// order (model_qwen3.c:459-467, then the residual add of
+// apply_residual_f32_f32_avx2, math_avx2.c:731-751).  Slots of 8 loaded
+// (16 bytes each) before their FMAs: one memory wait per 8 slots.
+__device__ __forceinline__ void combine16_cols(int t, int c8, int d, int k, const float *__restrict__ topk_w,
+					       const int32_t *__restrict__ topk_idx, const uint16_t *__restrict__ y,
+					       const float *res, float *out)
+{
+	float acc[8];
+#pragma unroll
+	for (int i = 0; i < 8; i++)
+		acc[i] = 0.0f;
+	constexpr int CG = 8;
+	for (int j0 = 0; j0 < k; j0 += CG) {
+		uint4 v[CG];
+		float g[CG];
+#pragma unroll
+		for (int q = 0; q < CG; q++) {
+			const int j = j0 + q;
+			const bool on = j < k && topk_idx[t * k + (j < k ? j : 0)] >= 0;
+			g[q] = on ? topk_w[t * k + j] : 0.0f;
+			// a slot without an expert reads slot j0's row and adds nothing
+			const size_t row = (size_t)t * k + (on ? j : j0);
+			v[q] = reinterpret_cast<const uint4 *>(y + row * d)[c8];
+		}
+#pragma unroll
+		for (int q = 0; q < CG; q++) {
+			const int j = j0 + q;
+			if (j < k && topk_idx[t * k + j] >= 0) {
+				const uint32_t w[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
+#pragma unroll
+				for (int i = 0; i < 4; i++) {
+					acc[2 * i] = __builtin_fmaf(g[q], __builtin_bit_cast(float, w[i] << 16), acc[2 * i]);
+					acc[2 * i + 1] = __builtin_fmaf(g[q], __builtin_bit_cast(float, w[i] & 0xffff0000u), acc[2 * i + 1]);
+				}
+			}
+		}
+	}
+	float4 *o = reinterpret_cast<float4 *>(out + (size_t)t * d) + 2 * c8;
+	float4 a = make_float4(acc[0], acc[1], acc[2], acc[3]), b = make_float4(acc[4], acc[5], acc[6], acc[7]);
+	if (res) {
+		const float4 *h = reinterpret_cast<const float4 *>(res + (size_t)t * d) + 2 * c8;
+		const float4 h0 = h[0], h1 = h[1];
+		a = make_float4(h0.x + a.x, h0.y + a.y, h0.z + a.z, h0.w + a.w);
+		b = make_float4(h1.x + b.x, h1.y + b.y, h1.z + b.z, h1.w + b.w);
+	}
+	o[0] = a;
+	o[1] = b;
+}
 #endif
 
 } // namespace tie

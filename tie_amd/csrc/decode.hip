@@ -867,15 +867,18 @@ __global__ __launch_bounds__(DEC_MAX_THREADS) void recompute_kernel(DecodeArgs a
 // fma(g_j, y_j[c], .) in slot order, y bf16), and, in workgroups of their
 // own, the exact recomputation of the listed ones (usually none) -- one
 // launch instead of two.  Workgroups [0, ncomb): token b / cpt, 1024
-// columns each; [ncomb, ncomb + nfix): recomputation.
+// (w8: 2048) columns each; [ncomb, ncomb + nfix): recomputation.
 struct CombineFixArgs {
-	int ncomb, cpt, nfix;
+	int ncomb, cpt, nfix, w8;
 	const float *topk_w;
 	const int32_t *topk_idx;
 	const uint16_t *y;
 	const int32_t *skip;
 };
 constexpr int CF_THREADS = 256;
+#ifndef TIE_CF_W8
+#define TIE_CF_W8 1
+#endif
 template <int TG, int TU, int TD>
 __global__ __launch_bounds__(CF_THREADS) void combine_fix_kernel(DecodeArgs a, CombineFixArgs c)
 {
@@ -886,6 +889,14 @@ __global__ __launch_bounds__(CF_THREADS) void combine_fix_kernel(DecodeArgs a, C
 		return;
 	}
 	const int t = b / c.cpt;
+	if (c.w8) {
+		// 8 columns per thread, 16-byte loads of y (d a multiple of 8)
+		const int c8 = (b - t * c.cpt) * CF_THREADS + threadIdx.x;
+		if (c.skip[t] || c8 * 8 >= a.d)
+			return;
+		combine16_cols(t, c8, a.d, a.k, c.topk_w, c.topk_idx, c.y, a.res, a.out);
+		return;
+	}
 	const int c4 = (b - t * c.cpt) * CF_THREADS + threadIdx.x; // float4 column
 	if (c.skip[t] || c4 * 4 >= a.d)
 		return;
@@ -1050,7 +1061,8 @@ hipError_t launch_combine_fix(const Layer &L, const float *x, int k, const float
 	a.list = list;
 	a.count = count;
 	CombineFixArgs c;
-	c.cpt = (L.d / 4 + CF_THREADS - 1) / CF_THREADS;
+	c.w8 = TIE_CF_W8 && L.d % 8 == 0;
+	c.cpt = (L.d / (c.w8 ? 8 : 4) + CF_THREADS - 1) / CF_THREADS;
 	c.ncomb = T * c.cpt;
 	c.nfix = T < 64 ? T : 64;
 	c.topk_w = topk_w;

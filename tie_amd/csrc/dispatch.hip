@@ -223,45 +223,7 @@ __global__ __launch_bounds__(256) void combine16_kernel(int T, int d, int k, con
 	const int c8 = blockIdx.x * blockDim.x + threadIdx.x; // 8-column group
 	if (c8 * 8 >= d)
 		return;
-	float acc[8];
-#pragma unroll
-	for (int i = 0; i < 8; i++)
-		acc[i] = 0.0f;
-	constexpr int CG = 8;
-	for (int j0 = 0; j0 < k; j0 += CG) {
-		uint4 v[CG];
-		float g[CG];
-#pragma unroll
-		for (int q = 0; q < CG; q++) {
-			const int j = j0 + q;
-			const bool on = j < k && topk_idx[t * k + (j < k ? j : 0)] >= 0;
-			g[q] = on ? topk_w[t * k + j] : 0.0f;
-			const size_t row = (size_t)t * k + (on ? j : j0);
-			v[q] = reinterpret_cast<const uint4 *>(y + row * d)[c8];
-		}
-#pragma unroll
-		for (int q = 0; q < CG; q++) {
-			const int j = j0 + q;
-			if (j < k && topk_idx[t * k + j] >= 0) {
-				const uint32_t w[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
-#pragma unroll
-				for (int i = 0; i < 4; i++) {
-					acc[2 * i] = __builtin_fmaf(g[q], __builtin_bit_cast(float, w[i] << 16), acc[2 * i]);
-					acc[2 * i + 1] = __builtin_fmaf(g[q], __builtin_bit_cast(float, w[i] & 0xffff0000u), acc[2 * i + 1]);
-				}
-			}
-		}
-	}
-	float4 *o = reinterpret_cast<float4 *>(out + (size_t)t * d) + 2 * c8;
-	float4 a = make_float4(acc[0], acc[1], acc[2], acc[3]), b = make_float4(acc[4], acc[5], acc[6], acc[7]);
-	if (res) {
-		const float4 *h = reinterpret_cast<const float4 *>(res + (size_t)t * d) + 2 * c8;
-		const float4 h0 = h[0], h1 = h[1];
-		a = make_float4(h0.x + a.x, h0.y + a.y, h0.z + a.z, h0.w + a.w);
-		b = make_float4(h1.x + b.x, h1.y + b.y, h1.z + b.z, h1.w + b.w);
-	}
-	o[0] = a;
-	o[1] = b;
+	combine16_cols(t, c8, d, k, topk_w, topk_idx, y, res, out);
 }
 
 hipError_t launch_combine(int T, int d, int k, const float *topk_w, const int32_t *topk_idx, const float *y,
