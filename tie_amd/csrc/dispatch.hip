@@ -80,10 +80,13 @@ hipError_t launch_dispatch(const Layer &L, int T, int k, const int32_t *topk_idx
 // token when E <= 128, else a wave per token), then group_pairs.  Saves
 // the separate selection launch.
 constexpr int RG_MAX_PAIRS = 4096;
+#ifndef TIE_RG_GMAX
+#define TIE_RG_GMAX 32
+#endif
 constexpr int RG_LDS_LOGITS = 8192; // T * E up to this: logits staged in LDS
-// G8: 8 tokens per wave (E <= 128 and more tokens than waves), else one
+// G > 0: G lanes per token (E <= 128 and more tokens than waves), else one
 // wave per token; separate instances keep each one's registers small
-template <bool G8, bool SIG>
+template <int G, bool SIG>
 __global__ __launch_bounds__(DSP_THREADS) void route_group_kernel(const float *__restrict__ logits, int T, int E,
 								  int k, int32_t *__restrict__ topk_idx,
 								  float *__restrict__ topk_w,
@@ -120,12 +123,12 @@ __global__ __launch_bounds__(DSP_THREADS) void route_group_kernel(const float *_
 		lg = slg;
 	}
 	__syncthreads();
-	if constexpr (G8) {
-		for (int t0 = 0; t0 < T; t0 += DSP_THREADS / 8) {
-			const int t = t0 + tid / 8;
+	if constexpr (G > 0) {
+		for (int t0 = 0; t0 < T; t0 += DSP_THREADS / G) {
+			const int t = t0 + tid / G;
 			if (t < T)
-				topk_softmax_group8<SIG>(lg + (size_t)t * E, E, k, gsel + (tid / 8) * MAX_K, etab,
-							 sidx + t * k, topk_w + (size_t)t * k, pbias);
+				topk_softmax_group<SIG, G>(lg + (size_t)t * E, E, k, gsel + (tid / G) * MAX_K, etab,
+							   sidx + t * k, topk_w + (size_t)t * k, pbias);
 		}
 	} else {
 		for (int t = tid >> 6; t < T; t += DSP_THREADS / 64)
@@ -141,9 +144,17 @@ __global__ __launch_bounds__(DSP_THREADS) void route_group_kernel(const float *_
 
 hipError_t launch_route_group(const Layer &L, int T, int k, const float *logits, Workspace &ws, hipStream_t s)
 {
-	const bool g8 = L.E <= 128 && T > DSP_THREADS / 64, sig = L.routing == ROUTE_SIGMOID;
-	auto kern = g8 ? (sig ? route_group_kernel<true, true> : route_group_kernel<true, false>)
-		       : route_group_kernel<false, false>;
+	// lanes per token: the most that still run every token in one pass of
+	// the workgroup (more lanes, shorter per-lane chains)
+	const bool grp = L.E <= 128 && T > DSP_THREADS / 64, sig = L.routing == ROUTE_SIGMOID;
+	int G = TIE_RG_GMAX;
+	while (G > 8 && T * G > DSP_THREADS)
+		G >>= 1;
+	auto kern = route_group_kernel<0, false>;
+	if (grp)
+		kern = G == 32 ? (sig ? route_group_kernel<32, true> : route_group_kernel<32, false>)
+		       : G == 16 ? (sig ? route_group_kernel<16, true> : route_group_kernel<16, false>)
+				 : (sig ? route_group_kernel<8, true> : route_group_kernel<8, false>);
 	hipLaunchKernelGGL(kern, dim3(1), dim3(DSP_THREADS), 0, s, logits, T, L.E, k, ws.topk_idx, ws.topk_w, ws.offsets,
 			   ws.pairs, ws.active, L.routing, L.pbias);
 	return hipGetLastError();

@@ -412,19 +412,21 @@ __device__ __forceinline__ void topk_softmax(const float *lg, int E, int k, cons
 		topk_softmax_wave<16>(lg, E, k, etab, out_idx, out_w, routing, pbias);
 }
 
-// The same selection for 8 tokens per wave: 8 lanes per token (E <= 128,
-// 16 entries per lane, entry e = 8q + lane % 8 in register q), so a wave
-// runs the rounds of 8 tokens at once (a round is a chain of dependent
-// vector operations; one token per wave leaves the SIMD mostly idle).
-// Identical order of selection (the same keys: value descending, index
-// ascending; NaN and -inf never qualify) and identical weight arithmetic
-// for both routings.  The argmax of a round runs over DPP lane moves
-// inside the 8 lanes.  `sel`: LDS scratch of MAX_K floats for the token.
-template <bool SIG>
-__device__ __forceinline__ void topk_softmax_group8(const float *lg, int E, int k, float *sel, const uint64_t *etab,
-						    int32_t *out_idx, float *out_w, const float *pbias)
+// The same selection for 64 / G tokens per wave: G lanes per token (G in
+// {8, 16, 32}; E <= 128, 128 / G entries per lane, entry e = G q + lane % G
+// in register q), so a wave runs the rounds of several tokens at once (a
+// round is a chain of dependent vector operations; one token per wave
+// leaves the SIMD mostly idle).  Identical order of selection (the same
+// keys: value descending, index ascending; NaN and -inf never qualify) and
+// identical weight arithmetic for both routings.  The argmax of a round runs
+// over lane moves inside the G lanes.  `sel`: LDS scratch of MAX_K floats
+// for the token.
+template <bool SIG, int G>
+__device__ __forceinline__ void topk_softmax_group(const float *lg, int E, int k, float *sel, const uint64_t *etab,
+						   int32_t *out_idx, float *out_w, const float *pbias)
 {
-	constexpr int G = 8, V = 16;
+	static_assert(G == 8 || G == 16 || G == 32, "8, 16 or 32 lanes per token");
+	constexpr int V = 128 / G;
 	const int lig = threadIdx.x & (G - 1);
 	constexpr bool sig = SIG;
 	uint32_t key[V];
@@ -482,6 +484,22 @@ __device__ __forceinline__ void topk_softmax_group8(const float *lg, int E, int 
 			bk = ok;
 			be = oe;
 		}
+		if constexpr (G >= 16) {
+			ok = (uint32_t)dppi<DPP_MIRROR>((int)bk);
+			oe = dppi<DPP_MIRROR>(be);
+			if (better(ok, oe, bk, be)) {
+				bk = ok;
+				be = oe;
+			}
+		}
+		if constexpr (G >= 32) {
+			ok = (uint32_t)__shfl_xor((int)bk, 16);
+			oe = __shfl_xor(be, 16);
+			if (better(ok, oe, bk, be)) {
+				bk = ok;
+				be = oe;
+			}
+		}
 		const bool found = bk > KEY_NINF;
 		if (found && (be & (G - 1)) == lig) {
 			// the winner's lane records the slot and removes the entry
@@ -514,7 +532,7 @@ __device__ __forceinline__ void topk_softmax_group8(const float *lg, int E, int 
 	for (int j = 1; j < k; j++)
 		if (sel[j] > mx)
 			mx = sel[j];
-	// e_j on lane j % 8, then the serial sum
+	// e_j on lane j % G, then the serial sum
 	float ev[MAX_K / G];
 #pragma unroll
 	for (int q = 0; q < MAX_K / G; q++) {
