@@ -101,6 +101,9 @@ template <int PC> __device__ __forceinline__ void step_fence(float (&a0)[PC][8],
 #ifndef TIE_EXACT_PCMAX
 #define TIE_EXACT_PCMAX 4
 #endif
+#ifndef TIE_DOWN_PM2
+#define TIE_DOWN_PM2 1
+#endif
 #ifdef TIE_EXACT_WPE
 #define EXACT_OCC __attribute__((amdgpu_waves_per_eu(TIE_EXACT_WPE)))
 #else
@@ -1054,15 +1057,25 @@ hipError_t launch_exact_block(const Layer &L, const float *x, int T, int k, cons
 			if (fused) {
 				g.pg_cap = clamp_pg(PART_FLOATS / (nb * 64));
 				const size_t lds = sizeof(float) * (size_t)g.pg_cap * nb * 64;
-				const void *fn = L.down.type == TIE_GGML_Q4_K ? (const void *)exact_down_kernel<TIE_GGML_Q4_K, true, PM>
-									       : (const void *)exact_down_kernel<TIE_GGML_Q6_K, true, PM>;
-				err = set_lds_limit(fn, lds);
-				if (err != hipSuccess)
-					return err;
-				block.x = 64 * pick_waves(fn, lds, n_wg, nb);
-				err = L.down.type == TIE_GGML_Q4_K
-					      ? launch_q(exact_down_kernel<TIE_GGML_Q4_K, true, PM>, grid, block, lds, 0, s, g)
-					      : launch_q(exact_down_kernel<TIE_GGML_Q6_K, true, PM>, grid, block, lds, 0, s, g);
+				// pairs dequantised together: 2 where experts average at
+				// most 4 pairs (92 instead of 125 registers: 5 waves per
+				// SIMD instead of 4), else PM
+				auto run = [&](auto pmc) -> hipError_t {
+					constexpr int P = decltype(pmc)::value;
+					const void *fn = L.down.type == TIE_GGML_Q4_K ? (const void *)exact_down_kernel<TIE_GGML_Q4_K, true, P>
+										       : (const void *)exact_down_kernel<TIE_GGML_Q6_K, true, P>;
+					hipError_t e2 = set_lds_limit(fn, lds);
+					if (e2 != hipSuccess)
+						return e2;
+					block.x = 64 * pick_waves(fn, lds, n_wg, nb);
+					return L.down.type == TIE_GGML_Q4_K
+						       ? launch_q(exact_down_kernel<TIE_GGML_Q4_K, true, P>, grid, block, lds, 0, s, g)
+						       : launch_q(exact_down_kernel<TIE_GGML_Q6_K, true, P>, grid, block, lds, 0, s, g);
+				};
+				if (TIE_DOWN_PM2 && (long)T * k <= 4L * L.E)
+					err = run(std::integral_constant<int, 2>{});
+				else
+					err = run(std::integral_constant<int, PM>{});
 			} else {
 				g.pg_cap = clamp_pg(PART_FLOATS / (F + nb * 64));
 				const size_t lds = sizeof(float) * (size_t)g.pg_cap * (F + nb * 64);
