@@ -75,24 +75,27 @@ __global__ __launch_bounds__(RS_THREADS) void router_small_kernel(const float *_
 }
 
 // ------------------------------------------------------------ router_mid
-// RS_TOK < T (up to a few hundred tokens): one workgroup per (expert, 32
+// RS_TOK < T (up to a few hundred tokens): one workgroup per (expert, TOK
 // tokens).  The expert row is staged in LDS (read as a broadcast); thread
 // (t, l) streams x[t][8i + l] from global memory (L2-resident) with many
-// loads in flight and runs the lane-l chain of token t.
-constexpr int RM_TOK = 32;
-constexpr int RM_THREADS = RM_TOK * 8;
-
-// U: inputs per lane and batch (d a multiple of 8 U)
-template <int U>
-__global__ __launch_bounds__(RM_THREADS) void router_mid_kernel(const float *__restrict__ x,
-								const float *__restrict__ W,
-								const float *__restrict__ bias, int T, int d, int E,
-								float *__restrict__ logits, ZeroArgs z)
+// loads in flight and runs the lane-l chain of token t.  TOK tokens per
+// workgroup: 16 up to 32 tokens (twice the workgroups, over more CUs),
+// else 32.
+// U: inputs per lane and batch (d a multiple of 8 U).  LM: the row staged
+// lane-major, its weights read a batch ahead in 16-byte reads (263
+// registers: one wave per SIMD, so only while one round of workgroups
+// covers the grid: up to 64 tokens)
+template <int U, int TOK, bool LM>
+__global__ __launch_bounds__(TOK * 8) void router_mid_kernel(const float *__restrict__ x,
+							     const float *__restrict__ W,
+							     const float *__restrict__ bias, int T, int d, int E,
+							     float *__restrict__ logits, ZeroArgs z)
 {
 	zero_words(z);
 	extern __shared__ float ws[]; // W row [d]
 	const int e = blockIdx.x;
-	const int t0 = blockIdx.y * RM_TOK;
+	constexpr int RM_THREADS = TOK * 8;
+	const int t0 = blockIdx.y * TOK;
 	const int tid = threadIdx.x;
 	const int t = t0 + (tid >> 3), l = tid & 7;
 	const bool live = t < T;
@@ -105,31 +108,72 @@ __global__ __launch_bounds__(RM_THREADS) void router_mid_kernel(const float *__r
 #pragma unroll
 	for (int u = 0; u < U; u++)
 		xa[u] = xt[8 * u];
-	const float4 *W4 = reinterpret_cast<const float4 *>(W + (size_t)e * d);
-	for (int i = tid; i < (d >> 2); i += RM_THREADS)
-		reinterpret_cast<float4 *>(ws)[i] = W4[i];
-	__syncthreads();
-	const float *wl = ws + l;
 	float acc = 0.0f;
-	for (int bt = 0; bt < nbt; bt += 2) {
-		if (bt + 1 < nbt) {
+	if constexpr (LM) {
+		// the row lane-major (lane l's weights 8i + l contiguous): one 16-byte
+		// LDS read brings 4 steps, and the next batch's weights are read while
+		// the current batch is multiplied
+		typedef float f4 __attribute__((ext_vector_type(4)));
+		stage_lane_major(ws, W + (size_t)e * d, d);
+		__syncthreads();
+		const f4 *wl = reinterpret_cast<const f4 *>(ws + l * lane_major_stride(d));
+		constexpr int U4 = U / 4;
+		f4 wa[U4], wb[U4];
+#pragma unroll
+		for (int q = 0; q < U4; q++)
+			wa[q] = wl[q];
+		for (int bt = 0; bt < nbt; bt += 2) {
+			if (bt + 1 < nbt) {
+#pragma unroll
+				for (int u = 0; u < U; u++)
+					xb[u] = xt[8 * U * (bt + 1) + 8 * u];
+#pragma unroll
+				for (int q = 0; q < U4; q++)
+					wb[q] = wl[U4 * (bt + 1) + q];
+			}
 #pragma unroll
 			for (int u = 0; u < U; u++)
-				xb[u] = xt[8 * U * (bt + 1) + 8 * u];
-		}
+				acc = __builtin_fmaf(xa[u], wa[u / 4][u % 4], acc);
+			if (bt + 1 >= nbt)
+				break;
+			if (bt + 2 < nbt) {
 #pragma unroll
-		for (int u = 0; u < U; u++)
-			acc = __builtin_fmaf(xa[u], wl[8 * U * bt + 8 * u], acc);
-		if (bt + 1 >= nbt)
-			break;
-		if (bt + 2 < nbt) {
+				for (int u = 0; u < U; u++)
+					xa[u] = xt[8 * U * (bt + 2) + 8 * u];
+#pragma unroll
+				for (int q = 0; q < U4; q++)
+					wa[q] = wl[U4 * (bt + 2) + q];
+			}
 #pragma unroll
 			for (int u = 0; u < U; u++)
-				xa[u] = xt[8 * U * (bt + 2) + 8 * u];
-		}
+				acc = __builtin_fmaf(xb[u], wb[u / 4][u % 4], acc);
+	}
+	} else {
+		const float4 *W4 = reinterpret_cast<const float4 *>(W + (size_t)e * d);
+		for (int i = tid; i < (d >> 2); i += RM_THREADS)
+			reinterpret_cast<float4 *>(ws)[i] = W4[i];
+		__syncthreads();
+		const float *wl = ws + l;
+		for (int bt = 0; bt < nbt; bt += 2) {
+			if (bt + 1 < nbt) {
 #pragma unroll
-		for (int u = 0; u < U; u++)
-			acc = __builtin_fmaf(xb[u], wl[8 * U * (bt + 1) + 8 * u], acc);
+				for (int u = 0; u < U; u++)
+					xb[u] = xt[8 * U * (bt + 1) + 8 * u];
+			}
+#pragma unroll
+			for (int u = 0; u < U; u++)
+				acc = __builtin_fmaf(xa[u], wl[8 * U * bt + 8 * u], acc);
+			if (bt + 1 >= nbt)
+				break;
+			if (bt + 2 < nbt) {
+#pragma unroll
+				for (int u = 0; u < U; u++)
+					xa[u] = xt[8 * U * (bt + 2) + 8 * u];
+			}
+#pragma unroll
+			for (int u = 0; u < U; u++)
+				acc = __builtin_fmaf(xb[u], wl[8 * U * (bt + 1) + 8 * u], acc);
+	}
 	}
 	const float r = hsum8_lanes(acc);
 	if (l == 0 && live)
@@ -349,8 +393,14 @@ hipError_t launch_router_logits(const Layer &L, const float *x, int T, float *lo
 				   RT_LDS, s, x, L.routerT, L.bias, T, d, E, logits, z);
 		return hipGetLastError();
 	}
-	hipLaunchKernelGGL(d % 512 == 0 ? router_mid_kernel<64> : router_mid_kernel<32>, dim3(E, (T + RM_TOK - 1) / RM_TOK), dim3(RM_THREADS),
-			   sizeof(float) * (size_t)d, s, x, L.router, L.bias, T, d, E, logits, z);
+	const bool u64 = d % 512 == 0;
+	const int tok = T <= 32 ? 16 : 32;
+	const bool lm = T <= 64;
+	auto kern = lm ? (tok == 16 ? (u64 ? router_mid_kernel<64, 16, true> : router_mid_kernel<32, 16, true>)
+				    : (u64 ? router_mid_kernel<64, 32, true> : router_mid_kernel<32, 32, true>))
+		       : (u64 ? router_mid_kernel<64, 32, false> : router_mid_kernel<32, 32, false>);
+	hipLaunchKernelGGL(kern, dim3(E, (T + tok - 1) / tok), dim3(tok * 8),
+			   sizeof(float) * (size_t)(lm ? lane_major_floats(d) : d), s, x, L.router, L.bias, T, d, E, logits, z);
 	return hipGetLastError();
 }
 
