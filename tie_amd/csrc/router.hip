@@ -40,11 +40,16 @@ __device__ __forceinline__ void zero_words(const ZeroArgs &z)
 }
 
 // ------------------------------------------------------------ router_small
-// T <= RS_TOK: one workgroup per expert row; the row and the tokens are
+// One token (RS_TOK at most): one workgroup per expert row; the row and the tokens are
 // staged in LDS with coalesced 16-byte loads and thread (t, l) runs the
 // lane-l chain of token t.  Spreads the 1 MiB router matrix over E
 // workgroups, which matters most at T = 1.
 constexpr int RS_TOK = 4;
+// router_small only for one token: from 2 tokens on router_mid is faster
+// (T=4: 11 -> 8.2 us)
+#ifndef TIE_RS_MAX_T
+#define TIE_RS_MAX_T 1
+#endif
 constexpr int RS_THREADS = 256;
 
 __global__ __launch_bounds__(RS_THREADS) void router_small_kernel(const float *__restrict__ x,
@@ -372,7 +377,7 @@ __global__ __launch_bounds__(RW_THREADS) void router_topk_kernel(const float *__
 hipError_t launch_router_logits(const Layer &L, const float *x, int T, float *logits, hipStream_t s, ZeroArgs z)
 {
 	const int d = L.d, E = L.E;
-	if (T <= RS_TOK && sizeof(float) * (size_t)(8 * (d / 8 + 4)) * (1 + RS_TOK) <= 160 * 1024) {
+	if (T <= TIE_RS_MAX_T && sizeof(float) * (size_t)(8 * (d / 8 + 4)) * (1 + RS_TOK) <= 160 * 1024) {
 		const size_t lds = sizeof(float) * (size_t)(8 * (d / 8 + 4)) * (1 + RS_TOK);
 		hipLaunchKernelGGL(router_small_kernel, dim3(E), dim3(RS_THREADS), lds, s, x, L.router, L.bias, T, d, E,
 				   logits, z);
