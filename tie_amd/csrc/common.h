@@ -324,8 +324,9 @@ __device__ __forceinline__ void combine16_cols(int t, int c8, int d, int k, cons
 			const int j = j0 + q;
 			const bool on = j < k && topk_idx[t * k + (j < k ? j : 0)] >= 0;
 			g[q] = on ? topk_w[t * k + j] : 0.0f;
-			// a slot without an expert reads slot j0's row and adds nothing
-			const size_t row = (size_t)t * k + (on ? j : j0);
+			// every slot's row is loaded (its address does not wait for
+			// topk_idx); a slot without an expert adds nothing
+			const size_t row = (size_t)t * k + (j < k ? j : j0);
 			v[q] = reinterpret_cast<const uint4 *>(y + row * d)[c8];
 		}
 #pragma unroll

@@ -192,8 +192,9 @@ __global__ __launch_bounds__(256) void combine_kernel(int T, int d, int k, const
 			const int j = j0 + q;
 			const bool on = j < k && topk_idx[t * k + (j < k ? j : 0)] >= 0;
 			g[q] = on ? topk_w[t * k + j] : 0.0f;
-			// a slot without an expert reads slot j0's row and adds nothing
-			const size_t row = (size_t)t * k + (on ? j : j0);
+			// every slot's row is loaded (its address does not wait for
+			// topk_idx); a slot without an expert adds nothing
+			const size_t row = (size_t)t * k + (j < k ? j : j0);
 			if (Y16) {
 				const uint2 b = reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(y) + row * d)[c4];
 				v[q] = make_float4(__builtin_bit_cast(float, b.x << 16), __builtin_bit_cast(float, b.x & 0xffff0000u),
