@@ -255,7 +255,7 @@ def run_config(torch, tie_amd, wl, T, k, steps, warmup, flags, cfg=None, graph=F
     U_avg = float(np.mean([U[s % nL] for s in range(steps)]))
     gu_b, dn_b = expert_bytes(cfg)
     pairs = T * k
-    y_bytes = 2 if cfg["down_type"] != synth.BF16 else 4  # the MFMA path's y: bf16 with quantised weights
+    y_bytes = 4  # the MFMA path's y: fp32
     h_bytes = 2 if cfg["down_type"] != synth.BF16 else 4  # h: f16 (quantised down) or bf16 hi + lo
     kern_bytes = {
         "router": E * d * 4 + T * d * 4,
@@ -306,6 +306,17 @@ def workload_name(synth, name, cfg):
         synth.TYPE_NAMES[cfg["down_type"]])
 
 
+def compute_dtype(m, cfg):
+    """Operand type of the workload's expert products: f16 (Q4_K / Q6_K
+    weights on the matrix cores, fp32 accumulation), bf16 (BF16 weights on
+    the matrix cores, activations split into two bf16 parts), or f32 (TIE's
+    exact fp32 arithmetic)."""
+    from tie_amd import synth
+    if any("mfma" in k for k in m["kernels"]):
+        return "bf16" if cfg.get("gu_type", cfg.get("wtype")) == synth.BF16 else "f16"
+    return "f32"
+
+
 def roofline(m, config):
     """Roofline object for the dominant (longest) kernel of a measurement of one
     workload; traffic is the copy-scaled HBM bytes per launch measured for that
@@ -315,6 +326,8 @@ def roofline(m, config):
     # candidates)
     name, kd = max(((n, v) for n, v in m["kernels"].items() if v.get("alg_bytes")), key=lambda kv: kv[1]["avg_us"])
     traffic = None
+    # the dominant kernel's event-timed duration must fit in a step
+    kernel_le_step = kd["avg_us"] <= 1e3 * m["ms"]
     tfile = os.path.join(ROOT, "profiles", "traffic.json")
     if os.path.exists(tfile):
         with open(tfile) as f:
@@ -328,11 +341,11 @@ def roofline(m, config):
         return {"kernel": name, "bound": "mfma", "achieved": kd["TFLOPs"], "peak": BF16_PEAK_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(kd["TFLOPs"] / BF16_PEAK_TFLOPS, 4), "traffic": traffic,
                 "alg_flops_per_launch": kd["alg_flops"], "alg_bytes_per_launch": kd["alg_bytes"],
-                "avg_us": kd["avg_us"]}
+                "avg_us": kd["avg_us"], "kernel_le_step": kernel_le_step}
     achieved = kd["GBps"]
     return {"kernel": name, "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-            "alg_bytes_per_launch": kd["alg_bytes"], "avg_us": kd["avg_us"]}
+            "alg_bytes_per_launch": kd["alg_bytes"], "avg_us": kd["avg_us"], "kernel_le_step": kernel_le_step}
 
 
 # ---------------------------------------------------------------- CPU baseline
@@ -408,6 +421,7 @@ def cpu_baseline(cfg, layer, x_gpu, gpu, budget_s):
     parity = {"tokens": int(len(rows)), "routing_mismatch": int((differ & ~near).sum()),
               "near_ties": int(near.sum()), "near_tie_mismatch": int((differ & near).sum()),
               "max_abs": float(err.max()), "max_ref": float(np.abs(ro).max()),
+              "max_abs_over_max_ref": float(err.max() / max(float(np.abs(ro).max()), 1e-30)),
               "rel_l2": float(np.linalg.norm(err) / max(np.linalg.norm(ro), 1e-30)),
               "against": "reference" if use_ref else "port"}
     base = {"value": round(n * len(rows) / el, 2), "unit": "tokens/s", "cores": threads,
@@ -510,6 +524,7 @@ def main():
     for name in names[1:]:
         r = results[name]
         extra[name] = {"tokens_per_s": round(r["tokens_per_s"], 1), "ms_per_step": round(r["ms"], 4),
+                       "dtype": compute_dtype(r, synth.CONFIGS[name]),
                        "ms_per_step_eager": round(r["ms_eager"], 4),
                        "block_GBps": round(r["block_GBps"], 1), "block_TFLOPs": round(r["block_TFLOPs"], 3),
                        "roofline": roofline(r, name), "cpu_baseline": cpu.get(name), "parity": parity.get(name),
@@ -527,7 +542,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16" if any("mfma" in k for k in m["kernels"]) else "f32",
+        "dtype": compute_dtype(m, cfg),
         "data": "synthetic (seeded GGUF-layout Q4_K/Q6_K blocks, N(0,1) inputs; %d weight layers cycled)" % m[
             "layers"],
         "config": {"workload": workload_name(synth, main_name, cfg), "T": cfg["T"], "path": args.path},
@@ -539,6 +554,14 @@ def main():
         "kernels": m["kernels"],
         "extra": extra,
     }
+    # the two figures BASELINE's metric is quoted on: the 30B block at T=1
+    # (HBM GB/s of its algorithmic bytes) and at T=2048 (MFMA TFLOP/s)
+    if "30b_t1" in results:
+        line["t1_block_GBps"] = round(results["30b_t1"]["block_GBps"], 1)
+        line["t1_block_hbm_frac"] = round(results["30b_t1"]["block_GBps"] / HBM_PEAK_GBS, 4)
+    if "30b_t2048" in results:
+        line["t2048_block_TFLOPs"] = round(results["30b_t2048"]["block_TFLOPs"], 2)
+        line["t2048_block_mfma_frac"] = round(results["30b_t2048"]["block_TFLOPs"] / BF16_PEAK_TFLOPS, 4)
     print(json.dumps(line), flush=True)
 
 

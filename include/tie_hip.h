@@ -249,12 +249,14 @@ void tie_hip_set_exact_max_tokens(int t);
  * 0 disarms).  Host-side fault injection for error-path tests. */
 void tie_hip_debug_fail_alloc(int n);
 
-/* Per-kernel timing: while enabled, every kernel the library launches is
- * bracketed by HIP events recorded on its launch stream.  Enabling (or
- * disabling) clears what was collected. */
+/* Per-kernel timing: while enabled, every kernel of a named section (router,
+ * dispatch, expert kernels, combine, ...) is launched with a start and stop
+ * event bound to its own dispatch (hipExtLaunchKernel): a section's time is
+ * the sum of its kernels' execution times.  Enabling (or disabling) clears
+ * what was collected. */
 int tie_hip_profile_enable(int on);
 
-/* Sum of event-timed durations and launch count per kernel name since the
+/* Sum of event-timed durations and section count per kernel name since the
  * last tie_hip_profile_enable(1); names come back comma-separated in
  * `names`.  Synchronises the device.  Returns the number of names. */
 int tie_hip_profile_read(char *names, size_t names_cap, double *total_ms, int *launches, int max_kernels);

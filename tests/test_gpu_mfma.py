@@ -9,7 +9,7 @@ ways:
   * against a float64 model of the same arithmetic (the kernels' operands
     emulated exactly: Q4_K / Q6_K weights dequantised in packed f16 with
     their factor 256, x rounded to f16, h rounded to an 11-bit significand
-    (f16 scaled by the layer's power of two), y rounded to bf16; BF16
+    (f16 scaled by the layer's power of two), y stored in fp32; BF16
     weights with activations split into two bf16 parts; TIE's table SwiGLU)
     -- this pins the kernels' tiling, operand layouts (including the K
     permutation), pipelines and epilogues;
@@ -29,10 +29,12 @@ from tie_amd import synth
 
 pytestmark = pytest.mark.gpu
 
-# rel. L2 bounds: quantised weights against the fp32 oracle (measured
-# 1.71e-3 .. 1.81e-3 on these inputs), and against the float64 model of the
-# kernels' own operands (measured 2.4e-5 .. 1.26e-4)
-ORACLE_RL2 = 4e-3
+# Quantised weights against the fp32 oracle: relative L2 and max |err| /
+# max |ref| both <= 1e-3 (the f16 operands' rounding: about 6e-4 of either,
+# from the weights, x and h; y is kept in fp32), and rel. L2 against the
+# float64 model of the kernels' own operands
+ORACLE_RL2 = 1e-3
+ORACLE_MAXREL = 1e-3
 MODEL_RL2 = 3e-4
 # BF16 weights (activations split into two bf16 parts): the north star's max
 # |err| bound (values O(1)), and rel. L2 (measured 4.4e-6 .. 4.6e-6)
@@ -167,9 +169,7 @@ def model(layer, x, idx, w, tab):
             h = g.astype(np.float64)
         else:
             h = bf16(g).astype(np.float64)
-        y = h @ Wd.T.astype(np.float64)
-        if h16:
-            y = bf16(y.astype(np.float32)).astype(np.float64)  # stored as bf16 for the combine
+        y = (h @ Wd.T.astype(np.float64)).astype(np.float32).astype(np.float64)  # stored as fp32 for the combine
         np.add.at(out, t, w[t, j].astype(np.float64)[:, None] * y)
     return out
 
@@ -183,6 +183,15 @@ def report(tag, out, ro):
     e = rel_l2(out, ro)
     mx = float(np.abs(out - ro).max())
     print("PARITY %s rel_l2=%.3e max_abs=%.3e max_ref=%.3e" % (tag, e, mx, float(np.abs(ro).max())), flush=True)
+    return e, mx
+
+
+def check_oracle(tag, out, ro):
+    """The 16-bit operand bound against the fp32 oracle: rel. L2 and
+    max |err| / max |ref| <= 1e-3."""
+    e, mx = report(tag, out, ro)
+    assert e <= ORACLE_RL2, (tag, e)
+    assert mx <= ORACLE_MAXREL * float(np.abs(ro).max()), (tag, mx)
     return e, mx
 
 
@@ -224,9 +233,8 @@ def test_quantised_against_model_and_oracle(shape, types):
     m = model(layer, x, ri, rw, bind.silu_table())
     e_model = rel_l2(out, m)
     print("rel L2 vs kernel model %.3e" % e_model, flush=True)
-    e_oracle, _ = report("q_%d_%d_%d_%d_%d_%d" % (d, F, E, k, T, types[0]), out, ro)
     assert e_model <= MODEL_RL2
-    assert e_oracle <= ORACLE_RL2
+    check_oracle("q_%d_%d_%d_%d_%d_%d" % (d, F, E, k, T, types[0]), out, ro)
 
 
 @pytest.mark.parametrize("T,zipf", [(48, None), (200, 1.2)])
@@ -251,18 +259,28 @@ def test_bf16_weights_split_activations(T, zipf):
 
 
 @pytest.mark.parametrize("cfg", ["30b_t2048", "235b_t1024"])
-def test_full_prefill_all_tokens(cfg):
+@pytest.mark.parametrize("scaled", [False, True])
+def test_full_prefill_all_tokens(cfg, scaled):
     """The headline prefill shapes at full size: every token's selection
-    bit-exact, every output row within the 16-bit bound."""
+    bit-exact, every output row within the 16-bit bound.  scaled: the
+    weights' fp16 super-block scales times 2^-6 (gate/up) and 2^-8 (down),
+    which brings the block's outputs from O(1e6) to O(1) (RMS about 0.5,
+    weights near a real model's ~N(0, 0.02)) and |g| near SiLU's curved
+    range; the relative bounds hold there too."""
     c = synth.CONFIGS[cfg]
     layer = synth_layer(c["seed"], c["d"], c["F"], c["E"], c["gu_type"], c["down_type"], None)
+    if scaled:
+        import copy
+        base, layer = layer, copy.copy(layer)
+        layer.gate = scaled_scales(base.gate, base.gate_type, 2.0 ** -6)
+        layer.up = scaled_scales(base.up, base.up_type, 2.0 ** -6)
+        layer.down = scaled_scales(base.down, base.down_type, 2.0 ** -8)
     x = synth.make_input(c["seed"], c["T"], c["d"])
     out, idx, w = run_mfma(layer, x, c["k"])
     ro, ri, rw = bind.moe_block(layer, x, c["k"])
     check_routing(idx, w, ri, rw)
-    e, _ = report(cfg, out, ro)
     assert np.isfinite(out).all()
-    assert e <= ORACLE_RL2
+    check_oracle(cfg + ("_o1" if scaled else ""), out, ro)
 
 
 def test_full_bf16_zipf_t512():
@@ -306,8 +324,7 @@ def test_small_activations():
     out, idx, w = run_mfma(layer, x, 4)
     ro, ri, rw = bind.moe_block(layer, x, 4)
     check_routing(idx, w, ri, rw)
-    e, _ = report("small_h", out, ro)
-    assert e <= ORACLE_RL2
+    check_oracle("small_h", out, ro)
 
 
 def test_out_of_range_tokens_recomputed_exactly():
@@ -344,8 +361,7 @@ def test_lfm2_prefill_routing_exact():
     out, idx, w = run_mfma(layer, x, c["k"])
     ro, ri, rw = bind.moe_block(layer, x, c["k"])
     check_routing(idx, w, ri, rw)
-    e, _ = report("lfm2_T300", out, ro)
-    assert e <= ORACLE_RL2
+    check_oracle("lfm2_T300", out, ro)
 
 
 def test_out_of_range_residual_in_place():
@@ -407,9 +423,8 @@ def test_dense_mat_mat_mfma(wtype):
         rest = np.setdiff1d(np.arange(T), [3])
         ref = f16(x[rest]).astype(np.float64) @ W16.T
         e_model = rel_l2(got[rest], ref)
-        e_oracle, _ = report("dense_mfma t%d T=%d" % (wtype, T), got[rest], ro[rest])
         assert e_model <= MODEL_RL2, e_model
-        assert e_oracle <= ORACLE_RL2, e_oracle
+        check_oracle("dense_mfma t%d T=%d" % (wtype, T), got[rest], ro[rest])
     M.close()
 
 

@@ -77,7 +77,7 @@ static uint8_t *g_scratch = nullptr;
 
 // ---------------------------------------------------------------- profiling
 struct ProfRec {
-	int name;
+	int name, section;
 	hipEvent_t a, b;
 };
 static bool g_prof = false;
@@ -99,7 +99,9 @@ static hipEvent_t prof_event()
 	return e;
 }
 
-void prof_begin(const char *name, hipStream_t s)
+static int g_prof_section = 0;
+
+void prof_begin(const char *name, hipStream_t)
 {
 	if (!g_prof)
 		return;
@@ -111,20 +113,30 @@ void prof_begin(const char *name, hipStream_t s)
 		id = (int)g_prof_names.size();
 		g_prof_names.push_back(name);
 	}
-	ProfRec r{id, prof_event(), prof_event()};
-	if (r.a)
-		(void)hipEventRecord(r.a, s);
-	g_prof_recs.push_back(r);
-	g_prof_open = (int)g_prof_recs.size() - 1;
+	g_prof_open = id;
+	g_prof_section++;
 }
 
-void prof_end(hipStream_t s)
+bool prof_kernel_events(hipEvent_t *start, hipEvent_t *stop)
 {
 	if (!g_prof || g_prof_open < 0)
-		return;
-	ProfRec &r = g_prof_recs[g_prof_open];
-	if (r.b)
-		(void)hipEventRecord(r.b, s);
+		return false;
+	ProfRec r{g_prof_open, g_prof_section, prof_event(), prof_event()};
+	if (!r.a || !r.b) {
+		if (r.a)
+			g_prof_pool.push_back(r.a);
+		if (r.b)
+			g_prof_pool.push_back(r.b);
+		return false;
+	}
+	g_prof_recs.push_back(r);
+	*start = r.a;
+	*stop = r.b;
+	return true;
+}
+
+void prof_end(hipStream_t)
+{
 	g_prof_open = -1;
 }
 
@@ -474,13 +486,13 @@ static int forward(tie_hip_layer *layer, const float *x, int T, int k, float *ou
 			// left the f16 range (listed by the kernels above; usually
 			// none), which are recomputed exactly in the same launch, from
 			// res as it was (res may be out)
-			HIP_TRY(launch_combine_fix(L, x, k, g.silu, ws.topk_idx, ws.topk_w, reinterpret_cast<const uint16_t *>(ws.y),
+			HIP_TRY(launch_combine_fix(L, x, k, g.silu, ws.topk_idx, ws.topk_w, ws.y,
 						   out, res, ws.tok_flag, ws.fix_list, ws.fix_count, T, s));
 		} else {
 			// the same in two launches (the recomputation's LDS would cost
 			// the combine occupancy); the combine skips the listed tokens
 			prof_begin("combine", s);
-			HIP_TRY(launch_combine(T, L.d, k, ws.topk_w, ws.topk_idx, ws.y, out, s, res, L.down.type != TIE_GGML_BF16,
+			HIP_TRY(launch_combine(T, L.d, k, ws.topk_w, ws.topk_idx, ws.y, out, s, res,
 					       mfma_f16_operands(L) ? ws.tok_flag : nullptr));
 			prof_end(s);
 			if (mfma_f16_operands(L))
@@ -1141,13 +1153,17 @@ extern "C" int tie_hip_profile_read(char *names, size_t names_cap, double *total
 		launches[i] = 0;
 		csv += (i ? "," : "") + g_prof_names[i];
 	}
+	// a section's kernels are summed; launches counts sections
+	int last_section = -1;
 	for (auto &r : g_prof_recs) {
-		if (r.name >= n || !r.a || !r.b)
+		if (r.name >= n)
 			continue;
 		float ms = 0.0f;
 		if (hipEventElapsedTime(&ms, r.a, r.b) == hipSuccess) {
 			total_ms[r.name] += ms;
-			launches[r.name] += 1;
+			if (r.section != last_section)
+				launches[r.name] += 1;
+			last_section = r.section;
 		}
 	}
 	if (names && names_cap) {

@@ -1,6 +1,7 @@
 // common.h -- shared definitions of the gfx950 MoE block kernels.
 #pragma once
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <stdint.h>
 #include <stddef.h>
 
@@ -150,12 +151,12 @@ bool recompute_supported(const Layer &L, int k);
 hipError_t launch_recompute(const Layer &L, const float *x, int k, const float *silu, const int32_t *topk_idx,
 			    const float *topk_w, float *out, const float *res, const int32_t *list,
 			    const int32_t *count, int T, hipStream_t s);
-// The matrix-core path's combine (bf16 y; tokens with skip[t] set left
+// The matrix-core path's combine (fp32 y; tokens with skip[t] set left
 // alone) and the exact recomputation of the listed tokens in one launch,
 // when combine_fix_preferred
 bool combine_fix_preferred(const Layer &L);
 hipError_t launch_combine_fix(const Layer &L, const float *x, int k, const float *silu, const int32_t *topk_idx,
-			      const float *topk_w, const uint16_t *y, float *out, const float *res,
+			      const float *topk_w, const float *y, float *out, const float *res,
 			      const int32_t *skip, const int32_t *list, const int32_t *count, int T, hipStream_t s);
 
 hipError_t launch_decode(const Layer &L, const float *x, int k, const float *silu, const float *logits,
@@ -188,9 +189,8 @@ bool mfma_dense_supported(const ExpertTensor &W, int T);
 hipError_t launch_mfma_dense(const ExpertTensor &W, const float *x, int T, float *out, Workspace &ws, hipStream_t s);
 int dense_groups(int T);
 // res (optional): out = res + combine (the residual add after the block)
-// y16: y holds bf16 values (the MFMA path's down output with quantised weights)
 hipError_t launch_combine(int T, int d, int k, const float *topk_w, const int32_t *topk_idx, const float *y,
-			  float *out, hipStream_t s, const float *res = nullptr, bool y16 = false,
+			  float *out, hipStream_t s, const float *res = nullptr,
 			  const int32_t *skip = nullptr);
 // TIE's RMSNorm of each row of x into out; tab/nbits: the host RSQRTSS table
 hipError_t launch_rmsnorm(const float *x, const float *w, float eps, int T, int d, float *out, const uint32_t *tab,
@@ -201,10 +201,26 @@ hipError_t launch_repack(const ExpertTensor &dst, const uint8_t *src, int E, int
 // kernel: the attribute call runs only when a launch needs more)
 hipError_t ensure_lds_limit(const void *fn, size_t bytes);
 
-// Per-kernel timing (tie_hip_profile_enable): HIP events recorded on the
-// launch stream around each kernel; no-ops while profiling is off.
+// Per-kernel timing (tie_hip_profile_enable): prof_begin / prof_end bracket
+// a named section of launches; every kernel launched through tie_launch
+// inside a section carries a start and a stop event bound to its own
+// dispatch (hipExtLaunchKernel), so a section's time is the sum of its
+// kernels' execution times, without the gaps that separate event records
+// between launches would add.  No-ops while profiling is off.
 void prof_begin(const char *name, hipStream_t s);
 void prof_end(hipStream_t s);
+// the event pair of the next launch in an open section (false: none)
+bool prof_kernel_events(hipEvent_t *start, hipEvent_t *stop);
+
+template <typename K, typename... A>
+inline void tie_launch(K kern, dim3 grid, dim3 block, size_t lds, hipStream_t s, A... args)
+{
+	hipEvent_t e0, e1;
+	if (prof_kernel_events(&e0, &e1))
+		hipExtLaunchKernelGGL(kern, grid, block, (uint32_t)lds, s, e0, e1, 0u, args...);
+	else
+		hipLaunchKernelGGL(kern, grid, block, lds, s, args...);
+}
 
 // ---------------------------------------------------------------- device helpers
 #if defined(__HIPCC__)
@@ -302,22 +318,19 @@ __device__ __forceinline__ float tie_swiglu(float g, float u, const float *__res
 	float s = __builtin_fmaf(frac, y2 - y1, y1);
 	return s * u;
 }
-// One token's combine over 8 columns (c8: 8-column group) of bf16 expert
+// One token's combine over 8 columns (c8: 8-column group) of fp32 expert
 // outputs: out[t][c] = [res[t][c] +] sum_j fma(g_j, y[t*k+j][c], .) in slot
 // order (model_qwen3.c:459-467, then the residual add of
 // apply_residual_f32_f32_avx2, math_avx2.c:731-751).  Slots of 8 loaded
-// (16 bytes each) before their FMAs: one memory wait per 8 slots.
-__device__ __forceinline__ void combine16_cols(int t, int c8, int d, int k, const float *__restrict__ topk_w,
-					       const int32_t *__restrict__ topk_idx, const uint16_t *__restrict__ y,
-					       const float *res, float *out)
+// (two 16-byte loads each) before their FMAs: one memory wait per 8 slots.
+__device__ __forceinline__ void combine8_cols(int t, int c8, int d, int k, const float *__restrict__ topk_w,
+					      const int32_t *__restrict__ topk_idx, const float *__restrict__ y,
+					      const float *res, float *out)
 {
-	float acc[8];
-#pragma unroll
-	for (int i = 0; i < 8; i++)
-		acc[i] = 0.0f;
+	float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
 	constexpr int CG = 8;
 	for (int j0 = 0; j0 < k; j0 += CG) {
-		uint4 v[CG];
+		float4 v[CG][2];
 		float g[CG];
 #pragma unroll
 		for (int q = 0; q < CG; q++) {
@@ -327,23 +340,26 @@ __device__ __forceinline__ void combine16_cols(int t, int c8, int d, int k, cons
 			// every slot's row is loaded (its address does not wait for
 			// topk_idx); a slot without an expert adds nothing
 			const size_t row = (size_t)t * k + (j < k ? j : j0);
-			v[q] = reinterpret_cast<const uint4 *>(y + row * d)[c8];
+			const float4 *yr = reinterpret_cast<const float4 *>(y + row * d) + 2 * c8;
+			v[q][0] = yr[0];
+			v[q][1] = yr[1];
 		}
 #pragma unroll
 		for (int q = 0; q < CG; q++) {
 			const int j = j0 + q;
 			if (j < k && topk_idx[t * k + j] >= 0) {
-				const uint32_t w[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
-#pragma unroll
-				for (int i = 0; i < 4; i++) {
-					acc[2 * i] = __builtin_fmaf(g[q], __builtin_bit_cast(float, w[i] << 16), acc[2 * i]);
-					acc[2 * i + 1] = __builtin_fmaf(g[q], __builtin_bit_cast(float, w[i] & 0xffff0000u), acc[2 * i + 1]);
-				}
+				a.x = __builtin_fmaf(g[q], v[q][0].x, a.x);
+				a.y = __builtin_fmaf(g[q], v[q][0].y, a.y);
+				a.z = __builtin_fmaf(g[q], v[q][0].z, a.z);
+				a.w = __builtin_fmaf(g[q], v[q][0].w, a.w);
+				b.x = __builtin_fmaf(g[q], v[q][1].x, b.x);
+				b.y = __builtin_fmaf(g[q], v[q][1].y, b.y);
+				b.z = __builtin_fmaf(g[q], v[q][1].z, b.z);
+				b.w = __builtin_fmaf(g[q], v[q][1].w, b.w);
 			}
 		}
 	}
 	float4 *o = reinterpret_cast<float4 *>(out + (size_t)t * d) + 2 * c8;
-	float4 a = make_float4(acc[0], acc[1], acc[2], acc[3]), b = make_float4(acc[4], acc[5], acc[6], acc[7]);
 	if (res) {
 		const float4 *h = reinterpret_cast<const float4 *>(res + (size_t)t * d) + 2 * c8;
 		const float4 h0 = h[0], h1 = h[1];

@@ -872,7 +872,7 @@ struct CombineFixArgs {
 	int ncomb, cpt, nfix, w8;
 	const float *topk_w;
 	const int32_t *topk_idx;
-	const uint16_t *y;
+	const float *y;
 	const int32_t *skip;
 };
 constexpr int CF_THREADS = 256;
@@ -894,7 +894,7 @@ __global__ __launch_bounds__(CF_THREADS) void combine_fix_kernel(DecodeArgs a, C
 		const int c8 = (b - t * c.cpt) * CF_THREADS + threadIdx.x;
 		if (c.skip[t] || c8 * 8 >= a.d)
 			return;
-		combine16_cols(t, c8, a.d, a.k, c.topk_w, c.topk_idx, c.y, a.res, a.out);
+		combine8_cols(t, c8, a.d, a.k, c.topk_w, c.topk_idx, c.y, a.res, a.out);
 		return;
 	}
 	const int c4 = (b - t * c.cpt) * CF_THREADS + threadIdx.x; // float4 column
@@ -906,11 +906,11 @@ __global__ __launch_bounds__(CF_THREADS) void combine_fix_kernel(DecodeArgs a, C
 		if (c.topk_idx[t * k + j] < 0)
 			continue;
 		const float g = c.topk_w[t * k + j];
-		const uint2 w = reinterpret_cast<const uint2 *>(c.y + ((size_t)t * k + j) * a.d)[c4];
-		acc.x = __builtin_fmaf(g, __builtin_bit_cast(float, w.x << 16), acc.x);
-		acc.y = __builtin_fmaf(g, __builtin_bit_cast(float, w.x & 0xffff0000u), acc.y);
-		acc.z = __builtin_fmaf(g, __builtin_bit_cast(float, w.y << 16), acc.z);
-		acc.w = __builtin_fmaf(g, __builtin_bit_cast(float, w.y & 0xffff0000u), acc.w);
+		const float4 v = reinterpret_cast<const float4 *>(c.y + ((size_t)t * k + j) * a.d)[c4];
+		acc.x = __builtin_fmaf(g, v.x, acc.x);
+		acc.y = __builtin_fmaf(g, v.y, acc.y);
+		acc.z = __builtin_fmaf(g, v.z, acc.z);
+		acc.w = __builtin_fmaf(g, v.w, acc.w);
 	}
 	if (a.res) {
 		const float4 h = reinterpret_cast<const float4 *>(a.res + (size_t)t * a.d)[c4];
@@ -968,7 +968,7 @@ static hipError_t dec_launch(K kern, dim3 grid, dim3 block, size_t lds, hipStrea
 	hipError_t err = ensure_lds_limit((const void *)kern, lds);
 	if (err != hipSuccess)
 		return err;
-	hipLaunchKernelGGL(kern, grid, block, lds, s, args...);
+	tie_launch(kern, grid, block, lds, s, args...);
 	return hipGetLastError();
 }
 
@@ -1032,10 +1032,10 @@ bool combine_fix_preferred(const Layer &L)
 	return recompute_lds(L) <= 24 * 1024;
 }
 
-// The combine of the matrix-core path's bf16 y (tokens listed in skip left
+// The combine of the matrix-core path's y (tokens listed in skip left
 // alone) and the exact recomputation of the listed tokens, in one launch.
 hipError_t launch_combine_fix(const Layer &L, const float *x, int k, const float *silu, const int32_t *topk_idx,
-			      const float *topk_w, const uint16_t *y, float *out, const float *res,
+			      const float *topk_w, const float *y, float *out, const float *res,
 			      const int32_t *skip, const int32_t *list, const int32_t *count, int T, hipStream_t s)
 {
 	if (T == 0)

@@ -70,7 +70,7 @@ hipError_t launch_dispatch(const Layer &L, int T, int k, const int32_t *topk_idx
 			return err;
 		attr = true;
 	}
-	hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(DSP_THREADS), lds, s, topk_idx, npairs, L.E, ws.offsets,
+	tie_launch(dispatch_kernel, dim3(1), dim3(DSP_THREADS), lds, s, topk_idx, npairs, L.E, ws.offsets,
 			   ws.pairs, ws.active);
 	return hipGetLastError();
 }
@@ -155,19 +155,17 @@ hipError_t launch_route_group(const Layer &L, int T, int k, const float *logits,
 		kern = G == 32 ? (sig ? route_group_kernel<32, true> : route_group_kernel<32, false>)
 		       : G == 16 ? (sig ? route_group_kernel<16, true> : route_group_kernel<16, false>)
 				 : (sig ? route_group_kernel<8, true> : route_group_kernel<8, false>);
-	hipLaunchKernelGGL(kern, dim3(1), dim3(DSP_THREADS), 0, s, logits, T, L.E, k, ws.topk_idx, ws.topk_w, ws.offsets,
+	tie_launch(kern, dim3(1), dim3(DSP_THREADS), 0, s, logits, T, L.E, k, ws.topk_idx, ws.topk_w, ws.offsets,
 			   ws.pairs, ws.active, L.routing, L.pbias);
 	return hipGetLastError();
 }
 
-// out[t][c] = fma(g_j, y[t*k+j][c], acc) for j = 0..k-1 (model_qwen3.c:459-467),
-// y fp32 or (Y16, the MFMA path with quantised weights) bf16;
+// out[t][c] = fma(g_j, y[t*k+j][c], acc) for j = 0..k-1 (model_qwen3.c:459-467);
 // with res: out[t][c] = res[t][c] + acc, the residual add that follows the
 // block (dispatch_apply_residual, model_qwen3.c:491, apply_residual_f32_f32_avx2
 // math_avx2.c:731-751).  res may be out (the hidden state updated in place).
 // Tokens with skip[t] != 0 (skip optional) are left alone: the exact
 // recomputation writes their rows afterwards, from res as it was.
-template <bool Y16>
 __global__ __launch_bounds__(256) void combine_kernel(int T, int d, int k, const float *__restrict__ topk_w,
 						      const int32_t *__restrict__ topk_idx,
 						      const float *__restrict__ y, const float *res, float *out,
@@ -195,13 +193,7 @@ __global__ __launch_bounds__(256) void combine_kernel(int T, int d, int k, const
 			// every slot's row is loaded (its address does not wait for
 			// topk_idx); a slot without an expert adds nothing
 			const size_t row = (size_t)t * k + (j < k ? j : j0);
-			if (Y16) {
-				const uint2 b = reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(y) + row * d)[c4];
-				v[q] = make_float4(__builtin_bit_cast(float, b.x << 16), __builtin_bit_cast(float, b.x & 0xffff0000u),
-						   __builtin_bit_cast(float, b.y << 16), __builtin_bit_cast(float, b.y & 0xffff0000u));
-			} else {
-				v[q] = reinterpret_cast<const float4 *>(y + row * d)[c4];
-			}
+			v[q] = reinterpret_cast<const float4 *>(y + row * d)[c4];
 		}
 #pragma unroll
 		for (int q = 0; q < CG; q++) {
@@ -224,33 +216,14 @@ __global__ __launch_bounds__(256) void combine_kernel(int T, int d, int k, const
 	reinterpret_cast<float4 *>(out + (size_t)t * d)[c4] = acc;
 }
 
-// The same for bf16 y with 8 columns per thread (16-byte loads of y).
-__global__ __launch_bounds__(256) void combine16_kernel(int T, int d, int k, const float *__restrict__ topk_w,
-							const int32_t *__restrict__ topk_idx, const uint16_t *__restrict__ y,
-							const float *res, float *out, const int32_t *__restrict__ skip)
-{
-	const int t = blockIdx.y;
-	if (skip && skip[t])
-		return;
-	const int c8 = blockIdx.x * blockDim.x + threadIdx.x; // 8-column group
-	if (c8 * 8 >= d)
-		return;
-	combine16_cols(t, c8, d, k, topk_w, topk_idx, y, res, out);
-}
-
 hipError_t launch_combine(int T, int d, int k, const float *topk_w, const int32_t *topk_idx, const float *y,
-			  float *out, hipStream_t s, const float *res, bool y16, const int32_t *skip)
+			  float *out, hipStream_t s, const float *res, const int32_t *skip)
 {
 	if (T == 0)
 		return hipSuccess;
-	if (y16 && d % 8 == 0) {
-		hipLaunchKernelGGL(combine16_kernel, dim3((d / 8 + 255) / 256, T), dim3(256), 0, s, T, d, k, topk_w, topk_idx,
-				   reinterpret_cast<const uint16_t *>(y), res, out, skip);
-		return hipGetLastError();
-	}
 	const int n4 = d / 4;
-	hipLaunchKernelGGL(y16 ? combine_kernel<true> : combine_kernel<false>, dim3((n4 + 255) / 256, T), dim3(256), 0, s,
-			   T, d, k, topk_w, topk_idx, y, res, out, skip);
+	tie_launch(combine_kernel, dim3((n4 + 255) / 256, T), dim3(256), 0, s, T, d, k, topk_w, topk_idx, y, res,
+			   out, skip);
 	return hipGetLastError();
 }
 

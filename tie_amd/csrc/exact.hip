@@ -837,7 +837,7 @@ static hipError_t launch_q(K kernel, dim3 grid, dim3 block, size_t lds, size_t s
 	hipError_t err = set_lds_limit((const void *)kernel, lds + static_lds);
 	if (err != hipSuccess)
 		return err;
-	hipLaunchKernelGGL(kernel, grid, block, lds, s, a);
+	tie_launch(kernel, grid, block, lds, s, a);
 	return hipGetLastError();
 }
 
@@ -1007,7 +1007,7 @@ hipError_t launch_exact_block(const Layer &L, const float *x, int T, int k, cons
 		if (same && L.gate.type == TIE_GGML_BF16) {
 			g.rows = L.F;
 			g.in = L.d;
-			hipLaunchKernelGGL(exact_gu_bf16_kernel, dim3(L.F / PANEL_ROWS, max_active, 2), dim3(BF_THREADS), 0,
+			tie_launch(exact_gu_bf16_kernel, dim3(L.F / PANEL_ROWS, max_active, 2), dim3(BF_THREADS), 0,
 					   s, g);
 			err = hipGetLastError();
 		} else if (same) {
@@ -1024,7 +1024,7 @@ hipError_t launch_exact_block(const Layer &L, const float *x, int T, int k, cons
 				if (t.type == TIE_GGML_BF16) {
 					h.rows = t.rows;
 					h.in = t.in;
-					hipLaunchKernelGGL(exact_gu_bf16_kernel, dim3(t.rows / PANEL_ROWS, max_active, 1),
+					tie_launch(exact_gu_bf16_kernel, dim3(t.rows / PANEL_ROWS, max_active, 1),
 							   dim3(BF_THREADS), 0, s, h);
 					err = hipGetLastError();
 				} else {
@@ -1140,7 +1140,7 @@ hipError_t launch_dense(const ExpertTensor &W, const float *x, int T, float *out
 	if (T == 0)
 		return hipSuccess;
 	const int G = dense_groups(T);
-	hipLaunchKernelGGL(dense_groups_kernel, dim3((T + 1 + 255) / 256 > (G + 1 + 255) / 256 ? (T + 1 + 255) / 256
+	tie_launch(dense_groups_kernel, dim3((T + 1 + 255) / 256 > (G + 1 + 255) / 256 ? (T + 1 + 255) / 256
 											  : (G + 1 + 255) / 256),
 			   dim3(256), 0, s, T, G, ws.offsets, ws.pairs, ws.active);
 	hipError_t err = hipGetLastError();
@@ -1161,7 +1161,7 @@ hipError_t launch_dense(const ExpertTensor &W, const float *x, int T, float *out
 	a.rows = W.rows;
 	a.in = W.in;
 	if (W.type == TIE_GGML_BF16) {
-		hipLaunchKernelGGL(exact_gu_bf16_kernel, dim3(W.rows / PANEL_ROWS, G, 1), dim3(BF_THREADS), 0, s, a);
+		tie_launch(exact_gu_bf16_kernel, dim3(W.rows / PANEL_ROWS, G, 1), dim3(BF_THREADS), 0, s, a);
 		return hipGetLastError();
 	}
 	return launch_gu_q(W.type, false, 1, W.rows, W.in, G, a, s);

@@ -55,12 +55,13 @@
 // h leaves the f16 range (|v| >= 65504, or not finite) is
 // listed by route_bucket_kernel / the gate/up epilogue and recomputed afterwards
 // in TIE's exact arithmetic (decode.hip), which overwrites its output row.
-// The expert outputs y are stored as bf16.  With BF16 expert
+// The expert outputs y are stored in fp32 (rounding them to bf16 would
+// add 2^-9 relative per element, the largest error term of the path).  With BF16 expert
 // weights (exact in bf16) the activations are split into a bf16 high part
 // and a bf16 remainder, stored as two bf16 planes (x by route_bucket_kernel, h
 // by the gate/up epilogue), two MFMAs per product; this keeps the products
 // to ~16 mantissa bits; that path is HBM-bound, so the extra MFMA work is
-// hidden, and its y stays fp32.
+// hidden.
 #include "common.h"
 #include "route.h"
 
@@ -157,9 +158,7 @@ struct MfmaArgs {
 	int h_f16;               // gate/up out: h as f16(h * h_scale), pair-permuted K order (quantised down)
 	float h_scale;           // 2^-h_shift of the layer
 	float y_scale;           // down out (f16 operands): 2^(h_shift - F16_SHIFT) takes both factors out
-	float *y;                // down out [pair][d] (BF16 weights: fp32)
-	uint16_t *y16;           // down out [pair][d] (quantised weights: bf16)
-	float *out32;            // down: fp32 rows [pair][rows] instead of y16 (dense matrices)
+	float *y;                // down out, fp32 rows: y [pair][d] (experts), out [token][rows] (dense matrices)
 	int mt_cap;              // pair rows per tile at most, below MT (0: MT; dense matrices at small T)
 	int32_t *tok_flag;       // [T] gate/up, h_f16: tokens whose h left the f16 range
 	int32_t *fix_list;       //     are appended here (once each) ...
@@ -1120,15 +1119,11 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 					const float4 v1 = *reinterpret_cast<const float4 *>(tl + r * LS + 8 * part + 4);
 					const int mrow = 32 * mt + 16 * half + r;
 					if (mrow < nrows) {
-						if (DOWN && a.out32) {
-							float *orow = a.out32 + (size_t)spair[mrow] * a.rows + slab * DN_COLS + 64 * w + 8 * part;
+						if (DOWN) {
+							// fp32 rows: y [pair][d] (experts) or out [token][rows] (dense)
+							float *orow = a.y + (size_t)spair[mrow] * a.rows + slab * DN_COLS + 64 * w + 8 * part;
 							*reinterpret_cast<float4 *>(orow) = v0;
 							*reinterpret_cast<float4 *>(orow + 4) = v1;
-						} else if (DOWN) {
-							const uint4 o = make_uint4(pack_bf16(v0.x, v0.y), pack_bf16(v0.z, v0.w),
-										   pack_bf16(v1.x, v1.y), pack_bf16(v1.z, v1.w));
-							uint16_t *yr = a.y16 + (size_t)spair[mrow] * a.rows + slab * DN_COLS + 64 * w + 8 * part;
-							*reinterpret_cast<uint4 *>(yr) = o;
 						} else {
 							const f16x8 hv = {(_Float16)v0.x, (_Float16)v0.y, (_Float16)v0.z, (_Float16)v0.w,
 									  (_Float16)v1.x, (_Float16)v1.y, (_Float16)v1.z, (_Float16)v1.w};
@@ -1174,19 +1169,13 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 					if (C::SPLIT)
 						a.h16lo[(size_t)p * a.rows + col] = bf16_bits(hv - bf16_bits_to_float(hi));
 				}
-			} else if (C::SPLIT) {
-				float *yr = a.y + (size_t)spair[mrow] * a.rows + slab * DN_COLS + 64 * w + (lane & 31);
-				yr[0] = acc[mt][0][i];
-				yr[32] = acc[mt][1][i];
 			} else {
-				// quantised weights: y as bf16 (the path's products already
-				// take 16-bit operands; half the bytes to the combine); the
-				// f16 weights' factor 2^F16_SHIFT and h's scale come out here
-				// (a power of two: exact)
+				// y in fp32; the f16 weights' factor 2^F16_SHIFT and h's
+				// scale come out here (a power of two: exact)
 				const float unscale = C::F16 ? a.y_scale : 1.0f;
-				uint16_t *yr = a.y16 + (size_t)spair[mrow] * a.rows + slab * DN_COLS + 64 * w + (lane & 31);
-				yr[0] = bf16_bits(acc[mt][0][i] * unscale);
-				yr[32] = bf16_bits(acc[mt][1][i] * unscale);
+				float *yr = a.y + (size_t)spair[mrow] * a.rows + slab * DN_COLS + 64 * w + (lane & 31);
+				yr[0] = acc[mt][0][i] * unscale;
+				yr[32] = acc[mt][1][i] * unscale;
 			}
 		}
 		// one M tile at a time: only its accumulators move to VGPRs
@@ -1460,11 +1449,11 @@ hipError_t launch_route_bucket(const Layer &L, const float *x, int T, int k, Wor
 	r.count = ws.fix_count;
 	const dim3 grid((T + RB_THREADS / 64 - 1) / (RB_THREADS / 64));
 	if (L.gate.type == TIE_GGML_BF16)
-		hipLaunchKernelGGL(route_bucket_kernel<2>, grid, dim3(RB_THREADS), 0, s, r);
+		tie_launch(route_bucket_kernel<2>, grid, dim3(RB_THREADS), 0, s, r);
 	else if (TIE_MFMA_F16)
-		hipLaunchKernelGGL(route_bucket_kernel<1>, grid, dim3(RB_THREADS), 0, s, r);
+		tie_launch(route_bucket_kernel<1>, grid, dim3(RB_THREADS), 0, s, r);
 	else
-		hipLaunchKernelGGL(route_bucket_kernel<0>, grid, dim3(RB_THREADS), 0, s, r);
+		tie_launch(route_bucket_kernel<0>, grid, dim3(RB_THREADS), 0, s, r);
 	return hipGetLastError();
 }
 
@@ -1517,7 +1506,7 @@ __global__ __launch_bounds__(BP_THREADS) void bucket_plan_kernel(const uint8_t *
 
 hipError_t launch_bucket_plan(const Layer &L, int T, int k, Workspace &ws, hipStream_t s)
 {
-	hipLaunchKernelGGL(bucket_plan_kernel, dim3(L.E), dim3(BP_THREADS), 0, s, ws.sel, k, T4(T), ws.bucket_cnt,
+	tie_launch(bucket_plan_kernel, dim3(L.E), dim3(BP_THREADS), 0, s, ws.sel, k, T4(T), ws.bucket_cnt,
 			   ws.bucket);
 	return hipGetLastError();
 }
@@ -1537,7 +1526,7 @@ static hipError_t launch_type(const MfmaArgs &a, dim3 grid, hipStream_t s)
 			return err;
 		attr = true;
 	}
-	hipLaunchKernelGGL((mfma_experts_kernel<TYPE, DOWN, MTR>), grid, dim3(MF_THREADS), lds, s, a);
+	tie_launch((mfma_experts_kernel<TYPE, DOWN, MTR>), grid, dim3(MF_THREADS), lds, s, a);
 	return hipGetLastError();
 }
 
@@ -1599,14 +1588,12 @@ hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, con
 	a.bstride = T4(T);
 	a.silu = silu;
 	a.y = ws.y;
-	a.y16 = reinterpret_cast<uint16_t *>(ws.y);
 	a.h_f16 = TIE_MFMA_F16 && (L.down.type == TIE_GGML_Q4_K || L.down.type == TIE_GGML_Q6_K);
 	a.h_scale = ldexpf(1.0f, -L.h_shift);
 	a.y_scale = ldexpf(1.0f, L.h_shift - F16_SHIFT);
 	a.tok_flag = ws.tok_flag;
 	a.fix_list = ws.fix_list;
 	a.fix_count = ws.fix_count;
-	a.out32 = nullptr;
 	// grid rows: a bound on each kernel's tiles (its own tile rows) plus 8
 	// rows: the XCD remap in the kernel reaches every live item only with
 	// at least 8 * ceil(live / 8) workgroups (rows past the tiles exit at
@@ -1700,7 +1687,7 @@ hipError_t launch_mfma_dense(const ExpertTensor &W, const float *x, int T, float
 		return hipSuccess;
 	if (!mfma_dense_supported(W, T))
 		return hipErrorInvalidValue;
-	hipLaunchKernelGGL(dense_prep_kernel, dim3((T + RB_THREADS / 64 - 1) / (RB_THREADS / 64)), dim3(RB_THREADS), 0, s, x,
+	tie_launch(dense_prep_kernel, dim3((T + RB_THREADS / 64 - 1) / (RB_THREADS / 64)), dim3(RB_THREADS), 0, s, x,
 			   T, W.in, ws.xb, ws.bucket_cnt, ws.bucket, ws.tok_flag);
 	hipError_t err = hipGetLastError();
 	if (err != hipSuccess)
@@ -1713,7 +1700,7 @@ hipError_t launch_mfma_dense(const ExpertTensor &W, const float *x, int T, float
 	a.bucket = ws.bucket;
 	a.bstride = T4(T);
 	a.y_scale = ldexpf(1.0f, -F16_SHIFT); // x unscaled; the weights' factor 2^F16_SHIFT out
-	a.out32 = out;
+	a.y = out;
 	a.w[0] = a.w[1] = W.data;
 	a.expert_bytes[0] = a.expert_bytes[1] = W.expert_bytes;
 	a.rows = W.rows;

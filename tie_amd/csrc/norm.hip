@@ -103,7 +103,7 @@ hipError_t launch_rmsnorm(const float *x, const float *w, float eps, int T, int 
 {
 	if (T == 0)
 		return hipSuccess;
-	hipLaunchKernelGGL(rmsnorm_kernel, dim3((T + NORM_THREADS / 64 - 1) / (NORM_THREADS / 64)), dim3(NORM_THREADS),
+	tie_launch(rmsnorm_kernel, dim3((T + NORM_THREADS / 64 - 1) / (NORM_THREADS / 64)), dim3(NORM_THREADS),
 			   0, s, x, w, eps, T, d, out, tab, nbits);
 	return hipGetLastError();
 }

@@ -84,13 +84,13 @@ hipError_t launch_repack(const ExpertTensor &t, const uint8_t *src, int E, int l
 	const int threads = 256, blocks = 4096;
 	if (t.type == TIE_GGML_Q4_K) {
 		const int aligned = ((uintptr_t)src % 16) == 0;
-		hipLaunchKernelGGL(repack_q4k_kernel, dim3(blocks), dim3(threads), 0, s, src, dst, E, t.rows, t.nb,
+		tie_launch(repack_q4k_kernel, dim3(blocks), dim3(threads), 0, s, src, dst, E, t.rows, t.nb,
 				   t.expert_bytes, aligned);
 	} else if (t.type == TIE_GGML_Q6_K) {
-		hipLaunchKernelGGL(repack_q6k_kernel, dim3(blocks), dim3(threads), 0, s, src, dst, E, t.rows, t.nb,
+		tie_launch(repack_q6k_kernel, dim3(blocks), dim3(threads), 0, s, src, dst, E, t.rows, t.nb,
 				   t.expert_bytes);
 	} else if (t.type == TIE_GGML_BF16) {
-		hipLaunchKernelGGL(repack_bf16_kernel, dim3(blocks), dim3(threads), 0, s, src, dst, E, t.rows, t.in,
+		tie_launch(repack_bf16_kernel, dim3(blocks), dim3(threads), 0, s, src, dst, E, t.rows, t.in,
 				   literal_bf16_stride);
 	} else {
 		return hipErrorInvalidValue;

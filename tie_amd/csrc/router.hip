@@ -349,7 +349,7 @@ __global__ void transpose_kernel(const float *__restrict__ W, float *__restrict_
 
 hipError_t launch_router_transpose(const Layer &L, hipStream_t s)
 {
-	hipLaunchKernelGGL(transpose_kernel, dim3((L.d + 31) / 32, (L.E + 31) / 32), dim3(32, 8), 0, s, L.router,
+	tie_launch(transpose_kernel, dim3((L.d + 31) / 32, (L.E + 31) / 32), dim3(32, 8), 0, s, L.router,
 			   (float *)L.routerT, L.E, L.d);
 	return hipGetLastError();
 }
@@ -379,7 +379,7 @@ hipError_t launch_router_logits(const Layer &L, const float *x, int T, float *lo
 	const int d = L.d, E = L.E;
 	if (T <= TIE_RS_MAX_T && sizeof(float) * (size_t)(8 * (d / 8 + 4)) * (1 + RS_TOK) <= 160 * 1024) {
 		const size_t lds = sizeof(float) * (size_t)(8 * (d / 8 + 4)) * (1 + RS_TOK);
-		hipLaunchKernelGGL(router_small_kernel, dim3(E), dim3(RS_THREADS), lds, s, x, L.router, L.bias, T, d, E,
+		tie_launch(router_small_kernel, dim3(E), dim3(RS_THREADS), lds, s, x, L.router, L.bias, T, d, E,
 				   logits, z);
 		return hipGetLastError();
 	}
@@ -394,7 +394,7 @@ hipError_t launch_router_logits(const Layer &L, const float *x, int T, float *lo
 				return err;
 			attr = true;
 		}
-		hipLaunchKernelGGL(router_logits_kernel, dim3((T + RT_TOK - 1) / RT_TOK, E / RT_EXP), dim3(RT_THREADS),
+		tie_launch(router_logits_kernel, dim3((T + RT_TOK - 1) / RT_TOK, E / RT_EXP), dim3(RT_THREADS),
 				   RT_LDS, s, x, L.routerT, L.bias, T, d, E, logits, z);
 		return hipGetLastError();
 	}
@@ -404,7 +404,7 @@ hipError_t launch_router_logits(const Layer &L, const float *x, int T, float *lo
 	auto kern = lm ? (tok == 16 ? (u64 ? router_mid_kernel<64, 16, true> : router_mid_kernel<32, 16, true>)
 				    : (u64 ? router_mid_kernel<64, 32, true> : router_mid_kernel<32, 32, true>))
 		       : (u64 ? router_mid_kernel<64, 32, false> : router_mid_kernel<32, 32, false>);
-	hipLaunchKernelGGL(kern, dim3(E, (T + tok - 1) / tok), dim3(tok * 8),
+	tie_launch(kern, dim3(E, (T + tok - 1) / tok), dim3(tok * 8),
 			   sizeof(float) * (size_t)(lm ? lane_major_floats(d) : d), s, x, L.router, L.bias, T, d, E, logits, z);
 	return hipGetLastError();
 }
@@ -412,7 +412,7 @@ hipError_t launch_router_logits(const Layer &L, const float *x, int T, float *lo
 hipError_t launch_router_select(const Layer &L, int T, int k, const float *logits, int32_t *topk_idx, float *topk_w,
 				hipStream_t s)
 {
-	hipLaunchKernelGGL(router_topk_kernel, dim3((T + RW_THREADS / 64 - 1) / (RW_THREADS / 64)), dim3(RW_THREADS), 0,
+	tie_launch(router_topk_kernel, dim3((T + RW_THREADS / 64 - 1) / (RW_THREADS / 64)), dim3(RW_THREADS), 0,
 			   s, logits, T, L.E, k, topk_idx, topk_w, L.routing, L.pbias);
 	return hipGetLastError();
 }
