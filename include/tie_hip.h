@@ -141,7 +141,11 @@ typedef struct tie_hip_layer_desc {
 } tie_hip_layer_desc;
 
 /* Upload (or copy on device) and repack one layer's weights into the
- * device layout.  The source buffers may be freed afterwards. */
+ * device layout.  The source buffers may be freed afterwards.  With
+ * src_on_device (and for tie_hip_matrix_create likewise) the library drains
+ * the device (hipDeviceSynchronize): no thread may be capturing a HIP graph
+ * meanwhile, as a device synchronisation fails or invalidates a capture in
+ * global or relaxed mode. */
 int tie_hip_layer_create(const tie_hip_layer_desc *desc, tie_hip_layer **out);
 void tie_hip_layer_destroy(tie_hip_layer *layer);
 
@@ -158,7 +162,21 @@ size_t tie_hip_layer_bytes(const tie_hip_layer *layer);
  * ordered by that stream.  When a call needs a larger workspace than its
  * stream holds, the library drains the whole device (hipDeviceSynchronize)
  * before freeing the old one; a call made during HIP graph capture must
- * therefore not grow it (warm the stream up with the largest T first). */
+ * therefore not grow it (warm the stream up with the largest T first).
+ *
+ * One token (T = 1, eager) runs as one launch whose workgroups hand values
+ * to each other; their waits are bounded.  Should a wait give up (the GPU
+ * did not run the workgroups together, e.g. under heavy sharing), that
+ * call's outputs are NaN and the stream's status word is set: the
+ * synchronous entry points (tie_hip_moe_ffn, _lfm2, tie_hip_qwen3_ffn)
+ * then return TIE_HIP_EHIP, and device-API callers read it with
+ * tie_hip_stream_status. */
+/* Frees the scratch workspace the library keeps for `stream` (grown by the
+ * forwards enqueued on it; at the 235B shape and large T, hundreds of MiB).
+ * Call it before destroying a stream that forwards ran on; otherwise the
+ * workspace lives until tie_hip_shutdown.  Drains the device first. */
+int tie_hip_stream_release(void *stream);
+
 int tie_hip_moe_forward(tie_hip_layer *layer, const float *x_dev, int T, int k, float *out_dev,
 			int32_t *topk_idx_dev, float *topk_w_dev, int flags, void *stream);
 
@@ -198,14 +216,13 @@ void tie_hip_matrix_destroy(tie_hip_matrix *m);
 
 /* dispatch_mat_mat (math_dispatch.c:304-359) on device pointers:
  * out_dev[t][r] = W[r] . x_dev[t] for t < T, x [T][in_dim] F32, out
- * [T][rows] F32.  TIE_HIP_PATH_EXACT, and TIE_HIP_PATH_AUTO for T up to the
- * exact threshold (64), use TIE's row kernels (mat_vec_row_f32_{f32,q4k,q6k,
- * bf16}_f32_avx2) bit for bit.  TIE_HIP_PATH_MFMA, and AUTO above the
- * threshold where supported (Q4_K or Q6_K, rows a multiple of 256), run the
- * f16 matrix cores with fp32 accumulation (relative L2 error about 3e-4 of
- * TIE's result); rows whose input does not fit the f16 range are recomputed
- * with the exact kernel.  TIE_HIP_PATH_MFMA on an unsupported matrix is an
- * error.  Enqueued on `stream`.  The attention projections, the dense FFN and the LM
+ * [T][rows] F32.  TIE_HIP_PATH_EXACT and TIE_HIP_PATH_AUTO (the default, at
+ * every T) use TIE's row kernels (mat_vec_row_f32_{f32,q4k,q6k,
+ * bf16}_f32_avx2) bit for bit.  TIE_HIP_PATH_MFMA (opt-in; Q4_K or Q6_K,
+ * rows a multiple of 256) runs the f16 matrix cores with fp32 accumulation
+ * (relative L2 error about 3e-4 of TIE's result); rows whose input does not
+ * fit the f16 range are recomputed with the exact kernel.
+ * TIE_HIP_PATH_MFMA on an unsupported matrix is an error.  Enqueued on `stream`.  The attention projections, the dense FFN and the LM
  * head of transformer_layer_qwen3 / main.c use it. */
 int tie_hip_mat_mat(tie_hip_matrix *m, const float *x_dev, int T, float *out_dev, int flags, void *stream);
 
@@ -227,6 +244,15 @@ typedef struct tie_hip_model tie_hip_model;
 /* Read the MoE shape of a GGUF file (host only, no GPU needed). */
 int tie_hip_gguf_inspect(const char *path, tie_hip_model_info *info);
 
+/* One tensor as the library's reader maps it (host only): its GGML type,
+ * ne[0..3] (GGUF order, 1 past n_dims), the file offset of its data (the
+ * data section starts at the first multiple of general.alignment, default
+ * 32, after the tensor infos: gguf_model_map_weights, gguf.c:941-944) and
+ * its size in bytes (0 for types the MoE path does not read).  name NULL:
+ * only the count.  Returns the file's tensor count, or a negative code. */
+int tie_hip_gguf_tensor_info(const char *path, const char *name, int *type, uint64_t ne[4], uint64_t *file_offset,
+			     uint64_t *bytes);
+
 /* Map a GGUF file and upload the MoE FFN of every layer from
  * first_moe_layer on: blk.N.ffn_gate_inp / ffn_gate_exps / ffn_up_exps /
  * ffn_down_exps (and exp_probs_b.bias for LFM2) into a tie_hip_layer, and
@@ -244,6 +270,18 @@ void tie_hip_model_close(tie_hip_model *m);
 /* The largest T that TIE_HIP_PATH_AUTO sends down the exact path. */
 int tie_hip_exact_max_tokens(void);
 void tie_hip_set_exact_max_tokens(int t);
+
+/* Synchronises `stream` (NULL = the library stream) and reports whether a
+ * one-token forward enqueued on it since the last check had a wait between
+ * workgroups give up (its outputs NaN): TIE_HIP_EHIP with a message, and
+ * the flag cleared; TIE_HIP_OK otherwise.  No counterpart in TIE (its CPU
+ * path cannot fail this way). */
+int tie_hip_stream_status(void *stream);
+
+/* Debug hook: the next n one-launch one-token forwards wait for a stamp no
+ * workgroup writes, with a 64-poll limit, so every wait gives up (and every
+ * workgroup still exits): the error path of tie_hip_stream_status. */
+void tie_hip_debug_decode_give_up(int n);
 
 /* Make the n-th next device allocation fail with TIE_HIP_ENOMEM (n >= 1;
  * 0 disarms).  Host-side fault injection for error-path tests. */

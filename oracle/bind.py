@@ -76,6 +76,12 @@ def ref():
             raise RuntimeError("reference build absent: oracle/_ref/libtie_ref.so")
         lib = ctypes.CDLL(REF_SO)
         lib.ref_silu_table.restype = _I
+        lib.ref_gguf_open.restype = _P
+        lib.ref_gguf_open.argtypes = [ctypes.c_char_p]
+        lib.ref_gguf_close.argtypes = [_P]
+        lib.ref_gguf_info.argtypes = [_P, _P, _P, _P]
+        lib.ref_gguf_tensor.argtypes = [_P, ctypes.c_uint64, ctypes.c_char_p, ctypes.c_size_t, _P, _P, _P, _P, _P]
+        lib.ref_gguf_value.argtypes = [_P, ctypes.c_char_p, _P]
         lib.ref_silu_table.argtypes = [_P, _I]
         lib.ref_pool_threads.restype = _I
         lib.ref_rms_norm.restype = _I
@@ -196,3 +202,34 @@ def libm_expf(x):
     out = np.empty_like(x)
     oracle().orc_expf_array(_ptr(x), _ptr(out), x.size)
     return out
+
+
+def ref_gguf(path, keys=()):
+    """TIE's own GGUF reader (gguf_model_parse, gguf.c:968-1047) on a file:
+    {"arch": id, "data_offset": .., "tensors": {name: (type, ne[4], file
+    offset, bytes)}, "values": {key: 8 raw bytes}} (None if TIE rejects the
+    file)."""
+    import os
+    lib = ref()
+    h = lib.ref_gguf_open(os.fsencode(path))
+    if not h:
+        return None
+    try:
+        cnt, doff, arch = ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_int()
+        lib.ref_gguf_info(h, ctypes.byref(cnt), ctypes.byref(doff), ctypes.byref(arch))
+        tensors = {}
+        for i in range(cnt.value):
+            name = ctypes.create_string_buffer(256)
+            t, nd, off, nb = ctypes.c_uint32(), ctypes.c_uint32(), ctypes.c_uint64(), ctypes.c_uint64()
+            ne = np.zeros(4, np.uint64)
+            lib.ref_gguf_tensor(h, i, name, 256, ctypes.byref(t), ctypes.byref(nd), _ptr(ne), ctypes.byref(off),
+                                ctypes.byref(nb))
+            tensors[name.value.decode()] = (t.value, tuple(int(v) for v in ne), off.value, nb.value)
+        values = {}
+        for k in keys:
+            buf = (ctypes.c_uint8 * 8)()
+            if lib.ref_gguf_value(h, k.encode(), buf) == 0:
+                values[k] = bytes(buf)
+        return {"arch": arch.value, "data_offset": doff.value, "tensors": tensors, "values": values}
+    finally:
+        lib.ref_gguf_close(h)

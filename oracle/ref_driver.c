@@ -252,3 +252,60 @@ int ref_moe_block(const float *x, int T, int d, int F, int E, int k, const float
 	free(ctx);
 	return 0;
 }
+
+/* ---- TIE's GGUF reader on a file (gguf_model_parse, gguf.c:977-1047, with
+ * gguf_model_metadata_read, gguf.c:793, and gguf_model_map_weights,
+ * gguf.c:892-966), for checking the library's own reader against it. */
+void *ref_gguf_open(const char *path)
+{
+	char p[4096];
+	strncpy(p, path, sizeof p - 1);
+	p[sizeof p - 1] = 0;
+	return gguf_model_parse(p);
+}
+
+void ref_gguf_close(void *h)
+{
+	if (h) {
+		gguf_model_close((struct GGUFModel *)h);
+		free(h);
+	}
+}
+
+/* tensor count, data section offset and architecture id (detect_architecture) */
+int ref_gguf_info(void *h, uint64_t *count, uint64_t *data_offset, int *arch)
+{
+	struct GGUFModel *g = (struct GGUFModel *)h;
+	*count = g->tensor_count;
+	*data_offset = g->tensor_data_offset;
+	*arch = g->arch;
+	return 0;
+}
+
+/* tensor i: name, type, dims, data pointer as a file offset, size */
+int ref_gguf_tensor(void *h, uint64_t i, char *name, size_t cap, uint32_t *type, uint32_t *n_dims, uint64_t *ne,
+		    uint64_t *file_offset, uint64_t *bytes)
+{
+	struct GGUFModel *g = (struct GGUFModel *)h;
+	if (i >= g->tensor_count)
+		return -1;
+	const GGUFTensor *t = &g->tensors[i];
+	strncpy(name, t->name, cap - 1);
+	name[cap - 1] = 0;
+	*type = t->type;
+	*n_dims = t->n_dims;
+	for (int j = 0; j < 4; j++)
+		ne[j] = t->dimensions[j];
+	*file_offset = (uint64_t)((uint8_t *)t->data - (uint8_t *)g->mapped_data);
+	*bytes = t->size;
+	return 0;
+}
+
+/* a scalar metadata value, its bytes as TIE's gguf_metadata_get_value copies them */
+int ref_gguf_value(void *h, const char *key, void *value)
+{
+	char k[512];
+	strncpy(k, key, sizeof k - 1);
+	k[sizeof k - 1] = 0;
+	return gguf_metadata_get_value((struct GGUFModel *)h, k, value);
+}

@@ -1,11 +1,11 @@
 """Summaries of rocprofv3 output for the MoE block kernels.
 
-    python -m tie_amd.profiling stats <kernel_trace.csv> [--title TEXT] [--command CMD]
+    python rocprof_summary.py stats <kernel_trace.csv> [--title TEXT] [--command CMD]
         Markdown table of per-kernel launch counts and durations (from the
         start/end timestamps of a --kernel-trace run), one row per kernel
         and grid shape.
 
-    python -m tie_amd.profiling traffic --fetch F.csv --write W.csv
+    python rocprof_summary.py traffic --fetch F.csv --write W.csv
             --copy-fetch CF.csv --copy-write CW.csv --copy-bytes N --config NAME
             [--out profiles/traffic.json]
         HBM bytes per forward of each block kernel from two --pmc runs

@@ -395,8 +395,8 @@ def test_out_of_range_residual_in_place():
 
 @pytest.mark.parametrize("wtype", QUANT)
 def test_dense_mat_mat_mfma(wtype):
-    """tie_hip_mat_mat on the matrix cores (TIE_HIP_PATH_MFMA, and the
-    default above the exact threshold): against the float64 model of its
+    """tie_hip_mat_mat on the matrix cores (TIE_HIP_PATH_MFMA; the default
+    keeps the exact row kernels): against the float64 model of its
     operands (x in f16, the f16 weights of q4k_f16 / q6k_f16) and against
     TIE's row kernels (the fp32 oracle); a token whose x leaves the f16 range
     is computed exactly instead (bit-exact).  The small matrix makes the
@@ -408,8 +408,8 @@ def test_dense_mat_mat_mfma(wtype):
     w = synth.expert_tensor(rng, wtype, 1, rows, in_dim)
     W16 = expert_weights(w, wtype, 0, rows, in_dim, True).astype(np.float64)
     M = tie_amd.Matrix(w, wtype, rows, in_dim)
-    for T, flags in ((65, tie_amd.PATH_AUTO), (200, tie_amd.PATH_MFMA), (7, tie_amd.PATH_MFMA), (32, tie_amd.PATH_MFMA),
-                     (130, tie_amd.PATH_AUTO)):
+    for T, flags in ((65, tie_amd.PATH_MFMA), (200, tie_amd.PATH_MFMA), (7, tie_amd.PATH_MFMA),
+                     (32, tie_amd.PATH_MFMA), (130, tie_amd.PATH_MFMA)):
         x = synth.make_input(61 + T, T, in_dim)
         x[3] *= np.float32(1e5)  # beyond f16: recomputed exactly
         print("dense mfma type=%d T=%d" % (wtype, T), flush=True)
@@ -425,6 +425,13 @@ def test_dense_mat_mat_mfma(wtype):
         e_model = rel_l2(got[rest], ref)
         assert e_model <= MODEL_RL2, e_model
         check_oracle("dense_mfma t%d T=%d" % (wtype, T), got[rest], ro[rest])
+    # the default (TIE_HIP_PATH_AUTO) keeps TIE's row kernels at any T: bit-exact
+    x = synth.make_input(70, 130, in_dim)
+    xd = torch.from_numpy(x).cuda()
+    out = torch.empty((130, rows), device="cuda")
+    M.mat_mat(xd, 130, out, flags=tie_amd.PATH_AUTO)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(bits(out.cpu().numpy()), bits(bind.mat_mat(x, w, wtype, rows)))
     M.close()
 
 

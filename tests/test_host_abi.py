@@ -3,6 +3,7 @@ declares, builds TIE's SiLU table on the host, and reports errors without
 exiting."""
 import os
 import re
+import sys
 
 import numpy as np
 import pytest
@@ -111,3 +112,36 @@ def test_header_compiles_as_c99_and_links(tmp_path):
     env = dict(os.environ, HIP_VISIBLE_DEVICES="", ROCR_VISIBLE_DEVICES="")
     r = subprocess.run([str(exe)], capture_output=True, text=True, env=env, timeout=120)
     assert r.returncode == 0, (r.returncode, r.stdout, r.stderr)
+
+
+REF_DIR = "/root/reference"
+
+
+@pytest.mark.skipif(not os.path.exists(os.path.join(REF_DIR, "model_qwen3.c")),
+                    reason="the reference sources are not present")
+def test_integration_snippets_compile_against_tie_headers(tmp_path):
+    """INTEGRATION.md's call-site snippets (engine_alloc set-up, the Qwen3 MoE
+    branch model_qwen3.c:404-471, the FFN half :390-491, the LFM2 branch
+    model_lfm2.c:414-497), pasted into functions shaped like TIE's own
+    (oracle/callsite.c) and compiled with TIE's headers (struct TIEContext,
+    Model, LayerWeights: main.h, model.h:170-253, engine.h:36-125) and TIE's
+    warning flags as errors: every argument type-checks against TIE's
+    structures.  A snippet with one argument of the wrong type must fail to
+    compile, so the check has teeth."""
+    import subprocess
+    inc = tmp_path / "inc"
+    inc.mkdir()
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "oracle", "extract_callsite.py"),
+                        os.path.join(ROOT, "INTEGRATION.md"), str(inc)], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    base = ["gcc", "-std=gnu99", "-Wall", "-Wno-pointer-sign", "-Wno-unused-label", "-funsigned-char", "-Werror",
+            "-DTIE_USE_HIP", "-I", REF_DIR, "-I", os.path.join(ROOT, "include"), "-I", str(inc), "-c",
+            os.path.join(ROOT, "oracle", "callsite.c"), "-o", str(tmp_path / "callsite.o")]
+    r = subprocess.run(base, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    # negative control: TIE's ffn_norm Tensor where the snippet passes F
+    q = (inc / "qwen3_moe.inc").read_text()
+    assert "ctx->model->expert_ffn_dim" in q
+    (inc / "qwen3_moe.inc").write_text(q.replace("ctx->model->expert_ffn_dim", "l->ffn_norm", 1))
+    r = subprocess.run(base, capture_output=True, text=True)
+    assert r.returncode != 0 and "qwen3_moe.inc" in r.stderr

@@ -25,12 +25,13 @@ SILU_TABLE_SIZE = 8192
 EXPORTS = (
     "tie_hip_init", "tie_hip_shutdown", "tie_hip_last_error", "tie_hip_moe_ffn", "tie_hip_moe_ffn_lfm2",
     "tie_hip_qwen3_ffn", "tie_hip_moe_forward_residual", "tie_hip_matrix_create", "tie_hip_matrix_destroy",
-    "tie_hip_mat_mat", "tie_hip_gguf_inspect", "tie_hip_gguf_load", "tie_hip_model_info_get", "tie_hip_model_layer",
+    "tie_hip_mat_mat", "tie_hip_gguf_inspect", "tie_hip_gguf_tensor_info", "tie_hip_gguf_load", "tie_hip_model_info_get", "tie_hip_model_layer",
     "tie_hip_model_ffn_norm", "tie_hip_model_close", "tie_hip_set_silu_table",
     "tie_hip_silu_table_host", "tie_hip_layer_create", "tie_hip_layer_destroy", "tie_hip_layer_bytes",
     "tie_hip_moe_forward", "tie_hip_exact_max_tokens", "tie_hip_set_exact_max_tokens",
     "tie_hip_debug_fail_alloc", "tie_hip_host_expf", "tie_hip_profile_enable", "tie_hip_profile_read",
-    "tie_hip_moe_forward_noalloc",
+    "tie_hip_moe_forward_noalloc", "tie_hip_stream_status", "tie_hip_debug_decode_give_up",
+    "tie_hip_stream_release",
 )
 
 
@@ -95,6 +96,8 @@ def lib():
         L.tie_hip_mat_mat.restype = I
         L.tie_hip_gguf_inspect.argtypes = [ctypes.c_char_p, ctypes.POINTER(ModelInfo)]
         L.tie_hip_gguf_inspect.restype = I
+        L.tie_hip_gguf_tensor_info.argtypes = [ctypes.c_char_p, ctypes.c_char_p, P, P, P, P]
+        L.tie_hip_gguf_tensor_info.restype = I
         L.tie_hip_gguf_load.argtypes = [ctypes.c_char_p, ctypes.POINTER(ctypes.c_void_p)]
         L.tie_hip_gguf_load.restype = I
         L.tie_hip_model_info_get.argtypes = [P, ctypes.POINTER(ModelInfo)]
@@ -126,6 +129,12 @@ def lib():
         L.tie_hip_debug_fail_alloc.restype = None
         L.tie_hip_host_expf.argtypes = [P, P, ctypes.c_size_t]
         L.tie_hip_host_expf.restype = None
+        L.tie_hip_stream_release.argtypes = [P]
+        L.tie_hip_stream_release.restype = I
+        L.tie_hip_stream_status.argtypes = [P]
+        L.tie_hip_stream_status.restype = I
+        L.tie_hip_debug_decode_give_up.argtypes = [I]
+        L.tie_hip_debug_decode_give_up.restype = None
         L.tie_hip_profile_enable.argtypes = [I]
         L.tie_hip_profile_enable.restype = I
         L.tie_hip_profile_read.argtypes = [ctypes.c_char_p, ctypes.c_size_t, P, P, I]
@@ -178,6 +187,21 @@ def host_expf(x):
     out = np.empty_like(x)
     lib().tie_hip_host_expf(_p(x), _p(out), x.size)
     return out
+
+
+def stream_status(stream=None):
+    """tie_hip_stream_status: raises TieError when a one-token forward on
+    the stream had a wait between workgroups give up since the last check."""
+    check(lib().tie_hip_stream_status(stream))
+
+
+def stream_release(stream=None):
+    """tie_hip_stream_release: free the workspace kept for the stream."""
+    check(lib().tie_hip_stream_release(stream))
+
+
+def debug_decode_give_up(n):
+    lib().tie_hip_debug_decode_give_up(int(n))
 
 
 def profile_enable(on=True):
@@ -233,6 +257,25 @@ def qwen3_ffn(hidden, layer, k, ffn_norm, eps, with_topk=True):
                                   _p(layer.gate), layer.gate_type, _p(layer.up), layer.up_type, _p(layer.down),
                                   layer.down_type, _p(idx), _p(w)))
     return h, idx, w
+
+
+def gguf_tensor_info(path, name):
+    """tie_hip_gguf_tensor_info: (type, ne[4], file offset, bytes) of one
+    tensor as the library's reader maps it (no GPU needed)."""
+    t = ctypes.c_int(0)
+    ne = np.zeros(4, np.uint64)
+    off = ctypes.c_uint64(0)
+    nb = ctypes.c_uint64(0)
+    rc = lib().tie_hip_gguf_tensor_info(os.fsencode(path), name.encode(), ctypes.byref(t), _p(ne),
+                                        ctypes.byref(off), ctypes.byref(nb))
+    check(min(rc, 0))  # >= 0: the tensor count
+    return t.value, tuple(int(v) for v in ne), off.value, nb.value
+
+
+def gguf_tensor_count(path):
+    n = lib().tie_hip_gguf_tensor_info(os.fsencode(path), None, None, None, None, None)
+    check(min(n, 0))
+    return n
 
 
 def gguf_inspect(path):

@@ -60,6 +60,7 @@ struct Ctx {
 	uint32_t *rsq = nullptr;   // host RSQRTSS table (built at the first residual call)
 	int rsq_bits = 0;
 	int exact_max_t = 64;
+	int debug_stale = 0; // one-launch decode calls left whose waits are made to give up (debug hook)
 	std::recursive_mutex mu;
 };
 
@@ -239,7 +240,7 @@ static size_t carve_workspace(uint8_t *b, size_t P, size_t FF, size_t DD, size_t
 		     o_hlo = take(P * FF * 2), o_xlo = take(Tcap * DD * 2), o_nm = take(Tcap * DD * 4);
 	const size_t o_bc = take(EE * 4), o_mk = take(EE * (size_t)T4((int)Tcap)), o_bk = take(EE * T4((int)Tcap) * 4);
 	const size_t o_fl = take(Tcap * 4), o_fx = take(Tcap * 4), o_fc = take(4);
-	const size_t o_lg = take(EE * 8), o_dn = take((size_t)MAX_K * FF * 8);
+	const size_t o_lg = take(EE * 8), o_dn = take((size_t)MAX_K * FF * 8), o_st = take(4);
 	if (!b)
 		return off;
 	w->topk_idx = (int32_t *)(b + o_idx);
@@ -264,6 +265,7 @@ static size_t carve_workspace(uint8_t *b, size_t P, size_t FF, size_t DD, size_t
 	w->one_lg = (unsigned long long *)(b + o_lg);
 	w->one_h = (unsigned long long *)(b + o_dn);
 	w->one_seq = 0;
+	w->one_status = (int32_t *)(b + o_st);
 	w->cap_pairs = P;
 	w->cap_F = FF;
 	w->cap_d = DD;
@@ -285,10 +287,12 @@ static int ensure_workspace(hipStream_t s, int T, int k, int d, int F, int E, Wo
 	const size_t EE = (size_t)E > w.cap_E ? E : w.cap_E;
 	const size_t bytes = carve_workspace(nullptr, P, FF, DD, EE, nullptr);
 	void *mem = nullptr;
+	int32_t status = 0; // a given-up wait not yet reported survives the growth
 	if (w.alloc) {
 		// work still queued on s (or, through events, on any stream the
 		// caller chained to it) may read the old buffer: drain the device
 		HIP_TRY(hipDeviceSynchronize());
+		HIP_TRY(hipMemcpy(&status, w.one_status, 4, hipMemcpyDeviceToHost));
 		HIP_TRY(hipFree(w.alloc));
 		w = Workspace();
 	}
@@ -301,7 +305,27 @@ static int ensure_workspace(hipStream_t s, int T, int k, int d, int F, int E, Wo
 	// later one)
 	HIP_TRY(hipMemset(w.one_lg, 0, (size_t)EE * 8));
 	HIP_TRY(hipMemset(w.one_h, 0, (size_t)MAX_K * FF * 8));
+	HIP_TRY(hipMemcpy(w.one_status, &status, 4, hipMemcpyHostToDevice));
 	return TIE_HIP_OK;
+}
+
+// The status word of stream s's workspace: TIE_HIP_EHIP (and the word
+// cleared) when a one-launch decode wait gave up since the last check.
+// Synchronises s.
+static int take_stream_status(hipStream_t s)
+{
+	auto it = g.ws.find(s);
+	if (it == g.ws.end() || !it->second.alloc)
+		return TIE_HIP_OK;
+	HIP_TRY(hipStreamSynchronize(s));
+	int32_t st = 0;
+	HIP_TRY(hipMemcpy(&st, it->second.one_status, 4, hipMemcpyDeviceToHost));
+	if (!st)
+		return TIE_HIP_OK;
+	const int32_t zero = 0;
+	HIP_TRY(hipMemcpy(it->second.one_status, &zero, 4, hipMemcpyHostToDevice));
+	return set_error(TIE_HIP_EHIP, "one-token forward: a wait between workgroups gave up (the GPU did not run "
+				       "them together); that call's outputs are NaN");
 }
 
 static void free_layer(tie_hip_layer *l)
@@ -407,13 +431,21 @@ static int create_layer(const tie_hip_layer_desc *ds, tie_hip_layer **out)
 	if (e == hipSuccess && rc == 0)
 		e = hipStreamSynchronize(g.stream);
 	if (e == hipSuccess && rc == 0) {
-		// the f16 scale of h from a sample of the gate weights (host or
-		// device source: unified addressing)
-		const size_t n = std::min<size_t>(L.gate.expert_bytes * E, (size_t)1 << 20);
-		std::vector<uint8_t> smp(n);
-		e = hipMemcpy(smp.data(), ds->gate_exps, n, hipMemcpyDefault);
-		if (e == hipSuccess)
-			L.h_shift = h_shift_estimate(ds->gate_type, smp.data(), n, d);
+		// the f16 scale of h from a sample of the gate weights: up to 4096
+		// super-blocks evenly strided over the whole tensor (every expert),
+		// gathered in one strided copy (host or device source: unified
+		// addressing)
+		const size_t bb = ds->gate_type == TIE_GGML_Q4_K ? Q4K_BYTES
+				: ds->gate_type == TIE_GGML_Q6_K ? Q6K_BYTES
+								 : 2 * QK; // BF16: 256 weights per sample
+		if (bb) {
+			const size_t nblk = L.gate.expert_bytes * E / bb;
+			const size_t cnt = std::min<size_t>(nblk, 4096), step = nblk / cnt;
+			std::vector<uint8_t> smp(cnt * bb);
+			e = hipMemcpy2D(smp.data(), bb, ds->gate_exps, step * bb, bb, cnt, hipMemcpyDefault);
+			if (e == hipSuccess)
+				L.h_shift = h_shift_estimate(ds->gate_type, smp.data(), smp.size(), d);
+		}
 	}
 	if (rc || e != hipSuccess) {
 		free_layer(l);
@@ -509,8 +541,16 @@ static int forward(tie_hip_layer *layer, const float *x, int T, int k, float *ou
 			HIP_TRY(hipMemset(ws.one_h, 0, (size_t)MAX_K * ws.cap_F * 8));
 			ws.one_seq = 1;
 		}
+		uint32_t wseq = ws.one_seq;
+		int spin = ONE_SPIN_MAX;
+		if (g.debug_stale > 0) {
+			// debug hook: wait for a stamp no workgroup writes, briefly
+			g.debug_stale--;
+			wseq ^= 0x80000000u;
+			spin = 64;
+		}
 		HIP_TRY(launch_decode_one(L, x, k, g.silu, ws.topk_idx, ws.topk_w, out, res, ws.one_lg, ws.one_h, ws.one_seq,
-					  s));
+					  wseq, spin, ws.one_status, s));
 	} else if (T == 1 && decode_supported(L, k)) {
 		// one token: router logits, then the experts and the combine in two
 		// launches (the selection runs in the gate/up prologue for E <= 128)
@@ -823,7 +863,7 @@ static int moe_ffn_host(const float *x, int T, int d, int F, int E, int k, const
 	if (topk_w_opt)
 		HIP_TRY(hipMemcpyAsync(topk_w_opt, g.w_dev, (size_t)T * k * 4, hipMemcpyDeviceToHost, g.stream));
 	HIP_TRY(hipStreamSynchronize(g.stream));
-	return TIE_HIP_OK;
+	return take_stream_status(g.stream);
 }
 
 extern "C" void tie_hip_model_close(tie_hip_model *m)
@@ -1036,10 +1076,11 @@ extern "C" int tie_hip_mat_mat(tie_hip_matrix *m, const float *x_dev, int T, flo
 	if (!x_dev || !out_dev)
 		return set_error(TIE_HIP_EINVAL, "null x/out");
 	hipStream_t s = stream ? (hipStream_t)stream : g.stream;
-	// the matrix cores: asked for, or by default above the exact threshold
-	// where the matrix allows them (Q4_K / Q6_K, rows a multiple of 256)
+	// the matrix cores only when asked for (Q4_K / Q6_K, rows a multiple of
+	// 256): TIE_HIP_PATH_AUTO keeps TIE's exact row kernels at every T, so a
+	// caller of dispatch_mat_mat gets TIE's bits unless it opts in
 	const bool mfma_ok = !m->F.router && mfma_dense_supported(m->W, T);
-	const bool mfma = (flags & TIE_HIP_PATH_MFMA) || (!(flags & TIE_HIP_PATH_EXACT) && T > g.exact_max_t && mfma_ok);
+	const bool mfma = (flags & TIE_HIP_PATH_MFMA) != 0;
 	if (mfma && !mfma_ok)
 		return set_error(TIE_HIP_EINVAL, "the matrix-core path needs a Q4_K / Q6_K matrix with rows a multiple of 256");
 	prof_begin(mfma ? "dense_mfma" : "dense", s);
@@ -1121,6 +1162,39 @@ extern "C" void tie_hip_set_exact_max_tokens(int t)
 {
 	std::lock_guard<std::recursive_mutex> lk(g.mu);
 	g.exact_max_t = t < 0 ? 0 : t;
+}
+
+extern "C" int tie_hip_stream_release(void *stream)
+{
+	std::lock_guard<std::recursive_mutex> lk(g.mu);
+	clear_error();
+	int rc = ensure_init();
+	if (rc)
+		return rc;
+	auto it = g.ws.find(stream ? (hipStream_t)stream : g.stream);
+	if (it == g.ws.end())
+		return TIE_HIP_OK;
+	HIP_TRY(hipDeviceSynchronize());
+	if (it->second.alloc)
+		HIP_TRY(hipFree(it->second.alloc));
+	g.ws.erase(it);
+	return TIE_HIP_OK;
+}
+
+extern "C" int tie_hip_stream_status(void *stream)
+{
+	std::lock_guard<std::recursive_mutex> lk(g.mu);
+	clear_error();
+	int rc = ensure_init();
+	if (rc)
+		return rc;
+	return take_stream_status(stream ? (hipStream_t)stream : g.stream);
+}
+
+extern "C" void tie_hip_debug_decode_give_up(int n)
+{
+	std::lock_guard<std::recursive_mutex> lk(g.mu);
+	g.debug_stale = n > 0 ? n : 0;
 }
 
 extern "C" void tie_hip_debug_fail_alloc(int n)

@@ -102,6 +102,7 @@ struct Workspace {
 	unsigned long long *one_lg = nullptr; // [E]  one-launch decode: {seq, logit} words
 	unsigned long long *one_h = nullptr; // [MAX_K * F] one-launch decode: {seq, h} words
 	uint32_t one_seq = 0;         // one-launch decode: sequence number of the last call
+	int32_t *one_status = nullptr; // [1] one-launch decode: 1 when a wait gave up (outputs NaN)
 	size_t cap_pairs = 0, cap_F = 0, cap_d = 0, cap_E = 0;
 	void *alloc = nullptr;
 };
@@ -167,7 +168,10 @@ hipError_t launch_decode(const Layer &L, const float *x, int k, const float *sil
 bool decode_one_supported(const Layer &L, int k);
 hipError_t launch_decode_one(const Layer &L, const float *x, int k, const float *silu, int32_t *topk_idx,
 			     float *topk_w, float *out, const float *res, unsigned long long *lg, unsigned long long *hw,
-			     uint32_t seq, hipStream_t s);
+			     uint32_t seq, uint32_t wseq, int spin, int32_t *status, hipStream_t s);
+// polls before a wait of the one-launch decode gives up (each poll sleeps
+// about 64 cycles: tens of milliseconds in all)
+constexpr int ONE_SPIN_MAX = 1 << 18;
 struct Layer;
 int mfma_gu_rows(const Layer &L, int npairs); // rows per gate/up tile (the tile list's and the kernel's)
 // Dense F32-input matrix product through the expert GEMV kernels: out[t][r]

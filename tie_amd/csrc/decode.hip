@@ -514,17 +514,18 @@ template <int TD> __global__ __launch_bounds__(DEC_MAX_THREADS) void decode_down
 // agent-scope relaxed atomics (sc1: coherent across the XCDs' L2s with no
 // cache write-back, invalidate or separate flag); seq (one per call) tells
 // a word of this call from one left by an earlier call.  The waits are
-// bounded: a wait that gives up produces NaN outputs instead of hanging.
-constexpr int SPIN_MAX = 1 << 18;
+// bounded (spin polls): a wait that gives up produces NaN outputs instead
+// of hanging, and sets the call's status word, which the host reads back
+// (tie_hip_stream_status; the synchronous entry points return the error).
 
 __device__ __forceinline__ unsigned long long ld_word(const unsigned long long *p)
 {
 	return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ unsigned long long wait_word64(const unsigned long long *p, uint32_t seq, int &bad)
+__device__ __forceinline__ unsigned long long wait_word64(const unsigned long long *p, uint32_t seq, int spin, int &bad)
 {
-	for (int i = 0; i < SPIN_MAX; i++) {
+	for (int i = 0; i < spin; i++) {
 		const unsigned long long v = ld_word(p);
 		if ((uint32_t)(v >> 32) == seq)
 			return v;
@@ -540,7 +541,10 @@ struct OneArgs {
 	const float *bias;        // [E] or null
 	unsigned long long *lg;   // [E] {seq, logit}
 	unsigned long long *hw;   // [k][F] {seq, h}
-	uint32_t seq;
+	uint32_t seq;             // the stamp this call writes
+	uint32_t wseq;            // the stamp its waits look for (seq; another value only from the debug hook)
+	int spin;                 // polls before a wait gives up
+	int32_t *status;          // set to 1 when a wait gave up
 	int nr, ng;               // router, gate/up workgroups
 	int rpr, rg, rd;          // rows per router, gate/up, down workgroup
 };
@@ -574,7 +578,7 @@ __device__ __forceinline__ void one_select(const OneArgs &o, uint64_t *etab, int
 	__syncthreads();
 	if (tid < o.a.E) {
 		int bad = 0;
-		const float v = __uint_as_float((uint32_t)wait_word64(o.lg + tid, o.seq, bad));
+		const float v = __uint_as_float((uint32_t)wait_word64(o.lg + tid, o.wseq, o.spin, bad));
 		if (bad)
 			*sbad = 1;
 		rank_key(v, tid, o.a.routing, o.a.pbias, etab, *rs);
@@ -688,6 +692,8 @@ template <int TG, int TU, int TD> __global__ __launch_bounds__(DEC_MAX_THREADS, 
 			const unsigned long long w = ((unsigned long long)o.seq << 32) | __float_as_uint(hv);
 			__hip_atomic_store(o.hw + (size_t)j * a.F + r0 + tid, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 		}
+		if (sbad && tid == 0)
+			__hip_atomic_store(o.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 		if (gb == 0) {
 			topk_rank_weights(a.k, etab, sel_idx, sel_w, a.routing, rsc);
 			if (tid < a.k) {
@@ -749,12 +755,12 @@ template <int TG, int TU, int TD> __global__ __launch_bounds__(DEC_MAX_THREADS, 
 						v[i] = ld_word(o.hw + base + i * (int)blockDim.x);
 #pragma unroll
 				for (int i = 0; i < 8; i++)
-					if ((pend & (1u << i)) && (uint32_t)(v[i] >> 32) == o.seq) {
+					if ((pend & (1u << i)) && (uint32_t)(v[i] >> 32) == o.wseq) {
 						pend &= ~(1u << i);
 						const int f = base + i * (int)blockDim.x; // = (j nb + b) QK + m
 						hs[(f / QK) * XSEG + f % QK] = __uint_as_float((uint32_t)v[i]);
 					}
-				if (pend && ++it >= SPIN_MAX) {
+				if (pend && ++it >= o.spin) {
 					bad = 1;
 					break;
 				}
@@ -774,6 +780,8 @@ template <int TG, int TU, int TD> __global__ __launch_bounds__(DEC_MAX_THREADS, 
 	combine_rows(part, nb, k, R, sel_idx, sel_w, outp, a.res ? a.res + r0 : nullptr);
 	if (sbad && tid < R)
 		outp[tid] = __builtin_nanf("");
+	if (sbad && tid == 0)
+		__hip_atomic_store(o.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #ifdef TIE_ONE_TRACE
 	if (tid == 0) {
 		ONE_T(t_end);
@@ -1202,7 +1210,7 @@ int decode_one_gate_up_groups(const Layer &L, int k)
 
 hipError_t launch_decode_one(const Layer &L, const float *x, int k, const float *silu, int32_t *topk_idx,
 			     float *topk_w, float *out, const float *res, unsigned long long *lg, unsigned long long *hw,
-			     uint32_t seq, hipStream_t s)
+			     uint32_t seq, uint32_t wseq, int spin, int32_t *status, hipStream_t s)
 {
 	OneArgs o;
 	memset(&o, 0, sizeof o);
@@ -1233,6 +1241,9 @@ hipError_t launch_decode_one(const Layer &L, const float *x, int k, const float 
 	o.lg = lg;
 	o.hw = hw;
 	o.seq = seq;
+	o.wseq = wseq;
+	o.spin = spin;
+	o.status = status;
 	o.nr = (L.E + o.rpr - 1) / o.rpr;
 	o.ng = (L.F / o.rg) * k;
 	const int nd = L.d / o.rd;

@@ -175,10 +175,13 @@ int GGUFFile::open(const char *path)
 		uint64_t n = 1;
 		for (uint32_t j = 0; j < t.n_dims; j++)
 			n *= t.ne[j];
+		// tensors of types the MoE path never reads (Q8_0 embeddings, F16
+		// attention, ...) keep bytes = 0; the loader refuses them only if
+		// it needs them
 		t.bytes = tensor_bytes(t.type, n);
-		if (t.bytes == 0 || data_offset + t.offset + t.bytes > size)
-			return set_error(TIE_HIP_EINVAL, "%s: tensor %s out of the file or of an unknown type %u", path,
-					 kv.first.c_str(), t.type);
+		if (data_offset + t.offset + t.bytes > size)
+			return set_error(TIE_HIP_EINVAL, "%s: tensor %s extends past the end of the file", path,
+					 kv.first.c_str());
 		t.data = (const uint8_t *)map + data_offset + t.offset;
 	}
 	return TIE_HIP_OK;
@@ -261,4 +264,30 @@ extern "C" int tie_hip_gguf_inspect(const char *path, tie_hip_model_info *info)
 	if (rc)
 		return rc;
 	return f.moe_info(*info);
+}
+
+extern "C" int tie_hip_gguf_tensor_info(const char *path, const char *name, int *type, uint64_t ne[4],
+					uint64_t *file_offset, uint64_t *bytes)
+{
+	if (!path)
+		return tie::set_error(TIE_HIP_EINVAL, "null path");
+	tie::GGUFFile f;
+	int rc = f.open(path);
+	if (rc)
+		return rc;
+	if (!name)
+		return (int)f.tensors.size();
+	const tie::GGUFTensor *t = f.tensor(name);
+	if (!t)
+		return tie::set_error(TIE_HIP_EINVAL, "%s: no tensor %s", path, name);
+	if (type)
+		*type = (int)t->type;
+	if (ne)
+		for (int j = 0; j < 4; j++)
+			ne[j] = t->ne[j];
+	if (file_offset)
+		*file_offset = f.data_offset + t->offset;
+	if (bytes)
+		*bytes = t->bytes;
+	return (int)f.tensors.size();
 }

@@ -175,7 +175,7 @@ CONFIGS = {
     "dense_q4k_t32": dict(kind="dense", rows=4096, **{"in": 2048}, wtype=Q4_K, T=32, seed=1271),
     "lmhead_q6k_t1": dict(kind="dense", rows=151936, **{"in": 2048}, wtype=Q6_K, T=1, seed=1272),
     "dense_q4k_t32_mfma": dict(kind="dense", rows=4096, **{"in": 2048}, wtype=Q4_K, T=32, seed=1271, path="mfma"),
-    "dense_q4k_t512": dict(kind="dense", rows=4096, **{"in": 2048}, wtype=Q4_K, T=512, seed=1273),
-    "dense_q6k_t2048": dict(kind="dense", rows=4096, **{"in": 4096}, wtype=Q6_K, T=2048, seed=1274),
+    "dense_q4k_t512": dict(kind="dense", rows=4096, **{"in": 2048}, wtype=Q4_K, T=512, seed=1273, path="mfma"),
+    "dense_q6k_t2048": dict(kind="dense", rows=4096, **{"in": 4096}, wtype=Q6_K, T=2048, seed=1274, path="mfma"),
     "235b_t1024": dict(d=4096, F=1536, E=128, k=8, T=1024, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1239),
 }
