@@ -19,7 +19,8 @@ int set_error(int code, const char *fmt, ...);
 void clear_error();
 int silu_table_host(float *tab, int n);
 int rsqrt_table_host(std::vector<uint32_t> &tab, int &nbits);
-int h_shift_estimate(int type, const uint8_t *b, size_t n_bytes, int d);
+double weight_mean_square(int type, const uint8_t *b, size_t n_bytes);
+void f16_shifts(double ms_gate, double ms_down, int d, int F, int &h_shift, int &y_shift);
 } // namespace tie
 
 struct tie_hip_layer {
@@ -431,21 +432,29 @@ static int create_layer(const tie_hip_layer_desc *ds, tie_hip_layer **out)
 	if (e == hipSuccess && rc == 0)
 		e = hipStreamSynchronize(g.stream);
 	if (e == hipSuccess && rc == 0) {
-		// the f16 scale of h from a sample of the gate weights: up to 4096
-		// super-blocks evenly strided over the whole tensor (every expert),
-		// gathered in one strided copy (host or device source: unified
-		// addressing)
-		const size_t bb = ds->gate_type == TIE_GGML_Q4_K ? Q4K_BYTES
-				: ds->gate_type == TIE_GGML_Q6_K ? Q6K_BYTES
-								 : 2 * QK; // BF16: 256 weights per sample
-		if (bb) {
-			const size_t nblk = L.gate.expert_bytes * E / bb;
+		// the f16 scales of h and y from samples of the gate and down
+		// weights: up to 4096 super-blocks (BF16: 256-weight runs) evenly
+		// strided over the whole tensor (every expert), gathered in one
+		// strided copy each (host or device source: unified addressing)
+		auto sample_ms = [&](int type, const void *src, size_t tensor_bytes, double &ms) {
+			const size_t bb = type == TIE_GGML_Q4_K ? Q4K_BYTES : type == TIE_GGML_Q6_K ? Q6K_BYTES : 2 * QK;
+			const size_t nblk = tensor_bytes / bb;
+			ms = 0.0;
+			if (nblk == 0)
+				return hipSuccess;
 			const size_t cnt = std::min<size_t>(nblk, 4096), step = nblk / cnt;
 			std::vector<uint8_t> smp(cnt * bb);
-			e = hipMemcpy2D(smp.data(), bb, ds->gate_exps, step * bb, bb, cnt, hipMemcpyDefault);
-			if (e == hipSuccess)
-				L.h_shift = h_shift_estimate(ds->gate_type, smp.data(), smp.size(), d);
-		}
+			const hipError_t err = hipMemcpy2D(smp.data(), bb, src, step * bb, bb, cnt, hipMemcpyDefault);
+			if (err == hipSuccess)
+				ms = weight_mean_square(type, smp.data(), smp.size());
+			return err;
+		};
+		double ms_g = 0.0, ms_d = 0.0;
+		e = sample_ms(ds->gate_type, ds->gate_exps, L.gate.expert_bytes * E, ms_g);
+		if (e == hipSuccess)
+			e = sample_ms(ds->down_type, ds->down_exps, L.down.expert_bytes * E, ms_d);
+		if (e == hipSuccess)
+			f16_shifts(ms_g, ms_d, d, F, L.h_shift, L.y_shift);
 	}
 	if (rc || e != hipSuccess) {
 		free_layer(l);
@@ -518,14 +527,16 @@ static int forward(tie_hip_layer *layer, const float *x, int T, int k, float *ou
 			// left the f16 range (listed by the kernels above; usually
 			// none), which are recomputed exactly in the same launch, from
 			// res as it was (res may be out)
-			HIP_TRY(launch_combine_fix(L, x, k, g.silu, ws.topk_idx, ws.topk_w, ws.y,
-						   out, res, ws.tok_flag, ws.fix_list, ws.fix_count, T, s));
+			HIP_TRY(launch_combine_fix(L, x, k, g.silu, ws.topk_idx, ws.topk_w,
+						   reinterpret_cast<const uint16_t *>(ws.y), L.y_shift, out, res, ws.tok_flag,
+						   ws.fix_list, ws.fix_count, T, s));
 		} else {
 			// the same in two launches (the recomputation's LDS would cost
 			// the combine occupancy); the combine skips the listed tokens
 			prof_begin("combine", s);
+			const bool y16 = mfma_f16_operands(L) && L.down.type != TIE_GGML_BF16;
 			HIP_TRY(launch_combine(T, L.d, k, ws.topk_w, ws.topk_idx, ws.y, out, s, res,
-					       mfma_f16_operands(L) ? ws.tok_flag : nullptr));
+					       mfma_f16_operands(L) ? ws.tok_flag : nullptr, y16, L.y_shift));
 			prof_end(s);
 			if (mfma_f16_operands(L))
 				HIP_TRY(launch_recompute(L, x, k, g.silu, ws.topk_idx, ws.topk_w, out, res, ws.fix_list,

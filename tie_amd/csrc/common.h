@@ -74,6 +74,7 @@ struct Layer {
 	const float *pbias = nullptr;  // [E] or null: LFM2 selection bias (exp_probs_b_bias)
 	ExpertTensor gate, up, down;
 	int h_shift = 0;               // MFMA path: h is stored as f16(h * 2^-h_shift)
+	int y_shift = 0;               // MFMA path, quantised down: y is stored as f16(y * 2^-y_shift)
 	void *alloc = nullptr;         // one device allocation holding everything
 	size_t bytes = 0;
 };
@@ -152,12 +153,12 @@ bool recompute_supported(const Layer &L, int k);
 hipError_t launch_recompute(const Layer &L, const float *x, int k, const float *silu, const int32_t *topk_idx,
 			    const float *topk_w, float *out, const float *res, const int32_t *list,
 			    const int32_t *count, int T, hipStream_t s);
-// The matrix-core path's combine (fp32 y; tokens with skip[t] set left
+// The matrix-core path's combine (f16 y; tokens with skip[t] set left
 // alone) and the exact recomputation of the listed tokens in one launch,
 // when combine_fix_preferred
 bool combine_fix_preferred(const Layer &L);
 hipError_t launch_combine_fix(const Layer &L, const float *x, int k, const float *silu, const int32_t *topk_idx,
-			      const float *topk_w, const float *y, float *out, const float *res,
+			      const float *topk_w, const uint16_t *y16, int y_shift, float *out, const float *res,
 			      const int32_t *skip, const int32_t *list, const int32_t *count, int T, hipStream_t s);
 
 hipError_t launch_decode(const Layer &L, const float *x, int k, const float *silu, const float *logits,
@@ -193,9 +194,10 @@ bool mfma_dense_supported(const ExpertTensor &W, int T);
 hipError_t launch_mfma_dense(const ExpertTensor &W, const float *x, int T, float *out, Workspace &ws, hipStream_t s);
 int dense_groups(int T);
 // res (optional): out = res + combine (the residual add after the block)
+// y16: y holds f16(y 2^-y_shift) (the matrix-core path's quantised down)
 hipError_t launch_combine(int T, int d, int k, const float *topk_w, const int32_t *topk_idx, const float *y,
-			  float *out, hipStream_t s, const float *res = nullptr,
-			  const int32_t *skip = nullptr);
+			  float *out, hipStream_t s, const float *res = nullptr, const int32_t *skip = nullptr,
+			  bool y16 = false, int y_shift = 0);
 // TIE's RMSNorm of each row of x into out; tab/nbits: the host RSQRTSS table
 hipError_t launch_rmsnorm(const float *x, const float *w, float eps, int T, int d, float *out, const uint32_t *tab,
 			  int nbits, hipStream_t s);
@@ -322,48 +324,65 @@ __device__ __forceinline__ float tie_swiglu(float g, float u, const float *__res
 	float s = __builtin_fmaf(frac, y2 - y1, y1);
 	return s * u;
 }
-// One token's combine over 8 columns (c8: 8-column group) of fp32 expert
+// One token's combine over 8 columns (c8: 8-column group) of the expert
 // outputs: out[t][c] = [res[t][c] +] sum_j fma(g_j, y[t*k+j][c], .) in slot
 // order (model_qwen3.c:459-467, then the residual add of
-// apply_residual_f32_f32_avx2, math_avx2.c:731-751).  Slots of 8 loaded
-// (two 16-byte loads each) before their FMAs: one memory wait per 8 slots.
+// apply_residual_f32_f32_avx2, math_avx2.c:731-751).  y is fp32, or (Y16)
+// f16 values scaled by 2^-y_shift, whose scale ysc = 2^y_shift is folded
+// into g (a power of two: exact).  Slots of 8 loaded before their FMAs: one
+// memory wait per 8 slots.
+template <bool Y16>
 __device__ __forceinline__ void combine8_cols(int t, int c8, int d, int k, const float *__restrict__ topk_w,
-					      const int32_t *__restrict__ topk_idx, const float *__restrict__ y,
+					      const int32_t *__restrict__ topk_idx, const void *__restrict__ yv, float ysc,
 					      const float *res, float *out)
 {
-	float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+	float acc[8];
+#pragma unroll
+	for (int i = 0; i < 8; i++)
+		acc[i] = 0.0f;
 	constexpr int CG = 8;
 	for (int j0 = 0; j0 < k; j0 += CG) {
-		float4 v[CG][2];
+		float4 v[CG][Y16 ? 1 : 2];
 		float g[CG];
 #pragma unroll
 		for (int q = 0; q < CG; q++) {
 			const int j = j0 + q;
 			const bool on = j < k && topk_idx[t * k + (j < k ? j : 0)] >= 0;
-			g[q] = on ? topk_w[t * k + j] : 0.0f;
+			g[q] = on ? (Y16 ? topk_w[t * k + j] * ysc : topk_w[t * k + j]) : 0.0f;
 			// every slot's row is loaded (its address does not wait for
 			// topk_idx); a slot without an expert adds nothing
 			const size_t row = (size_t)t * k + (j < k ? j : j0);
-			const float4 *yr = reinterpret_cast<const float4 *>(y + row * d) + 2 * c8;
-			v[q][0] = yr[0];
-			v[q][1] = yr[1];
+			if constexpr (Y16) {
+				v[q][0] = reinterpret_cast<const float4 *>(reinterpret_cast<const uint16_t *>(yv) + row * d)[c8];
+			} else {
+				const float4 *yr = reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(yv) + row * d) + 2 * c8;
+				v[q][0] = yr[0];
+				v[q][1] = yr[1];
+			}
 		}
 #pragma unroll
 		for (int q = 0; q < CG; q++) {
 			const int j = j0 + q;
 			if (j < k && topk_idx[t * k + j] >= 0) {
-				a.x = __builtin_fmaf(g[q], v[q][0].x, a.x);
-				a.y = __builtin_fmaf(g[q], v[q][0].y, a.y);
-				a.z = __builtin_fmaf(g[q], v[q][0].z, a.z);
-				a.w = __builtin_fmaf(g[q], v[q][0].w, a.w);
-				b.x = __builtin_fmaf(g[q], v[q][1].x, b.x);
-				b.y = __builtin_fmaf(g[q], v[q][1].y, b.y);
-				b.z = __builtin_fmaf(g[q], v[q][1].z, b.z);
-				b.w = __builtin_fmaf(g[q], v[q][1].w, b.w);
+				float y[8];
+				if constexpr (Y16) {
+					typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+					const h8 hv = __builtin_bit_cast(h8, v[q][0]);
+#pragma unroll
+					for (int i = 0; i < 8; i++)
+						y[i] = (float)hv[i];
+				} else {
+					const float4 a = v[q][0], b = v[q][1];
+					y[0] = a.x, y[1] = a.y, y[2] = a.z, y[3] = a.w, y[4] = b.x, y[5] = b.y, y[6] = b.z, y[7] = b.w;
+				}
+#pragma unroll
+				for (int i = 0; i < 8; i++)
+					acc[i] = __builtin_fmaf(g[q], y[i], acc[i]);
 			}
 		}
 	}
 	float4 *o = reinterpret_cast<float4 *>(out + (size_t)t * d) + 2 * c8;
+	float4 a = make_float4(acc[0], acc[1], acc[2], acc[3]), b = make_float4(acc[4], acc[5], acc[6], acc[7]);
 	if (res) {
 		const float4 *h = reinterpret_cast<const float4 *>(res + (size_t)t * d) + 2 * c8;
 		const float4 h0 = h[0], h1 = h[1];

@@ -871,22 +871,21 @@ __global__ __launch_bounds__(DEC_MAX_THREADS) void recompute_kernel(DecodeArgs a
 }
 
 // The matrix-core path's last launch: the combine of every token not listed
-// for recomputation (combine_kernel's operations: out[t][c] = [res +] sum_j
-// fma(g_j, y_j[c], .) in slot order, y bf16), and, in workgroups of their
-// own, the exact recomputation of the listed ones (usually none) -- one
-// launch instead of two.  Workgroups [0, ncomb): token b / cpt, 1024
-// (w8: 2048) columns each; [ncomb, ncomb + nfix): recomputation.
+// for recomputation (combine8_cols: out[t][c] = [res +] sum_j fma(g_j,
+// y_j[c], .) in slot order, y as f16 scaled by 2^-y_shift), and, in
+// workgroups of their own, the exact recomputation of the listed ones
+// (usually none) -- one launch instead of two.  Workgroups [0, ncomb):
+// token b / cpt, 2048 columns each (8 per thread); [ncomb, ncomb + nfix):
+// recomputation.
 struct CombineFixArgs {
-	int ncomb, cpt, nfix, w8;
+	int ncomb, cpt, nfix;
+	float ysc; // 2^y_shift
 	const float *topk_w;
 	const int32_t *topk_idx;
-	const float *y;
+	const uint16_t *y16;
 	const int32_t *skip;
 };
 constexpr int CF_THREADS = 256;
-#ifndef TIE_CF_W8
-#define TIE_CF_W8 1
-#endif
 template <int TG, int TU, int TD>
 __global__ __launch_bounds__(CF_THREADS) void combine_fix_kernel(DecodeArgs a, CombineFixArgs c)
 {
@@ -897,37 +896,11 @@ __global__ __launch_bounds__(CF_THREADS) void combine_fix_kernel(DecodeArgs a, C
 		return;
 	}
 	const int t = b / c.cpt;
-	if (c.w8) {
-		// 8 columns per thread, 16-byte loads of y (d a multiple of 8)
-		const int c8 = (b - t * c.cpt) * CF_THREADS + threadIdx.x;
-		if (c.skip[t] || c8 * 8 >= a.d)
-			return;
-		combine8_cols(t, c8, a.d, a.k, c.topk_w, c.topk_idx, c.y, a.res, a.out);
+	// 8 columns per thread, 16-byte loads of y (d is a multiple of 256)
+	const int c8 = (b - t * c.cpt) * CF_THREADS + threadIdx.x;
+	if (c.skip[t] || c8 * 8 >= a.d)
 		return;
-	}
-	const int c4 = (b - t * c.cpt) * CF_THREADS + threadIdx.x; // float4 column
-	if (c.skip[t] || c4 * 4 >= a.d)
-		return;
-	const int k = a.k;
-	float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-	for (int j = 0; j < k; j++) {
-		if (c.topk_idx[t * k + j] < 0)
-			continue;
-		const float g = c.topk_w[t * k + j];
-		const float4 v = reinterpret_cast<const float4 *>(c.y + ((size_t)t * k + j) * a.d)[c4];
-		acc.x = __builtin_fmaf(g, v.x, acc.x);
-		acc.y = __builtin_fmaf(g, v.y, acc.y);
-		acc.z = __builtin_fmaf(g, v.z, acc.z);
-		acc.w = __builtin_fmaf(g, v.w, acc.w);
-	}
-	if (a.res) {
-		const float4 h = reinterpret_cast<const float4 *>(a.res + (size_t)t * a.d)[c4];
-		acc.x = h.x + acc.x;
-		acc.y = h.y + acc.y;
-		acc.z = h.z + acc.z;
-		acc.w = h.w + acc.w;
-	}
-	reinterpret_cast<float4 *>(a.out + (size_t)t * a.d)[c4] = acc;
+	combine8_cols<true>(t, c8, a.d, a.k, c.topk_w, c.topk_idx, c.y16, c.ysc, a.res, a.out);
 }
 
 // ---------------------------------------------------------------- launchers
@@ -1040,10 +1013,10 @@ bool combine_fix_preferred(const Layer &L)
 	return recompute_lds(L) <= 24 * 1024;
 }
 
-// The combine of the matrix-core path's y (tokens listed in skip left
+// The combine of the matrix-core path's f16 y (tokens listed in skip left
 // alone) and the exact recomputation of the listed tokens, in one launch.
 hipError_t launch_combine_fix(const Layer &L, const float *x, int k, const float *silu, const int32_t *topk_idx,
-			      const float *topk_w, const float *y, float *out, const float *res,
+			      const float *topk_w, const uint16_t *y16, int y_shift, float *out, const float *res,
 			      const int32_t *skip, const int32_t *list, const int32_t *count, int T, hipStream_t s)
 {
 	if (T == 0)
@@ -1069,13 +1042,13 @@ hipError_t launch_combine_fix(const Layer &L, const float *x, int k, const float
 	a.list = list;
 	a.count = count;
 	CombineFixArgs c;
-	c.w8 = TIE_CF_W8 && L.d % 8 == 0;
-	c.cpt = (L.d / (c.w8 ? 8 : 4) + CF_THREADS - 1) / CF_THREADS;
+	c.cpt = (L.d / 8 + CF_THREADS - 1) / CF_THREADS;
+	c.ysc = ldexpf(1.0f, y_shift);
 	c.ncomb = T * c.cpt;
 	c.nfix = T < 64 ? T : 64;
 	c.topk_w = topk_w;
 	c.topk_idx = topk_idx;
-	c.y = y;
+	c.y16 = y16;
 	c.skip = skip;
 	const size_t lds = recompute_lds(L);
 	const dim3 grid(c.ncomb + c.nfix);

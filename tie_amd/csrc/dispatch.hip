@@ -216,11 +216,33 @@ __global__ __launch_bounds__(256) void combine_kernel(int T, int d, int k, const
 	reinterpret_cast<float4 *>(out + (size_t)t * d)[c4] = acc;
 }
 
+// The same with 8 columns per thread for f16 y scaled by 2^-y_shift (the
+// matrix-core path's quantised down; combine8_cols)
+__global__ __launch_bounds__(256) void combine16_kernel(int T, int d, int k, const float *__restrict__ topk_w,
+							const int32_t *__restrict__ topk_idx, const uint16_t *__restrict__ y,
+							float ysc, const float *res, float *out, const int32_t *__restrict__ skip)
+{
+	const int t = blockIdx.y;
+	if (skip && skip[t])
+		return;
+	const int c8 = blockIdx.x * blockDim.x + threadIdx.x;
+	if (c8 * 8 >= d)
+		return;
+	combine8_cols<true>(t, c8, d, k, topk_w, topk_idx, y, ysc, res, out);
+}
+
 hipError_t launch_combine(int T, int d, int k, const float *topk_w, const int32_t *topk_idx, const float *y,
-			  float *out, hipStream_t s, const float *res, const int32_t *skip)
+			  float *out, hipStream_t s, const float *res, const int32_t *skip, bool y16, int y_shift)
 {
 	if (T == 0)
 		return hipSuccess;
+	if (y16) {
+		if (d % 8)
+			return hipErrorInvalidValue;
+		tie_launch(combine16_kernel, dim3((d / 8 + 255) / 256, T), dim3(256), 0, s, T, d, k, topk_w, topk_idx,
+			   reinterpret_cast<const uint16_t *>(y), ldexpf(1.0f, y_shift), res, out, skip);
+		return hipGetLastError();
+	}
 	const int n4 = d / 4;
 	tie_launch(combine_kernel, dim3((n4 + 255) / 256, T), dim3(256), 0, s, T, d, k, topk_w, topk_idx, y, res,
 			   out, skip);

@@ -187,7 +187,7 @@ static float f16_host(uint16_t h)
 	return (h & 0x8000u) ? -v : v;
 }
 
-int h_shift_estimate(int type, const uint8_t *b, size_t n_bytes, int d)
+double weight_mean_square(int type, const uint8_t *b, size_t n_bytes)
 {
 	double ss = 0.0;
 	size_t n = 0;
@@ -246,10 +246,32 @@ int h_shift_estimate(int type, const uint8_t *b, size_t n_bytes, int d)
 		}
 	}
 	if (n == 0 || !(ss > 0.0) || !std::isfinite(ss))
-		return 0;
-	const double h_typ = (double)d * (ss / (double)n); // (sqrt(d) rms)^2
-	int s = (int)lrint(log2(h_typ)) - 2;
-	return s < -24 ? -24 : s > 24 ? 24 : s;
+		return 0.0;
+	return ss / (double)n;
+}
+
+// The MFMA path's f16 scales of h and y (powers of two), from mean squares
+// of sampled gate and down weights, for RMS-normed inputs (|x| ~ 1):
+// a gate / up row sum is ~ sqrt(d) rms(w_gate), h = silu(g) u ~ d ms_gate,
+// y ~ sqrt(F) h rms(w_down).  h is stored as f16(h 2^-h_shift) with the
+// typical |h| near 2^2, y as f16(y 2^-y_shift) with the typical |y| near
+// 2^4: 2^14 and 2^12 below f16's largest value, 2^16 and 2^18 above its
+// smallest normal one.
+void f16_shifts(double ms_gate, double ms_down, int d, int F, int &h_shift, int &y_shift)
+{
+	auto clamp = [](int v) { return v < -24 ? -24 : v > 24 ? 24 : v; };
+	if (!(ms_gate > 0.0) || !std::isfinite(ms_gate)) {
+		h_shift = y_shift = 0;
+		return;
+	}
+	const double h_typ = (double)d * ms_gate;
+	h_shift = clamp((int)lrint(log2(h_typ)) - 2);
+	if (!(ms_down > 0.0) || !std::isfinite(ms_down)) {
+		y_shift = 0;
+		return;
+	}
+	const double y_typ = sqrt((double)F) * h_typ * sqrt(ms_down);
+	y_shift = clamp((int)lrint(log2(y_typ)) - 4);
 }
 
 } // namespace tie

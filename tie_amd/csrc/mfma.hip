@@ -55,13 +55,16 @@
 // h leaves the f16 range (|v| >= 65504, or not finite) is
 // listed by route_bucket_kernel / the gate/up epilogue and recomputed afterwards
 // in TIE's exact arithmetic (decode.hip), which overwrites its output row.
-// The expert outputs y are stored in fp32 (rounding them to bf16 would
-// add 2^-9 relative per element, the largest error term of the path).  With BF16 expert
+// The expert outputs y of the quantised kernels are stored as
+// f16(y * 2^-y_shift), the layer's y_shift chosen at upload so the typical
+// |y| sits near 2^4 (an 11-bit significand: bf16's 8 bits were the largest
+// error term of the path, 2^-9 relative); a token with a y outside the f16
+// range is recomputed like one whose x or h is.  With BF16 expert
 // weights (exact in bf16) the activations are split into a bf16 high part
 // and a bf16 remainder, stored as two bf16 planes (x by route_bucket_kernel, h
 // by the gate/up epilogue), two MFMAs per product; this keeps the products
 // to ~16 mantissa bits; that path is HBM-bound, so the extra MFMA work is
-// hidden.
+// hidden, and its y stays fp32.
 #include "common.h"
 #include "route.h"
 
@@ -157,8 +160,9 @@ struct MfmaArgs {
 	uint16_t *h16lo;         // gate/up out, split mode: bf16 remainder plane
 	int h_f16;               // gate/up out: h as f16(h * h_scale), pair-permuted K order (quantised down)
 	float h_scale;           // 2^-h_shift of the layer
-	float y_scale;           // down out (f16 operands): 2^(h_shift - F16_SHIFT) takes both factors out
-	float *y;                // down out, fp32 rows: y [pair][d] (experts), out [token][rows] (dense matrices)
+	float y_scale;           // down out (f16 operands): 2^(h_shift - F16_SHIFT [- y_shift]) takes the factors out
+	float *y;                // down out, fp32 rows: y [pair][d] (BF16 experts), out [token][rows] (dense matrices)
+	uint16_t *y16;           // down out (quantised experts): y [pair][d] as f16(y 2^-y_shift)
 	int mt_cap;              // pair rows per tile at most, below MT (0: MT; dense matrices at small T)
 	int32_t *tok_flag;       // [T] gate/up, h_f16: tokens whose h left the f16 range
 	int32_t *fix_list;       //     are appended here (once each) ...
@@ -608,9 +612,13 @@ struct ASrc {
 	const uint32_t *roff;  // LDS: this lane's ROFF_STRIDE row byte offsets
 };
 
+// The LDS offset of a generic pointer into LDS: a flat LDS address is the
+// shared aperture's base in the high 32 bits and the offset in the low 32,
+// so truncation gives the offset (a cast to the LDS address space would add
+// a null-pointer test: a 64-bit compare and select per address).
 __device__ __forceinline__ uint32_t lds_addr(const void *p)
 {
-	return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+	return (uint32_t)(uintptr_t)p;
 }
 
 // 16 bytes from global memory to LDS address lds + 16 * lane.  Issued as
@@ -713,12 +721,32 @@ template <int TYPE, bool DOWN> struct Ops<TYPE, DOWN, true> {
 	}
 	__device__ static void deq(const BRegs<TYPE> &b, const F &f, const K16 &kc, int st, int s, V out[2])
 	{
+#if defined(TIE_DIAG_NODEQ)
+		// diagnostic timing build: raw words as operands, no dequantisation
+		if constexpr (TYPE == TIE_GGML_Q4_K) {
+			out[0] = __builtin_bit_cast(V, u32x4{b.q[0][0].x, b.q[0][0].y, b.q[0][1].x, b.q[0][1].y});
+			out[1] = __builtin_bit_cast(V, u32x4{b.q[1][0].x, b.q[1][0].y, b.q[1][1].x, b.q[1][1].y});
+		} else {
+			out[0] = __builtin_bit_cast(V, u32x4{b.ql[0][0].x, b.ql[0][0].y, b.qh[0][0].x, b.qh[0][0].y});
+			out[1] = __builtin_bit_cast(V, u32x4{b.ql[1][0].x, b.ql[1][0].y, b.qh[1][0].x, b.qh[1][0].y});
+		}
+		return;
+#endif
 		if constexpr (TYPE == TIE_GGML_Q4_K)
 			deq_step16(b, f, kc, s, out);
 		else
 			deq_step16_q6k(b, f, kc, st, s, out);
 	}
-	__device__ static f32x16 mma(V a, V b, f32x16 c) { return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0); }
+	__device__ static f32x16 mma(V a, V b, f32x16 c)
+	{
+#if defined(TIE_DIAG_NOMFMA)
+		// diagnostic timing build: one VALU op in place of the MFMA
+		c[0] += (float)a[0] * (float)b[0];
+		return c;
+#else
+		return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+#endif
+	}
 };
 
 // One stage of MFMAs over NMT live 32-row M tiles (BF16 weights, held in
@@ -1119,8 +1147,29 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 					const float4 v1 = *reinterpret_cast<const float4 *>(tl + r * LS + 8 * part + 4);
 					const int mrow = 32 * mt + 16 * half + r;
 					if (mrow < nrows) {
-						if (DOWN) {
-							// fp32 rows: y [pair][d] (experts) or out [token][rows] (dense)
+						if (DOWN && a.y16) {
+							// experts: y [pair][d] as f16(y 2^-y_shift); a value
+							// outside the f16 range sends the pair's token to
+							// the exact recomputation
+							const f16x8 yv = {(_Float16)v0.x, (_Float16)v0.y, (_Float16)v0.z, (_Float16)v0.w,
+									  (_Float16)v1.x, (_Float16)v1.y, (_Float16)v1.z, (_Float16)v1.w};
+							uint16_t *yr = a.y16 + (size_t)spair[mrow] * a.rows + slab * DN_COLS + 64 * w + 8 * part;
+							*reinterpret_cast<f16x8 *>(yr) = yv;
+							const float m = __builtin_fmaxf(
+								__builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(v0.x), __builtin_fabsf(v0.y)),
+										__builtin_fmaxf(__builtin_fabsf(v0.z), __builtin_fabsf(v0.w))),
+								__builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(v1.x), __builtin_fabsf(v1.y)),
+										__builtin_fmaxf(__builtin_fabsf(v1.z), __builtin_fabsf(v1.w))));
+							// fmax drops NaN: the sum of the eight is NaN if any is
+							const bool nan = (v0.x + v0.y + v0.z + v0.w + v1.x + v1.y + v1.z + v1.w) !=
+									 (v0.x + v0.y + v0.z + v0.w + v1.x + v1.y + v1.z + v1.w);
+							if (nan || !(m < 65504.0f)) {
+								const int tok = spair[mrow] / a.k;
+								if (a.tok_flag[tok] == 0) // listed already: no atomic
+									flag_token(a.tok_flag, a.fix_list, a.fix_count, tok);
+							}
+						} else if (DOWN) {
+							// fp32 rows: out [token][rows] (dense matrices)
 							float *orow = a.y + (size_t)spair[mrow] * a.rows + slab * DN_COLS + 64 * w + 8 * part;
 							*reinterpret_cast<float4 *>(orow) = v0;
 							*reinterpret_cast<float4 *>(orow + 4) = v1;
@@ -1589,8 +1638,9 @@ hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, con
 	a.silu = silu;
 	a.y = ws.y;
 	a.h_f16 = TIE_MFMA_F16 && (L.down.type == TIE_GGML_Q4_K || L.down.type == TIE_GGML_Q6_K);
+	a.y16 = a.h_f16 ? reinterpret_cast<uint16_t *>(ws.y) : nullptr;
 	a.h_scale = ldexpf(1.0f, -L.h_shift);
-	a.y_scale = ldexpf(1.0f, L.h_shift - F16_SHIFT);
+	a.y_scale = ldexpf(1.0f, L.h_shift - F16_SHIFT - L.y_shift);
 	a.tok_flag = ws.tok_flag;
 	a.fix_list = ws.fix_list;
 	a.fix_count = ws.fix_count;

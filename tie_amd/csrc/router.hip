@@ -218,9 +218,13 @@ constexpr int RT_IB = TIE_RT_IB < RT_KC / 8 ? TIE_RT_IB : RT_KC / 8; // K steps 
 #define TIE_RT_MIN_T 256
 #endif
 
+// The LDS offset of a generic pointer into LDS: a flat LDS address is the
+// shared aperture's base in the high 32 bits and the offset in the low 32,
+// so truncation gives the offset (a cast to the LDS address space would add
+// a null-pointer test: a 64-bit compare and select per address).
 __device__ __forceinline__ uint32_t rt_lds_addr(const void *p)
 {
-	return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+	return (uint32_t)(uintptr_t)p;
 }
 
 // 16 bytes from global memory to LDS address lds + 16 * lane (inline asm:
