@@ -283,6 +283,11 @@ int tie_hip_stream_status(void *stream);
  * workgroup still exits): the error path of tie_hip_stream_status. */
 void tie_hip_debug_decode_give_up(int n);
 
+/* Debug: the powers of two the layer's matrix-core path scales h and y by
+ * (h stored as f16(h 2^-h_shift), y as f16(y 2^-y_shift)), chosen at
+ * upload from samples of the gate and down weights. */
+int tie_hip_debug_layer_shifts(const tie_hip_layer *layer, int *h_shift, int *y_shift);
+
 /* Make the n-th next device allocation fail with TIE_HIP_ENOMEM (n >= 1;
  * 0 disarms).  Host-side fault injection for error-path tests. */
 void tie_hip_debug_fail_alloc(int n);

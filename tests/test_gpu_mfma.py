@@ -456,3 +456,24 @@ def test_dense_mat_mat_mfma_limits():
     torch.cuda.synchronize()
     np.testing.assert_array_equal(bits(out.cpu().numpy()), bits(bind.mat_mat(x, w, synth.Q4_K, rows)))
     M.close()
+
+
+def test_f16_scales_from_device_and_host_sources():
+    """The powers of two the matrix-core path scales h and y by are chosen
+    at upload from samples of the gate and down weights; a layer uploaded
+    from device memory gets the same ones as from host memory, and they
+    put the typical |h|, |y| well inside f16's range (30B shape: h near
+    2^14 before scaling, y near 2^21)."""
+    import torch
+    c = synth.CONFIGS["30b_t2048"]
+    layer = synth_layer(c["seed"], c["d"], c["F"], c["E"], c["gu_type"], c["down_type"], None)
+    Lh = tie_amd.Layer.from_synth(layer)
+    dev = [torch.from_numpy(np.ascontiguousarray(a)).cuda() for a in (layer.router, layer.gate, layer.up, layer.down)]
+    Ld = tie_amd.Layer(layer.d, layer.F, layer.E, *dev, layer.gate_type, layer.up_type, layer.down_type,
+                       on_device=True)
+    hs, ys = Lh.shifts()
+    print("shifts host %s device %s" % ((hs, ys), Ld.shifts()), flush=True)
+    assert Ld.shifts() == (hs, ys)
+    assert 8 <= hs <= 16 and 12 <= ys <= 22
+    Lh.close()
+    Ld.close()

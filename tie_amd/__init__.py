@@ -31,7 +31,7 @@ EXPORTS = (
     "tie_hip_moe_forward", "tie_hip_exact_max_tokens", "tie_hip_set_exact_max_tokens",
     "tie_hip_debug_fail_alloc", "tie_hip_host_expf", "tie_hip_profile_enable", "tie_hip_profile_read",
     "tie_hip_moe_forward_noalloc", "tie_hip_stream_status", "tie_hip_debug_decode_give_up",
-    "tie_hip_stream_release",
+    "tie_hip_stream_release", "tie_hip_debug_layer_shifts",
 )
 
 
@@ -129,6 +129,8 @@ def lib():
         L.tie_hip_debug_fail_alloc.restype = None
         L.tie_hip_host_expf.argtypes = [P, P, ctypes.c_size_t]
         L.tie_hip_host_expf.restype = None
+        L.tie_hip_debug_layer_shifts.argtypes = [P, P, P]
+        L.tie_hip_debug_layer_shifts.restype = I
         L.tie_hip_stream_release.argtypes = [P]
         L.tie_hip_stream_release.restype = I
         L.tie_hip_stream_status.argtypes = [P]
@@ -374,6 +376,12 @@ class Layer:
 
     def nbytes(self):
         return lib().tie_hip_layer_bytes(self.handle)
+
+    def shifts(self):
+        """(h_shift, y_shift): the matrix-core path's f16 scales of h and y."""
+        h, y = ctypes.c_int(0), ctypes.c_int(0)
+        check(lib().tie_hip_debug_layer_shifts(self.handle, ctypes.byref(h), ctypes.byref(y)))
+        return h.value, y.value
 
     def forward(self, x_dev, T, k, out_dev, topk_idx_dev=None, topk_w_dev=None, flags=PATH_AUTO, stream=None):
         """Enqueue the block on device pointers (torch tensors or ints)."""

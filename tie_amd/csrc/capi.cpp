@@ -433,26 +433,32 @@ static int create_layer(const tie_hip_layer_desc *ds, tie_hip_layer **out)
 		e = hipStreamSynchronize(g.stream);
 	if (e == hipSuccess && rc == 0) {
 		// the f16 scales of h and y from samples of the gate and down
-		// weights: up to 4096 super-blocks (BF16: 256-weight runs) evenly
-		// strided over the whole tensor (every expert), gathered in one
-		// strided copy each (host or device source: unified addressing)
-		auto sample_ms = [&](int type, const void *src, size_t tensor_bytes, double &ms) {
+		// weights: a run of super-blocks (BF16: 256-weight runs) from the
+		// middle of each of up to 128 experts, E plain copies (host or
+		// device source: unified addressing)
+		auto sample_ms = [&](int type, const void *src, size_t expert_bytes, double &ms) {
 			const size_t bb = type == TIE_GGML_Q4_K ? Q4K_BYTES : type == TIE_GGML_Q6_K ? Q6K_BYTES : 2 * QK;
-			const size_t nblk = tensor_bytes / bb;
+			const size_t per = std::min<size_t>(expert_bytes / bb, 32); // blocks per expert
+			const int nexp = E < 128 ? E : 128, estep = E / nexp;
 			ms = 0.0;
-			if (nblk == 0)
+			if (per == 0)
 				return hipSuccess;
-			const size_t cnt = std::min<size_t>(nblk, 4096), step = nblk / cnt;
-			std::vector<uint8_t> smp(cnt * bb);
-			const hipError_t err = hipMemcpy2D(smp.data(), bb, src, step * bb, bb, cnt, hipMemcpyDefault);
-			if (err == hipSuccess)
-				ms = weight_mean_square(type, smp.data(), smp.size());
-			return err;
+			std::vector<uint8_t> smp((size_t)nexp * per * bb);
+			for (int i = 0; i < nexp; i++) {
+				const size_t off = (size_t)(i * estep) * expert_bytes + (expert_bytes / bb / 2) * bb;
+				const size_t n = std::min(per * bb, (size_t)E * expert_bytes - off);
+				const hipError_t err = hipMemcpy(smp.data() + (size_t)i * per * bb, (const uint8_t *)src + off,
+								 n, hipMemcpyDefault);
+				if (err != hipSuccess)
+					return err;
+			}
+			ms = weight_mean_square(type, smp.data(), smp.size());
+			return hipSuccess;
 		};
 		double ms_g = 0.0, ms_d = 0.0;
-		e = sample_ms(ds->gate_type, ds->gate_exps, L.gate.expert_bytes * E, ms_g);
+		e = sample_ms(ds->gate_type, ds->gate_exps, L.gate.expert_bytes, ms_g);
 		if (e == hipSuccess)
-			e = sample_ms(ds->down_type, ds->down_exps, L.down.expert_bytes * E, ms_d);
+			e = sample_ms(ds->down_type, ds->down_exps, L.down.expert_bytes, ms_d);
 		if (e == hipSuccess)
 			f16_shifts(ms_g, ms_d, d, F, L.h_shift, L.y_shift);
 	}
@@ -1206,6 +1212,15 @@ extern "C" void tie_hip_debug_decode_give_up(int n)
 {
 	std::lock_guard<std::recursive_mutex> lk(g.mu);
 	g.debug_stale = n > 0 ? n : 0;
+}
+
+extern "C" int tie_hip_debug_layer_shifts(const tie_hip_layer *layer, int *h_shift, int *y_shift)
+{
+	if (!layer || !h_shift || !y_shift)
+		return set_error(TIE_HIP_EINVAL, "null argument");
+	*h_shift = layer->L.h_shift;
+	*y_shift = layer->L.y_shift;
+	return TIE_HIP_OK;
 }
 
 extern "C" void tie_hip_debug_fail_alloc(int n)

@@ -1163,9 +1163,12 @@ static void one_shape(const Layer &L, int k, int &rpr, int &rg, int &rd, int &th
 	lds = std::max(lds_r, std::max(lds_g, lds_d));
 }
 
+#ifndef TIE_ONE_MAX_D
+#define TIE_ONE_MAX_D 1048576
+#endif
 bool decode_one_supported(const Layer &L, int k)
 {
-	if (!decode_supported(L, k) || L.E > INLINE_E)
+	if (!decode_supported(L, k) || L.E > INLINE_E || L.d > TIE_ONE_MAX_D)
 		return false;
 	int rpr, rg, rd, threads;
 	size_t lds;
