@@ -23,7 +23,12 @@ def device():
     import torch
     assert torch.cuda.is_available(), "GPU test without a GPU"
     tie_amd.init(0)
+    # the host drop-in (TIE_HIP_PATH_AUTO) on the exact path for every batch
+    # these tests run (up to 64 tokens)
+    old = tie_amd.lib().tie_hip_exact_max_tokens()
+    tie_amd.lib().tie_hip_set_exact_max_tokens(64)
     yield
+    tie_amd.lib().tie_hip_set_exact_max_tokens(old)
     tie_amd.shutdown()
 
 

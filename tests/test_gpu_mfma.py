@@ -30,7 +30,7 @@ from tie_amd import synth
 pytestmark = pytest.mark.gpu
 
 # Quantised weights against the fp32 oracle: relative L2 and max |err| /
-# max |ref| both <= 1e-3 (the f16 operands' rounding: about 6.5e-4 of
+# max |ref| both <= 1e-3 (the f16 operands' rounding: about 5.5e-4 of
 # either, from the weights, x, h and y), and rel. L2 against the float64
 # model of the kernels' own operands
 ORACLE_RL2 = 1e-3
@@ -69,8 +69,9 @@ def sig11(a):
 
 def q4k_f16(buf):
     """Q4_K weights as the f16 kernels form them, divided by their factor
-    256: per sub-block D = d*sc and M = -dmin*m in fp32 (exact), times 256
-    rounded to f16, then code*D16 + M16 rounded once to f16 (v_pk_fma_f16).
+    256: per sub-block M = -dmin*m*256 rounded to f16, then (code*sc)*(d*256)
+    + M16 rounded once to f16 (code*sc and d*256 exact in f16;
+    v_pk_fma_f16).
     Super-block layout (TIE's block_q4_K): d, dmin (f16), 12 scale bytes,
     128 code bytes; sub-block 2g holds the low and 2g+1 the high nibbles of
     code bytes 32g..32g+31."""
@@ -87,9 +88,8 @@ def q4k_f16(buf):
     for j in range(4, 8):
         sc[:, j] = (s[:, j + 4] & 15) | ((s[:, j - 4] >> 6) << 4)
         mn[:, j] = (s[:, j + 4] >> 4) | ((s[:, j] >> 6) << 4)
-    D = (d[:, None] * sc.astype(np.float32)).astype(np.float32)
+    D16 = (d[:, None].astype(np.float64) * 256) * sc.astype(np.float64)  # exact: (code sc) (d 256) in the fma
     M = -(dmin[:, None] * mn.astype(np.float32)).astype(np.float32)
-    D16 = f16(D * 256).astype(np.float64)
     M16 = f16(M * 256).astype(np.float64)
     qs = b[:, 16:].reshape(nb, 4, 32)
     q = np.stack([qs & 15, qs >> 4], axis=2).reshape(nb, 8, 32).astype(np.float64)
@@ -99,8 +99,8 @@ def q4k_f16(buf):
 
 def q6k_f16(buf):
     """Q6_K weights as the f16 kernels form them, divided by their factor 256:
-    D = d*sc in fp32 (exact), D*256 rounded to f16, then (code - 32)*D16
-    rounded once to f16 (v_pk_mul_f16).  Super-block layout (TIE's
+    (code - 32)*sc in f16 (exact for |sc| <= 64, as in these blocks), times
+    d*256 (exact), rounded once to f16 (v_pk_mul_f16).  Super-block layout (TIE's
     block_q6_K): ql[128], qh[64], int8 scales[16], d (f16); half n, l < 32:
     weights 128n + l + 32i take ql nibble (ql[64n + l + 32(i%2)], low for
     i < 2), qh bits 2i of qh[32n + l], scale 8n + l//16 + 2i."""
@@ -118,8 +118,8 @@ def q6k_f16(buf):
             nib = nib & 15 if i < 2 else nib >> 4
             q[:, 128 * n + 32 * i + l] = nib | (((qh[:, 32 * n + l] >> (2 * i)) & 3) << 4)
             s[:, 128 * n + 32 * i + l] = sc[:, 8 * n + l // 16 + 2 * i]
-    D16 = f16((d[:, None] * s).astype(np.float32) * 256).astype(np.float64)
-    W = ((q - 32).astype(np.float64) * D16).astype(np.float16)  # exact in float64, one rounding
+    qs = f16((q - 32).astype(np.float32) * s).astype(np.float64)  # (code - 32) sc: exact when |sc| <= 64
+    W = (qs * (d[:, None].astype(np.float64) * 256)).astype(np.float16)  # one rounding
     return W.astype(np.float32).reshape(-1) / 256
 
 
@@ -477,3 +477,22 @@ def test_f16_scales_from_device_and_host_sources():
     assert 8 <= hs <= 16 and 12 <= ys <= 22
     Lh.close()
     Ld.close()
+
+
+def test_auto_path_threshold():
+    """TIE_HIP_PATH_AUTO: TIE's exact kernels up to tie_hip_exact_max_tokens()
+    tokens (24 by default; bit-exact), the matrix cores above (the 16-bit
+    bound), through the host drop-in."""
+    assert tie_amd.lib().tie_hip_exact_max_tokens() == 24
+    c = synth.CONFIGS["30b_t32"]
+    layer = synth_layer(c["seed"], c["d"], c["F"], c["E"], c["gu_type"], c["down_type"], None)
+    for T in (24, 25, 32):
+        x = synth.make_input(400 + T, T, c["d"])
+        print("auto T=%d" % T, flush=True)
+        out, idx, w = tie_amd.moe_ffn(x, layer, c["k"])
+        ro, ri, rw = bind.moe_block(layer, x, c["k"])
+        check_routing(idx, w, ri, rw)
+        if T <= 24:
+            np.testing.assert_array_equal(bits(out), bits(ro))
+        else:
+            check_oracle("auto_T%d" % T, out, ro)

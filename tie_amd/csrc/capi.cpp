@@ -60,7 +60,10 @@ struct Ctx {
 	size_t io_tokens = 0, io_d = 0, io_k = 0;
 	uint32_t *rsq = nullptr;   // host RSQRTSS table (built at the first residual call)
 	int rsq_bits = 0;
-	int exact_max_t = 64;
+	// TIE_HIP_PATH_AUTO: TIE's bit-exact kernels up to this many tokens,
+	// the matrix cores above (measured faster from T = 25 on at the 30B
+	// shape: T=24 0.111 / 0.115 ms, T=32 0.134 / 0.119 ms exact / MFMA)
+	int exact_max_t = 24;
 	int debug_stale = 0; // one-launch decode calls left whose waits are made to give up (debug hook)
 	std::recursive_mutex mu;
 };
@@ -533,14 +536,13 @@ static int forward(tie_hip_layer *layer, const float *x, int T, int k, float *ou
 			// left the f16 range (listed by the kernels above; usually
 			// none), which are recomputed exactly in the same launch, from
 			// res as it was (res may be out)
-			HIP_TRY(launch_combine_fix(L, x, k, g.silu, ws.topk_idx, ws.topk_w,
-						   reinterpret_cast<const uint16_t *>(ws.y), L.y_shift, out, res, ws.tok_flag,
-						   ws.fix_list, ws.fix_count, T, s));
+			HIP_TRY(launch_combine_fix(L, x, k, g.silu, ws.topk_idx, ws.topk_w, ws.y, TIE_MFMA_Y16 != 0, L.y_shift,
+						   out, res, ws.tok_flag, ws.fix_list, ws.fix_count, T, s));
 		} else {
 			// the same in two launches (the recomputation's LDS would cost
 			// the combine occupancy); the combine skips the listed tokens
 			prof_begin("combine", s);
-			const bool y16 = mfma_f16_operands(L) && L.down.type != TIE_GGML_BF16;
+			const bool y16 = TIE_MFMA_Y16 && mfma_f16_operands(L) && L.down.type != TIE_GGML_BF16;
 			HIP_TRY(launch_combine(T, L.d, k, ws.topk_w, ws.topk_idx, ws.y, out, s, res,
 					       mfma_f16_operands(L) ? ws.tok_flag : nullptr, y16, L.y_shift));
 			prof_end(s);

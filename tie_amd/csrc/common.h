@@ -124,6 +124,13 @@ struct ZeroArgs {
 };
 hipError_t launch_router_logits(const Layer &L, const float *x, int T, float *logits, hipStream_t s,
 				ZeroArgs z = ZeroArgs());
+// The matrix-core path's quantised down stores y as f16 scaled by the
+// layer's 2^-y_shift (1) or as fp32 (0): f16 halves the bytes the down
+// kernel writes and the combine reads, and adds 2^-12 relative rounding
+// per element (about 2e-4 relative L2 at the block's output)
+#ifndef TIE_MFMA_Y16
+#define TIE_MFMA_Y16 1
+#endif
 // the matrix-core path's selection, grouping into per-expert buckets and
 // A-operand conversion (mfma.hip)
 hipError_t launch_route_bucket(const Layer &L, const float *x, int T, int k, Workspace &ws, hipStream_t s);
@@ -158,7 +165,7 @@ hipError_t launch_recompute(const Layer &L, const float *x, int k, const float *
 // when combine_fix_preferred
 bool combine_fix_preferred(const Layer &L);
 hipError_t launch_combine_fix(const Layer &L, const float *x, int k, const float *silu, const int32_t *topk_idx,
-			      const float *topk_w, const uint16_t *y16, int y_shift, float *out, const float *res,
+			      const float *topk_w, const void *y, bool y16, int y_shift, float *out, const float *res,
 			      const int32_t *skip, const int32_t *list, const int32_t *count, int T, hipStream_t s);
 
 hipError_t launch_decode(const Layer &L, const float *x, int k, const float *silu, const float *logits,

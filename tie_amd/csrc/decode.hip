@@ -872,7 +872,7 @@ __global__ __launch_bounds__(DEC_MAX_THREADS) void recompute_kernel(DecodeArgs a
 
 // The matrix-core path's last launch: the combine of every token not listed
 // for recomputation (combine8_cols: out[t][c] = [res +] sum_j fma(g_j,
-// y_j[c], .) in slot order, y as f16 scaled by 2^-y_shift), and, in
+// y_j[c], .) in slot order, y fp32 or f16 scaled by 2^-y_shift), and, in
 // workgroups of their own, the exact recomputation of the listed ones
 // (usually none) -- one launch instead of two.  Workgroups [0, ncomb):
 // token b / cpt, 2048 columns each (8 per thread); [ncomb, ncomb + nfix):
@@ -882,7 +882,8 @@ struct CombineFixArgs {
 	float ysc; // 2^y_shift
 	const float *topk_w;
 	const int32_t *topk_idx;
-	const uint16_t *y16;
+	const uint16_t *y16; // f16 y (TIE_MFMA_Y16), or
+	const float *y32;    // fp32 y
 	const int32_t *skip;
 };
 constexpr int CF_THREADS = 256;
@@ -900,7 +901,10 @@ __global__ __launch_bounds__(CF_THREADS) void combine_fix_kernel(DecodeArgs a, C
 	const int c8 = (b - t * c.cpt) * CF_THREADS + threadIdx.x;
 	if (c.skip[t] || c8 * 8 >= a.d)
 		return;
-	combine8_cols<true>(t, c8, a.d, a.k, c.topk_w, c.topk_idx, c.y16, c.ysc, a.res, a.out);
+	if (c.y16)
+		combine8_cols<true>(t, c8, a.d, a.k, c.topk_w, c.topk_idx, c.y16, c.ysc, a.res, a.out);
+	else
+		combine8_cols<false>(t, c8, a.d, a.k, c.topk_w, c.topk_idx, c.y32, 1.0f, a.res, a.out);
 }
 
 // ---------------------------------------------------------------- launchers
@@ -1016,7 +1020,7 @@ bool combine_fix_preferred(const Layer &L)
 // The combine of the matrix-core path's f16 y (tokens listed in skip left
 // alone) and the exact recomputation of the listed tokens, in one launch.
 hipError_t launch_combine_fix(const Layer &L, const float *x, int k, const float *silu, const int32_t *topk_idx,
-			      const float *topk_w, const uint16_t *y16, int y_shift, float *out, const float *res,
+			      const float *topk_w, const void *y, bool y16, int y_shift, float *out, const float *res,
 			      const int32_t *skip, const int32_t *list, const int32_t *count, int T, hipStream_t s)
 {
 	if (T == 0)
@@ -1048,7 +1052,8 @@ hipError_t launch_combine_fix(const Layer &L, const float *x, int k, const float
 	c.nfix = T < 64 ? T : 64;
 	c.topk_w = topk_w;
 	c.topk_idx = topk_idx;
-	c.y16 = y16;
+	c.y16 = y16 ? reinterpret_cast<const uint16_t *>(y) : nullptr;
+	c.y32 = y16 ? nullptr : reinterpret_cast<const float *>(y);
 	c.skip = skip;
 	const size_t lds = recompute_lds(L);
 	const dim3 grid(c.ncomb + c.nfix);

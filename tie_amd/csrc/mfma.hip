@@ -161,6 +161,7 @@ struct MfmaArgs {
 	int h_f16;               // gate/up out: h as f16(h * h_scale), pair-permuted K order (quantised down)
 	float h_scale;           // 2^-h_shift of the layer
 	float y_scale;           // down out (f16 operands): 2^(h_shift - F16_SHIFT [- y_shift]) takes the factors out
+				 // (y_shift only for f16 y)
 	float *y;                // down out, fp32 rows: y [pair][d] (BF16 experts), out [token][rows] (dense matrices)
 	uint16_t *y16;           // down out (quantised experts): y [pair][d] as f16(y 2^-y_shift)
 	int mt_cap;              // pair rows per tile at most, below MT (0: MT; dense matrices at small T)
@@ -460,7 +461,8 @@ __device__ __forceinline__ void group_factors(const BRegs<TYPE> &b, int st, int 
 constexpr int F16_SHIFT = 8;
 
 struct Fac16 {
-	f16x2 DM[2][2]; // [row][sub-block]: (D * 2^S or D * 2^(S-4) for the high nibbles, M * 2^S)
+	f16x2 SN[2][2]; // [row][sub-block]: (sc, -1024 sc), or (sc / 16, -64 sc) for the high nibbles
+	f16x2 DM[2][2]; // [row][sub-block]: (d * 2^S, M * 2^S), M = -dmin * m
 };
 
 __device__ __forceinline__ f16x2 splat16(float v)
@@ -469,16 +471,20 @@ __device__ __forceinline__ f16x2 splat16(float v)
 	return f16x2{h, h};
 }
 
-// In packed f16: (d, dmin) * (2^S, -2^S) (exact), the sub-block's 6-bit
-// (sc, m) as f16 (in the mantissa of 1024.0, minus 1024), then one product:
-// (d*sc*2^S, -dmin*m*2^S), each rounded once from its exact value -- the
-// same f16 values as rounding the fp32 D and M.
+// In packed f16, exactly: the sub-block's 6-bit (sc, m) (in the mantissa
+// of 1024.0, minus 1024), (sc, -1024 sc) (low nibbles) or (sc / 16, -64 sc)
+// (high nibbles, which the dequantisation holds as 16 q), and d * 2^S; then
+// M = -dmin * m * 2^S, rounded once.  The weight is then
+// (q sc) d 2^S + M with q sc exact and one rounding (deq_step16), not
+// q (d sc) + M with d sc rounded to f16 first: that rounding, shared by the
+// 32 weights of a sub-block, was half of the weights' error.
 template <int TYPE>
 __device__ __forceinline__ void group_factors16(const BRegs<TYPE> &b, int st, int gi, Fac16 &f)
 {
 	const f16x2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
-	const f16x2 s0 = {(_Float16)(float)(1 << F16_SHIFT), (_Float16)(-(float)(1 << F16_SHIFT))};
-	const f16x2 s1 = {(_Float16)(float)(1 << (F16_SHIFT - 4)), (_Float16)(-(float)(1 << F16_SHIFT))};
+	const f16x2 sn0 = {(_Float16)1.0f, (_Float16)(-1024.0f)};
+	const f16x2 sn1 = {(_Float16)(1.0f / 16), (_Float16)(-64.0f)};
+	const f16x2 sdm = {(_Float16)(float)(1 << F16_SHIFT), (_Float16)(-(float)(1 << F16_SHIFT))};
 #pragma unroll
 	for (int j = 0; j < 2; j++) {
 		const int g = (4 / Cfg<TYPE>::SPB) * (st % Cfg<TYPE>::SPB) + gi;
@@ -488,7 +494,8 @@ __device__ __forceinline__ void group_factors16(const BRegs<TYPE> &b, int st, in
 			uint32_t sc, mn;
 			q4k_scale_min(b.sc[j], 2 * g + u, sc, mn);
 			const f16x2 sm = __builtin_bit_cast(f16x2, (sc | (mn << 16)) | 0x64006400u) - k1024;
-			f.DM[j][u] = sm * (dd * (u ? s1 : s0));
+			f.SN[j][u] = f16x2{sm[0], sm[0]} * (u ? sn1 : sn0);
+			f.DM[j][u] = f16x2{(_Float16)1.0f, sm[1]} * dd * sdm;
 		}
 	}
 }
@@ -508,7 +515,6 @@ __device__ __forceinline__ K16 k16_consts()
 __device__ __forceinline__ void deq_step16(const BRegs<TIE_GGML_Q4_K> &b, const Fac16 &f, const K16 &kc, int s,
 					   f16x8 out[2])
 {
-	const f16x2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
 #pragma unroll
 	for (int j = 0; j < 2; j++) {
 		const int sub = s & 3, u = sub >> 1;
@@ -518,9 +524,11 @@ __device__ __forceinline__ void deq_step16(const BRegs<TIE_GGML_Q4_K> &b, const 
 		f16x2 r[4];
 #pragma unroll
 		for (int i = 0; i < 4; i++) {
-			const f16x2 v = __builtin_bit_cast(f16x2, (w[i] & msk) | kc.magic) - k1024;
-			const f16x2 dm = f.DM[j][u];
-			r[i] = __builtin_elementwise_fma(v, f16x2{dm[0], dm[0]}, f16x2{dm[1], dm[1]});
+			// v = 1024 + q (low nibbles) or 1024 + 16 q (high); q sc exact
+			const f16x2 v = __builtin_bit_cast(f16x2, (w[i] & msk) | kc.magic);
+			const f16x2 sn = f.SN[j][u], dm = f.DM[j][u];
+			const f16x2 qs = __builtin_elementwise_fma(v, f16x2{sn[0], sn[0]}, f16x2{sn[1], sn[1]});
+			r[i] = __builtin_elementwise_fma(qs, f16x2{dm[0], dm[0]}, f16x2{dm[1], dm[1]});
 		}
 		out[j] = f16x8{r[0][0], r[0][1], r[1][0], r[1][1], r[2][0], r[2][1], r[3][0], r[3][1]};
 	}
@@ -582,12 +590,15 @@ __device__ __forceinline__ void deq_step16_q6k(const BRegs<TIE_GGML_Q6_K> &b, co
 		const uint32_t hi = ((ql.y >> nsh) & 0x0f0f0f0fu) | (qhs(qh.y) & 0xf0f0f0f0u);
 		const int si = lh + 2 * r;
 		const uint32_t sw = si < 4 ? b.sc[j].x : b.sc[j].y;
-		const f16x2 D = splat16(f.d6[j] * (float)(int8_t)((sw >> (8 * (si & 3))) & 0xffu) * (float)(1 << F16_SHIFT));
+		// (q - 32) sc exact in f16 (|sc| <= 64: |(q - 32) sc| <= 2048), then
+		// times d 2^S with one rounding: d sc is not rounded to f16 first
+		const f16x2 SC = splat16((float)(int8_t)((sw >> (8 * (si & 3))) & 0xffu));
+		const f16x2 D = splat16(f.d6[j] * (float)(1 << F16_SHIFT));
 		const uint32_t w[4] = {lo, lo >> 8, hi, hi >> 8};
 		f16x2 q[4];
 #pragma unroll
 		for (int i = 0; i < 4; i++)
-			q[i] = (__builtin_bit_cast(f16x2, (w[i] & kc.q6) | kc.magic) - k1056) * D;
+			q[i] = ((__builtin_bit_cast(f16x2, (w[i] & kc.q6) | kc.magic) - k1056) * SC) * D;
 		out[j] = f16x8{q[0][0], q[0][1], q[1][0], q[1][1], q[2][0], q[2][1], q[3][0], q[3][1]};
 	}
 }
@@ -1638,9 +1649,9 @@ hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, con
 	a.silu = silu;
 	a.y = ws.y;
 	a.h_f16 = TIE_MFMA_F16 && (L.down.type == TIE_GGML_Q4_K || L.down.type == TIE_GGML_Q6_K);
-	a.y16 = a.h_f16 ? reinterpret_cast<uint16_t *>(ws.y) : nullptr;
+	a.y16 = TIE_MFMA_Y16 && a.h_f16 ? reinterpret_cast<uint16_t *>(ws.y) : nullptr;
 	a.h_scale = ldexpf(1.0f, -L.h_shift);
-	a.y_scale = ldexpf(1.0f, L.h_shift - F16_SHIFT - L.y_shift);
+	a.y_scale = ldexpf(1.0f, L.h_shift - F16_SHIFT - (a.y16 ? L.y_shift : 0));
 	a.tok_flag = ws.tok_flag;
 	a.fix_list = ws.fix_list;
 	a.fix_count = ws.fix_count;

@@ -153,6 +153,8 @@ CONFIGS = {
     "30b_t2": dict(d=2048, F=768, E=128, k=8, T=2, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1242),
     "30b_t4": dict(d=2048, F=768, E=128, k=8, T=4, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1244),
     "30b_t8": dict(d=2048, F=768, E=128, k=8, T=8, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1240),
+    "30b_t16": dict(d=2048, F=768, E=128, k=8, T=16, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1252),
+    "30b_t24": dict(d=2048, F=768, E=128, k=8, T=24, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1253),
     "30b_t32": dict(d=2048, F=768, E=128, k=8, T=32, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1235),
     "30b_t64": dict(d=2048, F=768, E=128, k=8, T=64, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1243),
     "30b_t128": dict(d=2048, F=768, E=128, k=8, T=128, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1245),
