@@ -37,6 +37,13 @@ constexpr int MFMA_MT_GU_SMALL = 64;
 #ifndef TIE_MFMA_SMALL_AVG
 #define TIE_MFMA_SMALL_AVG 32
 #endif
+// gate/up and down tiles of the tiny-tile kernels (32 rows; the LDS left
+// over holds more weight stages in flight), used up to TIE_MFMA_TINY_AVG
+// pairs per expert
+constexpr int MFMA_MT_TINY = 32;
+#ifndef TIE_MFMA_TINY_AVG
+#define TIE_MFMA_TINY_AVG 8
+#endif
 
 // Device layout of one stacked expert tensor [E][rows][in].
 //
@@ -182,6 +189,7 @@ hipError_t launch_decode_one(const Layer &L, const float *x, int k, const float 
 constexpr int ONE_SPIN_MAX = 1 << 18;
 struct Layer;
 int mfma_gu_rows(const Layer &L, int npairs); // rows per gate/up tile (the tile list's and the kernel's)
+int mfma_dn_rows(const Layer &L, int npairs); // rows per down tile
 // Dense F32-input matrix product through the expert GEMV kernels: out[t][r]
 // = W[r] . x[t] (W one "expert": rows, in, panel layout); dense_groups(T)
 // token groups (the workspace needs that many experts and T pairs)

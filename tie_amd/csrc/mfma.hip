@@ -109,14 +109,16 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 #ifndef TIE_MFMA_GU_WPE
 #define TIE_MFMA_GU_WPE 2
 #endif
-// three weight stage buffers where they fit (1), or always two (0).  Off:
-// stage barriers wait 5-9% of a workgroup's cycles at T = 2048, and a third
-// buffer measured within +-2% (30B T = 2048, 235B T = 1024)
+// workgroups (one wave per SIMD each) per CU of the tiny-tile kernels
+#ifndef TIE_MFMA_TINY_GU_WPC
+#define TIE_MFMA_TINY_GU_WPC 4
+#endif
+#ifndef TIE_MFMA_TINY_DN_WPC
+#define TIE_MFMA_TINY_DN_WPC 3
+#endif
+// BF16 weights: loaded into registers two stages ahead (1) or one (0)
 #ifndef TIE_BF16_B3
 #define TIE_BF16_B3 1
-#endif
-#ifndef TIE_MFMA_BBUF3
-#define TIE_MFMA_BBUF3 0
 #endif
 #ifndef TIE_MFMA_DN_WPE
 #define TIE_MFMA_DN_WPE 2
@@ -209,13 +211,22 @@ template <int TYPE, bool DOWN = false, int MTR = 0> struct Cfg {
 	// weight stage buffers: three (the weights of stage s + 2 in flight
 	// while stage s computes: an HBM round trip is longer than a stage)
 	// where they fit the budget of two workgroups per CU, else two
-	static constexpr int LDS_BUDGET = (160 * 1024) / (MTR ? 3 : 2); // per workgroup: 3 (small tiles) or 2 per CU
+	// workgroups per CU: the tiny-tile kernels TIE_MFMA_TINY_GU_WPC /
+	// _DN_WPC, the small-tile gate/up kernels 3, the others 2
+	static constexpr int WG_PER_CU = MTR == MFMA_MT_TINY ? (DOWN ? TIE_MFMA_TINY_DN_WPC : TIE_MFMA_TINY_GU_WPC)
+					 : MTR && !DOWN ? 3 : 2;
+	static constexpr int LDS_BUDGET = (160 * 1024) / WG_PER_CU;
 	static constexpr int ROFF_BYTES = 4 * RPI * NWAVES * 16 + 4 * MT; // row offsets + pair ids
-	static constexpr int NBB = (TIE_MFMA_BBUF3 && B_LDS && 2 * ABUF + 3 * BBUF + ROFF_BYTES <= LDS_BUDGET) ? 3 : 2;
+	// stage buffers (activations and weights; NS - 1 stages in flight): as
+	// many as the LDS budget of WG_PER_CU workgroups per CU allows, up to 4
+	// (quantised weights; BF16 weights go to registers: 2 activation buffers)
+	static constexpr int NS = !B_LDS ? 2
+				  : 4 * (ABUF + BBUF) + ROFF_BYTES <= LDS_BUDGET ? 4
+				  : 3 * (ABUF + BBUF) + ROFF_BYTES <= LDS_BUDGET ? 3 : 2;
 	static_assert(NWAVES == 4, "epilogue tile size");
 	// DMA instructions one wave issues per weight stage (dma_b)
 	static constexpr int B_DMA = NCH + (TYPE == TIE_GGML_Q6_K ? 1 : 0);
-	static constexpr int LDS_A = 2 * ABUF, LDS_B = NBB * BBUF;
+	static constexpr int LDS_A = NS * ABUF, LDS_B = B_LDS ? NS * BBUF : 0;
 	// the f16 kernels' epilogue tiles (gate/up: after the 32 KiB SiLU
 	// table) reuse the stage buffers; the dynamic LDS covers both
 	static constexpr int EPI_BYTES = (F16 && !SPLIT) ? (DOWN ? 0 : 32768) + NWAVES * 16 * (DOWN ? 72 : 40) * 4 : 0;
@@ -885,18 +896,23 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 		static_assert(C::NPL == 1 && C::NSTEP % 2 == 0, "one activation plane, even step count");
 		BDma<TYPE> bd;
 		bdma_init<TYPE, DOWN>(a, e, slab, w, bd);
-		auto abuf = [&](int st) { return As + (st & 1) * C::ABUF; };
-		auto bbuf = [&](int st) { return Bs + (st % C::NBB) * C::BBUF; };
-		// stage st's activations and, NBB - 1 stages ahead, weights (issued
-		// last: the barrier may leave them in flight)
+		constexpr int NS = C::NS;
+		auto abuf = [&](int st) { return As + (st % NS) * C::ABUF; };
+		auto bbuf = [&](int st) { return Bs + (st % NS) * C::BBUF; };
+		// stage st's activations and weights into buffers st % NS
 		auto issue = [&](int st) {
-			if (st < nk)
+			if (st < nk) {
 				dma_a<TYPE, DOWN, NMT, MTR>(as, st, w, abuf(st));
-			if (st + C::NBB - 2 < nk)
-				dma_b<TYPE, DOWN>(bd, slab, st + C::NBB - 2, w, bbuf(st + C::NBB - 2));
+				dma_b<TYPE, DOWN>(bd, slab, st, w, bbuf(st));
+			}
 		};
+		// direct loads one wave issues per stage (dma_a + dma_b)
+		constexpr int NLIVE = (32 * NMT + NWAVES * C::RPI - 1) / (NWAVES * C::RPI);
+		constexpr int PER = NLIVE * C::NPL + C::B_DMA;
+		static_assert((NS - 2) * PER < 64, "vmcnt field");
 		// end of stage st: stage st + 1's data landed (and this stage's LDS
-		// reads done); the weights of stage st + NBB - 1 may be in flight
+		// reads done); the loads of the up to NS - 2 stages issued after it
+		// may stay in flight (loads complete in order)
 #ifdef TIE_MFMA_TRACE
 		unsigned long long bwait = 0;
 #endif
@@ -904,8 +920,11 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 #ifdef TIE_MFMA_TRACE
 			const unsigned long long tb = __builtin_readcyclecounter();
 #endif
-			if (C::NBB == 3 && st + 2 < nk)
-				stage_barrier_keep<C::B_DMA>();
+			const int keep = min(NS - 2, nk - 2 - st);
+			if (NS >= 4 && keep >= 2)
+				stage_barrier_keep<(NS >= 4 ? 2 * PER : 0)>();
+			else if (NS >= 3 && keep >= 1)
+				stage_barrier_keep<(NS >= 3 ? PER : 0)>();
 			else
 				stage_barrier();
 #ifdef TIE_MFMA_TRACE
@@ -938,7 +957,8 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 			}
 		};
 		constexpr int L = (C::NSTEP - 1) & 1; // slot of a stage's last step
-		// all steps but the last of stage st (the next stage's DMA with more)
+		// all steps but the last of stage st (the DMA of stage st + NS - 1
+		// with more)
 		auto steps = [&](int st, bool more) {
 #pragma unroll
 			for (int s = 0; s + 1 < C::NSTEP; s++) {
@@ -946,20 +966,20 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 				// the buffers written here were last read in stage st - 1,
 				// which every wave has left (its barrier)
 				if (s == 0 && more)
-					issue(st + 1);
+					issue(st + NS - 1);
 				prep(st, s + 1, (s & 1) ^ 1);
 				__builtin_amdgcn_sched_barrier(0);
 			}
 		};
-		if (C::NBB == 3)
-			dma_b<TYPE, DOWN>(bd, slab, 0, w, bbuf(0));
-		issue(0);
+#pragma unroll
+		for (int i = 0; i + 1 < NS; i++)
+			issue(i);
 		barrier_after(-1);
 		if constexpr (NMT < TIE_MFMA_PIPE_NMT) {
-			// few MFMAs per step: each stage self-contained (its DMA first,
-			// then its weights from LDS, then the steps)
+			// few MFMAs per step: each stage self-contained (the DMA of stage
+			// st + NS - 1 first, then its weights from LDS, then the steps)
 			for (int st = 0; st < nk; st++) {
-				issue(st + 1);
+				issue(st + NS - 1);
 				lds_b<TYPE>(bbuf(st), bp, bi, st, h, b);
 				prep(st, 0, 0);
 #pragma unroll
@@ -1257,7 +1277,9 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 // into registers) run one wave per SIMD
 constexpr int mf_wpe(int type, bool down, int mtr)
 {
-	return type == TIE_GGML_BF16 ? 1 : mtr ? 3 : down ? TIE_MFMA_DN_WPE : TIE_MFMA_GU_WPE;
+	return type == TIE_GGML_BF16 ? 1
+	       : mtr == MFMA_MT_TINY ? (down ? TIE_MFMA_TINY_DN_WPC : TIE_MFMA_TINY_GU_WPC)
+	       : mtr && !down ? 3 : down ? TIE_MFMA_DN_WPE : TIE_MFMA_GU_WPE;
 }
 
 template <int TYPE, bool DOWN, int MTR>
@@ -1352,7 +1374,8 @@ mfma_experts_kernel(MfmaArgs a)
 		run_tile<TYPE, DOWN, 1, MTR>(a, As, roff, spair, e, pbase, nrows, slab);
 		break;
 	case 2:
-		run_tile<TYPE, DOWN, 2, MTR>(a, As, roff, spair, e, pbase, nrows, slab);
+		if constexpr (MT_TILES >= 2)
+			run_tile<TYPE, DOWN, (MT_TILES >= 2 ? 2 : 1), MTR>(a, As, roff, spair, e, pbase, nrows, slab);
 		break;
 	case 3:
 		if constexpr (MT_TILES >= 3)
@@ -1591,13 +1614,22 @@ static hipError_t launch_type(const MfmaArgs &a, dim3 grid, hipStream_t s)
 }
 
 template <bool DOWN>
-static hipError_t launch_one(const MfmaArgs &a, int type, dim3 grid, hipStream_t s, bool small = false)
+static hipError_t launch_one(const MfmaArgs &a, int type, dim3 grid, hipStream_t s, int mt = 0)
 {
 	if constexpr (!DOWN) {
-		if (small && type == TIE_GGML_Q4_K)
+		if (mt == MFMA_MT_TINY && type == TIE_GGML_Q4_K)
+			return launch_type<TIE_GGML_Q4_K, false, MFMA_MT_TINY>(a, grid, s);
+		if (mt == MFMA_MT_TINY && type == TIE_GGML_Q6_K)
+			return launch_type<TIE_GGML_Q6_K, false, MFMA_MT_TINY>(a, grid, s);
+		if (mt == MFMA_MT_GU_SMALL && type == TIE_GGML_Q4_K)
 			return launch_type<TIE_GGML_Q4_K, false, MFMA_MT_GU_SMALL>(a, grid, s);
-		if (small && type == TIE_GGML_Q6_K)
+		if (mt == MFMA_MT_GU_SMALL && type == TIE_GGML_Q6_K)
 			return launch_type<TIE_GGML_Q6_K, false, MFMA_MT_GU_SMALL>(a, grid, s);
+	} else {
+		if (mt == MFMA_MT_TINY && type == TIE_GGML_Q4_K)
+			return launch_type<TIE_GGML_Q4_K, true, MFMA_MT_TINY>(a, grid, s);
+		if (mt == MFMA_MT_TINY && type == TIE_GGML_Q6_K)
+			return launch_type<TIE_GGML_Q6_K, true, MFMA_MT_TINY>(a, grid, s);
 	}
 	if (type == TIE_GGML_Q4_K)
 		return launch_type<TIE_GGML_Q4_K, DOWN>(a, grid, s);
@@ -1619,7 +1651,18 @@ bool mfma_f16_operands(const Layer &L)
 int mfma_gu_rows(const Layer &L, int npairs)
 {
 	const bool quant = L.gate.type == TIE_GGML_Q4_K || L.gate.type == TIE_GGML_Q6_K;
+	if (quant && npairs <= TIE_MFMA_TINY_AVG * L.E)
+		return MFMA_MT_TINY;
 	return quant && npairs <= TIE_MFMA_SMALL_AVG * L.E ? MFMA_MT_GU_SMALL : MFMA_MT_GU;
+}
+
+// Quantised down with at most TIE_MFMA_TINY_AVG pairs per expert on average:
+// 32-row tiles, whose small activation buffers leave the LDS for more
+// weight stages in flight (decode-sized batches stream the weights).
+int mfma_dn_rows(const Layer &L, int npairs)
+{
+	const bool quant = L.down.type == TIE_GGML_Q4_K || L.down.type == TIE_GGML_Q6_K;
+	return quant && npairs <= TIE_MFMA_TINY_AVG * L.E ? MFMA_MT_TINY : MFMA_MT_DN;
 }
 
 hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, const float *silu, Workspace &ws,
@@ -1659,9 +1702,9 @@ hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, con
 	// rows: the XCD remap in the kernel reaches every live item only with
 	// at least 8 * ceil(live / 8) workgroups (rows past the tiles exit at
 	// once)
-	const int mt_gu = mfma_gu_rows(L, npairs);
+	const int mt_gu = mfma_gu_rows(L, npairs), mt_dn = mfma_dn_rows(L, npairs);
 	const int gu_tiles = (npairs + mt_gu - 1) / mt_gu + L.E + 8;
-	const int dn_tiles = (npairs + MFMA_MT_DN - 1) / MFMA_MT_DN + L.E + 8;
+	const int dn_tiles = (npairs + mt_dn - 1) / mt_dn + L.E + 8;
 
 	prof_begin("mfma_gate_up", s);
 	a.w[0] = L.gate.data;
@@ -1674,7 +1717,7 @@ hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, con
 	a.a16lo = ws.xlo;
 	a.h16 = ws.hb;
 	a.h16lo = ws.hlo;
-	hipError_t err = launch_one<false>(a, L.gate.type, dim3(L.F / GU_COLS, gu_tiles), s, mt_gu == MFMA_MT_GU_SMALL);
+	hipError_t err = launch_one<false>(a, L.gate.type, dim3(L.F / GU_COLS, gu_tiles), s, mt_gu);
 	prof_end(s);
 	if (err != hipSuccess)
 		return err;
@@ -1690,7 +1733,7 @@ hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, con
 		prof_end(s);
 		return hipErrorInvalidValue; // h has no remainder plane for the split down path
 	}
-	err = launch_one<true>(a, L.down.type, dim3(L.d / DN_COLS, dn_tiles), s);
+	err = launch_one<true>(a, L.down.type, dim3(L.d / DN_COLS, dn_tiles), s, mt_dn);
 	prof_end(s);
 	return err;
 }
