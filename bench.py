@@ -243,10 +243,15 @@ def run_config(torch, tie_amd, wl, T, k, steps, warmup, flags, cfg=None, graph=F
         ms = 1e3 * (time.perf_counter() - t0) / steps
         del g
 
-    # per-kernel event timing over the same sequence of steps
+    # per-kernel timing over the same sequence of steps, from events bound to
+    # each kernel's own dispatch; the device is drained after every step so
+    # that no dispatch waits in the queue behind the previous step's kernels
+    # (a one-token step is one kernel, and its start event would otherwise
+    # include that wait)
     tie_amd.profile_enable(True)
     for s in range(steps):
         step(s)
+        torch.cuda.synchronize()
     prof = tie_amd.profile_read()
     tie_amd.profile_enable(False)
 

@@ -137,7 +137,7 @@ def traffic(fetch_csv, write_csv, copy_fetch_csv, copy_write_csv, copy_bytes):
     return res, {"fetch_scale": f_scale, "write_scale": w_scale}
 
 
-_DEFAULT_JSON = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "profiles", "traffic.json")
+_DEFAULT_JSON = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
 
 
 def traffic_markdown(path):
