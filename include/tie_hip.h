@@ -185,8 +185,8 @@ int tie_hip_moe_forward(tie_hip_layer *layer, const float *x_dev, int T, int k, 
  * HIP graph capture, serving loops, harnesses that forbid hipMalloc).  Its
  * scratch is one static 24 MiB device array per GPU (held until the process
  * ends) instead of the per-stream workspace: calls whose scratch would not
- * fit (T * k pairs with this layer's shape: T <= 91 at d = 2048, F = 768,
- * k = 8; T <= 46 at d = 4096, F = 1536, k = 8) return TIE_HIP_EINVAL.  All calls on a GPU share the array,
+ * fit (T * k pairs with this layer's shape: T <= 89 at d = 2048, F = 768,
+ * k = 8; T <= 44 at d = 4096, F = 1536, k = 8) return TIE_HIP_EINVAL.  All calls on a GPU share the array,
  * so calls that overlap in time on one GPU (other streams, other threads)
  * race: serialise them.  Same arguments, results and stream rules as
  * tie_hip_moe_forward otherwise. */

@@ -244,7 +244,8 @@ static size_t carve_workspace(uint8_t *b, size_t P, size_t FF, size_t DD, size_t
 		     o_hlo = take(P * FF * 2), o_xlo = take(Tcap * DD * 2), o_nm = take(Tcap * DD * 4);
 	const size_t o_bc = take(EE * 4), o_mk = take(EE * (size_t)T4((int)Tcap)), o_bk = take(EE * T4((int)Tcap) * 4);
 	const size_t o_fl = take(Tcap * 4), o_fx = take(Tcap * 4), o_fc = take(4);
-	const size_t o_lg = take(EE * 8), o_dn = take((size_t)MAX_K * FF * 8), o_st = take(4);
+	const size_t o_lg = take(ONE_LG_COPIES * one_copy_words(EE) * 8),
+		     o_dn = take(ONE_H_COPIES * one_copy_words((size_t)MAX_K * FF) * 8), o_st = take(4);
 	if (!b)
 		return off;
 	w->topk_idx = (int32_t *)(b + o_idx);
@@ -307,8 +308,8 @@ static int ensure_workspace(hipStream_t s, int T, int k, int d, int F, int E, Wo
 	w.alloc = mem;
 	// the one-launch decode's words start at sequence 0 (every call uses a
 	// later one)
-	HIP_TRY(hipMemset(w.one_lg, 0, (size_t)EE * 8));
-	HIP_TRY(hipMemset(w.one_h, 0, (size_t)MAX_K * FF * 8));
+	HIP_TRY(hipMemset(w.one_lg, 0, ONE_LG_COPIES * one_copy_words(EE) * 8));
+	HIP_TRY(hipMemset(w.one_h, 0, ONE_H_COPIES * one_copy_words((size_t)MAX_K * FF) * 8));
 	HIP_TRY(hipMemcpy(w.one_status, &status, 4, hipMemcpyHostToDevice));
 	return TIE_HIP_OK;
 }
@@ -556,8 +557,8 @@ static int forward(tie_hip_layer *layer, const float *x, int T, int k, float *ou
 		// not advance it)
 		if (++ws.one_seq == 0) {
 			HIP_TRY(hipStreamSynchronize(s));
-			HIP_TRY(hipMemset(ws.one_lg, 0, (size_t)ws.cap_E * 8));
-			HIP_TRY(hipMemset(ws.one_h, 0, (size_t)MAX_K * ws.cap_F * 8));
+			HIP_TRY(hipMemset(ws.one_lg, 0, ONE_LG_COPIES * one_copy_words(ws.cap_E) * 8));
+			HIP_TRY(hipMemset(ws.one_h, 0, ONE_H_COPIES * one_copy_words((size_t)MAX_K * ws.cap_F) * 8));
 			ws.one_seq = 1;
 		}
 		uint32_t wseq = ws.one_seq;
@@ -568,8 +569,9 @@ static int forward(tie_hip_layer *layer, const float *x, int T, int k, float *ou
 			wseq ^= 0x80000000u;
 			spin = 64;
 		}
-		HIP_TRY(launch_decode_one(L, x, k, g.silu, ws.topk_idx, ws.topk_w, out, res, ws.one_lg, ws.one_h, ws.one_seq,
-					  wseq, spin, ws.one_status, s));
+		HIP_TRY(launch_decode_one(L, x, k, g.silu, ws.topk_idx, ws.topk_w, out, res, ws.one_lg,
+					  one_copy_words(ws.cap_E), ws.one_h, one_copy_words((size_t)MAX_K * ws.cap_F),
+					  ws.one_seq, wseq, spin, ws.one_status, s));
 	} else if (T == 1 && decode_supported(L, k)) {
 		// one token: router logits, then the experts and the combine in two
 		// launches (the selection runs in the gate/up prologue for E <= 128)

@@ -107,8 +107,8 @@ struct Workspace {
 	int32_t *tok_flag = nullptr;  // [T]      f16 path: token's activations left the f16 range
 	int32_t *fix_list = nullptr;  // [T]      flagged tokens (recomputed exactly after the forward)
 	int32_t *fix_count = nullptr; // [1]
-	unsigned long long *one_lg = nullptr; // [E]  one-launch decode: {seq, logit} words
-	unsigned long long *one_h = nullptr; // [MAX_K * F] one-launch decode: {seq, h} words
+	unsigned long long *one_lg = nullptr; // [ONE_LG_COPIES][E, 4 KiB rows]  one-launch decode: {seq, logit} words
+	unsigned long long *one_h = nullptr; // [ONE_H_COPIES][MAX_K * F, 4 KiB rows] one-launch decode: {seq, h} words
 	uint32_t one_seq = 0;         // one-launch decode: sequence number of the last call
 	int32_t *one_status = nullptr; // [1] one-launch decode: 1 when a wait gave up (outputs NaN)
 	size_t cap_pairs = 0, cap_F = 0, cap_d = 0, cap_E = 0;
@@ -182,11 +182,27 @@ hipError_t launch_decode(const Layer &L, const float *x, int k, const float *sil
 // hand the logits and h over as sequence-stamped words in lg / hw; E <= 128)
 bool decode_one_supported(const Layer &L, int k);
 hipError_t launch_decode_one(const Layer &L, const float *x, int k, const float *silu, int32_t *topk_idx,
-			     float *topk_w, float *out, const float *res, unsigned long long *lg, unsigned long long *hw,
-			     uint32_t seq, uint32_t wseq, int spin, int32_t *status, hipStream_t s);
+			     float *topk_w, float *out, const float *res, unsigned long long *lg, size_t lg_copy,
+			     unsigned long long *hw, size_t hw_copy, uint32_t seq, uint32_t wseq, int spin, int32_t *status,
+			     hipStream_t s);
 // polls before a wait of the one-launch decode gives up (each poll sleeps
 // about 64 cycles: tens of milliseconds in all)
 constexpr int ONE_SPIN_MAX = 1 << 18;
+// The one-launch decode publishes the logits and h in several copies (4 KiB
+// apart, so in different memory channels), each polled by a share of the
+// reader workgroups: all readers polling one copy queue on its few lines.
+#ifndef TIE_ONE_LG_COPIES
+#define TIE_ONE_LG_COPIES 8
+#endif
+#ifndef TIE_ONE_H_COPIES
+#define TIE_ONE_H_COPIES 1
+#endif
+constexpr int ONE_LG_COPIES = TIE_ONE_LG_COPIES, ONE_H_COPIES = TIE_ONE_H_COPIES;
+// words between copies of n words
+constexpr size_t one_copy_words(size_t n)
+{
+	return (n * 8 + 4095) / 4096 * 512;
+}
 struct Layer;
 int mfma_gu_rows(const Layer &L, int npairs); // rows per gate/up tile (the tile list's and the kernel's)
 int mfma_dn_rows(const Layer &L, int npairs); // rows per down tile

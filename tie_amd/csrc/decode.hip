@@ -50,6 +50,9 @@ struct TopkScratch {
 }; // gate/up workgroups of the one-launch decode at most (done words)
 constexpr int XSEG = QK + XPAD;
 constexpr int DEC_MAX_THREADS = 512;
+// waves per SIMD the registers of the one-launch decode's two-lane form
+// leave room for (its workgroups must all be resident at once)
+constexpr int ONE_PAIR_WAVES = 6;
 constexpr size_t DEC_MAX_LDS = 150 * 1024; // dynamic LDS per workgroup at most (160 KiB per CU)
 
 typedef const float __attribute__((address_space(3))) dfloat; // LDS input rows
@@ -276,6 +279,198 @@ template <> struct RowBlock<TIE_GGML_Q6_K> {
 };
 
 
+// ---- block dots by two adjacent lanes (lanes 2i and 2i + 1 of a wave, both
+// active).  Each lane loads only the code words of its half of the steps,
+// keeps the accumulators those steps update (a step's accumulators belong
+// to one half), and lane 2i ends with the block's dot: TIE's FMAs in TIE's
+// order per accumulator, then hsum_f32_avx2's tree.  Half the registers and
+// half the dependent work of RowBlock per lane.
+typedef const uint2 __attribute__((address_space(1))) g2;
+typedef const uint32_t __attribute__((address_space(1))) g1;
+
+__device__ __forceinline__ void pin2(uint2 &v)
+{
+	asm volatile("" : "+v"(v.x), "+v"(v.y));
+}
+
+template <int TYPE> struct PairBlock;
+
+// Q4_K (q4k_dot): lane p takes dwords 2p, 2p + 1 of every code chunk, the
+// steps h = 2p, 2p + 1, whose accumulators 4h + i are a0 (p = 0) or a1 (p =
+// 1); v[l] = a0[l] + a1[l] on lane 0 with a1 moved over from lane 1.
+template <> struct PairBlock<TIE_GGML_Q4_K> {
+	uint4 s;    // chunk 0: d, dmin, scales
+	uint2 q[8]; // dwords 2p, 2p + 1 of code chunks 1..8
+	__device__ __forceinline__ void load(const uint8_t *blk, const uint8_t *, int p)
+	{
+		s = *(const uint4 *)(g4 *)blk;
+#pragma unroll
+		for (int i = 0; i < 8; i++)
+			q[i] = *(const uint2 *)(g2 *)(blk + 1024 * (1 + i) + 8 * p);
+	}
+	template <bool PX = false> __device__ __forceinline__ float dot(dfloat *x, int p)
+	{
+		const float d = half_bits_to_float(s.x & 0xffffu);
+		const float dmin = half_bits_to_float(s.x >> 16);
+		float a[8];
+#pragma unroll
+		for (int l = 0; l < 8; l++)
+			a[l] = 0.0f;
+		dfloat *xp = x + 8 * p;
+#pragma unroll
+		for (int g = 0; g < 4; g++) {
+			asm volatile("" : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(a[4]), "+v"(a[5]), "+v"(a[6]),
+					  "+v"(a[7]));
+			asm volatile("" : "+v"(xp));
+			pin2(q[2 * g]);
+			pin2(q[2 * g + 1]);
+			float D1, M1, D2, M2;
+			q4k_scale(s, 2 * g, d, dmin, D1, M1);
+			q4k_scale(s, 2 * g + 1, d, dmin, D2, M2);
+#pragma unroll
+			for (int o = 0; o < 2; o++) {
+#pragma unroll
+				for (int hh = 0; hh < 2; hh++) {
+					const uint32_t w = hh ? q[2 * g + o].y : q[2 * g + o].x;
+					uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
+					asm volatile("" : "+v"(lo), "+v"(hi));
+					dfloat *xb = xp + 64 * g + 16 * o + 4 * hh; // step h = 2p + hh
+					const vf4 xl = *(dfloat4 *)xb, xh = *(dfloat4 *)(xb + 32);
+					const float xlv[4] = {xl.x, xl.y, xl.z, xl.w}, xhv[4] = {xh.x, xh.y, xh.z, xh.w};
+#pragma unroll
+					for (int i = 0; i < 4; i++) {
+						const float wl = __builtin_fmaf(byte_f(lo, i), D1, M1);
+						const float wh = __builtin_fmaf(byte_f(hi, i), D2, M2);
+						float &A = a[4 * hh + i];
+						A = __builtin_fmaf(xlv[i], wl, A);
+						A = __builtin_fmaf(xhv[i], wh, A);
+					}
+				}
+			}
+		}
+		float v[8];
+#pragma unroll
+		for (int l = 0; l < 8; l++)
+			v[l] = a[l] + dppf<DPP_SHL1>(a[l]);
+		return hsum8(v);
+	}
+};
+
+// Q6_K (q6k_dot): lane p takes the steps hw = p (dwords p and p + 2 of the
+// ql / qh chunks), whose accumulators are 4p + i of a0 and of a1, so v[4p +
+// i] = a0 + a1 is local; hsum_f32_avx2's first level v[i] + v[i + 4] takes
+// lane 1's four on lane 0.  PX: each half step's inputs read one half step
+// ahead.
+template <> struct PairBlock<TIE_GGML_Q6_K> {
+	uint32_t ql[8][2]; // dwords p, p + 2 of the ql chunks
+	uint32_t qh[4][2]; // of the qh chunks
+	uint4 sc4;         // the int8 scales
+	uint32_t db;       // fp16 d
+	__device__ __forceinline__ void load(const uint8_t *blk, const uint8_t *dp, int p)
+	{
+#pragma unroll
+		for (int c = 0; c < 8; c++) {
+			ql[c][0] = *(const uint32_t *)(g1 *)(blk + 1024 * c + 4 * p);
+			ql[c][1] = *(const uint32_t *)(g1 *)(blk + 1024 * c + 8 + 4 * p);
+		}
+#pragma unroll
+		for (int c = 0; c < 4; c++) {
+			qh[c][0] = *(const uint32_t *)(g1 *)(blk + 1024 * (8 + c) + 4 * p);
+			qh[c][1] = *(const uint32_t *)(g1 *)(blk + 1024 * (8 + c) + 8 + 4 * p);
+		}
+		sc4 = *(const uint4 *)(g4 *)(blk + 1024 * 12);
+		db = *(const uint16_t *)dp;
+	}
+	template <bool PX = false> __device__ __forceinline__ float dot(dfloat *x, int p)
+	{
+		dfloat *xp = x + 4 * p;
+		// inputs of half step hs = 2 s + half of this lane's steps s
+		auto xat = [&](int hs) {
+			const int st = hs >> 1, half = hs & 1;
+			return xp + 128 * (st >> 2) + 8 * (st & 3) + 64 * half;
+		};
+		vf4 pa, pc;
+		if constexpr (PX) {
+			pa = *(dfloat4 *)xat(0);
+			pc = *(dfloat4 *)(xat(0) + 32);
+		}
+		const float d = half_bits_to_float(db);
+		auto sc = [&](int j) { return (float)(int8_t)((dword_of(sc4, j >> 2) >> (8 * (j & 3))) & 0xffu); };
+		float a0[4], a1[4];
+#pragma unroll
+		for (int i = 0; i < 4; i++)
+			a0[i] = a1[i] = 0.0f;
+#pragma unroll
+		for (int st = 0; st < 8; st++) {
+			// this lane's step st = q6k_dot's step 2 st + p
+			const int qt = st >> 1, n = st >> 2, l = 8 * (st & 3), hl = qt & 1, is = (l >= 16) ? 1 : 0;
+			const int w = st & 1; // dword p (0) or p + 2 (1)
+			if ((st & 1) == 0) {
+				asm volatile("" : "+v"(a0[0]), "+v"(a0[1]), "+v"(a0[2]), "+v"(a0[3]), "+v"(a1[0]), "+v"(a1[1]),
+						  "+v"(a1[2]), "+v"(a1[3]));
+				if constexpr (!PX)
+					asm volatile("" : "+v"(xp));
+				asm volatile("" : "+v"(sc4.x), "+v"(sc4.y), "+v"(sc4.z), "+v"(sc4.w));
+				asm volatile("" : "+v"(ql[4 * n + hl][0]), "+v"(ql[4 * n + hl][1]), "+v"(ql[4 * n + 2 + hl][0]),
+						  "+v"(ql[4 * n + 2 + hl][1]), "+v"(qh[2 * n + hl][0]), "+v"(qh[2 * n + hl][1]));
+			}
+			const float W0 = d * sc(8 * n + is + 0), W1 = d * sc(8 * n + is + 2);
+			const float W2 = d * sc(8 * n + is + 4), W3 = d * sc(8 * n + is + 6);
+			const uint32_t L = ql[4 * n + hl][w], L2 = ql[4 * n + 2 + hl][w], H = qh[2 * n + hl][w];
+			const uint32_t q1 = q6_codes(L, 0, H, 0), q2 = q6_codes(L2, 0, H, 2);
+			const uint32_t q3 = q6_codes(L, 4, H, 4), q4 = q6_codes(L2, 4, H, 6);
+#pragma unroll
+			for (int half = 0; half < 2; half++) {
+				uint32_t qa = half ? q3 : q1, qb = half ? q4 : q2;
+				asm volatile("" : "+v"(qa), "+v"(qb));
+				const float Wa = half ? W2 : W0, Wb = half ? W3 : W1;
+				vf4 xa, xc;
+				if constexpr (PX) {
+					xa = pa;
+					xc = pc;
+					const int hs = 2 * st + half;
+					if (hs + 1 < 16) {
+						pa = *(dfloat4 *)xat(hs + 1);
+						pc = *(dfloat4 *)(xat(hs + 1) + 32);
+					}
+				} else {
+					xa = *(dfloat4 *)xat(2 * st + half);
+					xc = *(dfloat4 *)(xat(2 * st + half) + 32);
+				}
+				const float xav[4] = {xa.x, xa.y, xa.z, xa.w}, xcv[4] = {xc.x, xc.y, xc.z, xc.w};
+#pragma unroll
+				for (int i = 0; i < 4; i++) {
+					const float fa = sbyte_f(qa, i), fb = sbyte_f(qb, i);
+					a0[i] = __builtin_fmaf(Wa, fa * xav[i], a0[i]);
+					a1[i] = __builtin_fmaf(Wb, fb * xcv[i], a1[i]);
+				}
+			}
+		}
+		float v[4];
+#pragma unroll
+		for (int i = 0; i < 4; i++)
+			v[i] = a0[i] + a1[i];
+		float s4[4];
+#pragma unroll
+		for (int i = 0; i < 4; i++)
+			s4[i] = v[i] + dppf<DPP_SHL1>(v[i]); // lane 0: v[i] + v[i + 4]
+		return (s4[0] + s4[1]) + (s4[2] + s4[3]);
+	}
+};
+
+// One (row, block) dot per lane (RowBlock) or per pair of lanes (PairBlock)
+// behind one interface; hp = the lane's half (0 without pairs).
+template <int TYPE, bool PAIR> struct LaneBlock : PairBlock<TYPE> {
+};
+template <int TYPE> struct LaneBlock<TYPE, false> {
+	RowBlock<TYPE> rb;
+	__device__ __forceinline__ void load(const uint8_t *blk, const uint8_t *dp, int) { rb.load(blk, dp); }
+	template <bool PX = false> __device__ __forceinline__ float dot(dfloat *x, int)
+	{
+		return rb.template dot<PX>(x);
+	}
+};
+
 // the row's fp16 d in a Q6_K panel (the d plane after the 13 chunks)
 __device__ __forceinline__ const uint8_t *q6k_d_of(const uint8_t *blk, int row)
 {
@@ -347,37 +542,30 @@ __device__ __forceinline__ void row_sums(float *part, int nb, int R)
 	__syncthreads();
 }
 
-// The combine of R rows from the down partial dots part[(j nb + b) R + r]:
-// y_j = serial block sum per (slot, row) on k R threads, then per row
-// out = fma(g_j, y_j, .) in slot order from +0 (model_qwen3.c:459-467;
-// slots without an expert add nothing), [res +].
-__device__ __forceinline__ void combine_rows(float *part, int nb, int k, int R, const int32_t *sel_idx,
+// The combine of R rows from the down partial dots part[(j nb + b) R + r],
+// one thread per row: y_j = serial block sum per slot, out = fma(g_j, y_j,
+// .) in slot order from +0 (model_qwen3.c:459-467; slots without an expert
+// add nothing), [res +].  The partial dots of several slots are read ahead
+// of their sums (the loop is unrolled), so one LDS latency is exposed per
+// few slots, not one per read; no barrier.
+__device__ __forceinline__ void combine_rows(const float *part, int nb, int k, int R, const int32_t *sel_idx,
 					     const float *sel_w, float *out, const float *res)
 {
 	const int t = threadIdx.x;
-	float y = 0.0f;
-	if (t < k * R) {
-		const int j = t / R, r = t - j * R;
-#pragma unroll 8
+	if (t >= R)
+		return;
+	float acc = 0.0f;
+#pragma unroll 4
+	for (int j = 0; j < k; j++) {
+		const float *pj = part + (size_t)j * nb * R + t;
+		float y = 0.0f;
+#pragma unroll 4
 		for (int b = 0; b < nb; b++)
-			y = y + part[(j * nb + b) * R + r];
+			y = y + pj[b * R];
+		if (sel_idx[j] >= 0)
+			acc = __builtin_fmaf(sel_w[j], y, acc);
 	}
-	__syncthreads();
-	if (t < k * R)
-		part[t] = y;
-	__syncthreads();
-	if (t < R) {
-		float yv[MAX_K];
-#pragma unroll
-		for (int j = 0; j < MAX_K; j++)
-			yv[j] = j < k ? part[j * R + t] : 0.0f;
-		float acc = 0.0f;
-#pragma unroll
-		for (int j = 0; j < MAX_K; j++)
-			if (j < k && sel_idx[j] >= 0)
-				acc = __builtin_fmaf(sel_w[j], yv[j], acc);
-		out[t] = res ? res[t] + acc : acc;
-	}
+	out[t] = res ? res[t] + acc : acc;
 }
 
 template <int TG, int TU, bool INLINE>
@@ -539,8 +727,9 @@ struct OneArgs {
 	DecodeArgs a;
 	const float *router;      // [E][d] F32 rows
 	const float *bias;        // [E] or null
-	unsigned long long *lg;   // [E] {seq, logit}
-	unsigned long long *hw;   // [k][F] {seq, h}
+	unsigned long long *lg;   // [ONE_LG_COPIES][E] {seq, logit}, copies lg_copy words apart
+	unsigned long long *hw;   // [ONE_H_COPIES][k][F] {seq, h}, copies hw_copy words apart
+	size_t lg_copy, hw_copy;
 	uint32_t seq;             // the stamp this call writes
 	uint32_t wseq;            // the stamp its waits look for (seq; another value only from the debug hook)
 	int spin;                 // polls before a wait gives up
@@ -553,7 +742,7 @@ struct OneArgs {
 // diagnostic timeline of the one-launch decode (s_memrealtime, 100 MHz):
 // [2i] earliest, [2i+1] latest time of event i over the workgroups
 constexpr int ONE_TRACE_WG = 8192;
-__device__ unsigned long long g_one_trace[ONE_TRACE_WG][6]; // role + 1, stamps
+__device__ unsigned long long g_one_trace[ONE_TRACE_WG][8]; // role + 1, stamps, (down) core clock at start / end
 __device__ __forceinline__ void one_mark(int i, unsigned long long t)
 {
 	if (blockIdx.x < ONE_TRACE_WG) {
@@ -578,7 +767,8 @@ __device__ __forceinline__ void one_select(const OneArgs &o, uint64_t *etab, int
 	__syncthreads();
 	if (tid < o.a.E) {
 		int bad = 0;
-		const float v = __uint_as_float((uint32_t)wait_word64(o.lg + tid, o.wseq, o.spin, bad));
+		const unsigned long long *lg = o.lg + (blockIdx.x % ONE_LG_COPIES) * o.lg_copy;
+		const float v = __uint_as_float((uint32_t)wait_word64(lg + tid, o.wseq, o.spin, bad));
 		if (bad)
 			*sbad = 1;
 		rank_key(v, tid, o.a.routing, o.a.pbias, etab, *rs);
@@ -591,8 +781,10 @@ __device__ __forceinline__ void one_select(const OneArgs &o, uint64_t *etab, int
 	topk_rank_block(o.a.E, o.a.k, etab, sel_idx, sel_w, o.a.routing, *rs, weights);
 }
 
-template <int TG, int TU, int TD> __global__ __launch_bounds__(DEC_MAX_THREADS, 4) void decode_one_kernel(OneArgs o)
+template <int TG, int TU, int TD, bool PAIR>
+__global__ __launch_bounds__(DEC_MAX_THREADS, PAIR ? ONE_PAIR_WAVES : 4) void decode_one_kernel(const OneArgs o_arg)
 {
+	constexpr int LP = PAIR ? 2 : 1; // lanes per (row, block) dot
 	ONE_T(t_start);
 	extern __shared__ __attribute__((aligned(16))) float dl[];
 	__shared__ int32_t sel_idx[MAX_K];
@@ -600,8 +792,10 @@ template <int TG, int TU, int TD> __global__ __launch_bounds__(DEC_MAX_THREADS, 
 	__shared__ uint64_t etab[32];
 	__shared__ RankScratch rsc;
 	__shared__ int sbad;
+	const int tid = threadIdx.x, b = blockIdx.x;
+	const OneArgs &o = o_arg;
 	const DecodeArgs &a = o.a;
-	const int tid = threadIdx.x, b = blockIdx.x, d = a.d;
+	const int d = a.d;
 	if (tid == 0)
 		sbad = 0;
 	if (b < o.nr) {
@@ -640,7 +834,10 @@ template <int TG, int TU, int TD> __global__ __launch_bounds__(DEC_MAX_THREADS, 
 				const int e = e0 + r;
 				const float v = o.bias ? s + o.bias[e] : s;
 				const unsigned long long w = ((unsigned long long)o.seq << 32) | __float_as_uint(v);
-				__hip_atomic_store(o.lg + e, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+				for (int c = 0; c < ONE_LG_COPIES; c++)
+					__hip_atomic_store(o.lg + c * o.lg_copy + e, w, __ATOMIC_RELAXED,
+							   __HIP_MEMORY_SCOPE_AGENT);
 			}
 		}
 #ifdef TIE_ONE_TRACE
@@ -671,17 +868,25 @@ template <int TG, int TU, int TD> __global__ __launch_bounds__(DEC_MAX_THREADS, 
 		const int e = sel_idx[j];
 		float hv = 0.0f; // a slot without an expert: its h is never used
 		if (e >= 0) {
-			for (int u = tid; u < 2 * nb * R; u += blockDim.x) {
+			// lanes (task, row[, half]): LP lanes per (row, block)
+			for (int u2 = tid; u2 < LP * 2 * nb * R; u2 += blockDim.x) {
+				const int hp = u2 & (LP - 1), u = u2 / LP;
 				const int task = u / R, r = u - task * R;
 				const int mat = task >= nb ? 1 : 0, bb = task - mat * nb;
 				const uint8_t *blk = panel_slot(a.w[mat], a.expert_bytes[mat], e, r0 + r, bb, nb,
 								panel_bytes(mat ? TU : TG));
 				float v;
-				if (mat == 0)
-					v = row_block_dot<TG>(blk, q6k_d_of(blk, r0 + r), (dfloat *)(xs + bb * XSEG));
-				else
-					v = row_block_dot<TU>(blk, q6k_d_of(blk, r0 + r), (dfloat *)(xs + bb * XSEG));
-				part[task * R + r] = v;
+				if (mat == 0) {
+					LaneBlock<TG, PAIR> pb;
+					pb.load(blk, q6k_d_of(blk, r0 + r), hp);
+					v = pb.dot((dfloat *)(xs + bb * XSEG), hp);
+				} else {
+					LaneBlock<TU, PAIR> pb;
+					pb.load(blk, q6k_d_of(blk, r0 + r), hp);
+					v = pb.dot((dfloat *)(xs + bb * XSEG), hp);
+				}
+				if (hp == 0)
+					part[task * R + r] = v;
 			}
 			__syncthreads();
 			row_sums(part, nb, R);
@@ -690,7 +895,10 @@ template <int TG, int TU, int TD> __global__ __launch_bounds__(DEC_MAX_THREADS, 
 		}
 		if (tid < R) {
 			const unsigned long long w = ((unsigned long long)o.seq << 32) | __float_as_uint(hv);
-			__hip_atomic_store(o.hw + (size_t)j * a.F + r0 + tid, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+			for (int c = 0; c < ONE_H_COPIES; c++)
+				__hip_atomic_store(o.hw + c * o.hw_copy + (size_t)j * a.F + r0 + tid, w, __ATOMIC_RELAXED,
+						   __HIP_MEMORY_SCOPE_AGENT);
 		}
 		if (sbad && tid == 0)
 			__hip_atomic_store(o.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -715,30 +923,36 @@ template <int TG, int TU, int TD> __global__ __launch_bounds__(DEC_MAX_THREADS, 
 	// block dot of (row, slot j, block b), task = j nb + b
 	const int R = o.rd, k = a.k, nb = a.F / QK;
 	const int r0 = (b - o.nr - o.ng) * R;
+#ifdef TIE_ONE_TRACE
+	const unsigned long long c_start = __builtin_amdgcn_s_memtime();
+#endif
 	float *hs = dl;                           // [k nb][XSEG]
 	float *part = dl + (size_t)k * nb * XSEG; // [k nb][R]
 	one_select(o, etab, sel_idx, sel_w, &sbad, &rsc, false);
 	ONE_T(t_sel);
-	const int ntask = k * nb;
-	const int task = tid / R, r = tid - task * R;
+	// lanes (task, row[, half]): LP lanes per (row, block)
+	const int ntask = k * nb, hp = tid & (LP - 1);
+	const int task = (tid / LP) / R, r = (tid / LP) - task * R;
 	const bool live = task < ntask;
 	const int jj = live ? task / nb : 0, bb = live ? task - jj * nb : 0;
 	const int e = live ? sel_idx[jj] : -1;
-	RowBlock<TD> rb;
+	LaneBlock<TD, PAIR> rb;
 	{
 		// the weights before the wait for h (unconditional: a lane without
 		// an expert reads expert 0's block and never uses it; a conditional
 		// load would have the compiler wait for it at once)
 		const int rr = live ? r0 + r : r0;
 		const uint8_t *blk = panel_slot(a.w[2], a.expert_bytes[2], e >= 0 ? e : 0, rr, bb, nb, panel_bytes(TD));
-		rb.load(blk, q6k_d_of(blk, rr));
+		rb.load(blk, q6k_d_of(blk, rr), hp);
 	}
 	// the gate weights while those loads are in flight
 	topk_rank_weights(k, etab, sel_idx, sel_w, a.routing, rsc);
+
 	// h (k F words of this call) -> LDS, 8 words of a thread polled at
 	// once, the ones not yet stamped again until all are
 	{
 		const int nw = k * a.F;
+		const unsigned long long *hw = o.hw + (blockIdx.x % ONE_H_COPIES) * o.hw_copy;
 		int bad = 0;
 		for (int base = tid; base < nw; base += 8 * (int)blockDim.x) {
 			unsigned long long v[8];
@@ -752,7 +966,7 @@ template <int TG, int TU, int TD> __global__ __launch_bounds__(DEC_MAX_THREADS, 
 #pragma unroll
 				for (int i = 0; i < 8; i++)
 					if (pend & (1u << i))
-						v[i] = ld_word(o.hw + base + i * (int)blockDim.x);
+						v[i] = ld_word(hw + base + i * (int)blockDim.x);
 #pragma unroll
 				for (int i = 0; i < 8; i++)
 					if ((pend & (1u << i)) && (uint32_t)(v[i] >> 32) == o.wseq) {
@@ -773,9 +987,16 @@ template <int TG, int TU, int TD> __global__ __launch_bounds__(DEC_MAX_THREADS, 
 	}
 	__syncthreads();
 	ONE_T(t_h);
-	if (live)
-		part[task * R + r] = e >= 0 ? rb.dot((dfloat *)(hs + (size_t)task * XSEG)) : 0.0f;
+	if (live) {
+		const float v = e >= 0 ? rb.template dot<true>((dfloat *)(hs + (size_t)task * XSEG), hp) : 0.0f;
+		if (hp == 0)
+			part[task * R + r] = v;
+	}
 	__syncthreads();
+#ifdef TIE_ONE_TRACE
+	if (tid == 0 && blockIdx.x < ONE_TRACE_WG)
+		g_one_trace[blockIdx.x][5] = __builtin_amdgcn_s_memrealtime(); // the down dots done
+#endif
 	float *outp = a.out + r0;
 	combine_rows(part, nb, k, R, sel_idx, sel_w, outp, a.res ? a.res + r0 : nullptr);
 	if (sbad && tid < R)
@@ -786,6 +1007,8 @@ template <int TG, int TU, int TD> __global__ __launch_bounds__(DEC_MAX_THREADS, 
 	if (tid == 0) {
 		ONE_T(t_end);
 		one_mark(6, t_start);
+		g_one_trace[blockIdx.x][6] = c_start;
+		g_one_trace[blockIdx.x][7] = __builtin_amdgcn_s_memtime();
 		one_mark(7, t_sel);
 		one_mark(8, t_h);
 		one_mark(9, t_end);
@@ -916,10 +1139,10 @@ static int round64(int n)
 
 // rows per workgroup: the largest power of two <= rmax (and <= 64) whose
 // tasks x rows fit one workgroup
-static int pick_rows(int ntask, int rmax)
+static int pick_rows(int ntask, int rmax, int max_threads = DEC_MAX_THREADS)
 {
 	int R = rmax;
-	while (R > 1 && ntask * R > DEC_MAX_THREADS)
+	while (R > 1 && ntask * R > max_threads)
 		R >>= 1;
 	return R;
 }
@@ -1153,19 +1376,49 @@ hipError_t launch_decode(const Layer &L, const float *x, int k, const float *sil
 }
 
 // ------------------------------------------------------------ one launch: launcher
-static void one_shape(const Layer &L, int k, int &rpr, int &rg, int &rd, int &threads, size_t &lds)
+// Shape of the one-launch decode with LP lanes per (row, block) dot.
+// gate/up: rg rows, 2 nb tasks per row; down: rd rows, k nb tasks per row
+// (powers of two); router: rpr rows.
+static void one_shape(const Layer &L, int k, int LP, int &rpr, int &rg, int &rd, int &threads, size_t &lds)
 {
 	const int nbd = L.d / QK, nbf = L.F / QK;
-	// gate/up: rg rows, 2 nb tasks per row; down: rd rows, k nb tasks per
-	// row (powers of two); router: rpr rows
-	rg = gu_rows(nbd);
-	rd = pick_rows(k * nbf, 8);
-	threads = round64(std::max(std::max(2 * nbd * rg, k * nbf * rd), L.E));
+	rg = pick_rows(LP * 2 * nbd, 16);
+	rd = pick_rows(LP * k * nbf, 8);
+	threads = round64(std::max(std::max(LP * 2 * nbd * rg, LP * k * nbf * rd), L.E));
 	rpr = L.d <= 2048 ? 2 : 1;
 	const size_t lds_r = sizeof(float) * (size_t)(1 + rpr) * lane_major_floats(L.d);
 	const size_t lds_g = sizeof(float) * ((size_t)nbd * XSEG + 2 * nbd * rg);
 	const size_t lds_d = sizeof(float) * ((size_t)k * nbf * XSEG + (size_t)k * nbf * rd);
 	lds = std::max(lds_r, std::max(lds_g, lds_d));
+}
+
+// compute units of the current device (cached per device)
+static int device_cus()
+{
+	static int cus[64];
+	int dev = 0;
+	if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+		return 0;
+	if (!cus[dev] && hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+		cus[dev] = 0;
+	return cus[dev];
+}
+
+// Two lanes per dot when every workgroup of that form is resident at once
+// (by waves per SIMD and by LDS per CU): the dots' latency halves, while a
+// grid that does not fit would start its down workgroups only as gate/up
+// ones retire, so their weights would no longer stream during gate/up.
+static bool one_pairs(const Layer &L, int k)
+{
+	int rpr, rg, rd, threads;
+	size_t lds;
+	one_shape(L, k, 2, rpr, rg, rd, threads, lds);
+	if (threads > DEC_MAX_THREADS || lds > DEC_MAX_LDS)
+		return false;
+	const long wgs = (L.E + rpr - 1) / rpr + (long)(L.F / rg) * k + L.d / rd;
+	const long waves_wg = threads / 64;
+	const long per_cu = std::min((long)(4 * ONE_PAIR_WAVES) / waves_wg, (long)((160 * 1024) / std::max(lds, (size_t)1)));
+	return wgs <= per_cu * device_cus();
 }
 
 #ifndef TIE_ONE_MAX_D
@@ -1177,7 +1430,7 @@ bool decode_one_supported(const Layer &L, int k)
 		return false;
 	int rpr, rg, rd, threads;
 	size_t lds;
-	one_shape(L, k, rpr, rg, rd, threads, lds);
+	one_shape(L, k, 1, rpr, rg, rd, threads, lds);
 	return threads <= DEC_MAX_THREADS && lds <= DEC_MAX_LDS && 8 * rpr <= threads;
 }
 
@@ -1185,13 +1438,14 @@ int decode_one_gate_up_groups(const Layer &L, int k)
 {
 	int rpr, rg, rd, threads;
 	size_t lds;
-	one_shape(L, k, rpr, rg, rd, threads, lds);
+	one_shape(L, k, one_pairs(L, k) ? 2 : 1, rpr, rg, rd, threads, lds);
 	return (L.F / rg) * k;
 }
 
 hipError_t launch_decode_one(const Layer &L, const float *x, int k, const float *silu, int32_t *topk_idx,
-			     float *topk_w, float *out, const float *res, unsigned long long *lg, unsigned long long *hw,
-			     uint32_t seq, uint32_t wseq, int spin, int32_t *status, hipStream_t s)
+			     float *topk_w, float *out, const float *res, unsigned long long *lg, size_t lg_copy,
+			     unsigned long long *hw, size_t hw_copy, uint32_t seq, uint32_t wseq, int spin, int32_t *status,
+			     hipStream_t s)
 {
 	OneArgs o;
 	memset(&o, 0, sizeof o);
@@ -1216,11 +1470,14 @@ hipError_t launch_decode_one(const Layer &L, const float *x, int k, const float 
 	a.pbias = L.pbias;
 	int threads;
 	size_t lds;
-	one_shape(L, k, o.rpr, o.rg, o.rd, threads, lds);
+	const bool pair = one_pairs(L, k);
+	one_shape(L, k, pair ? 2 : 1, o.rpr, o.rg, o.rd, threads, lds);
 	o.router = L.router;
 	o.bias = L.bias;
 	o.lg = lg;
 	o.hw = hw;
+	o.lg_copy = lg_copy;
+	o.hw_copy = hw_copy;
 	o.seq = seq;
 	o.wseq = wseq;
 	o.spin = spin;
@@ -1232,9 +1489,10 @@ hipError_t launch_decode_one(const Layer &L, const float *x, int k, const float 
 	const int tg = L.gate.type, tu = L.up.type, td = L.down.type;
 	hipError_t err;
 	prof_begin("decode_one", s);
-#define ONE(A, B)                                                                                                    \
-	(td == TIE_GGML_Q4_K ? dec_launch(decode_one_kernel<A, B, TIE_GGML_Q4_K>, grid, dim3(threads), lds, s, o)        \
-			     : dec_launch(decode_one_kernel<A, B, TIE_GGML_Q6_K>, grid, dim3(threads), lds, s, o))
+#define ONE_P(A, B, C)                                                                                               \
+	(pair ? dec_launch(decode_one_kernel<A, B, C, true>, grid, dim3(threads), lds, s, o)                             \
+	      : dec_launch(decode_one_kernel<A, B, C, false>, grid, dim3(threads), lds, s, o))
+#define ONE(A, B) (td == TIE_GGML_Q4_K ? ONE_P(A, B, TIE_GGML_Q4_K) : ONE_P(A, B, TIE_GGML_Q6_K))
 	if (tg == TIE_GGML_Q4_K && tu == TIE_GGML_Q4_K)
 		err = ONE(TIE_GGML_Q4_K, TIE_GGML_Q4_K);
 	else if (tg == TIE_GGML_Q4_K)
@@ -1244,6 +1502,7 @@ hipError_t launch_decode_one(const Layer &L, const float *x, int k, const float 
 	else
 		err = ONE(TIE_GGML_Q6_K, TIE_GGML_Q6_K);
 #undef ONE
+#undef ONE_P
 	prof_end(s);
 	return err;
 }
@@ -1543,11 +1802,11 @@ hipError_t launch_dense_rows(const ExpertTensor &W, const float *x, int T, float
 #ifdef TIE_ONE_TRACE
 extern "C" int tie_hip_debug_one_trace(unsigned long long *host, int reset)
 {
-	const size_t n = sizeof(unsigned long long) * tie::ONE_TRACE_WG * 6;
+	const size_t n = sizeof(unsigned long long) * tie::ONE_TRACE_WG * 8;
 	if (hipMemcpyFromSymbol(host, HIP_SYMBOL(tie::g_one_trace), n) != hipSuccess)
 		return -1;
 	if (reset) {
-		static unsigned long long z[tie::ONE_TRACE_WG * 6];
+		static unsigned long long z[tie::ONE_TRACE_WG * 8];
 		if (hipMemcpyToSymbol(HIP_SYMBOL(tie::g_one_trace), z, n) != hipSuccess)
 			return -1;
 	}
