@@ -517,20 +517,29 @@ static int forward(tie_hip_layer *layer, const float *x, int T, int k, float *ou
 		return rc;
 	Workspace &ws = *wsp;
 	if (mfma) {
-		// logits (clearing the selection bytes and the recomputation
-		// count), then selection, selection bytes and the A operand in one
-		// launch, then the per-expert pair lists
+		// logits (clearing the selection bytes or pair counts and the
+		// recomputation count), then selection, pair lists (small T) or
+		// selection bytes, and the A operand in one launch, then (large T)
+		// the per-expert pair lists
 		prof_begin("router", s);
 		ZeroArgs z;
-		z.p2 = reinterpret_cast<int32_t *>(ws.sel);
-		z.n2 = L.E * T4(T) / 4;
+		if (route_appends(T)) {
+			// the pair counts the routing appends to
+			z.p = ws.bucket_cnt;
+			z.n = L.E;
+		} else {
+			z.p2 = reinterpret_cast<int32_t *>(ws.sel);
+			z.n2 = L.E * T4(T) / 4;
+		}
 		z.one = ws.fix_count;
 		HIP_TRY(launch_router_logits(L, x, T, ws.logits, s, z));
 		HIP_TRY(launch_route_bucket(L, x, T, k, ws, s));
 		prof_end(s);
-		prof_begin("dispatch", s);
-		HIP_TRY(launch_bucket_plan(L, T, k, ws, s));
-		prof_end(s);
+		if (!route_appends(T)) {
+			prof_begin("dispatch", s);
+			HIP_TRY(launch_bucket_plan(L, T, k, ws, s));
+			prof_end(s);
+		}
 		HIP_TRY(launch_mfma_experts(L, x, T, k, g.silu, ws, s));
 		if (mfma_f16_operands(L) && combine_fix_preferred(L)) {
 			// the combine of every token, except those whose activations

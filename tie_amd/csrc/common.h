@@ -131,6 +131,17 @@ struct ZeroArgs {
 };
 hipError_t launch_router_logits(const Layer &L, const float *x, int T, float *logits, hipStream_t s,
 				ZeroArgs z = ZeroArgs());
+// the matrix-core path's routing appends its pairs to the per-expert lists
+// (atomics on the counts) up to this many tokens; above, selection bytes
+// and bucket_plan (contended atomics: T=2048 35 us against 10 us)
+#ifndef TIE_ROUTE_APPEND_MAX_T
+#define TIE_ROUTE_APPEND_MAX_T 256
+#endif
+constexpr int ROUTE_APPEND_MAX_T = TIE_ROUTE_APPEND_MAX_T;
+inline bool route_appends(int T)
+{
+	return T <= ROUTE_APPEND_MAX_T;
+}
 // The matrix-core path's quantised down stores y as f16 scaled by the
 // layer's 2^-y_shift (1) or as fp32 (0): f16 halves the bytes the down
 // kernel writes and the combine reads, and adds 2^-12 relative rounding

@@ -1401,7 +1401,13 @@ mfma_experts_kernel(MfmaArgs a)
 // engine.c:864-914), then each selected expert e records the slot that
 // chose it, sel[e][t] = j + 1 (a byte of its own: no atomics; the array is
 // zeroed by the logits kernel).  bucket_plan_kernel turns these rows into
-// per-expert pair lists.  The same wave converts the token's x row into the
+// per-expert pair lists.  Up to ROUTE_APPEND_MAX_T tokens the wave appends
+// its pairs to the lists itself instead (one atomic on the expert's count,
+// zeroed by the logits kernel, per pair; few pairs per count at these
+// sizes), and bucket_plan does not run: the order of pairs in a list then
+// varies from call to call, which changes no result (each pair's rows are
+// computed on their own, and h and y are addressed through the list or by
+// pair id).  The same wave converts the token's x row into the
 // gate/up A operand:
 //   MODE 0: bf16
 //   MODE 1: f16 with the K order inside each 8-group 0,2,1,3,4,6,5,7 (the
@@ -1417,6 +1423,7 @@ struct BucketArgs {
 	int32_t *topk_idx;
 	float *topk_w;
 	uint8_t *sel;
+	int32_t *cnt, *bucket; // non-null: append the pairs to the lists directly (small T)
 	const float *x;
 	uint16_t *xa, *xlo;
 	int32_t *flag, *list, *count;
@@ -1452,8 +1459,12 @@ template <int MODE> __global__ __launch_bounds__(RB_THREADS) void route_bucket_k
 	if (lane < r.k) {
 		// lane j wrote slot j above
 		const int e = r.topk_idx[(size_t)t * r.k + lane];
-		if (e >= 0)
-			r.sel[(size_t)e * r.ts + t] = (uint8_t)(lane + 1);
+		if (e >= 0) {
+			if (r.cnt)
+				r.bucket[(size_t)e * r.ts + atomicAdd(r.cnt + e, 1)] = t * r.k + lane;
+			else
+				r.sel[(size_t)e * r.ts + t] = (uint8_t)(lane + 1);
+		}
 	}
 	int bad = 0;
 	for (int base = 0; base < n4; base += 128 * (RB_X / 2)) {
@@ -1524,6 +1535,9 @@ hipError_t launch_route_bucket(const Layer &L, const float *x, int T, int k, Wor
 	r.topk_idx = ws.topk_idx;
 	r.topk_w = ws.topk_w;
 	r.sel = ws.sel;
+	const bool append = route_appends(T);
+	r.cnt = append ? ws.bucket_cnt : nullptr;
+	r.bucket = append ? ws.bucket : nullptr;
 	r.x = x;
 	r.xa = ws.xb;
 	r.xlo = ws.xlo;
