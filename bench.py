@@ -212,15 +212,21 @@ def run_config(torch, tie_amd, wl, T, k, steps, warmup, flags, cfg=None, graph=F
     torch.cuda.synchronize()
     gpu_out0 = (X[0].cpu().numpy(), out.cpu().numpy(), idx[0].cpu().numpy(), w[0].cpu().numpy())
     # eager: one library call per step from this Python loop (host launch
-    # overhead included)
+    # overhead included), on a stream of our own with two events inside the
+    # host clock's bracket (the GPU interval of the same steps)
+    es = torch.cuda.Stream()
     for s in range(warmup):
-        step(s)
+        step(s, stream=es.cuda_stream)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    ev0.record(es)
     for s in range(steps):
-        step(s)
+        step(s, stream=es.cuda_stream)
+    ev1.record(es)
     torch.cuda.synchronize()
     ms_eager = 1e3 * (time.perf_counter() - t0) / steps
+    gpu_ms_eager = ev0.elapsed_time(ev1)
     ms = ms_eager
     if graph:
         # the same `steps` forwards captured once as a HIP graph on a stream
@@ -254,6 +260,14 @@ def run_config(torch, tie_amd, wl, T, k, steps, warmup, flags, cfg=None, graph=F
         torch.cuda.synchronize()
     prof = tie_amd.profile_read()
     tie_amd.profile_enable(False)
+    if len(prof) == 1 and next(iter(prof.values()))[1] == steps and not graph:
+        # a step of one kernel (the one-token block): its steady-state
+        # duration is the per-launch time of the timed loop's back-to-back
+        # launches, from the events inside its host-clock bracket (a
+        # dispatch-bound event pair also counts the end-of-kernel release,
+        # which back-to-back launches overlap with the next start)
+        prof = {next(iter(prof)): (gpu_ms_eager, steps)}
+    tie_amd.stream_release(es.cuda_stream)
 
     idx_h = idx.cpu().numpy()
     U = np.array([len(np.unique(idx_h[l][idx_h[l] >= 0])) for l in range(nL)], np.float64)
