@@ -532,8 +532,15 @@ static int forward(tie_hip_layer *layer, const float *x, int T, int k, float *ou
 			z.n2 = L.E * T4(T) / 4;
 		}
 		z.one = ws.fix_count;
-		HIP_TRY(launch_router_logits(L, x, T, ws.logits, s, z));
-		HIP_TRY(launch_route_bucket(L, x, T, k, ws, s));
+		XConvArgs xc;
+		const bool xconv = router_converts_x(L, T) && L.gate.type != TIE_GGML_BF16 && mfma_f16_operands(L);
+		if (xconv) {
+			// the tiled logits kernel writes the f16 A operand and range flags
+			xc.xa = ws.xb;
+			xc.flag = ws.tok_flag;
+		}
+		HIP_TRY(launch_router_logits(L, x, T, ws.logits, s, z, xc));
+		HIP_TRY(launch_route_bucket(L, x, T, k, ws, s, xconv));
 		prof_end(s);
 		if (!route_appends(T)) {
 			prof_begin("dispatch", s);

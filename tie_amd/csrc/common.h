@@ -129,8 +129,18 @@ struct ZeroArgs {
 	int n = 0, n2 = 0;
 	int32_t *one = nullptr;
 };
+// The matrix-core path's f16 A operand of x (gate/up; K order 0,2,1,3,4,6,5,7
+// inside each group of 8) and the token's range flag (1: a value not finite
+// or not below 65504 in magnitude), written by the tiled logits kernel from
+// the x rows it stages anyway (router_converts_x); the routing kernel then
+// only lists the flagged tokens.
+struct XConvArgs {
+	uint16_t *xa = nullptr;
+	int32_t *flag = nullptr;
+};
+bool router_converts_x(const Layer &L, int T);
 hipError_t launch_router_logits(const Layer &L, const float *x, int T, float *logits, hipStream_t s,
-				ZeroArgs z = ZeroArgs());
+				ZeroArgs z = ZeroArgs(), XConvArgs xc = XConvArgs());
 // the matrix-core path's routing appends its pairs to the per-expert lists
 // (atomics on the counts) up to this many tokens; above, selection bytes
 // and bucket_plan (contended atomics: T=2048 35 us against 10 us)
@@ -151,7 +161,10 @@ inline bool route_appends(int T)
 #endif
 // the matrix-core path's selection, grouping into per-expert buckets and
 // A-operand conversion (mfma.hip)
-hipError_t launch_route_bucket(const Layer &L, const float *x, int T, int k, Workspace &ws, hipStream_t s);
+// converted: the logits kernel wrote the f16 A operand and the range flags
+// (XConvArgs); the routing then only lists the flagged tokens
+hipError_t launch_route_bucket(const Layer &L, const float *x, int T, int k, Workspace &ws, hipStream_t s,
+			       bool converted);
 hipError_t launch_bucket_plan(const Layer &L, int T, int k, Workspace &ws, hipStream_t s);
 hipError_t launch_router_select(const Layer &L, int T, int k, const float *logits, int32_t *topk_idx, float *topk_w,
 				hipStream_t s);

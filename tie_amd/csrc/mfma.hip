@@ -1424,6 +1424,7 @@ struct BucketArgs {
 	float *topk_w;
 	uint8_t *sel;
 	int32_t *cnt, *bucket; // non-null: append the pairs to the lists directly (small T)
+	int converted;         // MODE 1: the logits kernel wrote the A operand and flag[t] already
 	const float *x;
 	uint16_t *xa, *xlo;
 	int32_t *flag, *list, *count;
@@ -1448,11 +1449,14 @@ template <int MODE> __global__ __launch_bounds__(RB_THREADS) void route_bucket_k
 	const float4 *xr = reinterpret_cast<const float4 *>(r.x + (size_t)t * r.d);
 	const int n4 = r.d / 4;
 	float4 xv[RB_X];
+	const bool conv = !(MODE == 1 && r.converted);
+	if (conv) {
 #pragma unroll
-	for (int i = 0; i < RB_X / 2; i++) {
-		const int q = 2 * (lane + 64 * i);
-		xv[2 * i] = q < n4 ? xr[q] : make_float4(0, 0, 0, 0);
-		xv[2 * i + 1] = q < n4 ? xr[q + 1] : make_float4(0, 0, 0, 0);
+		for (int i = 0; i < RB_X / 2; i++) {
+			const int q = 2 * (lane + 64 * i);
+			xv[2 * i] = q < n4 ? xr[q] : make_float4(0, 0, 0, 0);
+			xv[2 * i + 1] = q < n4 ? xr[q + 1] : make_float4(0, 0, 0, 0);
+		}
 	}
 	topk_softmax(r.logits + (size_t)t * r.E, r.E, r.k, etab, r.topk_idx + (size_t)t * r.k, r.topk_w + (size_t)t * r.k,
 		     r.routing, r.pbias);
@@ -1464,6 +1468,14 @@ template <int MODE> __global__ __launch_bounds__(RB_THREADS) void route_bucket_k
 				r.bucket[(size_t)e * r.ts + atomicAdd(r.cnt + e, 1)] = t * r.k + lane;
 			else
 				r.sel[(size_t)e * r.ts + t] = (uint8_t)(lane + 1);
+		}
+	}
+	if constexpr (MODE == 1) {
+		if (!conv) {
+			// the A operand and the flag came with the logits: list the token
+			if (lane == 0 && r.flag[t])
+				r.list[atomicAdd(r.count, 1)] = t;
+			return;
 		}
 	}
 	int bad = 0;
@@ -1521,7 +1533,8 @@ template <int MODE> __global__ __launch_bounds__(RB_THREADS) void route_bucket_k
 	}
 }
 
-hipError_t launch_route_bucket(const Layer &L, const float *x, int T, int k, Workspace &ws, hipStream_t s)
+hipError_t launch_route_bucket(const Layer &L, const float *x, int T, int k, Workspace &ws, hipStream_t s,
+			       bool converted)
 {
 	BucketArgs r;
 	r.logits = ws.logits;
@@ -1544,6 +1557,7 @@ hipError_t launch_route_bucket(const Layer &L, const float *x, int T, int k, Wor
 	r.flag = ws.tok_flag;
 	r.list = ws.fix_list;
 	r.count = ws.fix_count;
+	r.converted = converted && L.gate.type != TIE_GGML_BF16 && TIE_MFMA_F16;
 	const dim3 grid((T + RB_THREADS / 64 - 1) / (RB_THREADS / 64));
 	if (L.gate.type == TIE_GGML_BF16)
 		tie_launch(route_bucket_kernel<2>, grid, dim3(RB_THREADS), 0, s, r);

@@ -261,10 +261,37 @@ __device__ __forceinline__ void rt_barrier()
 	asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+typedef _Float16 rt_f16x8 __attribute__((ext_vector_type(8)));
+
+// XConvArgs' conversion of the RT_TOK x RT_KC chunk staged at xs (token-major
+// rows of RT_KC floats), K offset kc: thread (t, q) of the first 16 RT_TOK
+// converts floats 8q .. 8q + 7 of token t; bad: its range flag so far
+__device__ __forceinline__ void rt_convert_chunk(const float *xs, const XConvArgs &xc, int t0, int nt, int d, int kc,
+						 int &bad)
+{
+	constexpr int QPT = RT_KC / 8; // threads per token
+	const int t = threadIdx.x / QPT, q = threadIdx.x % QPT;
+	if (t >= nt || threadIdx.x >= RT_TOK * QPT)
+		return;
+	const float4 a = *reinterpret_cast<const float4 *>(xs + t * RT_KC + 8 * q);
+	const float4 c = *reinterpret_cast<const float4 *>(xs + t * RT_KC + 8 * q + 4);
+	const float m = __builtin_fmaxf(__builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(a.x), __builtin_fabsf(a.y)),
+							__builtin_fmaxf(__builtin_fabsf(a.z), __builtin_fabsf(a.w))),
+					__builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(c.x), __builtin_fabsf(c.y)),
+							__builtin_fmaxf(__builtin_fabsf(c.z), __builtin_fabsf(c.w))));
+	// fmax drops NaN: test the values themselves for NaN
+	const bool nan = a.x != a.x || a.y != a.y || a.z != a.z || a.w != a.w || c.x != c.x || c.y != c.y ||
+			 c.z != c.z || c.w != c.w;
+	bad |= (nan || !(m < 65504.0f)) ? 1 : 0;
+	const rt_f16x8 h = {(_Float16)a.x, (_Float16)a.z, (_Float16)a.y, (_Float16)a.w,
+			    (_Float16)c.x, (_Float16)c.z, (_Float16)c.y, (_Float16)c.w};
+	*reinterpret_cast<rt_f16x8 *>(xc.xa + (size_t)(t0 + t) * d + kc + 8 * q) = h;
+}
+
 __global__ __launch_bounds__(RT_THREADS) void router_logits_kernel(const float *__restrict__ x,
 								   const float *__restrict__ WT,
 								   const float *__restrict__ bias, int T, int d, int E,
-								   float *__restrict__ logits, ZeroArgs z)
+								   float *__restrict__ logits, ZeroArgs z, XConvArgs xc)
 {
 	zero_words(z);
 	extern __shared__ __attribute__((aligned(16))) uint8_t rt_lds[];
@@ -285,6 +312,10 @@ __global__ __launch_bounds__(RT_THREADS) void router_logits_kernel(const float *
 		for (int b = 0; b < 4; b++)
 			acc[a][b] = 0.0f;
 
+	// the first expert tile's workgroups also convert their tokens' x rows
+	const bool conv = xc.xa && blockIdx.y == 0;
+	int bad = 0;
+
 	rt_dma_chunk(x, WT, E, d, t0, e0, nt, 0, rt_lds);
 	rt_barrier();
 	for (int c = 0; c < nkc; c++) {
@@ -292,6 +323,10 @@ __global__ __launch_bounds__(RT_THREADS) void router_logits_kernel(const float *
 			rt_dma_chunk(x, WT, E, d, t0, e0, nt, (c + 1) * RT_KC, rt_lds + ((c + 1) & 1) * RT_BUF);
 		const float *ws = reinterpret_cast<const float *>(rt_lds + (c & 1) * RT_BUF);
 		const float *xs = reinterpret_cast<const float *>(rt_lds + (c & 1) * RT_BUF + RT_WBYTES);
+		// before the FMAs: the stores have the chunk's FMAs to land before the
+		// stage barrier (which waits for every vector memory operation)
+		if (conv)
+			rt_convert_chunk(xs, xc, t0, nt, d, c * RT_KC, bad);
 		// operands of RT_IB K steps read into registers first (their LDS
 		// latencies overlap), then the FMAs in K order
 		for (int i0 = 0; i0 < RT_KC / 8; i0 += RT_IB) {
@@ -316,6 +351,15 @@ __global__ __launch_bounds__(RT_THREADS) void router_logits_kernel(const float *
 			}
 		}
 		rt_barrier();
+	}
+	if (conv) {
+		// a token's flag: the OR over its RT_KC / 8 threads (aligned lane groups)
+		constexpr int QPT = RT_KC / 8;
+		static_assert(64 % QPT == 0, "a token's threads in one wave");
+		const unsigned long long b = __ballot(bad);
+		const int lane = tid & 63, t = tid / QPT;
+		if (tid < RT_TOK * QPT && lane % QPT == 0 && t < nt)
+			xc.flag[t0 + t] = ((b >> lane) & ((1ull << QPT) - 1ull)) != 0 ? 1 : 0;
 	}
 
 	// hsum8 over the 8 lanes l of each chain group (math_avx2.c:14-21 order)
@@ -378,7 +422,18 @@ __global__ __launch_bounds__(RW_THREADS) void router_topk_kernel(const float *__
 			     pbias);
 }
 
-hipError_t launch_router_logits(const Layer &L, const float *x, int T, float *logits, hipStream_t s, ZeroArgs z)
+static bool router_tiled(const Layer &L, int T)
+{
+	return T > TIE_RT_MIN_T && L.E % RT_EXP == 0 && L.d % RT_KC == 0 && L.routerT;
+}
+
+bool router_converts_x(const Layer &L, int T)
+{
+	return router_tiled(L, T);
+}
+
+hipError_t launch_router_logits(const Layer &L, const float *x, int T, float *logits, hipStream_t s, ZeroArgs z,
+				XConvArgs xc)
 {
 	const int d = L.d, E = L.E;
 	if (T <= TIE_RS_MAX_T && sizeof(float) * (size_t)(8 * (d / 8 + 4)) * (1 + RS_TOK) <= 160 * 1024) {
@@ -389,7 +444,7 @@ hipError_t launch_router_logits(const Layer &L, const float *x, int T, float *lo
 	}
 	// the tiled kernel above 256 tokens: below that its one chunk in flight
 	// per K step leaves it waiting on memory, and router_mid is faster
-	if (T > TIE_RT_MIN_T && E % RT_EXP == 0 && d % RT_KC == 0 && L.routerT) {
+	if (router_tiled(L, T)) {
 		static bool attr = false;
 		if (!attr) {
 			const hipError_t err = hipFuncSetAttribute((const void *)router_logits_kernel,
@@ -399,7 +454,7 @@ hipError_t launch_router_logits(const Layer &L, const float *x, int T, float *lo
 			attr = true;
 		}
 		tie_launch(router_logits_kernel, dim3((T + RT_TOK - 1) / RT_TOK, E / RT_EXP), dim3(RT_THREADS),
-				   RT_LDS, s, x, L.routerT, L.bias, T, d, E, logits, z);
+				   RT_LDS, s, x, L.routerT, L.bias, T, d, E, logits, z, xc);
 		return hipGetLastError();
 	}
 	const bool u64 = d % 512 == 0;
