@@ -330,25 +330,33 @@ def test_small_activations():
     check_oracle("small_h", out, ro)
 
 
-def test_out_of_range_tokens_recomputed_exactly():
+@pytest.mark.parametrize("seed,E,T,far", [(93, 16, 160, None), (94, 32, 300, 297)])
+def test_out_of_range_tokens_recomputed_exactly(seed, E, T, far):
     """Tokens whose x (|x| >= 65504, NaN) or scaled h leave the f16 range
     are recomputed in TIE's exact arithmetic: their rows equal the oracle
-    bit for bit, and no other row changes."""
-    layer = synth_layer(93, 512, 512, 16, synth.Q4_K, synth.Q6_K, None)
-    T, k = 160, 4
-    x = synth.make_input(93, T, 512)
+    bit for bit, and no other row changes.  E = 16, T = 160: the
+    routing kernel converts x and flags the tokens; E = 32, T = 300: the
+    tiled logits kernel does (T > 256), with a flagged token in the last,
+    partial 16-token tile."""
+    layer = synth_layer(seed, 512, 512, E, synth.Q4_K, synth.Q6_K, None)
+    k = 4
+    x = synth.make_input(seed, T, 512)
     base_out, _, _ = run_mfma(layer, x, k)
     x2 = x.copy()
     x2[5] *= np.float32(1e5)     # x beyond f16
     x2[9] *= np.float32(200.0)   # x fits f16, h ~ 4e4 x typical: beyond
     x2[17, 3] = np.nan           # NaN logits: no expert, output 0
+    bad = [5, 9, 17]
+    if far is not None:
+        x2[far, 200] = np.float32(7e4)  # one value beyond f16 in a late K chunk
+        bad.append(far)
     out, idx, w = run_mfma(layer, x2, k)
     ro, ri, rw = bind.moe_block(layer, x2, k)
     check_routing(idx, w, ri, rw)
-    for t in (5, 9, 17):
+    for t in bad:
         np.testing.assert_array_equal(bits(out[t]), bits(ro[t]), err_msg="row %d" % t)
     assert (out[17] == 0).all()
-    rest = np.setdiff1d(np.arange(T), [5, 9, 17])
+    rest = np.setdiff1d(np.arange(T), bad)
     np.testing.assert_array_equal(bits(out[rest]), bits(base_out[rest]))
     assert np.isfinite(out[rest]).all()
 
