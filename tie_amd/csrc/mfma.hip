@@ -706,6 +706,12 @@ __device__ __forceinline__ void stage_barrier()
 #ifdef TIE_MFMA_TRACE
 __device__ unsigned long long g_mfma_trace[2][8];
 #endif
+#ifdef TIE_MFMA_TIMELINE
+// diagnostic timeline: [down][workgroup] = {start, end} (s_memrealtime,
+// 100 MHz) of each live workgroup of the last launch
+constexpr int MFMA_TL_WG = 16384;
+__device__ unsigned long long g_mfma_tl[2][MFMA_TL_WG][2];
+#endif
 
 // The same, but the N youngest vector loads (the next-but-one weight
 // stage's DMA, issued last) may stay in flight: loads complete in order, so
@@ -1306,6 +1312,9 @@ mfma_experts_kernel(MfmaArgs a)
 #ifdef TIE_MFMA_TRACE
 	const unsigned long long t_k0 = __builtin_readcyclecounter();
 #endif
+#ifdef TIE_MFMA_TIMELINE
+	const unsigned long long tl0 = __builtin_amdgcn_s_memrealtime();
+#endif
 	const int mtc = a.mt_cap > 0 && a.mt_cap < MT ? a.mt_cap : MT;
 	int e, li, off, slab;
 	{
@@ -1399,6 +1408,15 @@ mfma_experts_kernel(MfmaArgs a)
 		if constexpr (MT_TILES >= 6)
 			run_tile<TYPE, DOWN, (MT_TILES >= 6 ? 6 : 1), MTR>(a, As, roff, spair, e, pbase, nrows, slab);
 	}
+#ifdef TIE_MFMA_TIMELINE
+	{
+		const int lin = blockIdx.y * gridDim.x + blockIdx.x;
+		if (threadIdx.x == 0 && lin < MFMA_TL_WG) {
+			g_mfma_tl[DOWN][lin][0] = tl0;
+			g_mfma_tl[DOWN][lin][1] = __builtin_amdgcn_s_memrealtime();
+		}
+	}
+#endif
 }
 
 // ------------------------------------------------------------ routing
@@ -1859,6 +1877,21 @@ hipError_t launch_mfma_dense(const ExpertTensor &W, const float *x, int T, float
 }
 
 } // namespace tie
+
+#ifdef TIE_MFMA_TIMELINE
+extern "C" int tie_hip_debug_mfma_timeline(unsigned long long *host, int reset)
+{
+	const size_t n = sizeof(unsigned long long) * 2 * tie::MFMA_TL_WG * 2;
+	if (hipMemcpyFromSymbol(host, HIP_SYMBOL(tie::g_mfma_tl), n) != hipSuccess)
+		return -1;
+	if (reset) {
+		static unsigned long long z[2 * tie::MFMA_TL_WG * 2];
+		if (hipMemcpyToSymbol(HIP_SYMBOL(tie::g_mfma_tl), z, n) != hipSuccess)
+			return -1;
+	}
+	return 0;
+}
+#endif
 
 #ifdef TIE_MFMA_TRACE
 extern "C" int tie_hip_debug_mfma_trace(unsigned long long *host, int reset)
