@@ -830,8 +830,8 @@ __device__ __forceinline__ void stage_mfma(const BRegs<TYPE> &b, int st, const u
 // ------------------------------------------------------------------ kernel
 // One work tile with NMT live 32-row M tiles (nrows <= 32 NMT).
 template <int TYPE, bool DOWN, int NMT, int MTR>
-__device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_t *roff, const int32_t *spair, int e,
-					 int pbase, int nrows, int slab)
+__device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_t *roff, int32_t *spair, int e,
+					 int pbase, int nrows, int slab, int pair_id)
 {
 	using C = Cfg<TYPE, DOWN, MTR>;
 	const int nk = a.in / C::KST;
@@ -856,7 +856,7 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 		as.roff = roff + (C::RPI * w + rsub) * ROFF_STRIDE;
 		if (t < C::MT) {
 			const int r = t < nrows ? t : 0;
-			const int pr = spair[r];
+			const int pr = DOWN ? 0 : spair[r];
 			const int row = DOWN ? pbase + r : pr / a.k;
 			const int c = t / (C::RPI * NWAVES), ls = t % (C::RPI * NWAVES);
 			roff[ls * ROFF_STRIDE + c] = (uint32_t)((size_t)row * a.in * 2);
@@ -1089,6 +1089,15 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 #ifdef TIE_MFMA_TRACE
 	t_loop = __builtin_readcyclecounter();
 #endif
+	if constexpr (DOWN) {
+		// the tile's pair ids, for the epilogue's y rows and token flags (the
+		// down kernel's activation rows are the tile's dense h rows, so its
+		// stages never waited for these: loaded in the prologue, in a
+		// register until now)
+		if (t < nrows)
+			spair[t] = pair_id;
+		__syncthreads();
+	}
 	// gate/up: TIE's SiLU table (32 KiB) into the now idle stage buffers, so
 	// the epilogue's table lookups are LDS reads
 	const float *silu = a.silu;
@@ -1371,42 +1380,49 @@ mfma_experts_kernel(MfmaArgs a)
 	const int m0 = li * rpt;
 	const int pbase = off + m0; // the tile's first row in the dense h rows
 	const int nrows = min(rpt, cnt - m0);
-	// the tile's pair ids (rows m0 .. m0 + nrows - 1 of the expert's bucket)
+	// the tile's pair ids (rows m0 .. m0 + nrows - 1 of the expert's bucket):
+	// gate/up gathers its activation rows by them, the down kernel needs
+	// them only in its epilogue (run_tile stores them there)
+	int pair_id = 0;
 	if (threadIdx.x < nrows)
-		spair[threadIdx.x] = a.bucket[(size_t)e * a.bstride + m0 + threadIdx.x];
-	__syncthreads();
+		pair_id = a.bucket[(size_t)e * a.bstride + m0 + threadIdx.x];
+	if constexpr (!DOWN) {
+		if (threadIdx.x < nrows)
+			spair[threadIdx.x] = pair_id;
+		__syncthreads();
+	}
 #ifdef TIE_MFMA_TRACE
 	if (threadIdx.x == 0)
 		atomicAdd(&g_mfma_trace[DOWN][4], __builtin_readcyclecounter() - t_k0);
 #endif
 #ifdef TIE_MFMA_FIXED_NMT
 	// one tile height for every tile (one copy of run_tile's code)
-	run_tile<TYPE, DOWN, MT_TILES, MTR>(a, As, roff, spair, e, pbase, nrows, slab);
+	run_tile<TYPE, DOWN, MT_TILES, MTR>(a, As, roff, spair, e, pbase, nrows, slab, pair_id);
 	return;
 #endif
 	switch ((nrows + 31) >> 5) {
 	case 1:
-		run_tile<TYPE, DOWN, 1, MTR>(a, As, roff, spair, e, pbase, nrows, slab);
+		run_tile<TYPE, DOWN, 1, MTR>(a, As, roff, spair, e, pbase, nrows, slab, pair_id);
 		break;
 	case 2:
 		if constexpr (MT_TILES >= 2)
-			run_tile<TYPE, DOWN, (MT_TILES >= 2 ? 2 : 1), MTR>(a, As, roff, spair, e, pbase, nrows, slab);
+			run_tile<TYPE, DOWN, (MT_TILES >= 2 ? 2 : 1), MTR>(a, As, roff, spair, e, pbase, nrows, slab, pair_id);
 		break;
 	case 3:
 		if constexpr (MT_TILES >= 3)
-			run_tile<TYPE, DOWN, (MT_TILES >= 3 ? 3 : 1), MTR>(a, As, roff, spair, e, pbase, nrows, slab);
+			run_tile<TYPE, DOWN, (MT_TILES >= 3 ? 3 : 1), MTR>(a, As, roff, spair, e, pbase, nrows, slab, pair_id);
 		break;
 	case 4:
 		if constexpr (MT_TILES >= 4)
-			run_tile<TYPE, DOWN, (MT_TILES >= 4 ? 4 : 1), MTR>(a, As, roff, spair, e, pbase, nrows, slab);
+			run_tile<TYPE, DOWN, (MT_TILES >= 4 ? 4 : 1), MTR>(a, As, roff, spair, e, pbase, nrows, slab, pair_id);
 		break;
 	case 5:
 		if constexpr (MT_TILES >= 5)
-			run_tile<TYPE, DOWN, (MT_TILES >= 5 ? 5 : 1), MTR>(a, As, roff, spair, e, pbase, nrows, slab);
+			run_tile<TYPE, DOWN, (MT_TILES >= 5 ? 5 : 1), MTR>(a, As, roff, spair, e, pbase, nrows, slab, pair_id);
 		break;
 	default:
 		if constexpr (MT_TILES >= 6)
-			run_tile<TYPE, DOWN, (MT_TILES >= 6 ? 6 : 1), MTR>(a, As, roff, spair, e, pbase, nrows, slab);
+			run_tile<TYPE, DOWN, (MT_TILES >= 6 ? 6 : 1), MTR>(a, As, roff, spair, e, pbase, nrows, slab, pair_id);
 	}
 #ifdef TIE_MFMA_TIMELINE
 	{
