@@ -285,6 +285,12 @@ int tie_hip_stream_status(void *stream);
  * workgroup still exits): the error path of tie_hip_stream_status. */
 void tie_hip_debug_decode_give_up(int n);
 
+/* Debug: force the one-launch one-token kernel's form -- 0 a lane per
+ * (row, block) dot, 1 two lanes per dot where the shape's block size and LDS
+ * allow them; -1 chosen by the shape (two lanes when every workgroup fits
+ * at once).  Both forms give the same bits. */
+void tie_hip_debug_decode_form(int form);
+
 /* Debug: the powers of two the layer's matrix-core path scales h and y by
  * (h stored as f16(h 2^-h_shift), y as f16(y 2^-y_shift)), chosen at
  * upload from samples of the gate and down weights. */

@@ -244,6 +244,21 @@ def test_full_size_configs(cfg):
     run_both(layer, x, c["k"])
 
 
+@pytest.mark.parametrize("gu,dn", [(synth.Q4_K, synth.Q6_K), (synth.Q6_K, synth.Q4_K), (synth.Q4_K, synth.Q4_K)])
+def test_one_launch_forms_agree(gu, dn):
+    """Both forms of the one-launch one-token kernel give TIE's bits: a lane
+    per (row, block) dot, and lane pairs (each lane half of a block's
+    accumulators and code words, lane 0 gathering the other half)."""
+    layer = synth_layer(31, 1024, 768, 64, gu, dn, None)
+    try:
+        for form in (0, 1):
+            tie_amd.debug_decode_form(form)
+            print("one-launch form %d" % form, flush=True)
+            run_both(layer, synth.make_input(32 + form, 1, 1024), 8)
+    finally:
+        tie_amd.debug_decode_form(-1)
+
+
 @pytest.mark.parametrize("gu,dn", [(synth.BF16, synth.BF16), (synth.Q4_K, synth.BF16), (synth.BF16, synth.Q6_K)])
 def test_one_token_other_types(gu, dn):
     """One token with BF16 on either side: routing in the gate/up prologue

@@ -30,7 +30,7 @@ EXPORTS = (
     "tie_hip_silu_table_host", "tie_hip_layer_create", "tie_hip_layer_destroy", "tie_hip_layer_bytes",
     "tie_hip_moe_forward", "tie_hip_exact_max_tokens", "tie_hip_set_exact_max_tokens",
     "tie_hip_debug_fail_alloc", "tie_hip_host_expf", "tie_hip_profile_enable", "tie_hip_profile_read",
-    "tie_hip_moe_forward_noalloc", "tie_hip_stream_status", "tie_hip_debug_decode_give_up",
+    "tie_hip_moe_forward_noalloc", "tie_hip_stream_status", "tie_hip_debug_decode_give_up", "tie_hip_debug_decode_form",
     "tie_hip_stream_release", "tie_hip_debug_layer_shifts",
 )
 
@@ -137,6 +137,8 @@ def lib():
         L.tie_hip_stream_status.restype = I
         L.tie_hip_debug_decode_give_up.argtypes = [I]
         L.tie_hip_debug_decode_give_up.restype = None
+        L.tie_hip_debug_decode_form.argtypes = [I]
+        L.tie_hip_debug_decode_form.restype = None
         L.tie_hip_profile_enable.argtypes = [I]
         L.tie_hip_profile_enable.restype = I
         L.tie_hip_profile_read.argtypes = [ctypes.c_char_p, ctypes.c_size_t, P, P, I]
@@ -204,6 +206,12 @@ def stream_release(stream=None):
 
 def debug_decode_give_up(n):
     lib().tie_hip_debug_decode_give_up(int(n))
+
+
+def debug_decode_form(form):
+    """Force the one-token kernel's form (0 a lane per dot, 1 lane pairs;
+    -1 by the shape)."""
+    lib().tie_hip_debug_decode_form(int(form))
 
 
 def profile_enable(on=True):

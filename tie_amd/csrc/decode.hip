@@ -1408,13 +1408,21 @@ static int device_cus()
 // (by waves per SIMD and by LDS per CU): the dots' latency halves, while a
 // grid that does not fit would start its down workgroups only as gate/up
 // ones retire, so their weights would no longer stream during gate/up.
+// debug override of the choice (-1: by the shape, 0: one lane per dot, 1:
+// lane pairs where the shape allows them)
+static int g_one_force_form = -1;
+
 static bool one_pairs(const Layer &L, int k)
 {
+	if (g_one_force_form == 0)
+		return false;
 	int rpr, rg, rd, threads;
 	size_t lds;
 	one_shape(L, k, 2, rpr, rg, rd, threads, lds);
 	if (threads > DEC_MAX_THREADS || lds > DEC_MAX_LDS)
 		return false;
+	if (g_one_force_form == 1)
+		return true;
 	const long wgs = (L.E + rpr - 1) / rpr + (long)(L.F / rg) * k + L.d / rd;
 	const long waves_wg = threads / 64;
 	const long per_cu = std::min((long)(4 * ONE_PAIR_WAVES) / waves_wg, (long)((160 * 1024) / std::max(lds, (size_t)1)));
@@ -1797,7 +1805,12 @@ hipError_t launch_dense_rows(const ExpertTensor &W, const float *x, int T, float
 
 } // namespace tie
 
-
+// Debug: force the one-launch decode's form (0 a lane per dot, 1 lane pairs
+// where the shape allows them; -1 chosen by the shape)
+extern "C" void tie_hip_debug_decode_form(int form)
+{
+	tie::g_one_force_form = form;
+}
 
 #ifdef TIE_ONE_TRACE
 extern "C" int tie_hip_debug_one_trace(unsigned long long *host, int reset)
