@@ -86,6 +86,12 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 #ifndef TIE_Q4K_KST
 #define TIE_Q4K_KST 64
 #endif
+// the same for the 32-row tile kernels (decode-sized batches); 128 halves
+// their stage barriers but measured slower on the 30B shapes (T = 32:
+// 0.1202 vs 0.1193 ms, T = 64: 0.1358 vs 0.1315 ms)
+#ifndef TIE_Q4K_KST_TINY
+#define TIE_Q4K_KST_TINY 64
+#endif
 // Q6_K K per stage: 128 (one block half), or 64 (quarters {p, p + 2} of a
 // half, which share their ql / qh bytes; the activations' K order is
 // permuted to match)
@@ -189,7 +195,8 @@ template <int TYPE, bool DOWN = false, int MTR = 0> struct Cfg {
 	static constexpr bool F16 = TIE_MFMA_F16 && (TYPE == TIE_GGML_Q4_K || TYPE == TIE_GGML_Q6_K);
 	// K per stage (Q4_K optionally 64: one 64-weight group per stage)
 	static constexpr int KST = SPLIT ? 64
-				    : (TYPE == TIE_GGML_Q4_K ? TIE_Q4K_KST : TYPE == TIE_GGML_Q6_K ? TIE_Q6K_KST : 128);
+				    : (TYPE == TIE_GGML_Q4_K ? (MTR == MFMA_MT_TINY ? TIE_Q4K_KST_TINY : TIE_Q4K_KST)
+				       : TYPE == TIE_GGML_Q6_K ? TIE_Q6K_KST : 128);
 	// Q6_K 64-K stages hold quarters p and p + 2 of a block half
 	static constexpr bool APERM = TYPE == TIE_GGML_Q6_K && KST == 64;
 	static constexpr int SPB = QK / KST;                 // stages per 256-weight block (quantised)
@@ -311,8 +318,8 @@ __device__ __forceinline__ void load_b(const BSrc &s, int st, int h, BRegs<TYPE>
 // then the 4 panels' d planes (128 B each).  h = st % 2 (the block half).
 // Wave w moves items 4c + w (panel (4c + w) / NCH, slot (4c + w) % NCH);
 // their bases and panel offsets are set once per tile (BDma).
-template <int TYPE> struct BDma {
-	static constexpr int NCH = Cfg<TYPE>::NCH;
+template <int TYPE, int MTR = 0> struct BDma {
+	static constexpr int NCH = Cfg<TYPE, false, MTR>::NCH;
 	const uint8_t *base[NCH]; // expert base of the item's matrix (wave-uniform)
 	uint32_t pofs[NCH];       // the item's panel row offset in the expert (wave-uniform)
 	int slot[NCH];            // the item's LDS slot
@@ -322,10 +329,10 @@ template <int TYPE> struct BDma {
 	uint32_t dpofs;           // Q6_K: offset of panel w's d plane in its first block column
 };
 
-template <int TYPE, bool DOWN>
-__device__ __forceinline__ void bdma_init(const MfmaArgs &a, int e, int slab, int w, BDma<TYPE> &d)
+template <int TYPE, bool DOWN, int MTR = 0>
+__device__ __forceinline__ void bdma_init(const MfmaArgs &a, int e, int slab, int w, BDma<TYPE, MTR> &d)
 {
-	using C = Cfg<TYPE>;
+	using C = Cfg<TYPE, false, MTR>;
 	const uint32_t pbytes = (uint32_t)panel_bytes(TYPE);
 	const uint32_t nkb = (uint32_t)(a.in / QK);
 #pragma unroll
@@ -348,10 +355,10 @@ __device__ __forceinline__ void bdma_init(const MfmaArgs &a, int e, int slab, in
 	}
 }
 
-template <int TYPE, bool DOWN>
-__device__ __forceinline__ void dma_b(const BDma<TYPE> &d, int slab, int st, int w, uint8_t *B)
+template <int TYPE, bool DOWN, int MTR = 0>
+__device__ __forceinline__ void dma_b(const BDma<TYPE, MTR> &d, int slab, int st, int w, uint8_t *B)
 {
-	using C = Cfg<TYPE>;
+	using C = Cfg<TYPE, false, MTR>;
 	const int half = st & 1, part = st % C::SPB;
 	const uint32_t kofs = (uint32_t)(st / C::SPB) * (uint32_t)panel_bytes(TYPE);
 	const uint32_t lb = lds_addr(B);
@@ -379,10 +386,10 @@ __device__ __forceinline__ void dma_b(const BDma<TYPE> &d, int slab, int st, int
 
 // The lane's weights of the stage from LDS buffer B: row j of the lane in
 // panel p[j], slot i[j].
-template <int TYPE>
+template <int TYPE, int MTR = 0>
 __device__ __forceinline__ void lds_b(const uint8_t *B, const int p[2], const int i[2], int st, int h, BRegs<TYPE> &b)
 {
-	using C = Cfg<TYPE>;
+	using C = Cfg<TYPE, false, MTR>;
 #pragma unroll
 	for (int j = 0; j < 2; j++) {
 		const uint8_t *pb = B + p[j] * C::PB + i[j] * 16;
@@ -445,13 +452,13 @@ struct Fac {
 
 // Q4_K: group g = 2*(st%2) + gi of the block; sub-blocks 2g (low nibbles,
 // K 0..31 of the group) and 2g+1 (high nibbles, K 32..63).
-template <int TYPE>
+template <int TYPE, int MTR = 0>
 __device__ __forceinline__ void group_factors(const BRegs<TYPE> &b, int st, int gi, Fac &f)
 {
 #pragma unroll
 	for (int j = 0; j < 2; j++) {
 		if constexpr (TYPE == TIE_GGML_Q4_K) {
-			const int g = (4 / Cfg<TYPE>::SPB) * (st % Cfg<TYPE>::SPB) + gi;
+			const int g = (4 / Cfg<TYPE, false, MTR>::SPB) * (st % Cfg<TYPE, false, MTR>::SPB) + gi;
 			const float d = f16_to_f32(b.sc[j].x & 0xffffu), dmin = f16_to_f32(b.sc[j].x >> 16);
 #pragma unroll
 			for (int u = 0; u < 2; u++) {
@@ -489,7 +496,7 @@ __device__ __forceinline__ f16x2 splat16(float v)
 // (q sc) d 2^S + M with q sc exact and one rounding (deq_step16), not
 // q (d sc) + M with d sc rounded to f16 first: that rounding, shared by the
 // 32 weights of a sub-block, was half of the weights' error.
-template <int TYPE>
+template <int TYPE, int MTR = 0>
 __device__ __forceinline__ void group_factors16(const BRegs<TYPE> &b, int st, int gi, Fac16 &f)
 {
 	const f16x2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
@@ -498,7 +505,7 @@ __device__ __forceinline__ void group_factors16(const BRegs<TYPE> &b, int st, in
 	const f16x2 sdm = {(_Float16)(float)(1 << F16_SHIFT), (_Float16)(-(float)(1 << F16_SHIFT))};
 #pragma unroll
 	for (int j = 0; j < 2; j++) {
-		const int g = (4 / Cfg<TYPE>::SPB) * (st % Cfg<TYPE>::SPB) + gi;
+		const int g = (4 / Cfg<TYPE, false, MTR>::SPB) * (st % Cfg<TYPE, false, MTR>::SPB) + gi;
 		const f16x2 dd = __builtin_bit_cast(f16x2, b.sc[j].x);
 #pragma unroll
 		for (int u = 0; u < 2; u++) {
@@ -528,8 +535,10 @@ __device__ __forceinline__ void deq_step16(const BRegs<TIE_GGML_Q4_K> &b, const 
 {
 #pragma unroll
 	for (int j = 0; j < 2; j++) {
-		const int sub = s & 3, u = sub >> 1;
-		const u32x2 q = b.q[j][sub & 1];
+		// step s of the stage: 64-weight group gi = s / 4 (stages of 128 K
+		// hold two), quarter sub = s % 4
+		const int gi = s >> 2, sub = s & 3, u = sub >> 1;
+		const u32x2 q = b.q[j][2 * gi + (sub & 1)];
 		const uint32_t msk = u ? kc.hi : kc.lo;
 		uint32_t w[4] = {q.x, q.x >> 8, q.y, q.y >> 8};
 		f16x2 r[4];
@@ -726,26 +735,26 @@ template <int N> __device__ __forceinline__ void stage_barrier_keep()
 
 // Operand arithmetic of a quantised kernel: bf16 fragments, or f16 ones
 // (Q4_K gate/up).
-template <int TYPE, bool DOWN, bool F16 = Cfg<TYPE, DOWN>::F16> struct Ops;
-template <int TYPE, bool DOWN> struct Ops<TYPE, DOWN, false> {
+template <int TYPE, bool DOWN, int MTR = 0, bool F16 = Cfg<TYPE, DOWN>::F16> struct Ops;
+template <int TYPE, bool DOWN, int MTR> struct Ops<TYPE, DOWN, MTR, false> {
 	using V = bf16x8;
 	using F = Fac;
-	__device__ static void factors(const BRegs<TYPE> &b, int st, int gi, F &f) { group_factors<TYPE>(b, st, gi, f); }
+	__device__ static void factors(const BRegs<TYPE> &b, int st, int gi, F &f) { group_factors<TYPE, MTR>(b, st, gi, f); }
 	__device__ static void deq(const BRegs<TYPE> &b, const F &f, const K16 &, int st, int s, V out[2])
 	{
 		deq_step<TYPE>(b, f, st, s, out);
 	}
 	__device__ static f32x16 mma(V a, V b, f32x16 c) { return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0); }
 };
-template <int TYPE, bool DOWN> struct Ops<TYPE, DOWN, true> {
+template <int TYPE, bool DOWN, int MTR> struct Ops<TYPE, DOWN, MTR, true> {
 	using V = f16x8;
 	using F = typename std::conditional<TYPE == TIE_GGML_Q4_K, Fac16, Fac>::type;
 	__device__ static void factors(const BRegs<TYPE> &b, int st, int gi, F &f)
 	{
 		if constexpr (TYPE == TIE_GGML_Q4_K)
-			group_factors16<TYPE>(b, st, gi, f);
+			group_factors16<TYPE, MTR>(b, st, gi, f);
 		else
-			group_factors<TYPE>(b, st, gi, f);
+			group_factors<TYPE, MTR>(b, st, gi, f);
 	}
 	__device__ static void deq(const BRegs<TYPE> &b, const F &f, const K16 &kc, int st, int s, V out[2])
 	{
@@ -902,12 +911,12 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 		// weights dequantised; the next stage's DMA is issued after step 0's
 		// MFMAs; the last step's MFMAs run after the stage barrier, while the
 		// next stage's weights are read from LDS and its step 0 prepared.
-		using O = Ops<TYPE, DOWN>;
+		using O = Ops<TYPE, DOWN, MTR>;
 		using V = typename O::V;
 		constexpr int NA = NMT;
 		static_assert(C::NPL == 1 && C::NSTEP % 2 == 0, "one activation plane, even step count");
-		BDma<TYPE> bd;
-		bdma_init<TYPE, DOWN>(a, e, slab, w, bd);
+		BDma<TYPE, MTR> bd;
+		bdma_init<TYPE, DOWN, MTR>(a, e, slab, w, bd);
 		constexpr int NS = C::NS;
 		auto abuf = [&](int st) { return As + (st % NS) * C::ABUF; };
 		auto bbuf = [&](int st) { return Bs + (st % NS) * C::BBUF; };
@@ -915,7 +924,7 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 		auto issue = [&](int st) {
 			if (st < nk) {
 				dma_a<TYPE, DOWN, NMT, MTR>(as, st, w, abuf(st));
-				dma_b<TYPE, DOWN>(bd, slab, st, w, bbuf(st));
+				dma_b<TYPE, DOWN, MTR>(bd, slab, st, w, bbuf(st));
 			}
 		};
 		// direct loads one wave issues per stage (dma_a + dma_b)
@@ -992,7 +1001,7 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 			// st + NS - 1 first, then its weights from LDS, then the steps)
 			for (int st = 0; st < nk; st++) {
 				issue(st + NS - 1);
-				lds_b<TYPE>(bbuf(st), bp, bi, st, h, b);
+				lds_b<TYPE, MTR>(bbuf(st), bp, bi, st, h, b);
 				prep(st, 0, 0);
 #pragma unroll
 				for (int s = 0; s < C::NSTEP; s++) {
