@@ -36,8 +36,9 @@
 // MFMAs (the small-tile gate/up kernel: 40 KiB, 128 registers, three).  No register holds a prefetched stage, and the compiler's
 // wait-count pass never sees (and never waits for) the prefetch: the stage
 // barrier is the wait.  In the 32x32x16 B-operand layout a lane holds 8
-// consecutive K values of one weight row -- 8 consecutive quant bytes of
-// its lane-row in the panel -- which it reads from LDS and dequantises
+// K values of one weight row -- 8 consecutive quant bytes of its lane-row
+// in the panel (the activations' K order matches) -- which it reads from
+// LDS and dequantises
 // between the MFMAs: every weight of the tile is dequantised exactly once,
 // and each B fragment feeds one MFMA per 32-row M tile (an f16 lane holds
 // the pairs (0,2), (1,3), (4,6), (5,7) of those 8).  BF16 weights
@@ -251,13 +252,16 @@ template <int TYPE> struct BRegs;
 __device__ __forceinline__ uint32_t lds_addr(const void *p);
 __device__ __forceinline__ void dma16(const void *g, uint32_t lds);
 __device__ __forceinline__ void dma16s(const void *base, uint32_t voff, uint32_t lds);
+// Quantised weights: lane half h holds whole 16-byte code chunks (chunk h
+// of each pair), so the 32 lanes of a half read 32 consecutive rows' slots
+// (no LDS bank conflict); step s takes bytes 8 (s % 2) .. of them.
 template <> struct BRegs<TIE_GGML_Q4_K> {
-	u32x2 q[2][4];  // quant bytes 8h..8h+7 of the stage's 4 quant chunks
+	u32x4 q[2][2];  // per 64-weight group of the stage: quant chunk h of its two
 	u32x4 sc[2];    // chunk 0: d, dmin, 12 scale bytes
 };
 template <> struct BRegs<TIE_GGML_Q6_K> {
-	u32x2 ql[2][4]; // ql bytes 16p+8h..+7 of the half, p = 0..3
-	u32x2 qh[2][2]; // qh bytes 16p+8h..+7 of the half, p = 0..1
+	u32x4 ql[2][2]; // ql chunks 2c + h of the stage's ql slots, c < ql slots / 2
+	u32x4 qh[2];    // qh chunk h of the half
 	u32x2 sc[2];    // the half's 8 scales
 	uint32_t d[2];  // fp16 d
 };
@@ -277,37 +281,13 @@ struct BSrc {
 template <int TYPE>
 __device__ __forceinline__ void load_b(const BSrc &s, int st, int h, BRegs<TYPE> &b)
 {
+	static_assert(TYPE == TIE_GGML_BF16, "quantised weights are staged through LDS");
 	constexpr int KST = Cfg<TYPE>::KST;
-	if constexpr (TYPE == TIE_GGML_BF16) {
 #pragma unroll
-		for (int j = 0; j < 2; j++)
+	for (int j = 0; j < 2; j++)
 #pragma unroll
-			for (int q = 0; q < 4; q++)
-				b.w[j][q] = *reinterpret_cast<const u32x4 *>(s.p[j] + ((size_t)st * KST + 16 * q + 8 * h) * 2);
-	} else {
-		const size_t kb = (size_t)(st >> 1) * panel_bytes(TYPE); // two stages per 256-weight block
-		const int half = st & 1;
-#pragma unroll
-		for (int j = 0; j < 2; j++) {
-			const uint8_t *blk = s.p[j] + kb;
-			if constexpr (TYPE == TIE_GGML_Q4_K) {
-				// groups 2*half, 2*half+1: quant chunks 1+4*half .. 4+4*half
-#pragma unroll
-				for (int q = 0; q < 4; q++)
-					b.q[j][q] = *reinterpret_cast<const u32x2 *>(blk + (1 + 4 * half + q) * 1024 + 8 * h);
-				b.sc[j] = *reinterpret_cast<const u32x4 *>(blk);
-			} else {
-#pragma unroll
-				for (int q = 0; q < 4; q++)
-					b.ql[j][q] = *reinterpret_cast<const u32x2 *>(blk + (4 * half + q) * 1024 + 8 * h);
-#pragma unroll
-				for (int q = 0; q < 2; q++)
-					b.qh[j][q] = *reinterpret_cast<const u32x2 *>(blk + (8 + 2 * half + q) * 1024 + 8 * h);
-				b.sc[j] = *reinterpret_cast<const u32x2 *>(blk + 12 * 1024 + 8 * half);
-				b.d[j] = *reinterpret_cast<const uint16_t *>(blk + s.dofs[j]);
-			}
-		}
-	}
+		for (int q = 0; q < 4; q++)
+			b.w[j][q] = *reinterpret_cast<const u32x4 *>(s.p[j] + ((size_t)st * KST + 16 * q + 8 * h) * 2);
 }
 
 // The stage's weight chunks of the workgroup's 4 panels -> LDS buffer B:
@@ -395,22 +375,26 @@ __device__ __forceinline__ void lds_b(const uint8_t *B, const int p[2], const in
 		const uint8_t *pb = B + p[j] * C::PB + i[j] * 16;
 		if constexpr (TYPE == TIE_GGML_Q4_K) {
 #pragma unroll
-			for (int q = 0; q < C::NCH - 1; q++)
-				b.q[j][q] = *reinterpret_cast<const u32x2 *>(pb + (1 + q) * 1024 + 8 * h);
+			for (int g = 0; g < (C::NCH - 1) / 2; g++)
+				b.q[j][g] = *reinterpret_cast<const u32x4 *>(pb + (1 + 2 * g + h) * 1024);
 			b.sc[j] = *reinterpret_cast<const u32x4 *>(pb);
 		} else if constexpr (TYPE == TIE_GGML_Q6_K) {
 			constexpr int NQL = C::APERM ? 2 : 4; // ql chunk slots
 #pragma unroll
-			for (int q = 0; q < NQL; q++)
-				b.ql[j][q] = *reinterpret_cast<const u32x2 *>(pb + q * 1024 + 8 * h);
-#pragma unroll
-			for (int q = 0; q < 2; q++)
-				b.qh[j][q] = *reinterpret_cast<const u32x2 *>(pb + (NQL + q) * 1024 + 8 * h);
+			for (int c = 0; c < NQL / 2; c++)
+				b.ql[j][c] = *reinterpret_cast<const u32x4 *>(pb + (2 * c + h) * 1024);
+			b.qh[j] = *reinterpret_cast<const u32x4 *>(pb + (NQL + h) * 1024);
 			const int half = C::APERM ? (st >> 1) & 1 : st & 1;
 			b.sc[j] = *reinterpret_cast<const u32x2 *>(pb + (NQL + 2) * 1024 + 8 * half);
 			b.d[j] = *reinterpret_cast<const uint16_t *>(B + 4 * C::PB + p[j] * 128 + 2 * i[j]);
 		}
 	}
+}
+
+// the lane's half of the wave (its K half of each 16-K step)
+__device__ __forceinline__ int lane_half()
+{
+	return (threadIdx.x >> 5) & 1;
 }
 
 // 8 weight codes (bytes of lo, hi) -> bf16x8 of fma(q, D, M)
@@ -538,7 +522,8 @@ __device__ __forceinline__ void deq_step16(const BRegs<TIE_GGML_Q4_K> &b, const 
 		// step s of the stage: 64-weight group gi = s / 4 (stages of 128 K
 		// hold two), quarter sub = s % 4
 		const int gi = s >> 2, sub = s & 3, u = sub >> 1;
-		const u32x2 q = b.q[j][2 * gi + (sub & 1)];
+		const u32x4 q4 = b.q[j][gi];
+		const u32x2 q = (sub & 1) ? u32x2{q4.z, q4.w} : u32x2{q4.x, q4.y};
 		const uint32_t msk = u ? kc.hi : kc.lo;
 		uint32_t w[4] = {q.x, q.x >> 8, q.y, q.y >> 8};
 		f16x2 r[4];
@@ -556,10 +541,11 @@ __device__ __forceinline__ void deq_step16(const BRegs<TIE_GGML_Q4_K> &b, const 
 
 // Dequantise the B fragments of 16-K step s of stage st for both rows.
 // Q4_K: step s is in group gi = s/4; steps 0, 1 of a group take the low
-// nibbles of its two chunks, steps 2, 3 the high nibbles.  Q6_K: the stage
-// is half st%2 of the block; step s is quarter r = s/2, positions
-// l = 16*(s%2) + 8h + i, code q = ql nibble | qh bits << 4 with scale
-// 8*half + l/16 + 2r (TIE's block_q6_k).
+// nibbles of bytes 0..7, 8..15 of the lane half's chunk h, steps 2, 3 the
+// high nibbles (positions 16h + 8(s%2) + i of the sub-block).  Q6_K: step
+// s is quarter r of the stage's half, positions l = 16h + 8(s%2) + i (bytes
+// 8(s%2) .. of ql / qh chunk h), code q = ql nibble | qh bits << 4 with
+// scale 8*half + l/16 + 2r (TIE's block_q6_k).
 template <int TYPE>
 __device__ __forceinline__ void deq_step(const BRegs<TYPE> &b, const Fac &f, int st, int s, bf16x8 out[2])
 {
@@ -569,19 +555,21 @@ __device__ __forceinline__ void deq_step(const BRegs<TYPE> &b, const Fac &f, int
 			out[j] = __builtin_bit_cast(bf16x8, b.w[j][s]);
 		} else if constexpr (TYPE == TIE_GGML_Q4_K) {
 			const int gi = s >> 2, sub = s & 3, u = sub >> 1;
-			const u32x2 q = b.q[j][2 * gi + (sub & 1)];
+			const u32x4 q4 = b.q[j][gi];
+			const u32x2 q = (sub & 1) ? u32x2{q4.z, q4.w} : u32x2{q4.x, q4.y};
 			out[j] = deq8((q.x >> (4 * u)) & 0x0f0f0f0fu, (q.y >> (4 * u)) & 0x0f0f0f0fu, f.D[j][u], f.M[j][u]);
 		} else {
 			// quarter r; 64-K stages: quarter p for steps 0, 1 and p + 2 for 2, 3
 			const int r = Cfg<TYPE>::APERM ? (st & 1) + 2 * (s >> 1) : s >> 1, lh = s & 1;
-			const u32x2 ql = b.ql[j][Cfg<TYPE>::APERM ? lh : 2 * (r & 1) + lh];
-			const u32x2 qh = b.qh[j][lh];
+			const u32x4 ql4 = b.ql[j][Cfg<TYPE>::APERM ? 0 : r & 1], qh4 = b.qh[j];
+			const u32x2 ql = lh ? u32x2{ql4.z, ql4.w} : u32x2{ql4.x, ql4.y};
+			const u32x2 qh = lh ? u32x2{qh4.z, qh4.w} : u32x2{qh4.x, qh4.y};
 			const int nsh = 4 * (r >> 1), hsh = 2 * r;
 			const uint32_t lo = ((ql.x >> nsh) & 0x0f0f0f0fu) | (((qh.x >> hsh) & 0x03030303u) << 4);
 			const uint32_t hi = ((ql.y >> nsh) & 0x0f0f0f0fu) | (((qh.y >> hsh) & 0x03030303u) << 4);
-			const int si = lh + 2 * r;
-			const uint32_t sw = si < 4 ? b.sc[j].x : b.sc[j].y;
-			const float W = f.d6[j] * (float)(int8_t)((sw >> (8 * (si & 3))) & 0xffu);
+			// scale 2r + h: positions 16 h + 8 (s % 2) + i of the quarter
+			const uint32_t sw = r < 2 ? b.sc[j].x : b.sc[j].y;
+			const float W = f.d6[j] * (float)(int8_t)((sw >> (16 * (r & 1) + 8 * lane_half())) & 0xffu);
 			out[j] = deq8(lo, hi, W, -32.0f * W);
 		}
 	}
@@ -598,8 +586,9 @@ __device__ __forceinline__ void deq_step16_q6k(const BRegs<TIE_GGML_Q6_K> &b, co
 #pragma unroll
 	for (int j = 0; j < 2; j++) {
 		const int r = Cfg<TIE_GGML_Q6_K>::APERM ? (st & 1) + 2 * (s >> 1) : s >> 1, lh = s & 1;
-		const u32x2 ql = b.ql[j][Cfg<TIE_GGML_Q6_K>::APERM ? lh : 2 * (r & 1) + lh];
-		const u32x2 qh = b.qh[j][lh];
+		const u32x4 ql4 = b.ql[j][Cfg<TIE_GGML_Q6_K>::APERM ? 0 : r & 1], qh4 = b.qh[j];
+		const u32x2 ql = lh ? u32x2{ql4.z, ql4.w} : u32x2{ql4.x, ql4.y};
+		const u32x2 qh = lh ? u32x2{qh4.z, qh4.w} : u32x2{qh4.x, qh4.y};
 		const int nsh = 4 * (r >> 1), hsh = 2 * r;
 		// the code bytes' bits 6, 7 may hold other qh bits: the f16 pairs
 		// below keep 6 bits of each (kc.q6), so a rotate (bits 2 hsh.. of
@@ -608,11 +597,11 @@ __device__ __forceinline__ void deq_step16_q6k(const BRegs<TIE_GGML_Q6_K> &b, co
 		auto qhs = [&](uint32_t v) { return __builtin_amdgcn_alignbit(v, v, (uint32_t)(hsh + 28) & 31u); };
 		const uint32_t lo = ((ql.x >> nsh) & 0x0f0f0f0fu) | (qhs(qh.x) & 0xf0f0f0f0u);
 		const uint32_t hi = ((ql.y >> nsh) & 0x0f0f0f0fu) | (qhs(qh.y) & 0xf0f0f0f0u);
-		const int si = lh + 2 * r;
-		const uint32_t sw = si < 4 ? b.sc[j].x : b.sc[j].y;
+		// scale 2r + h: positions 16 h + 8 (s % 2) + i of the quarter
+		const uint32_t sw = r < 2 ? b.sc[j].x : b.sc[j].y;
 		// (q - 32) sc exact in f16 (|sc| <= 64: |(q - 32) sc| <= 2048), then
 		// times d 2^S with one rounding: d sc is not rounded to f16 first
-		const f16x2 SC = splat16((float)(int8_t)((sw >> (8 * (si & 3))) & 0xffu));
+		const f16x2 SC = splat16((float)(int8_t)((sw >> (16 * (r & 1) + 8 * lane_half())) & 0xffu));
 		const f16x2 D = splat16(f.d6[j] * (float)(1 << F16_SHIFT));
 		const uint32_t w[4] = {lo, lo >> 8, hi, hi >> 8};
 		f16x2 q[4];
@@ -856,8 +845,12 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 	{
 		const int rsub = lane / C::CPR, slot = lane % C::CPR;
 		const int chunk = slot ^ C::swz(C::RPI * w + rsub);
-		// APERM: chunks 0..3 are K 32p + 8c of the half, chunks 4..7 K 64 + 32p + 8(c - 4)
-		const int cofs = C::APERM ? 128 * (chunk >> 2) + 16 * (chunk & 3) : 16 * chunk;
+		// Slot 2s + h of a stage holds the K of step s, lane half h.
+		// Quantised weights: the 8-groups 1 and 2 of each 32-K quarter
+		// swapped (lane half h takes code chunk h, a step half of it).
+		// APERM: slots 0..3 are K 32p + ... of the half, slots 4..7 K 64 + 32p + ...
+		const int q8 = C::SPLIT ? chunk & 3 : ((chunk & 1) << 1) | ((chunk >> 1) & 1);
+		const int cofs = C::APERM ? 128 * (chunk >> 2) + 16 * q8 : 64 * (chunk >> 2) + 16 * q8;
 		as.base[0] = (const char *)a.a16;
 		as.base[1] = (const char *)a.a16lo;
 		as.cofs = cofs;
