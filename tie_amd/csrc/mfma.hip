@@ -1197,8 +1197,17 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 #pragma unroll
 				for (int q = 0; q < 16 * CPRW / 64; q++) {
 					const int cidx = lane + 64 * q, r = cidx / CPRW, part = cidx % CPRW;
-					const float4 v0 = *reinterpret_cast<const float4 *>(tl + r * LS + 8 * part);
-					const float4 v1 = *reinterpret_cast<const float4 *>(tl + r * LS + 8 * part + 4);
+					// down: odd rows read their second 4 columns first, so
+					// the two rows of a 16-lane read group fall in different
+					// banks (row stride 72 floats: 8 banks apart)
+					const int sw = DOWN ? 4 * (r & 1) : 0;
+					float4 u0 = *reinterpret_cast<const float4 *>(tl + r * LS + 8 * part + sw);
+					float4 u1 = *reinterpret_cast<const float4 *>(tl + r * LS + 8 * part + 4 - sw);
+					// (kept as two reads at these addresses, not folded into
+					// reads of the selected addresses)
+					asm volatile("" : "+v"(u0.x), "+v"(u0.y), "+v"(u0.z), "+v"(u0.w), "+v"(u1.x), "+v"(u1.y),
+						     "+v"(u1.z), "+v"(u1.w));
+					const float4 v0 = sw ? u1 : u0, v1 = sw ? u0 : u1;
 					const int mrow = 32 * mt + 16 * half + r;
 					if (mrow < nrows) {
 						if (DOWN && a.y16) {
