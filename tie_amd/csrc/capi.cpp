@@ -229,7 +229,8 @@ static int ensure_init()
 
 // The workspace layout for P pairs (and as many tokens at most), F, d and E
 // at most: its size, and (b != null) the pointers of *w into b.
-static size_t carve_workspace(uint8_t *b, size_t P, size_t FF, size_t DD, size_t EE, Workspace *w)
+static size_t carve_workspace(uint8_t *b, size_t P, size_t FF, size_t DD, size_t EE, Workspace *w,
+			      bool direct_h = true)
 {
 	const size_t Tcap = P; // tokens <= pairs since k >= 1
 	size_t off = 0;
@@ -244,6 +245,9 @@ static size_t carve_workspace(uint8_t *b, size_t P, size_t FF, size_t DD, size_t
 		     o_hlo = take(P * FF * 2), o_xlo = take(Tcap * DD * 2), o_nm = take(Tcap * DD * 4);
 	const size_t o_bc = take(EE * 4), o_mk = take(EE * (size_t)T4((int)Tcap)), o_bk = take(EE * T4((int)Tcap) * 4);
 	const size_t o_fl = take(Tcap * 4), o_fx = take(Tcap * 4), o_fc = take(4);
+	// h by expert for decode-sized matrix-core batches (not in the
+	// no-allocation entry point's scratch: that path groups h by position)
+	const size_t o_hd = direct_h ? take(EE * MFMA_DIRECT_T * FF * 2) : 0;
 	const size_t o_lg = take(ONE_LG_COPIES * one_copy_words(EE) * 8),
 		     o_dn = take(ONE_H_COPIES * one_copy_words((size_t)MAX_K * FF) * 8), o_st = take(4);
 	if (!b)
@@ -256,6 +260,7 @@ static size_t carve_workspace(uint8_t *b, size_t P, size_t FF, size_t DD, size_t
 	w->logits = (float *)(b + o_logits);
 	w->h = (float *)(b + o_h);
 	w->hb = (uint16_t *)(b + o_hb);
+	w->hd = direct_h ? (uint16_t *)(b + o_hd) : nullptr;
 	w->y = (float *)(b + o_y);
 	w->normed = (float *)(b + o_nm);
 	w->xb = (uint16_t *)(b + o_xb);
@@ -798,14 +803,14 @@ extern "C" int tie_hip_moe_forward_noalloc(tie_hip_layer *layer, const float *x_
 	if (T < 0 || k < 1 || k > L.E || k > MAX_K)
 		return set_error(TIE_HIP_EINVAL, "bad T=%d or k=%d", T, k);
 	const size_t P = (size_t)(T > 0 ? T : 1) * k;
-	const size_t need = carve_workspace(nullptr, P, L.F, L.d, L.E, nullptr);
+	const size_t need = carve_workspace(nullptr, P, L.F, L.d, L.E, nullptr, false);
 	if (need > SCRATCH_BYTES)
 		return set_error(TIE_HIP_EINVAL,
 				 "T=%d, k=%d needs %zu bytes of scratch, above the %zu of the no-allocation entry point "
 				 "(use tie_hip_moe_forward)",
 				 T, k, need, SCRATCH_BYTES);
 	Workspace ws;
-	carve_workspace(g_scratch, P, L.F, L.d, L.E, &ws);
+	carve_workspace(g_scratch, P, L.F, L.d, L.E, &ws, false);
 	hipStream_t s = stream ? (hipStream_t)stream : g.stream;
 	return forward(layer, x_dev, T, k, out_dev, topk_idx_dev, topk_w_dev, flags, s, nullptr, &ws);
 }

@@ -41,6 +41,11 @@ constexpr int MFMA_MT_GU_SMALL = 64;
 // over holds more weight stages in flight), used up to TIE_MFMA_TINY_AVG
 // pairs per expert
 constexpr int MFMA_MT_TINY = 32;
+// Up to this many tokens (an expert then has at most this many pairs: one
+// 32-row tile), the 32-row-tile kernels run one work item per (expert,
+// column slab) and h is laid out by expert ([E][MFMA_DIRECT_T][F]), so a
+// workgroup finds its tile without a scan of the counts
+constexpr int MFMA_DIRECT_T = 32;
 #ifndef TIE_MFMA_TINY_AVG
 #define TIE_MFMA_TINY_AVG 8
 #endif
@@ -96,6 +101,7 @@ struct Workspace {
 	float *logits = nullptr;      // [T][E]   router logits
 	float *h = nullptr;           // [2][T*k][F] gate and up row sums (exact path)
 	uint16_t *hb = nullptr;       // [T*k][F] SwiGLU activations (bf16 hi/lo, MFMA path)
+	uint16_t *hd = nullptr;       // [E][MFMA_DIRECT_T][F] h by expert (decode-sized MFMA batches; null: none)
 	float *y = nullptr;           // [T*k][d] expert outputs
 	float *normed = nullptr;      // [T][d]   RMSNorm of the hidden state (residual forward)
 	uint16_t *hlo = nullptr;      // [T*k][F] SwiGLU activations, bf16 remainder (MFMA path, BF16 weights)

@@ -104,6 +104,11 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 #ifndef TIE_MFMA_F16
 #define TIE_MFMA_F16 1
 #endif
+// decode-sized batches: items (expert, slab) found without a scan (0: the
+// scanned tile list, as for larger batches)
+#ifndef TIE_MFMA_DIRECT
+#define TIE_MFMA_DIRECT 1
+#endif
 // Tiles with at least this many 32-row M tiles run the cross-stage
 // software pipeline (fewer: each stage self-contained)
 #ifndef TIE_MFMA_PIPE_NMT
@@ -174,6 +179,7 @@ struct MfmaArgs {
 	float *y;                // down out, fp32 rows: y [pair][d] (BF16 experts), out [token][rows] (dense matrices)
 	uint16_t *y16;           // down out (quantised experts): y [pair][d] as f16(y 2^-y_shift)
 	int mt_cap;              // pair rows per tile at most, below MT (0: MT; dense matrices at small T)
+	int direct;              // 32-row tiles, T <= MFMA_DIRECT_T: item (expert, slab), h rows [E][MFMA_DIRECT_T]
 	int32_t *tok_flag;       // [T] gate/up, h_f16: tokens whose h left the f16 range
 	int32_t *fix_list;       //     are appended here (once each) ...
 	int32_t *fix_count;      //     ... and counted
@@ -1335,68 +1341,90 @@ mfma_experts_kernel(MfmaArgs a)
 #ifdef TIE_MFMA_TIMELINE
 	const unsigned long long tl0 = __builtin_amdgcn_s_memrealtime();
 #endif
-	const int mtc = a.mt_cap > 0 && a.mt_cap < MT ? a.mt_cap : MT;
-	int e, li, off, slab;
-	{
-		int *sc = reinterpret_cast<int *>(As); // [2 MF_THREADS / 64] scan | e, li, off
-		const int t = threadIdx.x;
-		int c4[4], n4[4], csum = 0, nsum = 0;
-#pragma unroll
-		for (int i = 0; i < 4; i++) {
-			const int ex = 4 * t + i;
-			c4[i] = ex < a.E ? a.cnt[ex] : 0;
-			n4[i] = (c4[i] + mtc - 1) / mtc;
-			csum += c4[i];
-			nsum += n4[i];
-		}
-		// one scan of both sums (tiles in the high word, pairs in the low)
-		long long tot;
-		const long long b2 = block_exclusive_scan64<MF_THREADS>(((long long)nsum << 32) | (long long)csum,
-									 reinterpret_cast<long long *>(sc), tot);
-		const int ntiles = (int)(tot >> 32);
-		int nbase = (int)(b2 >> 32), cbase = (int)(b2 & 0xffffffffll);
-		// this workgroup's item (XCD-aware order: consecutive workgroup ids
-		// go round-robin over the 8 XCDs, each with its own L2; the id is
-		// remapped so that each XCD takes a contiguous run of (tile, column
-		// slab) items, and the slabs of one expert tile share an XCD and read
-		// the tile's gathered activation rows from its L2)
+	int e, slab, pbase, nrows, pair_id = 0;
+	if (MTR == MFMA_MT_TINY && a.direct) {
+		// one item per (expert, column slab), in the XCD-aware order below;
+		// the expert's count and its pair ids (at most MFMA_DIRECT_T, read
+		// before the count is known) in one memory round trip
 		const int nslab = gridDim.x;
-		const int live = ntiles * nslab;
+		const int live = a.E * nslab;
 		const int per_xcd = (live + 7) / 8;
 		const int lin = blockIdx.y * gridDim.x + blockIdx.x;
 		const int v = (lin % 8) * per_xcd + lin / 8;
 		if (lin / 8 >= per_xcd || v >= live)
 			return;
-		const int tile = v / nslab;
+		e = v / nslab;
 		slab = v % nslab;
+		const int t = threadIdx.x;
+		if (t < MFMA_DIRECT_T && t < a.bstride)
+			pair_id = a.bucket[(size_t)e * a.bstride + t];
+		nrows = a.cnt[e];
+		if (nrows == 0)
+			return;
+		pbase = e * MFMA_DIRECT_T;
+	} else {
+		const int mtc = a.mt_cap > 0 && a.mt_cap < MT ? a.mt_cap : MT;
+		int li, off;
+		{
+			int *sc = reinterpret_cast<int *>(As); // [2 MF_THREADS / 64] scan | e, li, off
+			const int t = threadIdx.x;
+			int c4[4], n4[4], csum = 0, nsum = 0;
 #pragma unroll
-		for (int i = 0; i < 4; i++) {
-			if (tile >= nbase && tile < nbase + n4[i]) {
-				sc[2 * MF_THREADS / 64] = 4 * t + i;
-				sc[2 * MF_THREADS / 64 + 1] = tile - nbase;
-				sc[2 * MF_THREADS / 64 + 2] = cbase;
+			for (int i = 0; i < 4; i++) {
+				const int ex = 4 * t + i;
+				c4[i] = ex < a.E ? a.cnt[ex] : 0;
+				n4[i] = (c4[i] + mtc - 1) / mtc;
+				csum += c4[i];
+				nsum += n4[i];
 			}
-			nbase += n4[i];
-			cbase += c4[i];
+			// one scan of both sums (tiles in the high word, pairs in the low)
+			long long tot;
+			const long long b2 = block_exclusive_scan64<MF_THREADS>(((long long)nsum << 32) | (long long)csum,
+										 reinterpret_cast<long long *>(sc), tot);
+			const int ntiles = (int)(tot >> 32);
+			int nbase = (int)(b2 >> 32), cbase = (int)(b2 & 0xffffffffll);
+			// this workgroup's item (XCD-aware order: consecutive workgroup ids
+			// go round-robin over the 8 XCDs, each with its own L2; the id is
+			// remapped so that each XCD takes a contiguous run of (tile, column
+			// slab) items, and the slabs of one expert tile share an XCD and read
+			// the tile's gathered activation rows from its L2)
+			const int nslab = gridDim.x;
+			const int live = ntiles * nslab;
+			const int per_xcd = (live + 7) / 8;
+			const int lin = blockIdx.y * gridDim.x + blockIdx.x;
+			const int v = (lin % 8) * per_xcd + lin / 8;
+			if (lin / 8 >= per_xcd || v >= live)
+				return;
+			const int tile = v / nslab;
+			slab = v % nslab;
+#pragma unroll
+			for (int i = 0; i < 4; i++) {
+				if (tile >= nbase && tile < nbase + n4[i]) {
+					sc[2 * MF_THREADS / 64] = 4 * t + i;
+					sc[2 * MF_THREADS / 64 + 1] = tile - nbase;
+					sc[2 * MF_THREADS / 64 + 2] = cbase;
+				}
+				nbase += n4[i];
+				cbase += c4[i];
+			}
+			__syncthreads();
+			e = sc[2 * MF_THREADS / 64];
+			li = sc[2 * MF_THREADS / 64 + 1];
+			off = sc[2 * MF_THREADS / 64 + 2];
+			__syncthreads(); // the stage buffers are free again
 		}
-		__syncthreads();
-		e = sc[2 * MF_THREADS / 64];
-		li = sc[2 * MF_THREADS / 64 + 1];
-		off = sc[2 * MF_THREADS / 64 + 2];
-		__syncthreads(); // the stage buffers are free again
+		const int cnt = a.cnt[e];
+		const int ntl = (cnt + mtc - 1) / mtc;
+		const int rpt = (cnt + ntl - 1) / ntl;
+		const int m0 = li * rpt;
+		pbase = off + m0; // the tile's first row in the dense h rows
+		nrows = min(rpt, cnt - m0);
+		// the tile's pair ids (rows m0 .. m0 + nrows - 1 of the expert's bucket):
+		// gate/up gathers its activation rows by them, the down kernel needs
+		// them only in its epilogue (run_tile stores them there)
+		if (threadIdx.x < nrows)
+			pair_id = a.bucket[(size_t)e * a.bstride + m0 + threadIdx.x];
 	}
-	const int cnt = a.cnt[e];
-	const int ntl = (cnt + mtc - 1) / mtc;
-	const int rpt = (cnt + ntl - 1) / ntl;
-	const int m0 = li * rpt;
-	const int pbase = off + m0; // the tile's first row in the dense h rows
-	const int nrows = min(rpt, cnt - m0);
-	// the tile's pair ids (rows m0 .. m0 + nrows - 1 of the expert's bucket):
-	// gate/up gathers its activation rows by them, the down kernel needs
-	// them only in its epilogue (run_tile stores them there)
-	int pair_id = 0;
-	if (threadIdx.x < nrows)
-		pair_id = a.bucket[(size_t)e * a.bstride + m0 + threadIdx.x];
 	if constexpr (!DOWN) {
 		if (threadIdx.x < nrows)
 			spair[threadIdx.x] = pair_id;
@@ -1782,8 +1810,13 @@ hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, con
 	// at least 8 * ceil(live / 8) workgroups (rows past the tiles exit at
 	// once)
 	const int mt_gu = mfma_gu_rows(L, npairs), mt_dn = mfma_dn_rows(L, npairs);
-	const int gu_tiles = (npairs + mt_gu - 1) / mt_gu + L.E + 8;
-	const int dn_tiles = (npairs + mt_dn - 1) / mt_dn + L.E + 8;
+	// decode-sized batches: one item per (expert, slab) and h by expert
+	// (both kernels of 32-row tiles, f16 h, the workspace's expert-major h)
+	a.direct = TIE_MFMA_DIRECT && mt_gu == MFMA_MT_TINY && mt_dn == MFMA_MT_TINY && T <= MFMA_DIRECT_T &&
+		   a.h_f16 && ws.hd != nullptr;
+	const int gu_tiles = a.direct ? L.E + 8 : (npairs + mt_gu - 1) / mt_gu + L.E + 8;
+	const int dn_tiles = a.direct ? L.E + 8 : (npairs + mt_dn - 1) / mt_dn + L.E + 8;
+	uint16_t *hrows = a.direct ? ws.hd : ws.hb;
 
 	prof_begin("mfma_gate_up", s);
 	a.w[0] = L.gate.data;
@@ -1794,7 +1827,7 @@ hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, con
 	a.in = L.d;
 	a.a16 = ws.xb;
 	a.a16lo = ws.xlo;
-	a.h16 = ws.hb;
+	a.h16 = hrows;
 	a.h16lo = ws.hlo;
 	hipError_t err = launch_one<false>(a, L.gate.type, dim3(L.F / GU_COLS, gu_tiles), s, mt_gu);
 	prof_end(s);
@@ -1806,7 +1839,7 @@ hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, con
 	a.expert_bytes[0] = a.expert_bytes[1] = L.down.expert_bytes;
 	a.rows = L.d;
 	a.in = L.F;
-	a.a16 = ws.hb;
+	a.a16 = hrows;
 	a.a16lo = ws.hlo;
 	if (split_down && !split) {
 		prof_end(s);
