@@ -1,15 +1,22 @@
 """Benchmark of the MI355X Qwen3-MoE FFN block (one GPU).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 30b_t32] [--extra 30b_t1,...] [--graph]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 30b_t32] [--extra 30b_t1,...]
+                    [--graph | --eager]
 
 A step is one MoE block forward (router, top-k, dispatch, experts, combine)
 over one batch of T tokens of synthetic input, with weights and inputs
 already resident in HBM.  Weights are cycled over L independently generated
 layers (and inputs over L token batches) so that no step finds its experts
 in the 256 MB MALL or the L2 left warm by the previous steps.  The K timed
-steps are K library calls from a Python loop (eager: the way TIE's host
-loop calls the block), bracketed by device synchronisations.  --graph times
-one replay of a HIP graph that captured the same K calls instead.
+steps of a batched workload (T > 1) are one replay of a HIP graph that
+captured K library calls (the way a serving loop replays a captured
+forward: no host launch cost between the block's kernels), bracketed by
+device synchronisations; the eager loop (K library calls from a Python
+loop, the way TIE's host loop calls the block) is timed as well and
+reported as ms_per_step_eager.  One-token workloads are timed eagerly: under
+capture they take their three-launch form, and the one-launch kernel is
+what the host loop runs.  --eager times every workload eagerly, --graph
+every workload as a graph replay.
 
 Prints one JSON line: the headline workload (`value`, tokens/s), the
 roofline of its dominant kernel (event-timed on the library's stream), the
@@ -465,8 +472,10 @@ def main():
     ap.add_argument("--path", default="auto", choices=["auto", "exact", "mfma"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--graph", action="store_true",
-                    help="time one replay of a HIP graph that captured the K steps instead of the eager loop (one "
-                         "library call per step); under capture one-token forwards take their three-launch form")
+                    help="time every workload as one replay of a HIP graph that captured the K steps (the default "
+                         "for T > 1); under capture one-token forwards take their three-launch form")
+    ap.add_argument("--eager", action="store_true",
+                    help="time every workload as the eager loop (one library call per step)")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="only run a plain device copy of this many MiB 5 times (the reference kernel for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes) and exit")
@@ -518,7 +527,7 @@ def main():
         warm = args.warmup if name == args.config else max(2, args.warmup // 4)
         log("timing %s: T=%d, %d warm-up + %d steps" % (name, cfg["T"], warm, steps))
         results[name] = run_config(torch, tie_amd, workloads[key], cfg["T"], cfg["k"], steps, warm, flags, cfg,
-                                   graph=args.graph)
+                                   graph=args.graph or (not args.eager and cfg["T"] > 1))
         gpu_outs[name] = (key, results[name].pop("gpu_out0"))
         log(json.dumps({name: results[name]}))
 
@@ -544,7 +553,7 @@ def main():
         r = results[name]
         extra[name] = {"tokens_per_s": round(r["tokens_per_s"], 1), "ms_per_step": round(r["ms"], 4),
                        "dtype": compute_dtype(r, synth.CONFIGS[name]),
-                       "ms_per_step_eager": round(r["ms_eager"], 4),
+                       "ms_per_step_eager": round(r["ms_eager"], 4), "timing": r["timing"],
                        "block_GBps": round(r["block_GBps"], 1), "block_TFLOPs": round(r["block_TFLOPs"], 3),
                        "roofline": roofline(r, name), "cpu_baseline": cpu.get(name), "parity": parity.get(name),
                        "kernels": r["kernels"]}

@@ -506,3 +506,65 @@ def test_auto_path_threshold():
             np.testing.assert_array_equal(bits(out), bits(ro))
         else:
             check_oracle("auto_T%d" % T, out, ro)
+
+
+def test_graph_replays_of_batches():
+    """Batched forwards captured in one HIP graph -- the matrix-core path at
+    T = 32 (one work item per expert and slab) and at T = 300 (tiled router
+    logits, selection bytes and bucket_plan, one token beyond the f16 range
+    recomputed exactly), and the exact path at T = 8 -- replayed four times
+    with eager work on the library stream in between: every replay equals
+    the eager result bit for bit (no step relies on memory cleared outside
+    its own kernels)."""
+    import torch
+    cases = [(synth_layer(90, 2048, 768, 128, synth.Q4_K, synth.Q6_K, None), 32, 8, tie_amd.PATH_MFMA),
+             (synth_layer(91, 512, 512, 32, synth.Q4_K, synth.Q6_K, None), 300, 4, tie_amd.PATH_MFMA),
+             (synth_layer(92, 512, 256, 16, synth.Q6_K, synth.Q4_K, None), 8, 4, tie_amd.PATH_EXACT)]
+    Ls = [tie_amd.Layer.from_synth(c[0]) for c in cases]
+    xs = []
+    for i, (layer, T, k, _) in enumerate(cases):
+        x = synth.make_input(93 + i, T, layer.d)
+        if T == 300:
+            x[7] *= np.float32(1e5)
+        xs.append(torch.from_numpy(x).cuda())
+    outs = [torch.empty_like(x) for x in xs]
+    idxs = [torch.empty((c[1], c[2]), dtype=torch.int32, device="cuda") for c in cases]
+    s = torch.cuda.Stream()
+
+    def run_all():
+        for L, x, o, ix, (layer, T, k, fl) in zip(Ls, xs, outs, idxs, cases):
+            L.forward(x, T, k, o, ix, None, flags=fl, stream=s.cuda_stream)
+
+    with torch.cuda.stream(s):
+        run_all()
+    torch.cuda.synchronize()
+    eager = [o.cpu().numpy() for o in outs]
+    eager_idx = [ix.cpu().numpy() for ix in idxs]
+    for i, (layer, T, k, fl) in enumerate(cases):
+        ro, ri, _ = bind.moe_block(layer, xs[i].cpu().numpy(), k)
+        np.testing.assert_array_equal(eager_idx[i], ri)
+        if fl == tie_amd.PATH_EXACT:
+            np.testing.assert_array_equal(bits(eager[i]), bits(ro))
+        else:
+            check_oracle("graph_eager_%d" % i, eager[i], ro)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s, capture_error_mode="thread_local"):
+        run_all()
+    for rep in range(4):
+        for o, ix in zip(outs, idxs):
+            o.fill_(-1.0)
+            ix.fill_(-7)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        print("graph replay %d" % rep, flush=True)
+        for i in range(len(cases)):
+            np.testing.assert_array_equal(bits(outs[i].cpu().numpy()), bits(eager[i]),
+                                          err_msg="replay %d case %d" % (rep, i))
+            np.testing.assert_array_equal(idxs[i].cpu().numpy(), eager_idx[i])
+        # eager forwards between replays, on the library stream
+        layer, T, k, _ = cases[rep % 3]
+        tie_amd.moe_ffn(xs[rep % 3].cpu().numpy(), layer, k)
+    del g
+    for L in Ls:
+        L.close()
