@@ -41,7 +41,7 @@ extern "C" {
 #define TIE_SILU_TABLE_SIZE 8192 /* SILU_TABLE_SIZE, engine.h:10 */
 
 /* Forward flags */
-#define TIE_HIP_PATH_AUTO 0x0  /* exact fp32 GEMV path up to tie_hip_exact_max_tokens() (24), 16-bit MFMA grouped GEMM above */
+#define TIE_HIP_PATH_AUTO 0x0  /* exact fp32 GEMV path up to tie_hip_exact_max_tokens() (21), 16-bit MFMA grouped GEMM above */
 #define TIE_HIP_PATH_EXACT 0x1 /* always the fp32 path that reproduces TIE's arithmetic bit for bit */
 #define TIE_HIP_PATH_MFMA 0x2  /* always the grouped-GEMM path */
 
@@ -268,7 +268,7 @@ const float *tie_hip_model_ffn_norm(const tie_hip_model *m, int n);
 void tie_hip_model_close(tie_hip_model *m);
 
 /* The largest T that TIE_HIP_PATH_AUTO sends down the exact path (default
- * 24, where the matrix-core path becomes the faster one at the 30B shape;
+ * 21: from 22 tokens on the matrix-core path is the faster one at the 30B shape;
  * 64 or more keeps every decode-sized batch bit-exact). */
 int tie_hip_exact_max_tokens(void);
 void tie_hip_set_exact_max_tokens(int t);

@@ -61,9 +61,10 @@ struct Ctx {
 	uint32_t *rsq = nullptr;   // host RSQRTSS table (built at the first residual call)
 	int rsq_bits = 0;
 	// TIE_HIP_PATH_AUTO: TIE's bit-exact kernels up to this many tokens,
-	// the matrix cores above (measured faster from T = 25 on at the 30B
-	// shape: T=24 0.111 / 0.115 ms, T=32 0.134 / 0.119 ms exact / MFMA)
-	int exact_max_t = 24;
+	// the matrix cores above (measured faster from T = 22 on at the 30B
+	// shape, graph-timed: T=20 0.1002 / 0.1043 ms, T=22 0.1072 / 0.1065 ms,
+	// T=24 0.1115 / 0.1083 ms exact / MFMA)
+	int exact_max_t = 21;
 	int debug_stale = 0; // one-launch decode calls left whose waits are made to give up (debug hook)
 	std::recursive_mutex mu;
 };

@@ -154,6 +154,8 @@ CONFIGS = {
     "30b_t4": dict(d=2048, F=768, E=128, k=8, T=4, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1244),
     "30b_t8": dict(d=2048, F=768, E=128, k=8, T=8, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1240),
     "30b_t16": dict(d=2048, F=768, E=128, k=8, T=16, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1252),
+    "30b_t20": dict(d=2048, F=768, E=128, k=8, T=20, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1257),
+    "30b_t22": dict(d=2048, F=768, E=128, k=8, T=22, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1259),
     "30b_t24": dict(d=2048, F=768, E=128, k=8, T=24, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1253),
     "30b_t32": dict(d=2048, F=768, E=128, k=8, T=32, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1235),
     "30b_t64": dict(d=2048, F=768, E=128, k=8, T=64, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1243),
