@@ -1343,9 +1343,11 @@ mfma_experts_kernel(MfmaArgs a)
 #endif
 	int e, slab, pbase, nrows, pair_id = 0;
 	if (MTR == MFMA_MT_TINY && a.direct) {
-		// one item per (expert, column slab), in the XCD-aware order below;
-		// the expert's count and its pair ids (at most MFMA_DIRECT_T, read
-		// before the count is known) in one memory round trip
+		// one item per (expert, column slab), mapped to the workgroups in the
+		// same XCD-aware order as the tile list's items (the slabs of an
+		// expert on one XCD); the expert's count and its pair ids (at most
+		// MFMA_DIRECT_T, read before the count is known) in one memory round
+		// trip
 		const int nslab = gridDim.x;
 		const int live = a.E * nslab;
 		const int per_xcd = (live + 7) / 8;
