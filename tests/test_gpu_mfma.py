@@ -242,6 +242,37 @@ def test_quantised_against_model_and_oracle(shape, types):
     check_oracle("q_%d_%d_%d_%d_%d_%d" % (d, F, E, k, T, types[0]), out, ro)
 
 
+@pytest.mark.parametrize("case", ["full_tiles", "one_token", "wide_E"])
+def test_direct_items_edges(case):
+    """Batches of up to 32 tokens (one work item per expert and column slab,
+    h by expert) at their edges: 32 nearly equal tokens (the same experts
+    for all: full 32-row tiles), one token on the matrix cores, and 1024
+    experts (a grid of 1032 item rows, most experts without pairs)."""
+    if case == "full_tiles":
+        d, F, E, k, T = 2048, 768, 128, 8, 32
+        rng = np.random.default_rng(95)
+        base = synth.make_input(96, 1, d)
+        x = (base * (1 + 1e-4 * rng.standard_normal((T, d)))).astype(np.float32)
+    elif case == "one_token":
+        d, F, E, k, T = 2048, 768, 128, 8, 1
+        x = synth.make_input(97, T, d)
+    else:
+        d, F, E, k, T = 256, 256, 1024, 8, 16
+        x = synth.make_input(98, T, d)
+    layer = synth_layer(99 + E + T, d, F, E, synth.Q4_K, synth.Q6_K, None)
+    out, idx, w = run_mfma(layer, x, k)
+    ro, ri, rw = bind.moe_block(layer, x, k)
+    check_routing(idx, w, ri, rw)
+    if case == "full_tiles":
+        # the same experts for every token (most of them): full tiles
+        assert max(int((ri == e).sum()) for e in np.unique(ri)) == T
+    m = model(layer, x, ri, rw, bind.silu_table())
+    e_model = rel_l2(out, m)
+    print("rel L2 vs kernel model %.3e" % e_model, flush=True)
+    assert e_model <= MODEL_RL2
+    check_oracle("direct_%s" % case, out, ro)
+
+
 @pytest.mark.parametrize("T,zipf", [(48, None), (200, 1.2)])
 def test_bf16_weights_split_activations(T, zipf):
     d, F, E, k = 512, 256, 16, 4

@@ -40,8 +40,11 @@ def run(L, x, k, flags, noalloc):
     return out.cpu().numpy(), idx.cpu().numpy(), w.cpu().numpy()
 
 
+# (PATH_MFMA, (32, 9)): the no-allocation scratch keeps the scanned tile
+# list where the forward's workspace runs one item per (expert, slab) with
+# h by expert -- the two give the same bits
 @pytest.mark.parametrize("flags,Ts", [(tie_amd.PATH_EXACT, (40, 7)), (tie_amd.PATH_AUTO, (1, 1)),
-                                      (tie_amd.PATH_MFMA, (80, 33))])
+                                      (tie_amd.PATH_MFMA, (80, 33)), (tie_amd.PATH_MFMA, (32, 9))])
 def test_noalloc_matches_forward(flags, Ts):
     layer = synth_layer(71, 2048, 768, 128, synth.Q4_K, synth.Q6_K, None)
     L = tie_amd.Layer.from_synth(layer)
