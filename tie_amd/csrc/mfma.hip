@@ -125,6 +125,9 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 #ifndef TIE_MFMA_TINY_GU_WPC
 #define TIE_MFMA_TINY_GU_WPC 4
 #endif
+#ifndef TIE_TINY_SILU_GLOBAL
+#define TIE_TINY_SILU_GLOBAL 1
+#endif
 #ifndef TIE_MFMA_TINY_DN_WPC
 #define TIE_MFMA_TINY_DN_WPC 3
 #endif
@@ -243,7 +246,12 @@ template <int TYPE, bool DOWN = false, int MTR = 0> struct Cfg {
 	static constexpr int LDS_A = NS * ABUF, LDS_B = B_LDS ? NS * BBUF : 0;
 	// the f16 kernels' epilogue tiles (gate/up: after the 32 KiB SiLU
 	// table) reuse the stage buffers; the dynamic LDS covers both
-	static constexpr int EPI_BYTES = (F16 && !SPLIT) ? (DOWN ? 0 : 32768) + NWAVES * 16 * (DOWN ? 72 : 40) * 4 : 0;
+	// gate/up: TIE's SiLU table staged in LDS for the epilogue, except in
+	// the 32-row tile kernels, where the table's 32 KiB would cost a
+	// workgroup per CU (they read it from global memory, L2-resident)
+	static constexpr bool SILU_LDS = !DOWN && !(MTR == MFMA_MT_TINY && TIE_TINY_SILU_GLOBAL);
+	static constexpr int EPI_BYTES =
+		(F16 && !SPLIT) ? (SILU_LDS ? 32768 : 0) + NWAVES * 16 * (DOWN ? 72 : 40) * 4 : 0;
 	static constexpr int STAGE_BYTES = LDS_A + LDS_B > EPI_BYTES ? LDS_A + LDS_B : EPI_BYTES;
 	// The slot of 16-byte chunk c of row r is c ^ swz(r): the rows of a
 	// fragment read then spread over all LDS banks without row padding
@@ -1109,7 +1117,7 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 	// gate/up: TIE's SiLU table (32 KiB) into the now idle stage buffers, so
 	// the epilogue's table lookups are LDS reads
 	const float *silu = a.silu;
-	if constexpr (!DOWN) {
+	if constexpr (C::SILU_LDS) {
 		static_assert(SILU_N * 4 <= C::STAGE_BYTES, "SiLU table must fit the stage buffers");
 #pragma unroll
 		for (int c = 0; c < SILU_N * 4 / 1024 / NWAVES; c++) {
@@ -1132,8 +1140,8 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 		constexpr int LS = DOWN ? 72 : 40;          // LDS row stride (floats)
 		// half an M tile (16 rows) at a time: registers i = 8 half .. 8 half + 7
 		// hold rows 16 half .. 16 half + 15
-		float *tl = reinterpret_cast<float *>(As + (DOWN ? 0 : 32768) + w * (16 * LS * 4));
-		static_assert((DOWN ? 0 : 32768) + NWAVES * 16 * LS * 4 <= C::STAGE_BYTES, "epilogue tile");
+		float *tl = reinterpret_cast<float *>(As + (C::SILU_LDS ? 32768 : 0) + w * (16 * LS * 4));
+		static_assert((C::SILU_LDS ? 32768 : 0) + NWAVES * 16 * LS * 4 <= C::STAGE_BYTES, "epilogue tile");
 		const int c0 = lane & 31;
 		// gate/up: K positions 1, 2 (and 5, 6) of each 8-group of h swapped
 		// (the dequantised pairs' order)
