@@ -235,26 +235,34 @@ def run_config(torch, tie_amd, wl, T, k, steps, warmup, flags, cfg=None, graph=F
     ms_eager = 1e3 * (time.perf_counter() - t0) / steps
     gpu_ms_eager = ev0.elapsed_time(ev1)
     ms = ms_eager
+    timing = "eager"
     if graph:
         # the same `steps` forwards captured once as a HIP graph on a stream
         # of their own (its workspace sized by the warm-up) and replayed: the
-        # GPU's time per step without the host's launch cost
-        gs = torch.cuda.Stream()
-        with torch.cuda.stream(gs):
-            for s in range(max(warmup, nL)):
-                step(s, stream=gs.cuda_stream)
-        torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=gs, capture_error_mode="thread_local"):
-            for s in range(steps):
-                step(s, stream=gs.cuda_stream)
-        g.replay()  # warm-up replay
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        g.replay()
-        torch.cuda.synchronize()
-        ms = 1e3 * (time.perf_counter() - t0) / steps
-        del g
+        # GPU's time per step without the host's launch cost.  A capture
+        # that fails leaves the eager time as the result (and says why).
+        try:
+            gs = torch.cuda.Stream()
+            with torch.cuda.stream(gs):
+                for s in range(max(warmup, nL)):
+                    step(s, stream=gs.cuda_stream)
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=gs, capture_error_mode="thread_local"):
+                for s in range(steps):
+                    step(s, stream=gs.cuda_stream)
+            g.replay()  # warm-up replay
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            g.replay()
+            torch.cuda.synchronize()
+            ms = 1e3 * (time.perf_counter() - t0) / steps
+            timing = "graph"
+            del g
+        except Exception as exc:  # noqa: BLE001 -- any capture failure falls back to the eager time
+            torch.cuda.synchronize()
+            log("graph capture failed (%s): reporting the eager time" % exc)
+            timing = "eager (graph capture failed: %s)" % type(exc).__name__
 
     # per-kernel timing over the same sequence of steps, from events bound to
     # each kernel's own dispatch; the device is drained after every step so
@@ -267,7 +275,7 @@ def run_config(torch, tie_amd, wl, T, k, steps, warmup, flags, cfg=None, graph=F
         torch.cuda.synchronize()
     prof = tie_amd.profile_read()
     tie_amd.profile_enable(False)
-    if len(prof) == 1 and next(iter(prof.values()))[1] == steps and not graph:
+    if len(prof) == 1 and next(iter(prof.values()))[1] == steps and timing == "eager":
         # a step of one kernel (the one-token block): its steady-state
         # duration is the per-launch time of the timed loop's back-to-back
         # launches, from the events inside its host-clock bracket (a
@@ -321,7 +329,7 @@ def run_config(torch, tie_amd, wl, T, k, steps, warmup, flags, cfg=None, graph=F
     return dict(T=T, k=k, ms=ms, tokens_per_s=T / (ms * 1e-3), U=U_avg, block_bytes=block_bytes,
                 block_flops=block_flops, block_GBps=block_bytes / (ms * 1e-3) / 1e9,
                 block_TFLOPs=block_flops / (ms * 1e-3) / 1e12, kernels=kernels, layers=nL, gpu_out0=gpu_out0,
-                ms_eager=ms_eager, timing="graph" if graph else "eager")
+                ms_eager=ms_eager, timing=timing)
 
 
 def workload_name(synth, name, cfg):
