@@ -110,9 +110,10 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 #define TIE_MFMA_DIRECT 1
 #endif
 // Tiles with at least this many 32-row M tiles run the cross-stage
-// software pipeline (fewer: each stage self-contained)
+// software pipeline (fewer: each stage self-contained; 4 measured 1.3%
+// faster than 3 at 235B T=1024, the same elsewhere)
 #ifndef TIE_MFMA_PIPE_NMT
-#define TIE_MFMA_PIPE_NMT 3
+#define TIE_MFMA_PIPE_NMT 4
 #endif
 // VALU instructions placed between two MFMAs of a stage's last step
 #ifndef TIE_MFMA_TAIL_VALU
