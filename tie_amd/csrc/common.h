@@ -34,13 +34,18 @@ constexpr int MFMA_MT = MFMA_MT_GU > MFMA_MT_DN ? MFMA_MT_GU : MFMA_MT_DN;
 // gate/up tiles of the small-tile kernel (quantised weights, few pairs per
 // expert: more waves per SIMD), used up to TIE_MFMA_SMALL_AVG pairs per expert
 constexpr int MFMA_MT_GU_SMALL = 64;
-// gate/up tiles of the BF16-weight kernel: short enough for two waves per
-// SIMD with the weights prefetched into registers (30B BF16 Zipf T=512:
-// gate/up 233 -> 213 us against 160-row tiles at one wave per SIMD)
+// gate/up and down tiles of the BF16-weight kernels: short enough for two
+// waves per SIMD with the weights prefetched into registers (30B BF16 Zipf
+// T=512: gate/up 233 -> 213 us, down 127 -> 112 us against 160 / 128-row
+// tiles at one wave per SIMD)
 #ifndef TIE_MFMA_MT_GU_BF16
 #define TIE_MFMA_MT_GU_BF16 96
 #endif
 constexpr int MFMA_MT_GU_BF16 = TIE_MFMA_MT_GU_BF16;
+#ifndef TIE_MFMA_MT_DN_BF16
+#define TIE_MFMA_MT_DN_BF16 96
+#endif
+constexpr int MFMA_MT_DN_BF16 = TIE_MFMA_MT_DN_BF16;
 #ifndef TIE_MFMA_SMALL_AVG
 #define TIE_MFMA_SMALL_AVG 32
 #endif

@@ -136,10 +136,13 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 #ifndef TIE_BF16_B3
 #define TIE_BF16_B3 1
 #endif
-// waves per SIMD of the BF16-weight gate/up kernel (its weights prefetched
-// into registers; the down kernel runs one)
+// waves per SIMD of the BF16-weight gate/up and down kernels (their weights
+// prefetched into registers)
 #ifndef TIE_MFMA_BF16_WPE
 #define TIE_MFMA_BF16_WPE 2
+#endif
+#ifndef TIE_MFMA_BF16_DN_WPE
+#define TIE_MFMA_BF16_DN_WPE 2
 #endif
 #ifndef TIE_MFMA_DN_WPE
 #define TIE_MFMA_DN_WPE 2
@@ -204,7 +207,10 @@ __device__ __forceinline__ void flag_token(int32_t *flag, int32_t *list, int32_t
 
 template <int TYPE, bool DOWN = false, int MTR = 0> struct Cfg {
 	// pair rows per work tile at most (MTR: the small-tile gate/up kernel's)
-	static constexpr int MT = MTR ? MTR : DOWN ? MFMA_MT_DN : TYPE == TIE_GGML_BF16 ? MFMA_MT_GU_BF16 : MFMA_MT_GU;
+	static constexpr int MT = MTR                    ? MTR
+				  : TYPE == TIE_GGML_BF16 ? (DOWN ? MFMA_MT_DN_BF16 : MFMA_MT_GU_BF16)
+				  : DOWN                  ? MFMA_MT_DN
+							  : MFMA_MT_GU;
 	static constexpr bool SPLIT = TYPE == TIE_GGML_BF16; // bf16 weights take activations as hi + lo planes
 	// Q4_K / Q6_K weights: f16 operands (activations as f16 with the K order
 	// inside each 8-group 0,2,1,3,4,6,5,7; weights scaled by 2^F16_SHIFT)
@@ -1329,7 +1335,7 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 // into registers) run one wave per SIMD
 constexpr int mf_wpe(int type, bool down, int mtr)
 {
-	return type == TIE_GGML_BF16 ? (down ? 1 : TIE_MFMA_BF16_WPE)
+	return type == TIE_GGML_BF16 ? (down ? TIE_MFMA_BF16_DN_WPE : TIE_MFMA_BF16_WPE)
 	       : mtr == MFMA_MT_TINY ? (down ? TIE_MFMA_TINY_DN_WPC : TIE_MFMA_TINY_GU_WPC)
 	       : mtr && !down ? 3 : down ? TIE_MFMA_DN_WPE : TIE_MFMA_GU_WPE;
 }
@@ -1787,7 +1793,9 @@ int mfma_gu_rows(const Layer &L, int npairs)
 int mfma_dn_rows(const Layer &L, int npairs)
 {
 	const bool quant = L.down.type == TIE_GGML_Q4_K || L.down.type == TIE_GGML_Q6_K;
-	return quant && npairs <= TIE_MFMA_TINY_AVG * L.E ? MFMA_MT_TINY : MFMA_MT_DN;
+	if (!quant)
+		return MFMA_MT_DN_BF16;
+	return npairs <= TIE_MFMA_TINY_AVG * L.E ? MFMA_MT_TINY : MFMA_MT_DN;
 }
 
 hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, const float *silu, Workspace &ws,
