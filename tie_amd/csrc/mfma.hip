@@ -243,7 +243,9 @@ template <int TYPE, bool DOWN = false, int MTR = 0> struct Cfg {
 	// workgroups per CU: the tiny-tile kernels TIE_MFMA_TINY_GU_WPC /
 	// _DN_WPC, the small-tile gate/up kernels 3, the others 2
 	static constexpr int WG_PER_CU = MTR == MFMA_MT_TINY ? (DOWN ? TIE_MFMA_TINY_DN_WPC : TIE_MFMA_TINY_GU_WPC)
-					 : MTR && !DOWN ? 3 : 2;
+					 : MTR && !DOWN ? 3
+					 : DOWN         ? TIE_MFMA_DN_WPE
+							: TIE_MFMA_GU_WPE;
 	static constexpr int LDS_BUDGET = (160 * 1024) / WG_PER_CU;
 	static constexpr int ROFF_BYTES = 4 * RPI * NWAVES * 16 + 4 * MT; // row offsets + pair ids
 	// stage buffers (activations and weights; NS - 1 stages in flight): as
