@@ -518,6 +518,8 @@ __device__ __forceinline__ void group_factors16(const BRegs<TYPE> &b, int st, in
 #pragma unroll
 	for (int j = 0; j < 2; j++) {
 		const int g = (4 / Cfg<TYPE, false, MTR>::SPB) * (st % Cfg<TYPE, false, MTR>::SPB) + gi;
+		// (component x: this clang's __builtin_bit_cast of any other vector
+		// component reads component x -- copy such a one to a scalar first)
 		const f16x2 dd = __builtin_bit_cast(f16x2, b.sc[j].x);
 #pragma unroll
 		for (int u = 0; u < 2; u++) {
