@@ -111,7 +111,8 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 #endif
 // Tiles with at least this many 32-row M tiles run the cross-stage
 // software pipeline (fewer: each stage self-contained; 4 measured 1.3%
-// faster than 3 at 235B T=1024, the same elsewhere)
+// faster than 3 at 235B T=1024, the same elsewhere; 1 and 2 slower at
+// decode-sized batches: 30B T=32 +3.4% / +0.3%, LFM2 T=32 +8.6% / +2.3%)
 #ifndef TIE_MFMA_PIPE_NMT
 #define TIE_MFMA_PIPE_NMT 4
 #endif
