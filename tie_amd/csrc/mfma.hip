@@ -113,6 +113,12 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // software pipeline (fewer: each stage self-contained; 4 measured 1.3%
 // faster than 3 at 235B T=1024, the same elsewhere; 1 and 2 slower at
 // decode-sized batches: 30B T=32 +3.4% / +0.3%, LFM2 T=32 +8.6% / +2.3%)
+// Q4_K on the f16 matrix cores, 64-K stages: lane half h takes sub-block h
+// of the stage's group (nibble h of all 32 code bytes), so a lane needs the
+// scale factors of one sub-block, not two (0: both halves take both)
+#ifndef TIE_MFMA_UH
+#define TIE_MFMA_UH 1
+#endif
 #ifndef TIE_MFMA_PIPE_NMT
 #define TIE_MFMA_PIPE_NMT 4
 #endif
@@ -222,6 +228,9 @@ template <int TYPE, bool DOWN = false, int MTR = 0> struct Cfg {
 				       : TYPE == TIE_GGML_Q6_K ? TIE_Q6K_KST : 128);
 	// Q6_K 64-K stages hold quarters p and p + 2 of a block half
 	static constexpr bool APERM = TYPE == TIE_GGML_Q6_K && KST == 64;
+	// Q4_K f16, 64-K stages: K step s, lane half h is sub-block h, positions
+	// 8s .. 8s + 7 (TIE_MFMA_UH)
+	static constexpr bool UH = TIE_MFMA_UH && TYPE == TIE_GGML_Q4_K && F16 && KST == 64;
 	static constexpr int SPB = QK / KST;                 // stages per 256-weight block (quantised)
 	static constexpr int NPL = SPLIT ? 2 : 1;            // activation planes
 	static constexpr int RB = KST * 2;                   // bytes per A row, plane and stage
@@ -402,7 +411,12 @@ __device__ __forceinline__ void lds_b(const uint8_t *B, const int p[2], const in
 #pragma unroll
 	for (int j = 0; j < 2; j++) {
 		const uint8_t *pb = B + p[j] * C::PB + i[j] * 16;
-		if constexpr (TYPE == TIE_GGML_Q4_K) {
+		if constexpr (TYPE == TIE_GGML_Q4_K && C::UH) {
+			// both code chunks of the stage's group (the lane half takes its nibble)
+			b.q[j][0] = *reinterpret_cast<const u32x4 *>(pb + 1024);
+			b.q[j][1] = *reinterpret_cast<const u32x4 *>(pb + 2 * 1024);
+			b.sc[j] = *reinterpret_cast<const u32x4 *>(pb);
+		} else if constexpr (TYPE == TIE_GGML_Q4_K) {
 #pragma unroll
 			for (int g = 0; g < (C::NCH - 1) / 2; g++)
 				b.q[j][g] = *reinterpret_cast<const u32x4 *>(pb + (1 + 2 * g + h) * 1024);
@@ -516,6 +530,22 @@ __device__ __forceinline__ void group_factors16(const BRegs<TYPE> &b, int st, in
 	const f16x2 sn0 = {(_Float16)1.0f, (_Float16)(-1024.0f)};
 	const f16x2 sn1 = {(_Float16)(1.0f / 16), (_Float16)(-64.0f)};
 	const f16x2 sdm = {(_Float16)(float)(1 << F16_SHIFT), (_Float16)(-(float)(1 << F16_SHIFT))};
+	if constexpr (Cfg<TYPE, false, MTR>::UH) {
+		// the lane half's sub-block 2g + h only, into [j][0]
+		const int h = lane_half();
+		const f16x2 sn = h ? sn1 : sn0;
+		const int g = st % Cfg<TYPE, false, MTR>::SPB;
+#pragma unroll
+		for (int j = 0; j < 2; j++) {
+			const f16x2 dd = __builtin_bit_cast(f16x2, b.sc[j].x);
+			uint32_t sc, mn;
+			q4k_scale_min(b.sc[j], 2 * g + h, sc, mn);
+			const f16x2 sm = __builtin_bit_cast(f16x2, (sc | (mn << 16)) | 0x64006400u) - k1024;
+			f.SN[j][0] = f16x2{sm[0], sm[0]} * sn;
+			f.DM[j][0] = f16x2{(_Float16)1.0f, sm[1]} * dd * sdm;
+		}
+		return;
+	}
 #pragma unroll
 	for (int j = 0; j < 2; j++) {
 		const int g = (4 / Cfg<TYPE, false, MTR>::SPB) * (st % Cfg<TYPE, false, MTR>::SPB) + gi;
@@ -535,19 +565,41 @@ __device__ __forceinline__ void group_factors16(const BRegs<TYPE> &b, int st, in
 // The masks and the magic live in VGPRs (K16): a GFX9 VOP3 instruction takes
 // no literal, so only then is each pair one v_and_or_b32.
 struct K16 {
-	uint32_t lo, hi, magic, q6;
+	uint32_t lo, hi, magic, q6, uh; // uh: the lane half's nibble mask (lo or hi)
 };
 
 __device__ __forceinline__ K16 k16_consts()
 {
-	K16 k = {0x000f000fu, 0x00f000f0u, 0x64006400u, 0x003f003fu};
-	asm volatile("" : "+v"(k.lo), "+v"(k.hi), "+v"(k.magic), "+v"(k.q6));
+	K16 k = {0x000f000fu, 0x00f000f0u, 0x64006400u, 0x003f003fu, lane_half() ? 0x00f000f0u : 0x000f000fu};
+	asm volatile("" : "+v"(k.lo), "+v"(k.hi), "+v"(k.magic), "+v"(k.q6), "+v"(k.uh));
 	return k;
 }
 
+template <bool UH>
 __device__ __forceinline__ void deq_step16(const BRegs<TIE_GGML_Q4_K> &b, const Fac16 &f, const K16 &kc, int s,
 					   f16x8 out[2])
 {
+	if constexpr (UH) {
+		// step s: code bytes 8s .. 8s + 7 of the group (chunk s/2), the lane
+		// half's nibble, its sub-block's factors
+#pragma unroll
+		for (int j = 0; j < 2; j++) {
+			const u32x4 q4 = b.q[j][s >> 1];
+			const u32x2 q = (s & 1) ? u32x2{q4.z, q4.w} : u32x2{q4.x, q4.y};
+			const uint32_t w[4] = {q.x, q.x >> 8, q.y, q.y >> 8};
+			const f16x2 sn = f.SN[j][0], dm = f.DM[j][0];
+			f16x2 r[4];
+#pragma unroll
+			for (int i = 0; i < 4; i++) {
+				// v = 1024 + q (low nibbles) or 1024 + 16 q (high); q sc exact
+				const f16x2 v = __builtin_bit_cast(f16x2, (w[i] & kc.uh) | kc.magic);
+				const f16x2 qs = __builtin_elementwise_fma(v, f16x2{sn[0], sn[0]}, f16x2{sn[1], sn[1]});
+				r[i] = __builtin_elementwise_fma(qs, f16x2{dm[0], dm[0]}, f16x2{dm[1], dm[1]});
+			}
+			out[j] = f16x8{r[0][0], r[0][1], r[1][0], r[1][1], r[2][0], r[2][1], r[3][0], r[3][1]};
+		}
+		return;
+	}
 #pragma unroll
 	for (int j = 0; j < 2; j++) {
 		// step s of the stage: 64-weight group gi = s / 4 (stages of 128 K
@@ -796,7 +848,7 @@ template <int TYPE, bool DOWN, int MTR> struct Ops<TYPE, DOWN, MTR, true> {
 		return;
 #endif
 		if constexpr (TYPE == TIE_GGML_Q4_K)
-			deq_step16(b, f, kc, s, out);
+			deq_step16<Cfg<TYPE, DOWN, MTR>::UH>(b, f, kc, s, out);
 		else
 			deq_step16_q6k(b, f, kc, st, s, out);
 	}
@@ -881,7 +933,10 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 		// swapped (lane half h takes code chunk h, a step half of it).
 		// APERM: slots 0..3 are K 32p + ... of the half, slots 4..7 K 64 + 32p + ...
 		const int q8 = C::SPLIT ? chunk & 3 : ((chunk & 1) << 1) | ((chunk >> 1) & 1);
-		const int cofs = C::APERM ? 128 * (chunk >> 2) + 16 * q8 : 64 * (chunk >> 2) + 16 * q8;
+		// UH: slot 2s + h holds the 8-group 4h + s (sub-block h, positions 8s ..)
+		const int cofs = C::UH      ? 16 * (4 * (chunk & 1) + (chunk >> 1))
+				 : C::APERM ? 128 * (chunk >> 2) + 16 * q8
+					    : 64 * (chunk >> 2) + 16 * q8;
 		as.base[0] = (const char *)a.a16;
 		as.base[1] = (const char *)a.a16lo;
 		as.cofs = cofs;
