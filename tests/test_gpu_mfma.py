@@ -97,10 +97,12 @@ def q4k_f16(buf):
     return W.astype(np.float32).reshape(-1) / 256
 
 
-def q6k_f16(buf):
+def q6k_f16(buf, dfold=False):
     """Q6_K weights as the f16 kernels form them, divided by their factor 256:
     (code - 32)*sc in f16 (exact for |sc| <= 64, as in these blocks), times
-    d*256 (exact), rounded once to f16 (v_pk_mul_f16).  Super-block layout (TIE's
+    d*256 (exact), rounded once to f16 (v_pk_mul_f16); with dfold (the 32-row
+    tile kernels, which apply d*256 per 256-K block to an fp32 block sum) not
+    rounded.  Super-block layout (TIE's
     block_q6_K): ql[128], qh[64], int8 scales[16], d (f16); half n, l < 32:
     weights 128n + l + 32i take ql nibble (ql[64n + l + 32(i%2)], low for
     i < 2), qh bits 2i of qh[32n + l], scale 8n + l//16 + 2i."""
@@ -119,22 +121,26 @@ def q6k_f16(buf):
             q[:, 128 * n + 32 * i + l] = nib | (((qh[:, 32 * n + l] >> (2 * i)) & 3) << 4)
             s[:, 128 * n + 32 * i + l] = sc[:, 8 * n + l // 16 + 2 * i]
     qs = f16((q - 32).astype(np.float32) * s).astype(np.float64)  # (code - 32) sc: exact when |sc| <= 64
-    W = (qs * (d[:, None].astype(np.float64) * 256)).astype(np.float16)  # one rounding
-    return W.astype(np.float32).reshape(-1) / 256
+    W = qs * (d[:, None].astype(np.float64) * 256)
+    if not dfold:
+        W = W.astype(np.float16).astype(np.float32)  # one rounding
+    return W.reshape(-1) / 256
 
 
 QUANT = (synth.Q4_K, synth.Q6_K)
+TINY_AVG = 8  # pairs per expert on average up to which the kernels take 32-row tiles
 
 
-def expert_weights(buf, wtype, e, rows, inn, f16_ops):
-    """Expert e's [rows][inn] weights as the kernels' operands."""
+def expert_weights(buf, wtype, e, rows, inn, f16_ops, dfold=False):
+    """Expert e's [rows][inn] weights as the kernels' operands (dfold: the
+    32-row tile kernels' Q6_K form, q6k_f16)."""
     nbytes = rows * synth.row_bytes(wtype, inn)
     raw = np.ascontiguousarray(np.frombuffer(np.ascontiguousarray(buf).tobytes(), np.uint8,
                                              count=nbytes, offset=e * nbytes))
     if wtype == synth.BF16:
         return synth.bf16_bits_to_f32(raw.view(np.uint16)).reshape(rows, inn)
     if f16_ops:
-        return (q4k_f16(raw) if wtype == synth.Q4_K else q6k_f16(raw)).reshape(rows, inn)
+        return (q4k_f16(raw) if wtype == synth.Q4_K else q6k_f16(raw, dfold)).reshape(rows, inn)
     out = np.empty(rows * inn, np.float32)
     fn = bind.oracle().orc_dequant_q4k if wtype == synth.Q4_K else bind.oracle().orc_dequant_q6k
     fn(raw.ctypes.data, rows * inn, out.ctypes.data)
@@ -154,11 +160,14 @@ def model(layer, x, idx, w, tab):
     else:
         xa = bf16(x).astype(np.float64)
     out = np.zeros(x.shape, np.float64)
+    # 32-row tiles (at most TINY_AVG pairs per expert on average) for both
+    # quantised kernels
+    tiny = idx.size <= TINY_AVG * layer.E
     for e in np.unique(idx[idx >= 0]):
         t, j = np.nonzero(idx == e)
-        Wg = expert_weights(layer.gate, layer.gate_type, e, F, d, True)
-        Wu = expert_weights(layer.up, layer.up_type, e, F, d, True)
-        Wd = expert_weights(layer.down, layer.down_type, e, d, F, h16)
+        Wg = expert_weights(layer.gate, layer.gate_type, e, F, d, True, tiny)
+        Wu = expert_weights(layer.up, layer.up_type, e, F, d, True, tiny)
+        Wd = expert_weights(layer.down, layer.down_type, e, d, F, h16, tiny)
         X = xa[t]
         g = np.ascontiguousarray((X @ Wg.T.astype(np.float64)).astype(np.float32))
         u = np.ascontiguousarray((X @ Wu.T.astype(np.float64)).astype(np.float32))

@@ -119,6 +119,11 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 #ifndef TIE_MFMA_UH
 #define TIE_MFMA_UH 1
 #endif
+// Q6_K 32-row tiles: the block's d applied once per 256-K block to a
+// block accumulator (fp32) instead of to every dequantised weight (f16)
+#ifndef TIE_MFMA_DFOLD
+#define TIE_MFMA_DFOLD 1
+#endif
 #ifndef TIE_MFMA_PIPE_NMT
 #define TIE_MFMA_PIPE_NMT 4
 #endif
@@ -662,6 +667,7 @@ __device__ __forceinline__ void deq_step(const BRegs<TYPE> &b, const Fac &f, int
 // lo, hi, as in deq_step) -> f16 pairs (K 0,2), (1,3), (4,6), (5,7): a code
 // in the mantissa of 1024.0, minus 1056 = code - 32 (exact), times
 // d * sc * 2^F16_SHIFT (v_pk_mul_f16, one rounding).
+template <bool NOD = false> // NOD: without the factor d 2^S ((q - 32) sc, exact)
 __device__ __forceinline__ void deq_step16_q6k(const BRegs<TIE_GGML_Q6_K> &b, const Fac &f, const K16 &kc, int st, int s,
 					       f16x8 out[2])
 {
@@ -689,8 +695,11 @@ __device__ __forceinline__ void deq_step16_q6k(const BRegs<TIE_GGML_Q6_K> &b, co
 		const uint32_t w[4] = {lo, lo >> 8, hi, hi >> 8};
 		f16x2 q[4];
 #pragma unroll
-		for (int i = 0; i < 4; i++)
-			q[i] = ((__builtin_bit_cast(f16x2, (w[i] & kc.q6) | kc.magic) - k1056) * SC) * D;
+		for (int i = 0; i < 4; i++) {
+			q[i] = (__builtin_bit_cast(f16x2, (w[i] & kc.q6) | kc.magic) - k1056) * SC;
+			if constexpr (!NOD)
+				q[i] = q[i] * D;
+		}
 		out[j] = f16x8{q[0][0], q[0][1], q[1][0], q[1][1], q[2][0], q[2][1], q[3][0], q[3][1]};
 	}
 }
@@ -828,6 +837,7 @@ template <int TYPE, bool DOWN, int MTR> struct Ops<TYPE, DOWN, MTR, true> {
 		else
 			group_factors<TYPE, MTR>(b, st, gi, f);
 	}
+	template <bool NOD = false>
 	__device__ static void deq(const BRegs<TYPE> &b, const F &f, const K16 &kc, int st, int s, V out[2])
 	{
 #if defined(TIE_DIAG_NODEQ)
@@ -850,7 +860,7 @@ template <int TYPE, bool DOWN, int MTR> struct Ops<TYPE, DOWN, MTR, true> {
 		if constexpr (TYPE == TIE_GGML_Q4_K)
 			deq_step16<Cfg<TYPE, DOWN, MTR>::UH>(b, f, kc, s, out);
 		else
-			deq_step16_q6k(b, f, kc, st, s, out);
+			deq_step16_q6k<NOD>(b, f, kc, st, s, out);
 	}
 	__device__ static f32x16 mma(V a, V b, f32x16 c)
 	{
@@ -1043,11 +1053,13 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 			for (int i = 0; i < NA; i++)
 				fr[i] = *reinterpret_cast<const V *>(A + i * 32 * C::RB);
 		};
+		// Q6_K one-M-tile tiles: d applied per block (DF)
+		constexpr bool DF = TIE_MFMA_DFOLD && TYPE == TIE_GGML_Q6_K && NMT == 1 && MTR == MFMA_MT_TINY;
 		auto prep = [&](int st, int s, int slot) {
 			read(st, s, fa[slot]);
 			if (s == 0 || (TYPE == TIE_GGML_Q4_K && s % 4 == 0))
 				O::factors(b, st, s / 4, f);
-			O::deq(b, f, kc, st, s, fb[slot]);
+			O::template deq<DF>(b, f, kc, st, s, fb[slot]);
 		};
 		auto mm = [&](int slot) {
 #pragma unroll
@@ -1075,7 +1087,41 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 		for (int i = 0; i + 1 < NS; i++)
 			issue(i);
 		barrier_after(-1);
-		if constexpr (NMT < TIE_MFMA_PIPE_NMT) {
+		if constexpr (DF) {
+			// as below, block by block: the block's MFMAs into accb (from
+			// zero), then acc += d 2^S accb per lane column (fp32)
+			static_assert(C::SPB * C::KST == QK, "stages per block");
+			f32x16 accb[2];
+			for (int st0 = 0; st0 < nk; st0 += C::SPB) {
+#pragma unroll
+				for (int sb = 0; sb < C::SPB; sb++) {
+					const int st = st0 + sb;
+					issue(st + NS - 1);
+					lds_b<TYPE, MTR>(bbuf(st), bp, bi, st, h, b);
+					prep(st, 0, 0);
+#pragma unroll
+					for (int s = 0; s < C::NSTEP; s++) {
+#pragma unroll
+						for (int j = 0; j < 2; j++)
+							accb[j] = O::mma(fa[s & 1][0], fb[s & 1][j],
+									 (sb == 0 && s == 0) ? f32x16{} : accb[j]);
+						if (s + 1 < C::NSTEP)
+							prep(st, s + 1, (s & 1) ^ 1);
+						__builtin_amdgcn_sched_barrier(0);
+					}
+					if (sb + 1 == C::SPB) {
+#pragma unroll
+						for (int j = 0; j < 2; j++) {
+							const float D = f.d6[j] * (float)(1 << F16_SHIFT);
+#pragma unroll
+							for (int i = 0; i < 16; i++)
+								acc[0][j][i] = __builtin_fmaf(D, accb[j][i], acc[0][j][i]);
+						}
+					}
+					barrier_after(st);
+				}
+			}
+		} else if constexpr (NMT < TIE_MFMA_PIPE_NMT) {
 			// few MFMAs per step: each stage self-contained (the DMA of stage
 			// st + NS - 1 first, then its weights from LDS, then the steps)
 			for (int st = 0; st < nk; st++) {
