@@ -124,6 +124,10 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 #ifndef TIE_MFMA_DFOLD
 #define TIE_MFMA_DFOLD 1
 #endif
+// activation rows past the tile's own not moved into LDS
+#ifndef TIE_MFMA_ASKIP
+#define TIE_MFMA_ASKIP 1
+#endif
 #ifndef TIE_MFMA_PIPE_NMT
 #define TIE_MFMA_PIPE_NMT 4
 #endif
@@ -722,6 +726,7 @@ struct ASrc {
 	const char *base[2];   // planes (wave-uniform)
 	uint32_t cofs;         // this lane's chunk offset in a row
 	const uint32_t *roff;  // LDS: this lane's ROFF_STRIDE row byte offsets
+	int nrows;             // the tile's rows (wave-uniform)
 };
 
 // The LDS offset of a generic pointer into LDS: a flat LDS address is the
@@ -771,6 +776,12 @@ __device__ __forceinline__ void dma_a(const ASrc &s, int st, int w, const uint8_
 #pragma unroll
 		for (int c = 0; c < NLIVE; c++) {
 			const int r0 = C::RPI * (NWAVES * c + w);
+			// rows past the tile's are not moved (their fragments feed only
+			// output rows that are never stored); with two stage buffers every
+			// stage barrier waits for all loads, so the skipped ones change no
+			// wait count
+			if (TIE_MFMA_ASKIP && C::NS == 2 && r0 >= s.nrows)
+				continue;
 			const uint32_t dst = lds_addr(buf + pl * C::A_TILE + r0 * C::RB);
 			dma16s(s.base[pl], off[c] + lk, __builtin_amdgcn_readfirstlane(dst));
 		}
@@ -952,6 +963,7 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 		as.cofs = cofs;
 		// row r = RPI (NWAVES c + w') + rsub' is entry c of lane slot RPI w' + rsub'
 		as.roff = roff + (C::RPI * w + rsub) * ROFF_STRIDE;
+		as.nrows = nrows;
 		if (t < C::MT) {
 			const int r = t < nrows ? t : 0;
 			const int pr = DOWN ? 0 : spair[r];
