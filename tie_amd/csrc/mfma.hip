@@ -128,6 +128,10 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 #ifndef TIE_MFMA_ASKIP
 #define TIE_MFMA_ASKIP 1
 #endif
+// epilogue halves (16 rows) past the tile's rows skipped
+#ifndef TIE_MFMA_EPI_SKIP
+#define TIE_MFMA_EPI_SKIP 1
+#endif
 #ifndef TIE_MFMA_PIPE_NMT
 #define TIE_MFMA_PIPE_NMT 4
 #endif
@@ -1280,6 +1284,12 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 		for (int mt = 0; mt < NMT; mt++) {
 #pragma unroll
 			for (int half = 0; half < 2; half++) {
+				// (a half without rows of the tile has nothing to store; the
+				// 32- and 64-row tile kernels: 30B T=32 -1.3%, T=22 -2.2%,
+				// LFM2 T=32 -1.4%; the large tiles, mostly full, measured
+				// no gain)
+				if (TIE_MFMA_EPI_SKIP && MTR != 0 && 32 * mt + 16 * half >= nrows)
+					continue;
 				if constexpr (DOWN) {
 #pragma unroll
 					for (int ii = 0; ii < 8; ii++) {
