@@ -67,11 +67,13 @@ def sig11(a):
     return np.ldexp(np.round(m * 2048.0) / 2048.0, e)
 
 
-def q4k_f16(buf):
+def q4k_f16(buf, fold=False):
     """Q4_K weights as the f16 kernels form them, divided by their factor
     256: per sub-block M = -dmin*m*256 rounded to f16, then (code*sc)*(d*256)
     + M16 rounded once to f16 (code*sc and d*256 exact in f16;
-    v_pk_fma_f16).
+    v_pk_fma_f16); with fold (the 32-row gate/up tile kernels: MFMAs on
+    code*sc, d*256 applied per block in fp32, M16 times the activations'
+    sub-block sums) not rounded.
     Super-block layout (TIE's block_q4_K): d, dmin (f16), 12 scale bytes,
     128 code bytes; sub-block 2g holds the low and 2g+1 the high nibbles of
     code bytes 32g..32g+31."""
@@ -93,8 +95,10 @@ def q4k_f16(buf):
     M16 = f16(M * 256).astype(np.float64)
     qs = b[:, 16:].reshape(nb, 4, 32)
     q = np.stack([qs & 15, qs >> 4], axis=2).reshape(nb, 8, 32).astype(np.float64)
-    W = (q * D16[:, :, None] + M16[:, :, None]).astype(np.float16)  # exact in float64, one rounding
-    return W.astype(np.float32).reshape(-1) / 256
+    W = q * D16[:, :, None] + M16[:, :, None]  # exact in float64
+    if not fold:
+        W = W.astype(np.float16).astype(np.float32)  # one rounding
+    return W.reshape(-1) / 256
 
 
 def q6k_f16(buf, dfold=False):
@@ -131,16 +135,17 @@ QUANT = (synth.Q4_K, synth.Q6_K)
 TINY_AVG = 8  # pairs per expert on average up to which the kernels take 32-row tiles
 
 
-def expert_weights(buf, wtype, e, rows, inn, f16_ops, dfold=False):
+def expert_weights(buf, wtype, e, rows, inn, f16_ops, dfold=False, qfold=False):
     """Expert e's [rows][inn] weights as the kernels' operands (dfold: the
-    32-row tile kernels' Q6_K form, q6k_f16)."""
+    32-row tile kernels' Q6_K form, q6k_f16; qfold: their Q4_K gate/up form,
+    q4k_f16)."""
     nbytes = rows * synth.row_bytes(wtype, inn)
     raw = np.ascontiguousarray(np.frombuffer(np.ascontiguousarray(buf).tobytes(), np.uint8,
                                              count=nbytes, offset=e * nbytes))
     if wtype == synth.BF16:
         return synth.bf16_bits_to_f32(raw.view(np.uint16)).reshape(rows, inn)
     if f16_ops:
-        return (q4k_f16(raw) if wtype == synth.Q4_K else q6k_f16(raw, dfold)).reshape(rows, inn)
+        return (q4k_f16(raw, qfold) if wtype == synth.Q4_K else q6k_f16(raw, dfold)).reshape(rows, inn)
     out = np.empty(rows * inn, np.float32)
     fn = bind.oracle().orc_dequant_q4k if wtype == synth.Q4_K else bind.oracle().orc_dequant_q6k
     fn(raw.ctypes.data, rows * inn, out.ctypes.data)
@@ -165,8 +170,8 @@ def model(layer, x, idx, w, tab):
     tiny = idx.size <= TINY_AVG * layer.E
     for e in np.unique(idx[idx >= 0]):
         t, j = np.nonzero(idx == e)
-        Wg = expert_weights(layer.gate, layer.gate_type, e, F, d, True, tiny)
-        Wu = expert_weights(layer.up, layer.up_type, e, F, d, True, tiny)
+        Wg = expert_weights(layer.gate, layer.gate_type, e, F, d, True, tiny, tiny)
+        Wu = expert_weights(layer.up, layer.up_type, e, F, d, True, tiny, tiny)
         Wd = expert_weights(layer.down, layer.down_type, e, d, F, h16, tiny)
         X = xa[t]
         g = np.ascontiguousarray((X @ Wg.T.astype(np.float64)).astype(np.float32))

@@ -246,6 +246,7 @@ static size_t carve_workspace(uint8_t *b, size_t P, size_t FF, size_t DD, size_t
 		     o_hlo = take(P * FF * 2), o_xlo = take(Tcap * DD * 2), o_nm = take(Tcap * DD * 4);
 	const size_t o_bc = take(EE * 4), o_mk = take(EE * (size_t)T4((int)Tcap)), o_bk = take(EE * T4((int)Tcap) * 4);
 	const size_t o_fl = take(Tcap * 4), o_fx = take(Tcap * 4), o_fc = take(4);
+	const size_t o_xs = take(Tcap * 2 * (DD / 32 + 1) * 2);
 	// h by expert for decode-sized matrix-core batches (not in the
 	// no-allocation entry point's scratch: that path groups h by position)
 	const size_t o_hd = direct_h ? take(EE * MFMA_DIRECT_T * FF * 2) : 0;
@@ -267,6 +268,7 @@ static size_t carve_workspace(uint8_t *b, size_t P, size_t FF, size_t DD, size_t
 	w->xb = (uint16_t *)(b + o_xb);
 	w->hlo = (uint16_t *)(b + o_hlo);
 	w->xlo = (uint16_t *)(b + o_xlo);
+	w->xsum = (uint16_t *)(b + o_xs);
 	w->bucket_cnt = (int32_t *)(b + o_bc);
 	w->sel = b + o_mk;
 	w->bucket = (int32_t *)(b + o_bk);

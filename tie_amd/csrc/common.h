@@ -119,6 +119,8 @@ struct Workspace {
 	uint16_t *hlo = nullptr;      // [T*k][F] SwiGLU activations, bf16 remainder (MFMA path, BF16 weights)
 	uint16_t *xb = nullptr;       // [T][d]   x as bf16 (MFMA path)
 	uint16_t *xlo = nullptr;      // [T][d]   x - bf16(x) as bf16 (MFMA path, BF16 weights)
+	uint16_t *xsum = nullptr;     // [T][2][d/32] sums of f16(x) over each 32-K sub-block as f16 high and
+	                              //          remainder parts (MFMA path, Q4_K 32-row gate/up tiles)
 	int32_t *bucket_cnt = nullptr; // [E]   MFMA path: pairs per expert
 	uint8_t *sel = nullptr;       // [E][T4(T)] MFMA path: slot + 1 that chose the expert (0: none)
 	int32_t *bucket = nullptr;    // [E][T4(T)] MFMA path: each expert's pair ids in token order

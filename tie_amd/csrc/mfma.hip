@@ -132,6 +132,14 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 #ifndef TIE_MFMA_EPI_SKIP
 #define TIE_MFMA_EPI_SKIP 1
 #endif
+// Q4_K 32-row gate/up tiles (with TIE_MFMA_UH): the MFMAs take q sc
+// (exact), d is applied per 256-K block to an fp32 block sum, and the
+// minimum term by one MFMA per block over the routing's sub-block sums of
+// the activations (Workspace::xsum), in place of the second packed FMA
+// per weight pair
+#ifndef TIE_MFMA_QFOLD
+#define TIE_MFMA_QFOLD 1
+#endif
 #ifndef TIE_MFMA_PIPE_NMT
 #define TIE_MFMA_PIPE_NMT 4
 #endif
@@ -215,6 +223,8 @@ struct MfmaArgs {
 	int32_t *tok_flag;       // [T] gate/up, h_f16: tokens whose h left the f16 range
 	int32_t *fix_list;       //     are appended here (once each) ...
 	int32_t *fix_count;      //     ... and counted
+	const uint16_t *xsum;    // Q4_K 32-row gate/up tiles (QF): [T][2][in/32] sub-block sums of A, f16 high and
+	                         // remainder parts
 };
 
 // Token t's activations do not fit the f16 operands: list it (once) for
@@ -588,7 +598,30 @@ __device__ __forceinline__ K16 k16_consts()
 	return k;
 }
 
-template <bool UH>
+// The minimum term's factors of one weight row's block (its scale chunk
+// c0): f16 -dmin m_sb 2^S for sub-blocks sb = 0..7 (element sb), each rounded
+// once (m_sb dmin 2^S; dmin 2^S exact)
+__device__ __forceinline__ f16x8 q4k_mins16(const u32x4 &c0)
+{
+	const uint32_t x = c0.x, z = c0.z, w = c0.w;
+	const f16x2 dd = __builtin_bit_cast(f16x2, x);
+	const _Float16 nd = dd[1] * (_Float16)(-(float)(1 << F16_SHIFT));
+	const f16x2 ndm = {nd, nd};
+	const f16x2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+	// m_0..3: bits 0-5 of the bytes of z; m_4..7: the high nibbles of w's
+	// bytes and bits 6-7 of z's
+	const uint32_t m03 = z & 0x3f3f3f3fu;
+	const uint32_t m47 = ((w >> 4) & 0x0f0f0f0fu) | ((z >> 2) & 0x30303030u);
+	const uint32_t pr[4] = {__builtin_amdgcn_perm(0u, m03, 0x0c010c00u), __builtin_amdgcn_perm(0u, m03, 0x0c030c02u),
+				__builtin_amdgcn_perm(0u, m47, 0x0c010c00u), __builtin_amdgcn_perm(0u, m47, 0x0c030c02u)};
+	f16x2 m[4];
+#pragma unroll
+	for (int i = 0; i < 4; i++)
+		m[i] = (__builtin_bit_cast(f16x2, pr[i] | 0x64006400u) - k1024) * ndm;
+	return f16x8{m[0][0], m[0][1], m[1][0], m[1][1], m[2][0], m[2][1], m[3][0], m[3][1]};
+}
+
+template <bool UH, bool QS = false> // QS: q sc only (exact), without d and M
 __device__ __forceinline__ void deq_step16(const BRegs<TIE_GGML_Q4_K> &b, const Fac16 &f, const K16 &kc, int s,
 					   f16x8 out[2])
 {
@@ -607,7 +640,10 @@ __device__ __forceinline__ void deq_step16(const BRegs<TIE_GGML_Q4_K> &b, const 
 				// v = 1024 + q (low nibbles) or 1024 + 16 q (high); q sc exact
 				const f16x2 v = __builtin_bit_cast(f16x2, (w[i] & kc.uh) | kc.magic);
 				const f16x2 qs = __builtin_elementwise_fma(v, f16x2{sn[0], sn[0]}, f16x2{sn[1], sn[1]});
-				r[i] = __builtin_elementwise_fma(qs, f16x2{dm[0], dm[0]}, f16x2{dm[1], dm[1]});
+				if constexpr (QS)
+					r[i] = qs;
+				else
+					r[i] = __builtin_elementwise_fma(qs, f16x2{dm[0], dm[0]}, f16x2{dm[1], dm[1]});
 			}
 			out[j] = f16x8{r[0][0], r[0][1], r[1][0], r[1][1], r[2][0], r[2][1], r[3][0], r[3][1]};
 		}
@@ -873,7 +909,7 @@ template <int TYPE, bool DOWN, int MTR> struct Ops<TYPE, DOWN, MTR, true> {
 		return;
 #endif
 		if constexpr (TYPE == TIE_GGML_Q4_K)
-			deq_step16<Cfg<TYPE, DOWN, MTR>::UH>(b, f, kc, s, out);
+			deq_step16<Cfg<TYPE, DOWN, MTR>::UH, NOD>(b, f, kc, s, out);
 		else
 			deq_step16_q6k<NOD>(b, f, kc, st, s, out);
 	}
@@ -1069,13 +1105,15 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 			for (int i = 0; i < NA; i++)
 				fr[i] = *reinterpret_cast<const V *>(A + i * 32 * C::RB);
 		};
-		// Q6_K one-M-tile tiles: d applied per block (DF)
+		// one-M-tile tiles: d applied per block (Q6_K: DF; Q4_K gate/up: QF,
+		// with the minimum term from the sub-block sums)
 		constexpr bool DF = TIE_MFMA_DFOLD && TYPE == TIE_GGML_Q6_K && NMT == 1 && MTR == MFMA_MT_TINY;
+		constexpr bool QF = TIE_MFMA_QFOLD && C::UH && !DOWN && NMT == 1 && MTR == MFMA_MT_TINY;
 		auto prep = [&](int st, int s, int slot) {
 			read(st, s, fa[slot]);
 			if (s == 0 || (TYPE == TIE_GGML_Q4_K && s % 4 == 0))
 				O::factors(b, st, s / 4, f);
-			O::template deq<DF>(b, f, kc, st, s, fb[slot]);
+			O::template deq<DF || QF>(b, f, kc, st, s, fb[slot]);
 		};
 		auto mm = [&](int slot) {
 #pragma unroll
@@ -1103,11 +1141,22 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 		for (int i = 0; i + 1 < NS; i++)
 			issue(i);
 		barrier_after(-1);
-		if constexpr (DF) {
+		if constexpr (DF || QF) {
 			// as below, block by block: the block's MFMAs into accb (from
-			// zero), then acc += d 2^S accb per lane column (fp32)
+			// zero), then acc += d 2^S accb per lane column (fp32).  QF: and
+			// acc += S M, the block's 8 sub-block sums of the row's A (high
+			// parts in lane half 0, remainders in half 1) times the column's
+			// 8 minimum factors (in both halves)
 			static_assert(C::SPB * C::KST == QK, "stages per block");
 			f32x16 accb[2];
+			const uint16_t *xs = nullptr;
+			V sa;
+			if constexpr (QF) {
+				const int r = lane & 31;
+				const int tok = spair[r < nrows ? r : 0] / a.k;
+				xs = a.xsum + (size_t)(2 * tok + h) * (a.in / 32);
+				sa = *reinterpret_cast<const V *>(xs);
+			}
 			for (int st0 = 0; st0 < nk; st0 += C::SPB) {
 #pragma unroll
 				for (int sb = 0; sb < C::SPB; sb++) {
@@ -1128,10 +1177,20 @@ __device__ __forceinline__ void run_tile(const MfmaArgs &a, uint8_t *As, uint32_
 					if (sb + 1 == C::SPB) {
 #pragma unroll
 						for (int j = 0; j < 2; j++) {
-							const float D = f.d6[j] * (float)(1 << F16_SHIFT);
+							float D;
+							if constexpr (QF)
+								D = (float)f.DM[j][0][0]; // d 2^S (exact in f16)
+							else
+								D = f.d6[j] * (float)(1 << F16_SHIFT);
 #pragma unroll
 							for (int i = 0; i < 16; i++)
 								acc[0][j][i] = __builtin_fmaf(D, accb[j][i], acc[0][j][i]);
+							if constexpr (QF)
+								acc[0][j] = O::mma(sa, q4k_mins16(b.sc[j]), acc[0][j]);
+						}
+						if constexpr (QF) {
+							if (st0 + C::SPB < nk)
+								sa = *reinterpret_cast<const V *>(xs + 8 * ((st0 + C::SPB) / C::SPB));
 						}
 					}
 					barrier_after(st);
@@ -1657,7 +1716,25 @@ struct BucketArgs {
 	const float *x;
 	uint16_t *xa, *xlo;
 	int32_t *flag, *list, *count;
+	uint16_t *xsum; // MODE 1, non-null: also the sub-block sums of the A operand (Workspace::xsum)
 };
+
+// Sub-block sums of one token's f16 A row (MODE 1): lane group 4m..4m+3
+// holds the 8-groups of one 32-K sub-block (its lanes' 8-value sums in
+// fp32, then two lane exchanges); the first lane stores the f16 high and
+// remainder parts.  A sum outside the f16 range flags the token.
+__device__ __forceinline__ int store_xsum(uint16_t *xs, int t, int nsub, int sb, float part, bool store)
+{
+	part += __shfl_xor(part, 1);
+	part += __shfl_xor(part, 2);
+	if (!store || (threadIdx.x & 3) != 0)
+		return 0;
+	const _Float16 hi = (_Float16)part;
+	const _Float16 lo = (_Float16)(part - (float)hi);
+	xs[(size_t)(2 * t) * nsub + sb] = __builtin_bit_cast(uint16_t, hi);
+	xs[(size_t)(2 * t + 1) * nsub + sb] = __builtin_bit_cast(uint16_t, lo);
+	return !(__builtin_fabsf(part) < 65504.0f);
+}
 
 template <int MODE> __global__ __launch_bounds__(RB_THREADS) void route_bucket_kernel(BucketArgs r)
 {
@@ -1701,7 +1778,27 @@ template <int MODE> __global__ __launch_bounds__(RB_THREADS) void route_bucket_k
 	}
 	if constexpr (MODE == 1) {
 		if (!conv) {
-			// the A operand and the flag came with the logits: list the token
+			// the A operand and the flag came with the logits: its sub-block
+			// sums from it, then list the token
+			int sbad = 0;
+			if (r.xsum) {
+				const int nsub = r.d / 32;
+				const f16x8 *xr8 = reinterpret_cast<const f16x8 *>(r.xa + (size_t)t * r.d);
+				for (int g0 = 0; g0 < r.d / 8; g0 += 64) {
+					const int g8 = g0 + lane;
+					float part = 0.0f;
+					if (g8 < r.d / 8) {
+						const f16x8 v = xr8[g8];
+#pragma unroll
+						for (int i = 0; i < 8; i++)
+							part += (float)v[i];
+					}
+					sbad |= store_xsum(r.xsum, t, nsub, g8 >> 2, part, g8 < r.d / 8);
+				}
+				sbad = __any(sbad);
+			}
+			if (lane == 0 && sbad && !r.flag[t])
+				r.flag[t] = 1;
 			if (lane == 0 && r.flag[t])
 				r.list[atomicAdd(r.count, 1)] = t;
 			return;
@@ -1720,6 +1817,20 @@ template <int MODE> __global__ __launch_bounds__(RB_THREADS) void route_bucket_k
 #pragma unroll
 		for (int i = 0; i < RB_X / 2; i++) {
 			const int q = base + 2 * (lane + 64 * i); // float4 index of the pair's first half
+			if constexpr (MODE == 1) {
+				// sub-block sums of the f16 values (every lane takes part in
+				// the exchanges)
+				if (r.xsum) {
+					float part = 0.0f;
+					if (q < n4) {
+						const float4 a = xv[2 * i], c = xv[2 * i + 1];
+						part = (((((((float)(_Float16)a.x + (float)(_Float16)a.y) + (float)(_Float16)a.z) +
+							   (float)(_Float16)a.w) + (float)(_Float16)c.x) + (float)(_Float16)c.y) +
+							 (float)(_Float16)c.z) + (float)(_Float16)c.w;
+					}
+					bad |= store_xsum(r.xsum, t, r.d / 32, (q / 2) >> 2, part, q < n4);
+				}
+			}
 			if (q >= n4)
 				continue;
 			const float4 a = xv[2 * i], c = xv[2 * i + 1];
@@ -1762,6 +1873,13 @@ template <int MODE> __global__ __launch_bounds__(RB_THREADS) void route_bucket_k
 	}
 }
 
+// Q4_K gate/up in 32-row tiles with the minimum term from the sub-block sums
+static bool mfma_gu_qfold(const Layer &L, int npairs)
+{
+	return TIE_MFMA_QFOLD && TIE_MFMA_UH && TIE_MFMA_F16 && L.gate.type == TIE_GGML_Q4_K && L.d % QK == 0 &&
+	       mfma_gu_rows(L, npairs) == MFMA_MT_TINY;
+}
+
 hipError_t launch_route_bucket(const Layer &L, const float *x, int T, int k, Workspace &ws, hipStream_t s,
 			       bool converted)
 {
@@ -1787,6 +1905,7 @@ hipError_t launch_route_bucket(const Layer &L, const float *x, int T, int k, Wor
 	r.list = ws.fix_list;
 	r.count = ws.fix_count;
 	r.converted = converted && L.gate.type != TIE_GGML_BF16 && TIE_MFMA_F16;
+	r.xsum = mfma_gu_qfold(L, T * k) ? ws.xsum : nullptr;
 	const dim3 grid((T + RB_THREADS / 64 - 1) / (RB_THREADS / 64));
 	if (L.gate.type == TIE_GGML_BF16)
 		tie_launch(route_bucket_kernel<2>, grid, dim3(RB_THREADS), 0, s, r);
@@ -1981,6 +2100,7 @@ hipError_t launch_mfma_experts(const Layer &L, const float *x, int T, int k, con
 	a.in = L.d;
 	a.a16 = ws.xb;
 	a.a16lo = ws.xlo;
+	a.xsum = mfma_gu_qfold(L, npairs) ? ws.xsum : nullptr;
 	a.h16 = hrows;
 	a.h16lo = ws.hlo;
 	hipError_t err = launch_one<false>(a, L.gate.type, dim3(L.F / GU_COLS, gu_tiles), s, mt_gu);
