@@ -268,7 +268,7 @@ const float *tie_hip_model_ffn_norm(const tie_hip_model *m, int n);
 void tie_hip_model_close(tie_hip_model *m);
 
 /* The largest T that TIE_HIP_PATH_AUTO sends down the exact path (default
- * 16: from 17 tokens on the matrix-core path is the faster one at the 30B shape;
+ * 14: from 15 tokens on the matrix-core path is the faster one at the 30B shape;
  * 64 or more keeps every decode-sized batch bit-exact). */
 int tie_hip_exact_max_tokens(void);
 void tie_hip_set_exact_max_tokens(int t);

@@ -64,7 +64,7 @@ struct Ctx {
 	// the matrix cores above (measured faster from T = 22 on at the 30B
 	// shape, graph-timed: T=20 0.1002 / 0.1043 ms, T=22 0.1072 / 0.1065 ms,
 	// T=24 0.1115 / 0.1083 ms exact / MFMA)
-	int exact_max_t = 16;
+	int exact_max_t = 14;
 	int debug_stale = 0; // one-launch decode calls left whose waits are made to give up (debug hook)
 	std::recursive_mutex mu;
 };

@@ -153,6 +153,8 @@ CONFIGS = {
     "30b_t2": dict(d=2048, F=768, E=128, k=8, T=2, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1242),
     "30b_t4": dict(d=2048, F=768, E=128, k=8, T=4, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1244),
     "30b_t8": dict(d=2048, F=768, E=128, k=8, T=8, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1240),
+    "30b_t12": dict(d=2048, F=768, E=128, k=8, T=12, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1280),
+    "30b_t14": dict(d=2048, F=768, E=128, k=8, T=14, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1281),
     "30b_t16": dict(d=2048, F=768, E=128, k=8, T=16, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1252),
     "30b_t20": dict(d=2048, F=768, E=128, k=8, T=20, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1257),
     "30b_t22": dict(d=2048, F=768, E=128, k=8, T=22, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1259),
