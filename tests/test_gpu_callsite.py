@@ -3,7 +3,7 @@ model_qwen3.c:404-471 (MoE branch), model_qwen3.c:390-491 (FFN half) and
 model_lfm2.c:414-497 (LFM2 MoE branch), compiled against TIE's headers
 (struct TIEContext, Model, LayerWeights) by oracle/Makefile into
 oracle/_ref/callsite, run as a separate process on seeded inputs, and
-checked against the oracle: bit for bit on the exact path (T <= 64), within
+checked against the oracle: bit for bit on the exact path (small T), within
 the 16-bit bound on the matrix cores.  The binary is built where the
 reference sources are and travels with the tree; without it the tests skip.
 """
@@ -57,7 +57,7 @@ def test_qwen3_moe_branch_exact(tmp_path, tie_table):
 
 
 def test_qwen3_moe_branch_prefill(tmp_path, tie_table):
-    """T = 100: the default path above 64 tokens (the matrix cores)."""
+    """T = 100: the default path at this T (the matrix cores)."""
     layer = synth_layer(301, 2048, 768, 128, synth.Q4_K, synth.Q6_K, None)
     x = synth.make_input(301, 100, 2048)
     out = run_callsite(tmp_path, 0, layer, x, 8)
