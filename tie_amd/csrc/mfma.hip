@@ -1874,9 +1874,10 @@ template <int MODE> __global__ __launch_bounds__(RB_THREADS) void route_bucket_k
 }
 
 // Q4_K gate/up in 32-row tiles with the minimum term from the sub-block sums
+// (exactly when the kernel instantiation's QF is on: it reads Workspace::xsum)
 static bool mfma_gu_qfold(const Layer &L, int npairs)
 {
-	return TIE_MFMA_QFOLD && TIE_MFMA_UH && TIE_MFMA_F16 && L.gate.type == TIE_GGML_Q4_K && L.d % QK == 0 &&
+	return Cfg<TIE_GGML_Q4_K, false, MFMA_MT_TINY>::UH && TIE_MFMA_QFOLD && L.gate.type == TIE_GGML_Q4_K &&
 	       mfma_gu_rows(L, npairs) == MFMA_MT_TINY;
 }
 
