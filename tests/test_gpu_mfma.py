@@ -132,7 +132,7 @@ def q6k_f16(buf, dfold=False):
 
 
 QUANT = (synth.Q4_K, synth.Q6_K)
-TINY_AVG = 8  # pairs per expert on average up to which the kernels take 32-row tiles
+TINY_AVG = 16  # pairs per expert on average up to which the kernels take 32-row tiles
 
 
 def expert_weights(buf, wtype, e, rows, inn, f16_ops, dfold=False, qfold=False):
@@ -236,10 +236,11 @@ def check_routing(idx, w, ri, rw):
 
 # (d, F, E, k, T): small shapes, the 30B shape at few pairs per expert
 # (T = 32 and 7: one work item per expert and column slab, h by expert;
-# T = 64: the scanned tile list), and few experts at T = 1024 (256 pairs per
-# expert: full 160-row gate/up tiles, the cross-stage software pipeline,
-# several tiles per expert)
-@pytest.mark.parametrize("shape", [(256, 256, 16, 4, 40), (512, 512, 8, 2, 300), (2048, 768, 128, 8, 64),
+# T = 64: the scanned tile list), 25 pairs per expert (64-row gate/up
+# tiles), and few experts at T = 1024 (256 pairs per expert: full 160-row
+# gate/up tiles, the cross-stage software pipeline, several tiles per expert)
+@pytest.mark.parametrize("shape", [(256, 256, 16, 4, 40), (256, 256, 16, 4, 100), (512, 512, 8, 2, 300),
+                                   (2048, 768, 128, 8, 64),
                                    (2048, 768, 128, 8, 32), (512, 512, 16, 4, 7), (2048, 768, 8, 2, 1024)])
 @pytest.mark.parametrize("types", [(synth.Q4_K, synth.Q6_K), (synth.Q6_K, synth.Q4_K)])
 def test_quantised_against_model_and_oracle(shape, types):

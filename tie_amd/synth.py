@@ -163,6 +163,9 @@ CONFIGS = {
     "30b_t64": dict(d=2048, F=768, E=128, k=8, T=64, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1243),
     "30b_t128": dict(d=2048, F=768, E=128, k=8, T=128, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1245),
     "30b_t256": dict(d=2048, F=768, E=128, k=8, T=256, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1246),
+    "30b_t192": dict(d=2048, F=768, E=128, k=8, T=192, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1282),
+    "30b_t256": dict(d=2048, F=768, E=128, k=8, T=256, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1283),
+    "30b_t384": dict(d=2048, F=768, E=128, k=8, T=384, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1284),
     "30b_t512": dict(d=2048, F=768, E=128, k=8, T=512, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1247),
     "30b_t1024": dict(d=2048, F=768, E=128, k=8, T=1024, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1248),
     "30b_t32_ffn": dict(d=2048, F=768, E=128, k=8, T=32, gu_type=Q4_K, down_type=Q6_K, zipf=None, seed=1235,
